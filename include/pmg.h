@@ -1,0 +1,228 @@
+/*
+ * pmg.h -- C ABI of libpmg.so, the MI355X (gfx950) implementation of PromptMoGe's sparse 3-D refiner step.
+ *
+ * Conventions
+ *   - Every pointer argument named as a buffer is a DEVICE pointer owned by the caller, except where a comment says
+ *     "host". Nothing here allocates device memory except pmg_refiner_create (its persistent workspace).
+ *   - Every call is asynchronous on `stream` (a hipStream_t, NULL = the legacy default stream) and returns an int
+ *     status: PMG_OK, or an error code with a message available from pmg_last_error() (thread-local).
+ *   - Shapes are validated on the host before any launch; a launch whose shape the kernel does not support is
+ *     refused with PMG_E_INVALID, never attempted.
+ *   - Voxel index conventions follow the reference: M voxels in raster (b, i, j) order at level 0; a neighbour map
+ *     entry is the row index of the neighbour or -1; tap v = (di+1)*9 + (dj+1)*3 + (dz+1) for the 27 offsets of
+ *     make_conv_kernel_delta (promptmoge/_fallback/flex_gemm/_core.py:65-82), so the centre tap is v = 13.
+ *
+ * Which reference interface each entry point replaces is given with file:line into the reference tree.
+ */
+#ifndef PMG_H
+#define PMG_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    PMG_OK = 0,
+    PMG_E_INVALID = 1,  /* bad argument or unsupported shape (reference: assert / ValueError, _core.py:324, 351) */
+    PMG_E_HIP = 2,      /* a HIP runtime call failed */
+    PMG_E_OVERFLOW = 3, /* a capacity was exceeded; the caller grows and retries (VoxelStructure.swift:200-216) */
+    PMG_E_DEVICE = 4    /* a kernel reported an error through its device flag (e.g. a bounded wait expired) */
+};
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* pmg_last_error(void);
+/* ABI version, bumped on any signature change. */
+int pmg_version(void);
+
+/* ------------------------------------------------------------------------------------------------------------ *
+ * Numerics test hooks: evaluate the shared bit-reproducible fp32 functions (exp, log, silu) on the host CPU or on
+ * the GPU, so tests can show that both and the NumPy oracle produce identical bits. op: 0 exp, 1 log, 2 silu.
+ * ------------------------------------------------------------------------------------------------------------ */
+int pmg_math_host(int op, const float* in_host, float* out_host, int64_t n);
+int pmg_math_device(int op, const float* in, float* out, int64_t n, void* stream);
+
+/* ------------------------------------------------------------------------------------------------------------ *
+ * (1) Voxelisation -- replaces MoGeModel._voxelize (moge/model/v3.py:305-344).
+ *   zq[b,i,j] = rint(logz[b,i,j] * resolution)       (round half to even, as torch.round; v3.py:332)
+ *   zmin[b] = min over (i,j) of zq, zmax[b] = max     (v3.py:333-335; the z coordinate is zq - zmin[b] and the
+ *                                                      z extent is max_b(zmax - zmin) + 1)
+ * logz: [B*H*W] fp32 (the third channel of the point map, passed with its element stride `stride`, 1 for a plain
+ * map, 3 for the (x/z, y/z, logz) point map). zq: [B*H*W] int32; zmin, zmax: [B] int32.
+ * ------------------------------------------------------------------------------------------------------------ */
+int pmg_voxelize(const float* logz, int64_t stride, int B, int H, int W, float resolution, int32_t* zq,
+                 int32_t* zmin, int32_t* zmax, void* stream);
+
+/* ------------------------------------------------------------------------------------------------------------ *
+ * (2) Submanifold neighbour maps.
+ *
+ * pmg_nmap_column -- the level-0 column stencil, replaces _build_submanifold_nmap_column (_core.py:269-295):
+ *   nmap[(b,i,j), v] = flat(b, i+di, j+dj) iff that pixel is in frame and zq there == zq[b,i,j] + dz, else -1.
+ * Outputs (each may be NULL):
+ *   nmap_t    [27][M] int32, tap-major (the layout the convolutions read)
+ *   nmap_rows [M][27] int32, the reference's row-major (M, 27) layout
+ *   tile_mask [ceil(M/16)] uint32: bit v set iff any of the tile's 16 rows has tap v
+ *   coords    [M][4] int32 (b, i, j, zq - zmin[b]), the reference's coords (v3.py:337-340); needs zmin
+ * ------------------------------------------------------------------------------------------------------------ */
+int pmg_nmap_column(const int32_t* zq, const int32_t* zmin, int B, int H, int W, int32_t* nmap_t,
+                    int32_t* nmap_rows, uint32_t* tile_mask, int32_t* coords, void* stream);
+
+/* pmg_nmap_hash -- generic coordinates, replaces _SortedIndex + _build_submanifold_nmap_sorted
+ * (_core.py:105-124, 298-304) with an open-addressing GPU hash over the linearised keys of _linearise
+ * (_core.py:89-94). coords: [M][4] int32 (b, x, y, z), unique, inside sparse_shape (host array of 4 int64).
+ * Same outputs as pmg_nmap_column (coords excluded). The workspace holds the table (load factor <= 1/4). */
+size_t pmg_hash_workspace_bytes(int64_t M);
+int pmg_nmap_hash(const int32_t* coords, int64_t M, const int64_t* sparse_shape_host, int32_t* nmap_t,
+                  int32_t* nmap_rows, uint32_t* tile_mask, void* workspace, size_t workspace_bytes, void* stream);
+
+/* pmg_nmap_from_rows -- a caller-supplied (M, 27) map (a NeighborCache.nmap, _core.py:131-176) into the tap-major
+ * layout and tile masks the convolutions read. */
+int pmg_nmap_from_rows(const int32_t* nmap_rows, int64_t M, int32_t* nmap_t, uint32_t* tile_mask, void* stream);
+
+/* pmg_kmap_compact -- the 27 offset-major kernel maps, compacted: for each tap v, the output rows that have a
+ * neighbour at v in ascending order and the neighbour rows, exactly the reference's per-tap
+ * `rows = valid.nonzero()` and `src = idx[rows]` (_core.py:430-437).
+ *   offsets [28] int64 (device): tap v occupies [offsets[v], offsets[v+1]) of out_rows / in_rows
+ *   out_rows, in_rows: int32, capacity entries each (27*M always suffices)
+ * Returns PMG_E_OVERFLOW (after writing offsets) if the total exceeds capacity. */
+size_t pmg_kmap_workspace_bytes(int64_t M);
+int pmg_kmap_compact(const int32_t* nmap_t, int64_t M, int64_t* offsets, int32_t* out_rows, int32_t* in_rows,
+                     int64_t capacity, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------------------------------------------ *
+ * (3) Submanifold 3x3x3 convolutions, output-stationary implicit GEMM on MFMA, replacing submanifold_conv
+ * (_core.py:399-441):  out[m, n] = bias[n] + sum_v sum_c W[n, v, c] * x[nmap[v][m], c].
+ * Weights are in the reference module's own layout, (Co, 3, 3, 3, Ci) = [Co][27][Ci] (nn/__init__.py:30).
+ * Ci and Co must be multiples of 16 (int8, fp16) or of 4 and 16 (fp32). tile_mask must come from the same map.
+ *
+ * int8 (the deployed contract, moge/model/modules/qat.py:1-16 and SparseConvInt8.metal:36-142):
+ *   acc = sum int8*int8 in int32, then by epilogue
+ *     PMG_EPI_ACC   out int32 [M][Co] = acc                                          (parity dump)
+ *     PMG_EPI_Q     out int8  [M][Co] = quant(silu((acc*a_scale)*w_scale[n] + bias[n]), out_scale)
+ *     PMG_EPI_R     out fp32  [M][Co] = ((acc*a_scale)*w_scale[n] + bias[n]) + skip[m][n]   (skip may alias out)
+ *     PMG_EPI_BIAS  out fp32  [M][Co] = (acc*a_scale)*w_scale[n] + bias[n]
+ *   a_scale = clip/127 of the input activation, w_scale per output channel, quant as in qat.py:35-36.
+ * fp16 (teacher; fp32 accumulation): PMG_EPI_ACC / PMG_EPI_BIAS -> fp32 [M][Co] = acc (+ bias[n]);
+ *   PMG_EPI_SILU -> fp16 [M][Co] = half(silu(acc + bias[n])); PMG_EPI_R -> fp32 = (acc + bias[n]) + skip.
+ * fp32 (the flex_gemm shim on fp32 features): PMG_EPI_ACC / PMG_EPI_BIAS -> fp32.
+ * bias may be NULL (zero).
+ * ------------------------------------------------------------------------------------------------------------ */
+enum { PMG_EPI_ACC = 0, PMG_EPI_Q = 1, PMG_EPI_R = 2, PMG_EPI_BIAS = 3, PMG_EPI_SILU = 4 };
+
+int pmg_spconv_i8(const int8_t* x, const int32_t* nmap_t, const uint32_t* tile_mask, int64_t M, int Ci, int Co,
+                  const int8_t* w, int epilogue, float a_scale, const float* w_scale, const float* bias,
+                  float out_scale, const float* skip, void* out, void* stream);
+int pmg_spconv_f16(const uint16_t* x, const int32_t* nmap_t, const uint32_t* tile_mask, int64_t M, int Ci, int Co,
+                   const uint16_t* w, int epilogue, const float* bias, const float* skip, void* out, void* stream);
+int pmg_spconv_f32(const float* x, const int32_t* nmap_t, const uint32_t* tile_mask, int64_t M, int Ci, int Co,
+                   const float* w, int epilogue, const float* bias, float* out, void* stream);
+
+/* ------------------------------------------------------------------------------------------------------------ *
+ * Row operations of the residual block (SparseResBlock3d, moge/model/modules/flex_sparse_blocks.py:70-75;
+ * device design Refiner.metal:75-131).
+ *   pmg_ln_silu_quant: q[m] = quant(silu(LayerNorm(x[m]) * gamma + beta), out_scale)  -> int8 [M][C]
+ *   pmg_ln_silu_f16:   h[m] = half(silu(LayerNorm(x[m]) * gamma + beta))                -> fp16 [M][C]
+ * LayerNorm is two-pass (mean, then mean of squared deviations) with sums in channel order, eps inside the sqrt.
+ * C in {16, 32, 48, 64, 96, 128}.
+ * ------------------------------------------------------------------------------------------------------------ */
+int pmg_ln_silu_quant(const float* x, int64_t M, int C, const float* gamma, const float* beta, float eps,
+                      float out_scale, int8_t* q, void* stream);
+int pmg_ln_silu_f16(const float* x, int64_t M, int C, const float* gamma, const float* beta, float eps,
+                    uint16_t* h, void* stream);
+
+/* ------------------------------------------------------------------------------------------------------------ *
+ * (4) Robust metric fit -- replaces fit_scale_shift (moge/model/modules/prompt_stem.py:211-240): trimmed least
+ * squares target ~= s*z + t on mask, `iters` trim rounds then a final solve; k = max(long(fp32(1-trim)*count),
+ * min_points) and the trim threshold is the exact k-th smallest relative residual (torch.kthvalue), found by a
+ * radix select; (1, 0) when fewer than min_points mask pixels. Sums in fp64, one persistent kernel per batch item
+ * with device-wide barriers, no host round trip.
+ *   z, target: [B][N] fp32; mask: [B][N] uint8 (0/1); st: [B][2] fp32 (s, t) written on device.
+ *   info (may be NULL): [B][5] int32 = (count, k, ok, threshold bits of the last trim round, device error flag:
+ *   nonzero if a bounded device-wide wait expired, in which case (s, t) are not valid).
+ * N <= 2^22 per batch item.
+ * ------------------------------------------------------------------------------------------------------------ */
+size_t pmg_fit_workspace_bytes(int64_t N, int iters);
+int pmg_fit_scale_shift(const float* z, const float* target, const uint8_t* mask, int B, int64_t N, int iters,
+                        float trim, int min_points, float* st, int32_t* info, void* workspace,
+                        size_t workspace_bytes, void* stream);
+
+/* The prompt fit of MoGeModel._lidar_in_affine_frame (v3.py:362-383), prepared on the fly: z = exp(logz) on the
+ * H x W map (logz with element stride `stride`), target = nearest-resized LiDAR (F.interpolate 'nearest' index
+ * rule), mask = finite(d) & d > 0 & clamp(conf/2, 0, 1) >= 0.999. lidar, conf: [B][dh][dw] fp32. */
+int pmg_fit_prompt(const float* logz, int64_t stride, const float* lidar, const float* conf, int B, int H, int W,
+                   int dh, int dw, int iters, float trim, int min_points, float* st, int32_t* info,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------------------------------------------ *
+ * The fused refiner step -- replaces one iteration of the refine loop (v3.py:547-576) for a single-level
+ * refiner: prompt fit -> prompt residual/gate -> voxelise -> column neighbour map -> input_proj (+ prompt_proj)
+ * -> n_blocks residual blocks (LN, SiLU, conv1, SiLU, conv2, + skip) -> out_proj -> logz += delta
+ * (_refine_logz, v3.py:346-360), then optionally the metric fit on the refined depth. All on `stream`, no host
+ * synchronisation; the sequence is captured once into a HIP graph and replayed while the buffers and the stream
+ * are unchanged (on the legacy default stream, which cannot be captured, it is enqueued eagerly).
+ * ------------------------------------------------------------------------------------------------------------ */
+enum { PMG_PREC_INT8 = 0, PMG_PREC_FP16 = 1 };
+
+typedef struct {
+    int B, H, W;            /* point-map batch and size; M = B*H*W voxels at level 0 */
+    int C;                  /* refiner width (16 .. 128, multiple of 16) */
+    int n_blocks;           /* residual blocks; conv layers = 2 * n_blocks */
+    int precision;          /* PMG_PREC_INT8 or PMG_PREC_FP16 */
+    float depth_resolution; /* refiner_depth_resolution (v3.py:29), 256 */
+    int dh, dw;             /* LiDAR map size */
+    int fit_iters;          /* trim rounds of each fit */
+    float fit_trim;         /* 0.2 */
+    int fit_min_points;     /* 32 */
+    int use_prompt;         /* feed (residual, gate) through prompt_proj (v3.py:549-555) */
+    int soft_gate;          /* soft_residual_gate (v3.py:379-382) */
+    int final_fit;          /* also fit (s, t) of the refined depth against the LiDAR */
+    int use_graph;          /* capture the step into a HIP graph and replay it */
+} pmg_refiner_config;
+
+typedef struct {
+    const float* ln_gamma; /* [C] */
+    const float* ln_beta;  /* [C] */
+    const void* w1;        /* conv1 [C][27][C], int8 or fp16 by precision */
+    const float* w1_scale; /* [C] per-output-channel weight scale (int8 only) */
+    const float* b1;       /* [C] */
+    float a1_scale;        /* conv1 input activation scale clip/127 (int8 only) */
+    const void* w2;
+    const float* w2_scale;
+    const float* b2;
+    float a2_scale;
+} pmg_block_weights;
+
+typedef struct {
+    const float* in_w;  /* input_proj weight [C][3] */
+    const float* in_b;  /* [C] */
+    const float* pr_w;  /* prompt_proj weight [C][2] (NULL if !use_prompt) */
+    const float* pr_b;  /* [C] */
+    const float* out_w; /* out_proj weight [1][C] */
+    const float* out_b; /* [1] */
+    int n_blocks;
+    const pmg_block_weights* blocks; /* host array of n_blocks; the pointers inside are device pointers */
+} pmg_refiner_weights;
+
+typedef struct pmg_refiner pmg_refiner;
+
+pmg_refiner* pmg_refiner_create(const pmg_refiner_config* cfg);
+void pmg_refiner_destroy(pmg_refiner* r);
+int pmg_refiner_set_weights(pmg_refiner* r, const pmg_refiner_weights* w);
+/* points: [B][H][W][3] (x/z, y/z, logz) input; points_out: the same map with the refined logz (may alias points,
+ * the reference loop's `current_coord = cat(xy, refined_logz)`, v3.py:574). lidar, conf: [B][dh][dw] fp32.
+ * st_prompt: [B][2] prompt-fit (s, t) or NULL; st_final: [B][2] or NULL. */
+int pmg_refiner_step(pmg_refiner* r, const float* points, float* points_out, const float* lidar, const float* conf,
+                     float* st_prompt, float* st_final, void* stream);
+/* Synchronises `stream` and reports a device-side error flag of the last steps (PMG_E_DEVICE). */
+int pmg_refiner_check(pmg_refiner* r, void* stream);
+/* Device buffers of the last step, for parity tests: 0 zq, 1 nmap_t, 2 tile_mask, 3 x (fp32 residual),
+ * 4 q1 (conv1 input), 5 q2 (conv2 input). Returns NULL for an unknown id. */
+const void* pmg_refiner_buffer(pmg_refiner* r, int id);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PMG_H */

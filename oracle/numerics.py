@@ -1,0 +1,105 @@
+"""fp32 arithmetic restated operation by operation in NumPy float32, matching promptmoge_amd/csrc/pmg_math.h.
+
+NumPy float32 arithmetic is IEEE-754 with every operation individually rounded (no fused multiply-add), which is
+exactly how the kernels are compiled (-ffp-contract=off, correctly rounded division and sqrt). Constants are given
+by bit pattern so both sides use identical values.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+F32 = np.float32
+
+
+def _f(bits: int) -> np.float32:
+    return np.array([bits], dtype=np.uint32).view(np.float32)[0]
+
+
+LOG2E = _f(0x3FB8AA3B)
+LN2_HI = _f(0x3F317200)
+LN2_LO = _f(0x35BFBE8E)
+I6, I24, I120, I720, I5040 = _f(0x3E2AAAAB), _f(0x3D2AAAAB), _f(0x3C088889), _f(0x3AB60B61), _f(0x39500D01)
+C3, C5, C7, C9 = _f(0x3EAAAAAB), _f(0x3E4CCCCD), _f(0x3E124925), _f(0x3DE38E39)
+SQRT2 = _f(0x3FB504F3)
+
+
+def exp_f32(x) -> np.ndarray:
+    """Cody-Waite reduction, degree-7 Horner polynomial, exponent-field scaling (pmg_math.h exp_f32)."""
+    x = np.asarray(x, dtype=np.float32)
+    with np.errstate(over="ignore", invalid="ignore"):
+        kf = np.rint(x * LOG2E)
+        r = x - kf * LN2_HI
+        r = r - kf * LN2_LO
+        p = np.full_like(x, I5040)
+        for c in (I720, I120, I24, I6, F32(0.5), F32(1.0), F32(1.0)):
+            p = p * r + c
+        k = np.clip(np.nan_to_num(kf, nan=0.0), -126, 128).astype(np.int64)
+        scale = ((np.minimum(k, 127) + 127).astype(np.uint32) << np.uint32(23)).view(np.float32)
+        out = p * scale
+        out = np.where(k > 127, (p * _f(254 << 23)) * F32(2.0), out)
+        out = np.where(x > F32(88.8), F32(np.inf), out)
+        out = np.where(x < F32(-87.0), F32(0.0), out)
+        out = np.where(np.isnan(x), x, out)
+    return out.astype(np.float32)
+
+
+def log_f32(x) -> np.ndarray:
+    """log(x) = e*ln2 + 2 atanh((m-1)/(m+1)) for positive normal x (pmg_math.h log_f32)."""
+    x = np.asarray(x, dtype=np.float32)
+    u = x.view(np.uint32)
+    e = (u >> np.uint32(23)).astype(np.int32) - 127
+    m = ((u & np.uint32(0x007FFFFF)) | np.uint32(0x3F800000)).view(np.float32)
+    big = m > SQRT2
+    m = np.where(big, m * F32(0.5), m)
+    e = np.where(big, e + 1, e)
+    f = m - F32(1.0)
+    s = f / (F32(2.0) + f)
+    z = s * s
+    R = np.full_like(z, C9)
+    R = R * z + C7
+    R = R * z + C5
+    R = R * z + C3
+    R = R * z
+    t = s + s * R
+    logm = t + t
+    ef = e.astype(np.float32)
+    return (ef * LN2_HI + (ef * LN2_LO + logm)).astype(np.float32)
+
+
+def silu_f32(y) -> np.ndarray:
+    """y / (1 + exp(-y)) (SparseConvInt8.metal:108)."""
+    y = np.asarray(y, dtype=np.float32)
+    with np.errstate(over="ignore"):
+        return (y / (F32(1.0) + exp_f32(-y))).astype(np.float32)
+
+
+def quant_f32(y, s) -> np.ndarray:
+    """clamp(rint(y / s), -127, 127), the QAT quantiser (qat.py:35-36): correctly rounded fp32 division, then
+    round half to even."""
+    y = np.asarray(y, dtype=np.float32)
+    return np.clip(np.rint(y / np.float32(s)), F32(-127.0), F32(127.0)).astype(np.float32)
+
+
+def quant_i8(y, s) -> np.ndarray:
+    return quant_f32(y, s).astype(np.int8)
+
+
+def ln_silu(x: np.ndarray, gamma: np.ndarray, beta: np.ndarray, eps: float = 1e-6) -> np.ndarray:
+    """Two-pass LayerNorm with channel-order sums, affine, SiLU; fp32 op by op (pmg_rowops.hip ln_silu_row).
+    The reference's block is `silu(norm1(x))` with nn.LayerNorm(eps=1e-6) (flex_sparse_blocks.py:215, 230)."""
+    x = np.asarray(x, dtype=np.float32)
+    M, C = x.shape
+    s = np.zeros(M, dtype=np.float32)
+    for c in range(C):
+        s = s + x[:, c]
+    mean = s / F32(C)
+    v = np.zeros(M, dtype=np.float32)
+    for c in range(C):
+        d = x[:, c] - mean
+        v = v + d * d
+    var = v / F32(C)
+    rstd = F32(1.0) / np.sqrt(var + F32(eps))
+    y = (x - mean[:, None]) * rstd[:, None]
+    y = y * gamma.astype(np.float32)
+    y = y + beta.astype(np.float32)
+    return silu_f32(y)

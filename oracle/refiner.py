@@ -1,0 +1,195 @@
+"""One refinement step of a single-level refiner, restated from the reference.
+
+Step order (moge/model/v3.py:547-576 with _lidar_in_affine_frame 362-383 and _refine_logz 346-360):
+  1. prompt fit:   (s, t) = fit_scale_shift(exp(logz), nearest LiDAR, valid & conf/2 >= 0.999)
+  2. prompt feats: d_aff = (d - t) / max(s, 1e-6); ok = valid & d_aff > 1e-4; log_d_aff = ok ? log(max(d_aff, 1e-4))
+                   : logz; gate = c*ok (soft: (0.15 + 0.85c)*ok); residual = (log_d_aff - logz) * gate
+  3. voxelise + level-0 neighbour map
+  4. Sparse3DUNet, single level (sparse_unet.py:189-192, 258): h = input_proj(feats) + prompt_proj(residual, gate);
+     SparseResBlock3d x n (flex_sparse_blocks.py:229-234); out_proj
+  5. logz += out
+  6. optionally the same fit on the refined depth
+
+`step` computes the blocks in the deployed integer arithmetic (the QAT contract qat.py:1-16 as executed by
+SparseConvInt8.metal / Refiner.metal: int8 activations and weights, exact int32 accumulation, fp32 epilogues) or
+in fp16 (teacher); every fp32 operation in the order of the GPU kernels. `step_fakequant` is the reference's own
+fp32 formulation of the int8 model: _fallback's fp32 conv on fake-quantised operands (qat.py:28-57, 89-106).
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import numpy as np
+
+from .conv import conv_acc_int, conv_float, epilogue_q, epilogue_r
+from .fit import fit_f64, prompt_inputs
+from .numerics import F32, ln_silu, log_f32, quant_i8
+from .structure import nmap_column, voxelize
+
+
+def quantize_weight(w: np.ndarray):
+    """WeightFakeQuant (qat.py:52-57) with _fake_quant (qat.py:35-36): s = max|W[co]| / 127 in fp32, clamped at
+    1e-12, q = clamp(round(W / s), -127, 127)."""
+    w = np.asarray(w, dtype=np.float32)
+    s = (np.abs(w).reshape(w.shape[0], -1).max(axis=1) / F32(127.0)).astype(np.float32)
+    s = np.maximum(s, F32(1e-12))
+    q = np.clip(np.rint(w / s.reshape((-1,) + (1,) * (w.ndim - 1))), -127, 127)
+    return q.astype(np.int8), s
+
+
+def act_scale(clip: float) -> np.float32:
+    """ActFakeQuant scale clip / QMAX in fp32, clamped at 1e-12 (qat.py:35, 98)."""
+    return np.maximum(F32(clip) / F32(127.0), F32(1e-12))
+
+
+def prompt_feats(points, d, c, s, t, soft_gate=False):
+    """v3.py:379-383 and 552-555, op by op in fp32; d, c [B, H, W] (already nearest-resized)."""
+    logz = points[..., 2]
+    s = np.asarray(s, dtype=np.float32)[:, None, None]
+    t = np.asarray(t, dtype=np.float32)[:, None, None]
+    valid = np.isfinite(d) & (d > 0)
+    with np.errstate(invalid="ignore", over="ignore"):
+        daff = (d - t) / np.maximum(s, F32(1e-6))
+    ok = valid & (daff > F32(1e-4))
+    lda = np.where(ok, log_f32(np.maximum(np.where(ok, daff, F32(1.0)), F32(1e-4))), logz)
+    okf = ok.astype(np.float32)
+    gate = (F32(0.15) + F32(0.85) * c) * okf if soft_gate else c * okf
+    res = (lda - logz) * gate
+    return res.astype(np.float32), gate.astype(np.float32)
+
+
+def input_proj(f: np.ndarray, w, res=None, gate=None) -> np.ndarray:
+    """input_proj (+ prompt_proj), in the kernel's order: ((b + w0 f0) + w1 f1) + w2 f2 (+ ((pb + p0 r) + p1 g))."""
+    in_w, in_b = np.asarray(w.in_w, np.float32), np.asarray(w.in_b, np.float32)
+    y = in_b[None, :] + in_w[None, :, 0] * f[:, 0:1]
+    y = y + in_w[None, :, 1] * f[:, 1:2]
+    y = y + in_w[None, :, 2] * f[:, 2:3]
+    if res is not None:
+        pr_w, pr_b = np.asarray(w.pr_w, np.float32), np.asarray(w.pr_b, np.float32)
+        pp = pr_b[None, :] + pr_w[None, :, 0] * res[:, None]
+        pp = pp + pr_w[None, :, 1] * gate[:, None]
+        y = y + pp
+    return y.astype(np.float32)
+
+
+def out_proj(x: np.ndarray, w) -> np.ndarray:
+    """out_proj (C -> 1), channel-order sum from the bias."""
+    d = np.full(x.shape[0], np.float32(w.out_b[0]), dtype=np.float32)
+    ow = np.asarray(w.out_w, np.float32).reshape(-1)
+    for c in range(x.shape[1]):
+        d = d + ow[c] * x[:, c]
+    return d
+
+
+def blocks_int8(x, nmap, w, trace=None):
+    for blk in w.blocks:
+        q_w1, s_w1 = quantize_weight(blk.w1)
+        q_w2, s_w2 = quantize_weight(blk.w2)
+        a1, a2 = act_scale(blk.clip1), act_scale(blk.clip2)
+        q1 = quant_i8(ln_silu(x, blk.gamma, blk.beta), a1)
+        acc1 = conv_acc_int(q1, nmap, q_w1)
+        q2 = epilogue_q(acc1, a1, s_w1, blk.b1, a2)
+        acc2 = conv_acc_int(q2, nmap, q_w2)
+        x = epilogue_r(acc2, a2, s_w2, blk.b2, x)
+        if trace is not None:
+            trace.append(dict(q1=q1, acc1=acc1, q2=q2, acc2=acc2, x=x))
+    return x
+
+
+def blocks_fp16(x, nmap, w, trace=None):
+    """Teacher: fp16 conv operands, fp32 accumulation (here fp64, then rounded), fp32 residual stream."""
+    from .numerics import silu_f32
+
+    for blk in w.blocks:
+        h1 = ln_silu(x, blk.gamma, blk.beta).astype(np.float16)
+        y1 = conv_float(h1.astype(np.float64), nmap, np.asarray(blk.w1, np.float16).astype(np.float64),
+                        dtype=np.float64).astype(np.float32)
+        h2 = silu_f32(y1 + np.asarray(blk.b1, np.float32)).astype(np.float16)
+        y2 = conv_float(h2.astype(np.float64), nmap, np.asarray(blk.w2, np.float16).astype(np.float64),
+                        dtype=np.float64).astype(np.float32)
+        x = (y2 + np.asarray(blk.b2, np.float32)) + x
+        if trace is not None:
+            trace.append(dict(h1=h1, h2=h2, x=x))
+    return x
+
+
+def step(points, lidar, conf, w, *, precision="int8", iters=10, trim=0.2, min_points=32, use_prompt=True,
+         soft_gate=False, final_fit=False, resolution=256.0, trace: Optional[dict] = None):
+    """Returns (refined points [B, H, W, 3], (s, t) prompt fit, (s, t) final fit or None)."""
+    pts = np.array(points, dtype=np.float32, copy=True)
+    B, H, W, _ = pts.shape
+    M = B * H * W
+    st = None
+    res = gate = None
+    if use_prompt:
+        z, tg, m, d, c = prompt_inputs(pts, lidar, conf)
+        st = fit_f64(z, tg, m, iters, trim, min_points)
+        r, g = prompt_feats(pts, d, c, st[0], st[1], soft_gate)
+        res, gate = r.reshape(-1), g.reshape(-1)
+    zq, coords, _, _ = voxelize(pts, resolution)
+    nmap = nmap_column(zq)
+    x = input_proj(pts.reshape(M, 3), w, res, gate)
+    blk_trace = [] if trace is not None else None
+    x = (blocks_int8 if precision == "int8" else blocks_fp16)(x, nmap, w, blk_trace)
+    delta = out_proj(x, w)
+    pts[..., 2] = pts[..., 2] + delta.reshape(B, H, W)
+    fin = None
+    if final_fit:
+        z, tg, m, _, _ = prompt_inputs(pts, lidar, conf)
+        fin = fit_f64(z, tg, m, iters, trim, min_points)
+    if trace is not None:
+        trace.update(zq=zq, nmap=nmap, coords=coords, blocks=blk_trace, x=x, res=res, gate=gate)
+    return pts, st, fin
+
+
+# ------------------------------------------------------------------------------------------------------------------
+def _ln_ref(x, gamma, beta, eps=1e-6):
+    mu = x.mean(axis=1, keepdims=True, dtype=np.float32)
+    var = ((x - mu) ** 2).mean(axis=1, keepdims=True, dtype=np.float32)
+    return ((x - mu) / np.sqrt(var + np.float32(eps)) * gamma + beta).astype(np.float32)
+
+
+def _silu_ref(x):
+    return (x / (np.float32(1.0) + np.exp(-x))).astype(np.float32)
+
+
+def _fake_quant(x, s):
+    """_fake_quant forward value (qat.py:35-36): clamp(round(x / s), -127, 127) * s."""
+    s = np.float32(s)
+    return (np.clip(np.rint(x.astype(np.float32) / s), -127, 127) * s).astype(np.float32)
+
+
+def blocks_fakequant(x, nmap, w):
+    """The reference's fp32 formulation: _fallback conv on fake-quantised operands (qat.py:101-111, 52-57)."""
+    for blk in w.blocks:
+        q_w1, s_w1 = quantize_weight(blk.w1)
+        q_w2, s_w2 = quantize_weight(blk.w2)
+        w1 = (q_w1.astype(np.float32) * s_w1.reshape(-1, 1, 1, 1, 1)).astype(np.float32)
+        w2 = (q_w2.astype(np.float32) * s_w2.reshape(-1, 1, 1, 1, 1)).astype(np.float32)
+        h = _fake_quant(_silu_ref(_ln_ref(x, blk.gamma, blk.beta)), act_scale(blk.clip1))
+        h = _silu_ref(conv_float(h, nmap, w1, blk.b1))
+        h = _fake_quant(h, act_scale(blk.clip2))
+        x = conv_float(h, nmap, w2, blk.b2) + x
+    return x
+
+
+def step_fakequant(points, lidar, conf, w, *, iters=10, trim=0.2, min_points=32, use_prompt=True, soft_gate=False,
+                   resolution=256.0):
+    """The int8 step as the reference evaluates it on the CPU (fp32 fake quantisation, torch-style LN and exp)."""
+    pts = np.array(points, dtype=np.float32, copy=True)
+    B, H, W, _ = pts.shape
+    M = B * H * W
+    res = gate = None
+    if use_prompt:
+        z, tg, m, d, c = prompt_inputs(pts, lidar, conf)
+        z = np.exp(pts[..., 2]).reshape(B, -1).astype(np.float32)
+        s, t = fit_f64(z, tg, m, iters, trim, min_points)
+        r, g = prompt_feats(pts, d, c, s, t, soft_gate)
+        res, gate = r.reshape(-1), g.reshape(-1)
+    zq, _, _, _ = voxelize(pts, resolution)
+    nmap = nmap_column(zq)
+    x = input_proj(pts.reshape(M, 3), w, res, gate)
+    x = blocks_fakequant(x, nmap, w)
+    x2 = x @ np.asarray(w.out_w, np.float32).reshape(-1) + np.float32(w.out_b[0])
+    pts[..., 2] = pts[..., 2] + x2.reshape(B, H, W).astype(np.float32)
+    return pts

@@ -1,0 +1,338 @@
+// Error plumbing and the fused refiner step (pmg_refiner_*).
+//
+// The step is the refine-loop body of MoGeModel.forward (moge/model/v3.py:547-576) for a single-level refiner,
+// in the order of the reference's device engine (Refiner.swift:224-292): prompt fit, prompt residual/gate,
+// voxelise, neighbour map, input projection, residual blocks, output projection and log-depth update, then the
+// optional metric fit of the refined depth. Everything is enqueued on one stream with no host synchronisation:
+// at level 0 the voxel count is B*H*W, known on the host, so every grid is sized without reading the device.
+// The enqueue sequence is captured once into a HIP graph and replayed while the caller's buffers are unchanged.
+#include <climits>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "pmg_common.h"
+#include "pmg_internal.h"
+
+namespace pmg {
+
+static thread_local std::string g_last_error;
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+
+int fail(int code, const std::string& msg) {
+    set_error(msg);
+    return code;
+}
+
+int check_launch(const char* what) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(PMG_E_HIP, std::string(what) + ": launch failed: " + hipGetErrorString(e));
+    return PMG_OK;
+}
+
+int num_cus() {
+    static int cached[64];
+    static bool init[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!init[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+        init[dev] = true;
+    }
+    return cached[dev];
+}
+
+}  // namespace pmg
+
+using namespace pmg;
+
+struct pmg_refiner {
+    pmg_refiner_config cfg{};
+    int64_t M = 0;
+    bool have_weights = false;
+    pmg_refiner_weights w{};
+    std::vector<pmg_block_weights> blocks;
+
+    void* arena = nullptr;
+    size_t arena_bytes = 0;
+    int32_t* zq = nullptr;
+    int32_t* zmin = nullptr;
+    int32_t* zmax = nullptr;
+    int32_t* nmap_t = nullptr;
+    uint32_t* tmask = nullptr;
+    float* x = nullptr;
+    void* q1 = nullptr;
+    void* q2 = nullptr;
+    float* st_scratch = nullptr;
+    void* fit_ws[2] = {nullptr, nullptr};
+    size_t fit_ws_bytes = 0;
+
+    // Captured steps, keyed by (points, points_out, lidar, conf, st_prompt, st_final, stream); a ping-pong of
+    // two point buffers over K steps uses two entries.
+    struct Graph {
+        const void* key[7];
+        hipGraph_t graph;
+        hipGraphExec_t exec;
+    };
+    std::vector<Graph> graphs;
+};
+
+static size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+static void drop_graphs(pmg_refiner* r) {
+    for (auto& g : r->graphs) {
+        hipGraphExecDestroy(g.exec);
+        hipGraphDestroy(g.graph);
+    }
+    r->graphs.clear();
+}
+
+constexpr size_t kMaxGraphs = 4;
+
+// Enqueues one step on `s`.
+static int enqueue_step(pmg_refiner* r, const float* points, float* points_out, const float* lidar,
+                        const float* conf, float* st_prompt, float* st_final, hipStream_t s) {
+    const pmg_refiner_config& c = r->cfg;
+    const bool f16 = c.precision == PMG_PREC_FP16;
+    const int64_t M = r->M;
+    const int C = c.C;
+    float* st = st_prompt ? st_prompt : r->st_scratch;
+    if (c.use_prompt) {
+        FitLaunch f{};
+        f.mode = 1;
+        f.logz = points + 2;
+        f.stride = 3;
+        f.lidar = lidar;
+        f.conf = conf;
+        f.B = c.B;
+        f.H = c.H;
+        f.W = c.W;
+        f.dh = c.dh;
+        f.dw = c.dw;
+        f.N = (int64_t)c.H * c.W;
+        f.iters = c.fit_iters;
+        f.trim = c.fit_trim;
+        f.min_points = c.fit_min_points;
+        f.st = st;
+        f.info = nullptr;
+        f.workspace = r->fit_ws[0];
+        f.workspace_bytes = r->fit_ws_bytes;
+        if (int e = launch_fit(f, s)) return e;
+    }
+    if (int e = pmg_voxelize(points + 2, 3, c.B, c.H, c.W, c.depth_resolution, r->zq, r->zmin, r->zmax, s)) return e;
+    if (int e = pmg_nmap_column(r->zq, r->zmin, c.B, c.H, c.W, r->nmap_t, nullptr, r->tmask, nullptr, s)) return e;
+
+    const pmg_block_weights& b0 = r->blocks[0];
+    InputStage in{points, c.B, c.H, c.W, C, lidar, conf, c.dh, c.dw, st, c.use_prompt, c.soft_gate,
+                  r->w.in_w, r->w.in_b, r->w.pr_w, r->w.pr_b, r->x, b0.ln_gamma, b0.ln_beta, 1e-6f,
+                  b0.a1_scale, r->q1};
+    if (int e = launch_input_stage(in, f16, s)) return e;
+
+    const int nbk = (int)r->blocks.size();
+    for (int k = 0; k < nbk; ++k) {
+        const pmg_block_weights& bk = r->blocks[k];
+        if (k > 0) {
+            if (int e = launch_ln_silu(r->x, M, C, bk.ln_gamma, bk.ln_beta, 1e-6f, bk.a1_scale, r->q1, f16, s))
+                return e;
+        }
+        if (f16) {
+            if (int e = pmg_spconv_f16((const uint16_t*)r->q1, r->nmap_t, r->tmask, M, C, C, (const uint16_t*)bk.w1,
+                                       PMG_EPI_SILU, bk.b1, nullptr, r->q2, s))
+                return e;
+            if (int e = pmg_spconv_f16((const uint16_t*)r->q2, r->nmap_t, r->tmask, M, C, C, (const uint16_t*)bk.w2,
+                                       PMG_EPI_R, bk.b2, r->x, r->x, s))
+                return e;
+        } else {
+            if (int e = pmg_spconv_i8((const int8_t*)r->q1, r->nmap_t, r->tmask, M, C, C, (const int8_t*)bk.w1,
+                                      PMG_EPI_Q, bk.a1_scale, bk.w1_scale, bk.b1, bk.a2_scale, nullptr, r->q2, s))
+                return e;
+            if (int e = pmg_spconv_i8((const int8_t*)r->q2, r->nmap_t, r->tmask, M, C, C, (const int8_t*)bk.w2,
+                                      PMG_EPI_R, bk.a2_scale, bk.w2_scale, bk.b2, 1.0f, r->x, r->x, s))
+                return e;
+        }
+    }
+    if (int e = launch_out_apply(r->x, M, C, r->w.out_w, r->w.out_b, points, points_out, s)) return e;
+
+    if (c.final_fit) {
+        FitLaunch f{};
+        f.mode = 1;
+        f.logz = points_out + 2;
+        f.stride = 3;
+        f.lidar = lidar;
+        f.conf = conf;
+        f.B = c.B;
+        f.H = c.H;
+        f.W = c.W;
+        f.dh = c.dh;
+        f.dw = c.dw;
+        f.N = (int64_t)c.H * c.W;
+        f.iters = c.fit_iters;
+        f.trim = c.fit_trim;
+        f.min_points = c.fit_min_points;
+        f.st = st_final ? st_final : r->st_scratch + 2 * c.B;
+        f.info = nullptr;
+        f.workspace = r->fit_ws[1];
+        f.workspace_bytes = r->fit_ws_bytes;
+        if (int e = launch_fit(f, s)) return e;
+    }
+    return PMG_OK;
+}
+
+extern "C" {
+
+const char* pmg_last_error(void) { return g_last_error.c_str(); }
+
+int pmg_version(void) { return 1; }
+
+pmg_refiner* pmg_refiner_create(const pmg_refiner_config* cfg) {
+    if (!cfg) {
+        set_error("pmg_refiner_create: null config");
+        return nullptr;
+    }
+    const pmg_refiner_config& c = *cfg;
+    if (c.B < 1 || c.H < 1 || c.W < 1 || (int64_t)c.B * c.H * c.W > INT_MAX / 27 || !supported_width(c.C) ||
+        c.n_blocks < 1 || (c.precision != PMG_PREC_INT8 && c.precision != PMG_PREC_FP16) || c.dh < 1 || c.dw < 1 ||
+        c.fit_iters < 0 || c.fit_iters > 64 || c.fit_min_points < 1 || !(c.fit_trim >= 0.0f && c.fit_trim < 1.0f) ||
+        (int64_t)c.H * c.W > ((int64_t)1 << 22)) {
+        set_error("pmg_refiner_create: unsupported configuration");
+        return nullptr;
+    }
+    pmg_refiner* r = new pmg_refiner();
+    r->cfg = c;
+    r->M = (int64_t)c.B * c.H * c.W;
+    const int64_t M = r->M;
+    const size_t elt = c.precision == PMG_PREC_FP16 ? 2 : 1;
+    r->fit_ws_bytes = align_up(fit_workspace_bytes((int64_t)c.H * c.W, c.fit_iters), 256);
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = off;
+        off = align_up(off + bytes, 256);
+        return o;
+    };
+    const size_t o_zq = take(M * 4), o_zmin = take(c.B * 4), o_zmax = take(c.B * 4);
+    const size_t o_nmap = take(27 * M * 4), o_tm = take(((M + 15) / 16) * 4);
+    const size_t o_x = take(M * c.C * 4), o_q1 = take(M * c.C * elt), o_q2 = take(M * c.C * elt);
+    const size_t o_st = take(4 * c.B * 4), o_f0 = take(r->fit_ws_bytes), o_f1 = take(r->fit_ws_bytes);
+    r->arena_bytes = off;
+    if (hipMalloc(&r->arena, r->arena_bytes) != hipSuccess) {
+        set_error("pmg_refiner_create: hipMalloc of " + std::to_string(r->arena_bytes) + " bytes failed");
+        delete r;
+        return nullptr;
+    }
+    if (hipMemset(r->arena, 0, r->arena_bytes) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+        set_error("pmg_refiner_create: clearing the workspace failed");
+        hipFree(r->arena);
+        delete r;
+        return nullptr;
+    }
+    uint8_t* a = (uint8_t*)r->arena;
+    r->zq = (int32_t*)(a + o_zq);
+    r->zmin = (int32_t*)(a + o_zmin);
+    r->zmax = (int32_t*)(a + o_zmax);
+    r->nmap_t = (int32_t*)(a + o_nmap);
+    r->tmask = (uint32_t*)(a + o_tm);
+    r->x = (float*)(a + o_x);
+    r->q1 = a + o_q1;
+    r->q2 = a + o_q2;
+    r->st_scratch = (float*)(a + o_st);
+    r->fit_ws[0] = a + o_f0;
+    r->fit_ws[1] = a + o_f1;
+    return r;
+}
+
+void pmg_refiner_destroy(pmg_refiner* r) {
+    if (!r) return;
+    drop_graphs(r);
+    if (r->arena) hipFree(r->arena);
+    delete r;
+}
+
+int pmg_refiner_set_weights(pmg_refiner* r, const pmg_refiner_weights* w) {
+    PMG_REQUIRE(r && w, "null argument");
+    PMG_REQUIRE(w->n_blocks == r->cfg.n_blocks && w->blocks, "block count mismatch");
+    PMG_REQUIRE(w->in_w && w->in_b && w->out_w && w->out_b, "missing projection weights");
+    PMG_REQUIRE(!r->cfg.use_prompt || (w->pr_w && w->pr_b), "use_prompt needs prompt_proj weights");
+    const bool i8 = r->cfg.precision == PMG_PREC_INT8;
+    for (int k = 0; k < w->n_blocks; ++k) {
+        const pmg_block_weights& b = w->blocks[k];
+        PMG_REQUIRE(b.ln_gamma && b.ln_beta && b.w1 && b.b1 && b.w2 && b.b2, "missing block weights");
+        PMG_REQUIRE(aligned16(b.w1) && aligned16(b.w2), "conv weights must be 16-byte aligned");
+        if (i8)
+            PMG_REQUIRE(b.w1_scale && b.w2_scale && b.a1_scale > 0.0f && b.a2_scale > 0.0f,
+                        "int8 blocks need weight and activation scales");
+    }
+    r->w = *w;
+    r->blocks.assign(w->blocks, w->blocks + w->n_blocks);
+    r->w.blocks = nullptr;
+    r->have_weights = true;
+    drop_graphs(r);
+    return PMG_OK;
+}
+
+int pmg_refiner_step(pmg_refiner* r, const float* points, float* points_out, const float* lidar, const float* conf,
+                     float* st_prompt, float* st_final, void* stream) {
+    PMG_REQUIRE(r && r->have_weights, "weights not set");
+    PMG_REQUIRE(points && points_out, "null points");
+    PMG_REQUIRE((!r->cfg.use_prompt && !r->cfg.final_fit) || (lidar && conf), "LiDAR inputs required");
+    hipStream_t s = (hipStream_t)stream;
+    // The legacy default stream cannot be captured; on it the step is enqueued eagerly.
+    if (!r->cfg.use_graph || s == nullptr)
+        return enqueue_step(r, points, points_out, lidar, conf, st_prompt, st_final, s);
+    const void* key[7] = {points, points_out, lidar, conf, st_prompt, st_final, stream};
+    for (auto& g : r->graphs)
+        if (std::memcmp(g.key, key, sizeof key) == 0) {
+            PMG_CHECK_HIP(hipGraphLaunch(g.exec, s));
+            return PMG_OK;
+        }
+    if (r->graphs.size() >= kMaxGraphs) drop_graphs(r);
+    PMG_CHECK_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    const int e = enqueue_step(r, points, points_out, lidar, conf, st_prompt, st_final, s);
+    hipGraph_t graph = nullptr;
+    const hipError_t ce = hipStreamEndCapture(s, &graph);
+    if (e) {
+        if (graph) hipGraphDestroy(graph);
+        return e;
+    }
+    if (ce != hipSuccess) return fail(PMG_E_HIP, std::string("hipStreamEndCapture: ") + hipGetErrorString(ce));
+    hipGraphExec_t exec = nullptr;
+    const hipError_t ie = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    if (ie != hipSuccess) {
+        hipGraphDestroy(graph);
+        return fail(PMG_E_HIP, std::string("hipGraphInstantiate: ") + hipGetErrorString(ie));
+    }
+    pmg_refiner::Graph g{};
+    std::memcpy(g.key, key, sizeof key);
+    g.graph = graph;
+    g.exec = exec;
+    r->graphs.push_back(g);
+    PMG_CHECK_HIP(hipGraphLaunch(exec, s));
+    return PMG_OK;
+}
+
+int pmg_refiner_check(pmg_refiner* r, void* stream) {
+    PMG_REQUIRE(r, "null refiner");
+    PMG_CHECK_HIP(hipStreamSynchronize((hipStream_t)stream));
+    int err[2] = {0, 0};
+    for (int k = 0; k < 2; ++k)
+        PMG_CHECK_HIP(hipMemcpy(&err[k], (uint8_t*)r->fit_ws[k] + 4, sizeof(int), hipMemcpyDeviceToHost));
+    if (err[0] || err[1]) return fail(PMG_E_DEVICE, "pmg_refiner_check: a device-wide wait in the metric fit expired");
+    return PMG_OK;
+}
+
+const void* pmg_refiner_buffer(pmg_refiner* r, int id) {
+    if (!r) return nullptr;
+    switch (id) {
+        case 0: return r->zq;
+        case 1: return r->nmap_t;
+        case 2: return r->tmask;
+        case 3: return r->x;
+        case 4: return r->q1;
+        case 5: return r->q2;
+        default: return nullptr;
+    }
+}
+
+}  // extern "C"

@@ -1,0 +1,59 @@
+// Launchers shared between translation units (not part of the C ABI).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pmg {
+
+bool supported_width(int C);
+
+int launch_ln_silu(const float* x, int64_t M, int C, const float* gamma, const float* beta, float eps,
+                   float out_scale, void* out, bool f16, hipStream_t s);
+
+struct InputStage {
+    const float* points;
+    int B, H, W, C;
+    const float* lidar;
+    const float* conf;
+    int dh, dw;
+    const float* st;
+    int use_prompt, soft_gate;
+    const float* in_w;
+    const float* in_b;
+    const float* pr_w;
+    const float* pr_b;
+    float* x_out;
+    const float* gamma;
+    const float* beta;
+    float eps;
+    float out_scale;
+    void* q_out;
+};
+int launch_input_stage(const InputStage& in, bool f16, hipStream_t s);
+
+int launch_out_apply(const float* x, int64_t M, int C, const float* w, const float* b, const float* points,
+                     float* points_out, hipStream_t s);
+
+struct FitLaunch {
+    int mode;
+    const float* z;
+    const float* tg;
+    const uint8_t* mask;
+    const float* logz;
+    int64_t stride;
+    const float* lidar;
+    const float* conf;
+    int B, H, W, dh, dw;
+    int64_t N;
+    int iters;
+    float trim;
+    int min_points;
+    float* st;
+    int32_t* info;
+    void* workspace;
+    size_t workspace_bytes;
+};
+size_t fit_workspace_bytes(int64_t N, int iters);
+int launch_fit(const FitLaunch& f, hipStream_t s);
+
+}  // namespace pmg

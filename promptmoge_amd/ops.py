@@ -1,0 +1,239 @@
+"""Torch-facing wrappers of the libpmg entry points.
+
+Tensors are device tensors (HIP); every call enqueues on torch's current stream and returns without synchronising.
+Inputs are validated here (device, dtype, shape, contiguity) before the C ABI validates them again.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from typing import Optional, Sequence, Tuple
+
+import torch
+
+from . import _lib
+from ._lib import EPI_ACC, EPI_BIAS, EPI_Q, EPI_R, EPI_SILU, call, lib
+
+__all__ = [
+    "voxelize", "nmap_column", "nmap_hash", "nmap_from_rows", "kmap_compact", "spconv_i8", "spconv_f16",
+    "spconv_f32", "ln_silu_quant", "ln_silu_f16", "fit_scale_shift", "fit_prompt", "math_device",
+    "EPI_ACC", "EPI_Q", "EPI_R", "EPI_BIAS", "EPI_SILU",
+]
+
+
+def _stream() -> C.c_void_p:
+    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _p(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _dev(t: torch.Tensor, name: str, dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor")
+    if dtype is not None and t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    return t
+
+
+def math_device(op: int, x: torch.Tensor) -> torch.Tensor:
+    x = _dev(x, "x", torch.float32)
+    out = torch.empty_like(x)
+    call("pmg_math_device", op, _p(x), _p(out), x.numel(), _stream())
+    return out
+
+
+# ------------------------------------------------------------------------------------------------------------- (1)
+def voxelize(logz: torch.Tensor, resolution: float = 256.0, stride: int = 1,
+             shape: Optional[Tuple[int, int, int]] = None):
+    """zq = rint(logz * resolution) and per-batch (min, max). logz: [B, H, W] (stride 1) or the point map
+    [B, H, W, 3] viewed from its third channel (pass points[..., 2:] with stride 3 and shape=(B, H, W))."""
+    if shape is None:
+        B, H, W = logz.shape
+    else:
+        B, H, W = shape
+    dev = logz.device
+    zq = torch.empty((B, H, W), dtype=torch.int32, device=dev)
+    zmin = torch.empty((B,), dtype=torch.int32, device=dev)
+    zmax = torch.empty((B,), dtype=torch.int32, device=dev)
+    call("pmg_voxelize", _p(logz), stride, B, H, W, float(resolution), _p(zq), _p(zmin), _p(zmax), _stream())
+    return zq, zmin, zmax
+
+
+# ------------------------------------------------------------------------------------------------------------- (2)
+def nmap_column(zq: torch.Tensor, zmin: Optional[torch.Tensor] = None, *, taps: bool = True, rows: bool = False,
+                coords: bool = False):
+    """Level-0 column-stencil map. Returns (nmap_t [27, M] | None, tile_mask [ceil(M/16)], nmap_rows [M, 27] | None,
+    coords [M, 4] | None)."""
+    zq = _dev(zq, "zq", torch.int32)
+    B, H, W = zq.shape
+    M = B * H * W
+    dev = zq.device
+    nt = torch.empty((27, M), dtype=torch.int32, device=dev) if taps else None
+    nr = torch.empty((M, 27), dtype=torch.int32, device=dev) if rows else None
+    tm = torch.empty(((M + 15) // 16,), dtype=torch.int32, device=dev)
+    cd = torch.empty((M, 4), dtype=torch.int32, device=dev) if coords else None
+    if coords and zmin is None:
+        raise ValueError("coords need zmin")
+    call("pmg_nmap_column", _p(zq), _p(zmin), B, H, W, _p(nt), _p(nr), _p(tm), _p(cd), _stream())
+    return nt, tm, nr, cd
+
+
+def nmap_hash(coords: torch.Tensor, sparse_shape: Sequence[int], *, taps: bool = True, rows: bool = False):
+    """Generic map over unique (b, x, y, z) coords. Returns (nmap_t [27, M] | None, tile_mask, nmap_rows | None)."""
+    coords = _dev(coords, "coords", torch.int32)
+    if coords.ndim != 2 or coords.shape[1] != 4:
+        raise ValueError("coords must be (M, 4)")
+    M = coords.shape[0]
+    dev = coords.device
+    nt = torch.empty((27, M), dtype=torch.int32, device=dev) if taps else None
+    nr = torch.empty((M, 27), dtype=torch.int32, device=dev) if rows else None
+    tm = torch.empty(((M + 15) // 16,), dtype=torch.int32, device=dev)
+    ws_bytes = lib().pmg_hash_workspace_bytes(M)
+    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
+    shape = (C.c_int64 * 4)(*[int(s) for s in sparse_shape[:4]])
+    call("pmg_nmap_hash", _p(coords), M, shape, _p(nt), _p(nr), _p(tm), _p(ws), ws_bytes, _stream())
+    return nt, tm, nr
+
+
+def nmap_from_rows(nmap_rows: torch.Tensor):
+    """(M, 27) map -> (nmap_t [27, M], tile_mask)."""
+    nmap_rows = _dev(nmap_rows, "nmap_rows", torch.int32)
+    M = nmap_rows.shape[0]
+    nt = torch.empty((27, M), dtype=torch.int32, device=nmap_rows.device)
+    tm = torch.empty(((M + 15) // 16,), dtype=torch.int32, device=nmap_rows.device)
+    call("pmg_nmap_from_rows", _p(nmap_rows), M, _p(nt), _p(tm), _stream())
+    return nt, tm
+
+
+def kmap_compact(nmap_t: torch.Tensor, capacity: Optional[int] = None):
+    """Per-tap compacted kernel maps: (offsets [28] int64, out_rows, in_rows). Synchronises the stream."""
+    nmap_t = _dev(nmap_t, "nmap_t", torch.int32)
+    M = nmap_t.shape[1]
+    cap = 27 * M if capacity is None else int(capacity)
+    dev = nmap_t.device
+    off = torch.empty((28,), dtype=torch.int64, device=dev)
+    out_rows = torch.empty((max(cap, 1),), dtype=torch.int32, device=dev)
+    in_rows = torch.empty((max(cap, 1),), dtype=torch.int32, device=dev)
+    ws_bytes = lib().pmg_kmap_workspace_bytes(M)
+    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
+    call("pmg_kmap_compact", _p(nmap_t), M, _p(off), _p(out_rows), _p(in_rows), cap, _p(ws), ws_bytes, _stream())
+    total = int(off[27].item())
+    return off, out_rows[:total], in_rows[:total]
+
+
+# ------------------------------------------------------------------------------------------------------------- (3)
+def _conv_out(M: int, Co: int, epilogue: int, elt: str, dev) -> torch.Tensor:
+    if elt == "i8":
+        dt = {EPI_ACC: torch.int32, EPI_Q: torch.int8}.get(epilogue, torch.float32)
+    elif elt == "f16":
+        dt = torch.float16 if epilogue == EPI_SILU else torch.float32
+    else:
+        dt = torch.float32
+    return torch.empty((M, Co), dtype=dt, device=dev)
+
+
+def spconv_i8(x: torch.Tensor, nmap_t: torch.Tensor, tile_mask: torch.Tensor, w: torch.Tensor, epilogue: int = EPI_ACC,
+              *, a_scale: float = 1.0, w_scale: Optional[torch.Tensor] = None, bias: Optional[torch.Tensor] = None,
+              out_scale: float = 1.0, skip: Optional[torch.Tensor] = None,
+              out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """int8 submanifold conv. x: (M, Ci) int8; w: (Co, 3, 3, 3, Ci) or (Co, 27, Ci) int8."""
+    x = _dev(x, "x", torch.int8)
+    w = _dev(w, "w", torch.int8)
+    M, Ci = x.shape
+    Co = w.shape[0]
+    if w.numel() != Co * 27 * Ci:
+        raise ValueError("weight must be (Co, 3, 3, 3, Ci)")
+    if out is None:
+        out = _conv_out(M, Co, epilogue, "i8", x.device)
+    call("pmg_spconv_i8", _p(x), _p(nmap_t), _p(tile_mask), M, Ci, Co, _p(w), epilogue, float(a_scale), _p(w_scale),
+         _p(bias), float(out_scale), _p(skip), _p(out), _stream())
+    return out
+
+
+def spconv_f16(x: torch.Tensor, nmap_t: torch.Tensor, tile_mask: torch.Tensor, w: torch.Tensor,
+               epilogue: int = EPI_ACC, *, bias: Optional[torch.Tensor] = None, skip: Optional[torch.Tensor] = None,
+               out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    x = _dev(x, "x", torch.float16)
+    w = _dev(w, "w", torch.float16)
+    M, Ci = x.shape
+    Co = w.shape[0]
+    if w.numel() != Co * 27 * Ci:
+        raise ValueError("weight must be (Co, 3, 3, 3, Ci)")
+    if out is None:
+        out = _conv_out(M, Co, epilogue, "f16", x.device)
+    call("pmg_spconv_f16", _p(x), _p(nmap_t), _p(tile_mask), M, Ci, Co, _p(w), epilogue, _p(bias), _p(skip), _p(out),
+         _stream())
+    return out
+
+
+def spconv_f32(x: torch.Tensor, nmap_t: torch.Tensor, tile_mask: torch.Tensor, w: torch.Tensor,
+               bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    x = _dev(x, "x", torch.float32)
+    w = _dev(w, "w", torch.float32)
+    M, Ci = x.shape
+    Co = w.shape[0]
+    if w.numel() != Co * 27 * Ci:
+        raise ValueError("weight must be (Co, 3, 3, 3, Ci)")
+    out = torch.empty((M, Co), dtype=torch.float32, device=x.device)
+    call("pmg_spconv_f32", _p(x), _p(nmap_t), _p(tile_mask), M, Ci, Co, _p(w),
+         EPI_BIAS if bias is not None else EPI_ACC, _p(bias), _p(out), _stream())
+    return out
+
+
+def ln_silu_quant(x: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, out_scale: float,
+                  eps: float = 1e-6) -> torch.Tensor:
+    x = _dev(x, "x", torch.float32)
+    M, Cc = x.shape
+    q = torch.empty((M, Cc), dtype=torch.int8, device=x.device)
+    call("pmg_ln_silu_quant", _p(x), M, Cc, _p(gamma), _p(beta), float(eps), float(out_scale), _p(q), _stream())
+    return q
+
+
+def ln_silu_f16(x: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    x = _dev(x, "x", torch.float32)
+    M, Cc = x.shape
+    h = torch.empty((M, Cc), dtype=torch.float16, device=x.device)
+    call("pmg_ln_silu_f16", _p(x), M, Cc, _p(gamma), _p(beta), float(eps), _p(h), _stream())
+    return h
+
+
+# ------------------------------------------------------------------------------------------------------------- (4)
+def fit_scale_shift(z: torch.Tensor, target: torch.Tensor, mask: torch.Tensor, iters: int = 4, trim: float = 0.2,
+                    min_points: int = 32, return_info: bool = False):
+    """fit_scale_shift (prompt_stem.py:211-240) on the GPU. z, target: [B, N] fp32; mask: [B, N] bool/uint8.
+    Returns s, t: [B] (and info [B, 5] int32 = count, k, ok, threshold bits, error flag)."""
+    z = _dev(z.float().reshape(z.shape[0], -1).contiguous(), "z")
+    target = _dev(target.float().reshape(target.shape[0], -1).contiguous(), "target")
+    m8 = _dev(mask.reshape(mask.shape[0], -1).to(torch.uint8).contiguous(), "mask")
+    B, N = z.shape
+    st = torch.empty((B, 2), dtype=torch.float32, device=z.device)
+    info = torch.zeros((B, 5), dtype=torch.int32, device=z.device)
+    ws_bytes = lib().pmg_fit_workspace_bytes(N, iters)
+    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=z.device)
+    call("pmg_fit_scale_shift", _p(z), _p(target), _p(m8), B, N, int(iters), float(trim), int(min_points), _p(st),
+         _p(info), _p(ws), ws_bytes, _stream())
+    if return_info:
+        return st[:, 0], st[:, 1], info
+    return st[:, 0], st[:, 1]
+
+
+def fit_prompt(points: torch.Tensor, lidar: torch.Tensor, conf: torch.Tensor, iters: int = 4, trim: float = 0.2,
+               min_points: int = 32, return_info: bool = False):
+    """Prompt fit of _lidar_in_affine_frame (v3.py:362-378) on the point map [B, H, W, 3] and LiDAR [B, dh, dw]."""
+    points = _dev(points, "points", torch.float32)
+    lidar = _dev(lidar.float().contiguous(), "lidar")
+    conf = _dev(conf.float().contiguous(), "conf")
+    B, H, W, _ = points.shape
+    dh, dw = lidar.shape[-2:]
+    st = torch.empty((B, 2), dtype=torch.float32, device=points.device)
+    info = torch.zeros((B, 5), dtype=torch.int32, device=points.device)
+    ws_bytes = lib().pmg_fit_workspace_bytes(H * W, iters)
+    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=points.device)
+    call("pmg_fit_prompt", points.data_ptr() + 8, 3, _p(lidar), _p(conf), B, H, W, dh, dw, int(iters), float(trim),
+         int(min_points), _p(st), _p(info), _p(ws), ws_bytes, _stream())
+    if return_info:
+        return st[:, 0], st[:, 1], info
+    return st[:, 0], st[:, 1]

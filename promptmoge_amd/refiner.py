@@ -1,0 +1,137 @@
+"""The fused refiner step on the GPU, behind a host object and behind the reference's refiner-module interface.
+
+`RefinerStep` owns a libpmg refiner context (persistent workspace, HIP graph) and runs one refinement step of the
+refine loop (moge/model/v3.py:547-576) with no host synchronisation:
+
+    prompt fit (fit_scale_shift)  ->  residual/gate  ->  voxelise  ->  neighbour map  ->  input_proj + prompt_proj
+    ->  residual blocks  ->  out_proj  ->  logz += delta            [->  metric fit of the refined depth]
+
+The refined point map (x/z, y/z, logz + delta) is written to `out`, which may be the input itself; that is the
+reference loop's `current_coord = cat(xy, refined_logz)` (v3.py:574).
+"""
+from __future__ import annotations
+
+import ctypes as C
+from typing import List, Optional
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._lib import BlockWeights, RefinerConfig, RefinerWeights, call, lib
+from .spec import RefinerW, act_scale, quantize_weight
+
+
+class DeviceWeights:
+    """A RefinerW uploaded to the GPU in the layouts the kernels read. int8: per-output-channel quantised conv
+    weights in the module layout (Co, 3, 3, 3, Ci) with fp32 scales; fp16: fp16 conv weights."""
+
+    def __init__(self, w: RefinerW, precision: str, device="cuda"):
+        self.precision = precision
+        self.C = w.C
+        t = lambda a, dt=torch.float32: torch.as_tensor(np.ascontiguousarray(a)).to(device=device, dtype=dt)
+        self.in_w, self.in_b = t(w.in_w), t(w.in_b)
+        self.pr_w, self.pr_b = t(w.pr_w), t(w.pr_b)
+        self.out_w, self.out_b = t(w.out_w), t(w.out_b)
+        self.blocks = []
+        for b in w.blocks:
+            d = {"gamma": t(b.gamma), "beta": t(b.beta), "b1": t(b.b1), "b2": t(b.b2)}
+            if precision == "int8":
+                q1, s1 = quantize_weight(b.w1)
+                q2, s2 = quantize_weight(b.w2)
+                d.update(w1=t(q1, torch.int8), s1=t(s1), w2=t(q2, torch.int8), s2=t(s2),
+                         a1=float(act_scale(b.clip1)), a2=float(act_scale(b.clip2)))
+            else:
+                d.update(w1=t(b.w1, torch.float16), w2=t(b.w2, torch.float16), s1=None, s2=None, a1=1.0, a2=1.0)
+            self.blocks.append(d)
+        self._struct_blocks = (BlockWeights * len(self.blocks))()
+        for k, d in enumerate(self.blocks):
+            p = lambda x: None if x is None else x.data_ptr()
+            self._struct_blocks[k] = BlockWeights(
+                p(d["gamma"]), p(d["beta"]), p(d["w1"]), p(d["s1"]), p(d["b1"]), d["a1"],
+                p(d["w2"]), p(d["s2"]), p(d["b2"]), d["a2"])
+        self.struct = RefinerWeights(
+            self.in_w.data_ptr(), self.in_b.data_ptr(), self.pr_w.data_ptr(), self.pr_b.data_ptr(),
+            self.out_w.data_ptr(), self.out_b.data_ptr(), len(self.blocks),
+            C.cast(self._struct_blocks, C.POINTER(BlockWeights)))
+
+
+class RefinerStep:
+    """One fused refinement step for point maps of a fixed size.
+
+    points [B, H, W, 3] fp32 (x/z, y/z, logz) is refined in place; lidar, conf [B, dh, dw] fp32.
+    Returns the prompt fit (s, t) [B, 2] and, if `final_fit`, the metric fit of the refined depth [B, 2].
+    """
+
+    def __init__(self, weights: RefinerW, B: int, H: int, W: int, dh: Optional[int] = None,
+                 dw: Optional[int] = None, *, precision: str = "int8", depth_resolution: float = 256.0,
+                 fit_iters: int = 4, fit_trim: float = 0.2, fit_min_points: int = 32, use_prompt: bool = True,
+                 soft_gate: bool = False, final_fit: bool = False, use_graph: bool = True, device="cuda"):
+        if precision not in ("int8", "fp16"):
+            raise ValueError("precision must be 'int8' or 'fp16'")
+        self.B, self.H, self.W = B, H, W
+        self.dh, self.dw = dh or H, dw or W
+        self.final_fit = final_fit
+        self.weights = DeviceWeights(weights, precision, device)
+        cfg = RefinerConfig(B, H, W, weights.C, len(weights.blocks),
+                            _lib.PREC_INT8 if precision == "int8" else _lib.PREC_FP16, float(depth_resolution),
+                            self.dh, self.dw, int(fit_iters), float(fit_trim), int(fit_min_points), int(use_prompt),
+                            int(soft_gate), int(final_fit), int(use_graph))
+        self._h = lib().pmg_refiner_create(C.byref(cfg))
+        if not self._h:
+            raise _lib.PmgError(_lib.PMG_E_INVALID, lib().pmg_last_error().decode())
+        call("pmg_refiner_set_weights", self._h, C.byref(self.weights.struct))
+        self.st_prompt = torch.zeros((B, 2), dtype=torch.float32, device=device)
+        self.st_final = torch.zeros((B, 2), dtype=torch.float32, device=device)
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            lib().pmg_refiner_destroy(h)
+            self._h = None
+
+    def __call__(self, points: torch.Tensor, lidar: torch.Tensor, conf: torch.Tensor,
+                 out: Optional[torch.Tensor] = None):
+        """Refines `points` into `out` (default: in place). Returns (st_prompt [B, 2], st_final [B, 2] | None)."""
+        out = points if out is None else out
+        for name, t in (("points", points), ("out", out)):
+            if t.shape != (self.B, self.H, self.W, 3) or t.dtype != torch.float32 or not t.is_contiguous():
+                raise ValueError(f"{name} must be a contiguous fp32 [{self.B}, {self.H}, {self.W}, 3] tensor")
+        for name, t in (("lidar", lidar), ("conf", conf)):
+            if t.shape != (self.B, self.dh, self.dw) or t.dtype != torch.float32 or not t.is_contiguous():
+                raise ValueError(f"{name} must be a contiguous fp32 [{self.B}, {self.dh}, {self.dw}] tensor")
+        stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+        call("pmg_refiner_step", self._h, points.data_ptr(), out.data_ptr(), lidar.data_ptr(), conf.data_ptr(),
+             self.st_prompt.data_ptr(), self.st_final.data_ptr() if self.final_fit else None, stream)
+        return self.st_prompt, (self.st_final if self.final_fit else None)
+
+    def check(self) -> None:
+        """Synchronises and raises if a device-side bounded wait expired."""
+        call("pmg_refiner_check", self._h, C.c_void_p(torch.cuda.current_stream().cuda_stream))
+
+    def buffer(self, which: str) -> torch.Tensor:
+        """A copy of an internal buffer of the last step (parity tests): zq, nmap_t, tile_mask, x, q1, q2."""
+        ids = {"zq": 0, "nmap_t": 1, "tile_mask": 2, "x": 3, "q1": 4, "q2": 5}
+        M, Cc = self.B * self.H * self.W, self.weights.C
+        f16 = self.weights.precision == "fp16"
+        shape, dt = {
+            "zq": ((M,), torch.int32), "nmap_t": ((27, M), torch.int32), "tile_mask": (((M + 15) // 16,), torch.int32),
+            "x": ((M, Cc), torch.float32), "q1": ((M, Cc), torch.float16 if f16 else torch.int8),
+            "q2": ((M, Cc), torch.float16 if f16 else torch.int8),
+        }[which]
+        ptr = lib().pmg_refiner_buffer(self._h, ids[which])
+        out = torch.empty(shape, dtype=dt, device=self.st_prompt.device)
+        nbytes = out.numel() * out.element_size()
+        torch.cuda.current_stream().synchronize()
+        _copy_device(out.data_ptr(), ptr, nbytes)
+        return out
+
+
+def _copy_device(dst: int, src: int, nbytes: int) -> None:
+    """Synchronous device-to-device copy of a raw buffer (the HIP runtime torch already loaded)."""
+    hip = C.CDLL("libamdhip64.so")
+    hip.hipMemcpy.restype = C.c_int
+    hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    rc = hip.hipMemcpy(C.c_void_p(dst), C.c_void_p(src), C.c_size_t(nbytes), 3)  # hipMemcpyDeviceToDevice
+    if rc != 0:
+        raise RuntimeError(f"hipMemcpy failed with {rc}")

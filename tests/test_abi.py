@@ -1,0 +1,79 @@
+"""The C ABI without a GPU: the library loads, exports every function include/pmg.h declares (with the argument
+count the binding uses), and rejects invalid arguments on the host before any launch."""
+import ctypes as C
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from promptmoge_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "pmg.h"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    decls = re.findall(r"^[A-Za-z_][\w\s\*]*?\b(pmg_\w+)\s*\(([^;]*?)\)\s*;", text, flags=re.M | re.S)
+    out = {}
+    for name, args in decls:
+        args = " ".join(args.split())
+        out[name] = 0 if args in ("", "void") else args.count(",") + 1
+    return out
+
+
+def test_header_parsed():
+    fns = declared_functions()
+    assert "pmg_refiner_step" in fns and "pmg_spconv_i8" in fns and len(fns) >= 20
+
+
+def test_every_declared_symbol_is_exported_and_bound(libpmg):
+    fns = declared_functions()
+    for name, nargs in fns.items():
+        assert hasattr(libpmg, name), name
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes binding"
+        assert len(_lib.SIGNATURES[name][1]) == nargs, f"{name}: binding has {len(_lib.SIGNATURES[name][1])} args, header {nargs}"
+    assert set(_lib.SIGNATURES) == set(fns)
+
+
+def test_version_and_error_string(libpmg):
+    assert libpmg.pmg_version() == 1
+    rc = libpmg.pmg_voxelize(None, 1, 1, 1, 1, 256.0, None, None, None, None)
+    assert rc == _lib.PMG_E_INVALID
+    assert b"null" in libpmg.pmg_last_error()
+
+
+def test_invalid_shapes_rejected_on_host(libpmg):
+    dummy = C.c_void_p(16)  # never dereferenced: validation fails first
+    # Co not a multiple of 16
+    assert libpmg.pmg_spconv_i8(dummy, dummy, dummy, 10, 16, 24, dummy, 0, 1.0, dummy, None, 1.0, None, dummy,
+                                None) == _lib.PMG_E_INVALID
+    # Ci*1 not a multiple of 16
+    assert libpmg.pmg_spconv_i8(dummy, dummy, dummy, 10, 24, 32, dummy, 0, 1.0, dummy, None, 1.0, None, dummy,
+                                None) == _lib.PMG_E_INVALID
+    # fp32 conv with a Q epilogue
+    assert libpmg.pmg_spconv_f32(dummy, dummy, dummy, 10, 16, 16, dummy, 1, None, dummy, None) == _lib.PMG_E_INVALID
+    # unsupported LayerNorm width
+    assert libpmg.pmg_ln_silu_quant(dummy, 10, 40, dummy, dummy, 1e-6, 1.0, dummy, None) == _lib.PMG_E_INVALID
+    # fit: N out of range, workspace too small, min_points < 1
+    assert libpmg.pmg_fit_scale_shift(dummy, dummy, dummy, 1, 0, 4, 0.2, 32, dummy, None, dummy, 1 << 20,
+                                      None) == _lib.PMG_E_INVALID
+    assert libpmg.pmg_fit_scale_shift(dummy, dummy, dummy, 1, 1000, 4, 0.2, 32, dummy, None, dummy, 16,
+                                      None) == _lib.PMG_E_INVALID
+    assert libpmg.pmg_fit_scale_shift(dummy, dummy, dummy, 1, 1000, 4, 0.2, 0, dummy, None, dummy, 1 << 20,
+                                      None) == _lib.PMG_E_INVALID
+    # hash: shape too large for 64-bit keys
+    big = (C.c_int64 * 4)(1 << 20, 1 << 20, 1 << 20, 1 << 20)
+    assert libpmg.pmg_nmap_hash(C.c_void_p(16), 5, big, None, None, None, dummy, 1 << 30, None) == _lib.PMG_E_INVALID
+
+
+def test_refiner_create_rejects_bad_config(libpmg):
+    cfg = _lib.RefinerConfig(1, 8, 8, 40, 1, 0, 256.0, 8, 8, 4, 0.2, 32, 1, 0, 0, 1)  # C=40 unsupported
+    assert not libpmg.pmg_refiner_create(C.byref(cfg))
+    assert b"unsupported" in libpmg.pmg_last_error()
+
+
+def test_workspace_sizes(libpmg):
+    assert libpmg.pmg_hash_workspace_bytes(1_000_000) >= 4 * 1_000_000 * 12
+    assert libpmg.pmg_fit_workspace_bytes(307_200, 10) >= 10 * 3 * 2048 * 4
+    assert libpmg.pmg_kmap_workspace_bytes(1000) >= 27 * 4 * 4

@@ -1,0 +1,257 @@
+"""GPU parity of each kernel family against the oracle on identical seeded inputs.
+
+Integer outputs (voxel keys, neighbour maps, tile masks, compacted kernel maps, int32 accumulators, requantised
+int8) must be bit-exact; the fp32 quantities that feed a rounding (exp, log, SiLU, LayerNorm) are bit-exact too,
+because the kernels and the oracle run the same operation sequence. Tolerances, where used, are written in the test.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import conv as ocv
+from oracle import fit as ofit
+from oracle import numerics as onm
+from oracle import structure as ost
+from promptmoge_amd import ops, spec
+
+from conftest import announce
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(a, dev, dt=None):
+    t = torch.as_tensor(np.ascontiguousarray(a))
+    return t.to(device=dev, dtype=dt) if dt is not None else t.to(dev)
+
+
+def _scene(name="B"):
+    cfg = spec.CONFIGS[name]
+    return cfg, spec.make_scene(cfg)
+
+
+# ---------------------------------------------------------------------------------------------------------- math
+@pytest.mark.parametrize("op", [0, 1, 2])
+def test_math_bits(gpu, op):
+    announce(f"math op={op}")
+    x = np.logspace(-4, 6, 200_001).astype(np.float32) if op == 1 else np.linspace(-90, 90, 200_001, dtype=np.float32)
+    got = ops.math_device(op, _t(x, gpu)).cpu().numpy()
+    ref = [onm.exp_f32, onm.log_f32, onm.silu_f32][op](x)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+# ---------------------------------------------------------------------------------------------------------- structure
+@pytest.mark.parametrize("name", ["B", "A"])
+def test_voxelize_and_column_map(gpu, name):
+    announce(f"voxelize+column map config={name}")
+    cfg, sc = _scene(name)
+    pts = np.stack([sc.points, sc.points * np.float32(1.001)])  # B = 2
+    zq_o, coords_o, Z_o, zmin_o = ost.voxelize(pts)
+    nm_o = ost.nmap_column(zq_o)
+    P = _t(pts, gpu)
+    zq, zmin, zmax = ops.voxelize(P[..., 2:], 256.0, stride=3, shape=pts.shape[:3])
+    nt, tm, nr, cd = ops.nmap_column(zq, zmin, taps=True, rows=True, coords=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(zq.cpu().numpy(), zq_o)
+    assert np.array_equal(zmin.cpu().numpy(), zmin_o)
+    assert int((zmax - zmin).max()) + 1 == Z_o
+    assert np.array_equal(nr.cpu().numpy(), nm_o)
+    assert np.array_equal(nt.cpu().numpy(), nm_o.T)
+    assert np.array_equal(cd.cpu().numpy(), coords_o)
+    assert np.array_equal(tm.cpu().numpy().view(np.uint32), ost.tile_masks(nm_o))
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_hash_map_generic(gpu, seed):
+    announce(f"hash map generic seed={seed}")
+    rng = np.random.default_rng(seed)
+    shape = (2, 40, 50, 60)
+    allc = np.stack(np.meshgrid(*[np.arange(s) for s in shape], indexing="ij"), -1).reshape(-1, 4)
+    coords = allc[rng.random(allc.shape[0]) < 0.15].astype(np.int32)
+    coords = coords[rng.permutation(coords.shape[0])]          # caller's order, not sorted
+    ref = ost.nmap_sorted(coords, shape)
+    nt, tm, nr = ops.nmap_hash(_t(coords, gpu), shape, taps=True, rows=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(nr.cpu().numpy(), ref)
+    assert np.array_equal(nt.cpu().numpy(), ref.T)
+    assert np.array_equal(tm.cpu().numpy().view(np.uint32), ost.tile_masks(ref))
+
+
+def test_hash_map_surface_voxels(gpu):
+    announce("hash map surface voxels 200k")
+    coords = spec.make_voxels(200_000, grid=512, seed=5)
+    shape = (1, 512, 512, 512)
+    ref = ost.nmap_sorted(coords, shape)
+    nt, tm, _ = ops.nmap_hash(_t(coords, gpu), shape)
+    torch.cuda.synchronize()
+    assert np.array_equal(nt.cpu().numpy(), ref.T)
+    occ = (ref >= 0).sum(1).mean()
+    assert 6 <= occ <= 16, occ  # surface-like occupancy
+
+
+def test_kmap_and_rows(gpu):
+    announce("kmap compact + nmap_from_rows")
+    cfg, sc = _scene("B")
+    zq_o, _, _, _ = ost.voxelize(sc.points[None])
+    nm = ost.nmap_column(zq_o)
+    off_o, out_o, in_o = ost.kmap_compact(nm)
+    nt, tm = ops.nmap_from_rows(_t(nm, gpu))
+    off, out_rows, in_rows = ops.kmap_compact(nt)
+    assert np.array_equal(nt.cpu().numpy(), nm.T)
+    assert np.array_equal(tm.cpu().numpy().view(np.uint32), ost.tile_masks(nm))
+    assert np.array_equal(off.cpu().numpy(), off_o)
+    assert np.array_equal(out_rows.cpu().numpy(), out_o) and np.array_equal(in_rows.cpu().numpy(), in_o)
+
+
+# ---------------------------------------------------------------------------------------------------------- conv
+def _map_from_scene(gpu, H=96, W=128, seed=3):
+    cfg = spec.StepConfig("c", H, W, 100.0, 100.0, W / 2, H / 2, 16, 1, "int8", seed=seed)
+    sc = spec.make_scene(cfg)
+    zq_o, _, _, _ = ost.voxelize(sc.points[None])
+    nm = ost.nmap_column(zq_o)
+    nt, tm = ops.nmap_from_rows(_t(nm, gpu))
+    return nm, nt, tm
+
+
+@pytest.mark.parametrize("Ci,Co", [(16, 16), (32, 32), (48, 48), (64, 64), (128, 128), (32, 96), (48, 16)])
+def test_conv_int8_accumulator(gpu, Ci, Co):
+    announce(f"conv int8 acc Ci={Ci} Co={Co}")
+    rng = np.random.default_rng(Ci * 1000 + Co)
+    nm, nt, tm = _map_from_scene(gpu)
+    M = nm.shape[0]
+    x = rng.integers(-127, 128, size=(M, Ci)).astype(np.int8)
+    w = rng.integers(-127, 128, size=(Co, 3, 3, 3, Ci)).astype(np.int8)
+    acc = ops.spconv_i8(_t(x, gpu), nt, tm, _t(w, gpu), ops.EPI_ACC)
+    assert np.array_equal(acc.cpu().numpy(), ocv.conv_acc_int(x, nm, w))
+
+
+def test_conv_int8_generic_map(gpu):
+    announce("conv int8 acc on a hash map")
+    rng = np.random.default_rng(9)
+    coords = spec.make_voxels(60_000, grid=256, seed=8)
+    shape = (1, 256, 256, 256)
+    nm = ost.nmap_sorted(coords, shape)
+    nt, tm, _ = ops.nmap_hash(_t(coords, gpu), shape)
+    x = rng.integers(-127, 128, size=(coords.shape[0], 64)).astype(np.int8)
+    w = rng.integers(-127, 128, size=(64, 3, 3, 3, 64)).astype(np.int8)
+    acc = ops.spconv_i8(_t(x, gpu), nt, tm, _t(w, gpu), ops.EPI_ACC)
+    assert np.array_equal(acc.cpu().numpy(), ocv.conv_acc_int(x, nm, w))
+
+
+@pytest.mark.parametrize("C", [32, 48])
+def test_conv_int8_epilogues(gpu, C):
+    announce(f"conv int8 epilogues C={C}")
+    rng = np.random.default_rng(C)
+    nm, nt, tm = _map_from_scene(gpu)
+    M = nm.shape[0]
+    x = rng.integers(-127, 128, size=(M, C)).astype(np.int8)
+    wf = rng.normal(0, 0.05, size=(C, 3, 3, 3, C)).astype(np.float32)
+    q, s = spec.quantize_weight(wf)
+    b = rng.normal(0, 0.05, size=C).astype(np.float32)
+    a_s, o_s = np.float32(3.0 / 127), np.float32(1.7 / 127)
+    skip = rng.normal(size=(M, C)).astype(np.float32)
+    acc = ocv.conv_acc_int(x, nm, q)
+    X, Wq, S, Bv = _t(x, gpu), _t(q, gpu), _t(s, gpu), _t(b, gpu)
+    out_q = ops.spconv_i8(X, nt, tm, Wq, ops.EPI_Q, a_scale=a_s, w_scale=S, bias=Bv, out_scale=o_s)
+    assert np.array_equal(out_q.cpu().numpy(), ocv.epilogue_q(acc, a_s, s, b, o_s))
+    Sk = _t(skip, gpu)
+    out_r = ops.spconv_i8(X, nt, tm, Wq, ops.EPI_R, a_scale=a_s, w_scale=S, bias=Bv, skip=Sk, out=Sk.clone())
+    assert np.array_equal(out_r.cpu().numpy(), ocv.epilogue_r(acc, a_s, s, b, skip))
+    out_b = ops.spconv_i8(X, nt, tm, Wq, ops.EPI_BIAS, a_scale=a_s, w_scale=S, bias=Bv)
+    assert np.array_equal(out_b.cpu().numpy(), ocv.dequant(acc, a_s, s, b))
+
+
+@pytest.mark.parametrize("C", [32, 64])
+def test_conv_f16(gpu, C):
+    announce(f"conv fp16 C={C}")
+    rng = np.random.default_rng(100 + C)
+    nm, nt, tm = _map_from_scene(gpu)
+    M = nm.shape[0]
+    x = rng.normal(size=(M, C)).astype(np.float16)
+    w = rng.normal(0, 0.05, size=(C, 3, 3, 3, C)).astype(np.float16)
+    b = rng.normal(0, 0.05, size=C).astype(np.float32)
+    ref = ocv.conv_float(x.astype(np.float64), nm, w.astype(np.float64), dtype=np.float64)
+    got = ops.spconv_f16(_t(x, gpu), nt, tm, _t(w, gpu), ops.EPI_ACC).cpu().numpy()
+    # fp32 accumulation of exact fp16 products: error bound ~ n_terms * eps32 * sum|terms|
+    bound = 27 * C * 2 ** -23 * ocv.conv_float(np.abs(x.astype(np.float64)), nm, np.abs(w.astype(np.float64)),
+                                                dtype=np.float64)
+    assert (np.abs(got - ref) <= bound + 1e-6).all()
+    h = ops.spconv_f16(_t(x, gpu), nt, tm, _t(w, gpu), ops.EPI_SILU, bias=_t(b, gpu)).cpu().numpy()
+    hr = onm.silu_f32((got + b).astype(np.float32)).astype(np.float16)  # from the kernel's own accumulator
+    assert np.array_equal(h.view(np.uint16), hr.view(np.uint16))
+
+
+def test_conv_f32(gpu):
+    announce("conv fp32")
+    rng = np.random.default_rng(7)
+    nm, nt, tm = _map_from_scene(gpu)
+    M = nm.shape[0]
+    x = rng.normal(size=(M, 24)).astype(np.float32)
+    w = rng.normal(0, 0.05, size=(32, 3, 3, 3, 24)).astype(np.float32)
+    b = rng.normal(size=32).astype(np.float32)
+    got = ops.spconv_f32(_t(x, gpu), nt, tm, _t(w, gpu), _t(b, gpu)).cpu().numpy()
+    ref = ocv.conv_float(x.astype(np.float64), nm, w.astype(np.float64), b.astype(np.float64), dtype=np.float64)
+    assert np.abs(got - ref).max() < 1e-4
+
+
+# ---------------------------------------------------------------------------------------------------------- row ops
+@pytest.mark.parametrize("C", [16, 32, 48, 64, 128])
+def test_ln_silu(gpu, C):
+    announce(f"ln_silu C={C}")
+    rng = np.random.default_rng(C)
+    x = rng.normal(0.2, 1.5, size=(50_000, C)).astype(np.float32)
+    g = spec._f16(1 + rng.normal(0, 0.05, C))
+    b = spec._f16(rng.normal(0, 0.05, C))
+    s = np.float32(3.2 / 127)
+    X, G, Bt = _t(x, gpu), _t(g, gpu), _t(b, gpu)
+    y = onm.ln_silu(x, g, b)
+    assert np.array_equal(ops.ln_silu_quant(X, G, Bt, s).cpu().numpy(), onm.quant_i8(y, s))
+    assert np.array_equal(ops.ln_silu_f16(X, G, Bt).cpu().numpy().view(np.uint16), y.astype(np.float16).view(np.uint16))
+
+
+# ---------------------------------------------------------------------------------------------------------- fit
+def _close_st(s, t, so, to, tol=1e-5):
+    assert abs(float(s) - float(so)) <= tol * abs(float(so)), (s, so)
+    assert abs(float(t) - float(to)) <= tol * max(abs(float(to)), 1.0), (t, to)
+
+
+@pytest.mark.parametrize("iters", [0, 1, 4, 10])
+def test_fit_generic(gpu, iters):
+    announce(f"fit generic iters={iters}")
+    rng = np.random.default_rng(iters)
+    B, N = 2, 100_000
+    z = rng.uniform(0.5, 6, size=(B, N)).astype(np.float32)
+    t = (1.3 * z + 0.05 + rng.normal(0, 0.01, size=(B, N))).astype(np.float32)
+    t = np.where(rng.random((B, N)) < 0.05, t * 2.5, t).astype(np.float32)
+    m = rng.random((B, N)) < 0.7
+    so, to, info_o = ofit.fit_f64(z, t, m, iters=iters, return_info=True)
+    s, tt, info = ops.fit_scale_shift(_t(z, gpu), _t(t, gpu), _t(m, gpu), iters=iters, return_info=True)
+    s, tt, info = s.cpu().numpy(), tt.cpu().numpy(), info.cpu().numpy()
+    for b in range(B):
+        _close_st(s[b], tt[b], so[b], to[b])
+        assert info[b, 0] == info_o[b]["count"] and info[b, 1] == info_o[b]["k"] and info[b, 4] == 0
+
+
+def test_fit_edge_cases(gpu):
+    announce("fit edge cases")
+    z = np.full((3, 5000), 2.0, np.float32)
+    t = np.random.default_rng(0).uniform(1, 3, size=(3, 5000)).astype(np.float32)
+    m = np.ones_like(z, bool)
+    m[1, 31:] = False                      # 31 points: fallback (1, 0)
+    z[2] = np.linspace(0.5, 6, 5000)       # batch 2: ordinary
+    so, to = ofit.fit_f64(z, t, m, iters=4)
+    s, tt = ops.fit_scale_shift(_t(z, gpu), _t(t, gpu), _t(m, gpu), iters=4)
+    s, tt = s.cpu().numpy(), tt.cpu().numpy()
+    assert s[1] == 1.0 and tt[1] == 0.0
+    assert s[0] == 1.0  # constant z: den = 0
+    for b in (0, 2):
+        _close_st(s[b], tt[b], so[b], to[b])
+
+
+@pytest.mark.parametrize("name", ["B", "A", "H"])
+def test_fit_prompt_scene(gpu, name):
+    announce(f"fit prompt scene={name}")
+    cfg, sc = _scene(name)
+    z, tg, m, _, _ = ofit.prompt_inputs(sc.points[None], sc.lidar[None], sc.conf[None])
+    so, to = ofit.fit_f64(z, tg, m, iters=10)
+    s, t = ops.fit_prompt(_t(sc.points[None], gpu), _t(sc.lidar[None], gpu), _t(sc.conf[None], gpu), iters=10)
+    _close_st(s.item(), t.item(), so[0], to[0])

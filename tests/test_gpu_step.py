@@ -1,0 +1,104 @@
+"""GPU parity of the fused refiner step (RefinerStep) against the oracle's step on the same seeded inputs.
+
+The prompt fit must agree to 1e-5 relative (scale) / 1e-5 m (shift); the refined depth to 1e-3 relative. When the
+fit's (s, t) come out bit-identical (the usual case), every later stage is bit-identical too, and the test then
+requires the int8 codes and the residual stream of the last block to be exact.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import refiner as orf
+from promptmoge_amd import spec
+from promptmoge_amd.refiner import RefinerStep
+
+from conftest import announce
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(cfg, sc, w, *, B=1, use_graph=True, final_fit=False, reps=1):
+    dev = torch.device("cuda:0")
+    pts = np.broadcast_to(sc.points, (B,) + sc.points.shape).copy()
+    lid = np.broadcast_to(sc.lidar, (B,) + sc.lidar.shape).copy()
+    cnf = np.broadcast_to(sc.conf, (B,) + sc.conf.shape).copy()
+    step = RefinerStep(w, B, cfg.H, cfg.W, precision=cfg.precision, fit_iters=cfg.fit_iters, final_fit=final_fit,
+                       use_graph=use_graph)
+    stream = torch.cuda.Stream()
+    outs = []
+    with torch.cuda.stream(stream):
+        L, Cf = torch.from_numpy(lid).to(dev), torch.from_numpy(cnf).to(dev)
+        for _ in range(reps):
+            P = torch.from_numpy(pts).to(dev)
+            st, fin = step(P, L, Cf)
+            step.check()
+            outs.append((P.cpu().numpy(), st.cpu().numpy().copy(), None if fin is None else fin.cpu().numpy().copy()))
+    return step, pts, lid, cnf, outs
+
+
+@pytest.mark.parametrize("name", ["B", "A"])
+def test_step_int8(gpu, name):
+    announce(f"step int8 config={name}")
+    cfg = spec.CONFIGS[name]
+    sc = spec.make_scene(cfg)
+    w = spec.refiner_for(cfg, sc)
+    step, pts, lid, cnf, outs = _run(cfg, sc, w, final_fit=True)
+    P, st, fin = outs[0]
+    trace = {}
+    ref, st_o, fin_o = orf.step(pts, lid, cnf, w, precision="int8", iters=cfg.fit_iters, final_fit=True, trace=trace)
+    assert abs(st[0, 0] - st_o[0][0]) <= 1e-5 * abs(st_o[0][0]) and abs(st[0, 1] - st_o[1][0]) <= 1e-5
+    assert np.array_equal(step.buffer("zq").cpu().numpy(), trace["zq"].reshape(-1))
+    assert np.array_equal(step.buffer("nmap_t").cpu().numpy(), trace["nmap"].T)
+    d, dr = np.exp(P[..., 2].astype(np.float64)), np.exp(ref[..., 2].astype(np.float64))
+    assert (np.abs(d - dr) / dr).max() < 1e-3
+    assert abs(fin[0, 0] - fin_o[0][0]) <= 1e-5 * abs(fin_o[0][0]) and abs(fin[0, 1] - fin_o[1][0]) <= 1e-5
+    if st[0, 0] == st_o[0][0] and st[0, 1] == st_o[1][0]:
+        last = trace["blocks"][-1]
+        assert np.array_equal(step.buffer("q1").cpu().numpy(), last["q1"])
+        assert np.array_equal(step.buffer("q2").cpu().numpy(), last["q2"])
+        assert np.array_equal(step.buffer("x").cpu().numpy(), last["x"])
+        assert np.array_equal(P, ref)
+
+
+def test_step_fp16_teacher(gpu):
+    announce("step fp16 teacher (small)")
+    cfg = spec.StepConfig("t", 120, 160, 130.0, 130.0, 80.0, 60.0, 64, 3, "fp16", seed=13)
+    sc = spec.make_scene(cfg)
+    w = spec.refiner_for(cfg, sc)
+    step, pts, lid, cnf, outs = _run(cfg, sc, w)
+    P, st, _ = outs[0]
+    ref, st_o, _ = orf.step(pts, lid, cnf, w, precision="fp16", iters=cfg.fit_iters)
+    d, dr = np.exp(P[..., 2].astype(np.float64)), np.exp(ref[..., 2].astype(np.float64))
+    assert (np.abs(d - dr) / dr).max() < 1e-3
+
+
+def test_step_graph_replays_match_eager(gpu):
+    announce("step graph replay vs eager, B=2")
+    cfg = spec.CONFIGS["B"]
+    sc = spec.make_scene(cfg)
+    w = spec.refiner_for(cfg, sc)
+    _, _, _, _, eager = _run(cfg, sc, w, B=2, use_graph=False, final_fit=True, reps=1)
+    _, _, _, _, graph = _run(cfg, sc, w, B=2, use_graph=True, final_fit=True, reps=4)
+    for P, st, fin in graph:
+        assert np.array_equal(P, eager[0][0]) and np.array_equal(st, eager[0][1]) and np.array_equal(fin, eager[0][2])
+
+
+def test_step_multi_step_k3(gpu):
+    announce("step K=3 (points move, structure rebuilt each step)")
+    cfg = spec.StepConfig("k", 96, 128, 100.0, 100.0, 64.0, 48.0, 32, 2, "int8", seed=4)
+    sc = spec.make_scene(cfg)
+    w = spec.refiner_for(cfg, sc)
+    dev = torch.device("cuda:0")
+    step = RefinerStep(w, 1, cfg.H, cfg.W, fit_iters=10)
+    pts = sc.points[None].copy()
+    ref = pts.copy()
+    with torch.cuda.stream(torch.cuda.Stream()):
+        P = torch.from_numpy(pts).to(dev)
+        L, Cf = torch.from_numpy(sc.lidar[None]).to(dev), torch.from_numpy(sc.conf[None]).to(dev)
+        for _ in range(3):
+            step(P, L, Cf)
+            ref, _, _ = orf.step(ref, sc.lidar[None], sc.conf[None], w, iters=10)
+        step.check()
+        got = P.cpu().numpy()
+    d, dr = np.exp(got[..., 2].astype(np.float64)), np.exp(ref[..., 2].astype(np.float64))
+    assert (np.abs(d - dr) / dr).max() < 1e-3
