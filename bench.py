@@ -9,7 +9,8 @@ captured HIP graph of that chain; the metric fit of the refined depth is timed s
 
     value   active voxels refined per second = M / step time (whole job; one GPU)
     roofline  the dominant kernel of the step (largest time per step), algorithmic bytes per launch / its average
-              duration, both measured here with HIP events on the stream it runs on
+              duration, both measured here with HIP events on the stream it runs on (standalone launches of the
+              step's own kernels on the step's data)
     cpu_baseline  the oracle's restatement of the reference's CPU path (_fallback conv on fake-quantised operands,
               fit_scale_shift with an exact k-th selection) timed on this host on one Model-A step
     conv_microbench  isolated int8 conv on 1,000,000 surface voxels in 1024^3, C = 64 and 128
@@ -89,51 +90,47 @@ def main() -> int:
         ms_with_final = _events_ms(lambda: stepf(P, L, Cf, out=Pout), 50, stream)
         stepf.check()
 
-        # ---- per-kernel timing with the step's own shapes and data
+        # ---- per-kernel timing with the step's own shapes and data (standalone launches of the step's kernels)
         reps = args.kernel_reps
-        zq, zmin, zmax = ops.voxelize(P[..., 2:], 256.0, stride=3, shape=(1, cfg.H, cfg.W))
-        nt, tm, _, _ = ops.nmap_column(zq, zmin)
+        zq, _, _ = ops.voxelize(P[..., 2:], 256.0, stride=3, shape=(1, cfg.H, cfg.W))
         x = step.buffer("x")
-        blk = step.weights.blocks[0]
-        q1 = ops.ln_silu_quant(x, blk["gamma"], blk["beta"], blk["a1"])
-        q2 = ops.spconv_i8(q1, nt, tm, blk["w1"], ops.EPI_Q, a_scale=blk["a1"], w_scale=blk["s1"], bias=blk["b1"],
-                           out_scale=blk["a2"])
+        b0, b1 = step.weights.blocks[0], step.weights.blocks[-1]
+        q1 = ops.ln_silu_quant(x, b0["gamma"], b0["beta"], b0["a1"])
+        q2 = ops.spconv_col(q1, zq, b0["w1"], ops.EPI_Q, a_scale=b0["a1"], w_scale=b0["s1"], bias=b0["b1"],
+                            out_scale=b0["a2"])
         xr = x.clone()
+        nq = torch.empty_like(q1)
         kern = {}
         kern["fit_prompt"] = _events_ms(lambda: ops.fit_prompt(P, L, Cf, iters=cfg.fit_iters), reps, stream)
-        kern["voxelize"] = _events_ms(lambda: ops.voxelize(P[..., 2:], 256.0, stride=3, shape=(1, cfg.H, cfg.W)),
-                                      reps, stream)
-        kern["nmap_column"] = _events_ms(lambda: ops.nmap_column(zq, zmin), reps, stream)
-        kern["ln_silu_quant"] = _events_ms(lambda: ops.ln_silu_quant(x, blk["gamma"], blk["beta"], blk["a1"]), reps,
-                                           stream)
-        kern["conv_q"] = _events_ms(lambda: ops.spconv_i8(q1, nt, tm, blk["w1"], ops.EPI_Q, a_scale=blk["a1"],
-                                                          w_scale=blk["s1"], bias=blk["b1"], out_scale=blk["a2"],
-                                                          out=q2), reps, stream)
-        kern["conv_r"] = _events_ms(lambda: ops.spconv_i8(q2, nt, tm, blk["w2"], ops.EPI_R, a_scale=blk["a2"],
-                                                          w_scale=blk["s2"], bias=blk["b2"], skip=xr, out=xr),
-                                    reps, stream)
-        pairs = int((nt >= 0).sum().item())
+        kern["conv_q"] = _events_ms(lambda: ops.spconv_col(q1, zq, b0["w1"], ops.EPI_Q, a_scale=b0["a1"],
+                                                           w_scale=b0["s1"], bias=b0["b1"], out_scale=b0["a2"],
+                                                           out=q2), reps, stream)
+        kern["conv_rln"] = _events_ms(lambda: ops.spconv_col(q2, zq, b0["w2"], ops.EPI_RLN, a_scale=b0["a2"],
+                                                             w_scale=b0["s2"], bias=b0["b2"], skip=xr, out=xr,
+                                                             ln_gamma=b1["gamma"], ln_beta=b1["beta"],
+                                                             next_scale=b1["a1"], next_q=nq), reps, stream)
+        kern["conv_rout"] = _events_ms(lambda: ops.spconv_col(q2, zq, b1["w2"], ops.EPI_ROUT, a_scale=b1["a2"],
+                                                              w_scale=b1["s2"], bias=b1["b2"], skip=x,
+                                                              out_w=step.weights.out_w, out_b=step.weights.out_b,
+                                                              points=P, points_out=Pout), reps, stream)
         nb = cfg.n_blocks
-        per_step = {"fit_prompt": kern["fit_prompt"], "voxelize": kern["voxelize"],
-                    "nmap_column": kern["nmap_column"], "ln_silu_quant": (nb - 1) * kern["ln_silu_quant"],
-                    "conv_q": nb * kern["conv_q"], "conv_r": nb * kern["conv_r"]}
-        dominant = max(per_step, key=per_step.get)
-        # algorithmic bytes per launch (each byte the kernel must move at least once)
-        tiles = (M + 15) // 16
+        per_step = {"fit_prompt": kern["fit_prompt"], "conv_q": nb * kern["conv_q"],
+                    "conv_rln": (nb - 1) * kern["conv_rln"], "conv_rout": kern["conv_rout"]}
+        per_step["input_stage_and_launch_gaps"] = max(ms - sum(per_step.values()), 0.0)
+        dominant = max((k for k in per_step if k in kern), key=per_step.get)
+        # algorithmic bytes per launch (every byte the kernel must move at least once)
+        wb = 27 * C * C
         alg = {
-            "fit_prompt": M * 12,                                         # logz, LiDAR, conf: 4 B each
-            "voxelize": M * (4 + 4),                                      # logz in, key out
-            "nmap_column": M * (4 + 27 * 4) + tiles * 4,                  # keys in, map + tile masks out
-            "ln_silu_quant": M * C * (4 + 1),
-            "conv_q": M * (C + 27 * 4 + C) + tiles * 4 + 27 * C * C,      # x int8, map, out int8, masks, weights
-            "conv_r": M * (C + 27 * 4 + 8 * C) + tiles * 4 + 27 * C * C,  # + skip fp32 in, fp32 out
+            "fit_prompt": M * 12,                           # logz, LiDAR, conf: 4 B each
+            "conv_q": M * (C + 4 + C) + wb,                 # codes in, keys, codes out, weights
+            "conv_rln": M * (C + 4 + 4 * C + 4 * C + C) + wb,  # codes, keys, residual in/out, next codes
+            "conv_rout": M * (C + 4 + 4 * C + 12 + 12) + wb,  # codes, keys, residual, point map in/out
         }
         ach = alg[dominant] / (kern[dominant] * 1e-3) / 1e9
-        conv_ops = 2 * C * C * pairs
+        zq_np = zq.cpu().numpy()
         out["breakdown_ms"] = {k: round(v, 5) for k, v in kern.items()}
         out["per_step_ms_est"] = {k: round(v, 5) for k, v in per_step.items()}
-        out["conv_int8_tops"] = round(conv_ops / (kern["conv_q"] * 1e-3) / 1e12, 3)
-        out["pairs"] = pairs
+        out["kernel_gbs"] = {k: round(alg[k] / (kern[k] * 1e-3) / 1e9, 1) for k in kern}
         roofline = {"kernel": dominant, "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
                     "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
                     "algorithmic_bytes": int(alg[dominant]), "avg_launch_ms": round(kern[dominant], 5)}

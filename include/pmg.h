@@ -109,7 +109,8 @@ int pmg_kmap_compact(const int32_t* nmap_t, int64_t M, int64_t* offsets, int32_t
  * fp32 (the flex_gemm shim on fp32 features): PMG_EPI_ACC / PMG_EPI_BIAS -> fp32.
  * bias may be NULL (zero).
  * ------------------------------------------------------------------------------------------------------------ */
-enum { PMG_EPI_ACC = 0, PMG_EPI_Q = 1, PMG_EPI_R = 2, PMG_EPI_BIAS = 3, PMG_EPI_SILU = 4 };
+enum { PMG_EPI_ACC = 0, PMG_EPI_Q = 1, PMG_EPI_R = 2, PMG_EPI_BIAS = 3, PMG_EPI_SILU = 4, PMG_EPI_RLN = 5,
+       PMG_EPI_ROUT = 6 };
 
 int pmg_spconv_i8(const int8_t* x, const int32_t* nmap_t, const uint32_t* tile_mask, int64_t M, int Ci, int Co,
                   const int8_t* w, int epilogue, float a_scale, const float* w_scale, const float* bias,
@@ -119,12 +120,47 @@ int pmg_spconv_f16(const uint16_t* x, const int32_t* nmap_t, const uint32_t* til
 int pmg_spconv_f32(const float* x, const int32_t* nmap_t, const uint32_t* tile_mask, int64_t M, int Ci, int Co,
                    const float* w, int epilogue, const float* bias, float* out, void* stream);
 
+/* pmg_spconv_col -- the level-0 convolution computed straight from the voxel keys zq [B][H][W] (pmg_voxelize),
+ * with the column-stencil neighbourhood of _build_submanifold_nmap_column (_core.py:269-295) derived on the fly
+ * (no neighbour map is read), as one fused layer of the residual block (flex_sparse_blocks.py:229-234):
+ *   precision PMG_PREC_INT8: x int8 [M][C], w int8 [C][27][C]; PMG_PREC_FP16: x, w fp16.
+ *   PMG_EPI_ACC   out int32 (int8) / fp32 (fp16) [M][C] = acc
+ *   PMG_EPI_Q     int8: out int8 = quant(silu((acc*a_scale)*w_scale[n] + bias[n]), out_scale);
+ *                 fp16: out fp16 = half(silu(acc + bias[n]))
+ *   PMG_EPI_R     out fp32 = y + skip, y = (acc*a_scale)*w_scale[n] + bias[n] (int8) or acc + bias[n] (fp16)
+ *   PMG_EPI_RLN   as R, and next_q [M][C] = quant(silu(LayerNorm(out) * ln_gamma + ln_beta), next_scale) (int8) or
+ *                 half(silu(...)) (fp16): the next block's input (out may alias skip)
+ *   PMG_EPI_ROUT  as R without storing it, then points_out[m] = (points[m].xy, points[m].z + out_b + out_w . x_new)
+ * LayerNorm and the out_proj dot product sum in a fixed order: channels n = 16j + 4g + i are summed per group g
+ * (j outer, i inner) and the four group sums combined as ((s0 + s1) + (s2 + s3)). C in {16, 32, 48, 64, 128}. */
+typedef struct {
+    float a_scale;         /* int8: input activation scale clip/127 */
+    const float* w_scale;  /* int8: [C] per-output-channel weight scale */
+    const float* bias;     /* [C] or NULL */
+    float out_scale;       /* PMG_EPI_Q (int8): output scale */
+    const float* skip;     /* residual epilogues: [M][C] fp32 */
+    void* out;             /* main output (unused by PMG_EPI_ROUT) */
+    const float* ln_gamma; /* PMG_EPI_RLN: next block's LayerNorm affine [C] */
+    const float* ln_beta;
+    float ln_eps;
+    float next_scale; /* int8: next block's conv1 input scale */
+    void* next_q;     /* [M][C] int8 or fp16 */
+    const float* out_w; /* PMG_EPI_ROUT: out_proj weight [C] and bias [1] */
+    const float* out_b;
+    const float* points; /* [M][3] input point map */
+    float* points_out;   /* [M][3] refined point map (may alias points) */
+} pmg_conv_epilogue;
+
+int pmg_spconv_col(int precision, const void* x, const int32_t* zq, int B, int H, int W, int C, const void* w,
+                   int epilogue, const pmg_conv_epilogue* e, void* stream);
+
 /* ------------------------------------------------------------------------------------------------------------ *
  * Row operations of the residual block (SparseResBlock3d, moge/model/modules/flex_sparse_blocks.py:70-75;
  * device design Refiner.metal:75-131).
  *   pmg_ln_silu_quant: q[m] = quant(silu(LayerNorm(x[m]) * gamma + beta), out_scale)  -> int8 [M][C]
  *   pmg_ln_silu_f16:   h[m] = half(silu(LayerNorm(x[m]) * gamma + beta))                -> fp16 [M][C]
- * LayerNorm is two-pass (mean, then mean of squared deviations) with sums in channel order, eps inside the sqrt.
+ * LayerNorm is two-pass (mean, then mean of squared deviations), eps inside the sqrt, with the sums in the order of
+ * pmg_spconv_col's PMG_EPI_RLN (per group g of channels 16j+4g+i, then ((s0 + s1) + (s2 + s3))).
  * C in {16, 32, 48, 64, 96, 128}.
  * ------------------------------------------------------------------------------------------------------------ */
 int pmg_ln_silu_quant(const float* x, int64_t M, int C, const float* gamma, const float* beta, float eps,
@@ -217,8 +253,8 @@ int pmg_refiner_step(pmg_refiner* r, const float* points, float* points_out, con
                      float* st_prompt, float* st_final, void* stream);
 /* Synchronises `stream` and reports a device-side error flag of the last steps (PMG_E_DEVICE). */
 int pmg_refiner_check(pmg_refiner* r, void* stream);
-/* Device buffers of the last step, for parity tests: 0 zq, 1 nmap_t, 2 tile_mask, 3 x (fp32 residual),
- * 4 q1 (conv1 input), 5 q2 (conv2 input). Returns NULL for an unknown id. */
+/* Device buffers of the last step, for parity tests: 0 zq (voxel keys [M]), 3 x (fp32 residual [M][C] entering the
+ * last block), 4 q1 (the last block's conv1 input codes), 5 q2 (its conv2 input codes). NULL for any other id. */
 const void* pmg_refiner_buffer(pmg_refiner* r, int id);
 
 #ifdef __cplusplus

@@ -84,20 +84,28 @@ def quant_i8(y, s) -> np.ndarray:
     return quant_f32(y, s).astype(np.int8)
 
 
+def quad_sum(v: np.ndarray) -> np.ndarray:
+    """Row sum of (M, C) fp32 in the kernels' fixed order: group g = 0..3 accumulates channels 16j + 4g + i
+    (j outer, i inner, from 0), then ((s0 + s1) + (s2 + s3)). C must be a multiple of 16."""
+    v = np.asarray(v, dtype=np.float32)
+    M, C = v.shape
+    vr = v.reshape(M, C // 16, 4, 4)  # [m][j][g][i]
+    s = np.zeros((M, 4), dtype=np.float32)
+    for j in range(C // 16):
+        for i in range(4):
+            s = s + vr[:, j, :, i]
+    return (s[:, 0] + s[:, 1]) + (s[:, 2] + s[:, 3])
+
+
 def ln_silu(x: np.ndarray, gamma: np.ndarray, beta: np.ndarray, eps: float = 1e-6) -> np.ndarray:
-    """Two-pass LayerNorm with channel-order sums, affine, SiLU; fp32 op by op (pmg_rowops.hip ln_silu_row).
-    The reference's block is `silu(norm1(x))` with nn.LayerNorm(eps=1e-6) (flex_sparse_blocks.py:215, 230)."""
+    """Two-pass LayerNorm (quad-order sums), affine, SiLU; fp32 op by op (pmg_rowops.hip ln_silu_row and the
+    PMG_EPI_RLN epilogue). The reference's block is `silu(norm1(x))` with nn.LayerNorm(eps=1e-6)
+    (flex_sparse_blocks.py:215, 230)."""
     x = np.asarray(x, dtype=np.float32)
     M, C = x.shape
-    s = np.zeros(M, dtype=np.float32)
-    for c in range(C):
-        s = s + x[:, c]
-    mean = s / F32(C)
-    v = np.zeros(M, dtype=np.float32)
-    for c in range(C):
-        d = x[:, c] - mean
-        v = v + d * d
-    var = v / F32(C)
+    mean = quad_sum(x) / F32(C)
+    d = x - mean[:, None]
+    var = quad_sum(d * d) / F32(C)
     rstd = F32(1.0) / np.sqrt(var + F32(eps))
     y = (x - mean[:, None]) * rstd[:, None]
     y = y * gamma.astype(np.float32)

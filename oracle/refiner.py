@@ -23,7 +23,7 @@ import numpy as np
 
 from .conv import conv_acc_int, conv_float, epilogue_q, epilogue_r
 from .fit import fit_f64, prompt_inputs
-from .numerics import F32, ln_silu, log_f32, quant_i8
+from .numerics import F32, ln_silu, log_f32, quad_sum, quant_i8
 from .structure import nmap_column, voxelize
 
 
@@ -73,12 +73,9 @@ def input_proj(f: np.ndarray, w, res=None, gate=None) -> np.ndarray:
 
 
 def out_proj(x: np.ndarray, w) -> np.ndarray:
-    """out_proj (C -> 1), channel-order sum from the bias."""
-    d = np.full(x.shape[0], np.float32(w.out_b[0]), dtype=np.float32)
-    ow = np.asarray(w.out_w, np.float32).reshape(-1)
-    for c in range(x.shape[1]):
-        d = d + ow[c] * x[:, c]
-    return d
+    """out_proj (C -> 1): bias + the quad-order sum of out_w * x (the PMG_EPI_ROUT epilogue)."""
+    ow = np.asarray(w.out_w, np.float32).reshape(1, -1)
+    return np.float32(w.out_b[0]) + quad_sum(ow * x.astype(np.float32))
 
 
 def blocks_int8(x, nmap, w, trace=None):

@@ -11,7 +11,7 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().with_name("libpmg.so")
 
 PMG_OK, PMG_E_INVALID, PMG_E_HIP, PMG_E_OVERFLOW, PMG_E_DEVICE = 0, 1, 2, 3, 4
-EPI_ACC, EPI_Q, EPI_R, EPI_BIAS, EPI_SILU = 0, 1, 2, 3, 4
+EPI_ACC, EPI_Q, EPI_R, EPI_BIAS, EPI_SILU, EPI_RLN, EPI_ROUT = 0, 1, 2, 3, 4, 5, 6
 PREC_INT8, PREC_FP16 = 0, 1
 
 vp, i32, i64, f32, sz = C.c_void_p, C.c_int, C.c_int64, C.c_float, C.c_size_t
@@ -23,6 +23,14 @@ class PmgError(RuntimeError):
     def __init__(self, code: int, msg: str):
         super().__init__(f"libpmg error {code}: {msg}")
         self.code = code
+
+
+class ConvEpilogue(C.Structure):
+    _fields_ = [
+        ("a_scale", f32), ("w_scale", vp), ("bias", vp), ("out_scale", f32), ("skip", vp), ("out", vp),
+        ("ln_gamma", vp), ("ln_beta", vp), ("ln_eps", f32), ("next_scale", f32), ("next_q", vp),
+        ("out_w", vp), ("out_b", vp), ("points", vp), ("points_out", vp),
+    ]
 
 
 class RefinerConfig(C.Structure):
@@ -63,6 +71,7 @@ SIGNATURES = {
     "pmg_spconv_i8": (i32, [vp, vp, vp, i64, i32, i32, vp, i32, f32, vp, vp, f32, vp, vp, vp]),
     "pmg_spconv_f16": (i32, [vp, vp, vp, i64, i32, i32, vp, i32, vp, vp, vp, vp]),
     "pmg_spconv_f32": (i32, [vp, vp, vp, i64, i32, i32, vp, i32, vp, vp, vp]),
+    "pmg_spconv_col": (i32, [i32, vp, vp, i32, i32, i32, i32, vp, i32, C.c_void_p, vp]),
     "pmg_ln_silu_quant": (i32, [vp, i64, i32, vp, vp, f32, f32, vp, vp]),
     "pmg_ln_silu_f16": (i32, [vp, i64, i32, vp, vp, f32, vp, vp]),
     "pmg_fit_workspace_bytes": (sz, [i64, i32]),

@@ -1,9 +1,11 @@
 // Error plumbing and the fused refiner step (pmg_refiner_*).
 //
 // The step is the refine-loop body of MoGeModel.forward (moge/model/v3.py:547-576) for a single-level refiner,
-// in the order of the reference's device engine (Refiner.swift:224-292): prompt fit, prompt residual/gate,
-// voxelise, neighbour map, input projection, residual blocks, output projection and log-depth update, then the
-// optional metric fit of the refined depth. Everything is enqueued on one stream with no host synchronisation:
+// in the order of the reference's device engine (Refiner.swift:224-292): prompt fit, then one fused input kernel
+// (voxel keys, prompt residual/gate, input/prompt projections, first LayerNorm), then two convolutions per residual
+// block that derive the level-0 neighbourhood from the keys (the second one also normalises for the next block, or
+// applies out_proj and the log-depth update after the last block), then the optional metric fit of the refined
+// depth. Everything is enqueued on one stream with no host synchronisation:
 // at level 0 the voxel count is B*H*W, known on the host, so every grid is sized without reading the device.
 // The enqueue sequence is captured once into a HIP graph and replayed while the caller's buffers are unchanged.
 #include <climits>
@@ -61,8 +63,6 @@ struct pmg_refiner {
     int32_t* zq = nullptr;
     int32_t* zmin = nullptr;
     int32_t* zmax = nullptr;
-    int32_t* nmap_t = nullptr;
-    uint32_t* tmask = nullptr;
     float* x = nullptr;
     void* q1 = nullptr;
     void* q2 = nullptr;
@@ -122,39 +122,59 @@ static int enqueue_step(pmg_refiner* r, const float* points, float* points_out, 
         f.workspace_bytes = r->fit_ws_bytes;
         if (int e = launch_fit(f, s)) return e;
     }
-    if (int e = pmg_voxelize(points + 2, 3, c.B, c.H, c.W, c.depth_resolution, r->zq, r->zmin, r->zmax, s)) return e;
-    if (int e = pmg_nmap_column(r->zq, r->zmin, c.B, c.H, c.W, r->nmap_t, nullptr, r->tmask, nullptr, s)) return e;
-
     const pmg_block_weights& b0 = r->blocks[0];
     InputStage in{points, c.B, c.H, c.W, C, lidar, conf, c.dh, c.dw, st, c.use_prompt, c.soft_gate,
                   r->w.in_w, r->w.in_b, r->w.pr_w, r->w.pr_b, r->x, b0.ln_gamma, b0.ln_beta, 1e-6f,
-                  b0.a1_scale, r->q1};
+                  b0.a1_scale, r->q1, c.depth_resolution, r->zq};
     if (int e = launch_input_stage(in, f16, s)) return e;
 
+    // Residual blocks: conv1 (bias, SiLU, requantise) then conv2 (bias, skip, and either the next block's
+    // LayerNorm/SiLU/quantise or, after the last block, out_proj and the log-depth update).
+    const int prec = f16 ? PMG_PREC_FP16 : PMG_PREC_INT8;
     const int nbk = (int)r->blocks.size();
     for (int k = 0; k < nbk; ++k) {
         const pmg_block_weights& bk = r->blocks[k];
-        if (k > 0) {
-            if (int e = launch_ln_silu(r->x, M, C, bk.ln_gamma, bk.ln_beta, 1e-6f, bk.a1_scale, r->q1, f16, s))
-                return e;
-        }
-        if (f16) {
-            if (int e = pmg_spconv_f16((const uint16_t*)r->q1, r->nmap_t, r->tmask, M, C, C, (const uint16_t*)bk.w1,
-                                       PMG_EPI_SILU, bk.b1, nullptr, r->q2, s))
-                return e;
-            if (int e = pmg_spconv_f16((const uint16_t*)r->q2, r->nmap_t, r->tmask, M, C, C, (const uint16_t*)bk.w2,
-                                       PMG_EPI_R, bk.b2, r->x, r->x, s))
-                return e;
+        ColConvArgs a1{};
+        a1.x = r->q1;
+        a1.zq = r->zq;
+        a1.w = bk.w1;
+        a1.M = M;
+        a1.H = c.H;
+        a1.W = c.W;
+        a1.a_scale = bk.a1_scale;
+        a1.w_scale = bk.w1_scale;
+        a1.bias = bk.b1;
+        a1.out_scale = bk.a2_scale;
+        a1.out = r->q2;
+        if (int e = launch_conv_col(prec, a1, C, PMG_EPI_Q, s)) return e;
+        ColConvArgs a2{};
+        a2.x = r->q2;
+        a2.zq = r->zq;
+        a2.w = bk.w2;
+        a2.M = M;
+        a2.H = c.H;
+        a2.W = c.W;
+        a2.a_scale = bk.a2_scale;
+        a2.w_scale = bk.w2_scale;
+        a2.bias = bk.b2;
+        a2.skip = r->x;
+        a2.out = r->x;
+        if (k + 1 < nbk) {
+            const pmg_block_weights& bn = r->blocks[k + 1];
+            a2.ln_gamma = bn.ln_gamma;
+            a2.ln_beta = bn.ln_beta;
+            a2.ln_eps = 1e-6f;
+            a2.next_scale = bn.a1_scale;
+            a2.next_q = r->q1;
+            if (int e = launch_conv_col(prec, a2, C, PMG_EPI_RLN, s)) return e;
         } else {
-            if (int e = pmg_spconv_i8((const int8_t*)r->q1, r->nmap_t, r->tmask, M, C, C, (const int8_t*)bk.w1,
-                                      PMG_EPI_Q, bk.a1_scale, bk.w1_scale, bk.b1, bk.a2_scale, nullptr, r->q2, s))
-                return e;
-            if (int e = pmg_spconv_i8((const int8_t*)r->q2, r->nmap_t, r->tmask, M, C, C, (const int8_t*)bk.w2,
-                                      PMG_EPI_R, bk.a2_scale, bk.w2_scale, bk.b2, 1.0f, r->x, r->x, s))
-                return e;
+            a2.out_w = r->w.out_w;
+            a2.out_b = r->w.out_b;
+            a2.points = points;
+            a2.points_out = points_out;
+            if (int e = launch_conv_col(prec, a2, C, PMG_EPI_ROUT, s)) return e;
         }
     }
-    if (int e = launch_out_apply(r->x, M, C, r->w.out_w, r->w.out_b, points, points_out, s)) return e;
 
     if (c.final_fit) {
         FitLaunch f{};
@@ -213,7 +233,6 @@ pmg_refiner* pmg_refiner_create(const pmg_refiner_config* cfg) {
         return o;
     };
     const size_t o_zq = take(M * 4), o_zmin = take(c.B * 4), o_zmax = take(c.B * 4);
-    const size_t o_nmap = take(27 * M * 4), o_tm = take(((M + 15) / 16) * 4);
     const size_t o_x = take(M * c.C * 4), o_q1 = take(M * c.C * elt), o_q2 = take(M * c.C * elt);
     const size_t o_st = take(4 * c.B * 4), o_f0 = take(r->fit_ws_bytes), o_f1 = take(r->fit_ws_bytes);
     r->arena_bytes = off;
@@ -232,8 +251,6 @@ pmg_refiner* pmg_refiner_create(const pmg_refiner_config* cfg) {
     r->zq = (int32_t*)(a + o_zq);
     r->zmin = (int32_t*)(a + o_zmin);
     r->zmax = (int32_t*)(a + o_zmax);
-    r->nmap_t = (int32_t*)(a + o_nmap);
-    r->tmask = (uint32_t*)(a + o_tm);
     r->x = (float*)(a + o_x);
     r->q1 = a + o_q1;
     r->q2 = a + o_q2;
@@ -326,8 +343,6 @@ const void* pmg_refiner_buffer(pmg_refiner* r, int id) {
     if (!r) return nullptr;
     switch (id) {
         case 0: return r->zq;
-        case 1: return r->nmap_t;
-        case 2: return r->tmask;
         case 3: return r->x;
         case 4: return r->q1;
         case 5: return r->q2;

@@ -28,11 +28,10 @@ struct InputStage {
     float eps;
     float out_scale;
     void* q_out;
+    float resolution;
+    int32_t* zq_out;
 };
 int launch_input_stage(const InputStage& in, bool f16, hipStream_t s);
-
-int launch_out_apply(const float* x, int64_t M, int C, const float* w, const float* b, const float* points,
-                     float* points_out, hipStream_t s);
 
 struct FitLaunch {
     int mode;
@@ -55,5 +54,29 @@ struct FitLaunch {
 };
 size_t fit_workspace_bytes(int64_t N, int iters);
 int launch_fit(const FitLaunch& f, hipStream_t s);
+
+struct ColConvArgs {
+    const void* x;
+    const int32_t* zq;
+    const void* w;
+    int64_t M;
+    int H, W;
+    float a_scale;
+    const float* w_scale;
+    const float* bias;
+    float out_scale;
+    const float* skip;
+    void* out;
+    const float* ln_gamma;
+    const float* ln_beta;
+    float ln_eps;
+    float next_scale;
+    void* next_q;
+    const float* out_w;
+    const float* out_b;
+    const float* points;
+    float* points_out;
+};
+int launch_conv_col(int precision, const ColConvArgs& a, int C, int epi, hipStream_t s);
 
 }  // namespace pmg

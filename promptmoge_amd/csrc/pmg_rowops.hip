@@ -1,7 +1,7 @@
-// Per-voxel row operations of the refiner: the fused input stage (prompt residual + input/prompt projections +
-// the first block's LayerNorm/SiLU/quantise), LayerNorm/SiLU/quantise between residual blocks, and the output
-// projection fused with the log-depth update. One thread per voxel row, channel loops unrolled at compile time
-// (C is a template parameter), every sum in channel order so that the NumPy restatement reproduces the bits.
+// Per-voxel row operations of the refiner: the fused input stage (voxel keys, prompt residual, input/prompt
+// projections, the first block's LayerNorm/SiLU/quantise) and the standalone LayerNorm/SiLU/quantise. One thread per
+// voxel row, channel loops unrolled at compile time (C is a template parameter), every sum in a fixed order so that
+// the NumPy restatement reproduces the bits.
 #include <cstring>
 
 #include "pmg_common.h"
@@ -19,20 +19,31 @@ void fill_u32(void* p, uint32_t value, int64_t n, hipStream_t s) {
     hipLaunchKernelGGL(fill_u32_k, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, (uint32_t*)p, value, n);
 }
 
-// LayerNorm (two-pass, channel order), affine, SiLU. flex_sparse_blocks.py:70 (norm1, eps 1e-6, then SiLU).
+// Sum of a row in the "quad" order shared with the convolution epilogues (pmg_conv_col.hip): group g accumulates
+// channels 16j + 4g + i (j outer, i inner), then ((s0 + s1) + (s2 + s3)).
+template <int C>
+__device__ inline float quad_row_sum(const float (&v)[C]) {
+    float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < C / 16; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s[g] = s[g] + v[16 * j + 4 * g + i];
+    return (s[0] + s[1]) + (s[2] + s[3]);
+}
+
+// LayerNorm (two-pass), affine, SiLU. flex_sparse_blocks.py:230 (norm1, eps 1e-6, then SiLU).
 template <int C>
 __device__ inline void ln_silu_row(float (&h)[C], const float* gamma, const float* beta, float eps) {
-    float s = 0.0f;
-#pragma unroll
-    for (int c = 0; c < C; ++c) s = s + h[c];
-    const float mean = s / (float)C;
-    float v = 0.0f;
+    const float mean = quad_row_sum<C>(h) / (float)C;
+    float d2[C];
 #pragma unroll
     for (int c = 0; c < C; ++c) {
         const float d = h[c] - mean;
-        v = v + d * d;
+        d2[c] = d * d;
     }
-    const float var = v / (float)C;
+    const float var = quad_row_sum<C>(d2) / (float)C;
     const float rstd = 1.0f / __builtin_sqrtf(var + eps);
 #pragma unroll
     for (int c = 0; c < C; ++c) {
@@ -127,7 +138,9 @@ struct InputArgs {
     const float* beta;
     float eps;
     float out_scale;
-    void* q_out;  // int8 or fp16 [M][C]
+    void* q_out;        // int8 or fp16 [M][C]
+    float resolution;   // voxel keys: zq = rint(logz * resolution) (v3.py:332)
+    int32_t* zq_out;    // [M] or NULL
 };
 
 __device__ inline void prompt_feats(const InputArgs& a, int b, int i, int j, float logz, float& res, float& gate) {
@@ -155,6 +168,7 @@ __global__ __launch_bounds__(256) void input_stage_k(InputArgs a) {
     const int64_t m = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (m >= M) return;
     const float f0 = a.points[m * 3 + 0], f1 = a.points[m * 3 + 1], f2 = a.points[m * 3 + 2];
+    if (a.zq_out) a.zq_out[m] = (int32_t)rne(f2 * a.resolution);
     float res = 0.0f, gate = 0.0f;
     if (a.use_prompt) {
         const int64_t HW = (int64_t)a.H * a.W;
@@ -182,25 +196,6 @@ __global__ __launch_bounds__(256) void input_stage_k(InputArgs a) {
         store_h_row<C>(h, (_Float16*)a.q_out + m * C);
     else
         store_q_row<C>(h, a.out_scale, (int8_t*)a.q_out + m * C);
-}
-
-// out_proj (C -> 1) and the refined point map (x/z, y/z, logz + delta). sparse_unet.py:258; v3.py:359, 574.
-// points_out may alias points: each thread reads its row before writing it.
-template <int C>
-__global__ __launch_bounds__(256) void out_apply_k(const float* __restrict__ x, int64_t M,
-                                                   const float* __restrict__ w, const float* __restrict__ b,
-                                                   const float* points, float* points_out) {
-    const int64_t m = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (m >= M) return;
-    float h[C];
-    load_row<C>(x + m * C, h);
-    float d = b[0];
-#pragma unroll
-    for (int c = 0; c < C; ++c) d = d + w[c] * h[c];
-    const float p0 = points[m * 3 + 0], p1 = points[m * 3 + 1], p2 = points[m * 3 + 2];
-    points_out[m * 3 + 0] = p0;
-    points_out[m * 3 + 1] = p1;
-    points_out[m * 3 + 2] = p2 + d;
 }
 
 // ------------------------------------------------------------------------------------------------------------
@@ -233,7 +228,8 @@ int launch_ln_silu(const float* x, int64_t M, int C, const float* gamma, const f
 
 int launch_input_stage(const InputStage& in, bool f16, hipStream_t s) {
     InputArgs a{in.points, in.B, in.H, in.W, in.lidar, in.conf, in.dh, in.dw, in.st, in.use_prompt, in.soft_gate,
-                in.in_w, in.in_b, in.pr_w, in.pr_b, in.x_out, in.gamma, in.beta, in.eps, in.out_scale, in.q_out};
+                in.in_w, in.in_b, in.pr_w, in.pr_b, in.x_out, in.gamma, in.beta, in.eps, in.out_scale, in.q_out,
+                in.resolution, in.zq_out};
     const int64_t M = (int64_t)in.B * in.H * in.W;
     const dim3 g((unsigned)((M + 255) / 256));
     if (f16) {
@@ -242,13 +238,6 @@ int launch_input_stage(const InputStage& in, bool f16, hipStream_t s) {
         PMG_C_SWITCH(in.C, hipLaunchKernelGGL((input_stage_k<CC, false>), g, dim3(256), 0, s, a));
     }
     return check_launch("input_stage_k");
-}
-
-int launch_out_apply(const float* x, int64_t M, int C, const float* w, const float* b, const float* points,
-                     float* points_out, hipStream_t s) {
-    const dim3 g((unsigned)((M + 255) / 256));
-    PMG_C_SWITCH(C, hipLaunchKernelGGL((out_apply_k<CC>), g, dim3(256), 0, s, x, M, w, b, points, points_out));
-    return check_launch("out_apply_k");
 }
 
 // ------------------------------------------------------------------------------------------------------------

@@ -11,12 +11,12 @@ from typing import Optional, Sequence, Tuple
 import torch
 
 from . import _lib
-from ._lib import EPI_ACC, EPI_BIAS, EPI_Q, EPI_R, EPI_SILU, call, lib
+from ._lib import EPI_ACC, EPI_BIAS, EPI_Q, EPI_R, EPI_RLN, EPI_ROUT, EPI_SILU, ConvEpilogue, call, lib
 
 __all__ = [
     "voxelize", "nmap_column", "nmap_hash", "nmap_from_rows", "kmap_compact", "spconv_i8", "spconv_f16",
-    "spconv_f32", "ln_silu_quant", "ln_silu_f16", "fit_scale_shift", "fit_prompt", "math_device",
-    "EPI_ACC", "EPI_Q", "EPI_R", "EPI_BIAS", "EPI_SILU",
+    "spconv_f32", "spconv_col", "ln_silu_quant", "ln_silu_f16", "fit_scale_shift", "fit_prompt", "math_device",
+    "EPI_ACC", "EPI_Q", "EPI_R", "EPI_BIAS", "EPI_SILU", "EPI_RLN", "EPI_ROUT",
 ]
 
 
@@ -181,6 +181,38 @@ def spconv_f32(x: torch.Tensor, nmap_t: torch.Tensor, tile_mask: torch.Tensor, w
     call("pmg_spconv_f32", _p(x), _p(nmap_t), _p(tile_mask), M, Ci, Co, _p(w),
          EPI_BIAS if bias is not None else EPI_ACC, _p(bias), _p(out), _stream())
     return out
+
+
+def spconv_col(x: torch.Tensor, zq: torch.Tensor, w: torch.Tensor, epilogue: int = EPI_ACC, *, a_scale: float = 1.0,
+               w_scale: Optional[torch.Tensor] = None, bias: Optional[torch.Tensor] = None, out_scale: float = 1.0,
+               skip: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
+               ln_gamma: Optional[torch.Tensor] = None, ln_beta: Optional[torch.Tensor] = None, ln_eps: float = 1e-6,
+               next_scale: float = 1.0, next_q: Optional[torch.Tensor] = None, out_w: Optional[torch.Tensor] = None,
+               out_b: Optional[torch.Tensor] = None, points: Optional[torch.Tensor] = None,
+               points_out: Optional[torch.Tensor] = None):
+    """Level-0 conv from the voxel keys zq [B, H, W] (no neighbour map). x: (M, C) int8 or fp16; w: (C, 3, 3, 3, C).
+    Returns the main output (or points_out for EPI_ROUT)."""
+    prec = {torch.int8: _lib.PREC_INT8, torch.float16: _lib.PREC_FP16}[x.dtype]
+    x = _dev(x, "x")
+    zq = _dev(zq, "zq", torch.int32)
+    w = _dev(w, "w", x.dtype)
+    B, H, W = zq.shape
+    M, Cc = x.shape
+    if M != B * H * W or w.numel() != Cc * 27 * Cc:
+        raise ValueError("shape mismatch")
+    if out is None and epilogue != EPI_ROUT:
+        if epilogue == EPI_ACC:
+            dt = torch.int32 if prec == _lib.PREC_INT8 else torch.float32
+        elif epilogue == EPI_Q:
+            dt = x.dtype
+        else:
+            dt = torch.float32
+        out = torch.empty((M, Cc), dtype=dt, device=x.device)
+    e = ConvEpilogue(float(a_scale), _p(w_scale), _p(bias), float(out_scale), _p(skip), _p(out), _p(ln_gamma),
+                     _p(ln_beta), float(ln_eps), float(next_scale), _p(next_q), _p(out_w), _p(out_b), _p(points),
+                     _p(points_out))
+    call("pmg_spconv_col", prec, _p(x), _p(zq), B, H, W, Cc, _p(w), epilogue, C.byref(e), _stream())
+    return points_out if epilogue == EPI_ROUT else out
 
 
 def ln_silu_quant(x: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, out_scale: float,

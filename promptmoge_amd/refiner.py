@@ -59,7 +59,7 @@ class DeviceWeights:
 class RefinerStep:
     """One fused refinement step for point maps of a fixed size.
 
-    points [B, H, W, 3] fp32 (x/z, y/z, logz) is refined in place; lidar, conf [B, dh, dw] fp32.
+    points [B, H, W, 3] fp32 (x/z, y/z, logz) is refined into `out` (default in place); lidar, conf [B, dh, dw].
     Returns the prompt fit (s, t) [B, 2] and, if `final_fit`, the metric fit of the refined depth [B, 2].
     """
 
@@ -110,12 +110,13 @@ class RefinerStep:
         call("pmg_refiner_check", self._h, C.c_void_p(torch.cuda.current_stream().cuda_stream))
 
     def buffer(self, which: str) -> torch.Tensor:
-        """A copy of an internal buffer of the last step (parity tests): zq, nmap_t, tile_mask, x, q1, q2."""
-        ids = {"zq": 0, "nmap_t": 1, "tile_mask": 2, "x": 3, "q1": 4, "q2": 5}
+        """A copy of an internal buffer of the last step (parity tests): zq (voxel keys), x (residual entering the
+        last block), q1 / q2 (the last block's conv1 / conv2 input)."""
+        ids = {"zq": 0, "x": 3, "q1": 4, "q2": 5}
         M, Cc = self.B * self.H * self.W, self.weights.C
         f16 = self.weights.precision == "fp16"
         shape, dt = {
-            "zq": ((M,), torch.int32), "nmap_t": ((27, M), torch.int32), "tile_mask": (((M + 15) // 16,), torch.int32),
+            "zq": ((M,), torch.int32),
             "x": ((M, Cc), torch.float32), "q1": ((M, Cc), torch.float16 if f16 else torch.int8),
             "q2": ((M, Cc), torch.float16 if f16 else torch.int8),
         }[which]

@@ -121,9 +121,10 @@ def nearest_fill(depth: np.ndarray, conf: np.ndarray):
 
 
 def make_scene(cfg: StepConfig, seed: Optional[int] = None) -> Scene:
-    """Ray-cast piecewise-planar room (6-10 planes, depth clipped to [0.5, 6] m), sigma = 5 mm LiDAR noise, i.i.d.
-    confidence in {0, 1, 2} with P = (0.1, 0.2, 0.7), 3 % gross LiDAR outliers, and a network prediction in an
-    affine frame (lidar ~= 1.3 * exp(logz) + 0.05) with 1 % multiplicative noise."""
+    """Ray-cast piecewise-planar room (6-10 planes, depth clipped to [0.5, 6] m) plus sigma = 5 mm Gaussian noise:
+    that depth map is the LiDAR prompt (same resolution, 3 % gross outliers, i.i.d. confidence in {0, 1, 2} with
+    P = (0.1, 0.2, 0.7)) and, mapped into an affine frame (depth ~= 1.3 * exp(logz) + 0.05), the network's point
+    map (x/z, y/z, logz) that the refiner voxelises."""
     rng = np.random.default_rng(cfg.seed if seed is None else seed)
     H, W = cfg.H, cfg.W
     dx = (np.arange(W) - cfg.cx) / cfg.fx
@@ -133,15 +134,15 @@ def make_scene(cfg: StepConfig, seed: Optional[int] = None) -> Scene:
         D = _cylinders(rng, D, dx, dy)
     D = np.where(np.isfinite(D), D, 6.0)
     D = np.clip(D, 0.5, 6.0)
-    lidar = D + rng.normal(0.0, 0.005, size=D.shape)
+    D_obs = D + rng.normal(0.0, 0.005, size=D.shape)
     out = rng.random(D.shape) < 0.03
-    lidar = np.where(out, lidar * rng.uniform(0.5, 1.5, size=D.shape), lidar)
+    lidar = np.where(out, D_obs * rng.uniform(0.5, 1.5, size=D.shape), D_obs)
     conf = rng.choice(np.array([0.0, 1.0, 2.0]), size=D.shape, p=[0.1, 0.2, 0.7])
     if cfg.holes > 0:
         hole = rng.random(D.shape) < cfg.holes
         lidar = np.where(hole, 0.0, lidar)
         lidar, conf = nearest_fill(lidar, conf)
-    d_net = (D - T0) / S0 * np.exp(rng.normal(0.0, 0.01, size=D.shape))
+    d_net = (D_obs - T0) / S0
     points = np.stack(
         [np.broadcast_to(dx[None, :], (H, W)), np.broadcast_to(dy[:, None], (H, W)), np.log(d_net)], axis=-1
     ).astype(np.float32)

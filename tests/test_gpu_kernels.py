@@ -255,3 +255,86 @@ def test_fit_prompt_scene(gpu, name):
     so, to = ofit.fit_f64(z, tg, m, iters=10)
     s, t = ops.fit_prompt(_t(sc.points[None], gpu), _t(sc.lidar[None], gpu), _t(sc.conf[None], gpu), iters=10)
     _close_st(s.item(), t.item(), so[0], to[0])
+
+
+# ---------------------------------------------------------------------------------------------------------- level-0 conv
+def _col_setup(gpu, H=96, W=136, seed=3, B=2):
+    cfg = spec.StepConfig("c", H, W, 100.0, 100.0, W / 2, H / 2, 16, 1, "int8", seed=seed)
+    sc = spec.make_scene(cfg)
+    pts = np.stack([sc.points] + [sc.points * np.float32(1.0 + 0.01 * b) for b in range(1, B)])
+    zq_o, _, _, _ = ost.voxelize(pts)
+    nm = ost.nmap_column(zq_o)
+    return pts, zq_o, nm, _t(zq_o.astype(np.int32), gpu)
+
+
+@pytest.mark.parametrize("C", [16, 32, 48, 64, 128])
+def test_conv_col_int8_accumulator(gpu, C):
+    announce(f"conv col int8 acc C={C}")
+    rng = np.random.default_rng(C + 7)
+    pts, zq_o, nm, zq = _col_setup(gpu)  # W = 136: segments straddle image rows and the batch boundary
+    M = nm.shape[0]
+    x = rng.integers(-127, 128, size=(M, C)).astype(np.int8)
+    w = rng.integers(-127, 128, size=(C, 3, 3, 3, C)).astype(np.int8)
+    acc = ops.spconv_col(_t(x, gpu), zq, _t(w, gpu), ops.EPI_ACC)
+    assert np.array_equal(acc.cpu().numpy(), ocv.conv_acc_int(x, nm, w))
+
+
+@pytest.mark.parametrize("C", [32, 48])
+def test_conv_col_int8_fused_epilogues(gpu, C):
+    announce(f"conv col int8 epilogues Q/R/RLN/ROUT C={C}")
+    from oracle import refiner as orf
+
+    rng = np.random.default_rng(C)
+    pts, zq_o, nm, zq = _col_setup(gpu)
+    M = nm.shape[0]
+    x = rng.integers(-127, 128, size=(M, C)).astype(np.int8)
+    q, s = spec.quantize_weight(rng.normal(0, 0.05, size=(C, 3, 3, 3, C)).astype(np.float32))
+    b = rng.normal(0, 0.05, size=C).astype(np.float32)
+    g = spec._f16(1 + rng.normal(0, 0.05, C))
+    be = spec._f16(rng.normal(0, 0.05, C))
+    a_s, o_s, n_s = np.float32(3.0 / 127), np.float32(1.7 / 127), np.float32(2.9 / 127)
+    skip = rng.normal(size=(M, C)).astype(np.float32)
+    acc = ocv.conv_acc_int(x, nm, q)
+    X, Wq, S, Bv = _t(x, gpu), _t(q, gpu), _t(s, gpu), _t(b, gpu)
+    out_q = ops.spconv_col(X, zq, Wq, ops.EPI_Q, a_scale=a_s, w_scale=S, bias=Bv, out_scale=o_s)
+    assert np.array_equal(out_q.cpu().numpy(), ocv.epilogue_q(acc, a_s, s, b, o_s))
+    xr = ocv.epilogue_r(acc, a_s, s, b, skip)
+    out_r = ops.spconv_col(X, zq, Wq, ops.EPI_R, a_scale=a_s, w_scale=S, bias=Bv, skip=_t(skip, gpu))
+    assert np.array_equal(out_r.cpu().numpy(), xr)
+    Sk = _t(skip, gpu)  # RLN in place on the residual, as the step runs it
+    nq = torch.empty((M, C), dtype=torch.int8, device=gpu)
+    ops.spconv_col(X, zq, Wq, ops.EPI_RLN, a_scale=a_s, w_scale=S, bias=Bv, skip=Sk, out=Sk, ln_gamma=_t(g, gpu),
+                   ln_beta=_t(be, gpu), next_scale=n_s, next_q=nq)
+    assert np.array_equal(Sk.cpu().numpy(), xr)
+    assert np.array_equal(nq.cpu().numpy(), onm.quant_i8(onm.ln_silu(xr, g, be), n_s))
+    ow = rng.normal(0, 0.05, size=(1, C)).astype(np.float32)
+    ob = np.array([0.01], np.float32)
+    P = _t(pts, gpu)
+    Po = torch.empty_like(P)
+    ops.spconv_col(X, zq, Wq, ops.EPI_ROUT, a_scale=a_s, w_scale=S, bias=Bv, skip=_t(skip, gpu), out_w=_t(ow, gpu),
+                   out_b=_t(ob, gpu), points=P, points_out=Po)
+
+    class _W:
+        out_w, out_b = ow, ob
+
+    ref = pts.copy()
+    ref[..., 2] = ref[..., 2] + orf.out_proj(xr, _W).reshape(ref.shape[:3])
+    assert np.array_equal(Po.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("C", [32, 64])
+def test_conv_col_f16(gpu, C):
+    announce(f"conv col fp16 C={C}")
+    rng = np.random.default_rng(200 + C)
+    pts, zq_o, nm, zq = _col_setup(gpu)
+    M = nm.shape[0]
+    x = rng.normal(size=(M, C)).astype(np.float16)
+    w = rng.normal(0, 0.05, size=(C, 3, 3, 3, C)).astype(np.float16)
+    b = rng.normal(0, 0.05, size=C).astype(np.float32)
+    ref = ocv.conv_float(x.astype(np.float64), nm, w.astype(np.float64), dtype=np.float64)
+    got = ops.spconv_col(_t(x, gpu), zq, _t(w, gpu), ops.EPI_ACC).cpu().numpy()
+    bound = 27 * C * 2 ** -23 * ocv.conv_float(np.abs(x.astype(np.float64)), nm, np.abs(w.astype(np.float64)),
+                                                dtype=np.float64)
+    assert (np.abs(got - ref) <= bound + 1e-6).all()
+    h = ops.spconv_col(_t(x, gpu), zq, _t(w, gpu), ops.EPI_Q, bias=_t(b, gpu)).cpu().numpy()
+    assert np.array_equal(h.view(np.uint16), onm.silu_f32((got + b).astype(np.float32)).astype(np.float16).view(np.uint16))
