@@ -95,20 +95,20 @@ def main() -> int:
         zq, _, _ = ops.voxelize(P[..., 2:], 256.0, stride=3, shape=(1, cfg.H, cfg.W))
         x = step.buffer("x")
         b0, b1 = step.weights.blocks[0], step.weights.blocks[-1]
-        q1 = ops.ln_silu_quant(x, b0["gamma"], b0["beta"], b0["a1"])
+        q1 = ops.ln_silu_quant(x, b0["gamma"], b0["beta"], b0["m1"])
         q2 = ops.spconv_col(q1, zq, b0["w1"], ops.EPI_Q, a_scale=b0["a1"], w_scale=b0["s1"], bias=b0["b1"],
-                            out_scale=b0["a2"])
+                            out_mult=b0["m2"])
         xr = x.clone()
         nq = torch.empty_like(q1)
         kern = {}
         kern["fit_prompt"] = _events_ms(lambda: ops.fit_prompt(P, L, Cf, iters=cfg.fit_iters), reps, stream)
         kern["conv_q"] = _events_ms(lambda: ops.spconv_col(q1, zq, b0["w1"], ops.EPI_Q, a_scale=b0["a1"],
-                                                           w_scale=b0["s1"], bias=b0["b1"], out_scale=b0["a2"],
+                                                           w_scale=b0["s1"], bias=b0["b1"], out_mult=b0["m2"],
                                                            out=q2), reps, stream)
         kern["conv_rln"] = _events_ms(lambda: ops.spconv_col(q2, zq, b0["w2"], ops.EPI_RLN, a_scale=b0["a2"],
                                                              w_scale=b0["s2"], bias=b0["b2"], skip=xr, out=xr,
                                                              ln_gamma=b1["gamma"], ln_beta=b1["beta"],
-                                                             next_scale=b1["a1"], next_q=nq), reps, stream)
+                                                             next_mult=b1["m1"], next_q=nq), reps, stream)
         kern["conv_rout"] = _events_ms(lambda: ops.spconv_col(q2, zq, b1["w2"], ops.EPI_ROUT, a_scale=b1["a2"],
                                                               w_scale=b1["s2"], bias=b1["b2"], skip=x,
                                                               out_w=step.weights.out_w, out_b=step.weights.out_b,
@@ -127,7 +127,6 @@ def main() -> int:
             "conv_rout": M * (C + 4 + 4 * C + 12 + 12) + wb,  # codes, keys, residual, point map in/out
         }
         ach = alg[dominant] / (kern[dominant] * 1e-3) / 1e9
-        zq_np = zq.cpu().numpy()
         out["breakdown_ms"] = {k: round(v, 5) for k, v in kern.items()}
         out["per_step_ms_est"] = {k: round(v, 5) for k, v in per_step.items()}
         out["kernel_gbs"] = {k: round(alg[k] / (kern[k] * 1e-3) / 1e9, 1) for k in kern}
@@ -154,7 +153,7 @@ def main() -> int:
                 wm = torch.randint(-127, 128, (Cm, 3, 3, 3, Cm), generator=g, dtype=torch.int8).to(dev)
                 sm = torch.full((Cm,), 1e-4, device=dev)
                 om = torch.empty((coords.shape[0], Cm), dtype=torch.int8, device=dev)
-                f = lambda: ops.spconv_i8(xm, ntu, tmu, wm, ops.EPI_Q, a_scale=0.01, w_scale=sm, out_scale=0.05, out=om)
+                f = lambda: ops.spconv_i8(xm, ntu, tmu, wm, ops.EPI_Q, a_scale=0.01, w_scale=sm, out_mult=20.0, out=om)
                 f()
                 t = _events_ms(f, 10, stream)
                 tops = 2 * Cm * Cm * pu / (t * 1e-3) / 1e12

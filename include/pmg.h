@@ -100,10 +100,12 @@ int pmg_kmap_compact(const int32_t* nmap_t, int64_t M, int64_t* offsets, int32_t
  * int8 (the deployed contract, moge/model/modules/qat.py:1-16 and SparseConvInt8.metal:36-142):
  *   acc = sum int8*int8 in int32, then by epilogue
  *     PMG_EPI_ACC   out int32 [M][Co] = acc                                          (parity dump)
- *     PMG_EPI_Q     out int8  [M][Co] = quant(silu((acc*a_scale)*w_scale[n] + bias[n]), out_scale)
+ *     PMG_EPI_Q     out int8  [M][Co] = quant(silu((acc*a_scale)*w_scale[n] + bias[n]), out_mult)
  *     PMG_EPI_R     out fp32  [M][Co] = ((acc*a_scale)*w_scale[n] + bias[n]) + skip[m][n]   (skip may alias out)
  *     PMG_EPI_BIAS  out fp32  [M][Co] = (acc*a_scale)*w_scale[n] + bias[n]
- *   a_scale = clip/127 of the input activation, w_scale per output channel, quant as in qat.py:35-36.
+ *   a_scale = clip/127 of the input activation, w_scale per output channel; quant(y, mult) =
+ *   clamp(rint(y * mult), -127, 127) with mult = 127/clip of the output activation, the requantisation of the
+ *   reference's deployed kernels (SparseConvInt8.metal:109; mult computed as in Refiner.swift:148).
  * fp16 (teacher; fp32 accumulation): PMG_EPI_ACC / PMG_EPI_BIAS -> fp32 [M][Co] = acc (+ bias[n]);
  *   PMG_EPI_SILU -> fp16 [M][Co] = half(silu(acc + bias[n])); PMG_EPI_R -> fp32 = (acc + bias[n]) + skip.
  * fp32 (the flex_gemm shim on fp32 features): PMG_EPI_ACC / PMG_EPI_BIAS -> fp32.
@@ -114,7 +116,7 @@ enum { PMG_EPI_ACC = 0, PMG_EPI_Q = 1, PMG_EPI_R = 2, PMG_EPI_BIAS = 3, PMG_EPI_
 
 int pmg_spconv_i8(const int8_t* x, const int32_t* nmap_t, const uint32_t* tile_mask, int64_t M, int Ci, int Co,
                   const int8_t* w, int epilogue, float a_scale, const float* w_scale, const float* bias,
-                  float out_scale, const float* skip, void* out, void* stream);
+                  float out_mult, const float* skip, void* out, void* stream);
 int pmg_spconv_f16(const uint16_t* x, const int32_t* nmap_t, const uint32_t* tile_mask, int64_t M, int Ci, int Co,
                    const uint16_t* w, int epilogue, const float* bias, const float* skip, void* out, void* stream);
 int pmg_spconv_f32(const float* x, const int32_t* nmap_t, const uint32_t* tile_mask, int64_t M, int Ci, int Co,
@@ -125,10 +127,10 @@ int pmg_spconv_f32(const float* x, const int32_t* nmap_t, const uint32_t* tile_m
  * (no neighbour map is read), as one fused layer of the residual block (flex_sparse_blocks.py:229-234):
  *   precision PMG_PREC_INT8: x int8 [M][C], w int8 [C][27][C]; PMG_PREC_FP16: x, w fp16.
  *   PMG_EPI_ACC   out int32 (int8) / fp32 (fp16) [M][C] = acc
- *   PMG_EPI_Q     int8: out int8 = quant(silu((acc*a_scale)*w_scale[n] + bias[n]), out_scale);
+ *   PMG_EPI_Q     int8: out int8 = quant(silu((acc*a_scale)*w_scale[n] + bias[n]), out_mult);
  *                 fp16: out fp16 = half(silu(acc + bias[n]))
  *   PMG_EPI_R     out fp32 = y + skip, y = (acc*a_scale)*w_scale[n] + bias[n] (int8) or acc + bias[n] (fp16)
- *   PMG_EPI_RLN   as R, and next_q [M][C] = quant(silu(LayerNorm(out) * ln_gamma + ln_beta), next_scale) (int8) or
+ *   PMG_EPI_RLN   as R, and next_q [M][C] = quant(silu(LayerNorm(out) * ln_gamma + ln_beta), next_mult) (int8) or
  *                 half(silu(...)) (fp16): the next block's input (out may alias skip)
  *   PMG_EPI_ROUT  as R without storing it, then points_out[m] = (points[m].xy, points[m].z + out_b + out_w . x_new)
  * LayerNorm and the out_proj dot product sum in a fixed order: channels n = 16j + 4g + i are summed per group g
@@ -137,13 +139,13 @@ typedef struct {
     float a_scale;         /* int8: input activation scale clip/127 */
     const float* w_scale;  /* int8: [C] per-output-channel weight scale */
     const float* bias;     /* [C] or NULL */
-    float out_scale;       /* PMG_EPI_Q (int8): output scale */
+    float out_mult;        /* PMG_EPI_Q (int8): requantisation multiplier 127/clip of the output */
     const float* skip;     /* residual epilogues: [M][C] fp32 */
     void* out;             /* main output (unused by PMG_EPI_ROUT) */
     const float* ln_gamma; /* PMG_EPI_RLN: next block's LayerNorm affine [C] */
     const float* ln_beta;
     float ln_eps;
-    float next_scale; /* int8: next block's conv1 input scale */
+    float next_mult;  /* int8: 127/clip of the next block's conv1 input */
     void* next_q;     /* [M][C] int8 or fp16 */
     const float* out_w; /* PMG_EPI_ROUT: out_proj weight [C] and bias [1] */
     const float* out_b;
@@ -157,14 +159,14 @@ int pmg_spconv_col(int precision, const void* x, const int32_t* zq, int B, int H
 /* ------------------------------------------------------------------------------------------------------------ *
  * Row operations of the residual block (SparseResBlock3d, moge/model/modules/flex_sparse_blocks.py:70-75;
  * device design Refiner.metal:75-131).
- *   pmg_ln_silu_quant: q[m] = quant(silu(LayerNorm(x[m]) * gamma + beta), out_scale)  -> int8 [M][C]
+ *   pmg_ln_silu_quant: q[m] = quant(silu(LayerNorm(x[m]) * gamma + beta), out_mult)   -> int8 [M][C]
  *   pmg_ln_silu_f16:   h[m] = half(silu(LayerNorm(x[m]) * gamma + beta))                -> fp16 [M][C]
  * LayerNorm is two-pass (mean, then mean of squared deviations), eps inside the sqrt, with the sums in the order of
  * pmg_spconv_col's PMG_EPI_RLN (per group g of channels 16j+4g+i, then ((s0 + s1) + (s2 + s3))).
  * C in {16, 32, 48, 64, 96, 128}.
  * ------------------------------------------------------------------------------------------------------------ */
 int pmg_ln_silu_quant(const float* x, int64_t M, int C, const float* gamma, const float* beta, float eps,
-                      float out_scale, int8_t* q, void* stream);
+                      float out_mult, int8_t* q, void* stream);
 int pmg_ln_silu_f16(const float* x, int64_t M, int C, const float* gamma, const float* beta, float eps,
                     uint16_t* h, void* stream);
 
@@ -223,11 +225,13 @@ typedef struct {
     const void* w1;        /* conv1 [C][27][C], int8 or fp16 by precision */
     const float* w1_scale; /* [C] per-output-channel weight scale (int8 only) */
     const float* b1;       /* [C] */
-    float a1_scale;        /* conv1 input activation scale clip/127 (int8 only) */
+    float a1_scale;        /* conv1 input activation scale clip1/127 (int8 only) */
+    float q1_mult;         /* 127/clip1: quantises conv1's input (int8 only) */
     const void* w2;
     const float* w2_scale;
     const float* b2;
-    float a2_scale;
+    float a2_scale; /* clip2/127 */
+    float q2_mult;  /* 127/clip2: conv1's requantisation into conv2's input */
 } pmg_block_weights;
 
 typedef struct {

@@ -61,9 +61,9 @@ def dequant(acc: np.ndarray, a_scale, w_scale: np.ndarray, bias=None) -> np.ndar
     return y
 
 
-def epilogue_q(acc, a_scale, w_scale, bias, out_scale) -> np.ndarray:
-    """conv1 epilogue: bias, SiLU, requantise for the next layer (SparseConvInt8.metal:101-111; qat.py:35-36)."""
-    return quant_i8(silu_f32(dequant(acc, a_scale, w_scale, bias)), out_scale)
+def epilogue_q(acc, a_scale, w_scale, bias, out_mult) -> np.ndarray:
+    """conv1 epilogue: bias, SiLU, requantise for the next layer with mult = 127/clip (SparseConvInt8.metal:101-111)."""
+    return quant_i8(silu_f32(dequant(acc, a_scale, w_scale, bias)), out_mult)
 
 
 def epilogue_r(acc, a_scale, w_scale, bias, skip) -> np.ndarray:

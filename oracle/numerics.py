@@ -73,15 +73,15 @@ def silu_f32(y) -> np.ndarray:
         return (y / (F32(1.0) + exp_f32(-y))).astype(np.float32)
 
 
-def quant_f32(y, s) -> np.ndarray:
-    """clamp(rint(y / s), -127, 127), the QAT quantiser (qat.py:35-36): correctly rounded fp32 division, then
-    round half to even."""
+def quant_f32(y, mult) -> np.ndarray:
+    """clamp(rint(y * mult), -127, 127) with mult = 127/clip in fp32: the requantisation of the reference's deployed
+    int8 kernels (SparseConvInt8.metal:109, Refiner.metal:120, mult from Refiner.swift:148); round half to even."""
     y = np.asarray(y, dtype=np.float32)
-    return np.clip(np.rint(y / np.float32(s)), F32(-127.0), F32(127.0)).astype(np.float32)
+    return np.clip(np.rint(y * np.float32(mult)), F32(-127.0), F32(127.0)).astype(np.float32)
 
 
-def quant_i8(y, s) -> np.ndarray:
-    return quant_f32(y, s).astype(np.int8)
+def quant_i8(y, mult) -> np.ndarray:
+    return quant_f32(y, mult).astype(np.int8)
 
 
 def quad_sum(v: np.ndarray) -> np.ndarray:

@@ -11,8 +11,8 @@ Step order (moge/model/v3.py:547-576 with _lidar_in_affine_frame 362-383 and _re
   6. optionally the same fit on the refined depth
 
 `step` computes the blocks in the deployed integer arithmetic (the QAT contract qat.py:1-16 as executed by
-SparseConvInt8.metal / Refiner.metal: int8 activations and weights, exact int32 accumulation, fp32 epilogues) or
-in fp16 (teacher); every fp32 operation in the order of the GPU kernels. `step_fakequant` is the reference's own
+SparseConvInt8.metal / Refiner.metal: int8 activations and weights, exact int32 accumulation, fp32 epilogues,
+requantisation by 127/clip) or in fp16 (teacher); every fp32 operation in the order of the GPU kernels. `step_fakequant` is the reference's own
 fp32 formulation of the int8 model: _fallback's fp32 conv on fake-quantised operands (qat.py:28-57, 89-106).
 """
 from __future__ import annotations
@@ -38,8 +38,14 @@ def quantize_weight(w: np.ndarray):
 
 
 def act_scale(clip: float) -> np.float32:
-    """ActFakeQuant scale clip / QMAX in fp32, clamped at 1e-12 (qat.py:35, 98)."""
+    """ActFakeQuant scale clip / QMAX in fp32, clamped at 1e-12 (qat.py:35, 98); the deployed dequantisation scale
+    aScale = clip / 127 (Refiner.swift:147)."""
     return np.maximum(F32(clip) / F32(127.0), F32(1e-12))
+
+
+def act_mult(clip: float) -> np.float32:
+    """The deployed requantisation multiplier 127 / clip in fp32 (Refiner.swift:148)."""
+    return F32(127.0) / F32(clip)
 
 
 def prompt_feats(points, d, c, s, t, soft_gate=False):
@@ -83,9 +89,10 @@ def blocks_int8(x, nmap, w, trace=None):
         q_w1, s_w1 = quantize_weight(blk.w1)
         q_w2, s_w2 = quantize_weight(blk.w2)
         a1, a2 = act_scale(blk.clip1), act_scale(blk.clip2)
-        q1 = quant_i8(ln_silu(x, blk.gamma, blk.beta), a1)
+        m1, m2 = act_mult(blk.clip1), act_mult(blk.clip2)
+        q1 = quant_i8(ln_silu(x, blk.gamma, blk.beta), m1)
         acc1 = conv_acc_int(q1, nmap, q_w1)
-        q2 = epilogue_q(acc1, a1, s_w1, blk.b1, a2)
+        q2 = epilogue_q(acc1, a1, s_w1, blk.b1, m2)
         acc2 = conv_acc_int(q2, nmap, q_w2)
         x = epilogue_r(acc2, a2, s_w2, blk.b2, x)
         if trace is not None:

@@ -27,8 +27,8 @@ class PmgError(RuntimeError):
 
 class ConvEpilogue(C.Structure):
     _fields_ = [
-        ("a_scale", f32), ("w_scale", vp), ("bias", vp), ("out_scale", f32), ("skip", vp), ("out", vp),
-        ("ln_gamma", vp), ("ln_beta", vp), ("ln_eps", f32), ("next_scale", f32), ("next_q", vp),
+        ("a_scale", f32), ("w_scale", vp), ("bias", vp), ("out_mult", f32), ("skip", vp), ("out", vp),
+        ("ln_gamma", vp), ("ln_beta", vp), ("ln_eps", f32), ("next_mult", f32), ("next_q", vp),
         ("out_w", vp), ("out_b", vp), ("points", vp), ("points_out", vp),
     ]
 
@@ -44,7 +44,7 @@ class RefinerConfig(C.Structure):
 class BlockWeights(C.Structure):
     _fields_ = [
         ("ln_gamma", vp), ("ln_beta", vp), ("w1", vp), ("w1_scale", vp), ("b1", vp), ("a1_scale", f32),
-        ("w2", vp), ("w2_scale", vp), ("b2", vp), ("a2_scale", f32),
+        ("q1_mult", f32), ("w2", vp), ("w2_scale", vp), ("b2", vp), ("a2_scale", f32), ("q2_mult", f32),
     ]
 
 

@@ -125,7 +125,7 @@ static int enqueue_step(pmg_refiner* r, const float* points, float* points_out, 
     const pmg_block_weights& b0 = r->blocks[0];
     InputStage in{points, c.B, c.H, c.W, C, lidar, conf, c.dh, c.dw, st, c.use_prompt, c.soft_gate,
                   r->w.in_w, r->w.in_b, r->w.pr_w, r->w.pr_b, r->x, b0.ln_gamma, b0.ln_beta, 1e-6f,
-                  b0.a1_scale, r->q1, c.depth_resolution, r->zq};
+                  b0.q1_mult, r->q1, c.depth_resolution, r->zq};
     if (int e = launch_input_stage(in, f16, s)) return e;
 
     // Residual blocks: conv1 (bias, SiLU, requantise) then conv2 (bias, skip, and either the next block's
@@ -144,7 +144,7 @@ static int enqueue_step(pmg_refiner* r, const float* points, float* points_out, 
         a1.a_scale = bk.a1_scale;
         a1.w_scale = bk.w1_scale;
         a1.bias = bk.b1;
-        a1.out_scale = bk.a2_scale;
+        a1.out_mult = bk.q2_mult;
         a1.out = r->q2;
         if (int e = launch_conv_col(prec, a1, C, PMG_EPI_Q, s)) return e;
         ColConvArgs a2{};
@@ -164,7 +164,7 @@ static int enqueue_step(pmg_refiner* r, const float* points, float* points_out, 
             a2.ln_gamma = bn.ln_gamma;
             a2.ln_beta = bn.ln_beta;
             a2.ln_eps = 1e-6f;
-            a2.next_scale = bn.a1_scale;
+            a2.next_mult = bn.q1_mult;
             a2.next_q = r->q1;
             if (int e = launch_conv_col(prec, a2, C, PMG_EPI_RLN, s)) return e;
         } else {
@@ -278,7 +278,8 @@ int pmg_refiner_set_weights(pmg_refiner* r, const pmg_refiner_weights* w) {
         PMG_REQUIRE(b.ln_gamma && b.ln_beta && b.w1 && b.b1 && b.w2 && b.b2, "missing block weights");
         PMG_REQUIRE(aligned16(b.w1) && aligned16(b.w2), "conv weights must be 16-byte aligned");
         if (i8)
-            PMG_REQUIRE(b.w1_scale && b.w2_scale && b.a1_scale > 0.0f && b.a2_scale > 0.0f,
+            PMG_REQUIRE(b.w1_scale && b.w2_scale && b.a1_scale > 0.0f && b.a2_scale > 0.0f && b.q1_mult > 0.0f &&
+                            b.q2_mult > 0.0f,
                         "int8 blocks need weight and activation scales");
     }
     r->w = *w;

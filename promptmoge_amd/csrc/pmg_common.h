@@ -79,6 +79,62 @@ __device__ inline void grid_barrier(unsigned* counter, unsigned index, unsigned 
     __syncthreads();
 }
 
+// Row layout shared by the fused epilogues and the row kernels: a wave covers 16 rows; lane l holds row l % 16
+// and, of its C channels, n = 16j + 4g + i with g = l / 16 (j < C/16, i < 4). Row reductions run in the "quad"
+// order: each lane sums its channels (j outer, i inner) from 0, then the four lane groups combine as
+// ((s0 + s1) + (s2 + s3)) -- identical in every lane.
+__device__ inline float quad_sum(float s) {
+    const float a = s + __shfl_xor(s, 16, 64);
+    return a + __shfl_xor(a, 32, 64);
+}
+
+// LayerNorm (two-pass, quad order) + affine + SiLU of the lane's NB x 4 channels of one row, in place.
+template <int NB>
+__device__ inline void ln_silu_quad(float (&y)[NB][4], const float* gamma, const float* beta, float eps, int g) {
+    constexpr int C = 16 * NB;
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s = s + y[j][i];
+    const float mean = quad_sum(s) / (float)C;
+    float vs = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float d = y[j][i] - mean;
+            vs = vs + d * d;
+        }
+    const float var = quad_sum(vs) / (float)C;
+    const float rstd = 1.0f / __builtin_sqrtf(var + eps);
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int n = 16 * j + 4 * g + i;
+            float t = (y[j][i] - mean) * rstd;
+            t = t * gamma[n];
+            t = t + beta[n];
+            y[j][i] = silu_f32(t);
+        }
+}
+
+// Stores the lane's 4 channels of block j of row m as int8 codes (quant by mult) or fp16.
+__device__ inline void store_codes4(const float (&h)[4], float mult, int8_t* q) {
+    uint32_t pk = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pk |= (uint32_t)(uint8_t)quant_i8(h[i], mult) << (8 * i);
+    *(uint32_t*)q = pk;
+}
+__device__ inline void store_half4(const float (&h)[4], _Float16* o) {
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    h4 hv;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) hv[i] = (_Float16)h[i];
+    *(h4*)o = hv;
+}
+
 // Fill kernels (used instead of hipMemsetAsync so that the step can be captured into a HIP graph).
 void fill_u32(void* p, uint32_t value, int64_t n, hipStream_t s);
 

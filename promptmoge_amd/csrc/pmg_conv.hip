@@ -32,7 +32,7 @@ struct ConvArgs {
     float a_scale;
     const float* w_scale;
     const float* bias;
-    float out_scale;
+    float out_mult;
     const float* skip;
     void* out;
 };
@@ -80,7 +80,7 @@ __device__ inline void epilogue(const ConvArgs& a, int64_t m, int n, typename Ac
             y = y * a.w_scale[n];
             if (a.bias) y = y + a.bias[n];
             if constexpr (EPI == PMG_EPI_Q) {
-                ((int8_t*)a.out)[o] = quant_i8(silu_f32(y), a.out_scale);
+                ((int8_t*)a.out)[o] = quant_i8(silu_f32(y), a.out_mult);
             } else if constexpr (EPI == PMG_EPI_R) {
                 ((float*)a.out)[o] = y + a.skip[o];
             } else {
@@ -215,14 +215,14 @@ extern "C" {
 
 int pmg_spconv_i8(const int8_t* x, const int32_t* nmap_t, const uint32_t* tile_mask, int64_t M, int Ci, int Co,
                   const int8_t* w, int epilogue, float a_scale, const float* w_scale, const float* bias,
-                  float out_scale, const float* skip, void* out, void* stream) {
+                  float out_mult, const float* skip, void* out, void* stream) {
     if (int e = validate(x, nmap_t, tile_mask, M, Ci, Co, w, out, 1, "pmg_spconv_i8")) return e;
     PMG_REQUIRE(epilogue == PMG_EPI_ACC || w_scale, "w_scale required");
     PMG_REQUIRE(epilogue != PMG_EPI_R || skip, "skip required");
-    PMG_REQUIRE(epilogue != PMG_EPI_Q || out_scale > 0.0f, "out_scale must be positive");
+    PMG_REQUIRE(epilogue != PMG_EPI_Q || out_mult > 0.0f, "out_mult must be positive");
     if (M == 0) return PMG_OK;
     ConvArgs a{(const uint8_t*)x, nmap_t, tile_mask, (const uint8_t*)w, M, Co, Ci, Ci / 16,
-               a_scale, w_scale, bias, out_scale, skip, out};
+               a_scale, w_scale, bias, out_mult, skip, out};
     return conv_common<int8_t>(a, Ci, epilogue, (hipStream_t)stream);
 }
 

@@ -8,7 +8,7 @@ namespace pmg {
 bool supported_width(int C);
 
 int launch_ln_silu(const float* x, int64_t M, int C, const float* gamma, const float* beta, float eps,
-                   float out_scale, void* out, bool f16, hipStream_t s);
+                   float out_mult, void* out, bool f16, hipStream_t s);
 
 struct InputStage {
     const float* points;
@@ -26,7 +26,7 @@ struct InputStage {
     const float* gamma;
     const float* beta;
     float eps;
-    float out_scale;
+    float out_mult;
     void* q_out;
     float resolution;
     int32_t* zq_out;
@@ -64,13 +64,13 @@ struct ColConvArgs {
     float a_scale;
     const float* w_scale;
     const float* bias;
-    float out_scale;
+    float out_mult;
     const float* skip;
     void* out;
     const float* ln_gamma;
     const float* ln_beta;
     float ln_eps;
-    float next_scale;
+    float next_mult;
     void* next_q;
     const float* out_w;
     const float* out_b;

@@ -13,8 +13,9 @@
 //   log_f32   x = 2^e * m, m in [sqrt(2)/2, sqrt(2)], log(m) = 2 atanh(s), s = (m-1)/(m+1), odd series to s^9.
 //             Domain: positive normal x (callers clamp to >= 1e-4).
 //   silu_f32  y / (1 + exp(-y)), as in the reference's deployed epilogue (SparseConvInt8.metal:108).
-//   quant_i8  clamp(rint(y / s), -127, 127), the QAT rule (moge/model/modules/qat.py:35-36): a correctly
-//             rounded division, then round-half-to-even.
+//   quant_i8  clamp(rint(y * mult), -127, 127) with mult = 127/clip: the requantisation of the reference's
+//             deployed int8 kernels (SparseConvInt8.metal:109, Refiner.metal:120; mult from Refiner.swift:148),
+//             round-half-to-even as torch.round and Metal rint.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -89,8 +90,8 @@ PMG_HD float log_f32(float x) {
 
 PMG_HD float silu_f32(float y) { return y / (1.0f + exp_f32(-y)); }
 
-PMG_HD float quant_f32(float y, float s) { return fmin_(fmax_(rne(y / s), -127.0f), 127.0f); }
+PMG_HD float quant_f32(float y, float mult) { return fmin_(fmax_(rne(y * mult), -127.0f), 127.0f); }
 
-PMG_HD int8_t quant_i8(float y, float s) { return (int8_t)(int)quant_f32(y, s); }
+PMG_HD int8_t quant_i8(float y, float mult) { return (int8_t)(int)quant_f32(y, mult); }
 
 }  // namespace pmg

@@ -1,7 +1,7 @@
 // Per-voxel row operations of the refiner: the fused input stage (voxel keys, prompt residual, input/prompt
-// projections, the first block's LayerNorm/SiLU/quantise) and the standalone LayerNorm/SiLU/quantise. One thread per
-// voxel row, channel loops unrolled at compile time (C is a template parameter), every sum in a fixed order so that
-// the NumPy restatement reproduces the bits.
+// projections, the first block's LayerNorm/SiLU/quantise) and the standalone LayerNorm/SiLU/quantise, both in the
+// 16-rows-per-wave layout of the fused convolution epilogues, with every sum in a fixed order so that the NumPy
+// restatement reproduces the bits.
 #include <cstring>
 
 #include "pmg_common.h"
@@ -19,100 +19,37 @@ void fill_u32(void* p, uint32_t value, int64_t n, hipStream_t s) {
     hipLaunchKernelGGL(fill_u32_k, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, (uint32_t*)p, value, n);
 }
 
-// Sum of a row in the "quad" order shared with the convolution epilogues (pmg_conv_col.hip): group g accumulates
-// channels 16j + 4g + i (j outer, i inner), then ((s0 + s1) + (s2 + s3)).
-template <int C>
-__device__ inline float quad_row_sum(const float (&v)[C]) {
-    float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int j = 0; j < C / 16; ++j)
-#pragma unroll
-        for (int g = 0; g < 4; ++g)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) s[g] = s[g] + v[16 * j + 4 * g + i];
-    return (s[0] + s[1]) + (s[2] + s[3]);
-}
-
-// LayerNorm (two-pass), affine, SiLU. flex_sparse_blocks.py:230 (norm1, eps 1e-6, then SiLU).
-template <int C>
-__device__ inline void ln_silu_row(float (&h)[C], const float* gamma, const float* beta, float eps) {
-    const float mean = quad_row_sum<C>(h) / (float)C;
-    float d2[C];
-#pragma unroll
-    for (int c = 0; c < C; ++c) {
-        const float d = h[c] - mean;
-        d2[c] = d * d;
-    }
-    const float var = quad_row_sum<C>(d2) / (float)C;
-    const float rstd = 1.0f / __builtin_sqrtf(var + eps);
-#pragma unroll
-    for (int c = 0; c < C; ++c) {
-        float y = (h[c] - mean) * rstd;
-        y = y * gamma[c];
-        y = y + beta[c];
-        h[c] = silu_f32(y);
-    }
-}
-
-template <int C>
-__device__ inline void store_q_row(const float (&h)[C], float out_scale, int8_t* q) {
-#pragma unroll
-    for (int c0 = 0; c0 < C; c0 += 16) {
-        int32_t pk[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            uint32_t b = 0;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) b |= (uint32_t)(uint8_t)quant_i8(h[c0 + 4 * k + e], out_scale) << (8 * e);
-            pk[k] = (int32_t)b;
-        }
-        *(int4*)(q + c0) = make_int4(pk[0], pk[1], pk[2], pk[3]);
-    }
-}
-
-template <int C>
-__device__ inline void store_h_row(const float (&h)[C], _Float16* o) {
-#pragma unroll
-    for (int c0 = 0; c0 < C; c0 += 8) {
-        typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-        h8 v;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = (_Float16)h[c0 + e];
-        *(h8*)(o + c0) = v;
-    }
-}
-
-template <int C>
-__device__ inline void load_row(const float* x, float (&h)[C]) {
-#pragma unroll
-    for (int c = 0; c < C; c += 4) {
-        const float4 v = *(const float4*)(x + c);
-        h[c] = v.x;
-        h[c + 1] = v.y;
-        h[c + 2] = v.z;
-        h[c + 3] = v.w;
-    }
-}
-
-template <int C>
-__device__ inline void store_row(float* x, const float (&h)[C]) {
-#pragma unroll
-    for (int c = 0; c < C; c += 4) *(float4*)(x + c) = make_float4(h[c], h[c + 1], h[c + 2], h[c + 3]);
-}
-
+// Standalone LayerNorm -> SiLU -> int8 codes (or fp16) in the row layout of the fused epilogues: a wave covers 16
+// rows, lane l row l % 16 and channels 16j + 4g + i (g = l / 16), so the sums run in the same quad order and the
+// stores are 4- and 16-byte vectors.
 template <int C, bool F16>
 __global__ __launch_bounds__(256) void ln_silu_k(const float* __restrict__ x, int64_t M,
                                                  const float* __restrict__ gamma, const float* __restrict__ beta,
-                                                 float eps, float out_scale, void* __restrict__ out) {
-    const int64_t m = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (m >= M) return;
-    float h[C];
-    load_row<C>(x + m * C, h);
-    ln_silu_row<C>(h, gamma, beta, eps);
-    if constexpr (F16)
-        store_h_row<C>(h, (_Float16*)out + m * C);
-    else
-        store_q_row<C>(h, out_scale, (int8_t*)out + m * C);
+                                                 float eps, float out_mult, void* __restrict__ out) {
+    constexpr int NB = C / 16;
+    const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+    const int64_t m = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 16 + r;
+    const bool ok = m < M;
+    const int64_t mo = ok ? m : 0;
+    float y[NB][4];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+        const float4 v = *(const float4*)(x + mo * C + 16 * j + 4 * g);
+        y[j][0] = v.x;
+        y[j][1] = v.y;
+        y[j][2] = v.z;
+        y[j][3] = v.w;
+    }
+    ln_silu_quad<NB>(y, gamma, beta, eps, g);
+    if (!ok) return;
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+        const int64_t o = mo * C + 16 * j + 4 * g;
+        if constexpr (F16)
+            store_half4(y[j], (_Float16*)out + o);
+        else
+            store_codes4(y[j], out_mult, (int8_t*)out + o);
+    }
 }
 
 // ------------------------------------------------------------------------------------------------------------
@@ -137,7 +74,7 @@ struct InputArgs {
     const float* gamma;
     const float* beta;
     float eps;
-    float out_scale;
+    float out_mult;
     void* q_out;        // int8 or fp16 [M][C]
     float resolution;   // voxel keys: zq = rint(logz * resolution) (v3.py:332)
     int32_t* zq_out;    // [M] or NULL
@@ -164,38 +101,53 @@ __device__ inline void prompt_feats(const InputArgs& a, int b, int i, int j, flo
 
 template <int C, bool F16>
 __global__ __launch_bounds__(256) void input_stage_k(InputArgs a) {
+    constexpr int NB = C / 16;
     const int64_t M = (int64_t)a.B * a.H * a.W;
-    const int64_t m = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (m >= M) return;
-    const float f0 = a.points[m * 3 + 0], f1 = a.points[m * 3 + 1], f2 = a.points[m * 3 + 2];
-    if (a.zq_out) a.zq_out[m] = (int32_t)rne(f2 * a.resolution);
+    const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+    const int64_t m = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 16 + r;
+    const bool ok = m < M;
+    const int64_t mo = ok ? m : 0;
+    const float f0 = a.points[mo * 3 + 0], f1 = a.points[mo * 3 + 1], f2 = a.points[mo * 3 + 2];
+    if (ok && g == 0 && a.zq_out) a.zq_out[mo] = (int32_t)rne(f2 * a.resolution);
     float res = 0.0f, gate = 0.0f;
     if (a.use_prompt) {
         const int64_t HW = (int64_t)a.H * a.W;
-        const int b = (int)(m / HW);
-        const int p = (int)(m - b * HW);
+        const int b = (int)(mo / HW);
+        const int p = (int)(mo - b * HW);
         const int i = p / a.W, j = p - (p / a.W) * a.W;
         prompt_feats(a, b, i, j, f2, res, gate);
     }
-    float h[C];
+    float y[NB][4];
 #pragma unroll
-    for (int n = 0; n < C; ++n) {
-        float y = a.in_b[n] + a.in_w[3 * n] * f0;
-        y = y + a.in_w[3 * n + 1] * f1;
-        y = y + a.in_w[3 * n + 2] * f2;
-        if (a.use_prompt) {
-            float pp = a.pr_b[n] + a.pr_w[2 * n] * res;
-            pp = pp + a.pr_w[2 * n + 1] * gate;
-            y = y + pp;
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int n = 16 * j + 4 * g + i;
+            float t = a.in_b[n] + a.in_w[3 * n] * f0;
+            t = t + a.in_w[3 * n + 1] * f1;
+            t = t + a.in_w[3 * n + 2] * f2;
+            if (a.use_prompt) {
+                float pp = a.pr_b[n] + a.pr_w[2 * n] * res;
+                pp = pp + a.pr_w[2 * n + 1] * gate;
+                t = t + pp;
+            }
+            y[j][i] = t;
         }
-        h[n] = y;
+    if (ok) {
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+            *(float4*)(a.x_out + mo * C + 16 * j + 4 * g) = make_float4(y[j][0], y[j][1], y[j][2], y[j][3]);
     }
-    store_row<C>(a.x_out + m * C, h);
-    ln_silu_row<C>(h, a.gamma, a.beta, a.eps);
-    if constexpr (F16)
-        store_h_row<C>(h, (_Float16*)a.q_out + m * C);
-    else
-        store_q_row<C>(h, a.out_scale, (int8_t*)a.q_out + m * C);
+    ln_silu_quad<NB>(y, a.gamma, a.beta, a.eps, g);
+    if (!ok) return;
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+        const int64_t o = mo * C + 16 * j + 4 * g;
+        if constexpr (F16)
+            store_half4(y[j], (_Float16*)a.q_out + o);
+        else
+            store_codes4(y[j], a.out_mult, (int8_t*)a.q_out + o);
+    }
 }
 
 // ------------------------------------------------------------------------------------------------------------
@@ -213,25 +165,25 @@ __global__ __launch_bounds__(256) void input_stage_k(InputArgs a) {
 bool supported_width(int C) { return C == 16 || C == 32 || C == 48 || C == 64 || C == 96 || C == 128; }
 
 int launch_ln_silu(const float* x, int64_t M, int C, const float* gamma, const float* beta, float eps,
-                   float out_scale, void* out, bool f16, hipStream_t s) {
+                   float out_mult, void* out, bool f16, hipStream_t s) {
     if (M == 0) return PMG_OK;
-    const dim3 g((unsigned)((M + 255) / 256));
+    const dim3 g((unsigned)((M + 63) / 64));
     if (f16) {
         PMG_C_SWITCH(C, hipLaunchKernelGGL((ln_silu_k<CC, true>), g, dim3(256), 0, s, x, M, gamma, beta, eps,
-                                           out_scale, out));
+                                           out_mult, out));
     } else {
         PMG_C_SWITCH(C, hipLaunchKernelGGL((ln_silu_k<CC, false>), g, dim3(256), 0, s, x, M, gamma, beta, eps,
-                                           out_scale, out));
+                                           out_mult, out));
     }
     return check_launch("ln_silu_k");
 }
 
 int launch_input_stage(const InputStage& in, bool f16, hipStream_t s) {
     InputArgs a{in.points, in.B, in.H, in.W, in.lidar, in.conf, in.dh, in.dw, in.st, in.use_prompt, in.soft_gate,
-                in.in_w, in.in_b, in.pr_w, in.pr_b, in.x_out, in.gamma, in.beta, in.eps, in.out_scale, in.q_out,
+                in.in_w, in.in_b, in.pr_w, in.pr_b, in.x_out, in.gamma, in.beta, in.eps, in.out_mult, in.q_out,
                 in.resolution, in.zq_out};
     const int64_t M = (int64_t)in.B * in.H * in.W;
-    const dim3 g((unsigned)((M + 255) / 256));
+    const dim3 g((unsigned)((M + 63) / 64));
     if (f16) {
         PMG_C_SWITCH(in.C, hipLaunchKernelGGL((input_stage_k<CC, true>), g, dim3(256), 0, s, a));
     } else {
@@ -257,12 +209,12 @@ using namespace pmg;
 extern "C" {
 
 int pmg_ln_silu_quant(const float* x, int64_t M, int C, const float* gamma, const float* beta, float eps,
-                      float out_scale, int8_t* q, void* stream) {
+                      float out_mult, int8_t* q, void* stream) {
     PMG_REQUIRE(x && gamma && beta && q, "null buffer");
     PMG_REQUIRE(M >= 0, "bad voxel count");
-    PMG_REQUIRE(out_scale > 0.0f, "out_scale must be positive");
+    PMG_REQUIRE(out_mult > 0.0f, "out_mult must be positive");
     PMG_REQUIRE(aligned16(x) && aligned16(q), "x and q must be 16-byte aligned");
-    return launch_ln_silu(x, M, C, gamma, beta, eps, out_scale, q, false, (hipStream_t)stream);
+    return launch_ln_silu(x, M, C, gamma, beta, eps, out_mult, q, false, (hipStream_t)stream);
 }
 
 int pmg_ln_silu_f16(const float* x, int64_t M, int C, const float* gamma, const float* beta, float eps,

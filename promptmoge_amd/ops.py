@@ -137,7 +137,7 @@ def _conv_out(M: int, Co: int, epilogue: int, elt: str, dev) -> torch.Tensor:
 
 def spconv_i8(x: torch.Tensor, nmap_t: torch.Tensor, tile_mask: torch.Tensor, w: torch.Tensor, epilogue: int = EPI_ACC,
               *, a_scale: float = 1.0, w_scale: Optional[torch.Tensor] = None, bias: Optional[torch.Tensor] = None,
-              out_scale: float = 1.0, skip: Optional[torch.Tensor] = None,
+              out_mult: float = 1.0, skip: Optional[torch.Tensor] = None,
               out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """int8 submanifold conv. x: (M, Ci) int8; w: (Co, 3, 3, 3, Ci) or (Co, 27, Ci) int8."""
     x = _dev(x, "x", torch.int8)
@@ -149,7 +149,7 @@ def spconv_i8(x: torch.Tensor, nmap_t: torch.Tensor, tile_mask: torch.Tensor, w:
     if out is None:
         out = _conv_out(M, Co, epilogue, "i8", x.device)
     call("pmg_spconv_i8", _p(x), _p(nmap_t), _p(tile_mask), M, Ci, Co, _p(w), epilogue, float(a_scale), _p(w_scale),
-         _p(bias), float(out_scale), _p(skip), _p(out), _stream())
+         _p(bias), float(out_mult), _p(skip), _p(out), _stream())
     return out
 
 
@@ -184,10 +184,10 @@ def spconv_f32(x: torch.Tensor, nmap_t: torch.Tensor, tile_mask: torch.Tensor, w
 
 
 def spconv_col(x: torch.Tensor, zq: torch.Tensor, w: torch.Tensor, epilogue: int = EPI_ACC, *, a_scale: float = 1.0,
-               w_scale: Optional[torch.Tensor] = None, bias: Optional[torch.Tensor] = None, out_scale: float = 1.0,
+               w_scale: Optional[torch.Tensor] = None, bias: Optional[torch.Tensor] = None, out_mult: float = 1.0,
                skip: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
                ln_gamma: Optional[torch.Tensor] = None, ln_beta: Optional[torch.Tensor] = None, ln_eps: float = 1e-6,
-               next_scale: float = 1.0, next_q: Optional[torch.Tensor] = None, out_w: Optional[torch.Tensor] = None,
+               next_mult: float = 1.0, next_q: Optional[torch.Tensor] = None, out_w: Optional[torch.Tensor] = None,
                out_b: Optional[torch.Tensor] = None, points: Optional[torch.Tensor] = None,
                points_out: Optional[torch.Tensor] = None):
     """Level-0 conv from the voxel keys zq [B, H, W] (no neighbour map). x: (M, C) int8 or fp16; w: (C, 3, 3, 3, C).
@@ -208,19 +208,19 @@ def spconv_col(x: torch.Tensor, zq: torch.Tensor, w: torch.Tensor, epilogue: int
         else:
             dt = torch.float32
         out = torch.empty((M, Cc), dtype=dt, device=x.device)
-    e = ConvEpilogue(float(a_scale), _p(w_scale), _p(bias), float(out_scale), _p(skip), _p(out), _p(ln_gamma),
-                     _p(ln_beta), float(ln_eps), float(next_scale), _p(next_q), _p(out_w), _p(out_b), _p(points),
+    e = ConvEpilogue(float(a_scale), _p(w_scale), _p(bias), float(out_mult), _p(skip), _p(out), _p(ln_gamma),
+                     _p(ln_beta), float(ln_eps), float(next_mult), _p(next_q), _p(out_w), _p(out_b), _p(points),
                      _p(points_out))
     call("pmg_spconv_col", prec, _p(x), _p(zq), B, H, W, Cc, _p(w), epilogue, C.byref(e), _stream())
     return points_out if epilogue == EPI_ROUT else out
 
 
-def ln_silu_quant(x: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, out_scale: float,
+def ln_silu_quant(x: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, out_mult: float,
                   eps: float = 1e-6) -> torch.Tensor:
     x = _dev(x, "x", torch.float32)
     M, Cc = x.shape
     q = torch.empty((M, Cc), dtype=torch.int8, device=x.device)
-    call("pmg_ln_silu_quant", _p(x), M, Cc, _p(gamma), _p(beta), float(eps), float(out_scale), _p(q), _stream())
+    call("pmg_ln_silu_quant", _p(x), M, Cc, _p(gamma), _p(beta), float(eps), float(out_mult), _p(q), _stream())
     return q
 
 

@@ -19,7 +19,7 @@ import torch
 
 from . import _lib
 from ._lib import BlockWeights, RefinerConfig, RefinerWeights, call, lib
-from .spec import RefinerW, act_scale, quantize_weight
+from .spec import RefinerW, act_mult, act_scale, quantize_weight
 
 
 class DeviceWeights:
@@ -40,16 +40,18 @@ class DeviceWeights:
                 q1, s1 = quantize_weight(b.w1)
                 q2, s2 = quantize_weight(b.w2)
                 d.update(w1=t(q1, torch.int8), s1=t(s1), w2=t(q2, torch.int8), s2=t(s2),
-                         a1=float(act_scale(b.clip1)), a2=float(act_scale(b.clip2)))
+                         a1=float(act_scale(b.clip1)), a2=float(act_scale(b.clip2)),
+                         m1=float(act_mult(b.clip1)), m2=float(act_mult(b.clip2)))
             else:
-                d.update(w1=t(b.w1, torch.float16), w2=t(b.w2, torch.float16), s1=None, s2=None, a1=1.0, a2=1.0)
+                d.update(w1=t(b.w1, torch.float16), w2=t(b.w2, torch.float16), s1=None, s2=None, a1=1.0, a2=1.0,
+                         m1=1.0, m2=1.0)
             self.blocks.append(d)
         self._struct_blocks = (BlockWeights * len(self.blocks))()
         for k, d in enumerate(self.blocks):
             p = lambda x: None if x is None else x.data_ptr()
             self._struct_blocks[k] = BlockWeights(
-                p(d["gamma"]), p(d["beta"]), p(d["w1"]), p(d["s1"]), p(d["b1"]), d["a1"],
-                p(d["w2"]), p(d["s2"]), p(d["b2"]), d["a2"])
+                p(d["gamma"]), p(d["beta"]), p(d["w1"]), p(d["s1"]), p(d["b1"]), d["a1"], d["m1"],
+                p(d["w2"]), p(d["s2"]), p(d["b2"]), d["a2"], d["m2"])
         self.struct = RefinerWeights(
             self.in_w.data_ptr(), self.in_b.data_ptr(), self.pr_w.data_ptr(), self.pr_b.data_ptr(),
             self.out_w.data_ptr(), self.out_b.data_ptr(), len(self.blocks),

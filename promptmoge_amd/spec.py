@@ -211,8 +211,13 @@ def quantize_weight(w: np.ndarray):
 
 
 def act_scale(clip: float) -> np.float32:
-    """Per-tensor activation scale clip / 127 in fp32 (ActFakeQuant.forward, qat.py:98)."""
+    """Per-tensor activation scale clip / 127 in fp32 (ActFakeQuant.forward, qat.py:98; Refiner.swift:147)."""
     return np.maximum(np.float32(clip) / np.float32(127.0), np.float32(1e-12))
+
+
+def act_mult(clip: float) -> np.float32:
+    """Requantisation multiplier 127 / clip in fp32, as the deployed engine computes it (Refiner.swift:148)."""
+    return np.float32(127.0) / np.float32(clip)
 
 
 @dataclasses.dataclass

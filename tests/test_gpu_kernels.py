@@ -147,11 +147,11 @@ def test_conv_int8_epilogues(gpu, C):
     wf = rng.normal(0, 0.05, size=(C, 3, 3, 3, C)).astype(np.float32)
     q, s = spec.quantize_weight(wf)
     b = rng.normal(0, 0.05, size=C).astype(np.float32)
-    a_s, o_s = np.float32(3.0 / 127), np.float32(1.7 / 127)
+    a_s, o_s = np.float32(3.0 / 127), np.float32(127 / 1.7)
     skip = rng.normal(size=(M, C)).astype(np.float32)
     acc = ocv.conv_acc_int(x, nm, q)
     X, Wq, S, Bv = _t(x, gpu), _t(q, gpu), _t(s, gpu), _t(b, gpu)
-    out_q = ops.spconv_i8(X, nt, tm, Wq, ops.EPI_Q, a_scale=a_s, w_scale=S, bias=Bv, out_scale=o_s)
+    out_q = ops.spconv_i8(X, nt, tm, Wq, ops.EPI_Q, a_scale=a_s, w_scale=S, bias=Bv, out_mult=o_s)
     assert np.array_equal(out_q.cpu().numpy(), ocv.epilogue_q(acc, a_s, s, b, o_s))
     Sk = _t(skip, gpu)
     out_r = ops.spconv_i8(X, nt, tm, Wq, ops.EPI_R, a_scale=a_s, w_scale=S, bias=Bv, skip=Sk, out=Sk.clone())
@@ -201,7 +201,7 @@ def test_ln_silu(gpu, C):
     x = rng.normal(0.2, 1.5, size=(50_000, C)).astype(np.float32)
     g = spec._f16(1 + rng.normal(0, 0.05, C))
     b = spec._f16(rng.normal(0, 0.05, C))
-    s = np.float32(3.2 / 127)
+    s = np.float32(127 / 3.2)
     X, G, Bt = _t(x, gpu), _t(g, gpu), _t(b, gpu)
     y = onm.ln_silu(x, g, b)
     assert np.array_equal(ops.ln_silu_quant(X, G, Bt, s).cpu().numpy(), onm.quant_i8(y, s))
@@ -292,11 +292,11 @@ def test_conv_col_int8_fused_epilogues(gpu, C):
     b = rng.normal(0, 0.05, size=C).astype(np.float32)
     g = spec._f16(1 + rng.normal(0, 0.05, C))
     be = spec._f16(rng.normal(0, 0.05, C))
-    a_s, o_s, n_s = np.float32(3.0 / 127), np.float32(1.7 / 127), np.float32(2.9 / 127)
+    a_s, o_s, n_s = np.float32(3.0 / 127), np.float32(127 / 1.7), np.float32(127 / 2.9)
     skip = rng.normal(size=(M, C)).astype(np.float32)
     acc = ocv.conv_acc_int(x, nm, q)
     X, Wq, S, Bv = _t(x, gpu), _t(q, gpu), _t(s, gpu), _t(b, gpu)
-    out_q = ops.spconv_col(X, zq, Wq, ops.EPI_Q, a_scale=a_s, w_scale=S, bias=Bv, out_scale=o_s)
+    out_q = ops.spconv_col(X, zq, Wq, ops.EPI_Q, a_scale=a_s, w_scale=S, bias=Bv, out_mult=o_s)
     assert np.array_equal(out_q.cpu().numpy(), ocv.epilogue_q(acc, a_s, s, b, o_s))
     xr = ocv.epilogue_r(acc, a_s, s, b, skip)
     out_r = ops.spconv_col(X, zq, Wq, ops.EPI_R, a_scale=a_s, w_scale=S, bias=Bv, skip=_t(skip, gpu))
@@ -304,7 +304,7 @@ def test_conv_col_int8_fused_epilogues(gpu, C):
     Sk = _t(skip, gpu)  # RLN in place on the residual, as the step runs it
     nq = torch.empty((M, C), dtype=torch.int8, device=gpu)
     ops.spconv_col(X, zq, Wq, ops.EPI_RLN, a_scale=a_s, w_scale=S, bias=Bv, skip=Sk, out=Sk, ln_gamma=_t(g, gpu),
-                   ln_beta=_t(be, gpu), next_scale=n_s, next_q=nq)
+                   ln_beta=_t(be, gpu), next_mult=n_s, next_q=nq)
     assert np.array_equal(Sk.cpu().numpy(), xr)
     assert np.array_equal(nq.cpu().numpy(), onm.quant_i8(onm.ln_silu(xr, g, be), n_s))
     ow = rng.normal(0, 0.05, size=(1, C)).astype(np.float32)

@@ -47,7 +47,7 @@ def test_epilogues_closed_form():
     assert y.tolist() == [[12.5, -11.5, -2.0, 524288.0]]
     r = cv.epilogue_r(acc, a, ws, b, np.ones((1, 4), np.float32))
     assert r.tolist() == [[13.5, -10.5, -1.0, 524289.0]]
-    q = cv.epilogue_q(acc, a, ws, b, F32(0.125))
+    q = cv.epilogue_q(acc, a, ws, b, F32(8.0))  # multiplier 127/clip = 8
     silu = lambda v: v / (1 + np.exp(-v))
-    expect = [int(np.clip(np.rint(silu(float(v)) / 0.125), -127, 127)) for v in y[0]]
+    expect = [int(np.clip(np.rint(silu(float(v)) * 8.0), -127, 127)) for v in y[0]]
     assert q.tolist()[0] == expect  # 12.5 -> 99.99..; -11.5 -> ~0; -2 -> -1.9 -> -2 (=-0.238/0.125); saturates

@@ -49,10 +49,10 @@ def test_silu_accuracy():
 
 
 def test_quant_closed_form():
-    s = np.float32(0.5)
+    mult = np.float32(2.0)
     y = np.array([1.25, 1.75, -1.25, 0.0, 1000.0, -1000.0, 63.25, 63.75], dtype=np.float32)
-    # y / s = 2.5, 3.5, -2.5, 0, 2000, -2000, 126.5, 127.5 -> half to even, then saturate at +-127
-    assert nm.quant_i8(y, s).tolist() == [2, 4, -2, 0, 127, -127, 126, 127]
+    # y * 2 = 2.5, 3.5, -2.5, 0, 2000, -2000, 126.5, 127.5 -> half to even, then saturate at +-127
+    assert nm.quant_i8(y, mult).tolist() == [2, 4, -2, 0, 127, -127, 126, 127]
 
 
 def test_ln_silu_against_float64():
