@@ -90,6 +90,7 @@ __global__ __launch_bounds__(kColThreads) void spconv_col_k(ColConvArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t s_w[WLDS ? G::WBYTES : 16];
     __shared__ __attribute__((aligned(16))) uint8_t s_x[NBUF][G::XBYTES];
     __shared__ int s_z[NBUF][3 * kWin];
+    __shared__ __attribute__((aligned(16))) uint8_t s_zero[16];  // operand of absent taps and padding lanes
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int r = lane & 15, g = lane >> 4;
@@ -102,6 +103,7 @@ __global__ __launch_bounds__(kColThreads) void spconv_col_k(ColConvArgs a) {
     if constexpr (WLDS) {
         for (int e = tid; e < G::WBYTES / 16; e += kColThreads) ((v4i*)s_w)[e] = ((const v4i*)wg)[e];
     }
+    if (tid == 0) *(v4i*)s_zero = v4i{0, 0, 0, 0};
 
     // Window of segment `sg`: slice d in {0,1,2} holds voxels s0 + (d-1)*W - 1 + q, q in [0, kWin).
     v4i pf[G::PF];
@@ -154,10 +156,11 @@ __global__ __launch_bounds__(kColThreads) void spconv_col_k(ColConvArgs a) {
         const int buf = NBUF == 2 ? (it & 1) : 0;
         const int s0 = seg * kSeg;
         const int nxt = seg + gridDim.x;
-        if constexpr (NBUF == 2) {
-            if (nxt < nseg) fetch(nxt);  // in flight during this segment's compute
-        }
         __syncthreads();  // window `buf` (and the weights) visible to all waves
+        if constexpr (NBUF == 2) {
+            if (nxt < nseg) fetch(nxt);  // in flight during this segment's compute (issued after the barrier,
+                                         // which waits for all outstanding memory operations)
+        }
 
         // ---- 27-bit tap masks of the wave's 32 rows (lane l < 32 computes row l), branch-free
         uint32_t mk = 0;
@@ -192,84 +195,100 @@ __global__ __launch_bounds__(kColThreads) void spconv_col_k(ColConvArgs a) {
 #pragma unroll
             for (int j = 0; j < NB; ++j) acc[rb][j] = acc_t{0, 0, 0, 0};
 
-        const uint8_t* sx = s_x[buf];
-        const int lr0 = 32 * wv + r;
-        // Operands of one MFMA step for this lane: tap v (or -1), chunk c.
-        auto load_ops = [&](int v, int c, v4i& xa0, v4i& xa1, v4i (&wb)[NB]) {
-            xa0 = v4i{0, 0, 0, 0};
-            xa1 = v4i{0, 0, 0, 0};
-            const bool act = v >= 0 && c < NCH;
+        const int lr0 = 32 * wv + r;  // window-relative row of this lane in row block 0
+        // Operand addresses: lane-constant LDS byte offsets plus a wave-uniform (scalar) offset per tap. A lane whose
+        // row lacks the tap, or whose chunk is padding (c >= NCH), reads the zero slot instead of branching.
+        constexpr int SPT = NCH >= 4 ? NCH / 4 : 1;  // MFMA steps per tap (chunk 4s + g)
+        constexpr int TPS = NCH >= 3 ? 1 : 4 / NCH;  // taps per MFMA step (slot g / NCH, chunk g % NCH)
+        constexpr int WSTR = 16 * 27 * ROWB;         // byte distance between 16-channel weight blocks
+        const int slot = TPS == 1 ? 0 : g / NCH;
+        const int cl = TPS == 1 ? (g < NCH ? g : 0) : g - slot * NCH;  // chunk of this lane (step 0)
+        const bool lane_on = TPS == 1 ? g < NCH || NCH >= 4 : true;
+        const uint32_t mk0 = lane_on ? mrow0 : 0u, mk1 = lane_on ? mrow1 : 0u;
+        typedef const __attribute__((address_space(3))) uint8_t* lds_ptr;
+        const lds_ptr xbase = (lds_ptr)(s_x[buf]) + (lr0 * ROWB + cl * 16);
+        const lds_ptr zslot = (lds_ptr)s_zero;
+        const lds_ptr wbase = (lds_ptr)s_w + (WLDS ? r * 27 * ROWB + cl * 16 : 0);
+        const uint8_t* wgl = wg + (r * 27 * ROWB + cl * 16);
+
+        struct Ops {
+            v4i x0, x1, w[NB];
+        };
+        // v: this lane's tap (wave-uniform when TPS == 1); st: step within the tap (wave-uniform)
+        auto load = [&](int v, int st, Ops& o) {
             const int vv = v < 0 ? 0 : v;
-            const int base = (vv / 9) * kWin + (vv / 3) % 3;
-            if (act && ((mrow0 >> vv) & 1u)) xa0 = *(const v4i*)(sx + (base + lr0) * ROWB + c * 16);
-            if (act && ((mrow1 >> vv) & 1u)) xa1 = *(const v4i*)(sx + (base + lr0 + 16) * ROWB + c * 16);
+            const int xo = ((vv / 9) * kWin + (vv / 3) % 3) * ROWB + st * 64;
+            const bool h0 = v >= 0 && ((mk0 >> vv) & 1u);
+            const bool h1 = v >= 0 && ((mk1 >> vv) & 1u);
+            const lds_ptr p0 = h0 ? xbase + xo : zslot;
+            const lds_ptr p1 = h1 ? xbase + (xo + 16 * ROWB) : zslot;
+            o.x0 = *(const __attribute__((address_space(3))) v4i*)p0;
+            o.x1 = *(const __attribute__((address_space(3))) v4i*)p1;
+            const int wo = vv * ROWB + st * 64;
 #pragma unroll
             for (int j = 0; j < NB; ++j) {
-                wb[j] = v4i{0, 0, 0, 0};
-                const int off = ((16 * j + r) * 27 + vv) * ROWB + c * 16;
-                if (act) {
-                    if constexpr (WLDS)
-                        wb[j] = *(const v4i*)(s_w + off);
-                    else
-                        wb[j] = *(const v4i*)(wg + off);
-                }
+                if constexpr (WLDS)
+                    o.w[j] = *(const __attribute__((address_space(3))) v4i*)(wbase + (wo + j * WSTR));
+                else
+                    o.w[j] = *(const v4i*)(wgl + (wo + j * WSTR));
             }
         };
-        // Unit schedule: NCH >= 4 -> NCH/4 steps per tap (chunk 4s + g); NCH == 3 -> one step per tap (chunk g,
-        // group 3 idle); NCH in {1, 2} -> 4/NCH taps per step (slot g / NCH, chunk g % NCH).
-        constexpr int SPT = NCH >= 4 ? NCH / 4 : 1;
-        constexpr int TPS = NCH >= 3 ? 1 : 4 / NCH;
+        auto mma_all = [&](const Ops& o) {
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                mma_col(acc[0][j], o.w[j], o.x0, T{});
+                mma_col(acc[1][j], o.w[j], o.x1, T{});
+            }
+        };
+        // Scalar unit iterator over the active taps; after the last unit it yields v = -1 (zero operands), so the
+        // operand loads of the next unit are issued unconditionally and the LDS wait counts stay static.
         uint32_t rem = uni;
         int cur_v = -1, cur_s = SPT;
-        auto next_unit = [&](int& v_lane, int& c_lane) -> bool {
+        auto next = [&](int& v, int& st) {
             if constexpr (TPS == 1) {
                 if (cur_s == SPT) {
-                    if (rem == 0) return false;
-                    cur_v = __builtin_ctz(rem);
-                    rem &= rem - 1;
+                    cur_v = rem ? (int)__builtin_ctz(rem) : -1;
+                    rem = rem ? rem & (rem - 1) : 0u;
                     cur_s = 0;
                 }
-                v_lane = cur_v;
-                c_lane = 4 * cur_s + g;
-                ++cur_s;
-                return true;
+                v = cur_v;
+                st = cur_s++;
             } else {
-                if (rem == 0) return false;
                 int vs[TPS];
 #pragma unroll
                 for (int k = 0; k < TPS; ++k) {
                     vs[k] = rem ? (int)__builtin_ctz(rem) : -1;
-                    rem &= rem ? rem - 1 : 0u;
+                    rem = rem ? rem & (rem - 1) : 0u;
                 }
-                const int slot = g / NCH;
-                int v = vs[0];
+                int vl = vs[0];
 #pragma unroll
-                for (int k = 1; k < TPS; ++k) v = slot == k ? vs[k] : v;
-                v_lane = v;
-                c_lane = g - slot * NCH;
-                return true;
+                for (int k = 1; k < TPS; ++k) vl = slot == k ? vs[k] : vl;
+                v = vl;
+                st = 0;
             }
         };
-        {
-            v4i xa0, xa1, wb[NB];
-            int v, c;
-            bool have = next_unit(v, c);
-            if (have) load_ops(v, c, xa0, xa1, wb);
-            while (have) {
-                v4i nxa0, nxa1, nwb[NB];
-                int nv, nc;
-                const bool more = next_unit(nv, nc);
-                if (more) load_ops(nv, nc, nxa0, nxa1, nwb);
-#pragma unroll
-                for (int j = 0; j < NB; ++j) {
-                    mma_col(acc[0][j], wb[j], xa0, T{});
-                    mma_col(acc[1][j], wb[j], xa1, T{});
-                }
-                if (!more) break;
-                xa0 = nxa0;
-                xa1 = nxa1;
-#pragma unroll
-                for (int j = 0; j < NB; ++j) wb[j] = nwb[j];
+        const int ntap = __builtin_popcount(uni);
+        const int nunits = TPS == 1 ? ntap * SPT : (ntap + TPS - 1) / TPS;
+        if (nunits > 0) {
+            Ops A, B;
+            int v, st;
+            next(v, st);
+            load(v, st, A);
+            // sched_barrier keeps the next unit's operand loads ahead of the current unit's MFMAs, so LDS latency
+            // overlaps the matrix work instead of being sunk next to its use.
+            for (int k = 0;; k += 2) {
+                next(v, st);
+                load(v, st, B);
+                __builtin_amdgcn_sched_barrier(0);
+                mma_all(A);
+                __builtin_amdgcn_sched_barrier(0);
+                if (k + 1 >= nunits) break;
+                next(v, st);
+                load(v, st, A);
+                __builtin_amdgcn_sched_barrier(0);
+                mma_all(B);
+                __builtin_amdgcn_sched_barrier(0);
+                if (k + 2 >= nunits) break;
             }
         }
 

@@ -86,11 +86,18 @@ class RefinerStep:
         self.st_prompt = torch.zeros((B, 2), dtype=torch.float32, device=device)
         self.st_final = torch.zeros((B, 2), dtype=torch.float32, device=device)
 
-    def __del__(self):
+    def close(self) -> None:
+        """Releases the device workspace and graphs (also done when the object is collected)."""
         h = getattr(self, "_h", None)
         if h:
-            lib().pmg_refiner_destroy(h)
             self._h = None
+            lib().pmg_refiner_destroy(h)
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # interpreter shutdown: the library handle may already be gone
+            pass
 
     def __call__(self, points: torch.Tensor, lidar: torch.Tensor, conf: torch.Tensor,
                  out: Optional[torch.Tensor] = None):
