@@ -7,37 +7,258 @@ input_proj + prompt_proj -> 3 residual blocks = 6 int8 submanifold 3x3x3 conv la
 delta, on synthetic seeded inputs (promptmoge_amd.spec) already resident in HBM. One "step" is one replay of the
 captured HIP graph of that chain; the metric fit of the refined depth is timed separately (`final_fit_ms`).
 
-    value   active voxels refined per second = M / step time (whole job; one GPU)
-    roofline  the dominant kernel of the step (largest time per step), algorithmic bytes per launch / its average
-              duration, both measured here with HIP events on the stream it runs on (standalone launches of the
-              step's own kernels on the step's data)
+    value     active voxels refined per second = M / step time (whole job; one GPU)
+    roofline  the dominant kernel of the step (largest time per step): algorithmic bytes per launch / its average
+              launch duration. Durations come from HIP events around a captured graph of R back-to-back launches of
+              that kernel on the step's own data, recorded on the stream the kernel runs on. `traffic` is the HBM
+              bytes per launch measured by rocprofv3 FETCH_SIZE / WRITE_SIZE passes (see --write-traffic), read from
+              profiles/hbm_traffic_modelA.txt when that file is present.
     cpu_baseline  the oracle's restatement of the reference's CPU path (_fallback conv on fake-quantised operands,
-              fit_scale_shift with an exact k-th selection) timed on this host on one Model-A step
+              fit_scale_shift with an exact k-th selection) timed on this host: 1 warm-up + median of 5 Model-A steps
     conv_microbench  isolated int8 conv on 1,000,000 surface voxels in 1024^3, C = 64 and 128
+
+Other modes (used to produce the committed profiles):
+    --kernels-only     launch each per-step kernel --kernel-reps times eagerly (plus a 64 MiB copy for counter
+                       calibration) and exit; run under `rocprofv3 --pmc FETCH_SIZE` / `--pmc WRITE_SIZE`
+    --write-traffic OUT FETCH_DIR WRITE_DIR
+                       turn those two counter runs into per-kernel HBM bytes per launch (scaled by the copy kernel's
+                       known size) and write them to OUT
 """
 from __future__ import annotations
 
 import argparse
+import csv
+import glob
 import json
 import os
+import statistics
 import sys
 import time
 
+ROOT = os.path.dirname(os.path.abspath(__file__))
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
 METRIC = "refiner step latency ms + active voxels/s at 480×640; int8 conv TOPS (% peak)"
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_modelA.txt")
+CALIB_BYTES = 64 << 20  # the calibration copy: 64 MiB read + 64 MiB written
+
+# kernel-name substrings (as rocprofv3 prints them) for the per-step kernels
+KERNEL_SYMBOLS = {
+    "fit_prompt": "fit_k",
+    "conv_q": "spconv_col_k<signed char, 48, 1>",
+    "conv_rln": "spconv_col_k<signed char, 48, 5>",
+    "conv_rout": "spconv_col_k<signed char, 48, 6>",
+    "input_stage": "input_stage_k<48",
+}
 
 
-def _events_ms(fn, reps, stream):
+def graph_ms(fn, reps, stream):
+    """Average duration of fn() in ms: R launches captured into one graph, timed with events on `stream`."""
     import torch
 
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(reps):
-        fn()
-    e1.record(stream)
+    fn()
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / reps
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for _ in range(reps):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    times = []
+    for _ in range(3):
+        e0.record(stream)
+        g.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1) / reps)
+    return statistics.median(times)
+
+
+def algorithmic_bytes(cfg):
+    """Bytes per launch each per-step kernel must move, from the per-unit figures of the measurement contract:
+    conv  M*(Ci + b_out*Co + 108) + 27*Ci*Co  (codes in, outputs, a 27-entry int32 map per voxel, weights; the
+          column conv derives the map from 4-byte keys instead of reading 108 B, see `minimal` below)
+    fit   18 B per element per trim round (z, target, mask for the sums; again for the residual pass) + 9 B final.
+    `minimal` lists what these kernels actually have to read and write once."""
+    M, C, it = cfg.M, cfg.C, cfg.fit_iters
+    wb = 27 * C * C
+    contract = {
+        "fit_prompt": M * (18 * it + 9),
+        "conv_q": M * (C + C + 108) + wb,
+        "conv_rln": M * (C + 4 * C + 4 * C + C + 108) + wb,  # + fp32 residual in/out, next codes
+        "conv_rout": M * (C + 4 * C + 12 + 12 + 108) + wb,  # + fp32 residual in, point map in/out
+    }
+    minimal = {
+        "fit_prompt": M * 12,
+        "conv_q": M * (C + 4 + C) + wb,
+        "conv_rln": M * (C + 4 + 4 * C + 4 * C + C) + wb,
+        "conv_rout": M * (C + 4 + 4 * C + 12 + 12) + wb,
+    }
+    return contract, minimal
+
+
+def read_traffic():
+    """Per-kernel HBM bytes per launch from profiles/hbm_traffic_modelA.txt (lines `traffic <name> <fetch> <write>`)."""
+    out = {}
+    if not os.path.exists(TRAFFIC_FILE):
+        return out
+    for line in open(TRAFFIC_FILE):
+        p = line.split()
+        if len(p) == 4 and p[0] == "traffic":
+            out[p[1]] = (float(p[2]), float(p[3]))
+    return out
+
+
+def write_traffic(out_path, fetch_dir, write_dir):
+    """Averages FETCH_SIZE / WRITE_SIZE (KiB per dispatch) per kernel over two rocprofv3 --pmc runs of
+    `bench.py --kernels-only`, scales each counter so that the calibration copy reads and writes CALIB_BYTES,
+    and writes the per-kernel HBM bytes per launch."""
+
+    def load(d, counter):
+        vals = {}
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                if r["Counter_Name"] == counter:
+                    vals.setdefault((r["Kernel_Name"], r["Grid_Size"]), []).append(float(r["Counter_Value"]) * 1024)
+        return vals
+
+    fv, wv = load(fetch_dir, "FETCH_SIZE"), load(write_dir, "WRITE_SIZE")
+
+    def calib(vals):
+        # the copy kernel is the only dispatch moving about CALIB_BYTES; take the largest per-dispatch value
+        # among kernels whose name marks them as copies
+        cands = [statistics.median(v) for (k, _), v in vals.items() if "copy" in k.lower() or "elementwise" in k]
+        return CALIB_BYTES / max(cands)
+
+    fs, ws = calib(fv), calib(wv)
+    lines = [f"# HBM traffic per launch, Model A (480x640, C=48), from rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE",
+             f"# scale factors from a {CALIB_BYTES} B copy: FETCH_SIZE x{fs:.4f}, WRITE_SIZE x{ws:.4f}",
+             "# columns: traffic <kernel> <fetch bytes> <write bytes>"]
+    for name, sym in KERNEL_SYMBOLS.items():
+        f = [statistics.median(v) for (k, _), v in fv.items() if sym in k]
+        w = [statistics.median(v) for (k, _), v in wv.items() if sym in k]
+        if f and w:
+            lines.append(f"traffic {name} {f[0] * fs:.0f} {w[0] * ws:.0f}")
+    with open(out_path, "w") as fh:
+        fh.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
+def setup(cfg_name):
+    import torch
+
+    from promptmoge_amd import ops, spec
+    from promptmoge_amd.refiner import RefinerStep
+
+    dev = torch.device("cuda:0")
+    cfg = spec.CONFIGS[cfg_name]
+    sc = spec.make_scene(cfg)
+    w = spec.refiner_for(cfg, sc)
+    stream = torch.cuda.Stream()
+    env = {"cfg": cfg, "sc": sc, "w": w, "stream": stream}
+    with torch.cuda.stream(stream):
+        P = torch.from_numpy(sc.points[None].copy()).to(dev)
+        env.update(P=P, Pout=torch.empty_like(P), L=torch.from_numpy(sc.lidar[None].copy()).to(dev),
+                   Cf=torch.from_numpy(sc.conf[None].copy()).to(dev))
+        step = RefinerStep(w, 1, cfg.H, cfg.W, precision=cfg.precision, fit_iters=cfg.fit_iters)
+        step(env["P"], env["L"], env["Cf"], out=env["Pout"])
+        step.check()
+        zq, _, _ = ops.voxelize(P[..., 2:], 256.0, stride=3, shape=(1, cfg.H, cfg.W))
+        x = step.buffer("x").clone()
+        b0, b1 = step.weights.blocks[0], step.weights.blocks[-1]
+        q1 = ops.ln_silu_quant(x, b0["gamma"], b0["beta"], b0["m1"])
+        q2 = ops.spconv_col(q1, zq, b0["w1"], ops.EPI_Q, a_scale=b0["a1"], w_scale=b0["s1"], bias=b0["b1"],
+                            out_mult=b0["m2"])
+        xr, nq, Pk = x.clone(), torch.empty_like(q1), torch.empty_like(P)
+        torch.cuda.synchronize()
+    env["step"] = step
+    env["kernels"] = {
+        "fit_prompt": lambda: ops.fit_prompt(P, env["L"], env["Cf"], iters=cfg.fit_iters),
+        "conv_q": lambda: ops.spconv_col(q1, zq, b0["w1"], ops.EPI_Q, a_scale=b0["a1"], w_scale=b0["s1"],
+                                         bias=b0["b1"], out_mult=b0["m2"], out=q2),
+        "conv_rln": lambda: ops.spconv_col(q2, zq, b0["w2"], ops.EPI_RLN, a_scale=b0["a2"], w_scale=b0["s2"],
+                                           bias=b0["b2"], skip=xr, out=xr, ln_gamma=b1["gamma"], ln_beta=b1["beta"],
+                                           next_mult=b1["m1"], next_q=nq),
+        "conv_rout": lambda: ops.spconv_col(q2, zq, b1["w2"], ops.EPI_ROUT, a_scale=b1["a2"], w_scale=b1["s2"],
+                                            bias=b1["b2"], skip=x, out_w=step.weights.out_w,
+                                            out_b=step.weights.out_b, points=P, points_out=Pk),
+    }
+    return env
+
+
+def kernels_only(args):
+    import torch
+
+    env = setup(args.config)
+    with torch.cuda.stream(env["stream"]):
+        for _ in range(3):
+            env["step"](env["P"], env["L"], env["Cf"], out=env["Pout"])
+        for name, fn in env["kernels"].items():
+            for _ in range(args.kernel_reps):
+                fn()
+        a = torch.empty(CALIB_BYTES // 4, dtype=torch.float32, device="cuda")
+        b = torch.empty_like(a)
+        a.fill_(1.0)
+        for _ in range(args.kernel_reps):
+            b.copy_(a)
+        torch.cuda.synchronize()
+    print("kernels-only done", flush=True)
+    return 0
+
+
+def microbench(stream):
+    import torch
+
+    from promptmoge_amd import ops, spec
+
+    dev = torch.device("cuda:0")
+    coords = spec.make_voxels(1_000_000, 1024, seed=21)
+    with torch.cuda.stream(stream):
+        cd = torch.from_numpy(coords).to(dev)
+        shape = (1, 1024, 1024, 1024)
+        ntu, tmu, _ = ops.nmap_hash(cd, shape)
+        torch.cuda.synchronize()
+        hash_ms = graph_ms(lambda: ops.nmap_hash(cd, shape), 5, stream)
+        pu = int((ntu >= 0).sum().item())
+        M = coords.shape[0]
+        micro = {"voxels": int(M), "pairs": pu, "mean_active_taps": round(pu / M, 3), "hash_map_ms": round(hash_ms, 4),
+                 "hash_map_gbs": round((16 * M + 108 * M) / (hash_ms * 1e-3) / 1e9, 1)}
+        g = torch.Generator(device="cpu").manual_seed(5)
+        for Cm in (64, 128):
+            xm = torch.randint(-127, 128, (M, Cm), generator=g, dtype=torch.int8).to(dev)
+            wm = torch.randint(-127, 128, (Cm, 3, 3, 3, Cm), generator=g, dtype=torch.int8).to(dev)
+            sm = torch.full((Cm,), 1e-4, device=dev)
+            om = torch.empty((M, Cm), dtype=torch.int8, device=dev)
+            t = graph_ms(lambda: ops.spconv_i8(xm, ntu, tmu, wm, ops.EPI_Q, a_scale=0.01, w_scale=sm, out_mult=20.0,
+                                               out=om), 5, stream)
+            tops = 2 * Cm * Cm * pu / (t * 1e-3) / 1e12
+            micro[f"C{Cm}"] = {"ms": round(t, 4), "tops": round(tops, 2), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
+    return micro
+
+
+def cpu_baseline(env):
+    from oracle import refiner as orf
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:
+        threads = os.cpu_count() or 1
+    cfg, sc, w = env["cfg"], env["sc"], env["w"]
+    run = lambda: orf.step_fakequant(sc.points[None], sc.lidar[None], sc.conf[None], w, iters=cfg.fit_iters)
+    run()
+    ts = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        run()
+        ts.append(time.perf_counter() - t0)
+    tc = statistics.median(ts)
+    return {"value": round(cfg.M / tc, 1), "unit": "voxels/s", "cores": int(threads), "kind": "port",
+            "sample": f"1 warm-up + median of 5 steps of config {cfg.name} ({cfg.M} voxels each), NumPy restatement "
+                      f"of the _fallback path (BLAS {threads} threads, elementwise work 1 thread)",
+            "ms_per_step": round(tc * 1e3, 1)}
 
 
 def main() -> int:
@@ -45,137 +266,77 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="A", choices=["A", "B", "T", "H"])
+    ap.add_argument("--config", default="A", choices=["A", "B", "H"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-micro", action="store_true", help="skip the 1M-voxel conv microbench")
-    ap.add_argument("--kernel-reps", type=int, default=50)
+    ap.add_argument("--kernel-reps", type=int, default=20)
+    ap.add_argument("--kernels-only", action="store_true")
+    ap.add_argument("--write-traffic", nargs=3, metavar=("OUT", "FETCH_DIR", "WRITE_DIR"))
     args = ap.parse_args()
+    if args.write_traffic:
+        write_traffic(*args.write_traffic)
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the refiner step is per frame and this build uses no collectives); "
               f"--gpus {args.gpus} is not supported", file=sys.stderr)
         return 2
 
-    import numpy as np
     import torch
 
-    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-    from promptmoge_amd import ops, spec
+    sys.path.insert(0, ROOT)
+    if args.kernels_only:
+        return kernels_only(args)
     from promptmoge_amd.refiner import RefinerStep
 
-    dev = torch.device("cuda:0")
-    cfg = spec.CONFIGS[args.config]
-    sc = spec.make_scene(cfg)
-    w = spec.refiner_for(cfg, sc)
+    env = setup(args.config)
+    cfg, stream, step = env["cfg"], env["stream"], env["step"]
+    P, Pout, L, Cf = env["P"], env["Pout"], env["L"], env["Cf"]
     M, C = cfg.M, cfg.C
-    stream = torch.cuda.Stream()
-    out = {}
     with torch.cuda.stream(stream):
-        P = torch.from_numpy(sc.points[None].copy()).to(dev)
-        Pout = torch.empty_like(P)
-        L = torch.from_numpy(sc.lidar[None].copy()).to(dev)
-        Cf = torch.from_numpy(sc.conf[None].copy()).to(dev)
-        step = RefinerStep(w, 1, cfg.H, cfg.W, precision=cfg.precision, fit_iters=cfg.fit_iters)
         for _ in range(args.warmup):
             step(P, L, Cf, out=Pout)
         step.check()
         torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
-        ms = _events_ms(lambda: step(P, L, Cf, out=Pout), args.steps, stream)
+        e0.record(stream)
+        for _ in range(args.steps):
+            step(P, L, Cf, out=Pout)
+        e1.record(stream)
+        torch.cuda.synchronize()
         wall = time.perf_counter() - t0
+        ms = e0.elapsed_time(e1) / args.steps
         step.check()
 
-        stepf = RefinerStep(w, 1, cfg.H, cfg.W, precision=cfg.precision, fit_iters=cfg.fit_iters, final_fit=True)
+        stepf = RefinerStep(env["w"], 1, cfg.H, cfg.W, precision=cfg.precision, fit_iters=cfg.fit_iters,
+                            final_fit=True)
         for _ in range(5):
             stepf(P, L, Cf, out=Pout)
-        ms_with_final = _events_ms(lambda: stepf(P, L, Cf, out=Pout), 50, stream)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(50):
+            stepf(P, L, Cf, out=Pout)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms_with_final = e0.elapsed_time(e1) / 50
         stepf.check()
 
-        # ---- per-kernel timing with the step's own shapes and data (standalone launches of the step's kernels)
-        reps = args.kernel_reps
-        zq, _, _ = ops.voxelize(P[..., 2:], 256.0, stride=3, shape=(1, cfg.H, cfg.W))
-        x = step.buffer("x")
-        b0, b1 = step.weights.blocks[0], step.weights.blocks[-1]
-        q1 = ops.ln_silu_quant(x, b0["gamma"], b0["beta"], b0["m1"])
-        q2 = ops.spconv_col(q1, zq, b0["w1"], ops.EPI_Q, a_scale=b0["a1"], w_scale=b0["s1"], bias=b0["b1"],
-                            out_mult=b0["m2"])
-        xr = x.clone()
-        nq = torch.empty_like(q1)
-        kern = {}
-        kern["fit_prompt"] = _events_ms(lambda: ops.fit_prompt(P, L, Cf, iters=cfg.fit_iters), reps, stream)
-        kern["conv_q"] = _events_ms(lambda: ops.spconv_col(q1, zq, b0["w1"], ops.EPI_Q, a_scale=b0["a1"],
-                                                           w_scale=b0["s1"], bias=b0["b1"], out_mult=b0["m2"],
-                                                           out=q2), reps, stream)
-        kern["conv_rln"] = _events_ms(lambda: ops.spconv_col(q2, zq, b0["w2"], ops.EPI_RLN, a_scale=b0["a2"],
-                                                             w_scale=b0["s2"], bias=b0["b2"], skip=xr, out=xr,
-                                                             ln_gamma=b1["gamma"], ln_beta=b1["beta"],
-                                                             next_mult=b1["m1"], next_q=nq), reps, stream)
-        kern["conv_rout"] = _events_ms(lambda: ops.spconv_col(q2, zq, b1["w2"], ops.EPI_ROUT, a_scale=b1["a2"],
-                                                              w_scale=b1["s2"], bias=b1["b2"], skip=x,
-                                                              out_w=step.weights.out_w, out_b=step.weights.out_b,
-                                                              points=P, points_out=Pout), reps, stream)
-        nb = cfg.n_blocks
-        per_step = {"fit_prompt": kern["fit_prompt"], "conv_q": nb * kern["conv_q"],
-                    "conv_rln": (nb - 1) * kern["conv_rln"], "conv_rout": kern["conv_rout"]}
-        per_step["input_stage_and_launch_gaps"] = max(ms - sum(per_step.values()), 0.0)
-        dominant = max((k for k in per_step if k in kern), key=per_step.get)
-        # algorithmic bytes per launch (every byte the kernel must move at least once)
-        wb = 27 * C * C
-        alg = {
-            "fit_prompt": M * 12,                           # logz, LiDAR, conf: 4 B each
-            "conv_q": M * (C + 4 + C) + wb,                 # codes in, keys, codes out, weights
-            "conv_rln": M * (C + 4 + 4 * C + 4 * C + C) + wb,  # codes, keys, residual in/out, next codes
-            "conv_rout": M * (C + 4 + 4 * C + 12 + 12) + wb,  # codes, keys, residual, point map in/out
-        }
-        ach = alg[dominant] / (kern[dominant] * 1e-3) / 1e9
-        out["breakdown_ms"] = {k: round(v, 5) for k, v in kern.items()}
-        out["per_step_ms_est"] = {k: round(v, 5) for k, v in per_step.items()}
-        out["kernel_gbs"] = {k: round(alg[k] / (kern[k] * 1e-3) / 1e9, 1) for k in kern}
-        roofline = {"kernel": dominant, "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
-                    "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
-                    "algorithmic_bytes": int(alg[dominant]), "avg_launch_ms": round(kern[dominant], 5)}
+        kern = {k: graph_ms(fn, args.kernel_reps, stream) for k, fn in env["kernels"].items()}
+    nb = cfg.n_blocks
+    per_step = {"fit_prompt": kern["fit_prompt"], "conv_q": nb * kern["conv_q"],
+                "conv_rln": (nb - 1) * kern["conv_rln"], "conv_rout": kern["conv_rout"]}
+    per_step["input_stage_and_gaps"] = max(ms - sum(per_step.values()), 0.0)
+    dominant = max(kern, key=lambda k: per_step[k])
+    contract, minimal = algorithmic_bytes(cfg)
+    ach = contract[dominant] / (kern[dominant] * 1e-3) / 1e9
+    traffic = read_traffic().get(dominant)
+    roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None if traffic is None else int(sum(traffic)),
+                "kernel": dominant, "algorithmic_bytes": int(contract[dominant]),
+                "minimal_bytes": int(minimal[dominant]), "avg_launch_ms": round(kern[dominant], 5)}
 
-    # ---- conv microbench
-    micro = None
-    if not args.no_micro:
-        coords = spec.make_voxels(1_000_000, 1024, seed=21)
-        with torch.cuda.stream(stream):
-            cd = torch.from_numpy(coords).to(dev)
-            shape = (1, 1024, 1024, 1024)
-            ntu, tmu, _ = ops.nmap_hash(cd, shape)
-            torch.cuda.synchronize()
-            hash_ms = _events_ms(lambda: ops.nmap_hash(cd, shape), 10, stream)
-            pu = int((ntu >= 0).sum().item())
-            micro = {"voxels": int(coords.shape[0]), "pairs": pu, "mean_active_taps": round(pu / coords.shape[0], 3),
-                     "hash_map_ms": round(hash_ms, 4)}
-            g = torch.Generator(device="cpu").manual_seed(5)
-            for Cm in (64, 128):
-                xm = torch.randint(-127, 128, (coords.shape[0], Cm), generator=g, dtype=torch.int8).to(dev)
-                wm = torch.randint(-127, 128, (Cm, 3, 3, 3, Cm), generator=g, dtype=torch.int8).to(dev)
-                sm = torch.full((Cm,), 1e-4, device=dev)
-                om = torch.empty((coords.shape[0], Cm), dtype=torch.int8, device=dev)
-                f = lambda: ops.spconv_i8(xm, ntu, tmu, wm, ops.EPI_Q, a_scale=0.01, w_scale=sm, out_mult=20.0, out=om)
-                f()
-                t = _events_ms(f, 10, stream)
-                tops = 2 * Cm * Cm * pu / (t * 1e-3) / 1e12
-                micro[f"C{Cm}"] = {"ms": round(t, 4), "tops": round(tops, 2), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
-
-    # ---- CPU baseline: the oracle's restatement of the reference CPU path, one Model-A step
-    cpu = None
-    if not args.no_cpu:
-        from oracle import refiner as orf
-
-        try:
-            from threadpoolctl import threadpool_info
-
-            threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
-        except Exception:
-            threads = os.cpu_count() or 1
-        t0 = time.perf_counter()
-        orf.step_fakequant(sc.points[None], sc.lidar[None], sc.conf[None], w, iters=cfg.fit_iters)
-        tc = time.perf_counter() - t0
-        cpu = {"value": round(M / tc, 1), "unit": "voxels/s", "cores": int(threads), "kind": "port",
-               "sample": f"1 step of config {cfg.name} ({M} voxels), NumPy (BLAS {threads} threads, elementwise 1)",
-               "ms_per_step": round(tc * 1e3, 1)}
+    micro = None if args.no_micro else microbench(stream)
+    cpu = None if args.no_cpu else cpu_baseline(env)
 
     line = {
         "metric": METRIC, "value": round(M / (ms * 1e-3), 1), "unit": "voxels/s", "n_gpus": 1, "steps": args.steps,
@@ -186,7 +347,11 @@ def main() -> int:
                    "voxels": M, "parallelism": "1 GPU"},
         "final_fit_ms": round(ms_with_final - ms, 5), "step_with_final_fit_ms": round(ms_with_final, 5),
         "wall_s_timed": round(wall, 3),
-        "roofline": roofline, "cpu_baseline": cpu, "conv_microbench": micro, **out,
+        "roofline": roofline, "cpu_baseline": cpu, "conv_microbench": micro,
+        "kernel_ms": {k: round(v, 5) for k, v in kern.items()},
+        "per_step_ms": {k: round(v, 5) for k, v in per_step.items()},
+        "kernel_gbs_contract": {k: round(contract[k] / (kern[k] * 1e-3) / 1e9, 1) for k in kern},
+        "kernel_gbs_minimal": {k: round(minimal[k] / (kern[k] * 1e-3) / 1e9, 1) for k in kern},
     }
     print(json.dumps(line), flush=True)
     return 0
