@@ -173,13 +173,17 @@ int pmg_ln_silu_f16(const float* x, int64_t M, int C, const float* gamma, const 
 /* ------------------------------------------------------------------------------------------------------------ *
  * (4) Robust metric fit -- replaces fit_scale_shift (moge/model/modules/prompt_stem.py:211-240): trimmed least
  * squares target ~= s*z + t on mask, `iters` trim rounds then a final solve; k = max(long(fp32(1-trim)*count),
- * min_points) and the trim threshold is the exact k-th smallest relative residual (torch.kthvalue), found by a
- * radix select; (1, 0) when fewer than min_points mask pixels. Sums in fp64, one persistent kernel per batch item
- * with device-wide barriers, no host round trip.
+ * min_points) and the trim threshold is the exact k-th smallest relative residual (torch.kthvalue), selected
+ * inside a bracket around the previous round's threshold, or by radix passes when it leaves the bracket; (1, 0)
+ * when fewer than min_points mask pixels. Sums in fp64, one persistent kernel per batch item with device-wide
+ * barriers, no host round trip.
  *   z, target: [B][N] fp32; mask: [B][N] uint8 (0/1); st: [B][2] fp32 (s, t) written on device.
  *   info (may be NULL): [B][5] int32 = (count, k, ok, threshold bits of the last trim round, device error flag:
  *   nonzero if a bounded device-wide wait expired, in which case (s, t) are not valid).
- * N <= 2^22 per batch item.
+ *   workspace: pmg_fit_workspace_bytes(N, iters) bytes, zero-filled before its first use; every call leaves it
+ *   ready for the next one (calls that share a workspace must be ordered, e.g. on one stream). After an expired
+ *   wait (error flag set) zero-fill it again.
+ * N <= 2^21 per batch item.
  * ------------------------------------------------------------------------------------------------------------ */
 size_t pmg_fit_workspace_bytes(int64_t N, int iters);
 int pmg_fit_scale_shift(const float* z, const float* target, const uint8_t* mask, int B, int64_t N, int iters,

@@ -335,8 +335,13 @@ int pmg_refiner_check(pmg_refiner* r, void* stream) {
     PMG_CHECK_HIP(hipStreamSynchronize((hipStream_t)stream));
     int err[2] = {0, 0};
     for (int k = 0; k < 2; ++k)
-        PMG_CHECK_HIP(hipMemcpy(&err[k], (uint8_t*)r->fit_ws[k] + 4, sizeof(int), hipMemcpyDeviceToHost));
-    if (err[0] || err[1]) return fail(PMG_E_DEVICE, "pmg_refiner_check: a device-wide wait in the metric fit expired");
+        PMG_CHECK_HIP(hipMemcpy(&err[k], (uint8_t*)r->fit_ws[k] + 64, sizeof(int), hipMemcpyDeviceToHost));
+    if (err[0] || err[1]) {
+        // the fit's barrier state is undefined after an expired wait: start the workspaces over
+        for (int k = 0; k < 2; ++k) PMG_CHECK_HIP(hipMemset(r->fit_ws[k], 0, r->fit_ws_bytes));
+        PMG_CHECK_HIP(hipDeviceSynchronize());
+        return fail(PMG_E_DEVICE, "pmg_refiner_check: a device-wide wait in the metric fit expired");
+    }
     return PMG_OK;
 }
 

@@ -53,6 +53,42 @@ __device__ inline int wave_max_i32(int v) {
 }
 
 // ---------------------------------------------------------------------------------------------------------------
+// Wave-level inclusive scans with DPP (gfx9 encodings): Hillis-Steele over each 16-lane row with row_shr 1, 2, 4, 8,
+// then row 0's total into row 1 and row 2's into row 3 (row_bcast:15 on rows 1 and 3), then the total of rows 0-1
+// into rows 2-3 (row_bcast:31 on rows 2 and 3). Lanes whose source is outside the row read 0. Lane 63 ends with
+// the wave total. The additions happen in a fixed order, so floating-point results are reproducible; each step
+// is a VALU op, far cheaper than a cross-lane permute through the LDS crossbar.
+template <int CTRL, int ROW_MASK>
+__device__ inline uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xf, false);
+}
+template <int CTRL, int ROW_MASK>
+__device__ inline double dpp_f64(double v) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = dpp_u32<CTRL, ROW_MASK>((uint32_t)u);
+    const uint32_t hi = dpp_u32<CTRL, ROW_MASK>((uint32_t)(u >> 32));
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+__device__ inline uint32_t wave_incl_scan_u32(uint32_t v) {
+    v += dpp_u32<0x111, 0xf>(v);
+    v += dpp_u32<0x112, 0xf>(v);
+    v += dpp_u32<0x114, 0xf>(v);
+    v += dpp_u32<0x118, 0xf>(v);
+    v += dpp_u32<0x142, 0xa>(v);
+    v += dpp_u32<0x143, 0xc>(v);
+    return v;
+}
+__device__ inline double wave_incl_scan_f64(double v) {
+    v += dpp_f64<0x111, 0xf>(v);
+    v += dpp_f64<0x112, 0xf>(v);
+    v += dpp_f64<0x114, 0xf>(v);
+    v += dpp_f64<0x118, 0xf>(v);
+    v += dpp_f64<0x142, 0xa>(v);
+    v += dpp_f64<0x143, 0xc>(v);
+    return v;
+}
+
+// ---------------------------------------------------------------------------------------------------------------
 // Device-wide barrier for persistent kernels whose whole grid is resident (grid <= CUs x resident blocks/CU, one
 // kernel on the stream at a time). `counter` starts at 0 for the launch; barrier number `index` (0, 1, 2, ...)
 // waits until counter == (index + 1) * nblocks. The wait is bounded: on expiry the block raises `err` and every

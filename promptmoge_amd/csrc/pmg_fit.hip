@@ -5,15 +5,27 @@
 //       r = |s*z + t - target| / max(target, 1e-3) on mask, +inf elsewhere
 //       thr = kthvalue(r, min(k, N));  w = mask & (r <= thr)
 //
-// Design. One persistent kernel per batch item; its whole grid is resident, so phases are separated by a
-// device-wide barrier instead of kernel launches, and every element's (z, target, mask) lives in registers for
-// the whole fit: HBM is read once. Sums are accumulated in fp64 (n*sxx - sx^2 cancels badly in fp32) in a fixed
-// order (thread, wave butterfly, wave order, then block order), and every block reduces the per-block partials
-// itself, so all blocks hold bit-identical (s, t) without another barrier. The threshold is the exact k-th
-// smallest residual: non-negative fp32 values order like their bit patterns, so a radix select over the 32 bits
-// in digits of 11, 11 and 10 bits finds it (LDS histogram per block, merged with one global atomic per non-empty
-// bin, then every block scans the merged histogram). 4 barriers per trim round, 1 for the final solve.
+// Design. One persistent kernel per batch item with few, fat blocks (256 threads x 32 elements = 8192 elements each,
+// held in registers for the whole fit, so HBM is read once): a device-wide barrier costs more the more blocks
+// arrive (about 1.7 us at 38 blocks, 7.5 us at 256 on MI355X), and a trim round is latency-bound, not
+// bandwidth-bound. Phases are separated by a self-resetting barrier. Sums are accumulated in fp64
+// (n*sxx - sx^2 cancels badly in fp32) in a fixed order, and every block reduces the published per-block partials
+// itself, so all blocks hold bit-identical (s, t) and take identical branches.
+//
+// The threshold is the exact k-th smallest residual; non-negative fp32 values order like their bit patterns. A trim
+// round costs ONE barrier when the threshold stays inside a bracket [lo, hi] predicted from the previous round
+// (+-(2 |last move| + 1024) ulps, at most +-2^18): each block publishes how many of its residuals fall below lo,
+// its fp64 sums over those (they are in the new weight set whatever the exact threshold), and its residuals inside
+// the bracket ("candidates", with z and target). After the barrier every block loads all candidates into LDS,
+// selects the exact k-th among them (each thread ranks one candidate when there are at most 256, else an LDS radix
+// select), and adds the candidates at or below it to the sums -- the next (s, t) without a second barrier. When
+// the k-th falls outside the bracket (always in round 0), two global radix passes over the top 22 bits (LDS
+// histogram per block, merged by atomics) narrow the bracket to one 1024-value bin; if even that bin holds more
+// than kCandCap candidates, a third pass finds the threshold and the sums take one more barrier.
 // This replaces the reference device engine's approximate two-level histogram (MetricFit.metal:141-189).
+//
+// Workspace: zero-filled once before its first use; the kernel leaves it reusable (the barrier returns to zero,
+// histograms are cleared at the start of every launch, everything else is overwritten before it is read).
 #include <climits>
 
 #include "pmg_common.h"
@@ -22,8 +34,28 @@
 namespace pmg {
 
 constexpr int kFitThreads = 256;
-constexpr int kFitEPT = 16;  // elements per thread held in registers
+constexpr int kFitWaves = kFitThreads / 64;
+constexpr int kFitEPT = 32;                            // elements per thread, in registers
+constexpr int kFitPerBlock = kFitThreads * kFitEPT;    // 8192
+constexpr int kFitMaxBlocks = kFitThreads;             // N <= 2^21
 constexpr int kFitBins = 2048;
+constexpr int kCandCap = 32768;                        // candidates every block holds in LDS (128 KiB)
+constexpr uint32_t kInvalid = 0xffffffffu;             // residual key of a padding slot: above every residual
+constexpr int kFitTraceRounds = 64;
+constexpr size_t kFitHeader = 4096;                    // barrier, error flag, trace
+
+struct FitWs {
+    unsigned* bar;        // [0] arrivals, [1] generation
+    int* err;
+    uint32_t* trace;      // block 0's record: per round the selection path | candidates << 4 and the wall clock
+                          // (100 MHz) at its end, per round the threshold bits; launch and first-solve times
+    uint64_t* partials;   // [2][kFitMaxBlocks][5] fp64 bit patterns
+    unsigned* counts;     // [2][kFitMaxBlocks][2]: below, candidates
+    unsigned* hist;       // [iters][3][kFitBins]
+    uint32_t* c_key;      // [2][nb][kFitPerBlock]: residual bits | mask << 31
+    float* c_z;           // [2][nb][kFitPerBlock]
+    float* c_t;           // [2][nb][kFitPerBlock]
+};
 
 struct FitArgs {
     int mode;  // 0: (z, target, mask) arrays; 1: prompt map (logz, LiDAR, conf)
@@ -42,29 +74,49 @@ struct FitArgs {
     int b;  // batch item
     float* st;
     int32_t* info;
-    uint64_t* partials;  // [nblocks][5] fp64 bit patterns
-    unsigned* hist;      // [iters][3][kFitBins]
-    unsigned* counter;
-    int* err;
+    FitWs ws;
 };
 
-__device__ inline double wave_sum_f64(double v) {
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+// Device-wide barrier for a fully resident grid. The last block to arrive resets the arrival count and bumps the
+// generation; the others wait (bounded) for the generation to move. Global writes before it are visible after it.
+__device__ inline void fit_barrier(unsigned* bar, unsigned nb, int* err) {
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        const unsigned gen = __hip_atomic_load(&bar[1], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned old = __hip_atomic_fetch_add(&bar[0], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        if (old == nb - 1) {
+            __hip_atomic_store(&bar[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_add(&bar[1], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        } else if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) {
+            unsigned spins = 0;
+            while (__hip_atomic_load(&bar[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gen) {
+                __builtin_amdgcn_s_sleep(1);
+                if (++spins > (1u << 23)) {
+                    __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    }
+    __syncthreads();
 }
 
-// Fixed-order block reduction of 5 doubles; result valid in thread 0.
-__device__ inline void block_sum5(double (&v)[5], double (*red)[4]) {
+// Fixed-order block reduction of 5 doubles (DPP wave scans, then waves in order); result in every thread.
+__device__ inline void block_sum5(double (&v)[5], double (*red)[kFitWaves]) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
 #pragma unroll
     for (int k = 0; k < 5; ++k) {
-        v[k] = wave_sum_f64(v[k]);
-        if (lane == 0) red[k][w] = v[k];
+        v[k] = wave_incl_scan_f64(v[k]);
+        if (lane == 63) red[k][w] = v[k];
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
 #pragma unroll
-        for (int k = 0; k < 5; ++k) v[k] = ((red[k][0] + red[k][1]) + red[k][2]) + red[k][3];
+    for (int k = 0; k < 5; ++k) {
+        double s = red[k][0];
+        for (int q = 1; q < kFitWaves; ++q) s += red[k][q];
+        v[k] = s;
     }
     __syncthreads();
 }
@@ -72,81 +124,257 @@ __device__ inline void block_sum5(double (&v)[5], double (*red)[4]) {
 // Exclusive scan of one unsigned per thread over the block; also returns the block total.
 __device__ inline unsigned block_excl_scan(unsigned v, unsigned* tmp, unsigned& total) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    unsigned inc = v;
-    for (int o = 1; o < 64; o <<= 1) {
-        const unsigned t = __shfl_up(inc, o, 64);
-        if (lane >= o) inc += t;
-    }
+    const unsigned inc = wave_incl_scan_u32(v);
     if (lane == 63) tmp[w] = inc;
     __syncthreads();
     unsigned before = 0;
-    for (int k = 0; k < w; ++k) before += tmp[k];
-    total = tmp[0] + tmp[1] + tmp[2] + tmp[3];
+    total = 0;
+    for (int k = 0; k < kFitWaves; ++k) {
+        before += k < w ? tmp[k] : 0u;
+        total += tmp[k];
+    }
     __syncthreads();
     return before + inc - v;
 }
 
-__device__ inline void load_element(const FitArgs& a, int64_t i, float& z, float& tg, bool& m) {
-    if (a.mode == 0) {
-        const int64_t o = (int64_t)a.b * a.N + i;
-        z = a.z[o];
-        tg = a.tg[o];
-        m = a.mask[o] != 0;
-    } else {
-        // v3.py:373-378 with the nearest index rule of F.interpolate.
-        const int row = (int)(i / a.W), col = (int)(i - (int64_t)(i / a.W) * a.W);
-        const float scy = (float)a.dh / (float)a.H, scx = (float)a.dw / (float)a.W;
-        int sy = (int)__builtin_floorf((float)row * scy);
-        int sx = (int)__builtin_floorf((float)col * scx);
-        sy = sy < a.dh - 1 ? sy : a.dh - 1;
-        sx = sx < a.dw - 1 ? sx : a.dw - 1;
-        const int64_t p = ((int64_t)a.b * a.dh + sy) * a.dw + sx;
-        const float d = a.lidar[p];
-        const float c = fmin_(fmax_(a.conf[p] / 2.0f, 0.0f), 1.0f);
-        z = exp_f32(a.logz[((int64_t)a.b * a.N + i) * a.stride]);
-        tg = d;
-        m = __builtin_isfinite(d) && d > 0.0f && c >= 0.999f;
+// Two exclusive scans in one pass (returns a's exclusive prefix; totals of a and b).
+__device__ inline unsigned block_excl_scan2(unsigned a, unsigned b, uint2* tmp, unsigned& ta, unsigned& tb) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const unsigned ia = wave_incl_scan_u32(a), ib = wave_incl_scan_u32(b);
+    if (lane == 63) tmp[w] = make_uint2(ia, ib);
+    __syncthreads();
+    unsigned before = 0;
+    ta = 0;
+    tb = 0;
+    for (int k = 0; k < kFitWaves; ++k) {
+        const uint2 q = tmp[k];
+        before += k < w ? q.x : 0u;
+        ta += q.x;
+        tb += q.y;
     }
+    __syncthreads();
+    return before + ia - a;
+}
+
+// Phase timestamps of block 0 (100 MHz wall clock) into the workspace header, for profiling the selection phases;
+// compiled in with -DPMG_FIT_PHASE_TRACE.
+#ifdef PMG_FIT_PHASE_TRACE
+#define FIT_MARK(k)                                                                                      \
+    do {                                                                                                 \
+        if (b == 0 && tid == 0 && it < 32) ws.trace[256 + it * 8 + (k)] = (uint32_t)wall_clock64();     \
+    } while (0)
+#define FIT_MARK0(k)                                                                                     \
+    do {                                                                                                 \
+        if (b == 0 && tid == 0) ws.trace[900 + (k)] = (uint32_t)wall_clock64();                          \
+    } while (0)
+#else
+#define FIT_MARK(k) \
+    do {            \
+    } while (0)
+#define FIT_MARK0(k) \
+    do {             \
+    } while (0)
+#endif
+struct FitShared {
+    unsigned hist[kFitBins];
+    uint32_t cand[kCandCap];
+    unsigned off[kFitMaxBlocks + 1];
+    double red[5][kFitWaves];
+    unsigned tmp[kFitWaves];
+    uint2 tmp2[kFitWaves];
+    float s, t;
+    long long kk;
+    int ok;
+    unsigned bin, below;
+    unsigned total_below, total_cand;
+};
+
+// Finds, in a 2048-bin histogram, the bin holding the rank-th element (1-based); sets sh.bin and sh.below (the
+// count in the bins before it). The histogram is read through `load`.
+template <class Load>
+__device__ inline void find_bin(FitShared& sh, unsigned rank, Load load) {
+    constexpr int per = kFitBins / kFitThreads;  // 4 consecutive bins per thread
+    unsigned cnt[per];
+    unsigned local = 0;
+#pragma unroll
+    for (int e = 0; e < per; ++e) {
+        cnt[e] = load(threadIdx.x * per + e);
+        local += cnt[e];
+    }
+    if (threadIdx.x == 0) {
+        sh.bin = 0;
+        sh.below = 0;
+    }
+    unsigned total;
+    const unsigned excl = block_excl_scan(local, sh.tmp, total);
+    if (excl < rank && rank <= excl + local) {
+        unsigned cum = excl;
+#pragma unroll
+        for (int e = 0; e < per; ++e) {
+            if (cum + cnt[e] >= rank) {
+                sh.bin = (unsigned)(threadIdx.x * per + e);
+                sh.below = cum;
+                break;
+            }
+            cum += cnt[e];
+        }
+    }
+    __syncthreads();
+}
+
+// Region r of flat candidate index f: the largest r with off[r] <= f (empty regions are skipped over).
+__device__ inline int region_of(const unsigned* off, int nb, unsigned f) {
+    int lo = 0, hi = nb - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (off[mid] <= f) lo = mid;
+        else hi = mid - 1;
+    }
+    return lo;
 }
 
 __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
-    __shared__ double red[5][4];
-    __shared__ unsigned lh[kFitBins];
-    __shared__ unsigned tmp[4];
-    __shared__ float s_sh, t_sh;
-    __shared__ int64_t kk_sh;
-    __shared__ int ok_sh;
-    __shared__ unsigned bin_sh, below_sh;
+    __shared__ FitShared sh;
+    const int nb = (int)gridDim.x, b = (int)blockIdx.x, tid = (int)threadIdx.x;
+    const FitWs& ws = a.ws;
+    const int64_t cap_words = (int64_t)nb * kFitPerBlock;
 
-    const unsigned nb = gridDim.x;
-    const int64_t T = (int64_t)nb * kFitThreads;
-    const int64_t gt = (int64_t)blockIdx.x * kFitThreads + threadIdx.x;
+    if (b == 0 && tid == 0) ws.trace[2 * kFitTraceRounds + 1] = (uint32_t)wall_clock64();  // launch start
+    // clear this launch's global histograms; the first barrier orders this before any use
+    {
+        const int64_t words = (int64_t)(a.iters > 0 ? a.iters : 1) * 3 * kFitBins;
+        for (int64_t q = (int64_t)b * kFitThreads + tid; q < words; q += (int64_t)nb * kFitThreads) ws.hist[q] = 0u;
+    }
 
+    // ---- elements into registers: every load of the thread is issued before any is used
     float zr[kFitEPT], tr[kFitEPT];
     uint32_t mbits = 0, vbits = 0;
+    {
+        const uint32_t i0 = (uint32_t)b * kFitPerBlock + tid;  // N <= 2^21
 #pragma unroll
-    for (int j = 0; j < kFitEPT; ++j) {
-        const int64_t i = gt + j * T;
-        zr[j] = 0.0f;
-        tr[j] = 0.0f;
-        if (i < a.N) {
-            bool m;
-            load_element(a, i, zr[j], tr[j], m);
-            vbits |= 1u << j;
-            mbits |= (m ? 1u : 0u) << j;
+        for (int j = 0; j < kFitEPT; ++j)
+            if ((int64_t)i0 + j * kFitThreads < a.N) vbits |= 1u << j;
+        if (a.mode == 0) {
+            uint8_t mk[kFitEPT];
+            const int64_t o0 = (int64_t)a.b * a.N + i0;
+#pragma unroll
+            for (int j = 0; j < kFitEPT; ++j) {
+                const bool v = (vbits >> j) & 1u;
+                const int64_t o = o0 + j * kFitThreads;
+                zr[j] = v ? a.z[o] : 0.0f;
+                tr[j] = v ? a.tg[o] : 0.0f;
+                mk[j] = v ? a.mask[o] : (uint8_t)0;
+            }
+#pragma unroll
+            for (int j = 0; j < kFitEPT; ++j) mbits |= (mk[j] != 0 ? 1u : 0u) << j;
+        } else {
+            // v3.py:373-378: z = exp(logz); nearest LiDAR sample (F.interpolate's index rule); mask = valid & c >= 0.999
+            const uint32_t W = (uint32_t)a.W;
+            const float scy = (float)a.dh / (float)a.H, scx = (float)a.dw / (float)a.W;
+            float lc[kFitEPT];
+#pragma unroll
+            for (int j = 0; j < kFitEPT; ++j) {
+                const bool v = (vbits >> j) & 1u;
+                const uint32_t ij = i0 + (uint32_t)(j * kFitThreads);
+                const uint32_t row = ij / W, col = ij - row * W;  // branch-free 32-bit division
+                int sy = (int)__builtin_floorf((float)row * scy);
+                int sx = (int)__builtin_floorf((float)col * scx);
+                sy = sy < a.dh - 1 ? sy : a.dh - 1;
+                sx = sx < a.dw - 1 ? sx : a.dw - 1;
+                const int64_t p = ((int64_t)a.b * a.dh + sy) * a.dw + sx;
+                const int64_t i = (int64_t)i0 + j * kFitThreads;
+                zr[j] = v ? a.logz[((int64_t)a.b * a.N + i) * a.stride] : 0.0f;
+                tr[j] = v ? a.lidar[p] : 0.0f;
+                lc[j] = v ? a.conf[p] : 0.0f;
+            }
+#pragma unroll
+            for (int j = 0; j < kFitEPT; ++j) {
+                const float d = tr[j];
+                const float c = fmin_(fmax_(lc[j] / 2.0f, 0.0f), 1.0f);
+                zr[j] = ((vbits >> j) & 1u) ? exp_f32(zr[j]) : 0.0f;
+                const bool m = ((vbits >> j) & 1u) && __builtin_isfinite(d) && d > 0.0f && c >= 0.999f;
+                mbits |= (m ? 1u : 0u) << j;
+            }
         }
     }
-    uint32_t wbits = mbits;
-    unsigned bar = 0;
-    float s = 1.0f, t = 0.0f;
-    uint32_t thr = 0;
 
-    for (int it = 0; it <= a.iters; ++it) {
-        // ---- weighted sums, fp64, fixed order
+    int stage = 0;  // publish buffers alternate between consecutive publishes
+    // Publishes this block's fp64 sums (and, for a bracket stage, counts) into buffer `stage & 1`.
+    auto publish = [&](double (&v)[5], unsigned below, unsigned ncand) {
+        block_sum5(v, sh.red);
+        if (tid == 0) {
+            uint64_t* p = ws.partials + ((size_t)(stage & 1) * kFitMaxBlocks + b) * 5;
+#pragma unroll
+            for (int k = 0; k < 5; ++k) p[k] = __builtin_bit_cast(uint64_t, v[k]);
+            unsigned* c = ws.counts + ((size_t)(stage & 1) * kFitMaxBlocks + b) * 2;
+            c[0] = below;
+            c[1] = ncand;
+        }
+    };
+    // Sum of all blocks' published partials of buffer `stage & 1`, in block order, in every thread.
+    auto gather_partials = [&](double (&g)[5]) {
+#pragma unroll
+        for (int k = 0; k < 5; ++k) g[k] = 0.0;
+        if (tid < nb) {
+            const uint64_t* p = ws.partials + ((size_t)(stage & 1) * kFitMaxBlocks + tid) * 5;
+#pragma unroll
+            for (int k = 0; k < 5; ++k)
+                g[k] = __builtin_bit_cast(double, __hip_atomic_load(&p[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        }
+        block_sum5(g, sh.red);
+    };
+    double pp[5];  // this thread's share of the published partials (threads < nb), loaded right after a barrier
+    auto load_partials = [&]() {
+#pragma unroll
+        for (int k = 0; k < 5; ++k) pp[k] = 0.0;
+        if (tid < nb) {
+            const uint64_t* p = ws.partials + ((size_t)(stage & 1) * kFitMaxBlocks + tid) * 5;
+#pragma unroll
+            for (int k = 0; k < 5; ++k)
+                pp[k] = __builtin_bit_cast(double, __hip_atomic_load(&p[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        }
+    };
+    float s = 1.0f, t = 0.0f;
+    // Closed-form weighted LS on the global sums (prompt_stem.py:222-232); thread 0 decides, all threads read.
+    auto solve = [&](const double (&g)[5], bool first) {
+        if (tid == 0) {
+            const double n = g[0], sx = g[1], sy = g[2], sxx = g[3], sxy = g[4];
+            if (first) {
+                const int64_t count = (int64_t)n;
+                sh.ok = count >= a.min_points;
+                int64_t k = (int64_t)(a.keep * (float)count);
+                if (k < a.min_points) k = a.min_points;
+                sh.kk = k < a.N ? k : a.N;
+                if (a.info && b == 0) {
+                    a.info[5 * a.b + 0] = (int32_t)count;
+                    a.info[5 * a.b + 1] = (int32_t)k;
+                    a.info[5 * a.b + 2] = sh.ok;
+                }
+            }
+            const double nn = n > 1.0 ? n : 1.0;
+            const double den = nn * sxx - sx * sx;
+            const double sn = den > 1e-12 ? (nn * sxy - sx * sy) / (den > 1e-12 ? den : 1e-12) : 1.0;
+            const double tn = (sy - sn * sx) / nn;
+            float ns = s, nt = t;
+            if (sh.ok) {
+                ns = (float)sn;
+                nt = (float)tn;
+            }
+            sh.s = ns;
+            sh.t = nt;
+        }
+        __syncthreads();
+        s = sh.s;
+        t = sh.t;
+        __syncthreads();
+    };
+
+    // ---- round 0 weights: the mask
+    {
         double v[5] = {0.0, 0.0, 0.0, 0.0, 0.0};
 #pragma unroll
         for (int j = 0; j < kFitEPT; ++j) {
-            if ((wbits >> j) & 1u) {
+            if ((mbits >> j) & 1u) {
                 const double zd = zr[j], td = tr[j];
                 v[0] += 1.0;
                 v[1] += zd;
@@ -155,149 +383,374 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
                 v[4] += zd * td;
             }
         }
-        block_sum5(v, red);
-        if (threadIdx.x == 0) {
-#pragma unroll
-            for (int k = 0; k < 5; ++k)
-                __hip_atomic_store(&a.partials[blockIdx.x * 5 + k], __builtin_bit_cast(uint64_t, v[k]),
-                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        grid_barrier(a.counter, bar++, nb, a.err);
-        double g[5] = {0.0, 0.0, 0.0, 0.0, 0.0};
-        for (unsigned q = threadIdx.x; q < nb; q += kFitThreads) {
-#pragma unroll
-            for (int k = 0; k < 5; ++k)
-                g[k] += __builtin_bit_cast(double, __hip_atomic_load(&a.partials[q * 5 + k], __ATOMIC_RELAXED,
-                                                                     __HIP_MEMORY_SCOPE_AGENT));
-        }
-        block_sum5(g, red);
-        if (threadIdx.x == 0) {
-            const double n = g[0], sx = g[1], sy = g[2], sxx = g[3], sxy = g[4];
-            if (it == 0) {
-                const int64_t count = (int64_t)n;
-                ok_sh = count >= a.min_points;
-                int64_t k = (int64_t)(a.keep * (float)count);
-                if (k < a.min_points) k = a.min_points;
-                kk_sh = k < a.N ? k : a.N;
-                if (a.info && blockIdx.x == 0) {
-                    a.info[5 * a.b + 0] = (int32_t)count;
-                    a.info[5 * a.b + 1] = (int32_t)k;
-                    a.info[5 * a.b + 2] = ok_sh;
-                }
-            }
-            const double nn = n > 1.0 ? n : 1.0;
-            const double den = nn * sxx - sx * sx;
-            const double sn = den > 1e-12 ? (nn * sxy - sx * sy) / (den > 1e-12 ? den : 1e-12) : 1.0;
-            const double tn = (sy - sn * sx) / nn;
-            if (ok_sh) {
-                s = (float)sn;
-                t = (float)tn;
-            }
-            s_sh = s;
-            t_sh = t;
-        }
-        __syncthreads();
-        s = s_sh;
-        t = t_sh;
-        if (it == a.iters) break;
+        FIT_MARK0(0);
+        publish(v, 0u, 0u);
+        FIT_MARK0(1);
+        fit_barrier(ws.bar, nb, ws.err);
+        FIT_MARK0(2);
+        double g[5];
+        gather_partials(g);
+        ++stage;
+        solve(g, true);
+    }
 
-        // ---- relative residuals as ordered bit patterns (+inf off the mask)
+    if (b == 0 && tid == 0) ws.trace[2 * kFitTraceRounds] = (uint32_t)wall_clock64();  // initial solve done
+    uint32_t thr = 0, thr_prev = 0;
+    bool have_bracket = false, have_prev = false;
+    uint32_t lo = 0, hi = 0;
+
+    for (int it = 0; it < a.iters; ++it) {
+        // The element values and mask bits are loop-invariant; hiding that from the compiler keeps it from hoisting
+        // their fp64 products and per-element lane masks out of the loop into hundreds of extra registers.
+#pragma unroll
+        for (int j = 0; j < kFitEPT; ++j) asm volatile("" : "+v"(zr[j]), "+v"(tr[j]));
+        asm volatile("" : "+v"(mbits), "+v"(vbits));
+        // ---- relative residuals as ordered bit patterns (+inf off the mask, kInvalid on padding)
         uint32_t rb[kFitEPT];
 #pragma unroll
         for (int j = 0; j < kFitEPT; ++j) {
-            float r = u2f(0x7f800000u);
-            if ((mbits >> j) & 1u) {
-                float e = s * zr[j];
-                e = e + t;
-                e = e - tr[j];
-                r = __builtin_fabsf(e) / fmax_(tr[j], 1e-3f);
-            }
-            rb[j] = f2u(r);
+            float e = s * zr[j];
+            e = e + t;
+            e = e - tr[j];
+            const float r = __builtin_fabsf(e) / fmax_(tr[j], 1e-3f);
+            const uint32_t rm = ((mbits >> j) & 1u) ? f2u(r) : 0x7f800000u;
+            rb[j] = ((vbits >> j) & 1u) ? rm : kInvalid;
         }
+        const unsigned kk = (unsigned)sh.kk;
 
-        // ---- exact k-th smallest: radix select, digits 11/11/10 bits from the top
-        uint32_t prefix = 0, pmask = 0;
-        unsigned rank = (unsigned)kk_sh;
+        // Publishes below-count, below-sums and the candidates in [blo, bhi]; then a barrier; then the totals.
+        auto stage_bracket = [&](uint32_t blo, uint32_t bhi) {
+            FIT_MARK(0);
+            asm volatile("" : "+v"(mbits), "+v"(vbits));  // no per-element lane masks kept across phases
+            // branch-free: below-count, masked below-sums (fp64; z*z and z*t are exact in fp64), candidate count
+            double v[5] = {0.0, 0.0, 0.0, 0.0, 0.0};
+            unsigned below = 0, nc = 0, nm = 0;
 #pragma unroll
-        for (int pass = 0; pass < 3; ++pass) {
-            const int sh = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
-            const int nbins = pass == 2 ? 1024 : 2048;
-            for (int q = threadIdx.x; q < nbins; q += kFitThreads) lh[q] = 0;
-            __syncthreads();
+            for (int j = 0; j < kFitEPT; ++j) {
+                const uint32_t k = rb[j];
+                const bool isb = k < blo;
+                const bool inc = isb && ((mbits >> j) & 1u);
+                below += isb ? 1u : 0u;
+                nm += inc ? 1u : 0u;
+                nc += (!isb && k <= bhi) ? 1u : 0u;
+                const double zd = inc ? (double)zr[j] : 0.0;
+                const double td = inc ? (double)tr[j] : 0.0;
+                v[1] += zd;
+                v[2] += td;
+                v[3] += zd * zd;
+                v[4] += zd * td;
+            }
+            v[0] = (double)nm;
+            // one scan for both counts: below in the high half, candidates in the low half (each <= 8192 per block)
+            unsigned packed_total;
+            const unsigned packed = block_excl_scan((below << 16) | nc, sh.tmp, packed_total);
+            unsigned slot = packed & 0xffffu;
+            const unsigned ncb = packed_total & 0xffffu;
+            const size_t base = (size_t)(stage & 1) * cap_words + (size_t)b * kFitPerBlock;
 #pragma unroll
-            for (int j = 0; j < kFitEPT; ++j)
-                if (((vbits >> j) & 1u) && (rb[j] & pmask) == prefix)
-                    atomicAdd(&lh[(rb[j] >> sh) & (unsigned)(nbins - 1)], 1u);
+            for (int j = 0; j < kFitEPT; ++j) {
+                const uint32_t k = rb[j];
+                if (k >= blo && k <= bhi) {
+                    ws.c_key[base + slot] = k | (((mbits >> j) & 1u) << 31);
+                    ws.c_z[base + slot] = zr[j];
+                    ws.c_t[base + slot] = tr[j];
+                    ++slot;
+                }
+            }
+            publish(v, packed_total >> 16, ncb);
+            FIT_MARK(1);
+            fit_barrier(ws.bar, nb, ws.err);
+            FIT_MARK(2);
+            load_partials();
+            // totals and region offsets, in block order
+            unsigned cb = 0, cc = 0;
+            if (tid < nb) {
+                const unsigned* c = ws.counts + ((size_t)(stage & 1) * kFitMaxBlocks + tid) * 2;
+                cb = __hip_atomic_load(&c[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                cc = __hip_atomic_load(&c[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            unsigned tb, tc;
+            const unsigned offc = block_excl_scan2(cc, cb, sh.tmp2, tc, tb);
+            if (tid < nb) sh.off[tid] = offc;
+            if (tid == 0) {
+                sh.off[nb] = tc;
+                sh.total_below = tb;
+                sh.total_cand = tc;
+            }
             __syncthreads();
-            unsigned* gh = a.hist + ((int64_t)it * 3 + pass) * kFitBins;
-            for (int q = threadIdx.x; q < nbins; q += kFitThreads)
-                if (lh[q]) atomicAdd(&gh[q], lh[q]);
-            grid_barrier(a.counter, bar++, nb, a.err);
-            const int per = nbins / kFitThreads;  // 8 or 4 consecutive bins per thread
-            unsigned cnt[8];
-            unsigned local = 0;
-            for (int e = 0; e < per; ++e) {
-                cnt[e] = __hip_atomic_load(&gh[threadIdx.x * per + e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                local += cnt[e];
+            FIT_MARK(3);
+        };
+
+        // Exact k-th among the published candidates (all in [blo, bhi]) and the new (s, t); buffer `stage & 1`.
+        auto select_and_solve = [&](uint32_t blo, uint32_t bhi) {
+            const unsigned total = sh.total_cand;
+            unsigned rank = kk - sh.total_below;
+            const size_t bufo = (size_t)(stage & 1) * cap_words;
+            auto cand_index = [&](unsigned f) {
+                const int r = region_of(sh.off, nb, f);
+                return bufo + (size_t)r * kFitPerBlock + (f - sh.off[r]);
+            };
+            // candidates into LDS, flat in block-region order; the first 4 per thread also keep z and target in
+            // registers for the sums (loaded together with the keys, so usually no second round trip)
+            uint32_t hw[4];
+            float hz[4], ht[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const unsigned f = tid + u * kFitThreads;
+                hw[u] = 0;
+                hz[u] = 0.0f;
+                ht[u] = 0.0f;
+                if (f < total) {
+                    const size_t o = cand_index(f);
+                    hw[u] = ws.c_key[o];
+                    hz[u] = ws.c_z[o];
+                    ht[u] = ws.c_t[o];
+                }
             }
-            if (threadIdx.x == 0) {
-                bin_sh = 0;
-                below_sh = 0;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const unsigned f = tid + u * kFitThreads;
+                if (f < total) sh.cand[f] = hw[u];
             }
-            unsigned total;
-            const unsigned excl = block_excl_scan(local, tmp, total);
-            if (excl < rank && rank <= excl + local) {
-                unsigned cum = excl;
-                for (int e = 0; e < per; ++e) {
-                    if (cum + cnt[e] >= rank) {
-                        bin_sh = (unsigned)(threadIdx.x * per + e);
-                        below_sh = cum;
-                        break;
-                    }
-                    cum += cnt[e];
+            for (unsigned f0 = tid + 4 * kFitThreads; f0 < total; f0 += 8 * kFitThreads) {
+                uint32_t w[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const unsigned f = f0 + u * kFitThreads;
+                    w[u] = f < total ? ws.c_key[cand_index(f)] : 0u;
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const unsigned f = f0 + u * kFitThreads;
+                    if (f < total) sh.cand[f] = w[u];
                 }
             }
             __syncthreads();
-            prefix |= bin_sh << sh;
-            pmask |= (unsigned)(nbins - 1) << sh;
-            rank -= below_sh;
-            __syncthreads();
-        }
-        thr = prefix;
-        wbits = 0;
+            FIT_MARK(4);
+            uint32_t prefix = 0, pmask = 0;
+            int top = 0;
+            if (total <= (unsigned)kFitThreads) {
+                // few candidates: each thread ranks its own against all of them (LDS broadcast reads)
+                if (tid == 0) sh.bin = 0;
+                __syncthreads();
+                if ((unsigned)tid < total) {
+                    const uint32_t key = sh.cand[tid] & 0x7fffffffu;
+                    unsigned less = 0, eq = 0;
+                    for (unsigned g = 0; g < total; ++g) {
+                        const uint32_t kg = sh.cand[g] & 0x7fffffffu;
+                        less += kg < key ? 1u : 0u;
+                        eq += kg == key ? 1u : 0u;
+                    }
+                    if (less < rank && rank <= less + eq) sh.bin = key - blo;  // equal keys write equal values
+                }
+                __syncthreads();
+                prefix = sh.bin;
+            } else {
+                // MSD radix select over key - blo in [0, bhi - blo], 11 bits per pass
+                const uint32_t range = bhi - blo;
+                top = range ? 32 - __builtin_clz(range) : 0;
+            }
+            while (top > 0) {
+                const int width = top < 11 ? top : 11;
+                const int shb = top - width;
+                const uint32_t dmask = (1u << width) - 1u;
+                for (int q = tid; q < kFitBins; q += kFitThreads) sh.hist[q] = 0;
+                __syncthreads();
+                for (unsigned f = tid; f < total; f += kFitThreads) {
+                    const uint32_t key = (sh.cand[f] & 0x7fffffffu) - blo;
+                    if ((key & pmask) == prefix) atomicAdd(&sh.hist[(key >> shb) & dmask], 1u);
+                }
+                __syncthreads();
+                find_bin(sh, rank, [&](int q) { return sh.hist[q]; });
+                prefix |= sh.bin << shb;
+                pmask |= dmask << shb;
+                rank -= sh.below;
+                top = shb;
+            }
+            thr = blo + prefix;
+            FIT_MARK(5);
+            // sums: this thread's share of the published below-partials, then its candidates at or under thr in
+            // flat order; then one fixed-order block reduction
+            double v[5] = {pp[0], pp[1], pp[2], pp[3], pp[4]};
 #pragma unroll
-        for (int j = 0; j < kFitEPT; ++j)
-            if (((mbits >> j) & 1u) && rb[j] <= thr) wbits |= 1u << j;
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t w = hw[u];
+                if ((w >> 31) && (w & 0x7fffffffu) <= thr) {
+                    const double zd = hz[u], td = ht[u];
+                    v[0] += 1.0;
+                    v[1] += zd;
+                    v[2] += td;
+                    v[3] += zd * zd;
+                    v[4] += zd * td;
+                }
+            }
+            for (unsigned f0 = tid + 4 * kFitThreads; f0 < total; f0 += 8 * kFitThreads) {
+                // 8 candidates per trip: all loads issued before any is used
+                float cz[8], ct[8];
+                bool use[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const unsigned f = f0 + u * kFitThreads;
+                    const uint32_t w = f < total ? sh.cand[f] : 0u;
+                    use[u] = (w >> 31) && (w & 0x7fffffffu) <= thr;
+                    cz[u] = 0.0f;
+                    ct[u] = 0.0f;
+                    if (use[u]) {
+                        const size_t o = cand_index(f);
+                        cz[u] = ws.c_z[o];
+                        ct[u] = ws.c_t[o];
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    if (use[u]) {
+                        const double zd = cz[u], td = ct[u];
+                        v[0] += 1.0;
+                        v[1] += zd;
+                        v[2] += td;
+                        v[3] += zd * zd;
+                        v[4] += zd * td;
+                    }
+                }
+            }
+            block_sum5(v, sh.red);
+            ++stage;
+            solve(v, false);
+            FIT_MARK(6);
+        };
+
+        // One call site per phase keeps the unrolled element loops from being duplicated.
+        int path = have_bracket ? 0 : 2;  // 0 bracket, 1 bracket missed then radix, 2 radix, 3 radix + third pass
+        bool use_bracket = have_bracket;
+        uint32_t blo = lo, bhi = hi, prefix = 0;
+        unsigned rank = kk;
+#pragma nounroll
+        for (;;) {
+            if (!use_bracket) {
+                // ---- global radix passes over bits 31..21 and 20..10
+                uint32_t pmask = 0;
+                prefix = 0;
+                rank = kk;
+#pragma nounroll
+                for (int pass = 0; pass < 2; ++pass) {
+                    const int shb = pass == 0 ? 21 : 10;
+                    asm volatile("" : "+v"(mbits), "+v"(vbits));
+                    for (int q = tid; q < kFitBins; q += kFitThreads) sh.hist[q] = 0;
+                    __syncthreads();
+#pragma unroll
+                    for (int j = 0; j < kFitEPT; ++j)
+                        if (((vbits >> j) & 1u) && (rb[j] & pmask) == prefix)
+                            atomicAdd(&sh.hist[(rb[j] >> shb) & (kFitBins - 1)], 1u);
+                    __syncthreads();
+                    unsigned* gh = ws.hist + ((int64_t)it * 3 + pass) * kFitBins;
+                    for (int q = tid; q < kFitBins; q += kFitThreads)
+                        if (sh.hist[q]) atomicAdd(&gh[q], sh.hist[q]);
+                    fit_barrier(ws.bar, nb, ws.err);
+                    find_bin(sh, rank, [&](int q) {
+                        return __hip_atomic_load(&gh[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    });
+                    prefix |= sh.bin << shb;
+                    pmask |= (uint32_t)(kFitBins - 1) << shb;
+                    rank -= sh.below;
+                }
+                blo = prefix;
+                bhi = prefix | 1023u;
+            }
+            stage_bracket(blo, bhi);
+            const unsigned tbl = sh.total_below, tcd = sh.total_cand;
+            if (tbl < kk && kk <= tbl + tcd && tcd <= (unsigned)kCandCap) {
+                select_and_solve(blo, bhi);
+                break;
+            }
+            ++stage;
+            if (use_bracket) {  // the k-th left the bracket: narrow it with the radix passes
+                use_bracket = false;
+                path = 1;
+                continue;
+            }
+            // ---- one 1024-value bin holds more candidates than fit in LDS: a third global pass (bits 9..0) gives
+            // the threshold, and the sums take one more barrier
+            path = 3;
+            asm volatile("" : "+v"(mbits), "+v"(vbits));
+            for (int q = tid; q < kFitBins; q += kFitThreads) sh.hist[q] = 0;
+            __syncthreads();
+#pragma unroll
+            for (int j = 0; j < kFitEPT; ++j)
+                if (((vbits >> j) & 1u) && (rb[j] & ~1023u) == prefix) atomicAdd(&sh.hist[rb[j] & 1023u], 1u);
+            __syncthreads();
+            unsigned* gh = ws.hist + ((int64_t)it * 3 + 2) * kFitBins;
+            for (int q = tid; q < 1024; q += kFitThreads)
+                if (sh.hist[q]) atomicAdd(&gh[q], sh.hist[q]);
+            fit_barrier(ws.bar, nb, ws.err);
+            find_bin(sh, rank, [&](int q) {
+                return __hip_atomic_load(&gh[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            });
+            thr = prefix | sh.bin;
+            double v[5] = {0.0, 0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+            for (int j = 0; j < kFitEPT; ++j) {
+                if (((mbits >> j) & 1u) && rb[j] <= thr) {
+                    const double zd = zr[j], td = tr[j];
+                    v[0] += 1.0;
+                    v[1] += zd;
+                    v[2] += td;
+                    v[3] += zd * zd;
+                    v[4] += zd * td;
+                }
+            }
+            publish(v, 0u, 0u);
+            fit_barrier(ws.bar, nb, ws.err);
+            double g[5];
+            gather_partials(g);
+            ++stage;
+            solve(g, false);
+            break;
+        }
+
+        if (b == 0 && tid == 0 && it < kFitTraceRounds) {
+            ws.trace[2 * it] = (uint32_t)path | (sh.total_cand << 4);
+            ws.trace[768 + it] = thr;
+            ws.trace[2 * it + 1] = (uint32_t)wall_clock64();
+        }
+        // ---- next round's bracket: around thr, as wide as twice the last move (in ulps) plus a margin
+        uint64_t D = have_prev ? 2ull * (thr > thr_prev ? thr - thr_prev : thr_prev - thr) + 1024u : (1ull << 18);
+        if (D > (1ull << 18)) D = 1ull << 18;
+        lo = (uint64_t)thr > D ? thr - (uint32_t)D : 0u;
+        hi = (uint64_t)thr + D > 0x7fffffffull ? 0x7fffffffu : thr + (uint32_t)D;
+        have_bracket = true;
+        thr_prev = thr;
+        have_prev = true;
     }
 
-    if (blockIdx.x == 0 && threadIdx.x == 0) {
+    if (b == 0 && tid == 0) {
         a.st[2 * a.b] = s;
         a.st[2 * a.b + 1] = t;
         if (a.info) {
             a.info[5 * a.b + 3] = (int32_t)thr;
-            a.info[5 * a.b + 4] = __hip_atomic_load(a.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            a.info[5 * a.b + 4] = __hip_atomic_load(ws.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 }
 
-static int fit_blocks(int64_t N) {
-    const int64_t per_block = (int64_t)kFitThreads * kFitEPT;
-    int64_t nb = (N + per_block - 1) / per_block;
-    if (nb < 256) nb = 256;
-    return (int)nb;
-}
+static int fit_blocks(int64_t N) { return (int)((N + kFitPerBlock - 1) / kFitPerBlock); }
+
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 size_t fit_workspace_bytes(int64_t N, int iters) {
-    const int nb = fit_blocks(N);
-    return 256 + (size_t)nb * 5 * sizeof(uint64_t) + (size_t)(iters > 0 ? iters : 1) * 3 * kFitBins * sizeof(unsigned);
+    const size_t nb = (size_t)fit_blocks(N > 0 ? N : 1);
+    const size_t hist = (size_t)(iters > 0 ? iters : 1) * 3 * kFitBins * sizeof(unsigned);
+    const size_t cand = 2 * nb * kFitPerBlock * sizeof(uint32_t);
+    return kFitHeader + align256(2 * kFitMaxBlocks * 5 * sizeof(uint64_t)) + align256(2 * kFitMaxBlocks * 2 * sizeof(unsigned)) +
+           align256(hist) + 3 * align256(cand);
 }
 
 int launch_fit(const FitLaunch& f, hipStream_t s) {
-    PMG_REQUIRE(f.N > 0 && f.N <= (int64_t)1 << 22, "N must be in [1, 2^22]");
+    PMG_REQUIRE(f.N > 0 && f.N <= (int64_t)kFitMaxBlocks * kFitPerBlock, "N must be in [1, 2^21]");
     PMG_REQUIRE(f.iters >= 0 && f.iters <= 64, "iters must be in [0, 64]");
     PMG_REQUIRE(f.min_points >= 1, "min_points must be >= 1");
     PMG_REQUIRE(f.trim >= 0.0f && f.trim < 1.0f, "trim must be in [0, 1)");
     PMG_REQUIRE(f.workspace && f.workspace_bytes >= fit_workspace_bytes(f.N, f.iters), "workspace too small");
+    PMG_REQUIRE(aligned16(f.workspace), "workspace must be 16-byte aligned");
     const int nb = fit_blocks(f.N);
     static int max_resident = -1;
     if (max_resident < 0) {
@@ -305,21 +758,28 @@ int launch_fit(const FitLaunch& f, hipStream_t s) {
         PMG_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fit_k, kFitThreads, 0));
         max_resident = per_cu * num_cus();
     }
-    PMG_REQUIRE(nb <= max_resident, "fit grid of " + std::to_string(nb) + " blocks cannot be resident (max " +
-                                        std::to_string(max_resident) + ")");
-    uint8_t* ws = (uint8_t*)f.workspace;
-    unsigned* counter = (unsigned*)ws;
-    int* err = (int*)(ws + 4);
-    uint64_t* partials = (uint64_t*)(ws + 256);
-    unsigned* hist = (unsigned*)(partials + (size_t)nb * 5);
-    const int64_t hist_words = (int64_t)(f.iters > 0 ? f.iters : 1) * 3 * kFitBins;
-    fill_u32(err, 0u, 1, s);
+    PMG_REQUIRE(nb <= max_resident && nb <= kFitMaxBlocks,
+                "fit grid of " + std::to_string(nb) + " blocks cannot be resident (max " +
+                    std::to_string(max_resident) + ")");
+    uint8_t* p = (uint8_t*)f.workspace;
+    FitWs ws;
+    ws.bar = (unsigned*)p;
+    ws.err = (int*)(p + 64);
+    ws.trace = (uint32_t*)(p + 128);
+    p += kFitHeader;
+    ws.partials = (uint64_t*)p;
+    p += align256(2 * kFitMaxBlocks * 5 * sizeof(uint64_t));
+    ws.counts = (unsigned*)p;
+    p += align256(2 * kFitMaxBlocks * 2 * sizeof(unsigned));
+    ws.hist = (unsigned*)p;
+    p += align256((size_t)(f.iters > 0 ? f.iters : 1) * 3 * kFitBins * sizeof(unsigned));
+    const size_t cand = align256(2 * (size_t)nb * kFitPerBlock * sizeof(uint32_t));
+    ws.c_key = (uint32_t*)p;
+    ws.c_z = (float*)(p + cand);
+    ws.c_t = (float*)(p + 2 * cand);
     for (int b = 0; b < f.B; ++b) {
-        fill_u32(counter, 0u, 1, s);
-        fill_u32(hist, 0u, hist_words, s);
         FitArgs a{f.mode, f.z, f.tg, f.mask, f.logz, f.stride, f.lidar, f.conf, f.H, f.W, f.dh, f.dw,
-                  f.N, f.iters, (float)(1.0 - (double)f.trim), f.min_points, b, f.st, f.info,
-                  partials, hist, counter, err};
+                  f.N, f.iters, (float)(1.0 - (double)f.trim), f.min_points, b, f.st, f.info, ws};
         hipLaunchKernelGGL(fit_k, dim3(nb), dim3(kFitThreads), 0, s, a);
         if (int e = check_launch("fit_k")) return e;
     }

@@ -47,11 +47,11 @@ PMG_HD float fmax_(float a, float b) { return a > b ? a : b; }
 #define PMG_SQRT2 PMG_F(0x3fb504f3)
 
 PMG_HD float exp_f32(float x) {
-    if (x != x) return x;
-    if (x > 88.8f) return u2f(0x7f800000u);
-    if (x < -87.0f) return 0.0f;
-    const float kf = rne(x * PMG_LOG2E);
-    float r = x - kf * PMG_LN2_HI;
+    // Branch-free: the polynomial runs on x clamped into the domain (identical to x inside it), and selects
+    // produce the special values, so a wave never diverges here.
+    const float xc = fmin_(fmax_(x, -87.0f), 88.8f);
+    const float kf = rne(xc * PMG_LOG2E);
+    float r = xc - kf * PMG_LN2_HI;
     r = r - kf * PMG_LN2_LO;
     float p = PMG_I5040;
     p = p * r + PMG_I720;
@@ -61,19 +61,19 @@ PMG_HD float exp_f32(float x) {
     p = p * r + 0.5f;
     p = p * r + 1.0f;
     p = p * r + 1.0f;
-    const int k = (int)kf;  // in [-126, 128] on the accepted domain
-    if (k > 127) return (p * u2f(254u << 23)) * 2.0f;
-    return p * u2f((uint32_t)(k + 127) << 23);
+    const int k = (int)kf;  // in [-126, 128]
+    const float big = (p * u2f(254u << 23)) * 2.0f;
+    const float val = k > 127 ? big : p * u2f((uint32_t)(k + 127 > 0 ? k + 127 : 0) << 23);
+    const float out = x > 88.8f ? u2f(0x7f800000u) : (x < -87.0f ? 0.0f : val);
+    return x != x ? x : out;
 }
 
 PMG_HD float log_f32(float x) {
     const uint32_t u = f2u(x);
-    int e = (int)(u >> 23) - 127;
-    float m = u2f((u & 0x007fffffu) | 0x3f800000u);
-    if (m > PMG_SQRT2) {
-        m = m * 0.5f;
-        e = e + 1;
-    }
+    const float m0 = u2f((u & 0x007fffffu) | 0x3f800000u);
+    const bool hi = m0 > PMG_SQRT2;
+    const float m = hi ? m0 * 0.5f : m0;
+    const int e = (int)(u >> 23) - 127 + (hi ? 1 : 0);
     const float f = m - 1.0f;
     const float s = f / (2.0f + f);
     const float z = s * s;

@@ -233,6 +233,20 @@ def ln_silu_f16(x: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, eps: f
 
 
 # ------------------------------------------------------------------------------------------------------------- (4)
+_FIT_WS: dict = {}
+
+
+def _fit_workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    """The metric fit's workspace: zero-filled once, then reused by every call on the same (device, stream), since the
+    fit kernel leaves it ready for the next launch. Calls on one stream are ordered, so they never share it at once."""
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    ws = _FIT_WS.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros((nbytes,), dtype=torch.uint8, device=device)
+        _FIT_WS[key] = ws
+    return ws
+
+
 def fit_scale_shift(z: torch.Tensor, target: torch.Tensor, mask: torch.Tensor, iters: int = 4, trim: float = 0.2,
                     min_points: int = 32, return_info: bool = False):
     """fit_scale_shift (prompt_stem.py:211-240) on the GPU. z, target: [B, N] fp32; mask: [B, N] bool/uint8.
@@ -242,9 +256,9 @@ def fit_scale_shift(z: torch.Tensor, target: torch.Tensor, mask: torch.Tensor, i
     m8 = _dev(mask.reshape(mask.shape[0], -1).to(torch.uint8).contiguous(), "mask")
     B, N = z.shape
     st = torch.empty((B, 2), dtype=torch.float32, device=z.device)
-    info = torch.zeros((B, 5), dtype=torch.int32, device=z.device)
+    info = torch.empty((B, 5), dtype=torch.int32, device=z.device)
     ws_bytes = lib().pmg_fit_workspace_bytes(N, iters)
-    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=z.device)
+    ws = _fit_workspace(ws_bytes, z.device)
     call("pmg_fit_scale_shift", _p(z), _p(target), _p(m8), B, N, int(iters), float(trim), int(min_points), _p(st),
          _p(info), _p(ws), ws_bytes, _stream())
     if return_info:
@@ -261,9 +275,9 @@ def fit_prompt(points: torch.Tensor, lidar: torch.Tensor, conf: torch.Tensor, it
     B, H, W, _ = points.shape
     dh, dw = lidar.shape[-2:]
     st = torch.empty((B, 2), dtype=torch.float32, device=points.device)
-    info = torch.zeros((B, 5), dtype=torch.int32, device=points.device)
+    info = torch.empty((B, 5), dtype=torch.int32, device=points.device)
     ws_bytes = lib().pmg_fit_workspace_bytes(H * W, iters)
-    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=points.device)
+    ws = _fit_workspace(ws_bytes, points.device)
     call("pmg_fit_prompt", points.data_ptr() + 8, 3, _p(lidar), _p(conf), B, H, W, dh, dw, int(iters), float(trim),
          int(min_points), _p(st), _p(info), _p(ws), ws_bytes, _stream())
     if return_info:

@@ -132,16 +132,17 @@ class RefinerStep:
         ptr = lib().pmg_refiner_buffer(self._h, ids[which])
         out = torch.empty(shape, dtype=dt, device=self.st_prompt.device)
         nbytes = out.numel() * out.element_size()
-        torch.cuda.current_stream().synchronize()
-        _copy_device(out.data_ptr(), ptr, nbytes)
+        _copy_device(out.data_ptr(), ptr, nbytes, torch.cuda.current_stream().cuda_stream)
         return out
 
 
-def _copy_device(dst: int, src: int, nbytes: int) -> None:
-    """Synchronous device-to-device copy of a raw buffer (the HIP runtime torch already loaded)."""
+def _copy_device(dst: int, src: int, nbytes: int, stream: int) -> None:
+    """Device-to-device copy of a raw buffer, ordered on `stream` (the stream torch uses next), through the HIP
+    runtime torch already loaded. A plain hipMemcpy would not do: device-to-device it may return before the copy
+    is done, and it runs on the null stream, which torch's streams do not wait for."""
     hip = C.CDLL("libamdhip64.so")
-    hip.hipMemcpy.restype = C.c_int
-    hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
-    rc = hip.hipMemcpy(C.c_void_p(dst), C.c_void_p(src), C.c_size_t(nbytes), 3)  # hipMemcpyDeviceToDevice
+    hip.hipMemcpyAsync.restype = C.c_int
+    hip.hipMemcpyAsync.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]
+    rc = hip.hipMemcpyAsync(C.c_void_p(dst), C.c_void_p(src), C.c_size_t(nbytes), 3, C.c_void_p(stream))
     if rc != 0:
-        raise RuntimeError(f"hipMemcpy failed with {rc}")
+        raise RuntimeError(f"hipMemcpyAsync failed with {rc}")

@@ -229,6 +229,40 @@ def test_fit_generic(gpu, iters):
     for b in range(B):
         _close_st(s[b], tt[b], so[b], to[b])
         assert info[b, 0] == info_o[b]["count"] and info[b, 1] == info_o[b]["k"] and info[b, 4] == 0
+        if iters > 0 and s[b] == so[b] and tt[b] == to[b]:  # same (s, t) every round: the same exact k-th
+            assert info[b, 3] == np.float32(info_o[b]["thr"]).view(np.int32)
+
+
+@pytest.mark.parametrize("case", ["ties_all", "ties_some", "large"])
+def test_fit_selection_paths(gpu, case):
+    """Exercises the three ways the kernel finds the k-th residual: the bracket around the previous round's
+    threshold, the two global radix passes, and the third pass when one 1024-value bin holds more than the 32768
+    candidates a block keeps in LDS (exact-linear data: most residuals are exactly 0)."""
+    announce(f"fit selection path {case}")
+    rng = np.random.default_rng(len(case))
+    N = 300_000 if case == "large" else 120_000
+    if case == "ties_all":
+        z = rng.integers(1, 9, size=(1, N)).astype(np.float32)
+        t = (2 * z).astype(np.float32)
+        t = np.where(rng.random((1, N)) < 0.05, t * 3, t).astype(np.float32)
+    elif case == "ties_some":
+        z = rng.uniform(0.5, 6, size=(1, N)).astype(np.float32)
+        t = np.round(1.3 * z + 0.05 + rng.normal(0, 0.01, size=(1, N)), 2).astype(np.float32)
+    else:
+        z = rng.uniform(0.5, 6, size=(1, N)).astype(np.float32)
+        t = (0.7 * z + 0.3 + rng.normal(0, 0.02, size=(1, N))).astype(np.float32)
+        t = np.where(rng.random((1, N)) < 0.1, t * rng.uniform(0.3, 3, size=(1, N)), t).astype(np.float32)
+    m = rng.random((1, N)) < 0.7
+    so, to, info_o = ofit.fit_f64(z, t, m, iters=10, return_info=True)
+    s, tt, info = ops.fit_scale_shift(_t(z, gpu), _t(t, gpu), _t(m, gpu), iters=10, return_info=True)
+    s, tt, info = s.cpu().numpy(), tt.cpu().numpy(), info.cpu().numpy()
+    _close_st(s[0], tt[0], so[0], to[0])
+    assert info[0, 4] == 0
+    if s[0] == so[0] and tt[0] == to[0]:
+        assert info[0, 3] == np.float32(info_o[0]["thr"]).view(np.int32)
+    # a second call reuses the workspace left by the first
+    s2, t2 = ops.fit_scale_shift(_t(z, gpu), _t(t, gpu), _t(m, gpu), iters=10)
+    assert s2.item() == s[0] and t2.item() == tt[0]
 
 
 def test_fit_edge_cases(gpu):
