@@ -13,15 +13,19 @@
 // itself, so all blocks hold bit-identical (s, t) and take identical branches.
 //
 // The threshold is the exact k-th smallest residual; non-negative fp32 values order like their bit patterns. A trim
-// round costs ONE barrier when the threshold stays inside a bracket [lo, hi] predicted from the previous round
-// (+-(2 |last move| + 1024) ulps, at most +-2^18): each block publishes how many of its residuals fall below lo,
-// its fp64 sums over those (they are in the new weight set whatever the exact threshold), and its residuals inside
-// the bracket ("candidates", with z and target). After the barrier every block loads all candidates into LDS,
-// selects the exact k-th among them (each thread ranks one candidate when there are at most 256, else an LDS radix
-// select), and adds the candidates at or below it to the sums -- the next (s, t) without a second barrier. When
-// the k-th falls outside the bracket (always in round 0), two global radix passes over the top 22 bits (LDS
-// histogram per block, merged by atomics) narrow the bracket to one 1024-value bin; if even that bin holds more
-// than kCandCap candidates, a third pass finds the threshold and the sums take one more barrier.
+// round costs ONE barrier when the threshold stays inside a bracket [lo, hi] predicted from the previous rounds
+// (+-(2 |last move| + 1024) ulps, capped so that about 2048 candidates are expected at the density seen last time):
+// each block publishes how many of its residuals fall below lo, its fp64 sums over those (they are in the new weight
+// set whatever the exact threshold), and its residuals inside the bracket ("candidates", with z and target). After
+// the barrier every block loads all candidates into LDS, selects the exact k-th among them (each thread ranks one
+// candidate when there are at most 256, else an LDS radix select), and adds the candidates at or below it to the
+// sums -- the next (s, t) without a second barrier. Rounds 0 and 1 (no measured move yet), and any round whose k-th
+// leaves its bracket, first run two global radix passes over the top 22 bits (LDS histogram per block, merged by
+// atomics) that narrow the bracket to one 1024-value bin; if even that bin holds more than kCandCap candidates, a
+// third pass finds the threshold and the sums take one more barrier.
+//
+// Fixed point: once a round reproduces the previous round's (s, t) bit for bit, every later round would repeat
+// it exactly, so the loop stops there with the bit-identical result (on the synthetic scenes after 3 rounds).
 // This replaces the reference device engine's approximate two-level histogram (MetricFit.metal:141-189).
 //
 // Workspace: zero-filled once before its first use; the kernel leaves it reusable (the barrier returns to zero,
@@ -185,8 +189,10 @@ struct FitShared {
     float s, t;
     long long kk;
     int ok;
+    int same;  // the last solve reproduced the previous (s, t) bit for bit
     unsigned bin, below;
     unsigned total_below, total_cand;
+    uint32_t blo_last, bhi_last;  // bracket of the last stage
 };
 
 // Finds, in a 2048-bin histogram, the bin holding the rank-th element (1-based); sets sh.bin and sh.below (the
@@ -222,17 +228,6 @@ __device__ inline void find_bin(FitShared& sh, unsigned rank, Load load) {
     __syncthreads();
 }
 
-// Region r of flat candidate index f: the largest r with off[r] <= f (empty regions are skipped over).
-__device__ inline int region_of(const unsigned* off, int nb, unsigned f) {
-    int lo = 0, hi = nb - 1;
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (off[mid] <= f) lo = mid;
-        else hi = mid - 1;
-    }
-    return lo;
-}
-
 __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
     __shared__ FitShared sh;
     const int nb = (int)gridDim.x, b = (int)blockIdx.x, tid = (int)threadIdx.x;
@@ -254,19 +249,22 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
 #pragma unroll
         for (int j = 0; j < kFitEPT; ++j)
             if ((int64_t)i0 + j * kFitThreads < a.N) vbits |= 1u << j;
+        // Loads are unconditional (padding slots read the last element) so that none sits under a branch: a
+        // branch would make the compiler wait for each element's load before the next one is issued.
+        const int64_t last = a.N - 1;
         if (a.mode == 0) {
             uint8_t mk[kFitEPT];
-            const int64_t o0 = (int64_t)a.b * a.N + i0;
+            const int64_t o0 = (int64_t)a.b * a.N;
 #pragma unroll
             for (int j = 0; j < kFitEPT; ++j) {
-                const bool v = (vbits >> j) & 1u;
-                const int64_t o = o0 + j * kFitThreads;
-                zr[j] = v ? a.z[o] : 0.0f;
-                tr[j] = v ? a.tg[o] : 0.0f;
-                mk[j] = v ? a.mask[o] : (uint8_t)0;
+                int64_t i = (int64_t)i0 + j * kFitThreads;
+                i = i < last ? i : last;
+                zr[j] = a.z[o0 + i];
+                tr[j] = a.tg[o0 + i];
+                mk[j] = a.mask[o0 + i];
             }
 #pragma unroll
-            for (int j = 0; j < kFitEPT; ++j) mbits |= (mk[j] != 0 ? 1u : 0u) << j;
+            for (int j = 0; j < kFitEPT; ++j) mbits |= ((vbits >> j) & (mk[j] != 0 ? 1u : 0u)) << j;
         } else {
             // v3.py:373-378: z = exp(logz); nearest LiDAR sample (F.interpolate's index rule); mask = valid & c >= 0.999
             const uint32_t W = (uint32_t)a.W;
@@ -274,27 +272,32 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
             float lc[kFitEPT];
 #pragma unroll
             for (int j = 0; j < kFitEPT; ++j) {
-                const bool v = (vbits >> j) & 1u;
-                const uint32_t ij = i0 + (uint32_t)(j * kFitThreads);
+                int64_t i = (int64_t)i0 + j * kFitThreads;
+                i = i < last ? i : last;
+                const uint32_t ij = (uint32_t)i;
                 const uint32_t row = ij / W, col = ij - row * W;  // branch-free 32-bit division
                 int sy = (int)__builtin_floorf((float)row * scy);
                 int sx = (int)__builtin_floorf((float)col * scx);
                 sy = sy < a.dh - 1 ? sy : a.dh - 1;
                 sx = sx < a.dw - 1 ? sx : a.dw - 1;
                 const int64_t p = ((int64_t)a.b * a.dh + sy) * a.dw + sx;
-                const int64_t i = (int64_t)i0 + j * kFitThreads;
-                zr[j] = v ? a.logz[((int64_t)a.b * a.N + i) * a.stride] : 0.0f;
-                tr[j] = v ? a.lidar[p] : 0.0f;
-                lc[j] = v ? a.conf[p] : 0.0f;
+                zr[j] = a.logz[((int64_t)a.b * a.N + i) * a.stride];
+                tr[j] = a.lidar[p];
+                lc[j] = a.conf[p];
             }
 #pragma unroll
             for (int j = 0; j < kFitEPT; ++j) {
                 const float d = tr[j];
                 const float c = fmin_(fmax_(lc[j] / 2.0f, 0.0f), 1.0f);
-                zr[j] = ((vbits >> j) & 1u) ? exp_f32(zr[j]) : 0.0f;
+                zr[j] = exp_f32(zr[j]);
                 const bool m = ((vbits >> j) & 1u) && __builtin_isfinite(d) && d > 0.0f && c >= 0.999f;
                 mbits |= (m ? 1u : 0u) << j;
             }
+        }
+#pragma unroll
+        for (int j = 0; j < kFitEPT; ++j) {  // padding slots hold zeros
+            zr[j] = ((vbits >> j) & 1u) ? zr[j] : 0.0f;
+            tr[j] = ((vbits >> j) & 1u) ? tr[j] : 0.0f;
         }
     }
 
@@ -360,6 +363,7 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
                 ns = (float)sn;
                 nt = (float)tn;
             }
+            sh.same = f2u(ns) == f2u(s) && f2u(nt) == f2u(t);
             sh.s = ns;
             sh.t = nt;
         }
@@ -396,10 +400,11 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
 
     if (b == 0 && tid == 0) ws.trace[2 * kFitTraceRounds] = (uint32_t)wall_clock64();  // initial solve done
     uint32_t thr = 0, thr_prev = 0;
-    bool have_bracket = false, have_prev = false;
+    bool have_bracket = false, have_prev = false, have_prev2 = false;
     uint32_t lo = 0, hi = 0;
 
-    for (int it = 0; it < a.iters; ++it) {
+    // A fit that falls back to (1, 0) never changes (s, t): its trim rounds cannot affect the result.
+    for (int it = 0; it < (sh.ok ? a.iters : 0); ++it) {
         // The element values and mask bits are loop-invariant; hiding that from the compiler keeps it from hoisting
         // their fp64 products and per-element lane masks out of the loop into hundreds of extra registers.
 #pragma unroll
@@ -476,6 +481,8 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
                 sh.off[nb] = tc;
                 sh.total_below = tb;
                 sh.total_cand = tc;
+                sh.blo_last = blo;
+                sh.bhi_last = bhi;
             }
             __syncthreads();
             FIT_MARK(3);
@@ -486,43 +493,47 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
             const unsigned total = sh.total_cand;
             unsigned rank = kk - sh.total_below;
             const size_t bufo = (size_t)(stage & 1) * cap_words;
-            auto cand_index = [&](unsigned f) {
-                const int r = region_of(sh.off, nb, f);
-                return bufo + (size_t)r * kFitPerBlock + (f - sh.off[r]);
-            };
-            // candidates into LDS, flat in block-region order; the first 4 per thread also keep z and target in
-            // registers for the sums (loaded together with the keys, so usually no second round trip)
-            uint32_t hw[4];
-            float hz[4], ht[4];
+            // Thread (r, j) = (tid % nb, tid / nb) owns slots j, j + per, j + 2 per, ... of block r's region: no
+            // search from a flat index to a region, and its loads are independent. Keys go to LDS in flat order
+            // (region r at off[r]); the first kHold of the thread's candidates also keep z and target in registers
+            // for the sums (loaded with the keys: usually no second round trip).
+            constexpr int kHold = 12;
+            const int per = kFitThreads / nb;  // threads per region (nb <= kFitThreads)
+            const int rr = tid % nb, jj = tid / nb;
+            const bool act = jj < per;
+            const unsigned cr = act ? sh.off[rr + 1] - sh.off[rr] : 0u;
+            const unsigned obase = act ? sh.off[rr] : 0u;
+            const size_t rbase = bufo + (size_t)rr * kFitPerBlock;
+            uint32_t hw[kHold];
+            float hz[kHold], ht[kHold];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const unsigned f = tid + u * kFitThreads;
+            for (int u = 0; u < kHold; ++u) {
+                const unsigned slot = (unsigned)(jj + u * per);
                 hw[u] = 0;
                 hz[u] = 0.0f;
                 ht[u] = 0.0f;
-                if (f < total) {
-                    const size_t o = cand_index(f);
-                    hw[u] = ws.c_key[o];
-                    hz[u] = ws.c_z[o];
-                    ht[u] = ws.c_t[o];
+                if (slot < cr) {
+                    hw[u] = ws.c_key[rbase + slot];
+                    hz[u] = ws.c_z[rbase + slot];
+                    ht[u] = ws.c_t[rbase + slot];
                 }
             }
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const unsigned f = tid + u * kFitThreads;
-                if (f < total) sh.cand[f] = hw[u];
+            for (int u = 0; u < kHold; ++u) {
+                const unsigned slot = (unsigned)(jj + u * per);
+                if (slot < cr) sh.cand[obase + slot] = hw[u];
             }
-            for (unsigned f0 = tid + 4 * kFitThreads; f0 < total; f0 += 8 * kFitThreads) {
-                uint32_t w[8];
+            for (unsigned s0 = (unsigned)(jj + kHold * per); s0 < cr; s0 += (unsigned)(kHold * per)) {
+                uint32_t w[kHold];
 #pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const unsigned f = f0 + u * kFitThreads;
-                    w[u] = f < total ? ws.c_key[cand_index(f)] : 0u;
+                for (int u = 0; u < kHold; ++u) {
+                    const unsigned slot = s0 + (unsigned)(u * per);
+                    w[u] = slot < cr ? ws.c_key[rbase + slot] : 0u;
                 }
 #pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const unsigned f = f0 + u * kFitThreads;
-                    if (f < total) sh.cand[f] = w[u];
+                for (int u = 0; u < kHold; ++u) {
+                    const unsigned slot = s0 + (unsigned)(u * per);
+                    if (slot < cr) sh.cand[obase + slot] = w[u];
                 }
             }
             __syncthreads();
@@ -573,7 +584,7 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
             // flat order; then one fixed-order block reduction
             double v[5] = {pp[0], pp[1], pp[2], pp[3], pp[4]};
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
+            for (int u = 0; u < kHold; ++u) {
                 const uint32_t w = hw[u];
                 if ((w >> 31) && (w & 0x7fffffffu) <= thr) {
                     const double zd = hz[u], td = ht[u];
@@ -584,25 +595,20 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
                     v[4] += zd * td;
                 }
             }
-            for (unsigned f0 = tid + 4 * kFitThreads; f0 < total; f0 += 8 * kFitThreads) {
-                // 8 candidates per trip: all loads issued before any is used
-                float cz[8], ct[8];
-                bool use[8];
+            for (unsigned s0 = (unsigned)(jj + kHold * per); s0 < cr; s0 += (unsigned)(kHold * per)) {
+                // kHold candidates per trip: all loads issued before any is used
+                float cz[kHold], ct[kHold];
+                bool use[kHold];
 #pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const unsigned f = f0 + u * kFitThreads;
-                    const uint32_t w = f < total ? sh.cand[f] : 0u;
+                for (int u = 0; u < kHold; ++u) {
+                    const unsigned slot = s0 + (unsigned)(u * per);
+                    const uint32_t w = slot < cr ? sh.cand[obase + slot] : 0u;
                     use[u] = (w >> 31) && (w & 0x7fffffffu) <= thr;
-                    cz[u] = 0.0f;
-                    ct[u] = 0.0f;
-                    if (use[u]) {
-                        const size_t o = cand_index(f);
-                        cz[u] = ws.c_z[o];
-                        ct[u] = ws.c_t[o];
-                    }
+                    cz[u] = use[u] ? ws.c_z[rbase + slot] : 0.0f;
+                    ct[u] = use[u] ? ws.c_t[rbase + slot] : 0.0f;
                 }
 #pragma unroll
-                for (int u = 0; u < 8; ++u) {
+                for (int u = 0; u < kHold; ++u) {
                     if (use[u]) {
                         const double zd = cz[u], td = ct[u];
                         v[0] += 1.0;
@@ -620,8 +626,8 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
         };
 
         // One call site per phase keeps the unrolled element loops from being duplicated.
-        int path = have_bracket ? 0 : 2;  // 0 bracket, 1 bracket missed then radix, 2 radix, 3 radix + third pass
-        bool use_bracket = have_bracket;
+        int path = have_bracket && have_prev2 ? 0 : 2;  // 0 bracket, 1 bracket missed then radix, 2 radix, 3 radix + third pass
+        bool use_bracket = have_bracket && have_prev2;
         uint32_t blo = lo, bhi = hi, prefix = 0;
         unsigned rank = kk;
 #pragma nounroll
@@ -713,13 +719,25 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
             ws.trace[2 * it + 1] = (uint32_t)wall_clock64();
         }
         // ---- next round's bracket: around thr, as wide as twice the last move (in ulps) plus a margin
+        // ... but no wider than what holds about 2048 candidates at the density the last stage saw around its
+        // threshold (candidates per ulp of its bracket), and never wider than 2^18 ulps (3 %).
         uint64_t D = have_prev ? 2ull * (thr > thr_prev ? thr - thr_prev : thr_prev - thr) + 1024u : (1ull << 18);
-        if (D > (1ull << 18)) D = 1ull << 18;
+        {
+            const double dens = (double)sh.total_cand / (double)((uint64_t)sh.bhi_last - sh.blo_last + 1);
+            const double dmax = dens > 0.0 ? 1024.0 / dens : (double)(1u << 18);
+            uint64_t cap = dmax < 2048.0 ? 2048u : (dmax > (double)(1u << 18) ? (1ull << 18) : (uint64_t)dmax);
+            if (D > cap) D = cap;
+        }
         lo = (uint64_t)thr > D ? thr - (uint32_t)D : 0u;
         hi = (uint64_t)thr + D > 0x7fffffffull ? 0x7fffffffu : thr + (uint32_t)D;
         have_bracket = true;
         thr_prev = thr;
+        have_prev2 = have_prev;  // the first bracket waits for one measured move: round 1 usually jumps far
         have_prev = true;
+        // Fixed point: when a round reproduces the previous (s, t) bit for bit, the next round sees the same
+        // residuals, hence the same k-th value, weights and sums, so every remaining round -- and the final
+        // solve -- returns exactly these (s, t). Stopping here gives the bit-identical result.
+        if (sh.same) break;
     }
 
     if (b == 0 && tid == 0) {

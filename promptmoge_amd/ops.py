@@ -248,9 +248,12 @@ def _fit_workspace(nbytes: int, device: torch.device) -> torch.Tensor:
 
 
 def fit_scale_shift(z: torch.Tensor, target: torch.Tensor, mask: torch.Tensor, iters: int = 4, trim: float = 0.2,
-                    min_points: int = 32, return_info: bool = False):
-    """fit_scale_shift (prompt_stem.py:211-240) on the GPU. z, target: [B, N] fp32; mask: [B, N] bool/uint8.
-    Returns s, t: [B] (and info [B, 5] int32 = count, k, ok, threshold bits, error flag)."""
+                    min_points: int = 32, differentiable: bool = False, *, return_info: bool = False):
+    """fit_scale_shift (prompt_stem.py:211-240) on the GPU, same arguments: z, target, mask [B, ...] (flattened
+    from dim 1). Returns s, t: [B] fp32 (and, with return_info, info [B, 5] int32 = count, k, ok, threshold bits,
+    error flag). The result carries no gradient; `differentiable=True` under grad mode is refused."""
+    if differentiable and torch.is_grad_enabled() and z.requires_grad:
+        raise NotImplementedError("the GPU metric fit is inference-only (differentiable=True needs autograd)")
     z = _dev(z.float().reshape(z.shape[0], -1).contiguous(), "z")
     target = _dev(target.float().reshape(target.shape[0], -1).contiguous(), "target")
     m8 = _dev(mask.reshape(mask.shape[0], -1).to(torch.uint8).contiguous(), "mask")
