@@ -39,7 +39,9 @@ int pmg_version(void);
 
 /* ------------------------------------------------------------------------------------------------------------ *
  * Numerics test hooks: evaluate the shared bit-reproducible fp32 functions (exp, log, silu) on the host CPU or on
- * the GPU, so tests can show that both and the NumPy oracle produce identical bits. op: 0 exp, 1 log, 2 silu.
+ * the GPU, so tests can show that both and the NumPy oracle produce identical bits. op: 0 exp, 1 log, 2 silu;
+ * device only, op 3: in = n pairs (y, mult), out[i] = the int8 code clamp(rint(silu(y) * mult), +-127) as the
+ * epilogues compute it (hardware exp2/rcp with an exact re-evaluation near rounding ties).
  * ------------------------------------------------------------------------------------------------------------ */
 int pmg_math_host(int op, const float* in_host, float* out_host, int64_t n);
 int pmg_math_device(int op, const float* in, float* out, int64_t n, void* stream);

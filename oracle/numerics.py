@@ -75,9 +75,12 @@ def silu_f32(y) -> np.ndarray:
 
 def quant_f32(y, mult) -> np.ndarray:
     """clamp(rint(y * mult), -127, 127) with mult = 127/clip in fp32: the requantisation of the reference's deployed
-    int8 kernels (SparseConvInt8.metal:109, Refiner.metal:120, mult from Refiner.swift:148); round half to even."""
+    int8 kernels (SparseConvInt8.metal:109, Refiner.metal:120, mult from Refiner.swift:148); round half to even.
+    The clamp is max-then-min with "a > b ? a : b" / "a < b ? a : b", as pmg_math.h: a NaN input gives -127."""
     y = np.asarray(y, dtype=np.float32)
-    return np.clip(np.rint(y * np.float32(mult)), F32(-127.0), F32(127.0)).astype(np.float32)
+    q = np.rint(y * np.asarray(mult, dtype=np.float32))
+    q = np.where(q > F32(-127.0), q, F32(-127.0))
+    return np.where(q < F32(127.0), q, F32(127.0)).astype(np.float32)
 
 
 def quant_i8(y, mult) -> np.ndarray:

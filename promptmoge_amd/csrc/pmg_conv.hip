@@ -80,7 +80,7 @@ __device__ inline void epilogue(const ConvArgs& a, int64_t m, int n, typename Ac
             y = y * a.w_scale[n];
             if (a.bias) y = y + a.bias[n];
             if constexpr (EPI == PMG_EPI_Q) {
-                ((int8_t*)a.out)[o] = quant_i8(silu_f32(y), a.out_mult);
+                ((int8_t*)a.out)[o] = silu_quant_i8(y, a.out_mult);
             } else if constexpr (EPI == PMG_EPI_R) {
                 ((float*)a.out)[o] = y + a.skip[o];
             } else {

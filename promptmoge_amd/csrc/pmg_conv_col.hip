@@ -334,11 +334,7 @@ __global__ __launch_bounds__(kColThreads) void spconv_col_k(ColConvArgs a) {
                     for (int j = 0; j < NB; ++j) {
                         const int64_t o = mo * C + 16 * j + 4 * g;
                         if constexpr (sizeof(T) == 1) {
-                            uint32_t pk = 0;
-#pragma unroll
-                            for (int i = 0; i < 4; ++i)
-                                pk |= (uint32_t)(uint8_t)quant_i8(silu_f32(y[j][i]), a.out_mult) << (8 * i);
-                            *(uint32_t*)((int8_t*)a.out + o) = pk;
+                            store_silu_codes4(y[j], a.out_mult, (int8_t*)a.out + o);
                         } else {
                             typedef _Float16 h4 __attribute__((ext_vector_type(4)));
                             h4 hv;
@@ -359,13 +355,13 @@ __global__ __launch_bounds__(kColThreads) void spconv_col_k(ColConvArgs a) {
                     if (EPI != PMG_EPI_ROUT && ok) *(v4f*)((float*)a.out + o) = v4f{y[j][0], y[j][1], y[j][2], y[j][3]};
                 }
                 if constexpr (EPI == PMG_EPI_RLN) {
-                    ln_silu_quad<NB>(y, a.ln_gamma, a.ln_beta, a.ln_eps, g);
+                    ln_silu_quad<NB, sizeof(T) != 1>(y, a.ln_gamma, a.ln_beta, a.ln_eps, g);
                     if (ok) {
 #pragma unroll
                         for (int j = 0; j < NB; ++j) {
                             const int64_t o = mo * C + 16 * j + 4 * g;
                             if constexpr (sizeof(T) == 1)
-                                store_codes4(y[j], a.next_mult, (int8_t*)a.next_q + o);
+                                store_silu_codes4(y[j], a.next_mult, (int8_t*)a.next_q + o);
                             else
                                 store_half4(y[j], (_Float16*)a.next_q + o);
                         }

@@ -40,7 +40,7 @@ __global__ __launch_bounds__(256) void ln_silu_k(const float* __restrict__ x, in
         y[j][2] = v.z;
         y[j][3] = v.w;
     }
-    ln_silu_quad<NB>(y, gamma, beta, eps, g);
+    ln_silu_quad<NB, F16>(y, gamma, beta, eps, g);
     if (!ok) return;
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
@@ -48,7 +48,7 @@ __global__ __launch_bounds__(256) void ln_silu_k(const float* __restrict__ x, in
         if constexpr (F16)
             store_half4(y[j], (_Float16*)out + o);
         else
-            store_codes4(y[j], out_mult, (int8_t*)out + o);
+            store_silu_codes4(y[j], out_mult, (int8_t*)out + o);
     }
 }
 
@@ -138,7 +138,7 @@ __global__ __launch_bounds__(256) void input_stage_k(InputArgs a) {
         for (int j = 0; j < NB; ++j)
             *(float4*)(a.x_out + mo * C + 16 * j + 4 * g) = make_float4(y[j][0], y[j][1], y[j][2], y[j][3]);
     }
-    ln_silu_quad<NB>(y, a.gamma, a.beta, a.eps, g);
+    ln_silu_quad<NB, F16>(y, a.gamma, a.beta, a.eps, g);
     if (!ok) return;
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
@@ -146,7 +146,7 @@ __global__ __launch_bounds__(256) void input_stage_k(InputArgs a) {
         if constexpr (F16)
             store_half4(y[j], (_Float16*)a.q_out + o);
         else
-            store_codes4(y[j], a.out_mult, (int8_t*)a.q_out + o);
+            store_silu_codes4(y[j], a.out_mult, (int8_t*)a.q_out + o);
     }
 }
 
@@ -199,7 +199,11 @@ __device__ __host__ inline float math_op(int op, float x) {
 
 __global__ void math_k(int op, const float* in, float* out, int64_t n) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i < n) out[i] = math_op(op, in[i]);
+    if (i >= n) return;
+    if (op == 3)
+        out[i] = (float)silu_quant_i8(in[2 * i], in[2 * i + 1]);
+    else
+        out[i] = math_op(op, in[i]);
 }
 
 }  // namespace pmg
@@ -232,7 +236,7 @@ int pmg_math_host(int op, const float* in, float* out, int64_t n) {
 }
 
 int pmg_math_device(int op, const float* in, float* out, int64_t n, void* stream) {
-    PMG_REQUIRE(op >= 0 && op <= 2 && in && out && n >= 0, "bad argument");
+    PMG_REQUIRE(op >= 0 && op <= 3 && in && out && n >= 0, "bad argument");
     if (n == 0) return PMG_OK;
     hipLaunchKernelGGL(math_k, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, op, in, out,
                        n);

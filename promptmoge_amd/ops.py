@@ -39,9 +39,17 @@ def _dev(t: torch.Tensor, name: str, dtype: Optional[torch.dtype] = None) -> tor
 
 
 def math_device(op: int, x: torch.Tensor) -> torch.Tensor:
+    """Test hook: op 0/1/2 = exp/log/silu of x; op 3 = the epilogues' int8 SiLU code of x[:, 0] at mult x[:, 1]."""
     x = _dev(x, "x", torch.float32)
-    out = torch.empty_like(x)
-    call("pmg_math_device", op, _p(x), _p(out), x.numel(), _stream())
+    if op == 3:
+        if x.ndim != 2 or x.shape[1] != 2:
+            raise ValueError("op 3 takes (n, 2) pairs (y, mult)")
+        out = torch.empty((x.shape[0],), dtype=torch.float32, device=x.device)
+        n = x.shape[0]
+    else:
+        out = torch.empty_like(x)
+        n = x.numel()
+    call("pmg_math_device", op, _p(x), _p(out), n, _stream())
     return out
 
 

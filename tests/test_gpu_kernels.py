@@ -39,6 +39,55 @@ def test_math_bits(gpu, op):
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
 
 
+def _near_tie_inputs():
+    """(y, mult) pairs whose silu(y) * mult lies within a few ulps of every rounding tie k + 1/2 (k in -1..127):
+    float64 bisection for the exact preimage on each monotone branch of SiLU, then +-12 float32 ulps around it."""
+    ys, ms = [], []
+    for clip in (0.37, 1.0, 3.2, 11.0):
+        mult = np.float32(127.0) / np.float32(clip)
+        for k in range(-1, 128):
+            target = (k + 0.5) / float(mult)
+            branches = [(0.0, 200.0)] if target > 0 else [(-1.2784645, 0.0), (-60.0, -1.2784645)]
+            for lo, hi in branches:
+                f = lambda y: y / (1.0 + np.exp(-y)) - target
+                if f(lo) * f(hi) > 0:
+                    continue
+                a, b = lo, hi
+                for _ in range(200):
+                    mid = 0.5 * (a + b)
+                    if (f(a) <= 0) == (f(mid) <= 0):
+                        a = mid
+                    else:
+                        b = mid
+                y0 = np.float32(0.5 * (a + b))
+                bits = np.array([y0], np.float32).view(np.int32)[0]
+                for d in range(-12, 13):
+                    ys.append(np.array([bits + d], np.int32).view(np.float32)[0])
+                    ms.append(mult)
+    return np.array(ys, np.float32), np.array(ms, np.float32)
+
+
+def test_silu_quant_fast_path_is_bit_exact(gpu):
+    """The epilogues' SiLU requant (hardware exp2/rcp + exact re-evaluation near ties) equals the oracle's exact
+    quant_i8(silu_f32(y), mult) on adversarial near-tie inputs, special values and a dense random sweep."""
+    announce("silu quant fast path")
+    yt, mt = _near_tie_inputs()
+    rng = np.random.default_rng(7)
+    yr = rng.normal(0.0, 6.0, 2_000_000).astype(np.float32)
+    mr = (np.float32(127.0) / rng.uniform(0.2, 20.0, yr.size).astype(np.float32)).astype(np.float32)
+    sp = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 88.0, -88.0, 87.5, -87.5, 1e30, -1e30, 1e-40, -1e-40],
+                  np.float32)
+    y = np.concatenate([yt, yr, sp, sp])
+    m = np.concatenate([mt, mr, np.full(sp.size, 42.3, np.float32), np.full(sp.size, 1e6, np.float32)])
+    got = ops.math_device(3, _t(np.stack([y, m], 1), gpu)).cpu().numpy()
+    ref = onm.quant_i8(onm.silu_f32(y), m).astype(np.float32)
+    bad = np.nonzero(got != ref)[0]
+    assert bad.size == 0, (y[bad[:5]], m[bad[:5]], got[bad[:5]], ref[bad[:5]])
+    # the near-tie set really sits on ties: most of it takes the exact path
+    v = onm.silu_f32(yt).astype(np.float64) * mt
+    assert np.median(np.abs(np.abs(v - np.rint(v)) - 0.5)) < 1e-4
+
+
 # ---------------------------------------------------------------------------------------------------------- structure
 @pytest.mark.parametrize("name", ["B", "A"])
 def test_voxelize_and_column_map(gpu, name):

@@ -53,6 +53,8 @@ def test_quant_closed_form():
     y = np.array([1.25, 1.75, -1.25, 0.0, 1000.0, -1000.0, 63.25, 63.75], dtype=np.float32)
     # y * 2 = 2.5, 3.5, -2.5, 0, 2000, -2000, 126.5, 127.5 -> half to even, then saturate at +-127
     assert nm.quant_i8(y, mult).tolist() == [2, 4, -2, 0, 127, -127, 126, 127]
+    # NaN takes the kernels' clamp (max then min with strict compares): -127; infinities saturate
+    assert nm.quant_i8(np.array([np.nan, np.inf, -np.inf], np.float32), mult).tolist() == [-127, 127, -127]
 
 
 def test_ln_silu_against_float64():
