@@ -125,8 +125,8 @@ __device__ inline float quad_sum(float s) {
 }
 
 // LayerNorm (two-pass, quad order) + affine + SiLU of the lane's NB x 4 channels of one row, in place.
-template <int NB, bool SILU = true>
-__device__ inline void ln_silu_quad(float (&y)[NB][4], const float* gamma, const float* beta, float eps, int g) {
+template <int NB, bool SILU = true, class P = const float*>
+__device__ inline void ln_silu_quad(float (&y)[NB][4], P gamma, P beta, float eps, int g) {
     constexpr int C = 16 * NB;
     float s = 0.0f;
 #pragma unroll

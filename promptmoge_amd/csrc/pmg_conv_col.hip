@@ -80,6 +80,108 @@ struct ColGeom {
     static constexpr int PFZ = (3 * kWin + kColThreads - 1) / kColThreads;        // keys per thread
 };
 
+// Per-channel epilogue constants, read through a pointer type P (global, or LDS when a kernel stages them).
+template <class P>
+struct EpiConst {
+    P ws, bs, gamma, beta, ow;
+    bool has_bias;
+};
+__device__ inline EpiConst<const float*> epi_global(const ColConvArgs& a) {
+    return EpiConst<const float*>{a.w_scale, a.bias, a.ln_gamma, a.ln_beta, a.out_w, a.bias != nullptr};
+}
+
+// Epilogue of one 16-voxel tile: lane holds channels 16j + 4g + i (j < C/16, i < 4) of voxel m.
+template <typename T, int C, int EPI, class P = const float*>
+__device__ inline void col_epilogue(const ColConvArgs& a, const typename ColAcc<T>::type (&acc)[C / 16], int m,
+                                    int M, int g, const EpiConst<P>& k) {
+    constexpr int NB = C / 16;
+    const bool ok = m < M;
+    const int64_t mo = ok ? m : 0;
+    float y[NB][4];
+    if constexpr (EPI != PMG_EPI_ACC) {
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int n = 16 * j + 4 * g + i;
+                if constexpr (sizeof(T) == 1) {
+                    float t = (float)acc[j][i] * a.a_scale;
+                    t = t * k.ws[n];
+                    if (k.has_bias) t = t + k.bs[n];
+                    y[j][i] = t;
+                } else {
+                    float t = acc[j][i];
+                    if (k.has_bias) t = t + k.bs[n];
+                    y[j][i] = t;
+                }
+            }
+    }
+    if constexpr (EPI == PMG_EPI_ACC) {
+        if (ok) {
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                const int64_t o = mo * C + 16 * j + 4 * g;
+                if constexpr (sizeof(T) == 1)
+                    *(v4i*)((int32_t*)a.out + o) = acc[j];
+                else
+                    *(v4f*)((float*)a.out + o) = acc[j];
+            }
+        }
+    } else if constexpr (EPI == PMG_EPI_Q) {
+        if (ok) {
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                const int64_t o = mo * C + 16 * j + 4 * g;
+                if constexpr (sizeof(T) == 1) {
+                    store_silu_codes4(y[j], a.out_mult, (int8_t*)a.out + o);
+                } else {
+                    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+                    h4 hv;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) hv[i] = (_Float16)silu_f32(y[j][i]);
+                    *(h4*)((_Float16*)a.out + o) = hv;
+                }
+            }
+        }
+    } else {
+        // residual: x_new = y + skip
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const int64_t o = mo * C + 16 * j + 4 * g;
+            const v4f sk = *(const v4f*)(a.skip + o);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) y[j][i] = y[j][i] + sk[i];
+            if (EPI != PMG_EPI_ROUT && ok) *(v4f*)((float*)a.out + o) = v4f{y[j][0], y[j][1], y[j][2], y[j][3]};
+        }
+        if constexpr (EPI == PMG_EPI_RLN) {
+            ln_silu_quad<NB, sizeof(T) != 1>(y, k.gamma, k.beta, a.ln_eps, g);
+            if (ok) {
+#pragma unroll
+                for (int j = 0; j < NB; ++j) {
+                    const int64_t o = mo * C + 16 * j + 4 * g;
+                    if constexpr (sizeof(T) == 1)
+                        store_silu_codes4(y[j], a.next_mult, (int8_t*)a.next_q + o);
+                    else
+                        store_half4(y[j], (_Float16*)a.next_q + o);
+                }
+            }
+        } else if constexpr (EPI == PMG_EPI_ROUT) {
+            float p = 0.0f;
+#pragma unroll
+            for (int j = 0; j < NB; ++j)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) p = p + k.ow[16 * j + 4 * g + i] * y[j][i];
+            const float d = a.out_b[0] + quad_sum(p);
+            if (ok && g == 0) {
+                const float p0 = a.points[mo * 3 + 0], p1 = a.points[mo * 3 + 1], p2 = a.points[mo * 3 + 2];
+                a.points_out[mo * 3 + 0] = p0;
+                a.points_out[mo * 3 + 1] = p1;
+                a.points_out[mo * 3 + 2] = p2 + d;
+            }
+        }
+    }
+}
+
 template <typename T, int C, int EPI>
 __global__ __launch_bounds__(kColThreads) void spconv_col_k(ColConvArgs a) {
     typedef ColGeom<T, C> G;
@@ -292,96 +394,10 @@ __global__ __launch_bounds__(kColThreads) void spconv_col_k(ColConvArgs a) {
             }
         }
 
-        // ---- epilogue: lane holds channels 16j + 4g + i of voxel m
+        // ---- epilogue
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb) {
-            const int m = s0 + 32 * wv + 16 * rb + r;
-            const bool ok = m < M;
-            const int64_t mo = ok ? m : 0;
-            float y[NB][4];
-            if constexpr (EPI != PMG_EPI_ACC) {
-#pragma unroll
-                for (int j = 0; j < NB; ++j)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int n = 16 * j + 4 * g + i;
-                        if constexpr (sizeof(T) == 1) {
-                            float t = (float)acc[rb][j][i] * a.a_scale;
-                            t = t * a.w_scale[n];
-                            if (a.bias) t = t + a.bias[n];
-                            y[j][i] = t;
-                        } else {
-                            float t = acc[rb][j][i];
-                            if (a.bias) t = t + a.bias[n];
-                            y[j][i] = t;
-                        }
-                    }
-            }
-            if constexpr (EPI == PMG_EPI_ACC) {
-                if (ok) {
-#pragma unroll
-                    for (int j = 0; j < NB; ++j) {
-                        const int64_t o = mo * C + 16 * j + 4 * g;
-                        if constexpr (sizeof(T) == 1)
-                            *(v4i*)((int32_t*)a.out + o) = acc[rb][j];
-                        else
-                            *(v4f*)((float*)a.out + o) = acc[rb][j];
-                    }
-                }
-            } else if constexpr (EPI == PMG_EPI_Q) {
-                if (ok) {
-#pragma unroll
-                    for (int j = 0; j < NB; ++j) {
-                        const int64_t o = mo * C + 16 * j + 4 * g;
-                        if constexpr (sizeof(T) == 1) {
-                            store_silu_codes4(y[j], a.out_mult, (int8_t*)a.out + o);
-                        } else {
-                            typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-                            h4 hv;
-#pragma unroll
-                            for (int i = 0; i < 4; ++i) hv[i] = (_Float16)silu_f32(y[j][i]);
-                            *(h4*)((_Float16*)a.out + o) = hv;
-                        }
-                    }
-                }
-            } else {
-                // residual: x_new = y + skip
-#pragma unroll
-                for (int j = 0; j < NB; ++j) {
-                    const int64_t o = mo * C + 16 * j + 4 * g;
-                    const v4f sk = *(const v4f*)(a.skip + o);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) y[j][i] = y[j][i] + sk[i];
-                    if (EPI != PMG_EPI_ROUT && ok) *(v4f*)((float*)a.out + o) = v4f{y[j][0], y[j][1], y[j][2], y[j][3]};
-                }
-                if constexpr (EPI == PMG_EPI_RLN) {
-                    ln_silu_quad<NB, sizeof(T) != 1>(y, a.ln_gamma, a.ln_beta, a.ln_eps, g);
-                    if (ok) {
-#pragma unroll
-                        for (int j = 0; j < NB; ++j) {
-                            const int64_t o = mo * C + 16 * j + 4 * g;
-                            if constexpr (sizeof(T) == 1)
-                                store_silu_codes4(y[j], a.next_mult, (int8_t*)a.next_q + o);
-                            else
-                                store_half4(y[j], (_Float16*)a.next_q + o);
-                        }
-                    }
-                } else if constexpr (EPI == PMG_EPI_ROUT) {
-                    float p = 0.0f;
-#pragma unroll
-                    for (int j = 0; j < NB; ++j)
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) p = p + a.out_w[16 * j + 4 * g + i] * y[j][i];
-                    const float d = a.out_b[0] + quad_sum(p);
-                    if (ok && g == 0) {
-                        const float p0 = a.points[mo * 3 + 0], p1 = a.points[mo * 3 + 1], p2 = a.points[mo * 3 + 2];
-                        a.points_out[mo * 3 + 0] = p0;
-                        a.points_out[mo * 3 + 1] = p1;
-                        a.points_out[mo * 3 + 2] = p2 + d;
-                    }
-                }
-            }
-        }
+        for (int rb = 0; rb < 2; ++rb)
+            col_epilogue<T, C, EPI>(a, acc[rb], s0 + 32 * wv + 16 * rb + r, M, g, epi_global(a));
 
         // ---- hand the next window to the other buffer (or, single-buffered, reload this one)
         if constexpr (NBUF == 2) {
@@ -430,12 +446,243 @@ static int launch_col2(const ColConvArgs& a, int epi, hipStream_t s) {
     return fail(PMG_E_INVALID, "pmg_spconv_col: unknown epilogue");
 }
 
+// ---------------------------------------------------------------------------------------------------------------
+// int8, C <= 48: neighbour-pixel-major reduction over 64-row waves.
+//
+// A persistent 8-wave block (two waves per SIMD) owns segments of 512 voxels, 64 rows per wave in four 16-row tiles.
+// For each of the 9 pixel offsets (di, dj) a wave reads its rows' neighbour codes from the LDS window ONCE (one
+// ds_read_b128 per tile at a compile-time offset from one per-lane base address) and the neighbour keys. A row's
+// neighbour is at most one of the three taps (di, dj, dz), dz = key_nb - key_row, so the operand of tap dz is the
+// loaded chunk with the other rows (and the K-padding lanes) zeroed by v_cndmask; a dz that none of the wave's 64
+// rows has is skipped (wave-uniform branch). The weights of a tap are one 16-byte read per lane from LDS, laid out
+// in the MFMA operand order (block (v, j) = 16 x NCH consecutive 16-byte chunks), conflict-free, and each read feeds
+// the four tiles' MFMAs. The next offset's codes and keys are read before the current offset's MFMAs issue.
+// Per-channel epilogue constants are staged in LDS, so the epilogue issues no dependent global loads. The next
+// segment's window is loaded into registers during the compute and written to LDS at the end of the segment.
+constexpr int kColvThreads = 512;
+constexpr int kColvWaves = kColvThreads / 64;
+constexpr int kColvRows = 64;
+constexpr int kColvSeg = kColvRows * kColvWaves;  // 512 voxels
+constexpr int kColvWin = kColvSeg + 2;
+
+template <int C>
+struct ColvGeom {
+    static constexpr int ROWB = C;
+    static constexpr int NCH = C / 16;
+    static constexpr int NB = C / 16;
+    static constexpr int XBYTES = 3 * kColvWin * ROWB;
+    static constexpr int WBLK = 16 * NCH * 16;        // bytes of one (tap, 16-channel block) operand
+    static constexpr int WBYTES = 27 * NB * WBLK;
+    static constexpr int NCHUNK = 3 * kColvWin * NCH;
+    static constexpr int PF = (NCHUNK + kColvThreads - 1) / kColvThreads;
+    static constexpr int PFZ = (3 * kColvWin + kColvThreads - 1) / kColvThreads;
+};
+
+template <int C, int EPI>
+__global__ __launch_bounds__(kColvThreads, 1) void spconv_colv_k(ColConvArgs a) {
+    typedef ColvGeom<C> G;
+    constexpr int ROWB = G::ROWB, NCH = G::NCH, NB = G::NB;
+    static_assert(C == 16 || C == 32 || C == 48, "this kernel covers C <= 48");
+    static_assert(G::WBYTES < 65536, "weight offsets must fit the LDS immediate field");
+
+    __shared__ __attribute__((aligned(16))) uint8_t s_w[G::WBYTES];
+    __shared__ __attribute__((aligned(16))) uint8_t s_x[G::XBYTES];
+    __shared__ int s_z[3 * kColvWin];
+    __shared__ float s_k[5][C];  // w_scale, bias, ln gamma, ln beta, out_w
+
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int gc = g < NCH ? g : NCH - 1;  // chunk read by this lane; lanes g >= NCH are zeroed (K padding)
+    const bool kin = g < NCH;
+    const int M = (int)a.M;
+    const int H = a.H, W = a.W;
+    const int HW = H * W;
+    const uint8_t* __restrict__ xg = (const uint8_t*)a.x;
+    const uint8_t* __restrict__ wg = (const uint8_t*)a.w;
+
+    // weights: block (v, j), lane chunk (r, c) at ((v * NB + j) * 16 * NCH + c * 16 + r) * 16
+    for (int e = tid; e < 27 * NB * 16 * NCH; e += kColvThreads) {
+        const int rr = e % 16, c = (e / 16) % NCH, vj = e / (16 * NCH);
+        const int v = vj / NB, j = vj - (vj / NB) * NB;
+        ((v4i*)s_w)[e] = *(const v4i*)(wg + ((int64_t)(16 * j + rr) * 27 + v) * ROWB + 16 * c);
+    }
+    for (int e = tid; e < 5 * C; e += kColvThreads) {
+        const int q = e / C, n = e - (e / C) * C;
+        const float* src = q == 0 ? a.w_scale : q == 1 ? a.bias : q == 2 ? a.ln_gamma : q == 3 ? a.ln_beta : a.out_w;
+        s_k[q][n] = src ? src[n] : 0.0f;
+    }
+    typedef const __attribute__((address_space(3))) float* kptr;
+    const EpiConst<kptr> kc{(kptr)s_k[0], (kptr)s_k[1], (kptr)s_k[2], (kptr)s_k[3], (kptr)s_k[4], a.bias != nullptr};
+
+    v4i pf[G::PF];
+    int pfz[G::PFZ];
+    auto fetch = [&](int sg) {
+        const int s0 = sg * kColvSeg;
+#pragma unroll
+        for (int k = 0; k < G::PF; ++k) {
+            const int e = tid + k * kColvThreads;
+            pf[k] = v4i{0, 0, 0, 0};
+            if (e < G::NCHUNK) {
+                const int d = e / (kColvWin * NCH);
+                const int rem = e - d * (kColvWin * NCH);
+                const int q = rem / NCH, c = rem - (rem / NCH) * NCH;
+                const int p = s0 + (d - 1) * W - 1 + q;
+                if (p >= 0 && p < M) pf[k] = *(const v4i*)(xg + (int64_t)p * ROWB + c * 16);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < G::PFZ; ++k) {
+            const int e = tid + k * kColvThreads;
+            pfz[k] = kZFar;
+            if (e < 3 * kColvWin) {
+                const int d = e / kColvWin, q = e - (e / kColvWin) * kColvWin;
+                const int p = s0 + (d - 1) * W - 1 + q;
+                if (p >= 0 && p < M) pfz[k] = a.zq[p];
+            }
+        }
+    };
+    auto commit = [&]() {
+#pragma unroll
+        for (int k = 0; k < G::PF; ++k) {
+            const int e = tid + k * kColvThreads;
+            if (e < G::NCHUNK) ((v4i*)s_x)[e] = pf[k];
+        }
+#pragma unroll
+        for (int k = 0; k < G::PFZ; ++k) {
+            const int e = tid + k * kColvThreads;
+            if (e < 3 * kColvWin) s_z[e] = pfz[k];
+        }
+    };
+
+    typedef const __attribute__((address_space(3))) uint8_t lds_u8;
+    typedef const __attribute__((address_space(3))) v4i lds_v4i;
+    typedef const __attribute__((address_space(3))) int lds_int;
+    const int lr0 = kColvRows * wv + r;  // window-relative row of tile 0
+    const lds_u8* xb = (lds_u8*)s_x + lr0 * ROWB + gc * 16;
+    const lds_int* zb = (lds_int*)s_z + lr0;
+    const lds_u8* wb = (lds_u8*)s_w + (gc * 16 + r) * 16;
+
+    const int nseg = (M + kColvSeg - 1) / kColvSeg;
+    int seg = blockIdx.x;
+    if (seg < nseg) {
+        fetch(seg);
+        commit();
+    }
+    for (; seg < nseg; seg += gridDim.x) {
+        const int s0 = seg * kColvSeg;
+        const int nxt = seg + gridDim.x;
+        __syncthreads();  // window (and, the first time, weights and constants) visible to all waves
+        if (nxt < nseg) fetch(nxt);  // in flight during this segment's compute
+
+        int zc[4], pi[4], pj[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int m = s0 + kColvRows * wv + 16 * t + r;
+            const int pix = (m < M ? m : 0) % HW;
+            pi[t] = pix / W;
+            pj[t] = pix - pi[t] * W;
+            zc[t] = zb[kColvWin + 16 * t + 1];
+        }
+
+        v4i acc[4][NB];
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int j = 0; j < NB; ++j) acc[t][j] = v4i{0, 0, 0, 0};
+
+        struct Nb {
+            v4i x[4];
+            int z[4];
+        };
+        auto load_nb = [&](int o, Nb& n) {  // o = di * 3 + dj, compile-time after unrolling
+            const int di = o / 3, dj = o % 3;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                n.x[t] = *(lds_v4i*)(xb + (di * kColvWin + dj + 16 * t) * ROWB);
+                n.z[t] = zb[di * kColvWin + dj + 16 * t];
+            }
+        };
+        auto compute_nb = [&](int o, const Nb& n) {
+            const int di = o / 3, dj = o % 3;
+            int dz[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const bool in = (unsigned)(pi[t] + di - 1) < (unsigned)H && (unsigned)(pj[t] + dj - 1) < (unsigned)W;
+                dz[t] = in ? n.z[t] - zc[t] + 1 : 3;  // 0, 1, 2: tap dz - 1; anything else: no tap
+            }
+#pragma unroll
+            for (int d = 0; d < 3; ++d) {
+                const bool any = dz[0] == d || dz[1] == d || dz[2] == d || dz[3] == d;
+                if (__builtin_amdgcn_ballot_w64(any)) {
+                    const int v = o * 3 + d;
+                    v4i wop[NB];
+#pragma unroll
+                    for (int j = 0; j < NB; ++j) wop[j] = *(lds_v4i*)(wb + (v * NB + j) * G::WBLK);
+                    v4i xm[4];
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) xm[t] = (kin && dz[t] == d) ? n.x[t] : v4i{0, 0, 0, 0};
+#pragma unroll
+                    for (int j = 0; j < NB; ++j)
+#pragma unroll
+                        for (int t = 0; t < 4; ++t)
+                            acc[t][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wop[j], xm[t], acc[t][j], 0, 0, 0);
+                }
+            }
+        };
+        Nb A, B;
+        load_nb(0, A);
+#pragma unroll
+        for (int o = 0; o < 9; o += 2) {
+            if (o + 1 < 9) load_nb(o + 1, B);
+            __builtin_amdgcn_sched_barrier(0);
+            compute_nb(o, A);
+            __builtin_amdgcn_sched_barrier(0);
+            if (o + 1 < 9) {
+                if (o + 2 < 9) load_nb(o + 2, A);
+                __builtin_amdgcn_sched_barrier(0);
+                compute_nb(o + 1, B);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+            col_epilogue<int8_t, C, EPI, kptr>(a, acc[t], s0 + kColvRows * wv + 16 * t + r, M, g, kc);
+
+        if (nxt < nseg) {
+            __syncthreads();  // every wave is done reading this window
+            commit();
+        }
+    }
+}
+
+template <int C, int EPI>
+static int launch_colv(const ColConvArgs& a, hipStream_t s) {
+    const int64_t nseg = (a.M + kColvSeg - 1) / kColvSeg;
+    int64_t grid = num_cus();
+    if (grid > nseg) grid = nseg;
+    hipLaunchKernelGGL((spconv_colv_k<C, EPI>), dim3((unsigned)grid), dim3(kColvThreads), 0, s, a);
+    return check_launch("spconv_colv_k");
+}
+
+template <int C>
+static int launch_colv2(const ColConvArgs& a, int epi, hipStream_t s) {
+    switch (epi) {
+        case PMG_EPI_ACC: return launch_colv<C, PMG_EPI_ACC>(a, s);
+        case PMG_EPI_Q: return launch_colv<C, PMG_EPI_Q>(a, s);
+        case PMG_EPI_R: return launch_colv<C, PMG_EPI_R>(a, s);
+        case PMG_EPI_RLN: return launch_colv<C, PMG_EPI_RLN>(a, s);
+        case PMG_EPI_ROUT: return launch_colv<C, PMG_EPI_ROUT>(a, s);
+    }
+    return fail(PMG_E_INVALID, "pmg_spconv_col: unknown epilogue");
+}
+
 int launch_conv_col(int precision, const ColConvArgs& a, int C, int epi, hipStream_t s) {
     if (precision == PMG_PREC_INT8) {
         switch (C) {
-            case 16: return launch_col2<int8_t, 16>(a, epi, s);
-            case 32: return launch_col2<int8_t, 32>(a, epi, s);
-            case 48: return launch_col2<int8_t, 48>(a, epi, s);
+            case 16: return launch_colv2<16>(a, epi, s);
+            case 32: return launch_colv2<32>(a, epi, s);
+            case 48: return launch_colv2<48>(a, epi, s);
             case 64: return launch_col2<int8_t, 64>(a, epi, s);
             case 128: return launch_col2<int8_t, 128>(a, epi, s);
         }
