@@ -91,9 +91,18 @@ __device__ inline EpiConst<const float*> epi_global(const ColConvArgs& a) {
 }
 
 // Epilogue of one 16-voxel tile: lane holds channels 16j + 4g + i (j < C/16, i < 4) of voxel m.
+// The skip (residual) vectors of the residual epilogues are loaded by the caller (load_skip), so that a kernel can
+// issue them for several tiles before it needs them.
+template <int C>
+__device__ inline void load_skip(const ColConvArgs& a, int m, int M, int g, v4f (&sk)[C / 16]) {
+    const int64_t mo = m < M ? m : 0;
+#pragma unroll
+    for (int j = 0; j < C / 16; ++j) sk[j] = *(const v4f*)(a.skip + mo * C + 16 * j + 4 * g);
+}
+
 template <typename T, int C, int EPI, class P = const float*>
 __device__ inline void col_epilogue(const ColConvArgs& a, const typename ColAcc<T>::type (&acc)[C / 16], int m,
-                                    int M, int g, const EpiConst<P>& k) {
+                                    int M, int g, const EpiConst<P>& k, const v4f (&sk)[C / 16]) {
     constexpr int NB = C / 16;
     const bool ok = m < M;
     const int64_t mo = ok ? m : 0;
@@ -148,9 +157,8 @@ __device__ inline void col_epilogue(const ColConvArgs& a, const typename ColAcc<
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
             const int64_t o = mo * C + 16 * j + 4 * g;
-            const v4f sk = *(const v4f*)(a.skip + o);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) y[j][i] = y[j][i] + sk[i];
+            for (int i = 0; i < 4; ++i) y[j][i] = y[j][i] + sk[j][i];
             if (EPI != PMG_EPI_ROUT && ok) *(v4f*)((float*)a.out + o) = v4f{y[j][0], y[j][1], y[j][2], y[j][3]};
         }
         if constexpr (EPI == PMG_EPI_RLN) {
@@ -396,8 +404,12 @@ __global__ __launch_bounds__(kColThreads) void spconv_col_k(ColConvArgs a) {
 
         // ---- epilogue
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
-            col_epilogue<T, C, EPI>(a, acc[rb], s0 + 32 * wv + 16 * rb + r, M, g, epi_global(a));
+        for (int rb = 0; rb < 2; ++rb) {
+            v4f sk[NB];
+            if constexpr (EPI == PMG_EPI_R || EPI == PMG_EPI_RLN || EPI == PMG_EPI_ROUT)
+                load_skip<C>(a, s0 + 32 * wv + 16 * rb + r, M, g, sk);
+            col_epilogue<T, C, EPI>(a, acc[rb], s0 + 32 * wv + 16 * rb + r, M, g, epi_global(a), sk);
+        }
 
         // ---- hand the next window to the other buffer (or, single-buffered, reload this one)
         if constexpr (NBUF == 2) {
@@ -500,11 +512,16 @@ __global__ __launch_bounds__(kColvThreads, 1) void spconv_colv_k(ColConvArgs a) 
     const uint8_t* __restrict__ xg = (const uint8_t*)a.x;
     const uint8_t* __restrict__ wg = (const uint8_t*)a.w;
 
-    // weights: block (v, j), lane chunk (r, c) at ((v * NB + j) * 16 * NCH + c * 16 + r) * 16
-    for (int e = tid; e < 27 * NB * 16 * NCH; e += kColvThreads) {
+    // weights: block (v, j), lane chunk (r, c) at ((v * NB + j) * 16 * NCH + c * 16 + r) * 16; all of a thread's
+    // loads are issued before its first LDS store (the first window's loads follow them)
+    constexpr int WCH = 27 * NB * 16 * NCH, WPT = (WCH + kColvThreads - 1) / kColvThreads;
+    v4i wtmp[WPT];
+#pragma unroll
+    for (int k = 0; k < WPT; ++k) {
+        const int e = tid + k * kColvThreads;
         const int rr = e % 16, c = (e / 16) % NCH, vj = e / (16 * NCH);
         const int v = vj / NB, j = vj - (vj / NB) * NB;
-        ((v4i*)s_w)[e] = *(const v4i*)(wg + ((int64_t)(16 * j + rr) * 27 + v) * ROWB + 16 * c);
+        wtmp[k] = e < WCH ? *(const v4i*)(wg + ((int64_t)(16 * j + rr) * 27 + v) * ROWB + 16 * c) : v4i{0, 0, 0, 0};
     }
     for (int e = tid; e < 5 * C; e += kColvThreads) {
         const int q = e / C, n = e - (e / C) * C;
@@ -564,15 +581,17 @@ __global__ __launch_bounds__(kColvThreads, 1) void spconv_colv_k(ColConvArgs a) 
 
     const int nseg = (M + kColvSeg - 1) / kColvSeg;
     int seg = blockIdx.x;
-    if (seg < nseg) {
-        fetch(seg);
-        commit();
+    if (seg < nseg) fetch(seg);
+#pragma unroll
+    for (int k = 0; k < WPT; ++k) {
+        const int e = tid + k * kColvThreads;
+        if (e < WCH) ((v4i*)s_w)[e] = wtmp[k];
     }
+    if (seg < nseg) commit();
     for (; seg < nseg; seg += gridDim.x) {
         const int s0 = seg * kColvSeg;
         const int nxt = seg + gridDim.x;
         __syncthreads();  // window (and, the first time, weights and constants) visible to all waves
-        if (nxt < nseg) fetch(nxt);  // in flight during this segment's compute
 
         int zc[4], pi[4], pj[4];
 #pragma unroll
@@ -590,6 +609,9 @@ __global__ __launch_bounds__(kColvThreads, 1) void spconv_colv_k(ColConvArgs a) 
 #pragma unroll
             for (int j = 0; j < NB; ++j) acc[t][j] = v4i{0, 0, 0, 0};
 
+        // Straight-line over the 27 taps (v = 3 (di * 3 + dj) + dz + 1), software-pipelined: the codes and keys of
+        // pixel offset o + 1 are read when offset o starts, the weights of tap v + 1 before tap v's MFMAs. No tap is
+        // skipped: 64 rows cover almost every tap anyway, and branches would stop the loads from moving ahead.
         struct Nb {
             v4i x[4];
             int z[4];
@@ -602,52 +624,51 @@ __global__ __launch_bounds__(kColvThreads, 1) void spconv_colv_k(ColConvArgs a) 
                 n.z[t] = zb[di * kColvWin + dj + 16 * t];
             }
         };
-        auto compute_nb = [&](int o, const Nb& n) {
-            const int di = o / 3, dj = o % 3;
-            int dz[4];
+        auto load_w = [&](int v, v4i (&w)[NB]) {
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const bool in = (unsigned)(pi[t] + di - 1) < (unsigned)H && (unsigned)(pj[t] + dj - 1) < (unsigned)W;
-                dz[t] = in ? n.z[t] - zc[t] + 1 : 3;  // 0, 1, 2: tap dz - 1; anything else: no tap
-            }
+            for (int j = 0; j < NB; ++j) w[j] = *(lds_v4i*)(wb + (v * NB + j) * G::WBLK);
+        };
+        Nb X[2];
+        v4i Wt[2][NB];
+        int dz[4];
+        load_nb(0, X[0]);
+        load_w(0, Wt[0]);
 #pragma unroll
-            for (int d = 0; d < 3; ++d) {
-                const bool any = dz[0] == d || dz[1] == d || dz[2] == d || dz[3] == d;
-                if (__builtin_amdgcn_ballot_w64(any)) {
-                    const int v = o * 3 + d;
-                    v4i wop[NB];
+        for (int v = 0; v < 27; ++v) {
+            const int o = v / 3, d = v % 3;
+            const Nb& n = X[o & 1];
+            if (d == 0 && o + 1 < 9) load_nb(o + 1, X[(o + 1) & 1]);
+            if (v + 1 < 27) load_w(v + 1, Wt[(v + 1) & 1]);
+            __builtin_amdgcn_sched_barrier(0);
+            if (d == 0) {
+                const int di = o / 3, dj = o % 3;
 #pragma unroll
-                    for (int j = 0; j < NB; ++j) wop[j] = *(lds_v4i*)(wb + (v * NB + j) * G::WBLK);
-                    v4i xm[4];
-#pragma unroll
-                    for (int t = 0; t < 4; ++t) xm[t] = (kin && dz[t] == d) ? n.x[t] : v4i{0, 0, 0, 0};
-#pragma unroll
-                    for (int j = 0; j < NB; ++j)
-#pragma unroll
-                        for (int t = 0; t < 4; ++t)
-                            acc[t][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wop[j], xm[t], acc[t][j], 0, 0, 0);
+                for (int t = 0; t < 4; ++t) {
+                    const bool in =
+                        (unsigned)(pi[t] + di - 1) < (unsigned)H && (unsigned)(pj[t] + dj - 1) < (unsigned)W;
+                    dz[t] = in ? n.z[t] - zc[t] + 1 : 3;  // 0, 1, 2: tap dz - 1; anything else: no tap
                 }
             }
-        };
-        Nb A, B;
-        load_nb(0, A);
+            v4i xm[4];
 #pragma unroll
-        for (int o = 0; o < 9; o += 2) {
-            if (o + 1 < 9) load_nb(o + 1, B);
+            for (int t = 0; t < 4; ++t) xm[t] = (kin && dz[t] == d) ? n.x[t] : v4i{0, 0, 0, 0};
+#pragma unroll
+            for (int j = 0; j < NB; ++j)
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    acc[t][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(Wt[v & 1][j], xm[t], acc[t][j], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
-            compute_nb(o, A);
-            __builtin_amdgcn_sched_barrier(0);
-            if (o + 1 < 9) {
-                if (o + 2 < 9) load_nb(o + 2, A);
-                __builtin_amdgcn_sched_barrier(0);
-                compute_nb(o + 1, B);
-                __builtin_amdgcn_sched_barrier(0);
-            }
         }
-
+        if (nxt < nseg) fetch(nxt);  // the next window: in flight during the epilogue
+        // the residual inputs of all four tiles are requested before any is used
+        v4f sk[4][NB];
+        if constexpr (EPI == PMG_EPI_R || EPI == PMG_EPI_RLN || EPI == PMG_EPI_ROUT) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) load_skip<C>(a, s0 + kColvRows * wv + 16 * t + r, M, g, sk[t]);
+        }
 #pragma unroll
         for (int t = 0; t < 4; ++t)
-            col_epilogue<int8_t, C, EPI, kptr>(a, acc[t], s0 + kColvRows * wv + 16 * t + r, M, g, kc);
+            col_epilogue<int8_t, C, EPI, kptr>(a, acc[t], s0 + kColvRows * wv + 16 * t + r, M, g, kc, sk[t]);
 
         if (nxt < nseg) {
             __syncthreads();  // every wave is done reading this window
