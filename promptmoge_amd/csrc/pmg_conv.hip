@@ -176,6 +176,214 @@ static int pick_nb(int Co) {
     return 1;
 }
 
+// ---------------------------------------------------------------------------------------------------------------
+// int8, Ci = Co = C in {64, 128}: block-tiled, weight-staged variant for large maps (the 1M-voxel microbench).
+//
+// A persistent 8-wave block owns chunks of 512 output rows (64 rows per wave in four 16-row tiles) and all C output
+// channels. It walks the chunk's union of active taps (OR of its 32 tile masks). For each tap the whole block stages
+// that tap's C x C weights in LDS in MFMA operand order (one 1 KB block per 16 output channels and 64-wide K step:
+// conflict-free 16-byte reads), double-buffered so the next tap's weights load while this tap's MFMAs run. Every
+// wave gathers its rows' neighbour codes x[nmap[v][m]] straight from global memory, two taps ahead for the map
+// indices and one tap ahead for the codes, so the dependent index -> code loads overlap the matrix work. Each LDS
+// weight read feeds four tiles, each gathered chunk NB column blocks. Operands are swapped (D = W * X^T): a lane
+// ends with 4 consecutive output channels of one row and the epilogue stores vectors. Chunks are assigned so that
+// the blocks of one XCD (block b runs on XCD b % 8) process adjacent row ranges and share their neighbours in L2.
+constexpr int kG2Threads = 512;
+constexpr int kG2Waves = kG2Threads / 64;
+constexpr int kG2Chunk = kG2Waves * 64;
+
+template <int C, int EPI>
+__global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
+    constexpr int NB = C / 16, KS = C / 64;
+    constexpr int WCH = C * C / 16;                               // 16-byte chunks of one tap's weights
+    constexpr int WPT = (WCH + kG2Threads - 1) / kG2Threads;      // per thread
+    static_assert(C == 64 || C == 128, "C must be 64 or 128");
+
+    __shared__ __attribute__((aligned(16))) uint8_t s_w[2][C * C];
+    __shared__ float s_k[2][C];  // w_scale, bias
+    __shared__ uint32_t s_uni;
+
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int M = (int)a.M;
+    const int64_t ntile = (a.M + 15) >> 4;
+    const uint8_t* __restrict__ xg = a.x;
+    const uint8_t* __restrict__ wg = a.w;
+    typedef const __attribute__((address_space(3))) v4i lds_v4i;
+
+    for (int e = tid; e < 2 * C; e += kG2Threads) {
+        const int q = e / C, n = e - (e / C) * C;
+        const float* src = q == 0 ? a.w_scale : a.bias;
+        s_k[q][n] = src ? src[n] : 0.0f;
+    }
+
+    // chunk schedule: XCD x = b % 8 takes a contiguous range of chunks, its blocks interleaved within it
+    const int nchunk = (M + kG2Chunk - 1) / kG2Chunk;
+    const int G = gridDim.x, b = blockIdx.x;
+    const int nx = G >= 8 ? 8 : 1;
+    const int x = b % nx, bi = b / nx, nbx = (G - x + nx - 1) / nx;  // blocks on this XCD
+    const int c0 = (int)((int64_t)nchunk * x / nx), c1 = (int)((int64_t)nchunk * (x + 1) / nx);
+
+    auto w_load = [&](int v, v4i (&wr)[WPT]) {
+#pragma unroll
+        for (int k = 0; k < WPT; ++k) {
+            const int e = tid + k * kG2Threads;
+            const int l = e & 63, js = e >> 6;
+            const int j = js / KS, s = js - (js / KS) * KS;
+            wr[k] = e < WCH ? *(const v4i*)(wg + ((int64_t)(16 * j + (l & 15)) * 27 + v) * C + 64 * s + 16 * (l >> 4))
+                            : v4i{0, 0, 0, 0};
+        }
+    };
+    auto w_store = [&](int buf, const v4i (&wr)[WPT]) {
+#pragma unroll
+        for (int k = 0; k < WPT; ++k) {
+            const int e = tid + k * kG2Threads;
+            if (e < WCH) ((v4i*)s_w[buf])[e] = wr[k];
+        }
+    };
+
+    for (int ch = c0 + bi; ch < c1; ch += nbx) {
+        const int row0 = ch * kG2Chunk + wv * 64 + r;  // row of tile 0 for this lane
+        __syncthreads();  // the previous chunk's readers of s_uni and s_w are done
+        if (wv == 0) {
+            const int64_t tl = (int64_t)ch * (kG2Chunk / 16) + (lane & 31);
+            uint32_t mk = (lane < 32 && tl < ntile) ? a.tmask[tl] : 0u;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) mk |= __shfl_xor(mk, o, 64);
+            if (lane == 0) s_uni = mk & 0x7ffffffu;
+        }
+        __syncthreads();
+        uint32_t rem = s_uni;
+        v4i acc[4][NB];
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int j = 0; j < NB; ++j) acc[t][j] = v4i{0, 0, 0, 0};
+
+        if (rem) {
+            auto take = [&]() {
+                const int v = rem ? (int)__builtin_ctz(rem) : -1;
+                rem = rem ? rem & (rem - 1) : 0u;
+                return v;
+            };
+            auto idx_load = [&](int v, int (&id)[4]) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const int row = row0 + 16 * t;
+                    id[t] = (v >= 0 && row < M) ? a.nmap_t[(int64_t)v * M + row] : -1;
+                }
+            };
+            auto gather = [&](const int (&id)[4], v4i (&xs)[4][KS]) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+#pragma unroll
+                    for (int s = 0; s < KS; ++s)
+                        xs[t][s] = (id[t] >= 0 && id[t] < M)
+                                       ? *(const v4i*)(xg + (int64_t)id[t] * C + 64 * s + 16 * g)
+                                       : v4i{0, 0, 0, 0};
+            };
+            auto mma_tap = [&](int buf, const v4i (&xs)[4][KS]) {
+#pragma unroll
+                for (int s = 0; s < KS; ++s)
+#pragma unroll
+                    for (int j = 0; j < NB; ++j) {
+                        const v4i wop = *(lds_v4i*)(s_w[buf] + ((j * KS + s) * 64 + lane) * 16);
+#pragma unroll
+                        for (int t = 0; t < 4; ++t)
+                            acc[t][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wop, xs[t][s], acc[t][j], 0, 0, 0);
+                    }
+            };
+
+            int v0 = take(), v1 = take();
+            v4i wr[WPT];
+            int idA[4], idB[4];
+            v4i xA[4][KS], xB[4][KS];
+            w_load(v0, wr);
+            idx_load(v0, idA);
+            idx_load(v1, idB);
+            w_store(0, wr);
+            gather(idA, xA);
+            __syncthreads();
+            // invariant at the top: tap v0's weights in s_w[0] and codes in xA; v1's indices in idB
+            for (;;) {
+                // ---- tap v0 (buffer 0), while v1's weights and codes and v2's indices load
+                const int v2 = take();
+                if (v1 >= 0) w_load(v1, wr);
+                gather(idB, xB);
+                idx_load(v2, idA);
+                __builtin_amdgcn_sched_barrier(0);
+                mma_tap(0, xA);
+                __builtin_amdgcn_sched_barrier(0);
+                if (v1 < 0) break;
+                w_store(1, wr);
+                __syncthreads();
+                // ---- tap v1 (buffer 1), while v2's weights and codes and v3's indices load
+                const int v3 = take();
+                if (v2 >= 0) w_load(v2, wr);
+                gather(idA, xA);
+                idx_load(v3, idB);
+                __builtin_amdgcn_sched_barrier(0);
+                mma_tap(1, xB);
+                __builtin_amdgcn_sched_barrier(0);
+                if (v2 < 0) break;
+                w_store(0, wr);
+                __syncthreads();
+                v1 = v3;
+            }
+        }
+
+        // ---- epilogue: lane holds channels 16j + 4g + i of row row0 + 16t
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int m = row0 + 16 * t;
+            if (m >= M) continue;
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                const int64_t o = (int64_t)m * C + 16 * j + 4 * g;
+                if constexpr (EPI == PMG_EPI_ACC) {
+                    *(v4i*)((int32_t*)a.out + o) = acc[t][j];
+                } else {
+                    float y[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int n = 16 * j + 4 * g + i;
+                        float u = (float)acc[t][j][i] * a.a_scale;
+                        u = u * s_k[0][n];
+                        if (a.bias) u = u + s_k[1][n];
+                        y[i] = u;
+                    }
+                    if constexpr (EPI == PMG_EPI_Q) {
+                        store_silu_codes4(y, a.out_mult, (int8_t*)a.out + o);
+                    } else if constexpr (EPI == PMG_EPI_R) {
+                        const v4f sk = *(const v4f*)(a.skip + o);
+                        *(v4f*)((float*)a.out + o) = v4f{y[0] + sk[0], y[1] + sk[1], y[2] + sk[2], y[3] + sk[3]};
+                    } else {
+                        *(v4f*)((float*)a.out + o) = v4f{y[0], y[1], y[2], y[3]};
+                    }
+                }
+            }
+        }
+    }
+}
+
+template <int C>
+static int launch_g2(const ConvArgs& a, int epilogue, hipStream_t s) {
+    static int cus = -1;
+    if (cus < 0) cus = num_cus();
+    const int64_t nchunk = (a.M + kG2Chunk - 1) / kG2Chunk;
+    const unsigned grid = (unsigned)(nchunk < cus ? nchunk : cus);
+    switch (epilogue) {
+        case PMG_EPI_ACC: hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_ACC>), dim3(grid), dim3(kG2Threads), 0, s, a); break;
+        case PMG_EPI_Q: hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_Q>), dim3(grid), dim3(kG2Threads), 0, s, a); break;
+        case PMG_EPI_R: hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_R>), dim3(grid), dim3(kG2Threads), 0, s, a); break;
+        case PMG_EPI_BIAS:
+            hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_BIAS>), dim3(grid), dim3(kG2Threads), 0, s, a);
+            break;
+        default: return fail(PMG_E_INVALID, "spconv: epilogue not available for this precision");
+    }
+    return check_launch("spconv_g2_k");
+}
+
 template <typename T>
 static int conv_common(const ConvArgs& a, int Ci, int epilogue, hipStream_t s) {
     const int nb = pick_nb(a.Co);
@@ -223,6 +431,11 @@ int pmg_spconv_i8(const int8_t* x, const int32_t* nmap_t, const uint32_t* tile_m
     if (M == 0) return PMG_OK;
     ConvArgs a{(const uint8_t*)x, nmap_t, tile_mask, (const uint8_t*)w, M, Co, Ci, Ci / 16,
                a_scale, w_scale, bias, out_mult, skip, out};
+    if (Ci == Co && (Ci == 64 || Ci == 128) && epilogue != PMG_EPI_SILU && aligned16(out) &&
+        (epilogue != PMG_EPI_R || aligned16(skip))) {
+        if (Ci == 64) return launch_g2<64>(a, epilogue, (hipStream_t)stream);
+        return launch_g2<128>(a, epilogue, (hipStream_t)stream);
+    }
     return conv_common<int8_t>(a, Ci, epilogue, (hipStream_t)stream);
 }
 

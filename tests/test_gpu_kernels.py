@@ -186,7 +186,7 @@ def test_conv_int8_generic_map(gpu):
     assert np.array_equal(acc.cpu().numpy(), ocv.conv_acc_int(x, nm, w))
 
 
-@pytest.mark.parametrize("C", [32, 48])
+@pytest.mark.parametrize("C", [32, 48, 64, 128])
 def test_conv_int8_epilogues(gpu, C):
     announce(f"conv int8 epilogues C={C}")
     rng = np.random.default_rng(C)
