@@ -200,6 +200,21 @@ int pmg_fit_prompt(const float* logz, int64_t stride, const float* lidar, const 
                    void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------------------------------------------ *
+ * (5) LiDAR prompt fill.
+ *
+ * pmg_nearest_fill -- replaces nearest_fill (promptmoge/model.py:61-72): every pixel with depth <= 0 (or NaN)
+ * takes the depth of the nearest valid pixel and conf 1; valid pixels keep depth and conf; an image with no
+ * valid pixel is left as it is. "Nearest" is scipy.ndimage.distance_transform_edt's feature transform: least
+ * Euclidean distance, ties to the smallest column, then the smallest row -- the result is exact.
+ * depth, conf: [B][h][w] fp32 (conf may be NULL together with conf_out); depth_out / conf_out may alias them.
+ * src_index: [B][h][w] int32 flat index i*w + j of each pixel's source within its image (-1: no valid pixel),
+ * or NULL. h, w <= 8192. The workspace (pmg_nearest_fill_workspace_bytes) needs no initialisation.
+ * ------------------------------------------------------------------------------------------------------------ */
+size_t pmg_nearest_fill_workspace_bytes(int B, int h, int w);
+int pmg_nearest_fill(const float* depth, const float* conf, int B, int h, int w, float* depth_out, float* conf_out,
+                     int32_t* src_index, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------------------------------------------ *
  * The fused refiner step -- replaces one iteration of the refine loop (v3.py:547-576) for a single-level
  * refiner: prompt fit -> prompt residual/gate -> voxelise -> column neighbour map -> input_proj (+ prompt_proj)
  * -> n_blocks residual blocks (LN, SiLU, conv1, SiLU, conv2, + skip) -> out_proj -> logz += delta

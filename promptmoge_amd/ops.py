@@ -16,6 +16,7 @@ from ._lib import EPI_ACC, EPI_BIAS, EPI_Q, EPI_R, EPI_RLN, EPI_ROUT, EPI_SILU, 
 __all__ = [
     "voxelize", "nmap_column", "nmap_hash", "nmap_from_rows", "kmap_compact", "spconv_i8", "spconv_f16",
     "spconv_f32", "spconv_col", "ln_silu_quant", "ln_silu_f16", "fit_scale_shift", "fit_prompt", "math_device",
+    "nearest_fill",
     "EPI_ACC", "EPI_Q", "EPI_R", "EPI_BIAS", "EPI_SILU", "EPI_RLN", "EPI_ROUT",
 ]
 
@@ -294,3 +295,40 @@ def fit_prompt(points: torch.Tensor, lidar: torch.Tensor, conf: torch.Tensor, it
     if return_info:
         return st[:, 0], st[:, 1], info
     return st[:, 0], st[:, 1]
+
+
+def nearest_fill(depth: torch.Tensor, conf: Optional[torch.Tensor] = None, *, return_index: bool = False,
+                 out: Optional[Tuple[torch.Tensor, Optional[torch.Tensor]]] = None):
+    """nearest_fill (promptmoge/model.py:61-72) on the GPU for depth (and conf) maps [..., h, w] fp32.
+
+    Pixels with depth <= 0 (or NaN) take the depth of the nearest valid pixel -- the pixel scipy's exact EDT
+    feature transform names: least distance, ties to the smaller column, then the smaller row -- and conf 1; an
+    image without a valid pixel is returned as it is. Returns (depth, conf | None[, src_index]); `out` may be the
+    inputs themselves (in-place fill). src_index holds i*w + j of each pixel's source (-1: no valid pixel).
+    """
+    depth = _dev(depth, "depth", torch.float32)
+    if depth.ndim < 2:
+        raise ValueError("depth must be [..., h, w]")
+    h, w = depth.shape[-2:]
+    B = depth.numel() // max(h * w, 1)
+    if conf is not None:
+        conf = _dev(conf, "conf", torch.float32)
+        if conf.shape != depth.shape:
+            raise ValueError("conf must have the shape of depth")
+    if out is None:
+        d_out = torch.empty_like(depth)
+        c_out = torch.empty_like(conf) if conf is not None else None
+    else:
+        d_out, c_out = out
+        d_out = _dev(d_out, "depth_out", torch.float32)
+        if d_out.shape != depth.shape or (conf is not None and (c_out is None or c_out.shape != conf.shape)):
+            raise ValueError("out must match the inputs")
+    idx = torch.empty(depth.shape, dtype=torch.int32, device=depth.device) if return_index else None
+    if depth.numel() > 0:
+        ws_bytes = lib().pmg_nearest_fill_workspace_bytes(B, h, w)
+        ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=depth.device)
+        call("pmg_nearest_fill", _p(depth), _p(conf), B, h, w, _p(d_out), _p(c_out) if conf is not None else None,
+             _p(idx), _p(ws), ws_bytes, _stream())
+    if return_index:
+        return d_out, c_out, idx
+    return d_out, c_out

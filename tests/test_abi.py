@@ -77,3 +77,17 @@ def test_workspace_sizes(libpmg):
     assert libpmg.pmg_hash_workspace_bytes(1_000_000) >= 4 * 1_000_000 * 12
     assert libpmg.pmg_fit_workspace_bytes(307_200, 10) >= 10 * 3 * 2048 * 4
     assert libpmg.pmg_kmap_workspace_bytes(1000) >= 27 * 4 * 4
+
+
+def test_nearest_fill_rejected_on_host(libpmg):
+    dummy = C.c_void_p(16)
+    ws = libpmg.pmg_nearest_fill_workspace_bytes(1, 8, 8)
+    assert ws >= 8 * 8 * 4
+    # map taller than the LDS column buffer
+    assert libpmg.pmg_nearest_fill(dummy, None, 1, 8193, 8, dummy, None, None, dummy, 1 << 30,
+                                   None) == _lib.PMG_E_INVALID
+    # conf without conf_out
+    assert libpmg.pmg_nearest_fill(dummy, dummy, 1, 8, 8, dummy, None, None, dummy, ws, None) == _lib.PMG_E_INVALID
+    # workspace too small
+    assert libpmg.pmg_nearest_fill(dummy, None, 1, 8, 8, dummy, None, None, dummy, ws - 1,
+                                   None) == _lib.PMG_E_INVALID
