@@ -199,6 +199,17 @@ int pmg_fit_prompt(const float* logz, int64_t stride, const float* lidar, const 
                    int dh, int dw, int iters, float trim, int min_points, float* st, int32_t* info,
                    void* workspace, size_t workspace_bytes, void* stream);
 
+/* The final metric fit of MoGeModel.forward (v3.py:768-778, metric_from='lidar_ls'), at LiDAR resolution:
+ * d_lr = F.interpolate(depth, (dh, dw), mode='area') of depth z = exp(logz) on the H x W map (adaptive average
+ * pooling: fp32 window sum in row-major order / height / width), mask = conf >= 2 & lidar > 0 & d_lr > 0, and
+ * with mask_binary ([B][H][W] uint8, or NULL) also area-pooled mask_binary > 0.99; then fit (s, t) of
+ * lidar ~= s*d_lr + t as pmg_fit_scale_shift. The workspace (pmg_fit_final_workspace_bytes) must be zero-filled
+ * before its first use and is reusable afterwards. */
+size_t pmg_fit_final_workspace_bytes(int B, int dh, int dw, int iters);
+int pmg_fit_final(const float* logz, int64_t stride, const float* lidar, const float* conf, const uint8_t* mask_binary,
+                  int B, int H, int W, int dh, int dw, int iters, float trim, int min_points, float* st, int32_t* info,
+                  void* workspace, size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------------------------------------------ *
  * (5) LiDAR prompt fill.
  *
@@ -236,7 +247,7 @@ typedef struct {
     int fit_min_points;     /* 32 */
     int use_prompt;         /* feed (residual, gate) through prompt_proj (v3.py:549-555) */
     int soft_gate;          /* soft_residual_gate (v3.py:379-382) */
-    int final_fit;          /* also fit (s, t) of the refined depth against the LiDAR */
+    int final_fit;          /* also run the final metric fit (pmg_fit_final) on the refined depth */
     int use_graph;          /* capture the step into a HIP graph and replay it */
 } pmg_refiner_config;
 

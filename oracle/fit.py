@@ -97,3 +97,42 @@ def prompt_inputs(points, lidar, conf):
     z = exp_f32(points[..., 2])
     mask = valid & (c >= F32(0.999))
     return z.reshape(B, -1), d.reshape(B, -1), mask.reshape(B, -1), d, c
+
+
+def area_bounds(dst: int, src: int):
+    """adaptive_avg_pool window of output index o: rows [floor(o*src/dst), ceil((o+1)*src/dst))."""
+    o = np.arange(dst, dtype=np.int64)
+    return (o * src) // dst, ((o + 1) * src + dst - 1) // dst
+
+
+def area_pool(x, dh: int, dw: int) -> np.ndarray:
+    """F.interpolate(x, (dh, dw), mode='area') for x [B, H, W] fp32: the window sum in fp32, row-major order, then
+    divided by the window height and then by its width (adaptive_avg_pool2d)."""
+    x = np.asarray(x, dtype=np.float32)
+    B, H, W = x.shape
+    r0, r1 = area_bounds(dh, H)
+    c0, c1 = area_bounds(dw, W)
+    out = np.empty((B, dh, dw), dtype=np.float32)
+    for oh in range(dh):
+        for ow in range(dw):
+            win = x[:, r0[oh]:r1[oh], c0[ow]:c1[ow]].reshape(B, -1)
+            s = np.zeros(B, dtype=np.float32)
+            for k in range(win.shape[1]):
+                s = (s + win[:, k]).astype(np.float32)
+            out[:, oh, ow] = s / F32(r1[oh] - r0[oh]) / F32(c1[ow] - c0[ow])
+    return out
+
+
+def final_inputs(points, lidar, conf, mask_binary=None):
+    """The final metric fit's inputs (v3.py:768-775) at LiDAR resolution: d_lr = area-pooled depth z = exp(logz);
+    mask = conf >= 2 & lidar > 0 & d_lr > 0 (& area-pooled mask_binary > 0.99). Returns z, target, mask [B, dh*dw]."""
+    points = np.asarray(points, dtype=np.float32)
+    B = points.shape[0]
+    lidar = np.asarray(lidar, dtype=np.float32).reshape(B, *np.shape(lidar)[-2:])
+    conf = np.asarray(conf, dtype=np.float32).reshape(lidar.shape)
+    dh, dw = lidar.shape[-2:]
+    z = area_pool(exp_f32(points[..., 2]), dh, dw)
+    mask = (conf >= F32(2.0)) & (lidar > 0) & (z > 0)
+    if mask_binary is not None:
+        mask &= area_pool(np.asarray(mask_binary, dtype=np.float32), dh, dw) > F32(0.99)
+    return z.reshape(B, -1), lidar.reshape(B, -1), mask.reshape(B, -1)

@@ -22,7 +22,7 @@ from typing import Optional
 import numpy as np
 
 from .conv import conv_acc_int, conv_float, epilogue_q, epilogue_r
-from .fit import fit_f64, prompt_inputs
+from .fit import final_inputs, fit_f64, prompt_inputs
 from .numerics import F32, ln_silu, log_f32, quad_sum, quant_i8
 from .structure import nmap_column, voxelize
 
@@ -138,8 +138,8 @@ def step(points, lidar, conf, w, *, precision="int8", iters=10, trim=0.2, min_po
     delta = out_proj(x, w)
     pts[..., 2] = pts[..., 2] + delta.reshape(B, H, W)
     fin = None
-    if final_fit:
-        z, tg, m, _, _ = prompt_inputs(pts, lidar, conf)
+    if final_fit:  # v3.py:768-778, at LiDAR resolution
+        z, tg, m = final_inputs(pts, lidar, conf)
         fin = fit_f64(z, tg, m, iters, trim, min_points)
     if trace is not None:
         trace.update(zq=zq, nmap=nmap, coords=coords, blocks=blk_trace, x=x, res=res, gate=gate)

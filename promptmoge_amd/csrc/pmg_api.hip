@@ -68,7 +68,7 @@ struct pmg_refiner {
     void* q2 = nullptr;
     float* st_scratch = nullptr;
     void* fit_ws[2] = {nullptr, nullptr};
-    size_t fit_ws_bytes = 0;
+    size_t fit_ws_bytes[2] = {0, 0};  // prompt fit, final fit
 
     // Captured steps, keyed by (points, points_out, lidar, conf, st_prompt, st_final, stream); a ping-pong of
     // two point buffers over K steps uses two entries.
@@ -119,7 +119,7 @@ static int enqueue_step(pmg_refiner* r, const float* points, float* points_out, 
         f.st = st;
         f.info = nullptr;
         f.workspace = r->fit_ws[0];
-        f.workspace_bytes = r->fit_ws_bytes;
+        f.workspace_bytes = r->fit_ws_bytes[0];
         if (int e = launch_fit(f, s)) return e;
     }
     const pmg_block_weights& b0 = r->blocks[0];
@@ -177,26 +177,26 @@ static int enqueue_step(pmg_refiner* r, const float* points, float* points_out, 
     }
 
     if (c.final_fit) {
-        FitLaunch f{};
-        f.mode = 1;
+        // v3.py:768-778: area-pool the refined depth to the LiDAR grid, mask, fit.
+        FinalFit f{};
         f.logz = points_out + 2;
         f.stride = 3;
         f.lidar = lidar;
         f.conf = conf;
+        f.mask_binary = nullptr;
         f.B = c.B;
         f.H = c.H;
         f.W = c.W;
         f.dh = c.dh;
         f.dw = c.dw;
-        f.N = (int64_t)c.H * c.W;
         f.iters = c.fit_iters;
         f.trim = c.fit_trim;
         f.min_points = c.fit_min_points;
         f.st = st_final ? st_final : r->st_scratch + 2 * c.B;
         f.info = nullptr;
         f.workspace = r->fit_ws[1];
-        f.workspace_bytes = r->fit_ws_bytes;
-        if (int e = launch_fit(f, s)) return e;
+        f.workspace_bytes = r->fit_ws_bytes[1];
+        if (int e = launch_final_fit(f, s)) return e;
     }
     return PMG_OK;
 }
@@ -225,7 +225,8 @@ pmg_refiner* pmg_refiner_create(const pmg_refiner_config* cfg) {
     r->M = (int64_t)c.B * c.H * c.W;
     const int64_t M = r->M;
     const size_t elt = c.precision == PMG_PREC_FP16 ? 2 : 1;
-    r->fit_ws_bytes = align_up(fit_workspace_bytes((int64_t)c.H * c.W, c.fit_iters), 256);
+    r->fit_ws_bytes[0] = align_up(fit_workspace_bytes((int64_t)c.H * c.W, c.fit_iters), 256);
+    r->fit_ws_bytes[1] = c.final_fit ? align_up(final_fit_workspace_bytes(c.B, c.dh, c.dw, c.fit_iters), 256) : 256;
     size_t off = 0;
     auto take = [&](size_t bytes) {
         const size_t o = off;
@@ -234,7 +235,7 @@ pmg_refiner* pmg_refiner_create(const pmg_refiner_config* cfg) {
     };
     const size_t o_zq = take(M * 4), o_zmin = take(c.B * 4), o_zmax = take(c.B * 4);
     const size_t o_x = take(M * c.C * 4), o_q1 = take(M * c.C * elt), o_q2 = take(M * c.C * elt);
-    const size_t o_st = take(4 * c.B * 4), o_f0 = take(r->fit_ws_bytes), o_f1 = take(r->fit_ws_bytes);
+    const size_t o_st = take(4 * c.B * 4), o_f0 = take(r->fit_ws_bytes[0]), o_f1 = take(r->fit_ws_bytes[1]);
     r->arena_bytes = off;
     if (hipMalloc(&r->arena, r->arena_bytes) != hipSuccess) {
         set_error("pmg_refiner_create: hipMalloc of " + std::to_string(r->arena_bytes) + " bytes failed");
@@ -338,7 +339,7 @@ int pmg_refiner_check(pmg_refiner* r, void* stream) {
         PMG_CHECK_HIP(hipMemcpy(&err[k], (uint8_t*)r->fit_ws[k] + 64, sizeof(int), hipMemcpyDeviceToHost));
     if (err[0] || err[1]) {
         // the fit's barrier state is undefined after an expired wait: start the workspaces over
-        for (int k = 0; k < 2; ++k) PMG_CHECK_HIP(hipMemset(r->fit_ws[k], 0, r->fit_ws_bytes));
+        for (int k = 0; k < 2; ++k) PMG_CHECK_HIP(hipMemset(r->fit_ws[k], 0, r->fit_ws_bytes[k]));
         PMG_CHECK_HIP(hipDeviceSynchronize());
         return fail(PMG_E_DEVICE, "pmg_refiner_check: a device-wide wait in the metric fit expired");
     }

@@ -804,6 +804,77 @@ int launch_fit(const FitLaunch& f, hipStream_t s) {
     return PMG_OK;
 }
 
+// ------------------------------------------------------------------------------------------------------------
+// Final metric fit inputs (v3.py:768-775), one thread per LiDAR pixel: d_lr = F.interpolate(depth, (dh, dw),
+// mode='area') of z = exp(logz) -- adaptive average pooling, the window [floor(o*H/dh), ceil((o+1)*H/dh)) summed
+// in fp32 in row-major order and divided by its height, then by its width, as adaptive_avg_pool2d does -- and
+// mask = conf >= 2 & lidar > 0 & d_lr > 0 (& the pooled mask_binary > 0.99).
+__global__ __launch_bounds__(256) void final_inputs_k(const float* __restrict__ logz, int64_t stride,
+                                                      const float* __restrict__ lidar, const float* __restrict__ conf,
+                                                      const uint8_t* __restrict__ mask_binary, int H, int W, int dh,
+                                                      int dw, int64_t n_out, float* __restrict__ z_out,
+                                                      uint8_t* __restrict__ m_out) {
+    const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (q >= n_out) return;
+    const int64_t plane = (int64_t)dh * dw;
+    const int64_t b = q / plane;
+    const int rem = (int)(q - b * plane);
+    const int oh = rem / dw, ow = rem - oh * dw;
+    const int r0 = (int)(((int64_t)oh * H) / dh), r1 = (int)((((int64_t)oh + 1) * H + dh - 1) / dh);
+    const int c0 = (int)(((int64_t)ow * W) / dw), c1 = (int)((((int64_t)ow + 1) * W + dw - 1) / dw);
+    const int64_t base = b * H * W;
+    float sz = 0.0f, sm = 0.0f;
+    for (int r = r0; r < r1; ++r)
+        for (int c = c0; c < c1; ++c) {
+            const int64_t p = base + (int64_t)r * W + c;
+            sz = sz + exp_f32(logz[p * stride]);
+            if (mask_binary) sm = sm + (mask_binary[p] ? 1.0f : 0.0f);
+        }
+    const float kh = (float)(r1 - r0), kw = (float)(c1 - c0);
+    const float z = sz / kh / kw;
+    const float d = lidar[q];
+    bool m = conf[q] >= 2.0f && d > 0.0f && z > 0.0f;
+    if (mask_binary) m = m && (sm / kh / kw > 0.99f);
+    z_out[q] = z;
+    m_out[q] = m ? 1 : 0;
+}
+
+size_t final_fit_workspace_bytes(int B, int dh, int dw, int iters) {
+    const size_t n = (size_t)B * dh * dw;
+    return align256(fit_workspace_bytes((int64_t)dh * dw, iters)) + align256(n * sizeof(float)) + align256(n);
+}
+
+int launch_final_fit(const FinalFit& f, hipStream_t s) {
+    PMG_REQUIRE(f.logz && f.lidar && f.conf && f.st, "null buffer");
+    PMG_REQUIRE(f.B >= 1 && f.H >= 1 && f.W >= 1 && f.dh >= 1 && f.dw >= 1 && f.stride >= 1, "bad shape");
+    PMG_REQUIRE((int64_t)f.dh * f.dw <= (int64_t)kFitMaxBlocks * kFitPerBlock, "LiDAR map larger than 2^21 pixels");
+    PMG_REQUIRE(f.workspace && f.workspace_bytes >= final_fit_workspace_bytes(f.B, f.dh, f.dw, f.iters),
+                "workspace too small");
+    const int64_t N = (int64_t)f.dh * f.dw;
+    const int64_t n_out = (int64_t)f.B * N;
+    const size_t fit_bytes = align256(fit_workspace_bytes(N, f.iters));
+    float* z_lr = (float*)((uint8_t*)f.workspace + fit_bytes);
+    uint8_t* m_lr = (uint8_t*)f.workspace + fit_bytes + align256((size_t)n_out * sizeof(float));
+    hipLaunchKernelGGL(final_inputs_k, dim3((unsigned)((n_out + 255) / 256)), dim3(256), 0, s, f.logz, f.stride,
+                       f.lidar, f.conf, f.mask_binary, f.H, f.W, f.dh, f.dw, n_out, z_lr, m_lr);
+    if (int e = check_launch("final_inputs_k")) return e;
+    FitLaunch g{};
+    g.mode = 0;
+    g.z = z_lr;
+    g.tg = f.lidar;
+    g.mask = m_lr;
+    g.B = f.B;
+    g.N = N;
+    g.iters = f.iters;
+    g.trim = f.trim;
+    g.min_points = f.min_points;
+    g.st = f.st;
+    g.info = f.info;
+    g.workspace = f.workspace;
+    g.workspace_bytes = fit_bytes;
+    return launch_fit(g, s);
+}
+
 }  // namespace pmg
 
 using namespace pmg;
@@ -811,6 +882,11 @@ using namespace pmg;
 extern "C" {
 
 size_t pmg_fit_workspace_bytes(int64_t N, int iters) { return fit_workspace_bytes(N, iters); }
+
+size_t pmg_fit_final_workspace_bytes(int B, int dh, int dw, int iters) {
+    if (B < 1 || dh < 1 || dw < 1) return 0;
+    return final_fit_workspace_bytes(B, dh, dw, iters);
+}
 
 int pmg_fit_scale_shift(const float* z, const float* target, const uint8_t* mask, int B, int64_t N, int iters,
                         float trim, int min_points, float* st, int32_t* info, void* workspace,
@@ -859,6 +935,14 @@ int pmg_fit_prompt(const float* logz, int64_t stride, const float* lidar, const 
     f.workspace = workspace;
     f.workspace_bytes = workspace_bytes;
     return launch_fit(f, (hipStream_t)stream);
+}
+
+int pmg_fit_final(const float* logz, int64_t stride, const float* lidar, const float* conf, const uint8_t* mask_binary,
+                  int B, int H, int W, int dh, int dw, int iters, float trim, int min_points, float* st, int32_t* info,
+                  void* workspace, size_t workspace_bytes, void* stream) {
+    FinalFit f{logz, stride, lidar, conf, mask_binary, B, H, W, dh, dw, iters, trim, min_points, st, info,
+               workspace, workspace_bytes};
+    return launch_final_fit(f, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -55,6 +55,26 @@ struct FitLaunch {
 size_t fit_workspace_bytes(int64_t N, int iters);
 int launch_fit(const FitLaunch& f, hipStream_t s);
 
+// The final metric fit at LiDAR resolution (v3.py:768-778): area-pooled depth, LiDAR mask, then the fit. The
+// workspace starts with the fit's own (error flag at byte 64), followed by the pooled depth and mask.
+struct FinalFit {
+    const float* logz;
+    int64_t stride;
+    const float* lidar;
+    const float* conf;
+    const uint8_t* mask_binary;
+    int B, H, W, dh, dw;
+    int iters;
+    float trim;
+    int min_points;
+    float* st;
+    int32_t* info;
+    void* workspace;
+    size_t workspace_bytes;
+};
+size_t final_fit_workspace_bytes(int B, int dh, int dw, int iters);
+int launch_final_fit(const FinalFit& f, hipStream_t s);
+
 struct ColConvArgs {
     const void* x;
     const int32_t* zq;

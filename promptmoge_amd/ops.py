@@ -15,7 +15,8 @@ from ._lib import EPI_ACC, EPI_BIAS, EPI_Q, EPI_R, EPI_RLN, EPI_ROUT, EPI_SILU, 
 
 __all__ = [
     "voxelize", "nmap_column", "nmap_hash", "nmap_from_rows", "kmap_compact", "spconv_i8", "spconv_f16",
-    "spconv_f32", "spconv_col", "ln_silu_quant", "ln_silu_f16", "fit_scale_shift", "fit_prompt", "math_device",
+    "spconv_f32", "spconv_col", "ln_silu_quant", "ln_silu_f16", "fit_scale_shift", "fit_prompt", "fit_final",
+    "math_device",
     "nearest_fill",
     "EPI_ACC", "EPI_Q", "EPI_R", "EPI_BIAS", "EPI_SILU", "EPI_RLN", "EPI_ROUT",
 ]
@@ -296,6 +297,30 @@ def fit_prompt(points: torch.Tensor, lidar: torch.Tensor, conf: torch.Tensor, it
         return st[:, 0], st[:, 1], info
     return st[:, 0], st[:, 1]
 
+
+def fit_final(points: torch.Tensor, lidar: torch.Tensor, conf: torch.Tensor, mask_binary: Optional[torch.Tensor] = None,
+              iters: int = 4, trim: float = 0.2, min_points: int = 32, return_info: bool = False):
+    """Final metric fit (v3.py:768-778) of the depth exp(logz) of the point map [B, H, W, 3] against LiDAR
+    [B, dh, dw] at LiDAR resolution (area-pooled depth). Returns (s, t) [B] (and the per-item info [B, 5])."""
+    points = _dev(points, "points", torch.float32)
+    lidar = _dev(lidar.float().contiguous(), "lidar")
+    conf = _dev(conf.float().contiguous(), "conf")
+    B, H, W, _ = points.shape
+    dh, dw = lidar.shape[-2:]
+    mb = None
+    if mask_binary is not None:
+        mb = _dev(mask_binary.to(torch.uint8).contiguous(), "mask_binary")
+        if mb.numel() != B * H * W:
+            raise ValueError("mask_binary must be [B, H, W]")
+    st = torch.empty((B, 2), dtype=torch.float32, device=points.device)
+    info = torch.empty((B, 5), dtype=torch.int32, device=points.device)
+    ws_bytes = lib().pmg_fit_final_workspace_bytes(B, dh, dw, iters)
+    ws = _fit_workspace(ws_bytes, points.device)
+    call("pmg_fit_final", points.data_ptr() + 8, 3, _p(lidar), _p(conf), _p(mb), B, H, W, dh, dw, int(iters),
+         float(trim), int(min_points), _p(st), _p(info), _p(ws), ws_bytes, _stream())
+    if return_info:
+        return st[:, 0], st[:, 1], info
+    return st[:, 0], st[:, 1]
 
 def nearest_fill(depth: torch.Tensor, conf: Optional[torch.Tensor] = None, *, return_index: bool = False,
                  out: Optional[Tuple[torch.Tensor, Optional[torch.Tensor]]] = None):

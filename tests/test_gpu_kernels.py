@@ -340,6 +340,38 @@ def test_fit_prompt_scene(gpu, name):
     _close_st(s.item(), t.item(), so[0], to[0])
 
 
+def _lowres(sc, dh, dw):
+    """The scene's LiDAR and confidence sampled down to (dh, dw), nearest: a sensor coarser than the point map."""
+    H, W = sc.lidar.shape
+    iy = (np.arange(dh) * H) // dh
+    ix = (np.arange(dw) * W) // dw
+    return np.ascontiguousarray(sc.lidar[iy][:, ix]), np.ascontiguousarray(sc.conf[iy][:, ix])
+
+
+@pytest.mark.parametrize("name,dh,dw,with_mask", [("A", 192, 256, False), ("A", 192, 256, True), ("B", 240, 320, False),
+                                                   ("H", 189, 252, False)])
+def test_fit_final_scene(gpu, name, dh, dw, with_mask):
+    """The final metric fit (v3.py:768-778) at LiDAR resolution: area-pooled depth and the LiDAR mask."""
+    announce(f"fit final scene={name} lidar={dh}x{dw} mask_binary={with_mask}")
+    cfg, sc = _scene(name)
+    lid, cnf = _lowres(sc, dh, dw)
+    B = 2
+    pts = np.stack([sc.points, sc.points * np.float32(1.01)])
+    lid2, cnf2 = np.stack([lid, lid]), np.stack([cnf, cnf[::-1]])
+    mb = None
+    if with_mask:
+        rng = np.random.default_rng(4)
+        mb = rng.random((B, cfg.H, cfg.W)) > 0.002      # sparse holes: some windows fall below 0.99
+    z, tg, m = ofit.final_inputs(pts, lid2, cnf2, mb)
+    so, to, info_o = ofit.fit_f64(z, tg, m, iters=10, return_info=True)
+    s, t, info = ops.fit_final(_t(pts, gpu), _t(lid2, gpu), _t(cnf2, gpu), None if mb is None else _t(mb, gpu),
+                               iters=10, return_info=True)
+    s, t, info = s.cpu().numpy(), t.cpu().numpy(), info.cpu().numpy()
+    for b in range(B):
+        assert info[b, 0] == info_o[b]["count"] and info[b, 4] == 0   # the mask is exact
+        _close_st(s[b], t[b], so[b], to[b])
+
+
 # ---------------------------------------------------------------------------------------------------------- level-0 conv
 def _col_setup(gpu, H=96, W=136, seed=3, B=2):
     cfg = spec.StepConfig("c", H, W, 100.0, 100.0, W / 2, H / 2, 16, 1, "int8", seed=seed)

@@ -17,13 +17,14 @@ from conftest import announce
 pytestmark = pytest.mark.gpu
 
 
-def _run(cfg, sc, w, *, B=1, use_graph=True, final_fit=False, reps=1):
+def _run(cfg, sc, w, *, B=1, use_graph=True, final_fit=False, reps=1, lidar=None):
     dev = torch.device("cuda:0")
+    lidar, conf = (sc.lidar, sc.conf) if lidar is None else lidar
     pts = np.broadcast_to(sc.points, (B,) + sc.points.shape).copy()
-    lid = np.broadcast_to(sc.lidar, (B,) + sc.lidar.shape).copy()
-    cnf = np.broadcast_to(sc.conf, (B,) + sc.conf.shape).copy()
-    step = RefinerStep(w, B, cfg.H, cfg.W, precision=cfg.precision, fit_iters=cfg.fit_iters, final_fit=final_fit,
-                       use_graph=use_graph)
+    lid = np.broadcast_to(lidar, (B,) + lidar.shape).copy()
+    cnf = np.broadcast_to(conf, (B,) + conf.shape).copy()
+    step = RefinerStep(w, B, cfg.H, cfg.W, dh=lid.shape[-2], dw=lid.shape[-1], precision=cfg.precision,
+                       fit_iters=cfg.fit_iters, final_fit=final_fit, use_graph=use_graph)
     stream = torch.cuda.Stream()
     outs = []
     with torch.cuda.stream(stream):
@@ -57,6 +58,24 @@ def test_step_int8(gpu, name):
         assert np.array_equal(step.buffer("q2").cpu().numpy(), last["q2"])
         assert np.array_equal(step.buffer("x").cpu().numpy(), before["x"])  # residual entering the last block
         assert np.array_equal(P, ref)
+
+
+def test_step_int8_lowres_lidar(gpu):
+    """LiDAR coarser than the point map (192 x 256 under 480 x 640): the prompt fit reads it nearest-resized up,
+    the final fit area-pools the refined depth down to it (v3.py:373-378, 768-778)."""
+    announce("step int8 config=A lidar=192x256")
+    cfg = spec.CONFIGS["A"]
+    sc = spec.make_scene(cfg)
+    w = spec.refiner_for(cfg, sc)
+    iy, ix = (np.arange(192) * cfg.H) // 192, (np.arange(256) * cfg.W) // 256
+    lowres = (np.ascontiguousarray(sc.lidar[iy][:, ix]), np.ascontiguousarray(sc.conf[iy][:, ix]))
+    step, pts, lid, cnf, outs = _run(cfg, sc, w, final_fit=True, lidar=lowres)
+    P, st, fin = outs[0]
+    ref, st_o, fin_o = orf.step(pts, lid, cnf, w, precision="int8", iters=cfg.fit_iters, final_fit=True)
+    assert abs(st[0, 0] - st_o[0][0]) <= 1e-5 * abs(st_o[0][0]) and abs(st[0, 1] - st_o[1][0]) <= 1e-5
+    d, dr = np.exp(P[..., 2].astype(np.float64)), np.exp(ref[..., 2].astype(np.float64))
+    assert (np.abs(d - dr) / dr).max() < 1e-3
+    assert abs(fin[0, 0] - fin_o[0][0]) <= 1e-5 * abs(fin_o[0][0]) and abs(fin[0, 1] - fin_o[1][0]) <= 1e-5
 
 
 def test_step_fp16_teacher(gpu):

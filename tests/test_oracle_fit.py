@@ -73,3 +73,28 @@ def test_fp64_and_fp32_forms_agree_on_a_scene():
     b = fit.fit_f32(z, tg, m, iters=10)
     assert abs(a[0][0] - b[0][0]) / abs(a[0][0]) < 1e-5 and abs(a[1][0] - b[1][0]) < 1e-5 * max(1, abs(a[1][0]))
     assert abs(a[0][0] - spec.S0) < 0.01  # the generator's affine frame is recovered
+
+
+@pytest.mark.parametrize("H,W,dh,dw", [(480, 640, 192, 256), (48, 64, 48, 64), (75, 100, 24, 32), (37, 53, 10, 7),
+                                       (30, 30, 7, 11), (10, 10, 20, 20)])
+def test_area_pool_matches_torch_area_interpolate(H, W, dh, dw):
+    """area_pool is F.interpolate(mode='area') bit for bit (window sum in fp32, / height / width)."""
+    torch = pytest.importorskip("torch")
+    F = torch.nn.functional
+    x = np.random.default_rng(H * W + dh).uniform(0.3, 7.0, (2, H, W)).astype(np.float32)
+    ref = F.interpolate(torch.from_numpy(x)[:, None], (dh, dw), mode="area")[:, 0].numpy()
+    assert np.array_equal(fit.area_pool(x, dh, dw).view(np.uint32), ref.view(np.uint32))
+
+
+def test_final_inputs_mask_rules():
+    """v3.py:770-773: conf >= 2, lidar > 0, pooled depth > 0, and (if given) pooled mask_binary > 0.99."""
+    H, W = 6, 6
+    logz = np.zeros((1, H, W), np.float32)          # depth 1 everywhere
+    pts = np.stack([logz, logz, logz], -1)
+    lidar = np.array([[[1.0, 0.0], [2.0, np.nan]]], np.float32)
+    conf = np.array([[[2.0, 2.0], [1.0, 2.0]]], np.float32)
+    z, tg, m = fit.final_inputs(pts, lidar, conf)
+    assert np.array_equal(z, np.ones((1, 4), np.float32)) and m.tolist() == [[True, False, False, False]]
+    mb = np.ones((1, H, W), bool)
+    mb[0, 0, 0] = False                              # 8/9 of the first 3x3 window: 0.889 <= 0.99
+    assert fit.final_inputs(pts, lidar, conf, mb)[2].tolist() == [[False, False, False, False]]
