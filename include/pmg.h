@@ -134,7 +134,8 @@ int pmg_spconv_f32(const float* x, const int32_t* nmap_t, const uint32_t* tile_m
  *   PMG_EPI_R     out fp32 = y + skip, y = (acc*a_scale)*w_scale[n] + bias[n] (int8) or acc + bias[n] (fp16)
  *   PMG_EPI_RLN   as R, and next_q [M][C] = quant(silu(LayerNorm(out) * ln_gamma + ln_beta), next_mult) (int8) or
  *                 half(silu(...)) (fp16): the next block's input (out may alias skip)
- *   PMG_EPI_ROUT  as R without storing it, then points_out[m] = (points[m].xy, points[m].z + out_b + out_w . x_new)
+ *   PMG_EPI_ROUT  as R without storing it; delta = out_b + out_w . x_new; then points_out[m] = (points[m].xy,
+ *                 points[m].z + delta), or, with points NULL, out fp32 [M] = delta (the refiner module's output)
  * LayerNorm and the out_proj dot product sum in a fixed order: channels n = 16j + 4g + i are summed per group g
  * (j outer, i inner) and the four group sums combined as ((s0 + s1) + (s2 + s3)). C in {16, 32, 48, 64, 128}. */
 typedef struct {
@@ -143,7 +144,7 @@ typedef struct {
     const float* bias;     /* [C] or NULL */
     float out_mult;        /* PMG_EPI_Q (int8): requantisation multiplier 127/clip of the output */
     const float* skip;     /* residual epilogues: [M][C] fp32 */
-    void* out;             /* main output (unused by PMG_EPI_ROUT) */
+    void* out;             /* main output (PMG_EPI_ROUT: the [M] delta when points is NULL) */
     const float* ln_gamma; /* PMG_EPI_RLN: next block's LayerNorm affine [C] */
     const float* ln_beta;
     float ln_eps;
@@ -151,7 +152,7 @@ typedef struct {
     void* next_q;     /* [M][C] int8 or fp16 */
     const float* out_w; /* PMG_EPI_ROUT: out_proj weight [C] and bias [1] */
     const float* out_b;
-    const float* points; /* [M][3] input point map */
+    const float* points; /* [M][3] input point map, or NULL (PMG_EPI_ROUT writes delta to out) */
     float* points_out;   /* [M][3] refined point map (may alias points) */
 } pmg_conv_epilogue;
 
@@ -287,6 +288,15 @@ int pmg_refiner_set_weights(pmg_refiner* r, const pmg_refiner_weights* w);
  * st_prompt: [B][2] prompt-fit (s, t) or NULL; st_final: [B][2] or NULL. */
 int pmg_refiner_step(pmg_refiner* r, const float* points, float* points_out, const float* lidar, const float* conf,
                      float* st_prompt, float* st_final, void* stream);
+/* The refiner module alone -- Sparse3DUNet.forward (moge/model/modules/sparse_unet.py:176-258) for a single-level
+ * refiner, the call _refine_logz makes at v3.py:356-357: out = out_proj(blocks(input_proj(feats) +
+ * prompt_proj(prompt_feats))), (M, 1). feats: [M][3] fp32 (the point map reshaped, v3.py:342), M = B*H*W in
+ * raster order; coords: [M][4] int32 (b, i, j, z) as _voxelize builds them (v3.py:337-340) -- only the z column
+ * is read, as the key of the level-0 stencil -- or NULL to key by rint(feats[:, 2] * depth_resolution), the same
+ * key up to a per-batch offset; prompt_feats: [M][2] fp32 or NULL (then no prompt_proj, sparse_unet.py:191);
+ * out: [M] fp32. No fit runs. Captured into a HIP graph per (buffers, stream) like pmg_refiner_step. */
+int pmg_refiner_forward(pmg_refiner* r, const float* feats, const int32_t* coords, const float* prompt_feats,
+                        float* out, void* stream);
 /* Synchronises `stream` and reports a device-side error flag of the last steps (PMG_E_DEVICE). */
 int pmg_refiner_check(pmg_refiner* r, void* stream);
 /* Device buffers of the last step, for parity tests: 0 zq (voxel keys [M]), 3 x (fp32 residual [M][C] entering the

@@ -197,3 +197,18 @@ def step_fakequant(points, lidar, conf, w, *, iters=10, trim=0.2, min_points=32,
     x2 = x @ np.asarray(w.out_w, np.float32).reshape(-1) + np.float32(w.out_b[0])
     pts[..., 2] = pts[..., 2] + x2.reshape(B, H, W).astype(np.float32)
     return pts
+
+
+def forward(feats, zkeys, H, W, w, prompt_feats=None, precision="int8"):
+    """The single-level refiner module (sparse_unet.py:176-258 with one level; blocks flex_sparse_blocks.py:50-75):
+    out_proj(blocks(input_proj(feats) (+ prompt_proj(prompt_feats)))) -> (M,) on level-0 voxels keyed by zkeys
+    [B, H, W] (raster order; any per-batch offset of the keys gives the same map)."""
+    feats = np.asarray(feats, np.float32)
+    nmap = nmap_column(np.asarray(zkeys))
+    res = gate = None
+    if prompt_feats is not None:
+        pf = np.asarray(prompt_feats, np.float32)
+        res, gate = pf[:, 0], pf[:, 1]
+    x = input_proj(feats, w, res, gate)
+    x = (blocks_int8 if precision == "int8" else blocks_fp16)(x, nmap, w)
+    return out_proj(x, w)

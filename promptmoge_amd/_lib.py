@@ -85,6 +85,7 @@ SIGNATURES = {
     "pmg_refiner_destroy": (None, [vp]),
     "pmg_refiner_set_weights": (i32, [vp, C.POINTER(RefinerWeights)]),
     "pmg_refiner_step": (i32, [vp, vp, vp, vp, vp, vp, vp, vp]),
+    "pmg_refiner_forward": (i32, [vp, vp, vp, vp, vp, vp]),
     "pmg_refiner_check": (i32, [vp, vp]),
     "pmg_refiner_buffer": (vp, [vp, i32]),
 }

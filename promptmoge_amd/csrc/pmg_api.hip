@@ -70,10 +70,10 @@ struct pmg_refiner {
     void* fit_ws[2] = {nullptr, nullptr};
     size_t fit_ws_bytes[2] = {0, 0};  // prompt fit, final fit
 
-    // Captured steps, keyed by (points, points_out, lidar, conf, st_prompt, st_final, stream); a ping-pong of
-    // two point buffers over K steps uses two entries.
+    // Captured steps and forwards, keyed by (kind, buffers..., stream); a ping-pong of two point buffers over K
+    // steps uses two entries.
     struct Graph {
-        const void* key[7];
+        const void* key[8];
         hipGraph_t graph;
         hipGraphExec_t exec;
     };
@@ -92,45 +92,14 @@ static void drop_graphs(pmg_refiner* r) {
 
 constexpr size_t kMaxGraphs = 4;
 
-// Enqueues one step on `s`.
-static int enqueue_step(pmg_refiner* r, const float* points, float* points_out, const float* lidar,
-                        const float* conf, float* st_prompt, float* st_final, hipStream_t s) {
+// Residual blocks: conv1 (bias, SiLU, requantise) then conv2 (bias, skip, and either the next block's
+// LayerNorm/SiLU/quantise or, after the last block, out_proj and either the log-depth update of the point map or
+// the module's (M, 1) output). Expects x and q1 from the input stage.
+static int enqueue_blocks(pmg_refiner* r, const float* points, float* points_out, float* delta_out, hipStream_t s) {
     const pmg_refiner_config& c = r->cfg;
-    const bool f16 = c.precision == PMG_PREC_FP16;
+    const int prec = c.precision == PMG_PREC_FP16 ? PMG_PREC_FP16 : PMG_PREC_INT8;
     const int64_t M = r->M;
     const int C = c.C;
-    float* st = st_prompt ? st_prompt : r->st_scratch;
-    if (c.use_prompt) {
-        FitLaunch f{};
-        f.mode = 1;
-        f.logz = points + 2;
-        f.stride = 3;
-        f.lidar = lidar;
-        f.conf = conf;
-        f.B = c.B;
-        f.H = c.H;
-        f.W = c.W;
-        f.dh = c.dh;
-        f.dw = c.dw;
-        f.N = (int64_t)c.H * c.W;
-        f.iters = c.fit_iters;
-        f.trim = c.fit_trim;
-        f.min_points = c.fit_min_points;
-        f.st = st;
-        f.info = nullptr;
-        f.workspace = r->fit_ws[0];
-        f.workspace_bytes = r->fit_ws_bytes[0];
-        if (int e = launch_fit(f, s)) return e;
-    }
-    const pmg_block_weights& b0 = r->blocks[0];
-    InputStage in{points, c.B, c.H, c.W, C, lidar, conf, c.dh, c.dw, st, c.use_prompt, c.soft_gate,
-                  r->w.in_w, r->w.in_b, r->w.pr_w, r->w.pr_b, r->x, b0.ln_gamma, b0.ln_beta, 1e-6f,
-                  b0.q1_mult, r->q1, c.depth_resolution, r->zq};
-    if (int e = launch_input_stage(in, f16, s)) return e;
-
-    // Residual blocks: conv1 (bias, SiLU, requantise) then conv2 (bias, skip, and either the next block's
-    // LayerNorm/SiLU/quantise or, after the last block, out_proj and the log-depth update).
-    const int prec = f16 ? PMG_PREC_FP16 : PMG_PREC_INT8;
     const int nbk = (int)r->blocks.size();
     for (int k = 0; k < nbk; ++k) {
         const pmg_block_weights& bk = r->blocks[k];
@@ -170,11 +139,80 @@ static int enqueue_step(pmg_refiner* r, const float* points, float* points_out, 
         } else {
             a2.out_w = r->w.out_w;
             a2.out_b = r->w.out_b;
-            a2.points = points;
-            a2.points_out = points_out;
+            if (delta_out) {
+                a2.out = delta_out;
+            } else {
+                a2.points = points;
+                a2.points_out = points_out;
+            }
             if (int e = launch_conv_col(prec, a2, C, PMG_EPI_ROUT, s)) return e;
         }
     }
+    return PMG_OK;
+}
+
+static InputStage input_stage_args(pmg_refiner* r, const float* feats) {
+    const pmg_refiner_config& c = r->cfg;
+    const pmg_block_weights& b0 = r->blocks[0];
+    InputStage in{};
+    in.points = feats;
+    in.B = c.B;
+    in.H = c.H;
+    in.W = c.W;
+    in.C = c.C;
+    in.dh = c.dh;
+    in.dw = c.dw;
+    in.soft_gate = c.soft_gate;
+    in.in_w = r->w.in_w;
+    in.in_b = r->w.in_b;
+    in.pr_w = r->w.pr_w;
+    in.pr_b = r->w.pr_b;
+    in.x_out = r->x;
+    in.gamma = b0.ln_gamma;
+    in.beta = b0.ln_beta;
+    in.eps = 1e-6f;
+    in.out_mult = b0.q1_mult;
+    in.q_out = r->q1;
+    in.resolution = c.depth_resolution;
+    in.zq_out = r->zq;
+    return in;
+}
+
+// Enqueues one step on `s`.
+static int enqueue_step(pmg_refiner* r, const float* points, float* points_out, const float* lidar,
+                        const float* conf, float* st_prompt, float* st_final, hipStream_t s) {
+    const pmg_refiner_config& c = r->cfg;
+    const bool f16 = c.precision == PMG_PREC_FP16;
+    float* st = st_prompt ? st_prompt : r->st_scratch;
+    if (c.use_prompt) {
+        FitLaunch f{};
+        f.mode = 1;
+        f.logz = points + 2;
+        f.stride = 3;
+        f.lidar = lidar;
+        f.conf = conf;
+        f.B = c.B;
+        f.H = c.H;
+        f.W = c.W;
+        f.dh = c.dh;
+        f.dw = c.dw;
+        f.N = (int64_t)c.H * c.W;
+        f.iters = c.fit_iters;
+        f.trim = c.fit_trim;
+        f.min_points = c.fit_min_points;
+        f.st = st;
+        f.info = nullptr;
+        f.workspace = r->fit_ws[0];
+        f.workspace_bytes = r->fit_ws_bytes[0];
+        if (int e = launch_fit(f, s)) return e;
+    }
+    InputStage in = input_stage_args(r, points);
+    in.lidar = lidar;
+    in.conf = conf;
+    in.st = st;
+    in.use_prompt = c.use_prompt;
+    if (int e = launch_input_stage(in, f16, s)) return e;
+    if (int e = enqueue_blocks(r, points, points_out, nullptr, s)) return e;
 
     if (c.final_fit) {
         // v3.py:768-778: area-pool the refined depth to the LiDAR grid, mask, fit.
@@ -198,6 +236,54 @@ static int enqueue_step(pmg_refiner* r, const float* points, float* points_out, 
         f.workspace_bytes = r->fit_ws_bytes[1];
         if (int e = launch_final_fit(f, s)) return e;
     }
+    return PMG_OK;
+}
+
+// Enqueues the refiner module's forward (Sparse3DUNet.forward, sparse_unet.py:176-258, single level): input_proj
+// (+ prompt_proj of the given prompt features), the residual blocks, out_proj into delta_out [M].
+static int enqueue_forward(pmg_refiner* r, const float* feats, const int32_t* coords, const float* prompt_feats,
+                           float* delta_out, hipStream_t s) {
+    InputStage in = input_stage_args(r, feats);
+    in.prompt_in = prompt_feats;
+    in.use_prompt = prompt_feats != nullptr;
+    in.zkeys = coords ? coords + 3 : nullptr;
+    in.zkey_stride = 4;
+    if (int e = launch_input_stage(in, r->cfg.precision == PMG_PREC_FP16, s)) return e;
+    return enqueue_blocks(r, nullptr, nullptr, delta_out, s);
+}
+
+// Runs `enqueue` on `s` through the refiner's graph cache: captured the first time a key is seen, replayed after.
+// The legacy default stream cannot be captured; on it (or with use_graph off) the work is enqueued eagerly.
+template <typename F>
+static int run_cached(pmg_refiner* r, const void* const (&key)[8], hipStream_t s, F&& enqueue) {
+    if (!r->cfg.use_graph || s == nullptr) return enqueue();
+    for (auto& g : r->graphs)
+        if (std::memcmp(g.key, key, sizeof key) == 0) {
+            PMG_CHECK_HIP(hipGraphLaunch(g.exec, s));
+            return PMG_OK;
+        }
+    if (r->graphs.size() >= kMaxGraphs) drop_graphs(r);
+    PMG_CHECK_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    const int e = enqueue();
+    hipGraph_t graph = nullptr;
+    const hipError_t ce = hipStreamEndCapture(s, &graph);
+    if (e) {
+        if (graph) hipGraphDestroy(graph);
+        return e;
+    }
+    if (ce != hipSuccess) return fail(PMG_E_HIP, std::string("hipStreamEndCapture: ") + hipGetErrorString(ce));
+    hipGraphExec_t exec = nullptr;
+    const hipError_t ie = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    if (ie != hipSuccess) {
+        hipGraphDestroy(graph);
+        return fail(PMG_E_HIP, std::string("hipGraphInstantiate: ") + hipGetErrorString(ie));
+    }
+    pmg_refiner::Graph g{};
+    std::memcpy(g.key, key, sizeof key);
+    g.graph = graph;
+    g.exec = exec;
+    r->graphs.push_back(g);
+    PMG_CHECK_HIP(hipGraphLaunch(exec, s));
     return PMG_OK;
 }
 
@@ -297,38 +383,18 @@ int pmg_refiner_step(pmg_refiner* r, const float* points, float* points_out, con
     PMG_REQUIRE(points && points_out, "null points");
     PMG_REQUIRE((!r->cfg.use_prompt && !r->cfg.final_fit) || (lidar && conf), "LiDAR inputs required");
     hipStream_t s = (hipStream_t)stream;
-    // The legacy default stream cannot be captured; on it the step is enqueued eagerly.
-    if (!r->cfg.use_graph || s == nullptr)
-        return enqueue_step(r, points, points_out, lidar, conf, st_prompt, st_final, s);
-    const void* key[7] = {points, points_out, lidar, conf, st_prompt, st_final, stream};
-    for (auto& g : r->graphs)
-        if (std::memcmp(g.key, key, sizeof key) == 0) {
-            PMG_CHECK_HIP(hipGraphLaunch(g.exec, s));
-            return PMG_OK;
-        }
-    if (r->graphs.size() >= kMaxGraphs) drop_graphs(r);
-    PMG_CHECK_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-    const int e = enqueue_step(r, points, points_out, lidar, conf, st_prompt, st_final, s);
-    hipGraph_t graph = nullptr;
-    const hipError_t ce = hipStreamEndCapture(s, &graph);
-    if (e) {
-        if (graph) hipGraphDestroy(graph);
-        return e;
-    }
-    if (ce != hipSuccess) return fail(PMG_E_HIP, std::string("hipStreamEndCapture: ") + hipGetErrorString(ce));
-    hipGraphExec_t exec = nullptr;
-    const hipError_t ie = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
-    if (ie != hipSuccess) {
-        hipGraphDestroy(graph);
-        return fail(PMG_E_HIP, std::string("hipGraphInstantiate: ") + hipGetErrorString(ie));
-    }
-    pmg_refiner::Graph g{};
-    std::memcpy(g.key, key, sizeof key);
-    g.graph = graph;
-    g.exec = exec;
-    r->graphs.push_back(g);
-    PMG_CHECK_HIP(hipGraphLaunch(exec, s));
-    return PMG_OK;
+    const void* const key[8] = {(const void*)1, points, points_out, lidar, conf, st_prompt, st_final, stream};
+    return run_cached(r, key, s, [&] { return enqueue_step(r, points, points_out, lidar, conf, st_prompt, st_final, s); });
+}
+
+int pmg_refiner_forward(pmg_refiner* r, const float* feats, const int32_t* coords, const float* prompt_feats,
+                        float* out, void* stream) {
+    PMG_REQUIRE(r && r->have_weights, "weights not set");
+    PMG_REQUIRE(feats && out, "null buffer");
+    PMG_REQUIRE(!prompt_feats || (r->w.pr_w && r->w.pr_b), "prompt_feats given but the refiner has no prompt_proj");
+    hipStream_t s = (hipStream_t)stream;
+    const void* const key[8] = {(const void*)2, feats, coords, prompt_feats, out, nullptr, nullptr, stream};
+    return run_cached(r, key, s, [&] { return enqueue_forward(r, feats, coords, prompt_feats, out, s); });
 }
 
 int pmg_refiner_check(pmg_refiner* r, void* stream) {

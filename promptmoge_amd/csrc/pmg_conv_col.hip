@@ -181,10 +181,14 @@ __device__ inline void col_epilogue(const ColConvArgs& a, const typename ColAcc<
                 for (int i = 0; i < 4; ++i) p = p + k.ow[16 * j + 4 * g + i] * y[j][i];
             const float d = a.out_b[0] + quad_sum(p);
             if (ok && g == 0) {
-                const float p0 = a.points[mo * 3 + 0], p1 = a.points[mo * 3 + 1], p2 = a.points[mo * 3 + 2];
-                a.points_out[mo * 3 + 0] = p0;
-                a.points_out[mo * 3 + 1] = p1;
-                a.points_out[mo * 3 + 2] = p2 + d;
+                if (a.points) {  // _refine_logz: logz + out (v3.py:359)
+                    const float p0 = a.points[mo * 3 + 0], p1 = a.points[mo * 3 + 1], p2 = a.points[mo * 3 + 2];
+                    a.points_out[mo * 3 + 0] = p0;
+                    a.points_out[mo * 3 + 1] = p1;
+                    a.points_out[mo * 3 + 2] = p2 + d;
+                } else {  // the refiner module's own output, (M, 1) (sparse_unet.py:258)
+                    ((float*)a.out)[mo] = d;
+                }
             }
         }
     }
@@ -739,8 +743,8 @@ extern "C" int pmg_spconv_col(int precision, const void* x, const int32_t* zq, i
     PMG_REQUIRE(epilogue == PMG_EPI_ROUT || aligned16(e->out), "out must be 16-byte aligned");
     PMG_REQUIRE(epilogue != PMG_EPI_RLN || (e->ln_gamma && e->ln_beta && e->next_q && (!i8 || e->next_mult > 0.0f)),
                 "RLN needs LayerNorm parameters and next_q");
-    PMG_REQUIRE(epilogue != PMG_EPI_ROUT || (e->out_w && e->out_b && e->points && e->points_out),
-                "ROUT needs out_proj weights and the point maps");
+    PMG_REQUIRE(epilogue != PMG_EPI_ROUT || (e->out_w && e->out_b && ((e->points && e->points_out) || e->out)),
+                "ROUT needs out_proj weights and either the point maps or out");
     ColConvArgs a{};
     a.x = x;
     a.zq = zq;

@@ -30,6 +30,9 @@ struct InputStage {
     void* q_out;
     float resolution;
     int32_t* zq_out;
+    const float* prompt_in;  // [M][2] given prompt features, or NULL (computed from the LiDAR when use_prompt)
+    const int32_t* zkeys;    // given z keys (coords[:, 3]) with element stride zkey_stride, or NULL
+    int64_t zkey_stride;
 };
 int launch_input_stage(const InputStage& in, bool f16, hipStream_t s);
 

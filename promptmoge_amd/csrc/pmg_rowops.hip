@@ -78,6 +78,9 @@ struct InputArgs {
     void* q_out;        // int8 or fp16 [M][C]
     float resolution;   // voxel keys: zq = rint(logz * resolution) (v3.py:332)
     int32_t* zq_out;    // [M] or NULL
+    const float* prompt_in;  // [M][2] given prompt features (residual, gate), or NULL: computed from the LiDAR
+    const int32_t* zkeys;    // given voxel z keys (coords[:, 3], element stride zkey_stride), or NULL
+    int64_t zkey_stride;
 };
 
 __device__ inline void prompt_feats(const InputArgs& a, int b, int i, int j, float logz, float& res, float& gate) {
@@ -108,9 +111,13 @@ __global__ __launch_bounds__(256) void input_stage_k(InputArgs a) {
     const bool ok = m < M;
     const int64_t mo = ok ? m : 0;
     const float f0 = a.points[mo * 3 + 0], f1 = a.points[mo * 3 + 1], f2 = a.points[mo * 3 + 2];
-    if (ok && g == 0 && a.zq_out) a.zq_out[mo] = (int32_t)rne(f2 * a.resolution);
+    if (ok && g == 0 && a.zq_out)
+        a.zq_out[mo] = a.zkeys ? a.zkeys[mo * a.zkey_stride] : (int32_t)rne(f2 * a.resolution);
     float res = 0.0f, gate = 0.0f;
-    if (a.use_prompt) {
+    if (a.prompt_in) {  // Sparse3DUNet.forward's prompt_feats (sparse_unet.py:191-193)
+        res = a.prompt_in[mo * 2];
+        gate = a.prompt_in[mo * 2 + 1];
+    } else if (a.use_prompt) {
         const int64_t HW = (int64_t)a.H * a.W;
         const int b = (int)(mo / HW);
         const int p = (int)(mo - b * HW);
@@ -181,7 +188,7 @@ int launch_ln_silu(const float* x, int64_t M, int C, const float* gamma, const f
 int launch_input_stage(const InputStage& in, bool f16, hipStream_t s) {
     InputArgs a{in.points, in.B, in.H, in.W, in.lidar, in.conf, in.dh, in.dw, in.st, in.use_prompt, in.soft_gate,
                 in.in_w, in.in_b, in.pr_w, in.pr_b, in.x_out, in.gamma, in.beta, in.eps, in.out_mult, in.q_out,
-                in.resolution, in.zq_out};
+                in.resolution, in.zq_out, in.prompt_in, in.zkeys, in.zkey_stride};
     const int64_t M = (int64_t)in.B * in.H * in.W;
     const dim3 g((unsigned)((M + 63) / 64));
     if (f16) {

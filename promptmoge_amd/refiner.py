@@ -8,6 +8,9 @@ refine loop (moge/model/v3.py:547-576) with no host synchronisation:
 
 The refined point map (x/z, y/z, logz + delta) is written to `out`, which may be the input itself; that is the
 reference loop's `current_coord = cat(xy, refined_logz)` (v3.py:574).
+
+`FusedRefiner` is the refiner module alone, an nn.Module with Sparse3DUNet.forward's signature (the refiner-module
+plug point, v3.py:356-357); it runs input_proj -> blocks -> out_proj on given voxel features and returns (M, 1).
 """
 from __future__ import annotations
 
@@ -146,3 +149,92 @@ def _copy_device(dst: int, src: int, nbytes: int, stream: int) -> None:
     rc = hip.hipMemcpyAsync(C.c_void_p(dst), C.c_void_p(src), C.c_size_t(nbytes), 3, C.c_void_p(stream))
     if rc != 0:
         raise RuntimeError(f"hipMemcpyAsync failed with {rc}")
+
+
+class FusedRefiner(torch.nn.Module):
+    """The refiner module on the GPU, behind Sparse3DUNet.forward's signature (moge/model/modules/sparse_unet.py:
+    176-258): `forward(feats, coords, shape, encoder_feature, prompt_feats=None, encoder_bias_map=None) -> (M, 1)`,
+    what `_refine_logz` calls at v3.py:356-357 (`model.refiner = FusedRefiner(...)`, or `refiner=` there).
+
+    The network is the single-level refiner: input_proj (3 -> C) + prompt_proj (2 -> C) of the given prompt
+    features, n_blocks SparseResBlock3d(C) (flex_sparse_blocks.py:50-75) in the deployed int8 contract (or the fp16
+    teacher), out_proj (C -> 1). The voxels must be level 0 as _voxelize builds them (v3.py:305-344): one per
+    pixel in raster (b, i, j) order, so the neighbour map is the column stencil on coords[:, 3] and is never
+    materialised. `encoder_feature` and `encoder_bias_map` feed the multi-level U-Net's bottleneck fusion, which
+    a single-level refiner does not have; they are accepted and not read. Inference only.
+    """
+
+    def __init__(self, weights: RefinerW, *, precision: str = "int8", depth_resolution: float = 256.0,
+                 use_graph: bool = True, check_coords: bool = True):
+        super().__init__()
+        if precision not in ("int8", "fp16"):
+            raise ValueError("precision must be 'int8' or 'fp16'")
+        self.host_weights = weights
+        self.precision = precision
+        self.depth_resolution = float(depth_resolution)
+        self.use_graph = use_graph
+        self.check_coords = check_coords
+        self._weights = {}   # device -> DeviceWeights
+        self._ctx = {}       # (device, B, H, W) -> refiner handle
+
+    def _handle(self, device: torch.device, B: int, H: int, W: int):
+        key = (device.index, B, H, W)
+        h = self._ctx.get(key)
+        if h is None:
+            dw = self._weights.get(device.index)
+            if dw is None:
+                dw = self._weights[device.index] = DeviceWeights(self.host_weights, self.precision, device)
+            w = self.host_weights
+            cfg = RefinerConfig(B, H, W, w.C, len(w.blocks),
+                                _lib.PREC_INT8 if self.precision == "int8" else _lib.PREC_FP16,
+                                self.depth_resolution, H, W, 0, 0.2, 32, 1, 0, 0, int(self.use_graph))
+            h = lib().pmg_refiner_create(C.byref(cfg))
+            if not h:
+                raise _lib.PmgError(_lib.PMG_E_INVALID, lib().pmg_last_error().decode())
+            call("pmg_refiner_set_weights", h, C.byref(dw.struct))
+            self._ctx[key] = h
+        return h
+
+    def forward(self, feats: torch.Tensor, coords: Optional[torch.Tensor], shape, encoder_feature=None,
+                prompt_feats: Optional[torch.Tensor] = None, encoder_bias_map=None) -> torch.Tensor:
+        if torch.is_grad_enabled() and feats.requires_grad:
+            raise NotImplementedError("FusedRefiner is inference-only")
+        B, H, W = int(shape[0]), int(shape[1]), int(shape[2])
+        M = B * H * W
+        if feats.shape != (M, 3) or not feats.is_cuda:
+            raise ValueError(f"feats must be a GPU tensor (M, 3) with M = B*H*W = {M} (level-0 voxels)")
+        feats = feats.float().contiguous()
+        if coords is not None:
+            coords = coords.to(torch.int32).contiguous()
+            if coords.shape != (M, 4):
+                raise ValueError("coords must be (M, 4)")
+            if self.check_coords and not _is_raster(coords, B, H, W):
+                raise ValueError("coords are not level-0 raster order (one voxel per pixel, _voxelize)")
+        if prompt_feats is not None:
+            prompt_feats = prompt_feats.float().contiguous()
+            if prompt_feats.shape != (M, 2):
+                raise ValueError("prompt_feats must be (M, 2)")
+        out = torch.empty((M, 1), dtype=torch.float32, device=feats.device)
+        h = self._handle(feats.device, B, H, W)
+        p = lambda t: None if t is None else t.data_ptr()
+        call("pmg_refiner_forward", h, feats.data_ptr(), p(coords), p(prompt_feats), out.data_ptr(),
+             C.c_void_p(torch.cuda.current_stream().cuda_stream))
+        return out
+
+    def close(self) -> None:
+        for h in self._ctx.values():
+            lib().pmg_refiner_destroy(h)
+        self._ctx.clear()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # interpreter shutdown: the library handle may already be gone
+            pass
+
+
+def _is_raster(coords: torch.Tensor, B: int, H: int, W: int) -> bool:
+    """coords[:, :3] == (b, i, j) in raster order, the test of _is_one_voxel_per_column (_core.py:249-266)."""
+    m = torch.arange(B * H * W, device=coords.device, dtype=torch.int32)
+    ref = torch.stack([m // (H * W), (m // W) % H, m % W], dim=1)
+    return bool(torch.equal(coords[:, :3], ref))

@@ -244,6 +244,52 @@ class RefinerW:
     blocks: List[BlockW]
 
 
+
+def weights_from_state_dict(sd, stages=("down_stages.0", "bottleneck_stage"), clips=None) -> RefinerW:
+    """A single-level refiner's weights from a Sparse3DUNet state dict (sparse_unet.py:176-258), in the names the
+    reference's modules give them: input_proj / prompt_proj / out_proj (nn.Linear), and per SparseResBlock3d
+    (flex_sparse_blocks.py:50-75) under each stage prefix `<stage>.<k>.`: norm1, conv1, conv2 (weights
+    (Co, 3, 3, 3, Ci), nn/__init__.py:30). QAT-wrapped weights are read from `.parametrizations.weight.original`
+    (torch.nn.utils.parametrize, qat.py:111); activation clips from the quantisers' `aq_<module_path>.clip`
+    buffers (qat.py:76, 112-115), or from `clips` = {module path: clip}. Tensors may be torch tensors or arrays."""
+    f32 = lambda t: np.asarray(t.detach().cpu().float().numpy() if hasattr(t, "detach") else t, dtype=np.float32)
+
+    def get(name: str):
+        if name in sd:
+            return f32(sd[name])
+        base, _, leaf = name.rpartition(".")
+        alt = f"{base}.parametrizations.{leaf}.original"
+        if alt in sd:
+            return f32(sd[alt])
+        raise KeyError(name)
+
+    def clip(path: str) -> float:
+        if clips is not None and path in clips:
+            return float(clips[path])
+        key = "aq_" + path.replace(".", "_") + ".clip"
+        if key in sd:
+            return float(f32(sd[key]))
+        return 1.0
+
+    in_w, in_b = get("input_proj.weight"), get("input_proj.bias")
+    C = in_w.shape[0]
+    if "prompt_proj.weight" in sd or "prompt_proj.parametrizations.weight.original" in sd:
+        pr_w, pr_b = get("prompt_proj.weight"), get("prompt_proj.bias")
+    else:
+        pr_w, pr_b = np.zeros((C, 2), np.float32), np.zeros((C,), np.float32)
+    blocks = []
+    for stage in stages:
+        k = 0
+        while f"{stage}.{k}.norm1.weight" in sd:
+            p = f"{stage}.{k}"
+            blocks.append(BlockW(get(f"{p}.norm1.weight"), get(f"{p}.norm1.bias"), get(f"{p}.conv1.weight"),
+                                 get(f"{p}.conv1.bias"), get(f"{p}.conv2.weight"), get(f"{p}.conv2.bias"),
+                                 clip(f"{p}.conv1"), clip(f"{p}.conv2")))
+            k += 1
+    if not blocks:
+        raise ValueError(f"no SparseResBlock3d found under {stages}")
+    return RefinerW(C, in_w, in_b, pr_w, pr_b, get("out_proj.weight").reshape(1, C), get("out_proj.bias"), blocks)
+
 def _f16(x: np.ndarray) -> np.ndarray:
     return x.astype(np.float16).astype(np.float32)
 

@@ -120,3 +120,45 @@ def test_step_multi_step_k3(gpu):
         got = P.cpu().numpy()
     d, dr = np.exp(got[..., 2].astype(np.float64)), np.exp(ref[..., 2].astype(np.float64))
     assert (np.abs(d - dr) / dr).max() < 1e-3
+
+
+@pytest.mark.parametrize("precision", ["int8", "fp16"])
+def test_module_forward(gpu, precision):
+    """FusedRefiner behind Sparse3DUNet.forward's signature (sparse_unet.py:176-258): (M, 1) deltas for given voxel
+    features, level-0 coords and prompt features; int8 bit-exact against the oracle, fp16 within 1e-3 (log depth)."""
+    from promptmoge_amd.refiner import FusedRefiner
+    from oracle import structure as ost
+
+    announce(f"module forward {precision}")
+    cfg = spec.CONFIGS["B"] if precision == "int8" else spec.StepConfig("t", 96, 128, 100.0, 100.0, 64.0, 48.0, 64,
+                                                                         3, "fp16", seed=13)
+    sc = spec.make_scene(cfg)
+    w = spec.refiner_for(cfg, sc)
+    B, H, W = 2, cfg.H, cfg.W
+    pts = np.stack([sc.points, sc.points * np.float32(1.02)])
+    zq, coords, zext, _ = ost.voxelize(pts)
+    M = B * H * W
+    rng = np.random.default_rng(1)
+    pf = np.stack([rng.normal(0, 0.05, M), rng.uniform(0, 1, M)], 1).astype(np.float32)
+    feats = pts.reshape(M, 3)
+    dev = torch.device("cuda:0")
+    mod = FusedRefiner(w, precision=precision)
+    shape = torch.Size([B, H, W, int(zext), 3])
+    tf, tc, tp = (torch.from_numpy(a).to(dev) for a in (feats, coords, pf))
+    out = mod(tf, tc, shape, None, prompt_feats=tp)
+    out_nc = mod(tf, None, shape, None, prompt_feats=tp)     # keys from feats[:, 2]: same map
+    out_np = mod(tf, tc, shape, None)                         # no prompt_proj
+    again = mod(tf, tc, shape, None, prompt_feats=tp)         # graph replay
+    torch.cuda.synchronize()
+    ref = orf.forward(feats, zq, H, W, w, pf, precision=precision)
+    ref_np = orf.forward(feats, zq, H, W, w, None, precision=precision)
+    got, got_np = out.cpu().numpy()[:, 0], out_np.cpu().numpy()[:, 0]
+    assert out.shape == (M, 1)
+    assert np.array_equal(out.cpu().numpy(), out_nc.cpu().numpy())
+    assert np.array_equal(out.cpu().numpy(), again.cpu().numpy())
+    if precision == "int8":
+        assert np.array_equal(got, ref) and np.array_equal(got_np, ref_np)
+    else:
+        assert np.abs(got - ref).max() < 1e-3 and np.abs(got_np - ref_np).max() < 1e-3
+    with pytest.raises(ValueError):
+        mod(tf, torch.flip(tc, [0]).contiguous(), shape, None)    # not raster order

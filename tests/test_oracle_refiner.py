@@ -56,3 +56,30 @@ def test_fp16_step_matches_fp32_reference():
     ref = sc.points[..., 2] + (x @ w32.out_w.reshape(-1) + w32.out_b[0]).reshape(H, W)
     rel = np.abs(np.exp(pts[0, ..., 2].astype(np.float64)) - np.exp(ref.astype(np.float64))) / np.exp(ref)
     assert rel.max() < 1e-3, rel.max()
+
+
+def test_weights_from_reference_state_dict():
+    """spec.weights_from_state_dict reads the reference module's parameter names (plain and QAT-parametrised)."""
+    import torch
+    from promptmoge_amd import spec
+
+    w = spec.make_weights(32, 2, seed=3)
+    sd = {"input_proj.weight": torch.from_numpy(w.in_w), "input_proj.bias": torch.from_numpy(w.in_b),
+          "prompt_proj.weight": torch.from_numpy(w.pr_w), "prompt_proj.bias": torch.from_numpy(w.pr_b),
+          "out_proj.parametrizations.weight.original": torch.from_numpy(w.out_w),
+          "out_proj.bias": torch.from_numpy(w.out_b)}
+    for k, b in enumerate(w.blocks):
+        stage, idx = ("down_stages.0", k) if k == 0 else ("bottleneck_stage", k - 1)
+        p = f"{stage}.{idx}"
+        sd.update({f"{p}.norm1.weight": b.gamma, f"{p}.norm1.bias": b.beta,
+                   f"{p}.conv1.parametrizations.weight.original": torch.from_numpy(b.w1), f"{p}.conv1.bias": b.b1,
+                   f"{p}.conv2.weight": b.w2, f"{p}.conv2.bias": b.b2,
+                   "aq_" + p.replace(".", "_") + "_conv1.clip": torch.tensor(b.clip1),
+                   "aq_" + p.replace(".", "_") + "_conv2.clip": torch.tensor(b.clip2)})
+    got = spec.weights_from_state_dict(sd)
+    assert got.C == 32 and len(got.blocks) == 2
+    for a, b in zip(got.blocks, w.blocks):
+        for f in ("gamma", "beta", "w1", "b1", "w2", "b2"):
+            assert np.array_equal(getattr(a, f), getattr(b, f)), f
+        assert a.clip1 == pytest.approx(b.clip1) and a.clip2 == pytest.approx(b.clip2)
+    assert np.array_equal(got.out_w, w.out_w) and np.array_equal(got.in_w, w.in_w)
