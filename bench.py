@@ -237,6 +237,63 @@ def microbench(stream):
     return micro
 
 
+def frame_bench(name, stream, reps=10):
+    """One frame of a K-step configuration: K refine steps (each with its prompt fit, voxel keys and stencil
+    rebuilt, v3.py:537-578) and the final metric fit after the last one. H also times the GPU nearest_fill of its
+    LiDAR prompt with 20 % holes (model.py:61-72)."""
+    import numpy as np
+    import torch
+
+    from promptmoge_amd import ops, spec
+    from promptmoge_amd.refiner import RefinerStep
+
+    dev = torch.device("cuda:0")
+    cfg = spec.CONFIGS[name]
+    sc = spec.make_scene(cfg)
+    w = spec.refiner_for(cfg, sc)
+    K = cfg.steps
+    out = {"workload": f"{cfg.name}: {cfg.H}x{cfg.W} {cfg.precision} refiner, K={K} steps + final fit, C={cfg.C}, "
+                       f"{2 * cfg.n_blocks} conv layers, fit iters {cfg.fit_iters}", "voxels_per_step": cfg.M}
+    with torch.cuda.stream(stream):
+        P0 = torch.from_numpy(sc.points[None].copy()).to(dev)
+        bufs = [torch.empty_like(P0), torch.empty_like(P0)]
+        L = torch.from_numpy(sc.lidar[None].copy()).to(dev)
+        Cf = torch.from_numpy(sc.conf[None].copy()).to(dev)
+        mid = RefinerStep(w, 1, cfg.H, cfg.W, precision=cfg.precision, fit_iters=cfg.fit_iters)
+        last = RefinerStep(w, 1, cfg.H, cfg.W, precision=cfg.precision, fit_iters=cfg.fit_iters, final_fit=True)
+
+        def frame():
+            src = P0
+            for k in range(K):
+                dst = bufs[k % 2]
+                (last if k == K - 1 else mid)(src, L, Cf, out=dst)
+                src = dst
+
+        for _ in range(3):
+            frame()
+        mid.check()
+        last.check()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            frame()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        fms = e0.elapsed_time(e1) / reps
+        mid.check()
+        last.check()
+        out.update(ms_per_frame=round(fms, 4), ms_per_step=round(fms / K, 4),
+                   voxels_per_s=round(K * cfg.M / (fms * 1e-3), 1))
+        if cfg.holes > 0:
+            rng = np.random.default_rng(cfg.seed + 7)
+            raw = np.where(rng.random(sc.lidar.shape) < cfg.holes, 0.0, sc.lidar).astype(np.float32)
+            Lr = torch.from_numpy(raw[None]).to(dev)
+            Cr = Cf.clone()
+            out["nearest_fill_ms"] = round(graph_ms(lambda: ops.nearest_fill(Lr, Cr), 20, stream), 4)
+    return out
+
+
 def cpu_baseline(env):
     from oracle import refiner as orf
 
@@ -269,6 +326,7 @@ def main() -> int:
     ap.add_argument("--config", default="A", choices=["A", "B", "H"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-micro", action="store_true", help="skip the 1M-voxel conv microbench")
+    ap.add_argument("--no-others", action="store_true", help="skip the K-step T and H frame timings")
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--kernels-only", action="store_true")
     ap.add_argument("--write-traffic", nargs=3, metavar=("OUT", "FETCH_DIR", "WRITE_DIR"))
@@ -336,6 +394,7 @@ def main() -> int:
                 "minimal_bytes": int(minimal[dominant]), "avg_launch_ms": round(kern[dominant], 5)}
 
     micro = None if args.no_micro else microbench(stream)
+    others = None if args.no_others else {n: frame_bench(n, stream) for n in ("T", "H")}
     cpu = None if args.no_cpu else cpu_baseline(env)
 
     line = {
@@ -347,7 +406,7 @@ def main() -> int:
                    "voxels": M, "parallelism": "1 GPU"},
         "final_fit_ms": round(ms_with_final - ms, 5), "step_with_final_fit_ms": round(ms_with_final, 5),
         "wall_s_timed": round(wall, 3),
-        "roofline": roofline, "cpu_baseline": cpu, "conv_microbench": micro,
+        "roofline": roofline, "cpu_baseline": cpu, "conv_microbench": micro, "other_configs": others,
         "kernel_ms": {k: round(v, 5) for k, v in kern.items()},
         "per_step_ms": {k: round(v, 5) for k, v in per_step.items()},
         "kernel_gbs_contract": {k: round(contract[k] / (kern[k] * 1e-3) / 1e9, 1) for k in kern},
