@@ -72,9 +72,10 @@ int pmg_nmap_column(const int32_t* zq, const int32_t* zmin, int B, int H, int W,
                     int32_t* nmap_rows, uint32_t* tile_mask, int32_t* coords, void* stream);
 
 /* pmg_nmap_hash -- generic coordinates, replaces _SortedIndex + _build_submanifold_nmap_sorted
- * (_core.py:105-124, 298-304) with an open-addressing GPU hash over the linearised keys of _linearise
- * (_core.py:89-94). coords: [M][4] int32 (b, x, y, z), unique, inside sparse_shape (host array of 4 int64).
- * Same outputs as pmg_nmap_column (coords excluded). The workspace holds the table (load factor <= 1/4). */
+ * (_core.py:105-124, 298-304) with an open-addressing GPU hash of 4x4x4 bricks keyed by _linearise
+ * (_core.py:89-94) on the brick grid. coords: [M][4] int32 (b, x, y, z), unique, inside sparse_shape (host array
+ * of 4 int64); M < 2^30. Same outputs as pmg_nmap_column (coords excluded). The workspace (any contents) holds
+ * the table: 8 + 256 bytes per bucket, buckets = a power of two >= 1.5 M. */
 size_t pmg_hash_workspace_bytes(int64_t M);
 int pmg_nmap_hash(const int32_t* coords, int64_t M, const int64_t* sparse_shape_host, int32_t* nmap_t,
                   int32_t* nmap_rows, uint32_t* tile_mask, void* workspace, size_t workspace_bytes, void* stream);

@@ -4,7 +4,7 @@
 // 27-neighbour map is a 3x3 image stencil plus a depth predicate (_core.py:269-295): one thread per voxel reads
 // nine z values and writes its 27 map entries, coalesced across the wave in the tap-major layout the
 // convolutions read. Generic coordinates (the 1M-voxel microbench, levels >= 1) go through an open-addressing
-// hash over the reference's linearised keys (_core.py:89-94) with 64-bit compare-and-swap insertion.
+// hash of 4x4x4 bricks keyed by the reference's linearisation (_core.py:89-94) on the brick grid.
 //
 // Every map kernel also emits the per-16-row tile tap mask the convolutions branch on: bit v set iff any row of
 // the tile has tap v. It is reduced across each 16-lane group with shuffles and stored by the group's first lane,
@@ -115,87 +115,257 @@ __global__ __launch_bounds__(256) void nmap_column_k(const int32_t* __restrict__
 }
 
 // ------------------------------------------------------------------------------------------------------------
-// Open-addressing hash over linearised keys. Keys are 64-bit, EMPTY = all ones (a linearised in-bounds key is
-// never negative). Linear probing; the table has at least 4x as many slots as keys. Duplicate coordinates keep
-// the smallest row index (atomicMin), which makes the map independent of insertion order.
+// Generic coordinates: an open-addressing hash of 4x4x4 bricks. A bucket is one brick of the sparse grid: a
+// key and 64 row indices, one per cell. The 27 neighbours of a voxel
+// fall in at most 2x2x2 bricks (one per axis unless the voxel sits on a brick face), so a query resolves <= 8
+// buckets with independent loads and then reads its 27 cells from them; neighbouring voxels share those buckets,
+// which keeps the query's traffic in L1/L2 instead of one random 128-byte line per tap. Keys are the linearised
+// brick coordinates (the reference's _linearise, _core.py:89-94, on the brick grid); EMPTY = all ones. Cells
+// hold -1 until a voxel writes its row index. Coordinates must be unique, as in a sparse tensor; for a duplicated
+// coordinate the map names one of its rows.
 constexpr uint64_t kEmpty = ~0ull;
+constexpr int kBrickLog = 2;  // 4 cells per axis
 
-__device__ inline uint64_t mix64(uint64_t k) {
-    k ^= k >> 33;
-    k *= 0xff51afd7ed558ccdull;
-    k ^= k >> 33;
-    k *= 0xc4ceb9fe1a85ec53ull;
-    k ^= k >> 33;
-    return k;
+// Home bucket of a brick key: the key folded to 32 bits, Fibonacci-hashed (one 32-bit multiply; consecutive
+// bricks land far apart), top bits taken. cap = 2^cap_log2 buckets.
+__device__ inline uint64_t brick_home(uint64_t k, int cap_log2) {
+    const uint32_t f = (uint32_t)k ^ (uint32_t)(k >> 32) * 0x85ebca6bu;
+    return (uint64_t)((f * 0x9e3779b1u) >> (32 - cap_log2));
 }
 
 struct Shape4 {
     int64_t s0, s1, s2, s3;
 };
 
-// _linearise (_core.py:89-94): ((b*S1 + x)*S2 + y)*S3 + z.
-__device__ inline int64_t linearise(int b, int x, int y, int z, const Shape4& S) {
-    return (((int64_t)b * S.s1 + x) * S.s2 + y) * S.s3 + z;
+struct BrickTable {
+    uint64_t* head;  // [cap] brick key of each bucket
+    int32_t* vals;   // [cap][64] row index of each cell, -1 if empty
+    uint64_t cap_mask;
+    int cap_log2;
+    Shape4 S;   // sparse shape (b, x, y, z)
+    Shape4 Sb;  // brick grid: (b, ceil(x/4), ceil(y/4), ceil(z/4))
+};
+
+__device__ inline uint64_t brick_key(int b, int bx, int by, int bz, const Shape4& Sb) {
+    return (((uint64_t)b * Sb.s1 + bx) * Sb.s2 + by) * Sb.s3 + bz;
 }
 
-__global__ __launch_bounds__(256) void hash_clear_k(uint64_t* keys, int32_t* vals, int64_t cap) {
+__device__ inline int brick_cell(int x, int y, int z) { return ((x & 3) << 4) | ((y & 3) << 2) | (z & 3); }
+
+__device__ inline bool in_shape(int b, int x, int y, int z, const Shape4& S) {
+    return b >= 0 && b < S.s0 && x >= 0 && x < S.s1 && y >= 0 && y < S.s2 && z >= 0 && z < S.s3;
+}
+
+// Workgroups are dispatched round-robin over the 8 XCDs (block b runs on XCD b mod 8). Remapping block b to chunk
+// xcd_chunk(b) gives each XCD one contiguous range of chunks, so voxels that share buckets also share an L2.
+__device__ inline int64_t xcd_chunk(int64_t b, int64_t n) {
+    const int64_t x = b & 7, j = b >> 3, q = n >> 3, r = n & 7;
+    return x < r ? x * (q + 1) + j : r * (q + 1) + (x - r) * q + j;
+}
+
+__global__ __launch_bounds__(256) void brick_clear_k(uint64_t* head, int64_t cap) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i < cap) {
-        keys[i] = kEmpty;
-        vals[i] = INT_MAX;
-    }
+    if (i < cap) head[i] = kEmpty;
 }
 
-__global__ __launch_bounds__(256) void hash_insert_k(const int4* __restrict__ coords, int64_t M, Shape4 S,
-                                                     uint64_t* keys, int32_t* vals, uint64_t cap_mask) {
-    const int64_t m = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (m >= M) return;
-    const int4 c = coords[m];
-    const uint64_t key = (uint64_t)linearise(c.x, c.y, c.z, c.w, S);
-    uint64_t slot = mix64(key) & cap_mask;
-    for (uint64_t probe = 0; probe <= cap_mask; ++probe) {
-        const uint64_t prev = atomicCAS((unsigned long long*)&keys[slot], (unsigned long long)kEmpty,
-                                        (unsigned long long)key);
-        if (prev == kEmpty || prev == key) {
-            atomicMin(&vals[slot], (int)m);
-            return;
+// Finds or claims the bucket of brick key `bk`; `fresh` tells whether this call claimed it (its cells are then
+// still to be emptied). Keys only ever change from EMPTY to a brick, so a plain (possibly stale) read that shows a
+// key is final, and a stale EMPTY only costs a compare-and-swap that then reports the key. The table has more
+// buckets than there can be bricks, so the probe ends within cap steps.
+__device__ inline uint32_t brick_claim(const BrickTable& T, uint64_t bk, bool& fresh) {
+    uint64_t slot = brick_home(bk, T.cap_log2);
+    fresh = false;
+    for (uint64_t probe = 0; probe <= T.cap_mask; ++probe) {
+        const uint64_t t = T.head[slot];
+        if (t == bk) return (uint32_t)slot;
+        if (t == kEmpty) {
+            const unsigned long long prev =
+                atomicCAS((unsigned long long*)&T.head[slot], (unsigned long long)kEmpty, (unsigned long long)bk);
+            if (prev == kEmpty) {
+                fresh = true;
+                return (uint32_t)slot;
+            }
+            if (prev == bk) return (uint32_t)slot;
         }
-        slot = (slot + 1) & cap_mask;
+        slot = (slot + 1) & T.cap_mask;
     }
+    return 0xffffffffu;  // unreachable: the table never fills
 }
 
-__device__ inline int hash_lookup(const uint64_t* __restrict__ keys, const int32_t* __restrict__ vals,
-                                  uint64_t cap_mask, uint64_t key) {
-    uint64_t slot = mix64(key) & cap_mask;
-    for (uint64_t probe = 0; probe <= cap_mask; ++probe) {
-        const uint64_t k = keys[slot];
-        if (k == key) return vals[slot];
-        if (k == kEmpty) return -1;
-        slot = (slot + 1) & cap_mask;
+__device__ inline uint64_t shfl_up_u64(uint64_t v, int off) {
+    const uint32_t lo = (uint32_t)__shfl_up((int)(uint32_t)v, off, 64);
+    const uint32_t hi = (uint32_t)__shfl_up((int)(uint32_t)(v >> 32), off, 64);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// Lane index of the first lane of this lane's run: runs are maximal spans of consecutive lanes with head == false
+// after a head lane (a max-scan of the head lanes' indices).
+__device__ inline int run_start(bool head, int lane) {
+    int h = head ? lane : 0;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int t = __shfl_up(h, off, 64);
+        if (lane >= off) h = t > h ? t : h;
+    }
+    return h;
+}
+
+// Insertion, pass 1: every brick that holds a voxel gets a bucket with empty cells. Consecutive lanes of a wave in
+// the same brick form a run; the run's first lane claims (all runs in parallel; two runs of one brick find the
+// same bucket) and the run takes its slot. slot_of[m] = the voxel's bucket.
+__global__ __launch_bounds__(256) void brick_claim_k(const int4* __restrict__ coords, int64_t M, BrickTable T,
+                                                     uint32_t* __restrict__ slot_of) {
+    const int64_t m = xcd_chunk(blockIdx.x, gridDim.x) * 256 + threadIdx.x;
+    const int lane = threadIdx.x & 63;
+    bool valid = false;
+    uint64_t bk = 0;
+    if (m < M) {
+        const int4 c = coords[m];
+        valid = in_shape(c.x, c.y, c.z, c.w, T.S);
+        if (valid) bk = brick_key(c.x, c.y >> kBrickLog, c.z >> kBrickLog, c.w >> kBrickLog, T.Sb);
+    }
+    const bool prev_valid = __shfl_up((int)valid, 1, 64) != 0;
+    const uint64_t prev_bk = shfl_up_u64(bk, 1);
+    const bool head = valid && (lane == 0 || !prev_valid || prev_bk != bk);
+    uint32_t slot = 0xffffffffu;
+    bool fresh = false;
+    if (head) slot = brick_claim(T, bk, fresh);
+    // the wave empties the cells of the buckets it claimed, one coalesced 256-byte store per bucket
+    uint64_t todo = __ballot(fresh);
+    while (todo) {
+        const int l = __builtin_ctzll(todo);
+        const uint32_t fs = (uint32_t)__builtin_amdgcn_readlane((int)slot, l);
+        T.vals[(uint64_t)fs * 64 + lane] = -1;
+        todo &= todo - 1;
+    }
+    slot = (uint32_t)__shfl((int)slot, run_start(head, lane), 64);
+    if (m < M) slot_of[m] = valid ? slot : 0xffffffffu;
+}
+
+// Insertion, pass 2 (every bucket claimed and emptied): each voxel writes its row index into its cell.
+__global__ __launch_bounds__(256) void brick_store_k(const int4* __restrict__ coords, int64_t M, BrickTable T,
+                                                     const uint32_t* __restrict__ slot_of) {
+    const int64_t m = xcd_chunk(blockIdx.x, gridDim.x) * 256 + threadIdx.x;
+    if (m >= M) return;
+    const uint32_t slot = slot_of[m];
+    if (slot == 0xffffffffu) return;
+    const int4 c = coords[m];
+    T.vals[(uint64_t)slot * 64 + brick_cell(c.y, c.z, c.w)] = (int32_t)m;
+}
+
+// The bucket of brick key bk, or -1 if the brick holds no voxel; `first` is the key read at the home slot.
+__device__ inline int32_t brick_probe(const BrickTable& T, uint64_t bk, uint64_t home, uint64_t first) {
+    uint64_t slot = home;
+    uint64_t h = first;
+    for (uint64_t probe = 0; probe <= T.cap_mask; ++probe) {
+        if (h == bk) return (int32_t)slot;
+        if (h == kEmpty) break;
+        slot = (slot + 1) & T.cap_mask;
+        h = T.head[slot];
     }
     return -1;
 }
 
-// _SortedIndex.lookup (_core.py:114-124): out-of-bounds queries never hit.
-__global__ __launch_bounds__(256) void hash_query_k(const int4* __restrict__ coords, int64_t M, Shape4 S,
-                                                    const uint64_t* __restrict__ keys,
-                                                    const int32_t* __restrict__ vals, uint64_t cap_mask,
-                                                    int32_t* __restrict__ nmap_t, int32_t* __restrict__ nmap_rows,
-                                                    uint32_t* tile_mask) {
-    const int64_t m = (int64_t)blockIdx.x * 256 + threadIdx.x;
+// Query: the 27 neighbours of every voxel (_SortedIndex.lookup semantics, _core.py:114-124: out-of-bounds
+// neighbours never hit). Per axis the offsets -1, 0, +1 stay in the voxel's own brick except on a brick face,
+// where one of them enters the next brick in direction e = -1 or +1; bucket k = (kx, ky, kz) is the brick with
+// the extra step on the axes whose bit is set. The <= 8 buckets are resolved first (every home-slot header loaded
+// before any is compared), then each tap picks its bucket through a mux tree shared across taps (x, then y,
+// then z) and all 27 cell loads are issued together.
+__global__ __launch_bounds__(256) void brick_query_k(const int4* __restrict__ coords, int64_t M, BrickTable T,
+                                                     int32_t* __restrict__ nmap_t, int32_t* __restrict__ nmap_rows,
+                                                     uint32_t* tile_mask) {
+    const int64_t m = xcd_chunk(blockIdx.x, gridDim.x) * 256 + threadIdx.x;
     uint32_t rmask = 0;
     if (m < M) {
         const int4 c = coords[m];
-        const bool bok = c.x >= 0 && c.x < S.s0;
+        const int p[3] = {c.y, c.z, c.w};
+        const int ext[3] = {(int)T.S.s1, (int)T.S.s2, (int)T.S.s3};
+        const int bext[3] = {(int)T.Sb.s1, (int)T.Sb.s2, (int)T.Sb.s3};
+        const int64_t stride[3] = {T.Sb.s2 * T.Sb.s3, T.Sb.s3, 1};
+        const bool bok = c.x >= 0 && c.x < T.S.s0;
+        int b0[3], e[3], cp[3][3];
+        bool okd[3][3], sel[3][3], eok[3];
+#pragma unroll
+        for (int a = 0; a < 3; ++a) {
+            b0[a] = p[a] >> kBrickLog;
+            const int r = p[a] & 3;
+            e[a] = r == 0 ? -1 : (r == 3 ? 1 : 0);
+            eok[a] = e[a] != 0 && b0[a] + e[a] >= 0 && b0[a] + e[a] < bext[a];
+#pragma unroll
+            for (int di = 0; di < 3; ++di) {
+                const int q = p[a] + di - 1;
+                okd[a][di] = q >= 0 && q < ext[a];
+                sel[a][di] = (di == 0 && r == 0) || (di == 2 && r == 3);
+                cp[a][di] = (q & 3) << (4 - 2 * a);
+            }
+        }
+        const bool own = bok && b0[0] < bext[0] && b0[1] < bext[1] && b0[2] < bext[2] && b0[0] >= 0 &&
+                         b0[1] >= 0 && b0[2] >= 0;
+        const uint64_t key0 = own ? brick_key(c.x, b0[0], b0[1], b0[2], T.Sb) : 0;
+        uint64_t key[8], home[8], first[8];
+        bool want[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            bool ok = own;
+            int64_t kk = (int64_t)key0;
+#pragma unroll
+            for (int a = 0; a < 3; ++a)
+                if ((k >> (2 - a)) & 1) {
+                    ok = ok && eok[a];
+                    kk += e[a] * stride[a];
+                }
+            want[k] = ok;
+            key[k] = ok ? (uint64_t)kk : 0;
+            home[k] = brick_home(key[k], T.cap_log2);
+            first[k] = T.head[home[k]];  // unconditional: all 8 loads are issued before any compare
+        }
+        int32_t slot[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            slot[k] = -1;
+            if (want[k]) slot[k] = brick_probe(T, key[k], home[k], first[k]);
+        }
+        // Cell loads are unconditional (taps out of bounds or in an absent brick read cell 0 of bucket 0 and are
+        // discarded), so no load sits under a branch and all 27 are in flight together.
+        uint64_t idx[27];
+        uint32_t okbits = 0;
+#pragma unroll
+        for (int dx = 0; dx < 3; ++dx) {
+            int32_t sx[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) sx[j] = sel[0][dx] ? slot[4 + j] : slot[j];
+#pragma unroll
+            for (int dy = 0; dy < 3; ++dy) {
+                int32_t sy[2];
+#pragma unroll
+                for (int j = 0; j < 2; ++j) sy[j] = sel[1][dy] ? sx[2 + j] : sx[j];
+#pragma unroll
+                for (int dz = 0; dz < 3; ++dz) {
+                    const int v = dx * 9 + dy * 3 + dz;
+                    const int32_t sl = sel[2][dz] ? sy[1] : sy[0];
+                    const int cell = cp[0][dx] | cp[1][dy] | cp[2][dz];
+                    const bool ok = okd[0][dx] && okd[1][dy] && okd[2][dz] && sl >= 0;
+                    idx[v] = ok ? (uint64_t)sl * 64 + cell : 0;
+                    okbits |= (ok ? 1u : 0u) << v;
+                }
+            }
+        }
+        int hit[27];
+#pragma unroll
+        for (int v = 0; v < 27; ++v) hit[v] = T.vals[idx[v]];
+#pragma unroll
         for (int v = 0; v < 27; ++v) {
-            const int dx = v / 9 - 1, dy = (v / 3) % 3 - 1, dz = v % 3 - 1;
-            const int x = c.y + dx, y = c.z + dy, z = c.w + dz;
-            int hit = -1;
-            if (bok && x >= 0 && x < S.s1 && y >= 0 && y < S.s2 && z >= 0 && z < S.s3)
-                hit = hash_lookup(keys, vals, cap_mask, (uint64_t)linearise(c.x, x, y, z, S));
-            if (nmap_t) nmap_t[(int64_t)v * M + m] = hit;
-            if (nmap_rows) nmap_rows[m * 27 + v] = hit;
-            rmask |= (hit >= 0 ? 1u : 0u) << v;
+            hit[v] = ((okbits >> v) & 1u) ? hit[v] : -1;
+            rmask |= (hit[v] >= 0 ? 1u : 0u) << v;
+        }
+        if (nmap_t) {
+#pragma unroll
+            for (int v = 0; v < 27; ++v) nmap_t[(int64_t)v * M + m] = hit[v];
+        }
+        if (nmap_rows) {
+#pragma unroll
+            for (int v = 0; v < 27; ++v) nmap_rows[m * 27 + v] = hit[v];
         }
     }
     store_tile_mask(rmask, m, M, tile_mask);
@@ -340,16 +510,23 @@ int pmg_nmap_column(const int32_t* zq, const int32_t* zmin, int B, int H, int W,
     return check_launch("nmap_column_k");
 }
 
-static int64_t hash_capacity(int64_t M) {
+static size_t align_up_sz(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Buckets: a power of two above 1.5x the most bricks M voxels can occupy (load factor < 2/3).
+static int64_t hash_capacity(int64_t bricks) {
     int64_t cap = 1024;
-    while (cap < 4 * M) cap <<= 1;
+    while (cap < bricks + bricks / 2) cap <<= 1;
     return cap;
+}
+
+static size_t hash_bytes(int64_t cap, int64_t M) {
+    return align_up_sz((size_t)cap * sizeof(uint64_t), 256) + align_up_sz((size_t)cap * 64 * sizeof(int32_t), 256) +
+           (size_t)M * sizeof(uint32_t);
 }
 
 size_t pmg_hash_workspace_bytes(int64_t M) {
     if (M < 0) return 0;
-    const int64_t cap = hash_capacity(M);
-    return (size_t)cap * (sizeof(uint64_t) + sizeof(int32_t)) + 256;
+    return hash_bytes(hash_capacity(M), M);
 }
 
 int pmg_nmap_hash(const int32_t* coords, int64_t M, const int64_t* shape, int32_t* nmap_t, int32_t* nmap_rows,
@@ -358,25 +535,34 @@ int pmg_nmap_hash(const int32_t* coords, int64_t M, const int64_t* shape, int32_
     PMG_REQUIRE(M >= 0 && M <= INT_MAX, "bad voxel count");
     PMG_REQUIRE(aligned16(coords), "coords must be 16-byte aligned");
     for (int d = 0; d < 4; ++d) PMG_REQUIRE(shape[d] > 0 && shape[d] <= INT_MAX, "bad sparse shape");
-    // The linearised key must fit in 63 bits so that no key equals the EMPTY marker.
-    const double span = (double)shape[0] * (double)shape[1] * (double)shape[2] * (double)shape[3];
+    // Brick keys must fit in 63 bits so that no key equals the EMPTY marker.
+    const Shape4 Sb{shape[0], (shape[1] + 3) / 4, (shape[2] + 3) / 4, (shape[3] + 3) / 4};
+    const double span = (double)Sb.s0 * (double)Sb.s1 * (double)Sb.s2 * (double)Sb.s3;
     PMG_REQUIRE(span < 9.0e18, "sparse shape too large for 64-bit keys");
     PMG_REQUIRE(workspace && workspace_bytes >= pmg_hash_workspace_bytes(M), "workspace too small");
+    PMG_REQUIRE(M < ((int64_t)1 << 30), "at most 2^30 voxels (32-bit bucket hashing)");
     if (M == 0) return PMG_OK;
     hipStream_t s = (hipStream_t)stream;
-    const int64_t cap = hash_capacity(M);
-    uint64_t* keys = (uint64_t*)workspace;
-    int32_t* vals = (int32_t*)(keys + cap);
-    Shape4 S{shape[0], shape[1], shape[2], shape[3]};
-    hipLaunchKernelGGL(hash_clear_k, dim3((unsigned)((cap + 255) / 256)), dim3(256), 0, s, keys, vals, cap);
-    if (int e = check_launch("hash_clear_k")) return e;
+    const int64_t bricks = span < (double)M ? (int64_t)span : M;
+    const int64_t cap = hash_capacity(bricks);
+    BrickTable T;
+    T.head = (uint64_t*)workspace;
+    T.vals = (int32_t*)((char*)workspace + align_up_sz((size_t)cap * sizeof(uint64_t), 256));
+    uint32_t* slot_of = (uint32_t*)((char*)T.vals + align_up_sz((size_t)cap * 64 * sizeof(int32_t), 256));
+    T.cap_mask = (uint64_t)(cap - 1);
+    T.cap_log2 = 0;
+    while (((int64_t)1 << T.cap_log2) < cap) ++T.cap_log2;
+    T.S = Shape4{shape[0], shape[1], shape[2], shape[3]};
+    T.Sb = Sb;
+    hipLaunchKernelGGL(brick_clear_k, dim3((unsigned)((cap + 255) / 256)), dim3(256), 0, s, T.head, cap);
+    if (int e = check_launch("brick_clear_k")) return e;
     const dim3 g((unsigned)((M + 255) / 256));
-    hipLaunchKernelGGL(hash_insert_k, g, dim3(256), 0, s, (const int4*)coords, M, S, keys, vals,
-                       (uint64_t)(cap - 1));
-    if (int e = check_launch("hash_insert_k")) return e;
-    hipLaunchKernelGGL(hash_query_k, g, dim3(256), 0, s, (const int4*)coords, M, S, (const uint64_t*)keys,
-                       (const int32_t*)vals, (uint64_t)(cap - 1), nmap_t, nmap_rows, tile_mask);
-    return check_launch("hash_query_k");
+    hipLaunchKernelGGL(brick_claim_k, g, dim3(256), 0, s, (const int4*)coords, M, T, slot_of);
+    if (int e = check_launch("brick_claim_k")) return e;
+    hipLaunchKernelGGL(brick_store_k, g, dim3(256), 0, s, (const int4*)coords, M, T, (const uint32_t*)slot_of);
+    if (int e = check_launch("brick_store_k")) return e;
+    hipLaunchKernelGGL(brick_query_k, g, dim3(256), 0, s, (const int4*)coords, M, T, nmap_t, nmap_rows, tile_mask);
+    return check_launch("brick_query_k");
 }
 
 int pmg_nmap_from_rows(const int32_t* nmap_rows, int64_t M, int32_t* nmap_t, uint32_t* tile_mask, void* stream) {

@@ -125,6 +125,43 @@ def test_hash_map_generic(gpu, seed):
     assert np.array_equal(tm.cpu().numpy().view(np.uint32), ost.tile_masks(ref))
 
 
+def test_hash_map_duplicates_and_edges(gpu):
+    """A duplicated coordinate resolves to one of its rows (coords are unique in a sparse tensor; the reference's
+    unstable sort leaves the choice open too); voxels on every face and corner of a shape whose extents are not
+    multiples of the 4-cell brick; two batch items."""
+    announce("hash map duplicates and edges")
+    rng = np.random.default_rng(3)
+    shape = (2, 9, 6, 7)
+    allc = np.stack(np.meshgrid(*[np.arange(s) for s in shape], indexing="ij"), -1).reshape(-1, 4)
+    base = allc[rng.random(allc.shape[0]) < 0.5]
+    dup = base[rng.integers(0, base.shape[0], 200)]
+    coords = np.concatenate([base, dup])[rng.permutation(base.shape[0] + 200)].astype(np.int32)
+    rows = {}
+    for i, c in enumerate(map(tuple, coords)):
+        rows.setdefault(c, set()).add(i)
+    delta = ost.kernel_delta(1)
+    nt, tm, nr = ops.nmap_hash(_t(coords, gpu), shape, taps=True, rows=True)
+    torch.cuda.synchronize()
+    got = nr.cpu().numpy()
+    present = np.zeros_like(got, dtype=bool)
+    for i, c in enumerate(coords):
+        for v in range(27):
+            q = tuple(int(a) for a in (c + delta[v]))
+            inb = all(0 <= q[d] < shape[d] for d in range(4))
+            cand = rows.get(q) if inb else None
+            present[i, v] = cand is not None
+            assert (got[i, v] in cand) if cand else got[i, v] == -1, (i, v)
+    # the same coordinate always resolves to the same row within one map
+    key_row = {}
+    for i, c in enumerate(coords):
+        for v in range(27):
+            if got[i, v] >= 0:
+                q = tuple(int(a) for a in (c + delta[v]))
+                assert key_row.setdefault(q, got[i, v]) == got[i, v]
+    assert np.array_equal(nt.cpu().numpy(), got.T)
+    assert np.array_equal(tm.cpu().numpy().view(np.uint32), ost.tile_masks(np.where(present, 0, -1)))
+
+
 def test_hash_map_surface_voxels(gpu):
     announce("hash map surface voxels 200k")
     coords = spec.make_voxels(200_000, grid=512, seed=5)
