@@ -74,11 +74,21 @@ int pmg_nmap_column(const int32_t* zq, const int32_t* zmin, int B, int H, int W,
 /* pmg_nmap_hash -- generic coordinates, replaces _SortedIndex + _build_submanifold_nmap_sorted
  * (_core.py:105-124, 298-304) with an open-addressing GPU hash of 4x4x4 bricks keyed by _linearise
  * (_core.py:89-94) on the brick grid. coords: [M][4] int32 (b, x, y, z), unique, inside sparse_shape (host array
- * of 4 int64); M < 2^30. Same outputs as pmg_nmap_column (coords excluded). The workspace (any contents) holds
- * the table: 8 + 256 bytes per bucket, buckets = a power of two >= 1.5 M. */
+ * of 4 int64); M < 2^30. Same outputs as pmg_nmap_column (coords excluded), plus row_mask [M] uint32 (bit v set
+ * iff row m has tap v; may be NULL). The workspace (any contents) holds the table: 8 + 256 bytes per bucket,
+ * buckets = a power of two >= 1.5 M. */
 size_t pmg_hash_workspace_bytes(int64_t M);
 int pmg_nmap_hash(const int32_t* coords, int64_t M, const int64_t* sparse_shape_host, int32_t* nmap_t,
-                  int32_t* nmap_rows, uint32_t* tile_mask, void* workspace, size_t workspace_bytes, void* stream);
+                  int32_t* nmap_rows, uint32_t* tile_mask, uint32_t* row_mask, void* workspace,
+                  size_t workspace_bytes, void* stream);
+
+/* pmg_row_order -- a processing order for pmg_spconv_i8_ordered (no counterpart in the reference; it changes no
+ * result): the rows sorted, stably, by the top 16 bits of their 27-bit tap mask (row_mask [M], bit v = tap v
+ * present, as pmg_nmap_hash writes it), so that 16-row tiles share their taps. order [M] int32 = row indices;
+ * order_tile_mask [ceil(M/16)] = the union of the tap masks of order[16t .. 16t+15]. */
+size_t pmg_row_order_workspace_bytes(int64_t M);
+int pmg_row_order(const uint32_t* row_mask, int64_t M, int32_t* order, uint32_t* order_tile_mask, void* workspace,
+                  size_t workspace_bytes, void* stream);
 
 /* pmg_nmap_from_rows -- a caller-supplied (M, 27) map (a NeighborCache.nmap, _core.py:131-176) into the tap-major
  * layout and tile masks the convolutions read. */
@@ -106,6 +116,8 @@ int pmg_kmap_compact(const int32_t* nmap_t, int64_t M, int64_t* offsets, int32_t
  *     PMG_EPI_Q     out int8  [M][Co] = quant(silu((acc*a_scale)*w_scale[n] + bias[n]), out_mult)
  *     PMG_EPI_R     out fp32  [M][Co] = ((acc*a_scale)*w_scale[n] + bias[n]) + skip[m][n]   (skip may alias out)
  *     PMG_EPI_BIAS  out fp32  [M][Co] = (acc*a_scale)*w_scale[n] + bias[n]
+ *     PMG_EPI_QLIN  out int8  [M][Co] = quant((acc*a_scale)*w_scale[n] + bias[n], out_mult), no activation: with
+ *                   a_scale = out_mult = 1 and no bias, the plain per-channel requantisation clamp(rint(acc*m[n]))
  *   a_scale = clip/127 of the input activation, w_scale per output channel; quant(y, mult) =
  *   clamp(rint(y * mult), -127, 127) with mult = 127/clip of the output activation, the requantisation of the
  *   reference's deployed kernels (SparseConvInt8.metal:109; mult computed as in Refiner.swift:148).
@@ -115,11 +127,17 @@ int pmg_kmap_compact(const int32_t* nmap_t, int64_t M, int64_t* offsets, int32_t
  * bias may be NULL (zero).
  * ------------------------------------------------------------------------------------------------------------ */
 enum { PMG_EPI_ACC = 0, PMG_EPI_Q = 1, PMG_EPI_R = 2, PMG_EPI_BIAS = 3, PMG_EPI_SILU = 4, PMG_EPI_RLN = 5,
-       PMG_EPI_ROUT = 6 };
+       PMG_EPI_ROUT = 6, PMG_EPI_QLIN = 7 };
 
 int pmg_spconv_i8(const int8_t* x, const int32_t* nmap_t, const uint32_t* tile_mask, int64_t M, int Ci, int Co,
                   const int8_t* w, int epilogue, float a_scale, const float* w_scale, const float* bias,
                   float out_mult, const float* skip, void* out, void* stream);
+/* pmg_spconv_i8 with the rows processed in `order` (pmg_row_order) and tile masks of that order: the same
+ * results, with the MFMA work of each tile limited to its rows' taps. Ci = Co = 64 or 128. */
+int pmg_spconv_i8_ordered(const int8_t* x, const int32_t* nmap_t, const int32_t* order,
+                          const uint32_t* order_tile_mask, int64_t M, int Ci, int Co, const int8_t* w, int epilogue,
+                          float a_scale, const float* w_scale, const float* bias, float out_mult, const float* skip,
+                          void* out, void* stream);
 int pmg_spconv_f16(const uint16_t* x, const int32_t* nmap_t, const uint32_t* tile_mask, int64_t M, int Ci, int Co,
                    const uint16_t* w, int epilogue, const float* bias, const float* skip, void* out, void* stream);
 int pmg_spconv_f32(const float* x, const int32_t* nmap_t, const uint32_t* tile_mask, int64_t M, int Ci, int Co,

@@ -66,6 +66,12 @@ def epilogue_q(acc, a_scale, w_scale, bias, out_mult) -> np.ndarray:
     return quant_i8(silu_f32(dequant(acc, a_scale, w_scale, bias)), out_mult)
 
 
+def epilogue_qlin(acc, a_scale, w_scale, bias, out_mult) -> np.ndarray:
+    """Requantisation with no activation, clamp(rint(y * out_mult), +-127) of the dequantised y: with a_scale =
+    out_mult = 1 and no bias it is the per-channel q = clamp(rint(acc * m[n]), +-127) of the conv microbenchmark."""
+    return quant_i8(dequant(acc, a_scale, w_scale, bias), out_mult)
+
+
 def epilogue_r(acc, a_scale, w_scale, bias, skip) -> np.ndarray:
     """conv2 epilogue: bias plus the block's identity skip (SparseConvInt8.metal:133-141; flex_sparse_blocks.py:234)."""
     return dequant(acc, a_scale, w_scale, bias) + skip.astype(np.float32)

@@ -11,7 +11,7 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().with_name("libpmg.so")
 
 PMG_OK, PMG_E_INVALID, PMG_E_HIP, PMG_E_OVERFLOW, PMG_E_DEVICE = 0, 1, 2, 3, 4
-EPI_ACC, EPI_Q, EPI_R, EPI_BIAS, EPI_SILU, EPI_RLN, EPI_ROUT = 0, 1, 2, 3, 4, 5, 6
+EPI_ACC, EPI_Q, EPI_R, EPI_BIAS, EPI_SILU, EPI_RLN, EPI_ROUT, EPI_QLIN = 0, 1, 2, 3, 4, 5, 6, 7
 PREC_INT8, PREC_FP16 = 0, 1
 
 vp, i32, i64, f32, sz = C.c_void_p, C.c_int, C.c_int64, C.c_float, C.c_size_t
@@ -64,11 +64,14 @@ SIGNATURES = {
     "pmg_voxelize": (i32, [vp, i64, i32, i32, i32, f32, vp, vp, vp, vp]),
     "pmg_nmap_column": (i32, [vp, vp, i32, i32, i32, vp, vp, vp, vp, vp]),
     "pmg_hash_workspace_bytes": (sz, [i64]),
-    "pmg_nmap_hash": (i32, [vp, i64, vp, vp, vp, vp, vp, sz, vp]),
+    "pmg_nmap_hash": (i32, [vp, i64, vp, vp, vp, vp, vp, vp, sz, vp]),
+    "pmg_row_order_workspace_bytes": (sz, [i64]),
+    "pmg_row_order": (i32, [vp, i64, vp, vp, vp, sz, vp]),
     "pmg_nmap_from_rows": (i32, [vp, i64, vp, vp, vp]),
     "pmg_kmap_workspace_bytes": (sz, [i64]),
     "pmg_kmap_compact": (i32, [vp, i64, vp, vp, vp, i64, vp, sz, vp]),
     "pmg_spconv_i8": (i32, [vp, vp, vp, i64, i32, i32, vp, i32, f32, vp, vp, f32, vp, vp, vp]),
+    "pmg_spconv_i8_ordered": (i32, [vp, vp, vp, vp, i64, i32, i32, vp, i32, f32, vp, vp, f32, vp, vp, vp]),
     "pmg_spconv_f16": (i32, [vp, vp, vp, i64, i32, i32, vp, i32, vp, vp, vp, vp]),
     "pmg_spconv_f32": (i32, [vp, vp, vp, i64, i32, i32, vp, i32, vp, vp, vp]),
     "pmg_spconv_col": (i32, [i32, vp, vp, i32, i32, i32, i32, vp, i32, C.c_void_p, vp]),

@@ -35,6 +35,7 @@ struct ConvArgs {
     float out_mult;
     const float* skip;
     void* out;
+    const int32_t* order;  // rows in processing order (tile masks follow it), or NULL for 0 .. M-1
 };
 
 template <typename T>
@@ -81,6 +82,8 @@ __device__ inline void epilogue(const ConvArgs& a, int64_t m, int n, typename Ac
             if (a.bias) y = y + a.bias[n];
             if constexpr (EPI == PMG_EPI_Q) {
                 ((int8_t*)a.out)[o] = silu_quant_i8(y, a.out_mult);
+            } else if constexpr (EPI == PMG_EPI_QLIN) {
+                ((int8_t*)a.out)[o] = quant_i8(y, a.out_mult);
             } else if constexpr (EPI == PMG_EPI_R) {
                 ((float*)a.out)[o] = y + a.skip[o];
             } else {
@@ -188,15 +191,23 @@ static int pick_nb(int Co) {
 // weight read feeds four tiles, each gathered chunk NB column blocks. Operands are swapped (D = W * X^T): a lane
 // ends with 4 consecutive output channels of one row and the epilogue stores vectors. Chunks are assigned so that
 // the blocks of one XCD (block b runs on XCD b % 8) process adjacent row ranges and share their neighbours in L2.
-constexpr int kG2Threads = 512;
+constexpr int kBufWord3 = 0x00020000;  // buffer descriptor word 3 for raw (untyped) loads on gfx9
+constexpr int kG2Threads = 512;       // 8 waves: two per SIMD, 256 registers each
 constexpr int kG2Waves = kG2Threads / 64;
-constexpr int kG2Chunk = kG2Waves * 64;
+constexpr int kG2Tiles = 4;           // 16-row tiles per wave
+constexpr int kG2Chunk = kG2Waves * kG2Tiles * 16;  // 512 rows per block step
 
+// Generic-map int8 convolution for Ci = Co = C in {64, 128}: a persistent block per CU walks chunks of 512 output
+// rows (in `order` if given); each of its 8 waves owns 64 rows (4 tiles of 16) with 4 x C/16 int32 accumulator
+// tiles. Per tap of the chunk's tap union the block stages that tap's C*C weights in LDS in operand order; each
+// LDS operand feeds the wave's 4 tiles (4 MFMAs of 16 cycles), and the next operand is read before they issue.
+// A wave skips the gathers and MFMAs of taps none of its 4 tiles has. Weights, neighbour rows and indices move
+// one tap ahead; an absent neighbour (index -1) becomes an out-of-range buffer offset, which loads zeros.
 template <int C, int EPI>
 __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
-    constexpr int NB = C / 16, KS = C / 64;
-    constexpr int WCH = C * C / 16;                               // 16-byte chunks of one tap's weights
-    constexpr int WPT = (WCH + kG2Threads - 1) / kG2Threads;      // per thread
+    constexpr int NB = C / 16, KS = C / 64, T = kG2Tiles;
+    constexpr int WCH = C * C / 16;           // 16-byte chunks of one tap's weights
+    constexpr int WPT = (WCH + kG2Threads - 1) / kG2Threads;  // per thread
     static_assert(C == 64 || C == 128, "C must be 64 or 128");
 
     __shared__ __attribute__((aligned(16))) uint8_t s_w[2][C * C];
@@ -207,9 +218,14 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
     const int r = lane & 15, g = lane >> 4;
     const int M = (int)a.M;
     const int64_t ntile = (a.M + 15) >> 4;
-    const uint8_t* __restrict__ xg = a.x;
-    const uint8_t* __restrict__ wg = a.w;
     typedef const __attribute__((address_space(3))) v4i lds_v4i;
+    // Buffer resources: loads past num_records return zeros. The launcher guarantees every byte range fits in
+    // 32 bits.
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, (int)(a.M * C), kBufWord3);
+    const __amdgpu_buffer_rsrc_t nr =
+        __builtin_amdgcn_make_buffer_rsrc((void*)a.nmap_t, (short)0, (int)(a.M * 27 * 4), kBufWord3);
+    const __amdgpu_buffer_rsrc_t wr_ =
+        __builtin_amdgcn_make_buffer_rsrc((void*)a.w, (short)0, 27 * C * C, kBufWord3);
 
     for (int e = tid; e < 2 * C; e += kG2Threads) {
         const int q = e / C, n = e - (e / C) * C;
@@ -224,26 +240,43 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
     const int x = b % nx, bi = b / nx, nbx = (G - x + nx - 1) / nx;  // blocks on this XCD
     const int c0 = (int)((int64_t)nchunk * x / nx), c1 = (int)((int64_t)nchunk * (x + 1) / nx);
 
+    // Weights of tap v, operand order in LDS: chunk e = tid + k*512 holds lane l = e & 63 of (j, s) = e >> 6, i.e.
+    // W[16j + (l & 15)][v][64s + 16(l >> 4) .. +16] of the [Co][27][Ci] tensor. The lane part of the address is
+    // fixed per thread, the (j, s, v) part is the same for the whole wave (a scalar offset).
+    const int w_lane = (r * 27) * C + 16 * g;
     auto w_load = [&](int v, v4i (&wr)[WPT]) {
 #pragma unroll
         for (int k = 0; k < WPT; ++k) {
-            const int e = tid + k * kG2Threads;
-            const int l = e & 63, js = e >> 6;
-            const int j = js / KS, s = js - (js / KS) * KS;
-            wr[k] = e < WCH ? *(const v4i*)(wg + ((int64_t)(16 * j + (l & 15)) * 27 + v) * C + 64 * s + 16 * (l >> 4))
-                            : v4i{0, 0, 0, 0};
+            const int js = wv + k * kG2Waves;  // wave-uniform
+            const int j = js / KS, s2 = js - (js / KS) * KS;
+            wr[k] = js < NB * KS ? __builtin_amdgcn_raw_buffer_load_b128(wr_, w_lane, ((16 * j * 27) + v) * C + 64 * s2, 0)
+                                 : v4i{0, 0, 0, 0};
         }
     };
     auto w_store = [&](int buf, const v4i (&wr)[WPT]) {
 #pragma unroll
-        for (int k = 0; k < WPT; ++k) {
-            const int e = tid + k * kG2Threads;
-            if (e < WCH) ((v4i*)s_w[buf])[e] = wr[k];
-        }
+        for (int k = 0; k < WPT; ++k)
+            if (tid + k * kG2Threads < WCH) ((v4i*)s_w[buf])[tid + k * kG2Threads] = wr[k];
     };
 
     for (int ch = c0 + bi; ch < c1; ch += nbx) {
-        const int row0 = ch * kG2Chunk + wv * 64 + r;  // row of tile 0 for this lane
+        const int pos0 = ch * kG2Chunk + wv * (16 * T) + r;  // position of tile 0's row for this lane
+        // the T rows of this lane: positions pos0 + 16t, through the order if there is one
+        int rowi[T];
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const int p = pos0 + 16 * t;
+            rowi[t] = a.order ? (p < M ? a.order[p] : 0) : p;
+        }
+        // this wave's taps: the union of its T tiles' masks (uniform)
+        uint32_t wmask;
+        {
+            const int64_t tl = (int64_t)ch * (kG2Chunk / 16) + wv * T + (lane & (T - 1));
+            uint32_t mk = (lane < T && tl < ntile) ? a.tmask[tl] : 0u;
+#pragma unroll
+            for (int o = 1; o < T; o <<= 1) mk |= __shfl_xor(mk, o, 64);
+            wmask = (uint32_t)__builtin_amdgcn_readfirstlane((int)mk);
+        }
         __syncthreads();  // the previous chunk's readers of s_uni and s_w are done
         if (wv == 0) {
             const int64_t tl = (int64_t)ch * (kG2Chunk / 16) + (lane & 31);
@@ -254,9 +287,9 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
         }
         __syncthreads();
         uint32_t rem = s_uni;
-        v4i acc[4][NB];
+        v4i acc[T][NB];
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < T; ++t)
 #pragma unroll
             for (int j = 0; j < NB; ++j) acc[t][j] = v4i{0, 0, 0, 0};
 
@@ -266,53 +299,64 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
                 rem = rem ? rem & (rem - 1) : 0u;
                 return v;
             };
-            auto idx_load = [&](int v, int (&id)[4]) {
+            // Rows past M read whatever the map holds there (or zeros past its end): their results are never
+            // stored. Tap -1 (none left) reads index 0s, equally unused.
+            auto mine = [&](int v) { return v >= 0 && ((wmask >> v) & 1u); };
+            auto idx_load = [&](int v, int (&id)[T]) {
+                const int vo = (v < 0 ? 0 : v) * M * 4;  // scalar
 #pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    const int row = row0 + 16 * t;
-                    id[t] = (v >= 0 && row < M) ? a.nmap_t[(int64_t)v * M + row] : -1;
+                for (int t = 0; t < T; ++t) id[t] = __builtin_amdgcn_raw_buffer_load_b32(nr, rowi[t] * 4, vo, 0);
+            };
+            auto gather = [&](int v, const int (&id)[T], v4i (&xs)[T][KS]) {
+                if (!mine(v)) return;
+#pragma unroll
+                for (int t = 0; t < T; ++t) {
+                    const int off = id[t] >= 0 ? id[t] * C + 16 * g : (int)0x80000000;
+#pragma unroll
+                    for (int s2 = 0; s2 < KS; ++s2) xs[t][s2] = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 64 * s2, 0);
                 }
             };
-            auto gather = [&](const int (&id)[4], v4i (&xs)[4][KS]) {
+            // One LDS weight operand feeds the wave's T tiles; the next one is read before they issue.
+            auto mma_tap = [&](int v, int buf, const v4i (&xs)[T][KS]) {
+                if (!mine(v)) return;
+                const uint8_t* wb = s_w[buf] + lane * 16;
+                v4i wop = *(lds_v4i*)(wb);
 #pragma unroll
-                for (int t = 0; t < 4; ++t)
-#pragma unroll
-                    for (int s = 0; s < KS; ++s)
-                        xs[t][s] = (id[t] >= 0 && id[t] < M)
-                                       ? *(const v4i*)(xg + (int64_t)id[t] * C + 64 * s + 16 * g)
-                                       : v4i{0, 0, 0, 0};
-            };
-            auto mma_tap = [&](int buf, const v4i (&xs)[4][KS]) {
-#pragma unroll
-                for (int s = 0; s < KS; ++s)
-#pragma unroll
-                    for (int j = 0; j < NB; ++j) {
-                        const v4i wop = *(lds_v4i*)(s_w[buf] + ((j * KS + s) * 64 + lane) * 16);
-#pragma unroll
-                        for (int t = 0; t < 4; ++t)
-                            acc[t][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wop, xs[t][s], acc[t][j], 0, 0, 0);
+                for (int q = 0; q < NB * KS; ++q) {
+                    const int s2 = q / NB, j = q - (q / NB) * NB;
+                    v4i nxt = wop;
+                    if (q + 1 < NB * KS) {
+                        const int s3 = (q + 1) / NB, j3 = (q + 1) - ((q + 1) / NB) * NB;
+                        nxt = *(lds_v4i*)(wb + ((j3 * KS + s3) * 64) * 16);
                     }
+                    __builtin_amdgcn_sched_barrier(0);  // keep the next operand's read ahead of these MFMAs
+#pragma unroll
+                    for (int t = 0; t < T; ++t)
+                        acc[t][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wop, xs[t][s2], acc[t][j], 0, 0, 0);
+                    __builtin_amdgcn_sched_barrier(0);
+                    wop = nxt;
+                }
             };
 
             int v0 = take(), v1 = take();
             v4i wr[WPT];
-            int idA[4], idB[4];
-            v4i xA[4][KS], xB[4][KS];
+            int idA[T], idB[T];
+            v4i xA[T][KS], xB[T][KS];
             w_load(v0, wr);
             idx_load(v0, idA);
             idx_load(v1, idB);
             w_store(0, wr);
-            gather(idA, xA);
+            gather(v0, idA, xA);
             __syncthreads();
             // invariant at the top: tap v0's weights in s_w[0] and codes in xA; v1's indices in idB
             for (;;) {
                 // ---- tap v0 (buffer 0), while v1's weights and codes and v2's indices load
                 const int v2 = take();
                 if (v1 >= 0) w_load(v1, wr);
-                gather(idB, xB);
+                gather(v1, idB, xB);
                 idx_load(v2, idA);
                 __builtin_amdgcn_sched_barrier(0);
-                mma_tap(0, xA);
+                mma_tap(v0, 0, xA);
                 __builtin_amdgcn_sched_barrier(0);
                 if (v1 < 0) break;
                 w_store(1, wr);
@@ -320,23 +364,24 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
                 // ---- tap v1 (buffer 1), while v2's weights and codes and v3's indices load
                 const int v3 = take();
                 if (v2 >= 0) w_load(v2, wr);
-                gather(idA, xA);
+                gather(v2, idA, xA);
                 idx_load(v3, idB);
                 __builtin_amdgcn_sched_barrier(0);
-                mma_tap(1, xB);
+                mma_tap(v1, 1, xB);
                 __builtin_amdgcn_sched_barrier(0);
                 if (v2 < 0) break;
                 w_store(0, wr);
                 __syncthreads();
+                v0 = v2;
                 v1 = v3;
             }
         }
 
-        // ---- epilogue: lane holds channels 16j + 4g + i of row row0 + 16t
+        // ---- epilogue: lane holds channels 16j + 4g + i of row rowi[t] (position pos0 + 16t)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const int m = row0 + 16 * t;
-            if (m >= M) continue;
+        for (int t = 0; t < T; ++t) {
+            if (pos0 + 16 * t >= M) continue;
+            const int m = rowi[t];
 #pragma unroll
             for (int j = 0; j < NB; ++j) {
                 const int64_t o = (int64_t)m * C + 16 * j + 4 * g;
@@ -354,6 +399,8 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
                     }
                     if constexpr (EPI == PMG_EPI_Q) {
                         store_silu_codes4(y, a.out_mult, (int8_t*)a.out + o);
+                    } else if constexpr (EPI == PMG_EPI_QLIN) {
+                        store_codes4(y, a.out_mult, (int8_t*)a.out + o);
                     } else if constexpr (EPI == PMG_EPI_R) {
                         const v4f sk = *(const v4f*)(a.skip + o);
                         *(v4f*)((float*)a.out + o) = v4f{y[0] + sk[0], y[1] + sk[1], y[2] + sk[2], y[3] + sk[3]};
@@ -375,6 +422,9 @@ static int launch_g2(const ConvArgs& a, int epilogue, hipStream_t s) {
     switch (epilogue) {
         case PMG_EPI_ACC: hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_ACC>), dim3(grid), dim3(kG2Threads), 0, s, a); break;
         case PMG_EPI_Q: hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_Q>), dim3(grid), dim3(kG2Threads), 0, s, a); break;
+        case PMG_EPI_QLIN:
+            hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_QLIN>), dim3(grid), dim3(kG2Threads), 0, s, a);
+            break;
         case PMG_EPI_R: hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_R>), dim3(grid), dim3(kG2Threads), 0, s, a); break;
         case PMG_EPI_BIAS:
             hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_BIAS>), dim3(grid), dim3(kG2Threads), 0, s, a);
@@ -393,6 +443,9 @@ static int conv_common(const ConvArgs& a, int Ci, int epilogue, hipStream_t s) {
         case PMG_EPI_R: return launch_nb<T, PMG_EPI_R>(a, nb, s);
         case PMG_EPI_Q:
             if constexpr (sizeof(T) == 1) return launch_nb<T, PMG_EPI_Q>(a, nb, s);
+            break;
+        case PMG_EPI_QLIN:
+            if constexpr (sizeof(T) == 1) return launch_nb<T, PMG_EPI_QLIN>(a, nb, s);
             break;
         case PMG_EPI_SILU:
             if constexpr (sizeof(T) == 2) return launch_nb<T, PMG_EPI_SILU>(a, nb, s);
@@ -427,16 +480,38 @@ int pmg_spconv_i8(const int8_t* x, const int32_t* nmap_t, const uint32_t* tile_m
     if (int e = validate(x, nmap_t, tile_mask, M, Ci, Co, w, out, 1, "pmg_spconv_i8")) return e;
     PMG_REQUIRE(epilogue == PMG_EPI_ACC || w_scale, "w_scale required");
     PMG_REQUIRE(epilogue != PMG_EPI_R || skip, "skip required");
-    PMG_REQUIRE(epilogue != PMG_EPI_Q || out_mult > 0.0f, "out_mult must be positive");
+    PMG_REQUIRE((epilogue != PMG_EPI_Q && epilogue != PMG_EPI_QLIN) || out_mult > 0.0f, "out_mult must be positive");
     if (M == 0) return PMG_OK;
     ConvArgs a{(const uint8_t*)x, nmap_t, tile_mask, (const uint8_t*)w, M, Co, Ci, Ci / 16,
                a_scale, w_scale, bias, out_mult, skip, out};
-    if (Ci == Co && (Ci == 64 || Ci == 128) && epilogue != PMG_EPI_SILU && aligned16(out) &&
+    // The block-tiled kernel addresses x and the map through 32-bit buffer offsets.
+    const bool fits32 = M * 27 * 4 < ((int64_t)1 << 31) && M * Ci < ((int64_t)1 << 31);
+    if (Ci == Co && (Ci == 64 || Ci == 128) && fits32 && epilogue != PMG_EPI_SILU && aligned16(out) &&
         (epilogue != PMG_EPI_R || aligned16(skip))) {
         if (Ci == 64) return launch_g2<64>(a, epilogue, (hipStream_t)stream);
         return launch_g2<128>(a, epilogue, (hipStream_t)stream);
     }
     return conv_common<int8_t>(a, Ci, epilogue, (hipStream_t)stream);
+}
+
+int pmg_spconv_i8_ordered(const int8_t* x, const int32_t* nmap_t, const int32_t* order, const uint32_t* order_tile_mask,
+                          int64_t M, int Ci, int Co, const int8_t* w, int epilogue, float a_scale,
+                          const float* w_scale, const float* bias, float out_mult, const float* skip, void* out,
+                          void* stream) {
+    if (int e = validate(x, nmap_t, order_tile_mask, M, Ci, Co, w, out, 1, "pmg_spconv_i8_ordered")) return e;
+    PMG_REQUIRE(order, "null order");
+    PMG_REQUIRE(epilogue == PMG_EPI_ACC || w_scale, "w_scale required");
+    PMG_REQUIRE(epilogue != PMG_EPI_R || skip, "skip required");
+    PMG_REQUIRE((epilogue != PMG_EPI_Q && epilogue != PMG_EPI_QLIN) || out_mult > 0.0f, "out_mult must be positive");
+    PMG_REQUIRE(Ci == Co && (Ci == 64 || Ci == 128), "pmg_spconv_i8_ordered: Ci = Co = 64 or 128");
+    PMG_REQUIRE(M * 27 * 4 < ((int64_t)1 << 31) && M * Ci < ((int64_t)1 << 31), "pmg_spconv_i8_ordered: M too large");
+    PMG_REQUIRE(epilogue != PMG_EPI_SILU && aligned16(out) && (epilogue != PMG_EPI_R || aligned16(skip)),
+                "pmg_spconv_i8_ordered: unsupported epilogue or unaligned output");
+    if (M == 0) return PMG_OK;
+    ConvArgs a{(const uint8_t*)x, nmap_t, order_tile_mask, (const uint8_t*)w, M, Co, Ci, Ci / 16,
+               a_scale, w_scale, bias, out_mult, skip, out, order};
+    if (Ci == 64) return launch_g2<64>(a, epilogue, (hipStream_t)stream);
+    return launch_g2<128>(a, epilogue, (hipStream_t)stream);
 }
 
 int pmg_spconv_f16(const uint16_t* x, const int32_t* nmap_t, const uint32_t* tile_mask, int64_t M, int Ci, int Co,

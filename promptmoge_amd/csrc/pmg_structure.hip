@@ -274,7 +274,7 @@ __device__ inline int32_t brick_probe(const BrickTable& T, uint64_t bk, uint64_t
 // then z) and all 27 cell loads are issued together.
 __global__ __launch_bounds__(256) void brick_query_k(const int4* __restrict__ coords, int64_t M, BrickTable T,
                                                      int32_t* __restrict__ nmap_t, int32_t* __restrict__ nmap_rows,
-                                                     uint32_t* tile_mask) {
+                                                     uint32_t* tile_mask, uint32_t* __restrict__ row_mask) {
     const int64_t m = xcd_chunk(blockIdx.x, gridDim.x) * 256 + threadIdx.x;
     uint32_t rmask = 0;
     if (m < M) {
@@ -367,6 +367,7 @@ __global__ __launch_bounds__(256) void brick_query_k(const int4* __restrict__ co
 #pragma unroll
             for (int v = 0; v < 27; ++v) nmap_rows[m * 27 + v] = hit[v];
         }
+        if (row_mask) row_mask[m] = rmask;
     }
     store_tile_mask(rmask, m, M, tile_mask);
 }
@@ -530,7 +531,7 @@ size_t pmg_hash_workspace_bytes(int64_t M) {
 }
 
 int pmg_nmap_hash(const int32_t* coords, int64_t M, const int64_t* shape, int32_t* nmap_t, int32_t* nmap_rows,
-                  uint32_t* tile_mask, void* workspace, size_t workspace_bytes, void* stream) {
+                  uint32_t* tile_mask, uint32_t* row_mask, void* workspace, size_t workspace_bytes, void* stream) {
     PMG_REQUIRE(coords && shape, "null argument");
     PMG_REQUIRE(M >= 0 && M <= INT_MAX, "bad voxel count");
     PMG_REQUIRE(aligned16(coords), "coords must be 16-byte aligned");
@@ -561,7 +562,8 @@ int pmg_nmap_hash(const int32_t* coords, int64_t M, const int64_t* shape, int32_
     if (int e = check_launch("brick_claim_k")) return e;
     hipLaunchKernelGGL(brick_store_k, g, dim3(256), 0, s, (const int4*)coords, M, T, (const uint32_t*)slot_of);
     if (int e = check_launch("brick_store_k")) return e;
-    hipLaunchKernelGGL(brick_query_k, g, dim3(256), 0, s, (const int4*)coords, M, T, nmap_t, nmap_rows, tile_mask);
+    hipLaunchKernelGGL(brick_query_k, g, dim3(256), 0, s, (const int4*)coords, M, T, nmap_t, nmap_rows, tile_mask,
+                       row_mask);
     return check_launch("brick_query_k");
 }
 

@@ -11,14 +11,15 @@ from typing import Optional, Sequence, Tuple
 import torch
 
 from . import _lib
-from ._lib import EPI_ACC, EPI_BIAS, EPI_Q, EPI_R, EPI_RLN, EPI_ROUT, EPI_SILU, ConvEpilogue, call, lib
+from ._lib import EPI_ACC, EPI_BIAS, EPI_Q, EPI_QLIN, EPI_R, EPI_RLN, EPI_ROUT, EPI_SILU, ConvEpilogue, call, lib
 
 __all__ = [
-    "voxelize", "nmap_column", "nmap_hash", "nmap_from_rows", "kmap_compact", "spconv_i8", "spconv_f16",
+    "voxelize", "nmap_column", "nmap_hash", "row_order", "nmap_from_rows", "kmap_compact", "spconv_i8",
+    "spconv_i8_ordered", "spconv_f16",
     "spconv_f32", "spconv_col", "ln_silu_quant", "ln_silu_f16", "fit_scale_shift", "fit_prompt", "fit_final",
     "math_device",
     "nearest_fill",
-    "EPI_ACC", "EPI_Q", "EPI_R", "EPI_BIAS", "EPI_SILU", "EPI_RLN", "EPI_ROUT",
+    "EPI_ACC", "EPI_Q", "EPI_R", "EPI_BIAS", "EPI_SILU", "EPI_RLN", "EPI_ROUT", "EPI_QLIN",
 ]
 
 
@@ -91,8 +92,10 @@ def nmap_column(zq: torch.Tensor, zmin: Optional[torch.Tensor] = None, *, taps: 
     return nt, tm, nr, cd
 
 
-def nmap_hash(coords: torch.Tensor, sparse_shape: Sequence[int], *, taps: bool = True, rows: bool = False):
-    """Generic map over unique (b, x, y, z) coords. Returns (nmap_t [27, M] | None, tile_mask, nmap_rows | None)."""
+def nmap_hash(coords: torch.Tensor, sparse_shape: Sequence[int], *, taps: bool = True, rows: bool = False,
+              row_mask: bool = False):
+    """Generic map over unique (b, x, y, z) coords. Returns (nmap_t [27, M] | None, tile_mask, nmap_rows | None), and
+    with row_mask=True a fourth item, each row's 27-bit tap mask [M] (int32)."""
     coords = _dev(coords, "coords", torch.int32)
     if coords.ndim != 2 or coords.shape[1] != 4:
         raise ValueError("coords must be (M, 4)")
@@ -103,9 +106,23 @@ def nmap_hash(coords: torch.Tensor, sparse_shape: Sequence[int], *, taps: bool =
     tm = torch.empty(((M + 15) // 16,), dtype=torch.int32, device=dev)
     ws_bytes = lib().pmg_hash_workspace_bytes(M)
     ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
+    rm = torch.empty((M,), dtype=torch.int32, device=dev) if row_mask else None
     shape = (C.c_int64 * 4)(*[int(s) for s in sparse_shape[:4]])
-    call("pmg_nmap_hash", _p(coords), M, shape, _p(nt), _p(nr), _p(tm), _p(ws), ws_bytes, _stream())
-    return nt, tm, nr
+    call("pmg_nmap_hash", _p(coords), M, shape, _p(nt), _p(nr), _p(tm), _p(rm), _p(ws), ws_bytes, _stream())
+    return (nt, tm, nr, rm) if row_mask else (nt, tm, nr)
+
+
+def row_order(row_mask: torch.Tensor):
+    """Processing order for spconv_i8_ordered: rows stably sorted by the top 16 bits of their tap mask, and the
+    tile masks [ceil(M/16)] of that order. Returns (order [M] int32, order_tile_mask)."""
+    row_mask = _dev(row_mask, "row_mask", torch.int32)
+    M = row_mask.shape[0]
+    order = torch.empty((M,), dtype=torch.int32, device=row_mask.device)
+    otm = torch.empty(((M + 15) // 16,), dtype=torch.int32, device=row_mask.device)
+    ws_bytes = lib().pmg_row_order_workspace_bytes(M)
+    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=row_mask.device)
+    call("pmg_row_order", _p(row_mask), M, _p(order), _p(otm), _p(ws), ws_bytes, _stream())
+    return order, otm
 
 
 def nmap_from_rows(nmap_rows: torch.Tensor):
@@ -137,7 +154,7 @@ def kmap_compact(nmap_t: torch.Tensor, capacity: Optional[int] = None):
 # ------------------------------------------------------------------------------------------------------------- (3)
 def _conv_out(M: int, Co: int, epilogue: int, elt: str, dev) -> torch.Tensor:
     if elt == "i8":
-        dt = {EPI_ACC: torch.int32, EPI_Q: torch.int8}.get(epilogue, torch.float32)
+        dt = {EPI_ACC: torch.int32, EPI_Q: torch.int8, EPI_QLIN: torch.int8}.get(epilogue, torch.float32)
     elif elt == "f16":
         dt = torch.float16 if epilogue == EPI_SILU else torch.float32
     else:
@@ -160,6 +177,26 @@ def spconv_i8(x: torch.Tensor, nmap_t: torch.Tensor, tile_mask: torch.Tensor, w:
         out = _conv_out(M, Co, epilogue, "i8", x.device)
     call("pmg_spconv_i8", _p(x), _p(nmap_t), _p(tile_mask), M, Ci, Co, _p(w), epilogue, float(a_scale), _p(w_scale),
          _p(bias), float(out_mult), _p(skip), _p(out), _stream())
+    return out
+
+
+def spconv_i8_ordered(x: torch.Tensor, nmap_t: torch.Tensor, order: torch.Tensor, order_tile_mask: torch.Tensor,
+                      w: torch.Tensor, epilogue: int = EPI_ACC, *, a_scale: float = 1.0,
+                      w_scale: Optional[torch.Tensor] = None, bias: Optional[torch.Tensor] = None,
+                      out_mult: float = 1.0, skip: Optional[torch.Tensor] = None,
+                      out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """spconv_i8 with rows processed in `order` (row_order): identical results, less MFMA work. Ci = Co = 64, 128."""
+    x = _dev(x, "x", torch.int8)
+    w = _dev(w, "w", torch.int8)
+    order = _dev(order, "order", torch.int32)
+    M, Ci = x.shape
+    Co = w.shape[0]
+    if w.numel() != Co * 27 * Ci:
+        raise ValueError("weight must be (Co, 3, 3, 3, Ci)")
+    if out is None:
+        out = _conv_out(M, Co, epilogue, "i8", x.device)
+    call("pmg_spconv_i8_ordered", _p(x), _p(nmap_t), _p(order), _p(order_tile_mask), M, Ci, Co, _p(w), epilogue,
+         float(a_scale), _p(w_scale), _p(bias), float(out_mult), _p(skip), _p(out), _stream())
     return out
 
 

@@ -37,7 +37,7 @@ def test_every_declared_symbol_is_exported_and_bound(libpmg):
 
 
 def test_version_and_error_string(libpmg):
-    assert libpmg.pmg_version() == 1
+    assert libpmg.pmg_version() == 2
     rc = libpmg.pmg_voxelize(None, 1, 1, 1, 1, 256.0, None, None, None, None)
     assert rc == _lib.PMG_E_INVALID
     assert b"null" in libpmg.pmg_last_error()
@@ -64,7 +64,11 @@ def test_invalid_shapes_rejected_on_host(libpmg):
                                       None) == _lib.PMG_E_INVALID
     # hash: shape too large for 64-bit keys
     big = (C.c_int64 * 4)(1 << 20, 1 << 20, 1 << 20, 1 << 20)
-    assert libpmg.pmg_nmap_hash(C.c_void_p(16), 5, big, None, None, None, dummy, 1 << 30, None) == _lib.PMG_E_INVALID
+    assert libpmg.pmg_nmap_hash(C.c_void_p(16), 5, big, None, None, None, None, dummy, 1 << 30,
+                                None) == _lib.PMG_E_INVALID
+    # ordered conv: only Ci = Co = 64 / 128
+    assert libpmg.pmg_spconv_i8_ordered(dummy, dummy, dummy, dummy, 10, 32, 32, dummy, 0, 1.0, dummy, None, 1.0,
+                                        None, dummy, None) == _lib.PMG_E_INVALID
 
 
 def test_refiner_create_rejects_bad_config(libpmg):

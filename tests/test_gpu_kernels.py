@@ -223,6 +223,53 @@ def test_conv_int8_generic_map(gpu):
     assert np.array_equal(acc.cpu().numpy(), ocv.conv_acc_int(x, nm, w))
 
 
+def test_row_order_is_a_stable_sort_by_mask(gpu):
+    """pmg_row_order: a permutation sorting the rows stably by the top 16 bits of their tap mask, with the tile
+    unions of that order; the hash's row masks are the bits of its map rows."""
+    announce("row order 200k surface voxels")
+    coords = spec.make_voxels(200_000, grid=512, seed=5)
+    shape = (1, 512, 512, 512)
+    nt, tm, nr, rm = ops.nmap_hash(_t(coords, gpu), shape, rows=True, row_mask=True)
+    order, otm = ops.row_order(rm)
+    torch.cuda.synchronize()
+    rows = nr.cpu().numpy()
+    masks = ((rows >= 0).astype(np.uint64) << np.arange(27, dtype=np.uint64)).sum(1).astype(np.uint32)
+    assert np.array_equal(rm.cpu().numpy().view(np.uint32), masks)
+    expect = np.argsort(masks >> 11, kind="stable")
+    assert np.array_equal(order.cpu().numpy(), expect)
+    m = masks[expect]
+    pad = np.zeros(((len(m) + 15) // 16) * 16, np.uint32)
+    pad[:len(m)] = m
+    assert np.array_equal(otm.cpu().numpy().view(np.uint32), np.bitwise_or.reduce(pad.reshape(-1, 16), axis=1))
+
+
+@pytest.mark.parametrize("C", [64, 128])
+def test_conv_int8_ordered_matches_unordered(gpu, C):
+    """The ordered convolution gives bit-identical results to the plain one (accumulators and every epilogue)."""
+    announce(f"conv int8 ordered C={C}")
+    rng = np.random.default_rng(C + 1)
+    coords = spec.make_voxels(70_001, grid=256, seed=4)
+    shape = (1, 256, 256, 256)
+    nt, tm, _, rm = ops.nmap_hash(_t(coords, gpu), shape, row_mask=True)
+    order, otm = ops.row_order(rm)
+    M = coords.shape[0]
+    x = _t(rng.integers(-127, 128, size=(M, C)).astype(np.int8), gpu)
+    w = _t(rng.integers(-127, 128, size=(C, 3, 3, 3, C)).astype(np.int8), gpu)
+    sc = _t(rng.uniform(1e-5, 1e-4, C).astype(np.float32), gpu)
+    b = _t(rng.normal(0, 0.05, C).astype(np.float32), gpu)
+    skip = _t(rng.normal(size=(M, C)).astype(np.float32), gpu)
+    kw = dict(a_scale=0.02, w_scale=sc, bias=b, out_mult=30.0)
+    for epi, extra in ((ops.EPI_ACC, {}), (ops.EPI_Q, {}), (ops.EPI_R, {"skip": skip}), (ops.EPI_BIAS, {}),
+                       (ops.EPI_QLIN, {})):
+        a = ops.spconv_i8(x, nt, tm, w, epi, **kw, **extra)
+        o = ops.spconv_i8_ordered(x, nt, order, otm, w, epi, **kw, **extra)
+        torch.cuda.synchronize()
+        assert torch.equal(a, o), epi
+    nm = ost.nmap_sorted(coords, shape)
+    assert np.array_equal(ops.spconv_i8_ordered(x, nt, order, otm, w).cpu().numpy(),
+                          ocv.conv_acc_int(x.cpu().numpy(), nm, w.cpu().numpy()))
+
+
 @pytest.mark.parametrize("C", [32, 48, 64, 128])
 def test_conv_int8_epilogues(gpu, C):
     announce(f"conv int8 epilogues C={C}")
@@ -244,6 +291,13 @@ def test_conv_int8_epilogues(gpu, C):
     assert np.array_equal(out_r.cpu().numpy(), ocv.epilogue_r(acc, a_s, s, b, skip))
     out_b = ops.spconv_i8(X, nt, tm, Wq, ops.EPI_BIAS, a_scale=a_s, w_scale=S, bias=Bv)
     assert np.array_equal(out_b.cpu().numpy(), ocv.dequant(acc, a_s, s, b))
+    out_l = ops.spconv_i8(X, nt, tm, Wq, ops.EPI_QLIN, a_scale=a_s, w_scale=S, bias=Bv, out_mult=o_s)
+    assert np.array_equal(out_l.cpu().numpy(), ocv.epilogue_qlin(acc, a_s, s, b, o_s))
+    # the microbenchmark's plain per-channel requantisation: q = clamp(rint(acc * m[n]), +-127)
+    m = (s * np.float32(0.05)).astype(np.float32)
+    out_m = ops.spconv_i8(X, nt, tm, Wq, ops.EPI_QLIN, w_scale=_t(m, gpu))
+    expect = np.clip(np.rint(acc.astype(np.float32) * m[None, :]), -127, 127).astype(np.int8)
+    assert np.array_equal(out_m.cpu().numpy(), expect)
 
 
 @pytest.mark.parametrize("C", [32, 64])
