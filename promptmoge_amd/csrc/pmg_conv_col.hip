@@ -463,26 +463,28 @@ static int launch_col2(const ColConvArgs& a, int epi, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// int8, C <= 48: neighbour-pixel-major reduction over 64-row waves.
+// int8, C <= 48: neighbour-pixel-major reduction over waves of 16*TT rows.
 //
-// A persistent 8-wave block (two waves per SIMD) owns segments of 512 voxels, 64 rows per wave in four 16-row tiles.
+// A persistent 8-wave block (two waves per SIMD) owns segments of 128*TT voxels, 16*TT rows per wave in TT 16-row
+// tiles (TT = 4, 2 or 1, whichever spreads the segments most evenly over the CUs).
 // For each of the 9 pixel offsets (di, dj) a wave reads its rows' neighbour codes from the LDS window ONCE (one
 // ds_read_b128 per tile at a compile-time offset from one per-lane base address) and the neighbour keys. A row's
 // neighbour is at most one of the three taps (di, dj, dz), dz = key_nb - key_row, so the operand of tap dz is the
-// loaded chunk with the other rows (and the K-padding lanes) zeroed by v_cndmask; a dz that none of the wave's 64
-// rows has is skipped (wave-uniform branch). The weights of a tap are one 16-byte read per lane from LDS, laid out
+// loaded chunk with the other rows (and the K-padding lanes) zeroed by v_cndmask. The weights of a tap are one 16-byte read per lane from LDS, laid out
 // in the MFMA operand order (block (v, j) = 16 x NCH consecutive 16-byte chunks), conflict-free, and each read feeds
-// the four tiles' MFMAs. The next offset's codes and keys are read before the current offset's MFMAs issue.
+// the TT tiles' MFMAs. The next offset's codes and keys are read before the current offset's MFMAs issue.
 // Per-channel epilogue constants are staged in LDS, so the epilogue issues no dependent global loads. The next
 // segment's window is loaded into registers during the compute and written to LDS at the end of the segment.
 constexpr int kColvThreads = 512;
 constexpr int kColvWaves = kColvThreads / 64;
-constexpr int kColvRows = 64;
-constexpr int kColvSeg = kColvRows * kColvWaves;  // 512 voxels
-constexpr int kColvWin = kColvSeg + 2;
 
-template <int C>
+// TT = 16-row tiles per wave: a segment is 128 * TT voxels (the launcher picks TT to balance the segments over
+// the CUs).
+template <int C, int TT>
 struct ColvGeom {
+    static constexpr int kColvRows = 16 * TT;
+    static constexpr int kColvSeg = kColvRows * kColvWaves;
+    static constexpr int kColvWin = kColvSeg + 2;
     static constexpr int ROWB = C;
     static constexpr int NCH = C / 16;
     static constexpr int NB = C / 16;
@@ -494,9 +496,10 @@ struct ColvGeom {
     static constexpr int PFZ = (3 * kColvWin + kColvThreads - 1) / kColvThreads;
 };
 
-template <int C, int EPI>
+template <int C, int EPI, int TT>
 __global__ __launch_bounds__(kColvThreads, 1) void spconv_colv_k(ColConvArgs a) {
-    typedef ColvGeom<C> G;
+    typedef ColvGeom<C, TT> G;
+    constexpr int kColvRows = G::kColvRows, kColvSeg = G::kColvSeg, kColvWin = G::kColvWin;
     constexpr int ROWB = G::ROWB, NCH = G::NCH, NB = G::NB;
     static_assert(C == 16 || C == 32 || C == 48, "this kernel covers C <= 48");
     static_assert(G::WBYTES < 65536, "weight offsets must fit the LDS immediate field");
@@ -597,9 +600,9 @@ __global__ __launch_bounds__(kColvThreads, 1) void spconv_colv_k(ColConvArgs a) 
         const int nxt = seg + gridDim.x;
         __syncthreads();  // window (and, the first time, weights and constants) visible to all waves
 
-        int zc[4], pi[4], pj[4];
+        int zc[TT], pi[TT], pj[TT];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
+        for (int t = 0; t < TT; ++t) {
             const int m = s0 + kColvRows * wv + 16 * t + r;
             const int pix = (m < M ? m : 0) % HW;
             pi[t] = pix / W;
@@ -607,23 +610,23 @@ __global__ __launch_bounds__(kColvThreads, 1) void spconv_colv_k(ColConvArgs a) 
             zc[t] = zb[kColvWin + 16 * t + 1];
         }
 
-        v4i acc[4][NB];
+        v4i acc[TT][NB];
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < TT; ++t)
 #pragma unroll
             for (int j = 0; j < NB; ++j) acc[t][j] = v4i{0, 0, 0, 0};
 
         // Straight-line over the 27 taps (v = 3 (di * 3 + dj) + dz + 1), software-pipelined: the codes and keys of
         // pixel offset o + 1 are read when offset o starts, the weights of tap v + 1 before tap v's MFMAs. No tap is
-        // skipped: 64 rows cover almost every tap anyway, and branches would stop the loads from moving ahead.
+        // skipped: the wave's rows cover almost every tap anyway, and branches would stop the loads from moving ahead.
         struct Nb {
-            v4i x[4];
-            int z[4];
+            v4i x[TT];
+            int z[TT];
         };
         auto load_nb = [&](int o, Nb& n) {  // o = di * 3 + dj, compile-time after unrolling
             const int di = o / 3, dj = o % 3;
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
+            for (int t = 0; t < TT; ++t) {
                 n.x[t] = *(lds_v4i*)(xb + (di * kColvWin + dj + 16 * t) * ROWB);
                 n.z[t] = zb[di * kColvWin + dj + 16 * t];
             }
@@ -634,7 +637,7 @@ __global__ __launch_bounds__(kColvThreads, 1) void spconv_colv_k(ColConvArgs a) 
         };
         Nb X[2];
         v4i Wt[2][NB];
-        int dz[4];
+        int dz[TT];
         load_nb(0, X[0]);
         load_w(0, Wt[0]);
 #pragma unroll
@@ -647,31 +650,31 @@ __global__ __launch_bounds__(kColvThreads, 1) void spconv_colv_k(ColConvArgs a) 
             if (d == 0) {
                 const int di = o / 3, dj = o % 3;
 #pragma unroll
-                for (int t = 0; t < 4; ++t) {
+                for (int t = 0; t < TT; ++t) {
                     const bool in =
                         (unsigned)(pi[t] + di - 1) < (unsigned)H && (unsigned)(pj[t] + dj - 1) < (unsigned)W;
                     dz[t] = in ? n.z[t] - zc[t] + 1 : 3;  // 0, 1, 2: tap dz - 1; anything else: no tap
                 }
             }
-            v4i xm[4];
+            v4i xm[TT];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) xm[t] = (kin && dz[t] == d) ? n.x[t] : v4i{0, 0, 0, 0};
+            for (int t = 0; t < TT; ++t) xm[t] = (kin && dz[t] == d) ? n.x[t] : v4i{0, 0, 0, 0};
 #pragma unroll
             for (int j = 0; j < NB; ++j)
 #pragma unroll
-                for (int t = 0; t < 4; ++t)
+                for (int t = 0; t < TT; ++t)
                     acc[t][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(Wt[v & 1][j], xm[t], acc[t][j], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
         }
         if (nxt < nseg) fetch(nxt);  // the next window: in flight during the epilogue
         // the residual inputs of all four tiles are requested before any is used
-        v4f sk[4][NB];
+        v4f sk[TT][NB];
         if constexpr (EPI == PMG_EPI_R || EPI == PMG_EPI_RLN || EPI == PMG_EPI_ROUT) {
 #pragma unroll
-            for (int t = 0; t < 4; ++t) load_skip<C>(a, s0 + kColvRows * wv + 16 * t + r, M, g, sk[t]);
+            for (int t = 0; t < TT; ++t) load_skip<C>(a, s0 + kColvRows * wv + 16 * t + r, M, g, sk[t]);
         }
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < TT; ++t)
             col_epilogue<int8_t, C, EPI, kptr>(a, acc[t], s0 + kColvRows * wv + 16 * t + r, M, g, kc, sk[t]);
 
         if (nxt < nseg) {
@@ -681,12 +684,28 @@ __global__ __launch_bounds__(kColvThreads, 1) void spconv_colv_k(ColConvArgs a) 
     }
 }
 
+// Rows on the critical path (the most segments any block walks, times the segment size) for TT tiles per wave.
+static int64_t colv_span(int64_t M, int64_t cus, int tt) {
+    const int64_t seg = 128 * tt, nseg = (M + seg - 1) / seg;
+    return (nseg + cus - 1) / cus * seg;
+}
+
 template <int C, int EPI>
 static int launch_colv(const ColConvArgs& a, hipStream_t s) {
-    const int64_t nseg = (a.M + kColvSeg - 1) / kColvSeg;
-    int64_t grid = num_cus();
-    if (grid > nseg) grid = nseg;
-    hipLaunchKernelGGL((spconv_colv_k<C, EPI>), dim3((unsigned)grid), dim3(kColvThreads), 0, s, a);
+    const int64_t cus = num_cus();
+    // the largest TT whose span is within 1/16 of the best: larger segments amortise the window halo and feed
+    // each LDS weight read to more tiles
+    const int64_t s4 = colv_span(a.M, cus, 4), s2 = colv_span(a.M, cus, 2), s1 = colv_span(a.M, cus, 1);
+    const int64_t best = s4 < s2 ? (s4 < s1 ? s4 : s1) : (s2 < s1 ? s2 : s1);
+    const int tt = s4 * 16 <= best * 17 ? 4 : (s2 * 16 <= best * 17 ? 2 : 1);
+    const int64_t nseg = (a.M + 128 * tt - 1) / (128 * tt);
+    const unsigned grid = (unsigned)(cus < nseg ? cus : nseg);
+    if (tt == 4)
+        hipLaunchKernelGGL((spconv_colv_k<C, EPI, 4>), dim3(grid), dim3(kColvThreads), 0, s, a);
+    else if (tt == 2)
+        hipLaunchKernelGGL((spconv_colv_k<C, EPI, 2>), dim3(grid), dim3(kColvThreads), 0, s, a);
+    else
+        hipLaunchKernelGGL((spconv_colv_k<C, EPI, 1>), dim3(grid), dim3(kColvThreads), 0, s, a);
     return check_launch("spconv_colv_k");
 }
 
