@@ -45,9 +45,9 @@ CALIB_BYTES = 64 << 20  # the calibration copy: 64 MiB read + 64 MiB written
 # kernel-name substrings (as rocprofv3 prints them) for the per-step kernels
 KERNEL_SYMBOLS = {
     "fit_prompt": "fit_k",
-    "conv_q": "spconv_colv_k<48, 1>",
-    "conv_rln": "spconv_colv_k<48, 5>",
-    "conv_rout": "spconv_colv_k<48, 6>",
+    "conv_q": "spconv_colv_k<48, 1,",
+    "conv_rln": "spconv_colv_k<48, 5,",
+    "conv_rout": "spconv_colv_k<48, 6,",
     "input_stage": "input_stage_k<48",
 }
 
