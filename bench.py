@@ -134,6 +134,10 @@ def write_traffic(out_path, fetch_dir, write_dir):
     fs, ws = calib(fv), calib(wv)
     lines = [f"# HBM traffic per launch, Model A (480x640, C=48), from rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE",
              f"# scale factors from a {CALIB_BYTES} B copy: FETCH_SIZE x{fs:.4f}, WRITE_SIZE x{ws:.4f}",
+             "# commands (GPU box, from /tmp with TMPDIR=/tmp), then this summary:",
+             "#   rocprofv3 --pmc FETCH_SIZE --output-format csv -d <F> -o k -- python3 <repo>/bench.py --kernels-only",
+             "#   rocprofv3 --pmc WRITE_SIZE --output-format csv -d <W> -o k -- python3 <repo>/bench.py --kernels-only",
+             "#   python3 <repo>/bench.py --write-traffic <this file> <F> <W>",
              "# columns: traffic <kernel> <fetch bytes> <write bytes>"]
     for name, sym in KERNEL_SYMBOLS.items():
         f = [statistics.median(v) for (k, _), v in fv.items() if sym in k]
