@@ -463,10 +463,11 @@ static int launch_col2(const ColConvArgs& a, int epi, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// int8, C <= 48: neighbour-pixel-major reduction over waves of 16*TT rows.
+// int8, C <= 64: neighbour-pixel-major reduction over waves of 16*TT rows.
 //
 // A persistent 8-wave block (two waves per SIMD) owns segments of 128*TT voxels, 16*TT rows per wave in TT 16-row
-// tiles (TT = 4, 2 or 1, whichever spreads the segments most evenly over the CUs).
+// tiles (TT = 4, 2 or 1, whichever spreads the segments most evenly over the CUs; at C = 64 the 108 KB of weights
+// leave LDS room for TT = 1 only).
 // For each of the 9 pixel offsets (di, dj) a wave reads its rows' neighbour codes from the LDS window ONCE (one
 // ds_read_b128 per tile at a compile-time offset from one per-lane base address) and the neighbour keys. A row's
 // neighbour is at most one of the three taps (di, dj, dz), dz = key_nb - key_row, so the operand of tap dz is the
@@ -501,8 +502,8 @@ __global__ __launch_bounds__(kColvThreads, 1) void spconv_colv_k(ColConvArgs a) 
     typedef ColvGeom<C, TT> G;
     constexpr int kColvRows = G::kColvRows, kColvSeg = G::kColvSeg, kColvWin = G::kColvWin;
     constexpr int ROWB = G::ROWB, NCH = G::NCH, NB = G::NB;
-    static_assert(C == 16 || C == 32 || C == 48, "this kernel covers C <= 48");
-    static_assert(G::WBYTES < 65536, "weight offsets must fit the LDS immediate field");
+    static_assert(C == 16 || C == 32 || C == 48 || C == 64, "this kernel covers C <= 64");
+    static_assert(C < 64 || TT == 1, "at C = 64 the 27 taps' weights (108 KB) leave LDS room for one tile per wave");
 
     __shared__ __attribute__((aligned(16))) uint8_t s_w[G::WBYTES];
     __shared__ __attribute__((aligned(16))) uint8_t s_x[G::XBYTES];
@@ -693,6 +694,12 @@ static int64_t colv_span(int64_t M, int64_t cus, int tt) {
 template <int C, int EPI>
 static int launch_colv(const ColConvArgs& a, hipStream_t s) {
     const int64_t cus = num_cus();
+    if constexpr (C == 64) {
+        const int64_t nseg = (a.M + 127) / 128;
+        const unsigned grid = (unsigned)(cus < nseg ? cus : nseg);
+        hipLaunchKernelGGL((spconv_colv_k<C, EPI, 1>), dim3(grid), dim3(kColvThreads), 0, s, a);
+        return check_launch("spconv_colv_k");
+    }
     // the largest TT whose span is within 1/16 of the best: larger segments amortise the window halo and feed
     // each LDS weight read to more tiles
     const int64_t s4 = colv_span(a.M, cus, 4), s2 = colv_span(a.M, cus, 2), s1 = colv_span(a.M, cus, 1);
@@ -700,12 +707,14 @@ static int launch_colv(const ColConvArgs& a, hipStream_t s) {
     const int tt = s4 * 16 <= best * 17 ? 4 : (s2 * 16 <= best * 17 ? 2 : 1);
     const int64_t nseg = (a.M + 128 * tt - 1) / (128 * tt);
     const unsigned grid = (unsigned)(cus < nseg ? cus : nseg);
-    if (tt == 4)
-        hipLaunchKernelGGL((spconv_colv_k<C, EPI, 4>), dim3(grid), dim3(kColvThreads), 0, s, a);
-    else if (tt == 2)
-        hipLaunchKernelGGL((spconv_colv_k<C, EPI, 2>), dim3(grid), dim3(kColvThreads), 0, s, a);
-    else
-        hipLaunchKernelGGL((spconv_colv_k<C, EPI, 1>), dim3(grid), dim3(kColvThreads), 0, s, a);
+    if constexpr (C < 64) {
+        if (tt == 4)
+            hipLaunchKernelGGL((spconv_colv_k<C, EPI, 4>), dim3(grid), dim3(kColvThreads), 0, s, a);
+        else if (tt == 2)
+            hipLaunchKernelGGL((spconv_colv_k<C, EPI, 2>), dim3(grid), dim3(kColvThreads), 0, s, a);
+        else
+            hipLaunchKernelGGL((spconv_colv_k<C, EPI, 1>), dim3(grid), dim3(kColvThreads), 0, s, a);
+    }
     return check_launch("spconv_colv_k");
 }
 
@@ -727,7 +736,7 @@ int launch_conv_col(int precision, const ColConvArgs& a, int C, int epi, hipStre
             case 16: return launch_colv2<16>(a, epi, s);
             case 32: return launch_colv2<32>(a, epi, s);
             case 48: return launch_colv2<48>(a, epi, s);
-            case 64: return launch_col2<int8_t, 64>(a, epi, s);
+            case 64: return launch_colv2<64>(a, epi, s);
             case 128: return launch_col2<int8_t, 128>(a, epi, s);
         }
     } else {
