@@ -16,6 +16,9 @@ captured HIP graph of that chain; the metric fit of the refined depth is timed s
     cpu_baseline  the oracle's restatement of the reference's CPU path (_fallback conv on fake-quantised operands,
               fit_scale_shift with an exact k-th selection) timed on this host: 1 warm-up + median of 5 Model-A steps
     conv_microbench  isolated int8 conv on 1,000,000 surface voxels in 1024^3, C = 64 and 128
+    measured_peaks   this device's practical HBM copy bandwidth and int8 MFMA rate (pmg_probe_copy / _mfma_i8);
+              `roofline.frac` is against the published 8 TB/s, `roofline.frac_measured` against the copy probe
+    other_configs    one K-step frame of the fp16 teacher (T) and of the hi-res config (H, with nearest_fill)
 
 Other modes (used to produce the committed profiles):
     --kernels-only     launch each per-step kernel --kernel-reps times eagerly (plus a 64 MiB copy for counter
@@ -211,6 +214,48 @@ def kernels_only(args):
     return 0
 
 
+def measured_peaks(stream):
+    """The device's practical peaks with the kernels' instruction forms (pmg_probe_copy: 16-byte vector copy of
+    1 GiB, read + write bytes; pmg_probe_mfma_i8: register-only v_mfma_i32_16x16x64_i8 loops at 8 and 16 waves
+    per CU, the better of the two). Median of 3 event-timed runs each."""
+    import ctypes as C
+
+    import torch
+
+    from promptmoge_amd._lib import call
+
+    nbytes = 1 << 30
+    with torch.cuda.stream(stream):
+        a = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+        b = torch.empty_like(a)
+        a.fill_(1)
+        sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+        sp = C.c_void_p(stream.cuda_stream)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+        def timed(fn):
+            fn()
+            ts = []
+            for _ in range(3):
+                e0.record(stream)
+                fn()
+                e1.record(stream)
+                torch.cuda.synchronize()
+                ts.append(e0.elapsed_time(e1))
+            return statistics.median(ts)
+
+        t = timed(lambda: call("pmg_probe_copy", a.data_ptr(), b.data_ptr(), nbytes, sp))
+        hbm = 2 * nbytes / (t * 1e-3) / 1e9
+        best = 0.0
+        iters = 2048
+        cus = torch.cuda.get_device_properties(0).multi_processor_count
+        for wpc in (8, 16):
+            t = timed(lambda: call("pmg_probe_mfma_i8", iters, wpc, sink.data_ptr(), sp))
+            ops = cus * wpc * iters * 16 * 32768.0
+            best = max(best, ops / (t * 1e-3) / 1e12)
+        del a, b
+    return {"hbm_copy_gbs": round(hbm, 1), "int8_mfma_tops": round(best, 1)}
+
 def microbench(stream):
     import torch
 
@@ -397,7 +442,13 @@ def main() -> int:
                 "kernel": dominant, "algorithmic_bytes": int(contract[dominant]),
                 "minimal_bytes": int(minimal[dominant]), "avg_launch_ms": round(kern[dominant], 5)}
 
+    peaks = measured_peaks(stream)
+    roofline["measured_peak"] = peaks["hbm_copy_gbs"]
+    roofline["frac_measured"] = round(ach / peaks["hbm_copy_gbs"], 4)
     micro = None if args.no_micro else microbench(stream)
+    if micro:
+        for Cm in ("C64", "C128"):
+            micro[Cm]["frac_measured_int8"] = round(micro[Cm]["tops"] / peaks["int8_mfma_tops"], 4)
     others = None if args.no_others else {n: frame_bench(n, stream) for n in ("T", "H")}
     cpu = None if args.no_cpu else cpu_baseline(env)
 
@@ -410,7 +461,8 @@ def main() -> int:
                    "voxels": M, "parallelism": "1 GPU"},
         "final_fit_ms": round(ms_with_final - ms, 5), "step_with_final_fit_ms": round(ms_with_final, 5),
         "wall_s_timed": round(wall, 3),
-        "roofline": roofline, "cpu_baseline": cpu, "conv_microbench": micro, "other_configs": others,
+        "roofline": roofline, "measured_peaks": peaks, "cpu_baseline": cpu, "conv_microbench": micro,
+        "other_configs": others,
         "kernel_ms": {k: round(v, 5) for k, v in kern.items()},
         "per_step_ms": {k: round(v, 5) for k, v in per_step.items()},
         "kernel_gbs_contract": {k: round(contract[k] / (kern[k] * 1e-3) / 1e9, 1) for k in kern},

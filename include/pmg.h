@@ -46,6 +46,14 @@ int pmg_version(void);
 int pmg_math_host(int op, const float* in_host, float* out_host, int64_t n);
 int pmg_math_device(int op, const float* in, float* out, int64_t n, void* stream);
 
+/* Peak probes (no counterpart in the reference): the device's practical rates with the kernels' instruction forms,
+ * for reporting kernels against measured as well as published peaks. pmg_probe_copy streams `bytes` from src to
+ * dst (16-byte vectors); pmg_probe_mfma_i8 runs iters x 16 independent v_mfma_i32_16x16x64_i8 per wave on
+ * waves_per_cu waves per CU (32768 * 16 * iters int8 ops per wave); sink receives nothing but must be valid. The
+ * caller times them with events on `stream`. */
+int pmg_probe_copy(const void* src, void* dst, int64_t bytes, void* stream);
+int pmg_probe_mfma_i8(int iters, int waves_per_cu, int32_t* sink, void* stream);
+
 /* ------------------------------------------------------------------------------------------------------------ *
  * (1) Voxelisation -- replaces MoGeModel._voxelize (moge/model/v3.py:305-344).
  *   zq[b,i,j] = rint(logz[b,i,j] * resolution)       (round half to even, as torch.round; v3.py:332)

@@ -61,6 +61,8 @@ SIGNATURES = {
     "pmg_version": (i32, []),
     "pmg_math_host": (i32, [i32, vp, vp, i64]),
     "pmg_math_device": (i32, [i32, vp, vp, i64, vp]),
+    "pmg_probe_copy": (i32, [vp, vp, i64, vp]),
+    "pmg_probe_mfma_i8": (i32, [i32, i32, vp, vp]),
     "pmg_voxelize": (i32, [vp, i64, i32, i32, i32, f32, vp, vp, vp, vp]),
     "pmg_nmap_column": (i32, [vp, vp, i32, i32, i32, vp, vp, vp, vp, vp]),
     "pmg_hash_workspace_bytes": (sz, [i64]),
