@@ -91,9 +91,11 @@ int pmg_nmap_hash(const int32_t* coords, int64_t M, const int64_t* sparse_shape_
                   size_t workspace_bytes, void* stream);
 
 /* pmg_row_order -- a processing order for pmg_spconv_i8_ordered (no counterpart in the reference; it changes no
- * result): the rows sorted, stably, by the top 16 bits of their 27-bit tap mask (row_mask [M], bit v = tap v
- * present, as pmg_nmap_hash writes it), so that 16-row tiles share their taps. order [M] int32 = row indices;
- * order_tile_mask [ceil(M/16)] = the union of the tap masks of order[16t .. 16t+15]. */
+ * result): within each window of 4096 consecutive rows, the rows sorted, stably, by the top 16 bits of their
+ * 27-bit tap mask (row_mask [M], bit v = tap v present, as pmg_nmap_hash writes it), so that 16-row tiles share
+ * their taps while each window keeps its rows' neighbourhood. order [M] int32 = row indices (order[i] lies in
+ * the window of i); order_tile_mask [ceil(M/16)] = the union of the tap masks of order[16t .. 16t+15]. The
+ * workspace is not used (pmg_row_order_workspace_bytes returns a nominal 256 bytes). */
 size_t pmg_row_order_workspace_bytes(int64_t M);
 int pmg_row_order(const uint32_t* row_mask, int64_t M, int32_t* order, uint32_t* order_tile_mask, void* workspace,
                   size_t workspace_bytes, void* stream);
