@@ -162,13 +162,18 @@ __device__ inline void ln_silu_quad(float (&y)[NB][4], P gamma, P beta, float ep
 // exact evaluation is within 4.5e-7 of the true value. So unless v lies within twice the sum of both bounds of a
 // rounding tie (k + 1/2, including the saturation edge 127.5), both round to the same integer, and only those rare
 // elements (a few per 10^4) take the exact path. NaN and infinities fall through to the same clamp as the exact form.
-__device__ inline int8_t silu_quant_i8(float y, float mult) {
+__device__ inline float silu_quant_fast(float y, float mult, bool& unsure) {
     const float e = __builtin_amdgcn_exp2f(y * -PMG_LOG2E);
     const float v = (y * __builtin_amdgcn_rcpf(1.0f + e)) * mult;
     const float q0 = rne(v);
     const float tol = __builtin_fabsf(v) * (__builtin_fabsf(y) * 1.5e-7f + 1.8e-6f);
-    float q = fmin_(fmax_(q0, -127.0f), 127.0f);
-    if (0.5f - __builtin_fabsf(v - q0) <= tol) q = quant_f32(silu_f32(y), mult);
+    unsure = 0.5f - __builtin_fabsf(v - q0) <= tol;
+    return fmin_(fmax_(q0, -127.0f), 127.0f);
+}
+__device__ inline int8_t silu_quant_i8(float y, float mult) {
+    bool unsure;
+    float q = silu_quant_fast(y, mult, unsure);
+    if (unsure) q = quant_f32(silu_f32(y), mult);
     return (int8_t)(int)q;
 }
 
@@ -179,12 +184,52 @@ __device__ inline void store_codes4(const float (&h)[4], float mult, int8_t* q) 
     for (int i = 0; i < 4; ++i) pk |= (uint32_t)(uint8_t)quant_i8(h[i], mult) << (8 * i);
     *(uint32_t*)q = pk;
 }
-// As store_codes4 for silu(t): the codes of silu of the 4 pre-activations t.
+// As store_codes4 for silu(t): the codes of silu of the 4 pre-activations t (silu_quant_i8 with one branch to the
+// exact evaluation per 4 values).
 __device__ inline void store_silu_codes4(const float (&t)[4], float mult, int8_t* q) {
+    float c[4];
+    bool u[4], any = false;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        c[i] = silu_quant_fast(t[i], mult, u[i]);
+        any = any || u[i];
+    }
+    if (any) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (u[i]) c[i] = quant_f32(silu_f32(t[i]), mult);
+    }
     uint32_t pk = 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) pk |= (uint32_t)(uint8_t)silu_quant_i8(t[i], mult) << (8 * i);
+    for (int i = 0; i < 4; ++i) pk |= (uint32_t)(uint8_t)(int)c[i] << (8 * i);
     *(uint32_t*)q = pk;
+}
+// silu_quant_i8 of NB x 4 values, packed four codes to a word, with one branch to the exact evaluation for all of
+// them (so the fast evaluations of the NB x 4 values can interleave).
+template <int NB>
+__device__ inline void silu_codes_packed(const float (&t)[NB][4], float mult, uint32_t (&pk)[NB]) {
+    float c[NB][4];
+    bool u[NB][4], any = false;
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            c[j][i] = silu_quant_fast(t[j][i], mult, u[j][i]);
+            any = any || u[j][i];
+        }
+    if (any) {
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (u[j][i]) c[j][i] = quant_f32(silu_f32(t[j][i]), mult);
+    }
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+        pk[j] = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pk[j] |= (uint32_t)(uint8_t)(int)c[j][i] << (8 * i);
+    }
 }
 __device__ inline void store_half4(const float (&h)[4], _Float16* o) {
     typedef _Float16 h4 __attribute__((ext_vector_type(4)));

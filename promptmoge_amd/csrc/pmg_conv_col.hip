@@ -31,6 +31,7 @@
 // group g sums its channels 16j+4g+i (j outer, i inner), then ((s0 + s1) + (s2 + s3)) across the four groups; every
 // LayerNorm of the step uses that same order.
 #include <climits>
+#include <type_traits>
 
 #include "pmg_common.h"
 #include "pmg_internal.h"
@@ -113,16 +114,22 @@ __device__ inline void col_epilogue(const ColConvArgs& a, const typename ColAcc<
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int n = 16 * j + 4 * g + i;
-                if constexpr (sizeof(T) == 1) {
-                    float t = (float)acc[j][i] * a.a_scale;
-                    t = t * k.ws[n];
-                    if (k.has_bias) t = t + k.bs[n];
-                    y[j][i] = t;
+                // the bias of an LDS-staged constant set is zero-filled when absent, so it is read unconditionally
+                // and the add is a select rather than a branch
+                float b = 0.0f;
+                if constexpr (std::is_same<P, const float*>::value) {
+                    if (k.has_bias) b = k.bs[n];
                 } else {
-                    float t = acc[j][i];
-                    if (k.has_bias) t = t + k.bs[n];
-                    y[j][i] = t;
+                    b = k.bs[n];
                 }
+                float t;
+                if constexpr (sizeof(T) == 1) {
+                    t = (float)acc[j][i] * a.a_scale;
+                    t = t * k.ws[n];
+                } else {
+                    t = acc[j][i];
+                }
+                y[j][i] = k.has_bias ? t + b : t;
             }
     }
     if constexpr (EPI == PMG_EPI_ACC) {
@@ -137,13 +144,18 @@ __device__ inline void col_epilogue(const ColConvArgs& a, const typename ColAcc<
             }
         }
     } else if constexpr (EPI == PMG_EPI_Q) {
-        if (ok) {
+        if constexpr (sizeof(T) == 1) {
+            uint32_t pk[NB];
+            silu_codes_packed<NB>(y, a.out_mult, pk);
+            if (ok) {
+#pragma unroll
+                for (int j = 0; j < NB; ++j) *(uint32_t*)((int8_t*)a.out + mo * C + 16 * j + 4 * g) = pk[j];
+            }
+        } else if (ok) {
 #pragma unroll
             for (int j = 0; j < NB; ++j) {
                 const int64_t o = mo * C + 16 * j + 4 * g;
-                if constexpr (sizeof(T) == 1) {
-                    store_silu_codes4(y[j], a.out_mult, (int8_t*)a.out + o);
-                } else {
+                {
                     typedef _Float16 h4 __attribute__((ext_vector_type(4)));
                     h4 hv;
 #pragma unroll
@@ -163,15 +175,17 @@ __device__ inline void col_epilogue(const ColConvArgs& a, const typename ColAcc<
         }
         if constexpr (EPI == PMG_EPI_RLN) {
             ln_silu_quad<NB, sizeof(T) != 1>(y, k.gamma, k.beta, a.ln_eps, g);
-            if (ok) {
+            if constexpr (sizeof(T) == 1) {
+                uint32_t pk[NB];
+                silu_codes_packed<NB>(y, a.next_mult, pk);
+                if (ok) {
 #pragma unroll
-                for (int j = 0; j < NB; ++j) {
-                    const int64_t o = mo * C + 16 * j + 4 * g;
-                    if constexpr (sizeof(T) == 1)
-                        store_silu_codes4(y[j], a.next_mult, (int8_t*)a.next_q + o);
-                    else
-                        store_half4(y[j], (_Float16*)a.next_q + o);
+                    for (int j = 0; j < NB; ++j)
+                        *(uint32_t*)((int8_t*)a.next_q + mo * C + 16 * j + 4 * g) = pk[j];
                 }
+            } else if (ok) {
+#pragma unroll
+                for (int j = 0; j < NB; ++j) store_half4(y[j], (_Float16*)a.next_q + mo * C + 16 * j + 4 * g);
             }
         } else if constexpr (EPI == PMG_EPI_ROUT) {
             float p = 0.0f;
@@ -463,54 +477,64 @@ static int launch_col2(const ColConvArgs& a, int epi, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// int8, C <= 64: neighbour-pixel-major reduction over waves of 16*TT rows.
+// int8, C <= 64: neighbour-pixel-major reduction, two wave groups in ping-pong.
 //
-// A persistent 8-wave block (two waves per SIMD) owns segments of 128*TT voxels, 16*TT rows per wave in TT 16-row
-// tiles (TT = 4, 2 or 1, whichever spreads the segments most evenly over the CUs; at C = 64 the 108 KB of weights
-// leave LDS room for TT = 1 only).
-// For each of the 9 pixel offsets (di, dj) a wave reads its rows' neighbour codes from the LDS window ONCE (one
-// ds_read_b128 per tile at a compile-time offset from one per-lane base address) and the neighbour keys. A row's
-// neighbour is at most one of the three taps (di, dj, dz), dz = key_nb - key_row, so the operand of tap dz is the
-// loaded chunk with the other rows (and the K-padding lanes) zeroed by v_cndmask. The weights of a tap are one 16-byte read per lane from LDS, laid out
-// in the MFMA operand order (block (v, j) = 16 x NCH consecutive 16-byte chunks), conflict-free, and each read feeds
-// the TT tiles' MFMAs. The next offset's codes and keys are read before the current offset's MFMAs issue.
-// Per-channel epilogue constants are staged in LDS, so the epilogue issues no dependent global loads. The next
-// segment's window is loaded into registers during the compute and written to LDS at the end of the segment.
-constexpr int kColvThreads = 512;
-constexpr int kColvWaves = kColvThreads / 64;
-
-// TT = 16-row tiles per wave: a segment is 128 * TT voxels (the launcher picks TT to balance the segments over
-// the CUs).
-template <int C, int TT>
+// A persistent block holds two groups of WG waves (WG = 4: one wave of each group per SIMD). Each group owns its own
+// LDS window buffer and walks its own segments of 16 * TT * WG voxels (16 * TT rows per wave in TT 16-row tiles). The
+// groups run half a period apart: while one group's waves issue the matrix work of a segment (after the global
+// loads of their next window and, where registers allow, of the segment's residual inputs), the other group's
+// waves (on the same SIMDs) write their next window to LDS and run the previous segment's epilogue. Every half
+// period ends at one block barrier (LDS waits only; global stores are not waited for), so the MFMA pipe and the
+// VALU of a SIMD are busy at the same time instead of in turn.
+//
+// Matrix work of a segment. At level 0 a row's neighbour at pixel offset (di, dj) is at most one of the three taps
+// (di, dj, dz), dz = key_nb - key_row, and the centre offset holds only the row itself (one voxel per pixel). So the
+// reduction runs over K = 8 offsets x 3 taps x C + C instead of 27 x C: the four lane groups of an MFMA operand
+// (16 K-values each) take four different offsets -- group G = 0 takes offsets 0..3, G = 1 offsets 5..8 -- and one
+// MFMA step covers (tap dz, channel chunk c) of all four: lane group g supplies chunk c of its offset's neighbour
+// row, zeroed (v_cndmask) unless that neighbour's dz is the step's. Per 16-channel output block that is
+// 6 * C/16 + 1 steps (the last one the centre tap, lane groups >= C/16 zero) instead of 27 with up to 75 % K
+// padding: 19 instead of 27 MFMAs at C = 48, 13 at C = 32. Each lane reads its offset's codes once per group
+// (one ds_read_b128 per chunk and tile) and keeps them for the three dz steps; the next group's codes are read
+// into the registers of chunks already done. The weights of a step are one conflict-free 16-byte read per lane
+// from LDS, laid out in the MFMA operand order, read two steps ahead, and each read feeds the TT tiles' MFMAs.
+// The weights stay in LDS for the whole block; per-channel epilogue constants are staged in LDS too, so the
+// epilogue issues no dependent global loads.
+template <int C, int TT, int WG>
 struct ColvGeom {
-    static constexpr int kColvRows = 16 * TT;
-    static constexpr int kColvSeg = kColvRows * kColvWaves;
-    static constexpr int kColvWin = kColvSeg + 2;
+    static constexpr int kThreads = 128 * WG;       // two groups
+    static constexpr int kGroupThreads = 64 * WG;
+    static constexpr int kRows = 16 * TT;           // rows per wave
+    static constexpr int kSeg = kRows * WG;         // rows per segment (one group)
+    static constexpr int kWin = kSeg + 2;
     static constexpr int ROWB = C;
     static constexpr int NCH = C / 16;
     static constexpr int NB = C / 16;
-    static constexpr int XBYTES = 3 * kColvWin * ROWB;
-    static constexpr int WBLK = 16 * NCH * 16;        // bytes of one (tap, 16-channel block) operand
-    static constexpr int WBYTES = 27 * NB * WBLK;
-    static constexpr int NCHUNK = 3 * kColvWin * NCH;
-    static constexpr int PF = (NCHUNK + kColvThreads - 1) / kColvThreads;
-    static constexpr int PFZ = (3 * kColvWin + kColvThreads - 1) / kColvThreads;
+    static constexpr int XBYTES = 3 * kWin * ROWB;
+    static constexpr int ZWORDS = 3 * kWin;
+    static constexpr int NSTEP = 6 * NCH + 1;       // MFMA steps per 16-channel output block
+    static constexpr int WBYTES = NSTEP * NB * 1024;  // one 64-lane x 16-byte operand per (step, block)
+    static constexpr int NCHUNK = 3 * kWin * NCH;
+    static constexpr int PF = (NCHUNK + kGroupThreads - 1) / kGroupThreads;  // window chunks per thread
+    static constexpr int PFZ = (ZWORDS + kGroupThreads - 1) / kGroupThreads;  // window keys per thread
+    static constexpr int LDS = WBYTES + 2 * XBYTES + 2 * ZWORDS * 4 + 5 * C * 4;
 };
 
-template <int C, int EPI, int TT>
-__global__ __launch_bounds__(kColvThreads, 1) void spconv_colv_k(ColConvArgs a) {
-    typedef ColvGeom<C, TT> G;
-    constexpr int kColvRows = G::kColvRows, kColvSeg = G::kColvSeg, kColvWin = G::kColvWin;
+template <int C, int EPI, int TT, int WG>
+__global__ __launch_bounds__(128 * WG, 1) void spconv_colv_k(ColConvArgs a) {
+    typedef ColvGeom<C, TT, WG> G;
+    constexpr int kRows = G::kRows, kSeg = G::kSeg, kWin = G::kWin, GT = G::kGroupThreads;
     constexpr int ROWB = G::ROWB, NCH = G::NCH, NB = G::NB;
     static_assert(C == 16 || C == 32 || C == 48 || C == 64, "this kernel covers C <= 64");
-    static_assert(C < 64 || TT == 1, "at C = 64 the 27 taps' weights (108 KB) leave LDS room for one tile per wave");
+    static_assert(G::LDS <= 160 * 1024, "weights and two windows must fit the 160 KB of LDS");
 
     __shared__ __attribute__((aligned(16))) uint8_t s_w[G::WBYTES];
-    __shared__ __attribute__((aligned(16))) uint8_t s_x[G::XBYTES];
-    __shared__ int s_z[3 * kColvWin];
+    __shared__ __attribute__((aligned(16))) uint8_t s_x[2][G::XBYTES];
+    __shared__ int s_z[2][G::ZWORDS];
     __shared__ float s_k[5][C];  // w_scale, bias, ln gamma, ln beta, out_w
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int grp = wv / WG, wq = wv - grp * WG, gtid = tid - grp * GT;
     const int r = lane & 15, g = lane >> 4;
     const int gc = g < NCH ? g : NCH - 1;  // chunk read by this lane; lanes g >= NCH are zeroed (K padding)
     const bool kin = g < NCH;
@@ -520,18 +544,22 @@ __global__ __launch_bounds__(kColvThreads, 1) void spconv_colv_k(ColConvArgs a) 
     const uint8_t* __restrict__ xg = (const uint8_t*)a.x;
     const uint8_t* __restrict__ wg = (const uint8_t*)a.w;
 
-    // weights: block (v, j), lane chunk (r, c) at ((v * NB + j) * 16 * NCH + c * 16 + r) * 16; all of a thread's
-    // loads are issued before its first LDS store (the first window's loads follow them)
-    constexpr int WCH = 27 * NB * 16 * NCH, WPT = (WCH + kColvThreads - 1) / kColvThreads;
+    // weights: operand (step st, block j) at ((st * NB + j) * 64 + lane) * 16. Step 1 + (G * 3 + d) * NCH + c, lane
+    // (r, q): W[16j + r][tap 3 * (5G + q) + d][chunk c]; step 0 (centre), lane (r, q): W[16j + r][13][chunk q],
+    // zero for q >= NCH. All of a thread's loads are issued before its first LDS store.
+    constexpr int WCH = G::NSTEP * NB * 64, WPT = (WCH + G::kThreads - 1) / G::kThreads;
     v4i wtmp[WPT];
 #pragma unroll
     for (int k = 0; k < WPT; ++k) {
-        const int e = tid + k * kColvThreads;
-        const int rr = e % 16, c = (e / 16) % NCH, vj = e / (16 * NCH);
-        const int v = vj / NB, j = vj - (vj / NB) * NB;
-        wtmp[k] = e < WCH ? *(const v4i*)(wg + ((int64_t)(16 * j + rr) * 27 + v) * ROWB + 16 * c) : v4i{0, 0, 0, 0};
+        const int e = tid + k * G::kThreads;
+        const int rr = e % 16, q = (e / 16) % 4, sj = e / 64;
+        const int st = sj / NB, j = sj - (sj / NB) * NB;
+        const int u = st - 1, gi = u / (3 * NCH), d = (u / NCH) % 3, c = u % NCH;
+        const int v = st == 0 ? 13 : 3 * (5 * gi + q) + d, ch = st == 0 ? q : c;
+        const bool ok = e < WCH && (st > 0 || q < NCH);
+        wtmp[k] = ok ? *(const v4i*)(wg + ((int64_t)(16 * j + rr) * 27 + v) * ROWB + 16 * ch) : v4i{0, 0, 0, 0};
     }
-    for (int e = tid; e < 5 * C; e += kColvThreads) {
+    for (int e = tid; e < 5 * C; e += G::kThreads) {
         const int q = e / C, n = e - (e / C) * C;
         const float* src = q == 0 ? a.w_scale : q == 1 ? a.bias : q == 2 ? a.ln_gamma : q == 3 ? a.ln_beta : a.out_w;
         s_k[q][n] = src ? src[n] : 0.0f;
@@ -539,17 +567,19 @@ __global__ __launch_bounds__(kColvThreads, 1) void spconv_colv_k(ColConvArgs a) 
     typedef const __attribute__((address_space(3))) float* kptr;
     const EpiConst<kptr> kc{(kptr)s_k[0], (kptr)s_k[1], (kptr)s_k[2], (kptr)s_k[3], (kptr)s_k[4], a.bias != nullptr};
 
+    // window of segment sg: slice d in {0,1,2} holds voxels s0 + (d-1)*W - 1 + q, q in [0, kWin); loaded by the
+    // group's threads into registers, then written to the group's LDS buffer
     v4i pf[G::PF];
     int pfz[G::PFZ];
     auto fetch = [&](int sg) {
-        const int s0 = sg * kColvSeg;
+        const int s0 = sg * kSeg;
 #pragma unroll
         for (int k = 0; k < G::PF; ++k) {
-            const int e = tid + k * kColvThreads;
+            const int e = gtid + k * GT;
             pf[k] = v4i{0, 0, 0, 0};
             if (e < G::NCHUNK) {
-                const int d = e / (kColvWin * NCH);
-                const int rem = e - d * (kColvWin * NCH);
+                const int d = e / (kWin * NCH);
+                const int rem = e - d * (kWin * NCH);
                 const int q = rem / NCH, c = rem - (rem / NCH) * NCH;
                 const int p = s0 + (d - 1) * W - 1 + q;
                 if (p >= 0 && p < M) pf[k] = *(const v4i*)(xg + (int64_t)p * ROWB + c * 16);
@@ -557,165 +587,209 @@ __global__ __launch_bounds__(kColvThreads, 1) void spconv_colv_k(ColConvArgs a) 
         }
 #pragma unroll
         for (int k = 0; k < G::PFZ; ++k) {
-            const int e = tid + k * kColvThreads;
+            const int e = gtid + k * GT;
             pfz[k] = kZFar;
-            if (e < 3 * kColvWin) {
-                const int d = e / kColvWin, q = e - (e / kColvWin) * kColvWin;
+            if (e < G::ZWORDS) {
+                const int d = e / kWin, q = e - (e / kWin) * kWin;
                 const int p = s0 + (d - 1) * W - 1 + q;
                 if (p >= 0 && p < M) pfz[k] = a.zq[p];
             }
         }
     };
+    uint8_t* const xbuf = s_x[grp];
+    int* const zbuf = s_z[grp];
     auto commit = [&]() {
 #pragma unroll
         for (int k = 0; k < G::PF; ++k) {
-            const int e = tid + k * kColvThreads;
-            if (e < G::NCHUNK) ((v4i*)s_x)[e] = pf[k];
+            const int e = gtid + k * GT;
+            if (e < G::NCHUNK) ((v4i*)xbuf)[e] = pf[k];
         }
 #pragma unroll
         for (int k = 0; k < G::PFZ; ++k) {
-            const int e = tid + k * kColvThreads;
-            if (e < 3 * kColvWin) s_z[e] = pfz[k];
+            const int e = gtid + k * GT;
+            if (e < G::ZWORDS) zbuf[e] = pfz[k];
         }
     };
 
     typedef const __attribute__((address_space(3))) uint8_t lds_u8;
     typedef const __attribute__((address_space(3))) v4i lds_v4i;
     typedef const __attribute__((address_space(3))) int lds_int;
-    const int lr0 = kColvRows * wv + r;  // window-relative row of tile 0
-    const lds_u8* xb = (lds_u8*)s_x + lr0 * ROWB + gc * 16;
-    const lds_int* zb = (lds_int*)s_z + lr0;
-    const lds_u8* wb = (lds_u8*)s_w + (gc * 16 + r) * 16;
+    const int lr0 = kRows * wq + r;  // window-relative row of tile 0
+    // this lane's pixel offset in group G: o = 5G + g, (di, dj) = (o / 3, o % 3); window row of the neighbour of
+    // local row lr: di * kWin + lr + dj
+    const int o0 = g, o1 = 5 + g;
+    const int ri0 = o0 / 3 - 1, rj0 = o0 % 3 - 1, ri1 = o1 / 3 - 1, rj1 = o1 % 3 - 1;
+    const lds_u8* xg0 = (lds_u8*)xbuf + (lr0 + (o0 / 3) * kWin + o0 % 3) * ROWB;
+    const lds_u8* xg1 = (lds_u8*)xbuf + (lr0 + (o1 / 3) * kWin + o1 % 3) * ROWB;
+    const lds_int* zg0 = (lds_int*)zbuf + lr0 + (o0 / 3) * kWin + o0 % 3;
+    const lds_int* zg1 = (lds_int*)zbuf + lr0 + (o1 / 3) * kWin + o1 % 3;
+    const lds_u8* xcb = (lds_u8*)xbuf + (lr0 + kWin + 1) * ROWB + gc * 16;  // the row itself, chunk g
+    const lds_int* zcb = (lds_int*)zbuf + lr0 + kWin + 1;
+    const lds_u8* wb = (lds_u8*)s_w + lane * 16;
 
-    const int nseg = (M + kColvSeg - 1) / kColvSeg;
-    int seg = blockIdx.x;
-    if (seg < nseg) fetch(seg);
+    // this group's segments: first, first + stride, ...; group 0 has at least as many as group 1
+    const int nseg = (M + kSeg - 1) / kSeg;
+    const int stride = 2 * (int)gridDim.x;
+    const int first = 2 * (int)blockIdx.x + grp;
+    const int nk = first < nseg ? (nseg - 1 - first) / stride + 1 : 0;
+    const int first0 = 2 * (int)blockIdx.x;
+    const int nk0 = first0 < nseg ? (nseg - 1 - first0) / stride + 1 : 0;
+
+    if (nk > 0) fetch(first);
 #pragma unroll
     for (int k = 0; k < WPT; ++k) {
-        const int e = tid + k * kColvThreads;
+        const int e = tid + k * G::kThreads;
         if (e < WCH) ((v4i*)s_w)[e] = wtmp[k];
     }
-    if (seg < nseg) commit();
-    for (; seg < nseg; seg += gridDim.x) {
-        const int s0 = seg * kColvSeg;
-        const int nxt = seg + gridDim.x;
-        __syncthreads();  // window (and, the first time, weights and constants) visible to all waves
+    if (nk > 0) commit();
+    __syncthreads();  // weights, constants and both groups' first windows visible
 
-        int zc[TT], pi[TT], pj[TT];
+    constexpr bool kRes = EPI == PMG_EPI_R || EPI == PMG_EPI_RLN || EPI == PMG_EPI_ROUT;
+    constexpr bool kSkipEarly = TT * NB <= 8;  // else the residual inputs would not fit in registers beside the MFMAs
+    v4i acc[TT][NB];
+    v4f sk[TT][NB];  // residual inputs of the segment in flight
+    // Half periods: group 0 runs M0 E0 M1 E1 ..., group 1 runs - M0 E0 M1 E1 ... (Mk: loads of window k+1 and of
+    // segment k's residual inputs issued, then the matrix work of segment k; Ek: window k+1 written to LDS, then
+    // the epilogue of segment k; -: idle). The global loads thus have a whole half period to arrive. Both groups
+    // walk 2 * nk0 + 1 half periods, each ended by a barrier, so the barrier counts match.
+    const int steps = 2 * nk0 + 1;
+    for (int step = 0, hp = -grp; step < steps; ++step, ++hp) {
+        const int kk = hp >> 1;
+        if (hp < 0) {
+        } else if ((hp & 1) == 0) {
+            if (kk < nk) {
+                const int s0 = (first + kk * stride) * kSeg;
+                if (kk + 1 < nk) fetch(first + (kk + 1) * stride);
+                if constexpr (kRes && kSkipEarly) {
 #pragma unroll
-        for (int t = 0; t < TT; ++t) {
-            const int m = s0 + kColvRows * wv + 16 * t + r;
-            const int pix = (m < M ? m : 0) % HW;
-            pi[t] = pix / W;
-            pj[t] = pix - pi[t] * W;
-            zc[t] = zb[kColvWin + 16 * t + 1];
-        }
-
-        v4i acc[TT][NB];
-#pragma unroll
-        for (int t = 0; t < TT; ++t)
-#pragma unroll
-            for (int j = 0; j < NB; ++j) acc[t][j] = v4i{0, 0, 0, 0};
-
-        // Straight-line over the 27 taps (v = 3 (di * 3 + dj) + dz + 1), software-pipelined: the codes and keys of
-        // pixel offset o + 1 are read when offset o starts, the weights of tap v + 1 before tap v's MFMAs. No tap is
-        // skipped: the wave's rows cover almost every tap anyway, and branches would stop the loads from moving ahead.
-        struct Nb {
-            v4i x[TT];
-            int z[TT];
-        };
-        auto load_nb = [&](int o, Nb& n) {  // o = di * 3 + dj, compile-time after unrolling
-            const int di = o / 3, dj = o % 3;
-#pragma unroll
-            for (int t = 0; t < TT; ++t) {
-                n.x[t] = *(lds_v4i*)(xb + (di * kColvWin + dj + 16 * t) * ROWB);
-                n.z[t] = zb[di * kColvWin + dj + 16 * t];
-            }
-        };
-        auto load_w = [&](int v, v4i (&w)[NB]) {
-#pragma unroll
-            for (int j = 0; j < NB; ++j) w[j] = *(lds_v4i*)(wb + (v * NB + j) * G::WBLK);
-        };
-        Nb X[2];
-        v4i Wt[2][NB];
-        int dz[TT];
-        load_nb(0, X[0]);
-        load_w(0, Wt[0]);
-#pragma unroll
-        for (int v = 0; v < 27; ++v) {
-            const int o = v / 3, d = v % 3;
-            const Nb& n = X[o & 1];
-            if (d == 0 && o + 1 < 9) load_nb(o + 1, X[(o + 1) & 1]);
-            if (v + 1 < 27) load_w(v + 1, Wt[(v + 1) & 1]);
-            __builtin_amdgcn_sched_barrier(0);
-            if (d == 0) {
-                const int di = o / 3, dj = o % 3;
+                    for (int t = 0; t < TT; ++t) load_skip<C>(a, s0 + kRows * wq + 16 * t + r, M, g, sk[t]);
+                }
+                int zc[TT], pi[TT], pj[TT];
 #pragma unroll
                 for (int t = 0; t < TT; ++t) {
-                    const bool in =
-                        (unsigned)(pi[t] + di - 1) < (unsigned)H && (unsigned)(pj[t] + dj - 1) < (unsigned)W;
-                    dz[t] = in ? n.z[t] - zc[t] + 1 : 3;  // 0, 1, 2: tap dz - 1; anything else: no tap
+                    const int m = s0 + kRows * wq + 16 * t + r;
+                    const int pix = (m < M ? m : 0) % HW;
+                    pi[t] = pix / W;
+                    pj[t] = pix - pi[t] * W;
+                    zc[t] = zcb[16 * t];
                 }
-            }
-            v4i xm[TT];
-#pragma unroll
-            for (int t = 0; t < TT; ++t) xm[t] = (kin && dz[t] == d) ? n.x[t] : v4i{0, 0, 0, 0};
-#pragma unroll
-            for (int j = 0; j < NB; ++j)
 #pragma unroll
                 for (int t = 0; t < TT; ++t)
-                    acc[t][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(Wt[v & 1][j], xm[t], acc[t][j], 0, 0, 0);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        if (nxt < nseg) fetch(nxt);  // the next window: in flight during the epilogue
-        // the residual inputs of all four tiles are requested before any is used
-        v4f sk[TT][NB];
-        if constexpr (EPI == PMG_EPI_R || EPI == PMG_EPI_RLN || EPI == PMG_EPI_ROUT) {
 #pragma unroll
-            for (int t = 0; t < TT; ++t) load_skip<C>(a, s0 + kColvRows * wv + 16 * t + r, M, g, sk[t]);
-        }
-#pragma unroll
-        for (int t = 0; t < TT; ++t)
-            col_epilogue<int8_t, C, EPI, kptr>(a, acc[t], s0 + kColvRows * wv + 16 * t + r, M, g, kc, sk[t]);
+                    for (int j = 0; j < NB; ++j) acc[t][j] = v4i{0, 0, 0, 0};
 
-        if (nxt < nseg) {
-            __syncthreads();  // every wave is done reading this window
-            commit();
+                // Straight-line over the NSTEP steps, software-pipelined (see above).
+                constexpr int NSTEP = G::NSTEP;
+                auto load_w = [&](int st, v4i (&w)[NB]) {  // st compile-time after unrolling
+#pragma unroll
+                    for (int j = 0; j < NB; ++j) w[j] = *(lds_v4i*)(wb + (st * NB + j) * 1024);
+                };
+                v4i Wt[3][NB];
+                v4i X[NCH][TT];  // codes of the current group's offsets
+                int zz[TT], dz[TT];
+                load_w(0, Wt[0]);
+                load_w(1, Wt[1]);
+#pragma unroll
+                for (int t = 0; t < TT; ++t) {
+                    const v4i xc = *(lds_v4i*)(xcb + 16 * t * ROWB);
+                    X[0][t] = kin ? xc : v4i{0, 0, 0, 0};
+                }
+#pragma unroll
+                for (int t = 0; t < TT; ++t) zz[t] = zg0[16 * t];
+#pragma unroll
+                for (int st = 0; st < NSTEP; ++st) {
+                    const int u = st - 1, gi = u / (3 * NCH), d = (u / NCH) % 3, c = u % NCH;
+                    if (st + 2 < NSTEP) load_w(st + 2, Wt[(st + 2) % 3]);
+                    if (st == 1 + 2 * NCH) {  // group 1's keys, one dz pass ahead
+#pragma unroll
+                        for (int t = 0; t < TT; ++t) zz[t] = zg1[16 * t];
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                    v4i xm[TT];
+                    if (st == 0) {
+#pragma unroll
+                        for (int t = 0; t < TT; ++t) xm[t] = X[0][t];
+                    } else {
+                        if (d == 0 && c == 0) {
+                            const int ri = gi == 0 ? ri0 : ri1, rj = gi == 0 ? rj0 : rj1;
+#pragma unroll
+                            for (int t = 0; t < TT; ++t) {
+                                const bool in =
+                                    (unsigned)(pi[t] + ri) < (unsigned)H && (unsigned)(pj[t] + rj) < (unsigned)W;
+                                dz[t] = in ? zz[t] - zc[t] + 1 : 3;  // 0, 1, 2: tap dz - 1; anything else: none
+                            }
+                        }
+#pragma unroll
+                        for (int t = 0; t < TT; ++t) xm[t] = dz[t] == d ? X[c][t] : v4i{0, 0, 0, 0};
+                    }
+#pragma unroll
+                    for (int j = 0; j < NB; ++j)
+#pragma unroll
+                        for (int t = 0; t < TT; ++t)
+                            acc[t][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(Wt[st % 3][j], xm[t], acc[t][j], 0, 0, 0);
+                    __builtin_amdgcn_sched_barrier(0);
+                    // codes of the next group: after the centre, group 0's; during group 0's last dz pass, group
+                    // 1's chunk c into the registers of group 0's chunk c
+                    if (st == 0) {
+#pragma unroll
+                        for (int cc = 0; cc < NCH; ++cc)
+#pragma unroll
+                            for (int t = 0; t < TT; ++t) X[cc][t] = *(lds_v4i*)(xg0 + 16 * t * ROWB + 16 * cc);
+                    } else if (gi == 0 && d == 2) {
+#pragma unroll
+                        for (int t = 0; t < TT; ++t) X[c][t] = *(lds_v4i*)(xg1 + 16 * t * ROWB + 16 * c);
+                    }
+                }
+            }
+        } else if (kk < nk) {
+            const int s0 = (first + kk * stride) * kSeg;
+            if constexpr (kRes && !kSkipEarly) {
+#pragma unroll
+                for (int t = 0; t < TT; ++t) load_skip<C>(a, s0 + kRows * wq + 16 * t + r, M, g, sk[t]);
+            }
+            if (kk + 1 < nk) commit();  // this group's matrix work on its window ended at the last barrier
+#pragma unroll
+            for (int t = 0; t < TT; ++t)
+                col_epilogue<int8_t, C, EPI, kptr>(a, acc[t], s0 + kRows * wq + 16 * t + r, M, g, kc, sk[t]);
         }
+        __syncthreads();
     }
 }
 
-// Rows on the critical path (the most segments any block walks, times the segment size) for TT tiles per wave.
-static int64_t colv_span(int64_t M, int64_t cus, int tt) {
-    const int64_t seg = 128 * tt, nseg = (M + seg - 1) / seg;
-    return (nseg + cus - 1) / cus * seg;
+// Rows on the critical path (the most segments either group of a block walks, times the segment size).
+static int64_t colv_span(int64_t M, int64_t blocks_max, int seg) {
+    const int64_t nseg = (M + seg - 1) / seg;
+    const int64_t blocks = (nseg + 1) / 2 < blocks_max ? (nseg + 1) / 2 : blocks_max;
+    return (nseg + 2 * blocks - 1) / (2 * blocks) * seg;
+}
+
+template <int C, int EPI, int TT, int WG>
+static int launch_colv_tt(const ColConvArgs& a, hipStream_t s) {
+    typedef ColvGeom<C, TT, WG> G;
+    const int64_t nseg = (a.M + G::kSeg - 1) / G::kSeg;
+    const int64_t cus = num_cus();
+    const unsigned grid = (unsigned)((nseg + 1) / 2 < cus ? (nseg + 1) / 2 : cus);
+    hipLaunchKernelGGL((spconv_colv_k<C, EPI, TT, WG>), dim3(grid), dim3(G::kThreads), 0, s, a);
+    return check_launch("spconv_colv_k");
 }
 
 template <int C, int EPI>
 static int launch_colv(const ColConvArgs& a, hipStream_t s) {
+    // the largest TT (tiles per wave) whose span is within 1/16 of the best: larger segments amortise the window
+    // halo and feed each LDS weight read to more tiles. Registers allow TT = 4 up to C = 32, TT = 2 up to C = 48.
+    constexpr int WG = 4;
     const int64_t cus = num_cus();
-    if constexpr (C == 64) {
-        const int64_t nseg = (a.M + 127) / 128;
-        const unsigned grid = (unsigned)(cus < nseg ? cus : nseg);
-        hipLaunchKernelGGL((spconv_colv_k<C, EPI, 1>), dim3(grid), dim3(kColvThreads), 0, s, a);
-        return check_launch("spconv_colv_k");
-    }
-    // the largest TT whose span is within 1/16 of the best: larger segments amortise the window halo and feed
-    // each LDS weight read to more tiles
-    const int64_t s4 = colv_span(a.M, cus, 4), s2 = colv_span(a.M, cus, 2), s1 = colv_span(a.M, cus, 1);
+    const int64_t s4 = C <= 32 ? colv_span(a.M, cus, 64 * WG) : INT64_MAX;
+    const int64_t s2 = C <= 48 ? colv_span(a.M, cus, 32 * WG) : INT64_MAX;
+    const int64_t s1 = colv_span(a.M, cus, 16 * WG);
     const int64_t best = s4 < s2 ? (s4 < s1 ? s4 : s1) : (s2 < s1 ? s2 : s1);
-    const int tt = s4 * 16 <= best * 17 ? 4 : (s2 * 16 <= best * 17 ? 2 : 1);
-    const int64_t nseg = (a.M + 128 * tt - 1) / (128 * tt);
-    const unsigned grid = (unsigned)(cus < nseg ? cus : nseg);
-    if constexpr (C < 64) {
-        if (tt == 4)
-            hipLaunchKernelGGL((spconv_colv_k<C, EPI, 4>), dim3(grid), dim3(kColvThreads), 0, s, a);
-        else if (tt == 2)
-            hipLaunchKernelGGL((spconv_colv_k<C, EPI, 2>), dim3(grid), dim3(kColvThreads), 0, s, a);
-        else
-            hipLaunchKernelGGL((spconv_colv_k<C, EPI, 1>), dim3(grid), dim3(kColvThreads), 0, s, a);
+    if constexpr (C <= 32) {
+        if (s4 * 16 <= best * 17) return launch_colv_tt<C, EPI, 4, WG>(a, s);
     }
-    return check_launch("spconv_colv_k");
+    if constexpr (C <= 48) {
+        if (s2 * 16 <= best * 17) return launch_colv_tt<C, EPI, 2, WG>(a, s);
+    }
+    return launch_colv_tt<C, EPI, 1, WG>(a, s);
 }
 
 template <int C>
