@@ -199,33 +199,33 @@ constexpr int kG2Chunk = kG2Waves * kG2Tiles * 16;  // 512 rows per block step
 
 // Generic-map int8 convolution for Ci = Co = C in {64, 128}: a persistent block per CU walks chunks of 512 output
 // rows (in `order` if given); each of its 8 waves owns 64 rows (4 tiles of 16) with 4 x C/16 int32 accumulator
-// tiles. Per tap of the chunk's tap union the block stages that tap's C*C weights in LDS in operand order; each
-// LDS operand feeds the wave's 4 tiles (4 MFMAs of 16 cycles), and the next operand is read before they issue.
-// A wave skips the gathers and MFMAs of taps none of its 4 tiles has. Weights, neighbour rows and indices move
-// one tap ahead; an absent neighbour (index -1) becomes an out-of-range buffer offset, which loads zeros.
+// tiles. The 27 taps run in fixed order in groups of GRP taps (4 at C = 64, 2 at C = 128: registers); each
+// group's weights go straight from global memory into LDS in operand order (global_load_lds, no registers), one
+// group ahead and double-buffered, so the block meets at one barrier per group. Each LDS weight operand feeds the
+// wave's 4 tiles (4 MFMAs of 16 cycles) and the next operand is read before they issue. A wave skips the gathers
+// and MFMAs of taps none of its 4 tiles has. Neighbour codes move one tap ahead, indices two; an absent
+// neighbour (index -1) becomes an out-of-range buffer offset, which loads zeros.
 template <int C, int EPI>
 __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
+    constexpr int GRP = C == 64 ? 4 : 2;
     constexpr int NB = C / 16, KS = C / 64, T = kG2Tiles;
-    constexpr int WCH = C * C / 16;           // 16-byte chunks of one tap's weights
-    constexpr int WPT = (WCH + kG2Threads - 1) / kG2Threads;  // per thread
+    constexpr int WCH = C * C / 16;
+    constexpr int WPT = (WCH + kG2Threads - 1) / kG2Threads;
+    constexpr int TAPB = C * C;  // bytes of one tap's weights
     static_assert(C == 64 || C == 128, "C must be 64 or 128");
 
-    __shared__ __attribute__((aligned(16))) uint8_t s_w[2][C * C];
-    __shared__ float s_k[2][C];  // w_scale, bias
-    __shared__ uint32_t s_uni;
+    __shared__ __attribute__((aligned(16))) uint8_t s_w[2][GRP * TAPB];
+    __shared__ float s_k[2][C];
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int r = lane & 15, g = lane >> 4;
     const int M = (int)a.M;
     const int64_t ntile = (a.M + 15) >> 4;
     typedef const __attribute__((address_space(3))) v4i lds_v4i;
-    // Buffer resources: loads past num_records return zeros. The launcher guarantees every byte range fits in
-    // 32 bits.
+    typedef __attribute__((address_space(3))) void lds_void;
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, (int)(a.M * C), kBufWord3);
     const __amdgpu_buffer_rsrc_t nr =
         __builtin_amdgcn_make_buffer_rsrc((void*)a.nmap_t, (short)0, (int)(a.M * 27 * 4), kBufWord3);
-    const __amdgpu_buffer_rsrc_t wr_ =
-        __builtin_amdgcn_make_buffer_rsrc((void*)a.w, (short)0, 27 * C * C, kBufWord3);
 
     for (int e = tid; e < 2 * C; e += kG2Threads) {
         const int q = e / C, n = e - (e / C) * C;
@@ -233,42 +233,40 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
         s_k[q][n] = src ? src[n] : 0.0f;
     }
 
-    // chunk schedule: XCD x = b % 8 takes a contiguous range of chunks, its blocks interleaved within it
     const int nchunk = (M + kG2Chunk - 1) / kG2Chunk;
     const int G = gridDim.x, b = blockIdx.x;
     const int nx = G >= 8 ? 8 : 1;
-    const int x = b % nx, bi = b / nx, nbx = (G - x + nx - 1) / nx;  // blocks on this XCD
+    const int x = b % nx, bi = b / nx, nbx = (G - x + nx - 1) / nx;
     const int c0 = (int)((int64_t)nchunk * x / nx), c1 = (int)((int64_t)nchunk * (x + 1) / nx);
 
-    // Weights of tap v, operand order in LDS: chunk e = tid + k*512 holds lane l = e & 63 of (j, s) = e >> 6, i.e.
-    // W[16j + (l & 15)][v][64s + 16(l >> 4) .. +16] of the [Co][27][Ci] tensor. The lane part of the address is
-    // fixed per thread, the (j, s, v) part is the same for the whole wave (a scalar offset).
-    const int w_lane = (r * 27) * C + 16 * g;
-    auto w_load = [&](int v, v4i (&wr)[WPT]) {
+    // weights of tap v into slot q of buffer bf: chunk e = tid + k*512 holds lane l = e & 63 of operand (j, s) =
+    // e >> 6, i.e. W[16j + (l & 15)][v][64s + 16(l >> 4) .. +16] of the [Co][27][Ci] tensor
+    const uint8_t* wg = (const uint8_t*)a.w + (r * 27) * C + 16 * g;
+    auto w_dma = [&](int v, int bf, int q) {
+        if (v >= 27) return;
 #pragma unroll
         for (int k = 0; k < WPT; ++k) {
             const int js = wv + k * kG2Waves;  // wave-uniform
-            const int j = js / KS, s2 = js - (js / KS) * KS;
-            wr[k] = js < NB * KS ? __builtin_amdgcn_raw_buffer_load_b128(wr_, w_lane, ((16 * j * 27) + v) * C + 64 * s2, 0)
-                                 : v4i{0, 0, 0, 0};
+            if (js < NB * KS) {
+                const int j = js / KS, s2 = js - (js / KS) * KS;
+                __builtin_amdgcn_global_load_lds(wg + ((16 * j * 27) + v) * C + 64 * s2,
+                                                 (lds_void*)(s_w[bf] + q * TAPB + js * 64 * 16), 16, 0, 0);
+            }
         }
     };
-    auto w_store = [&](int buf, const v4i (&wr)[WPT]) {
+    auto group_dma = [&](int grp, int bf) {
 #pragma unroll
-        for (int k = 0; k < WPT; ++k)
-            if (tid + k * kG2Threads < WCH) ((v4i*)s_w[buf])[tid + k * kG2Threads] = wr[k];
+        for (int q = 0; q < GRP; ++q) w_dma(GRP * grp + q, bf, q);
     };
 
     for (int ch = c0 + bi; ch < c1; ch += nbx) {
-        const int pos0 = ch * kG2Chunk + wv * (16 * T) + r;  // position of tile 0's row for this lane
-        // the T rows of this lane: positions pos0 + 16t, through the order if there is one
+        const int pos0 = ch * kG2Chunk + wv * (16 * T) + r;
         int rowi[T];
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             const int p = pos0 + 16 * t;
             rowi[t] = a.order ? (p < M ? a.order[p] : 0) : p;
         }
-        // this wave's taps: the union of its T tiles' masks (uniform)
         uint32_t wmask;
         {
             const int64_t tl = (int64_t)ch * (kG2Chunk / 16) + wv * T + (lane & (T - 1));
@@ -277,107 +275,84 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
             for (int o = 1; o < T; o <<= 1) mk |= __shfl_xor(mk, o, 64);
             wmask = (uint32_t)__builtin_amdgcn_readfirstlane((int)mk);
         }
-        __syncthreads();  // the previous chunk's readers of s_uni and s_w are done
-        if (wv == 0) {
-            const int64_t tl = (int64_t)ch * (kG2Chunk / 16) + (lane & 31);
-            uint32_t mk = (lane < 32 && tl < ntile) ? a.tmask[tl] : 0u;
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) mk |= __shfl_xor(mk, o, 64);
-            if (lane == 0) s_uni = mk & 0x7ffffffu;
-        }
-        __syncthreads();
-        uint32_t rem = s_uni;
         v4i acc[T][NB];
 #pragma unroll
         for (int t = 0; t < T; ++t)
 #pragma unroll
             for (int j = 0; j < NB; ++j) acc[t][j] = v4i{0, 0, 0, 0};
 
-        if (rem) {
-            auto take = [&]() {
-                const int v = rem ? (int)__builtin_ctz(rem) : -1;
-                rem = rem ? rem & (rem - 1) : 0u;
-                return v;
-            };
-            // Rows past M read whatever the map holds there (or zeros past its end): their results are never
-            // stored. Tap -1 (none left) reads index 0s, equally unused.
-            auto mine = [&](int v) { return v >= 0 && ((wmask >> v) & 1u); };
-            auto idx_load = [&](int v, int (&id)[T]) {
-                const int vo = (v < 0 ? 0 : v) * M * 4;  // scalar
+        auto mine = [&](int v) { return v < 27 && ((wmask >> v) & 1u); };
+        auto idx_load = [&](int v, int (&id)[T]) {
+            const int vo = (v < 27 ? v : 0) * M * 4;
 #pragma unroll
-                for (int t = 0; t < T; ++t) id[t] = __builtin_amdgcn_raw_buffer_load_b32(nr, rowi[t] * 4, vo, 0);
-            };
-            auto gather = [&](int v, const int (&id)[T], v4i (&xs)[T][KS]) {
-                if (!mine(v)) return;
+            for (int t = 0; t < T; ++t) id[t] = __builtin_amdgcn_raw_buffer_load_b32(nr, rowi[t] * 4, vo, 0);
+        };
+        auto gather = [&](int v, const int (&id)[T], v4i (&xs)[T][KS]) {
+            if (!mine(v)) return;
 #pragma unroll
-                for (int t = 0; t < T; ++t) {
-                    const int off = id[t] >= 0 ? id[t] * C + 16 * g : (int)0x80000000;
+            for (int t = 0; t < T; ++t) {
+                const int off = id[t] >= 0 ? id[t] * C + 16 * g : (int)0x80000000;
 #pragma unroll
-                    for (int s2 = 0; s2 < KS; ++s2) xs[t][s2] = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 64 * s2, 0);
-                }
-            };
-            // One LDS weight operand feeds the wave's T tiles; the next one is read before they issue.
-            auto mma_tap = [&](int v, int buf, const v4i (&xs)[T][KS]) {
-                if (!mine(v)) return;
-                const uint8_t* wb = s_w[buf] + lane * 16;
-                v4i wop = *(lds_v4i*)(wb);
-#pragma unroll
-                for (int q = 0; q < NB * KS; ++q) {
-                    const int s2 = q / NB, j = q - (q / NB) * NB;
-                    v4i nxt = wop;
-                    if (q + 1 < NB * KS) {
-                        const int s3 = (q + 1) / NB, j3 = (q + 1) - ((q + 1) / NB) * NB;
-                        nxt = *(lds_v4i*)(wb + ((j3 * KS + s3) * 64) * 16);
-                    }
-                    __builtin_amdgcn_sched_barrier(0);  // keep the next operand's read ahead of these MFMAs
-#pragma unroll
-                    for (int t = 0; t < T; ++t)
-                        acc[t][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wop, xs[t][s2], acc[t][j], 0, 0, 0);
-                    __builtin_amdgcn_sched_barrier(0);
-                    wop = nxt;
-                }
-            };
-
-            int v0 = take(), v1 = take();
-            v4i wr[WPT];
-            int idA[T], idB[T];
-            v4i xA[T][KS], xB[T][KS];
-            w_load(v0, wr);
-            idx_load(v0, idA);
-            idx_load(v1, idB);
-            w_store(0, wr);
-            gather(v0, idA, xA);
-            __syncthreads();
-            // invariant at the top: tap v0's weights in s_w[0] and codes in xA; v1's indices in idB
-            for (;;) {
-                // ---- tap v0 (buffer 0), while v1's weights and codes and v2's indices load
-                const int v2 = take();
-                if (v1 >= 0) w_load(v1, wr);
-                gather(v1, idB, xB);
-                idx_load(v2, idA);
-                __builtin_amdgcn_sched_barrier(0);
-                mma_tap(v0, 0, xA);
-                __builtin_amdgcn_sched_barrier(0);
-                if (v1 < 0) break;
-                w_store(1, wr);
-                __syncthreads();
-                // ---- tap v1 (buffer 1), while v2's weights and codes and v3's indices load
-                const int v3 = take();
-                if (v2 >= 0) w_load(v2, wr);
-                gather(v2, idA, xA);
-                idx_load(v3, idB);
-                __builtin_amdgcn_sched_barrier(0);
-                mma_tap(v1, 1, xB);
-                __builtin_amdgcn_sched_barrier(0);
-                if (v2 < 0) break;
-                w_store(0, wr);
-                __syncthreads();
-                v0 = v2;
-                v1 = v3;
+                for (int s2 = 0; s2 < KS; ++s2) xs[t][s2] = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 64 * s2, 0);
             }
+        };
+        auto mma_tap = [&](int v, const uint8_t* wbase, const v4i (&xs)[T][KS]) {
+            if (!mine(v)) return;
+            const uint8_t* wb = wbase + lane * 16;
+            v4i wop = *(lds_v4i*)(wb);
+#pragma unroll
+            for (int q = 0; q < NB * KS; ++q) {
+                const int s2 = q / NB, j = q - (q / NB) * NB;
+                v4i nxt = wop;
+                if (q + 1 < NB * KS) {
+                    const int s3 = (q + 1) / NB, j3 = (q + 1) - ((q + 1) / NB) * NB;
+                    nxt = *(lds_v4i*)(wb + ((j3 * KS + s3) * 64) * 16);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int t = 0; t < T; ++t)
+                    acc[t][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wop, xs[t][s2], acc[t][j], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                wop = nxt;
+            }
+        };
+
+        __syncthreads();  // the previous chunk's readers of s_w are done
+        group_dma(0, 0);
+        int idA[T], idB[T];
+        v4i xA[T][KS], xB[T][KS];
+        idx_load(0, idA);
+        idx_load(1, idB);
+        gather(0, idA, xA);
+        __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) & lgkmcnt(0): group 0 in LDS, tap 0 gathered
+        __syncthreads();
+        constexpr int NG = (27 + GRP - 1) / GRP;  // the last group's last slot (tap 27) is empty
+#pragma unroll 1
+        for (int grp = 0; grp < NG; ++grp) {
+            const int bf = grp & 1;
+            if (grp + 1 < NG) group_dma(grp + 1, bf ^ 1);  // the other buffer: free since the last barrier
+            // taps 3 grp + q; the gathers and indices run one and two taps ahead
+#pragma unroll
+            for (int q = 0; q < GRP; ++q) {
+                const int v = GRP * grp + q;
+                // even taps' codes in xA, odd taps' in xB (v & 1 == q: compile-time)
+                if ((q & 1) == 0) {
+                    gather(v + 1, idB, xB);
+                    idx_load(v + 2, idA);
+                    __builtin_amdgcn_sched_barrier(0);
+                    mma_tap(v, s_w[bf] + q * TAPB, xA);
+                } else {
+                    gather(v + 1, idA, xA);
+                    idx_load(v + 2, idB);
+                    __builtin_amdgcn_sched_barrier(0);
+                    mma_tap(v, s_w[bf] + q * TAPB, xB);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            __builtin_amdgcn_s_waitcnt(0);  // this wave's part of the next group is in LDS (and the next codes)
+            __syncthreads();
         }
 
-        // ---- epilogue: lane holds channels 16j + 4g + i of row rowi[t] (position pos0 + 16t)
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             if (pos0 + 16 * t >= M) continue;
