@@ -6,7 +6,7 @@
 //       thr = kthvalue(r, min(k, N));  w = mask & (r <= thr)
 //
 // Design. One persistent kernel per batch item with few, fat blocks (256 threads x 32 elements = 8192 elements each,
-// held in registers for the whole fit, so HBM is read once): a device-wide barrier costs more the more blocks
+// or x 16 up to 2^19 elements; held in registers for the whole fit, so HBM is read once): a device-wide barrier costs more the more blocks
 // arrive (about 1.7 us at 38 blocks, 7.5 us at 256 on MI355X), and a trim round is latency-bound, not
 // bandwidth-bound. Phases are separated by a self-resetting barrier. Sums are accumulated in fp64
 // (n*sxx - sx^2 cancels badly in fp32) in a fixed order, and every block reduces the published per-block partials
@@ -39,8 +39,8 @@ namespace pmg {
 
 constexpr int kFitThreads = 256;
 constexpr int kFitWaves = kFitThreads / 64;
-constexpr int kFitEPT = 32;                            // elements per thread, in registers
-constexpr int kFitPerBlock = kFitThreads * kFitEPT;    // 8192
+constexpr int kFitEPTMax = 32;                         // elements per thread, in registers (16 or 32)
+constexpr int kFitPerBlockMax = kFitThreads * kFitEPTMax;  // 8192
 constexpr int kFitMaxBlocks = kFitThreads;             // N <= 2^21
 constexpr int kFitBins = 2048;
 constexpr int kCandCap = 32768;                        // candidates every block holds in LDS (128 KiB)
@@ -56,9 +56,9 @@ struct FitWs {
     uint64_t* partials;   // [2][kFitMaxBlocks][5] fp64 bit patterns
     unsigned* counts;     // [2][kFitMaxBlocks][2]: below, candidates
     unsigned* hist;       // [iters][3][kFitBins]
-    uint32_t* c_key;      // [2][nb][kFitPerBlock]: residual bits | mask << 31
-    float* c_z;           // [2][nb][kFitPerBlock]
-    float* c_t;           // [2][nb][kFitPerBlock]
+    uint32_t* c_key;      // [2][nb][elements per block]: residual bits | mask << 31
+    float* c_z;           // [2][nb][elements per block]
+    float* c_t;           // [2][nb][elements per block]
 };
 
 struct FitArgs {
@@ -228,7 +228,10 @@ __device__ inline void find_bin(FitShared& sh, unsigned rank, Load load) {
     __syncthreads();
 }
 
+template <int kFitEPT>
 __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
+    constexpr int kFitPerBlock = kFitThreads * kFitEPT;
+    static_assert(kFitEPT <= 32, "element masks are 32-bit");
     __shared__ FitShared sh;
     const int nb = (int)gridDim.x, b = (int)blockIdx.x, tid = (int)threadIdx.x;
     const FitWs& ws = a.ws;
@@ -750,35 +753,48 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
     }
 }
 
-static int fit_blocks(int64_t N) { return (int)((N + kFitPerBlock - 1) / kFitPerBlock); }
+// Elements per thread: 16 up to 2^19 elements (twice the blocks: faster loads and per-block passes, while the
+// device-wide barrier still costs little), else 32.
+static int fit_ept(int64_t N) { return N <= (int64_t(1) << 19) ? 16 : 32; }
+static int fit_blocks(int64_t N) {
+    const int64_t per = (int64_t)kFitThreads * fit_ept(N);
+    return (int)((N + per - 1) / per);
+}
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 size_t fit_workspace_bytes(int64_t N, int iters) {
-    const size_t nb = (size_t)fit_blocks(N > 0 ? N : 1);
+    const int64_t n = N > 0 ? N : 1;
+    const size_t nb = (size_t)fit_blocks(n);
     const size_t hist = (size_t)(iters > 0 ? iters : 1) * 3 * kFitBins * sizeof(unsigned);
-    const size_t cand = 2 * nb * kFitPerBlock * sizeof(uint32_t);
+    const size_t cand = 2 * nb * (size_t)kFitThreads * fit_ept(n) * sizeof(uint32_t);
     return kFitHeader + align256(2 * kFitMaxBlocks * 5 * sizeof(uint64_t)) + align256(2 * kFitMaxBlocks * 2 * sizeof(unsigned)) +
            align256(hist) + 3 * align256(cand);
 }
 
 int launch_fit(const FitLaunch& f, hipStream_t s) {
-    PMG_REQUIRE(f.N > 0 && f.N <= (int64_t)kFitMaxBlocks * kFitPerBlock, "N must be in [1, 2^21]");
+    PMG_REQUIRE(f.N > 0 && f.N <= (int64_t)kFitMaxBlocks * kFitPerBlockMax, "N must be in [1, 2^21]");
     PMG_REQUIRE(f.iters >= 0 && f.iters <= 64, "iters must be in [0, 64]");
     PMG_REQUIRE(f.min_points >= 1, "min_points must be >= 1");
     PMG_REQUIRE(f.trim >= 0.0f && f.trim < 1.0f, "trim must be in [0, 1)");
     PMG_REQUIRE(f.workspace && f.workspace_bytes >= fit_workspace_bytes(f.N, f.iters), "workspace too small");
     PMG_REQUIRE(aligned16(f.workspace), "workspace must be 16-byte aligned");
     const int nb = fit_blocks(f.N);
-    static int max_resident = -1;
-    if (max_resident < 0) {
+    const int ept = fit_ept(f.N);
+    static int max_resident[2] = {-1, -1};
+    int& mr = max_resident[ept == 16 ? 0 : 1];
+    if (mr < 0) {
         int per_cu = 0;
-        PMG_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fit_k, kFitThreads, 0));
-        max_resident = per_cu * num_cus();
+        if (ept == 16)
+            PMG_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fit_k<16>, kFitThreads, 0));
+        else
+            PMG_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fit_k<32>, kFitThreads, 0));
+        mr = per_cu * num_cus();
     }
-    PMG_REQUIRE(nb <= max_resident && nb <= kFitMaxBlocks,
+    const int max_resident_n = mr;
+    PMG_REQUIRE(nb <= max_resident_n && nb <= kFitMaxBlocks,
                 "fit grid of " + std::to_string(nb) + " blocks cannot be resident (max " +
-                    std::to_string(max_resident) + ")");
+                    std::to_string(max_resident_n) + ")");
     uint8_t* p = (uint8_t*)f.workspace;
     FitWs ws;
     ws.bar = (unsigned*)p;
@@ -791,14 +807,17 @@ int launch_fit(const FitLaunch& f, hipStream_t s) {
     p += align256(2 * kFitMaxBlocks * 2 * sizeof(unsigned));
     ws.hist = (unsigned*)p;
     p += align256((size_t)(f.iters > 0 ? f.iters : 1) * 3 * kFitBins * sizeof(unsigned));
-    const size_t cand = align256(2 * (size_t)nb * kFitPerBlock * sizeof(uint32_t));
+    const size_t cand = align256(2 * (size_t)nb * kFitThreads * ept * sizeof(uint32_t));
     ws.c_key = (uint32_t*)p;
     ws.c_z = (float*)(p + cand);
     ws.c_t = (float*)(p + 2 * cand);
     for (int b = 0; b < f.B; ++b) {
         FitArgs a{f.mode, f.z, f.tg, f.mask, f.logz, f.stride, f.lidar, f.conf, f.H, f.W, f.dh, f.dw,
                   f.N, f.iters, (float)(1.0 - (double)f.trim), f.min_points, b, f.st, f.info, ws};
-        hipLaunchKernelGGL(fit_k, dim3(nb), dim3(kFitThreads), 0, s, a);
+        if (ept == 16)
+            hipLaunchKernelGGL(fit_k<16>, dim3(nb), dim3(kFitThreads), 0, s, a);
+        else
+            hipLaunchKernelGGL(fit_k<32>, dim3(nb), dim3(kFitThreads), 0, s, a);
         if (int e = check_launch("fit_k")) return e;
     }
     return PMG_OK;
@@ -847,7 +866,7 @@ size_t final_fit_workspace_bytes(int B, int dh, int dw, int iters) {
 int launch_final_fit(const FinalFit& f, hipStream_t s) {
     PMG_REQUIRE(f.logz && f.lidar && f.conf && f.st, "null buffer");
     PMG_REQUIRE(f.B >= 1 && f.H >= 1 && f.W >= 1 && f.dh >= 1 && f.dw >= 1 && f.stride >= 1, "bad shape");
-    PMG_REQUIRE((int64_t)f.dh * f.dw <= (int64_t)kFitMaxBlocks * kFitPerBlock, "LiDAR map larger than 2^21 pixels");
+    PMG_REQUIRE((int64_t)f.dh * f.dw <= (int64_t)kFitMaxBlocks * kFitPerBlockMax, "LiDAR map larger than 2^21 pixels");
     PMG_REQUIRE(f.workspace && f.workspace_bytes >= final_fit_workspace_bytes(f.B, f.dh, f.dw, f.iters),
                 "workspace too small");
     const int64_t N = (int64_t)f.dh * f.dw;
