@@ -102,9 +102,30 @@ __device__ inline void prompt_feats(const InputArgs& a, int b, int i, int j, flo
     res = (lda - logz) * gate;
 }
 
+// One wave per 16 rows, lane (r, g) holds channels 16j + 4g + i of row r. The per-channel constants (input_proj,
+// prompt_proj, LayerNorm) are staged in LDS once per block; the prompt features of a row are computed by its
+// lane-group-0 lane and passed to the row's other lanes.
 template <int C, bool F16>
 __global__ __launch_bounds__(256) void input_stage_k(InputArgs a) {
     constexpr int NB = C / 16;
+    __shared__ __attribute__((aligned(16))) float s_c[10 * C];  // in_w [C][3], in_b, pr_w [C][2], pr_b, gamma, beta
+    for (int e = threadIdx.x; e < 10 * C; e += 256) {
+        float v;
+        if (e < 3 * C) v = a.in_w[e];
+        else if (e < 4 * C) v = a.in_b[e - 3 * C];
+        else if (e < 6 * C) v = a.use_prompt ? a.pr_w[e - 4 * C] : 0.0f;
+        else if (e < 7 * C) v = a.use_prompt ? a.pr_b[e - 6 * C] : 0.0f;
+        else if (e < 8 * C) v = a.gamma[e - 7 * C];
+        else if (e < 9 * C) v = a.beta[e - 8 * C];
+        else v = 0.0f;
+        s_c[e] = v;
+    }
+    const float* c_inw = s_c;
+    const float* c_inb = s_c + 3 * C;
+    const float* c_prw = s_c + 4 * C;
+    const float* c_prb = s_c + 6 * C;
+    const float* c_gam = s_c + 7 * C;
+    const float* c_bet = s_c + 8 * C;
     const int64_t M = (int64_t)a.B * a.H * a.W;
     const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
     const int64_t m = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 16 + r;
@@ -118,42 +139,59 @@ __global__ __launch_bounds__(256) void input_stage_k(InputArgs a) {
         res = a.prompt_in[mo * 2];
         gate = a.prompt_in[mo * 2 + 1];
     } else if (a.use_prompt) {
-        const int64_t HW = (int64_t)a.H * a.W;
-        const int b = (int)(mo / HW);
-        const int p = (int)(mo - b * HW);
-        const int i = p / a.W, j = p - (p / a.W) * a.W;
-        prompt_feats(a, b, i, j, f2, res, gate);
+        if (g == 0) {
+            const int64_t HW = (int64_t)a.H * a.W;
+            const int b = (int)(mo / HW);
+            const int p = (int)(mo - b * HW);
+            const int i = p / a.W, j = p - (p / a.W) * a.W;
+            prompt_feats(a, b, i, j, f2, res, gate);
+        }
+        res = __shfl(res, r, 64);  // lane r (group 0) holds row r's values
+        gate = __shfl(gate, r, 64);
     }
+    __syncthreads();  // constants staged
+    const bool prompt = a.use_prompt;
     float y[NB][4];
 #pragma unroll
-    for (int j = 0; j < NB; ++j)
+    for (int j = 0; j < NB; ++j) {
+        const int n0 = 16 * j + 4 * g;
+        const float4 w0 = *(const float4*)(c_inw + 3 * n0), w1 = *(const float4*)(c_inw + 3 * n0 + 4);
+        const float4 w2 = *(const float4*)(c_inw + 3 * n0 + 8);
+        const float wi[12] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w, w2.x, w2.y, w2.z, w2.w};
+        const float4 bi = *(const float4*)(c_inb + n0);
+        const float4 p0 = *(const float4*)(c_prw + 2 * n0), p1 = *(const float4*)(c_prw + 2 * n0 + 4);
+        const float pw[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+        const float4 pb = *(const float4*)(c_prb + n0);
+        const float bb[4] = {bi.x, bi.y, bi.z, bi.w}, pbb[4] = {pb.x, pb.y, pb.z, pb.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int n = 16 * j + 4 * g + i;
-            float t = a.in_b[n] + a.in_w[3 * n] * f0;
-            t = t + a.in_w[3 * n + 1] * f1;
-            t = t + a.in_w[3 * n + 2] * f2;
-            if (a.use_prompt) {
-                float pp = a.pr_b[n] + a.pr_w[2 * n] * res;
-                pp = pp + a.pr_w[2 * n + 1] * gate;
+            float t = bb[i] + wi[3 * i] * f0;
+            t = t + wi[3 * i + 1] * f1;
+            t = t + wi[3 * i + 2] * f2;
+            if (prompt) {
+                float pp = pbb[i] + pw[2 * i] * res;
+                pp = pp + pw[2 * i + 1] * gate;
                 t = t + pp;
             }
             y[j][i] = t;
         }
+    }
     if (ok) {
 #pragma unroll
         for (int j = 0; j < NB; ++j)
             *(float4*)(a.x_out + mo * C + 16 * j + 4 * g) = make_float4(y[j][0], y[j][1], y[j][2], y[j][3]);
     }
-    ln_silu_quad<NB, F16>(y, a.gamma, a.beta, a.eps, g);
+    typedef const __attribute__((address_space(3))) float* kptr;
+    ln_silu_quad<NB, F16, kptr>(y, (kptr)c_gam, (kptr)c_bet, a.eps, g);
     if (!ok) return;
+    if constexpr (F16) {
 #pragma unroll
-    for (int j = 0; j < NB; ++j) {
-        const int64_t o = mo * C + 16 * j + 4 * g;
-        if constexpr (F16)
-            store_half4(y[j], (_Float16*)a.q_out + o);
-        else
-            store_silu_codes4(y[j], a.out_mult, (int8_t*)a.q_out + o);
+        for (int j = 0; j < NB; ++j) store_half4(y[j], (_Float16*)a.q_out + mo * C + 16 * j + 4 * g);
+    } else {
+        uint32_t pk[NB];
+        silu_codes_packed<NB>(y, a.out_mult, pk);
+#pragma unroll
+        for (int j = 0; j < NB; ++j) *(uint32_t*)((int8_t*)a.q_out + mo * C + 16 * j + 4 * g) = pk[j];
     }
 }
 
