@@ -18,7 +18,8 @@ captured HIP graph of that chain; the metric fit of the refined depth is timed s
     conv_microbench  isolated int8 conv on 1,000,000 surface voxels in 1024^3, C = 64 and 128
     measured_peaks   this device's practical HBM copy bandwidth and int8 MFMA rate (pmg_probe_copy / _mfma_i8);
               `roofline.frac` is against the published 8 TB/s, `roofline.frac_measured` against the copy probe
-    other_configs    one K-step frame of the fp16 teacher (T) and of the hi-res config (H, with nearest_fill)
+    other_configs    one K-step frame of the fp16 teacher (T) and of the hi-res config (H, with nearest_fill); the
+              first U-Net level step of Model A (pool cache, mean pool, nearest upsampling: pool_L0)
 
 Other modes (used to produce the committed profiles):
     --kernels-only     launch each per-step kernel --kernel-reps times eagerly (plus a 64 MiB copy for counter
@@ -343,6 +344,47 @@ def frame_bench(name, stream, reps=10):
     return out
 
 
+def pool_bench(stream, reps=20):
+    """The first U-Net level step of Model A (flex_sparse_blocks.py:78-105): the 307,200 level-0 voxels pooled by 2
+    (pool cache: sort, unique, parent, segments -- with the host read of the output count the reference also
+    makes), the C=48 mean pooling, and the nearest upsampling back."""
+    import numpy as np
+    import torch
+
+    from promptmoge_amd import ops, spec
+
+    dev = torch.device("cuda:0")
+    cfg = spec.CONFIGS["A"]
+    sc = spec.make_scene(cfg)
+    with torch.cuda.stream(stream):
+        # level-0 voxels (v3.py:305-344) from the GPU voxeliser: (0, i, j, zq - zmin) in raster order
+        P = torch.from_numpy(sc.points[None].copy()).to(dev)
+        zq, zmin, zmax = ops.voxelize(P[..., 2:], 256.0, stride=3, shape=(1, cfg.H, cfg.W))
+        Z = int(zmax[0] - zmin[0]) + 1
+        ii, jj = torch.meshgrid(torch.arange(cfg.H, device=dev), torch.arange(cfg.W, device=dev), indexing="ij")
+        ct = torch.stack([torch.zeros_like(ii), ii, jj, (zq[0] - zmin[0]).long()], -1).reshape(-1, 4)
+        ct = ct.to(torch.int32).contiguous()
+        shape = (1, cfg.H, cfg.W, Z)
+        osh = [1, (cfg.H + 1) // 2, (cfg.W + 1) // 2, (Z + 1) // 2]
+        f = torch.from_numpy(np.random.default_rng(1).normal(size=(cfg.M, cfg.C)).astype(np.float32)).to(dev)
+        oc, parent, seg, offs = ops.pool_cache(ct, shape, (2, 2, 2), osh)
+        n = oc.shape[0]
+        times = []
+        for _ in range(reps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            ops.pool_cache(ct, shape, (2, 2, 2), osh)
+            times.append((time.perf_counter() - t0) * 1e3)
+        pooled = ops.sparse_pool(f, seg, offs, n)
+        pool_ms = graph_ms(lambda: ops.sparse_pool(f, seg, offs, n), 20, stream)
+        up_ms = graph_ms(lambda: ops.sparse_upsample(pooled, parent), 20, stream)
+    return {"workload": f"A level 0 -> 1: {cfg.M} voxels pooled by 2 -> {n}, C={cfg.C} fp32 mean pool, nearest up",
+            "voxels_in": cfg.M, "voxels_out": int(n), "cache_ms": round(statistics.median(times), 4),
+            "pool_ms": round(pool_ms, 4), "upsample_ms": round(up_ms, 4),
+            "pool_gbs": round((cfg.M * cfg.C * 4 + n * cfg.C * 4 + cfg.M * 4 + n * 8) / (pool_ms * 1e-3) / 1e9, 1),
+            "upsample_gbs": round((cfg.M * cfg.C * 4 * 2 + cfg.M * 4) / (up_ms * 1e-3) / 1e9, 1)}
+
+
 def cpu_baseline(env):
     from oracle import refiner as orf
 
@@ -450,6 +492,8 @@ def main() -> int:
         for Cm in ("C64", "C128"):
             micro[Cm]["frac_measured_int8"] = round(micro[Cm]["tops"] / peaks["int8_mfma_tops"], 4)
     others = None if args.no_others else {n: frame_bench(n, stream) for n in ("T", "H")}
+    if others is not None:
+        others["pool_L0"] = pool_bench(stream)
     cpu = None if args.no_cpu else cpu_baseline(env)
 
     line = {

@@ -100,6 +100,30 @@ size_t pmg_row_order_workspace_bytes(int64_t M);
 int pmg_row_order(const uint32_t* row_mask, int64_t M, int32_t* order, uint32_t* order_tile_mask, void* workspace,
                   size_t workspace_bytes, void* stream);
 
+/* pmg_pool_cache -- build_pool_cache (promptmoge/_fallback/flex_gemm/_core.py:339-395) for the perfect-partition
+ * pool MoGe uses (kernel == stride, padding 0), output coordinates not given: the output voxels are the distinct
+ * floor(coords / stride) in increasing _linearise order on the output grid (_core.py:89-94). coords [M][4] int32
+ * (b, x, y, z) inside sparse_shape (host int64[4]); stride host int32[3]; out_sparse_shape host int64[4] (the
+ * batch extent unchanged). Outputs (device, capacity M): out_coords [num_out][4], parent [M] (input row -> output
+ * row), seg_indices [M] (stable argsort of parent), seg_offsets [num_out + 1] (int64); counts [2] int64 on the
+ * device: num_out, and the number of input voxels outside sparse_shape (then the cache is not valid). */
+size_t pmg_pool_cache_workspace_bytes(int64_t M);
+int pmg_pool_cache(const int32_t* coords, int64_t M, const int64_t* sparse_shape, const int32_t* stride,
+                   const int64_t* out_sparse_shape, int32_t* out_coords, int32_t* parent, int32_t* seg_indices,
+                   int64_t* seg_offsets, int64_t* counts, void* workspace, size_t workspace_bytes, void* stream);
+
+/* pmg_sparse_pool -- sparse_pool (_core.py:444-481) on a pool cache: out[r] = sum of feats[seg_indices[k]],
+ * k in [seg_offsets[r], seg_offsets[r+1]), accumulated in that (input) order in fp32 like the reference's
+ * index_add_, divided by the group size for reduce = 1 ('mean'); reduce = 0 is 'sum'. feats [M][C] fp32, C a
+ * multiple of 4; out [num_out][C]. */
+int pmg_sparse_pool(const float* feats, int64_t M, int C, const int32_t* seg_indices, const int64_t* seg_offsets,
+                    int64_t num_out, int reduce, float* out, void* stream);
+
+/* pmg_sparse_upsample -- sparse_upsample 'nearest' (_core.py:484-505) with the transposed pool cache:
+ * out[i] = feats[parent[i]] for rows of row_bytes bytes (a multiple of 16; any element type). */
+int pmg_sparse_upsample(const void* feats, int64_t row_bytes, const int32_t* parent, int64_t rows_out, void* out,
+                        void* stream);
+
 /* pmg_nmap_from_rows -- a caller-supplied (M, 27) map (a NeighborCache.nmap, _core.py:131-176) into the tap-major
  * layout and tile masks the convolutions read. */
 int pmg_nmap_from_rows(const int32_t* nmap_rows, int64_t M, int32_t* nmap_t, uint32_t* tile_mask, void* stream);

@@ -14,6 +14,8 @@ Modules
   fit        fit_scale_shift (prompt_stem.py:211-240): fp64-sum form (what the kernel computes) and the literal fp32
              form of the reference
   fill       nearest_fill (promptmoge/model.py:61-72): the exact EDT feature transform in two separable passes
+  pool       build_pool_cache / sparse_pool / sparse_upsample (_core.py:339-505): perfect-partition pooling with
+             sorted unique output keys, mean/sum in input order, nearest upsampling by parent
   refiner    the fused step (v3.py:346-383, 547-576; sparse_unet.py:176-258 single level; flex_sparse_blocks.py:70-75)
              in the deployed int8 / fp16 arithmetic, and the reference's fp32 fake-quant (QAT) formulation
 

@@ -4,8 +4,9 @@ MI355X kernels of libpmg.so: neighbour maps from the GPU column stencil or the G
 Same names, argument meaning, return values and error style as the reference, so that `promptmoge/model.py:29-30`
 selects this package when it is importable as `flex_gemm` (see `promptmoge_amd.flex_gemm.install`). Every
 computation runs in libpmg.so; there is no CPU path (the library raises if it is missing). Supported: 3x3x3
-kernels, dilation 1, one batch dimension -- what MoGe's refiner uses. Pooling and upsampling (the multi-level U-Net
-rows) are not built yet and raise NotImplementedError.
+kernels, dilation 1, one batch dimension -- what MoGe's refiner uses -- and the perfect-partition pooling and
+nearest upsampling of its multi-level U-Net (build_pool_cache with output coordinates given raises
+NotImplementedError: MoGe does not use that branch).
 """
 from __future__ import annotations
 
@@ -253,16 +254,71 @@ def submanifold_conv(feats: Tensor, coords: Tensor, shape: torch.Size, weight: T
     return out.to(out_dtype).contiguous(), neighbor_cache
 
 
-def build_pool_cache(*_args, **_kwargs):
-    """Perfect-partition pooling map (_core.py:339-398): not built yet (multi-level U-Net)."""
-    raise NotImplementedError("libpmg does not implement sparse pooling yet (single-level refiner only)")
+def build_pool_cache(coords: Tensor, sparse_shape: Sequence[int], kernel_size: Sequence[int], stride: Sequence[int],
+                     padding: Sequence[int], output_coords: Optional[Tensor] = None,
+                     output_sparse_shape: Optional[Sequence[int]] = None) -> NeighborCache:
+    """Perfect-partition pool cache (_core.py:339-395): output coords = the unique floor(coord / stride) in
+    increasing _linearise order, `parent` (input row -> output row), `seg_indices` (stable argsort of parent) and
+    `seg_offsets`, built on the GPU (pmg_pool_cache). Only kernel == stride and padding == 0, as the reference;
+    given output coordinates (the reference's lookup branch, which MoGe does not use) raise NotImplementedError."""
+    D = len(kernel_size)
+    assert tuple(kernel_size) == tuple(stride), "only kernel == stride supported"
+    assert all(p == 0 for p in padding), "only padding == 0 supported"
+    batch_dims = coords.shape[1] - D
+    if D != 3 or batch_dims != 1:
+        raise NotImplementedError("libpmg pooling expects coords (b, x, y, z)")
+    if output_sparse_shape is None:
+        output_sparse_shape = [int(s) if d < batch_dims else -(-int(s) // int(stride[d - batch_dims]))
+                               for d, s in enumerate(sparse_shape)]
+    if output_coords is not None:
+        raise NotImplementedError("libpmg pooling builds its output coordinates (output_coords must be None)")
+    coords_i = coords.to(torch.int32).contiguous()
+    out_coords, parent, seg, offs = _ops.pool_cache(coords_i, [int(v) for v in sparse_shape],
+                                                    [int(v) for v in stride], [int(v) for v in output_sparse_shape])
+    return NeighborCache(coords, out_coords.to(coords.dtype), seg_indices=seg, seg_offsets=offs, parent=parent,
+                         kernel_size=tuple(kernel_size), stride=tuple(stride), input_sparse_shape=sparse_shape,
+                         output_sparse_shape=output_sparse_shape)
 
 
-def sparse_pool(*_args, **_kwargs):
-    """Sparse pooling (_core.py:444-481): not built yet (multi-level U-Net)."""
-    raise NotImplementedError("libpmg does not implement sparse pooling yet (single-level refiner only)")
+def sparse_pool(feats: Tensor, coords: Tensor, shape: torch.Size, kernel_size, stride=None, padding=None,
+                reduce: str = "mean", output_coords: Optional[Tensor] = None, output_shape: Optional[torch.Size] = None,
+                neighbor_cache: Optional[NeighborCache] = None):
+    """Sparse pooling (_core.py:444-481) -> (feats (N, C), out_coords, out_shape, neighbor_cache). 'mean' and
+    'sum'; the rows of each output are summed in input order in fp32 (for fp32 features: the reference's
+    index_add_ bit for bit), then divided by the group size for 'mean'."""
+    D = len(kernel_size)
+    stride = tuple(stride) if stride is not None else tuple(kernel_size)
+    padding = tuple(padding) if padding is not None else (0,) * D
+    sparse_dim = coords.shape[1]
+    sparse_in = tuple(shape[:sparse_dim])
+    sparse_out = tuple(output_shape[:sparse_dim]) if output_shape is not None else None
+    if reduce not in ("mean", "sum"):
+        raise NotImplementedError(f"reduce={reduce!r} not needed by MoGe")
+    if neighbor_cache is None:
+        neighbor_cache = build_pool_cache(coords, sparse_in, kernel_size, stride, padding, output_coords, sparse_out)
+    out_coords = neighbor_cache.output_coords
+    num_out = int(out_coords.shape[0])
+    C = feats.shape[1]
+    x = _pad_to(feats.detach().float().contiguous(), 1, 4)
+    acc = _ops.sparse_pool(x, neighbor_cache.seg_indices, neighbor_cache.seg_offsets, num_out, reduce)
+    acc = acc[:, :C].to(feats.dtype).contiguous()
+    out_shape = torch.Size([*neighbor_cache.output_sparse_shape, C])
+    return acc, out_coords, out_shape, neighbor_cache
 
 
-def sparse_upsample(*_args, **_kwargs):
-    """Nearest sparse upsampling (_core.py:484-505): not built yet (multi-level U-Net)."""
-    raise NotImplementedError("libpmg does not implement sparse upsampling yet (single-level refiner only)")
+def sparse_upsample(feats: Tensor, coords: Tensor, shape: torch.Size, scale_factor, *, mode: str = "nearest",
+                    output_coords: Optional[Tensor] = None, output_shape: Optional[torch.Size] = None,
+                    neighbor_cache=None, **_ignored):
+    """Nearest sparse upsampling with the transposed pool cache (_core.py:484-505): out[i] = feats[parent[i]]."""
+    assert mode == "nearest", "MoGe only uses nearest upsampling"
+    assert neighbor_cache is not None and neighbor_cache.is_transposed, (
+        "reference path requires the transposed pool cache (MoGe always supplies it)")
+    assert output_coords is not None
+    parent = neighbor_cache.parent
+    assert parent.shape[0] == output_coords.shape[0]
+    C = feats.shape[1]
+    unit = max(1, 16 // feats.element_size())
+    x = _pad_to(feats.detach().contiguous(), 1, unit)
+    out = _ops.sparse_upsample(x, parent.to(torch.int32).contiguous())[:, :C].contiguous()
+    out_shape = torch.Size([*tuple(output_shape[: output_coords.shape[1]]), C])
+    return out, output_coords, out_shape, neighbor_cache

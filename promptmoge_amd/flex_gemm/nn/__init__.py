@@ -2,8 +2,7 @@
 
 `SubmanifoldConv3d` must be THIS class for QAT wrapping (qat.py:126-129) and owns `weight` (Co, k, k, k, Ci) and
 `bias` (Co,) parameters initialised like the reference's, so checkpoints and `torch.nn.utils.parametrize` work
-unchanged. The pooling/upsampling modules construct (so models build) but their forward raises until the
-multi-level rows are built."""
+unchanged. SparsePool3d / SparseUpsample3d run the GPU pooling and nearest upsampling of _core.py."""
 from __future__ import annotations
 
 import math

@@ -125,6 +125,57 @@ def row_order(row_mask: torch.Tensor):
     return order, otm
 
 
+def pool_cache(coords: torch.Tensor, sparse_shape: Sequence[int], stride: Sequence[int],
+               out_sparse_shape: Sequence[int]):
+    """build_pool_cache (_core.py:339-395), perfect partition, output coordinates not given. Returns
+    (out_coords [N, 4] int32, parent [M] int32, seg_indices [M] int32, seg_offsets [N + 1] int64). Reads the
+    output count back to the host once (the reference's int(...) sync)."""
+    coords = _dev(coords, "coords", torch.int32)
+    if coords.ndim != 2 or coords.shape[1] != 4:
+        raise ValueError("coords must be (M, 4)")
+    M = coords.shape[0]
+    dev = coords.device
+    oc = torch.empty((max(M, 1), 4), dtype=torch.int32, device=dev)
+    parent = torch.empty((M,), dtype=torch.int32, device=dev)
+    seg = torch.empty((M,), dtype=torch.int32, device=dev)
+    offs = torch.empty((M + 1,), dtype=torch.int64, device=dev)
+    counts = torch.empty((2,), dtype=torch.int64, device=dev)
+    ws_bytes = lib().pmg_pool_cache_workspace_bytes(M)
+    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
+    shp = (C.c_int64 * 4)(*[int(v) for v in sparse_shape[:4]])
+    st = (C.c_int32 * 3)(*[int(v) for v in stride[:3]])
+    osh = (C.c_int64 * 4)(*[int(v) for v in out_sparse_shape[:4]])
+    call("pmg_pool_cache", _p(coords), M, shp, st, osh, _p(oc), _p(parent), _p(seg), _p(offs), _p(counts), _p(ws),
+         ws_bytes, _stream())
+    n, bad = (int(v) for v in counts.cpu())
+    if bad:
+        raise ValueError(f"pool_cache: {bad} voxels lie outside the sparse shape {tuple(sparse_shape[:4])}")
+    return oc[:n], parent, seg, offs[:n + 1]
+
+
+def sparse_pool(feats: torch.Tensor, seg_indices: torch.Tensor, seg_offsets: torch.Tensor, num_out: int,
+                reduce: str = "mean") -> torch.Tensor:
+    """sparse_pool's reduction (_core.py:464-476) over a pool cache: fp32 sums in input order, / group size."""
+    if reduce not in ("mean", "sum"):
+        raise NotImplementedError(f"reduce={reduce!r} not needed by MoGe")
+    feats = _dev(feats, "feats", torch.float32)
+    M, Cc = feats.shape
+    out = torch.empty((num_out, Cc), dtype=torch.float32, device=feats.device)
+    call("pmg_sparse_pool", _p(feats), M, Cc, _p(seg_indices), _p(seg_offsets), num_out, 1 if reduce == "mean" else 0,
+         _p(out), _stream())
+    return out
+
+
+def sparse_upsample(feats: torch.Tensor, parent: torch.Tensor) -> torch.Tensor:
+    """Nearest upsampling (_core.py:484-505): out[i] = feats[parent[i]]."""
+    feats = _dev(feats, "feats")
+    parent = _dev(parent, "parent", torch.int32)
+    out = torch.empty((parent.shape[0],) + tuple(feats.shape[1:]), dtype=feats.dtype, device=feats.device)
+    row_bytes = feats[0].numel() * feats.element_size() if feats.shape[0] else 16
+    call("pmg_sparse_upsample", _p(feats), row_bytes, _p(parent), parent.shape[0], _p(out), _stream())
+    return out
+
+
 def nmap_from_rows(nmap_rows: torch.Tensor):
     """(M, 27) map -> (nmap_t [27, M], tile_mask)."""
     nmap_rows = _dev(nmap_rows, "nmap_rows", torch.int32)

@@ -49,14 +49,25 @@ def test_conv_module_parameters_and_init():
     assert [n for n, _ in m.named_parameters()] == ["weight", "bias"]
 
 
-def test_pool_and_upsample_construct_but_are_not_built():
+def test_pool_and_upsample_modules_and_interface_errors():
     p = fg.nn.SparsePool3d(2)
     u = fg.nn.SparseUpsample3d(2)
-    assert p.kernel_size == (2, 2, 2) and p.stride == (2, 2, 2) and u.scale_factor == (2, 2, 2)
+    assert p.kernel_size == (2, 2, 2) and p.stride == (2, 2, 2) and p.reduce == "mean" and u.scale_factor == (2, 2, 2)
+    coords = torch.zeros((1, 4), dtype=torch.int32)
+    # the reference's assertions (_core.py:349-350, 490-494), raised before any device work
+    with pytest.raises(AssertionError):
+        fg.ops.build_pool_cache(coords, (1, 4, 4, 4), (2, 2, 2), (3, 3, 3), (0, 0, 0))
+    with pytest.raises(AssertionError):
+        fg.ops.build_pool_cache(coords, (1, 4, 4, 4), (2, 2, 2), (2, 2, 2), (1, 1, 1))
     with pytest.raises(NotImplementedError):
-        p(torch.zeros(1, 4), torch.zeros(1, 4, dtype=torch.int32), torch.Size([1, 2, 2, 2, 4]))
+        fg.ops.build_pool_cache(coords, (1, 4, 4, 4), (2, 2, 2), (2, 2, 2), (0, 0, 0), output_coords=coords)
     with pytest.raises(NotImplementedError):
-        fg.ops.build_pool_cache(None)
+        fg.ops.sparse_pool(torch.zeros(1, 4), coords, torch.Size([1, 4, 4, 4, 4]), (2, 2, 2), reduce="max")
+    with pytest.raises(AssertionError):
+        fg.ops.sparse_upsample(torch.zeros(1, 4), coords, torch.Size([1, 2, 2, 2, 4]), (2, 2, 2),
+                               output_coords=coords, neighbor_cache=None)
+    with pytest.raises(ValueError):  # coords on the CPU: the library wants device tensors
+        fg.ops.build_pool_cache(coords, (1, 4, 4, 4), (2, 2, 2), (2, 2, 2), (0, 0, 0))
 
 
 def test_unsupported_kernels_rejected_before_any_device_work():
