@@ -7,8 +7,8 @@
 //
 // Design. One persistent kernel per batch item with few, fat blocks (256 threads x 32 elements = 8192 elements each,
 // or x 16 up to 2^19 elements; held in registers for the whole fit, so HBM is read once): a device-wide barrier costs more the more blocks
-// arrive (about 1.7 us at 38 blocks, 7.5 us at 256 on MI355X), and a trim round is latency-bound, not
-// bandwidth-bound. Phases are separated by a self-resetting barrier. Sums are accumulated in fp64
+// arrive, and a trim round is latency-bound, not bandwidth-bound. Phases are separated by a device-wide barrier of
+// per-block flags (fit_barrier). Sums are accumulated in fp64
 // (n*sxx - sx^2 cancels badly in fp32) in a fixed order, and every block reduces the published per-block partials
 // itself, so all blocks hold bit-identical (s, t) and take identical branches.
 //
@@ -28,8 +28,9 @@
 // it exactly, so the loop stops there with the bit-identical result (on the synthetic scenes after 3 rounds).
 // This replaces the reference device engine's approximate two-level histogram (MetricFit.metal:141-189).
 //
-// Workspace: zero-filled once before its first use; the kernel leaves it reusable (the barrier returns to zero,
-// histograms are cleared at the start of every launch, everything else is overwritten before it is read).
+// Workspace: zero-filled once before its first use; the kernel leaves it reusable (the barrier flags and their
+// epoch only grow, histograms are cleared at the start of every launch, everything else is overwritten before it is
+// read).
 #include <climits>
 
 #include "pmg_common.h"
@@ -49,7 +50,8 @@ constexpr int kFitTraceRounds = 64;
 constexpr size_t kFitHeader = 4096;                    // barrier, error flag, trace
 
 struct FitWs {
-    unsigned* bar;        // [0] arrivals, [1] generation
+    unsigned* bar;        // [2]: the synchronisation epoch (the last flag value of the previous launch)
+    unsigned* flags;      // [kFitMaxBlocks][16]: each block's arrival count, one 64-byte line per block
     int* err;
     uint32_t* trace;      // block 0's record: per round the selection path | candidates << 4 and the wall clock
                           // (100 MHz) at its end, per round the threshold bits; launch and first-solve times
@@ -81,25 +83,27 @@ struct FitArgs {
     FitWs ws;
 };
 
-// Device-wide barrier for a fully resident grid. The last block to arrive resets the arrival count and bumps the
-// generation; the others wait (bounded) for the generation to move. Global writes before it are visible after it.
-__device__ inline void fit_barrier(unsigned* bar, unsigned nb, int* err) {
+// Device-wide barrier for a fully resident grid, by per-block flags: block b's thread 0 publishes (release, agent
+// scope) the barrier's sequence number in its own flag line; thread t < nb waits (bounded) until block t's flag has
+// reached it, then acquires. Global writes before it are visible after it. Flag values only grow within a launch
+// and across launches (the epoch in bar[2]), so a block that is already one barrier ahead still satisfies a late
+// waiter; every data buffer exchanged across a barrier is double-buffered, so that block cannot overwrite what the
+// late waiter is about to read. Half the cost of a central arrival counter (no serialised read-modify-write, and
+// every waiter polls one line in parallel with the others).
+__device__ inline void fit_barrier(const FitWs& ws, unsigned nb, unsigned want) {
     __syncthreads();
     if (threadIdx.x == 0) {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        const unsigned gen = __hip_atomic_load(&bar[1], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
-        const unsigned old = __hip_atomic_fetch_add(&bar[0], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        if (old == nb - 1) {
-            __hip_atomic_store(&bar[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_fetch_add(&bar[1], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-        } else if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) {
-            unsigned spins = 0;
-            while (__hip_atomic_load(&bar[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gen) {
-                __builtin_amdgcn_s_sleep(1);
-                if (++spins > (1u << 23)) {
-                    __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    break;
-                }
+        __hip_atomic_store(&ws.flags[blockIdx.x * 16], want, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (threadIdx.x < nb && __hip_atomic_load(ws.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) {
+        unsigned spins = 0;
+        while ((int)(__hip_atomic_load(&ws.flags[threadIdx.x * 16], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) -
+                     want) < 0) {
+            __builtin_amdgcn_s_sleep(1);
+            if (++spins > (1u << 23)) {
+                __hip_atomic_store(ws.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
             }
         }
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
@@ -236,6 +240,9 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
     const int nb = (int)gridDim.x, b = (int)blockIdx.x, tid = (int)threadIdx.x;
     const FitWs& ws = a.ws;
     const int64_t cap_words = (int64_t)nb * kFitPerBlock;
+    // barrier sequence numbers continue from the previous launch's last one (every block performs the same
+    // barriers; block 0 advances the epoch when it is done, after every block has read it here)
+    unsigned sync_seq = __hip_atomic_load(&ws.bar[2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
     if (b == 0 && tid == 0) ws.trace[2 * kFitTraceRounds + 1] = (uint32_t)wall_clock64();  // launch start
     // clear this launch's global histograms; the first barrier orders this before any use
@@ -393,7 +400,7 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
         FIT_MARK0(0);
         publish(v, 0u, 0u);
         FIT_MARK0(1);
-        fit_barrier(ws.bar, nb, ws.err);
+        fit_barrier(ws, nb, ++sync_seq);
         FIT_MARK0(2);
         double g[5];
         gather_partials(g);
@@ -467,7 +474,7 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
             }
             publish(v, packed_total >> 16, ncb);
             FIT_MARK(1);
-            fit_barrier(ws.bar, nb, ws.err);
+            fit_barrier(ws, nb, ++sync_seq);
             FIT_MARK(2);
             load_partials();
             // totals and region offsets, in block order
@@ -654,7 +661,7 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
                     unsigned* gh = ws.hist + ((int64_t)it * 3 + pass) * kFitBins;
                     for (int q = tid; q < kFitBins; q += kFitThreads)
                         if (sh.hist[q]) atomicAdd(&gh[q], sh.hist[q]);
-                    fit_barrier(ws.bar, nb, ws.err);
+                    fit_barrier(ws, nb, ++sync_seq);
                     find_bin(sh, rank, [&](int q) {
                         return __hip_atomic_load(&gh[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     });
@@ -690,7 +697,7 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
             unsigned* gh = ws.hist + ((int64_t)it * 3 + 2) * kFitBins;
             for (int q = tid; q < 1024; q += kFitThreads)
                 if (sh.hist[q]) atomicAdd(&gh[q], sh.hist[q]);
-            fit_barrier(ws.bar, nb, ws.err);
+            fit_barrier(ws, nb, ++sync_seq);
             find_bin(sh, rank, [&](int q) {
                 return __hip_atomic_load(&gh[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             });
@@ -708,7 +715,7 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
                 }
             }
             publish(v, 0u, 0u);
-            fit_barrier(ws.bar, nb, ws.err);
+            fit_barrier(ws, nb, ++sync_seq);
             double g[5];
             gather_partials(g);
             ++stage;
@@ -744,6 +751,7 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
     }
 
     if (b == 0 && tid == 0) {
+        __hip_atomic_store(&ws.bar[2], sync_seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         a.st[2 * a.b] = s;
         a.st[2 * a.b + 1] = t;
         if (a.info) {
@@ -768,7 +776,8 @@ size_t fit_workspace_bytes(int64_t N, int iters) {
     const size_t nb = (size_t)fit_blocks(n);
     const size_t hist = (size_t)(iters > 0 ? iters : 1) * 3 * kFitBins * sizeof(unsigned);
     const size_t cand = 2 * nb * (size_t)kFitThreads * fit_ept(n) * sizeof(uint32_t);
-    return kFitHeader + align256(2 * kFitMaxBlocks * 5 * sizeof(uint64_t)) + align256(2 * kFitMaxBlocks * 2 * sizeof(unsigned)) +
+    return kFitHeader + align256(kFitMaxBlocks * 64) + align256(2 * kFitMaxBlocks * 5 * sizeof(uint64_t)) +
+           align256(2 * kFitMaxBlocks * 2 * sizeof(unsigned)) +
            align256(hist) + 3 * align256(cand);
 }
 
@@ -801,6 +810,8 @@ int launch_fit(const FitLaunch& f, hipStream_t s) {
     ws.err = (int*)(p + 64);
     ws.trace = (uint32_t*)(p + 128);
     p += kFitHeader;
+    ws.flags = (unsigned*)p;
+    p += align256(kFitMaxBlocks * 64);
     ws.partials = (uint64_t*)p;
     p += align256(2 * kFitMaxBlocks * 5 * sizeof(uint64_t));
     ws.counts = (unsigned*)p;
