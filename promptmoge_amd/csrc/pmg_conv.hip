@@ -16,6 +16,8 @@
 //
 // Rows are gathered straight from global memory into registers (16-byte loads hit L2 for the image-local
 // neighbourhoods of level 0); the weights, at most 27*Co*Ci elements, stay L1/L2 resident.
+#include <type_traits>
+
 #include "pmg_common.h"
 
 namespace pmg {
@@ -183,14 +185,20 @@ static int pick_nb(int Co) {
 // int8, Ci = Co = C in {64, 128}: block-tiled, weight-staged variant for large maps (the 1M-voxel microbench).
 //
 // A persistent 8-wave block owns chunks of 512 output rows (64 rows per wave in four 16-row tiles) and all C output
-// channels. It walks the chunk's union of active taps (OR of its 32 tile masks). For each tap the whole block stages
-// that tap's C x C weights in LDS in MFMA operand order (one 1 KB block per 16 output channels and 64-wide K step:
-// conflict-free 16-byte reads), double-buffered so the next tap's weights load while this tap's MFMAs run. Every
-// wave gathers its rows' neighbour codes x[nmap[v][m]] straight from global memory, two taps ahead for the map
-// indices and one tap ahead for the codes, so the dependent index -> code loads overlap the matrix work. Each LDS
-// weight read feeds four tiles, each gathered chunk NB column blocks. Operands are swapped (D = W * X^T): a lane
-// ends with 4 consecutive output channels of one row and the epilogue stores vectors. Chunks are assigned so that
-// the blocks of one XCD (block b runs on XCD b % 8) process adjacent row ranges and share their neighbours in L2.
+// channels. The taps' C x C weights pass through LDS in MFMA operand order (one 1 KB block per 16 output channels
+// and 64-wide K step: conflict-free 16-byte reads), a group of taps at a time, double-buffered. Every wave gathers
+// its rows' neighbour codes x[nmap[v][m]] straight from global memory into registers one tap ahead, and the map
+// indices three taps ahead. Each LDS weight read feeds four tiles, each gathered chunk NB column blocks. Operands
+// are swapped (D = W * X^T): a lane ends with 4 consecutive output channels of one row and the epilogue stores
+// vectors. Chunks are assigned so that the blocks of one XCD (block b runs on XCD b % 8) process adjacent row
+// ranges and share their neighbours in L2.
+//
+// Every global load of the tap loop is issued unconditionally and none goes straight to LDS, so the compiler's
+// vmcnt waits name exactly the load they need: an MFMA waits for its own tap's codes, not for the loads issued
+// after them (an LDS-DMA weight load made every weight read wait for all outstanding loads, and a branch around a
+// gather made the waits at the join conservative). Counters show the kernel limited by the L1 path of the gathers
+// (texture data unit busy 75 % at C = 128, most of it waiting on the cache; each 512-row chunk gathers ~27 times
+// its own rows), not by the gather latency: a three-tap-deep gather ring at C = 64 was no faster.
 constexpr int kBufWord3 = 0x00020000;  // buffer descriptor word 3 for raw (untyped) loads on gfx9
 constexpr int kG2Threads = 512;       // 8 waves: two per SIMD, 256 registers each
 constexpr int kG2Waves = kG2Threads / 64;
@@ -199,22 +207,23 @@ constexpr int kG2Chunk = kG2Waves * kG2Tiles * 16;  // 512 rows per block step
 
 // Generic-map int8 convolution for Ci = Co = C in {64, 128}: a persistent block per CU walks chunks of 512 output
 // rows (in `order` if given); each of its 8 waves owns 64 rows (4 tiles of 16) with 4 x C/16 int32 accumulator
-// tiles. The 27 taps run in fixed order in groups of GRP taps (4 at C = 64, 2 at C = 128: registers); each
-// group's weights go straight from global memory into LDS in operand order (global_load_lds, no registers), one
-// group ahead and double-buffered, so the block meets at one barrier per group. Each LDS weight operand feeds the
-// wave's 4 tiles (4 MFMAs of 16 cycles) and the next operand is read before they issue. A wave skips the gathers
-// and MFMAs of taps none of its 4 tiles has. Neighbour codes move one tap ahead, indices two; an absent
-// neighbour (index -1) becomes an out-of-range buffer offset, which loads zeros.
+// tiles. The 27 taps run in fixed order in groups of GRP taps (4 at C = 64, 2 at C = 128: registers); the next
+// group's weights are loaded into registers during this group and stored into the other LDS buffer, so the block
+// meets at one barrier per group. Each LDS weight operand feeds the wave's 4 tiles (4 MFMAs of 16 cycles) and the
+// next operand is read before they issue. A wave skips the MFMAs of taps none of its 4 tiles has; an absent
+// neighbour (index -1), and every index of such a tap, becomes an out-of-range buffer offset, which loads zeros.
 template <int C, int EPI>
 __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
     constexpr int GRP = C == 64 ? 4 : 2;
     constexpr int NB = C / 16, KS = C / 64, T = kG2Tiles;
-    constexpr int WCH = C * C / 16;
-    constexpr int WPT = (WCH + kG2Threads - 1) / kG2Threads;
-    constexpr int TAPB = C * C;  // bytes of one tap's weights
+    constexpr int NF = NB * KS;                          // 1 KB operand fragments per tap
+    constexpr int WPT = GRP * NF / kG2Waves;             // fragments staged per wave per group
+    constexpr int NG = (27 + GRP - 1) / GRP;             // tap groups; taps >= 27 of the last one are empty
+    constexpr int NG2 = (NG + 1) / 2;                    // loop trips of two groups (one per LDS buffer)
     static_assert(C == 64 || C == 128, "C must be 64 or 128");
+    static_assert(GRP * NF % kG2Waves == 0, "staging split");
 
-    __shared__ __attribute__((aligned(16))) uint8_t s_w[2][GRP * TAPB];
+    __shared__ __attribute__((aligned(16))) v4i s_w[2][GRP * NF * 64];
     __shared__ float s_k[2][C];
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -222,10 +231,10 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
     const int M = (int)a.M;
     const int64_t ntile = (a.M + 15) >> 4;
     typedef const __attribute__((address_space(3))) v4i lds_v4i;
-    typedef __attribute__((address_space(3))) void lds_void;
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, (int)(a.M * C), kBufWord3);
     const __amdgpu_buffer_rsrc_t nr =
         __builtin_amdgcn_make_buffer_rsrc((void*)a.nmap_t, (short)0, (int)(a.M * 27 * 4), kBufWord3);
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc((void*)a.w, (short)0, C * 27 * C, kBufWord3);
 
     for (int e = tid; e < 2 * C; e += kG2Threads) {
         const int q = e / C, n = e - (e / C) * C;
@@ -239,33 +248,37 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
     const int x = b % nx, bi = b / nx, nbx = (G - x + nx - 1) / nx;
     const int c0 = (int)((int64_t)nchunk * x / nx), c1 = (int)((int64_t)nchunk * (x + 1) / nx);
 
-    // weights of tap v into slot q of buffer bf: chunk e = tid + k*512 holds lane l = e & 63 of operand (j, s) =
-    // e >> 6, i.e. W[16j + (l & 15)][v][64s + 16(l >> 4) .. +16] of the [Co][27][Ci] tensor
-    const uint8_t* wg = (const uint8_t*)a.w + (r * 27) * C + 16 * g;
-    auto w_dma = [&](int v, int bf, int q) {
-        if (v >= 27) return;
+    // Weights of group grp through registers into LDS (no LDS DMA: the compiler then keeps exact vmcnt waits for
+    // the gathers). Fragment f = wv + 8k of the group is tap slot q = f / NF, operand js = f % NF = (j, s), and
+    // lane l holds W[16j + (l & 15)][v][64s + 16(l >> 4) .. +16] of the [Co][27][Ci] tensor; taps >= 27 load zeros
+    // (out-of-range buffer offset).
+    const int wlane = (r * 27) * C + 16 * g;
+    // staged in PARTS pieces of WPP fragments per wave, one piece per tap of the group where that divides evenly
+    // (C = 128: 8 registers held for one tap instead of 16 for the whole group)
+    constexpr int PARTS = WPT % GRP == 0 ? GRP : 1, WPP = WPT / PARTS;
+    auto w_load = [&](int grp, int part, v4i (&st)[WPP]) {
 #pragma unroll
-        for (int k = 0; k < WPT; ++k) {
-            const int js = wv + k * kG2Waves;  // wave-uniform
-            if (js < NB * KS) {
-                const int j = js / KS, s2 = js - (js / KS) * KS;
-                __builtin_amdgcn_global_load_lds(wg + ((16 * j * 27) + v) * C + 64 * s2,
-                                                 (lds_void*)(s_w[bf] + q * TAPB + js * 64 * 16), 16, 0, 0);
-            }
+        for (int kk = 0; kk < WPP; ++kk) {
+            const int f = wv + kG2Waves * (part * WPP + kk);
+            const int q = f / NF, js = f - (f / NF) * NF;
+            const int j = js / KS, s2 = js - (js / KS) * KS;
+            const int v = GRP * grp + q;
+            const int off = v < 27 ? wlane + ((16 * j * 27) + v) * C + 64 * s2 : (int)0x80000000;
+            st[kk] = __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 0);
         }
     };
-    auto group_dma = [&](int grp, int bf) {
+    auto w_store = [&](v4i* dst, int part, const v4i (&st)[WPP]) {
 #pragma unroll
-        for (int q = 0; q < GRP; ++q) w_dma(GRP * grp + q, bf, q);
+        for (int kk = 0; kk < WPP; ++kk) dst[(wv + kG2Waves * (part * WPP + kk)) * 64 + lane] = st[kk];
     };
 
     for (int ch = c0 + bi; ch < c1; ch += nbx) {
         const int pos0 = ch * kG2Chunk + wv * (16 * T) + r;
-        int rowi[T];
+        int roff[T];
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             const int p = pos0 + 16 * t;
-            rowi[t] = a.order ? (p < M ? a.order[p] : 0) : p;
+            roff[t] = 4 * (a.order ? (p < M ? a.order[p] : 0) : p);
         }
         uint32_t wmask;
         {
@@ -281,14 +294,14 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
 #pragma unroll
             for (int j = 0; j < NB; ++j) acc[t][j] = v4i{0, 0, 0, 0};
 
-        auto mine = [&](int v) { return v < 27 && ((wmask >> v) & 1u); };
+        // map indices of tap v (taps >= 27: out-of-range, zeros); gathers of the rows they name (absent: zeros).
+        // Every load is issued unconditionally, so the compiler's vmcnt waits stay exact.
         auto idx_load = [&](int v, int (&id)[T]) {
-            const int vo = (v < 27 ? v : 0) * M * 4;
+            const int vo = (v < 27 ? v : 27) * M * 4;
 #pragma unroll
-            for (int t = 0; t < T; ++t) id[t] = __builtin_amdgcn_raw_buffer_load_b32(nr, rowi[t] * 4, vo, 0);
+            for (int t = 0; t < T; ++t) id[t] = __builtin_amdgcn_raw_buffer_load_b32(nr, roff[t], vo, 0);
         };
-        auto gather = [&](int v, const int (&id)[T], v4i (&xs)[T][KS]) {
-            if (!mine(v)) return;
+        auto gather = [&](const int (&id)[T], v4i (&xs)[T][KS]) {
 #pragma unroll
             for (int t = 0; t < T; ++t) {
                 const int off = id[t] >= 0 ? id[t] * C + 16 * g : (int)0x80000000;
@@ -296,17 +309,16 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
                 for (int s2 = 0; s2 < KS; ++s2) xs[t][s2] = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 64 * s2, 0);
             }
         };
-        auto mma_tap = [&](int v, const uint8_t* wbase, const v4i (&xs)[T][KS]) {
-            if (!mine(v)) return;
-            const uint8_t* wb = wbase + lane * 16;
+        auto mma_tap = [&](const v4i* wslot, const v4i (&xs)[T][KS]) {
+            const v4i* wb = wslot + lane;
             v4i wop = *(lds_v4i*)(wb);
 #pragma unroll
-            for (int q = 0; q < NB * KS; ++q) {
+            for (int q = 0; q < NF; ++q) {
                 const int s2 = q / NB, j = q - (q / NB) * NB;
                 v4i nxt = wop;
-                if (q + 1 < NB * KS) {
+                if (q + 1 < NF) {
                     const int s3 = (q + 1) / NB, j3 = (q + 1) - ((q + 1) / NB) * NB;
-                    nxt = *(lds_v4i*)(wb + ((j3 * KS + s3) * 64) * 16);
+                    nxt = *(lds_v4i*)(wb + (j3 * KS + s3) * 64);
                 }
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -317,46 +329,58 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
             }
         };
 
-        __syncthreads();  // the previous chunk's readers of s_w are done
-        group_dma(0, 0);
-        int idA[T], idB[T];
-        v4i xA[T][KS], xB[T][KS];
-        idx_load(0, idA);
-        idx_load(1, idB);
-        gather(0, idA, xA);
-        __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) & lgkmcnt(0): group 0 in LDS, tap 0 gathered
-        __syncthreads();
-        constexpr int NG = (27 + GRP - 1) / GRP;  // the last group's last slot (tap 27) is empty
-#pragma unroll 1
-        for (int grp = 0; grp < NG; ++grp) {
-            const int bf = grp & 1;
-            if (grp + 1 < NG) group_dma(grp + 1, bf ^ 1);  // the other buffer: free since the last barrier
-            // taps 3 grp + q; the gathers and indices run one and two taps ahead
+        int I[2][T];  // indices three taps ahead: tap v+3 reuses the slot that tap v+1's gather just read
+        v4i X[2][T][KS];
+#pragma unroll
+        for (int part = 0; part < PARTS; ++part) {
+            v4i st[WPP];
+            w_load(0, part, st);
+            w_store(s_w[0], part, st);
+        }
+        {
+            int i0[T];
+            idx_load(0, i0);
+            idx_load(1, I[1]);
+            idx_load(2, I[0]);
+            gather(i0, X[0]);
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's weight stores are in LDS
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+
+        // One group: weights of the next group are loaded at its start and stored into the other buffer at its end
+        // (every wave left that buffer at the last barrier); per tap v, the codes of tap v+1 and the indices of
+        // tap v+3 are requested before tap v's MFMAs. H = the buffer (group parity), compile-time, so the X and I
+        // ring slots are too.
+        auto group = [&](auto Hc, int grp) {
+            constexpr int H = decltype(Hc)::value;
 #pragma unroll
             for (int q = 0; q < GRP; ++q) {
                 const int v = GRP * grp + q;
-                // even taps' codes in xA, odd taps' in xB (v & 1 == q: compile-time)
-                if ((q & 1) == 0) {
-                    gather(v + 1, idB, xB);
-                    idx_load(v + 2, idA);
-                    __builtin_amdgcn_sched_barrier(0);
-                    mma_tap(v, s_w[bf] + q * TAPB, xA);
-                } else {
-                    gather(v + 1, idA, xA);
-                    idx_load(v + 2, idB);
-                    __builtin_amdgcn_sched_barrier(0);
-                    mma_tap(v, s_w[bf] + q * TAPB, xB);
-                }
+                const int p = (GRP * H + q) & 3;  // v mod 4 (GRP * grp = 4 * trip + GRP * H)
+                v4i st[WPP];
+                if (q < PARTS) w_load(grp + 1, q, st);
+                gather(I[(p + 1) & 1], X[(p + 1) & 1]);
+                idx_load(v + 3, I[(p + 1) & 1]);
                 __builtin_amdgcn_sched_barrier(0);
+                if (v < 27 && ((wmask >> v) & 1u)) mma_tap(s_w[H] + q * NF * 64, X[p & 1]);
+                __builtin_amdgcn_sched_barrier(0);
+                if (q < PARTS) w_store(s_w[H ^ 1], q, st);
             }
-            __builtin_amdgcn_s_waitcnt(0);  // this wave's part of the next group is in LDS (and the next codes)
-            __syncthreads();
+            __builtin_amdgcn_s_waitcnt(0xc07f);
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+        };
+#pragma unroll 1
+        for (int it = 0; it < NG2; ++it) {
+            group(std::integral_constant<int, 0>{}, 2 * it);
+            group(std::integral_constant<int, 1>{}, 2 * it + 1);
         }
 
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             if (pos0 + 16 * t >= M) continue;
-            const int m = rowi[t];
+            const int m = roff[t] >> 2;
 #pragma unroll
             for (int j = 0; j < NB; ++j) {
                 const int64_t o = (int64_t)m * C + 16 * j + 4 * g;
