@@ -283,7 +283,9 @@ int pmg_nearest_fill(const float* depth, const float* conf, int B, int h, int w,
  * The fused refiner step -- replaces one iteration of the refine loop (v3.py:547-576) for a single-level
  * refiner: prompt fit -> prompt residual/gate -> voxelise -> column neighbour map -> input_proj (+ prompt_proj)
  * -> n_blocks residual blocks (LN, SiLU, conv1, SiLU, conv2, + skip) -> out_proj -> logz += delta
- * (_refine_logz, v3.py:346-360), then optionally the metric fit on the refined depth. All on `stream`, no host
+ * (_refine_logz, v3.py:346-360; scaled by the output gate if configured) -> optionally the elastic anchor (a
+ * second prompt-style fit on the refined depth, then the per-pixel pull toward the LiDAR, v3.py:570-573), then
+ * optionally the metric fit on the refined depth. All on `stream`, no host
  * synchronisation; the sequence is captured once into a HIP graph and replayed while the buffers and the stream
  * are unchanged (on the legacy default stream, which cannot be captured, it is enqueued eagerly).
  * ------------------------------------------------------------------------------------------------------------ */
@@ -303,6 +305,11 @@ typedef struct {
     int soft_gate;          /* soft_residual_gate (v3.py:379-382) */
     int final_fit;          /* also run the final metric fit (pmg_fit_final) on the refined depth */
     int use_graph;          /* capture the step into a HIP graph and replay it */
+    int output_gate;        /* refiner_output_gate (v3.py:565-569): logz + g * delta, g = floor + (1 - floor) * u,
+                               u the LiDAR uncertainty of the pixel (v3.py:386-393) */
+    float output_gate_floor;/* output_gate_floor, 0.1 */
+    float anchor;           /* anchor_strength beta (v3.py:570-573): after the update, logz moves by
+                               beta * gate * (log_d_aff - logz) with the LiDAR re-fitted to the refined depth; 0 = off */
 } pmg_refiner_config;
 
 typedef struct {

@@ -7,7 +7,9 @@ Step order (moge/model/v3.py:547-576 with _lidar_in_affine_frame 362-383 and _re
   3. voxelise + level-0 neighbour map
   4. Sparse3DUNet, single level (sparse_unet.py:189-192, 258): h = input_proj(feats) + prompt_proj(residual, gate);
      SparseResBlock3d x n (flex_sparse_blocks.py:229-234); out_proj
-  5. logz += out
+  5. logz += out; with the output gate (v3.py:565-569) logz = cur + g * ((cur + out) - cur), g = floor + (1 - floor)
+     * u, u = _lidar_uncertainty (v3.py:386-393); with the elastic anchor beta > 0 (v3.py:570-573) the prompt fit
+     is repeated on the refined depth and logz += beta * gate * (log_d_aff - logz) (hard gate)
   6. optionally the same fit on the refined depth
 
 `step` computes the blocks in the deployed integer arithmetic (the QAT contract qat.py:1-16 as executed by
@@ -117,8 +119,39 @@ def blocks_fp16(x, nmap, w, trace=None):
     return x
 
 
+def lidar_uncertainty(d, c):
+    """_lidar_uncertainty (v3.py:386-393) on nearest-resized d, c [B, H, W]: 1 - c * (1 - range_uncertainty(d)),
+    range_uncertainty = clamp((d - 3) / (5 - 3), 0, 1) (prompt_stem.py:28-29, 41-42); 1 where d is not a value."""
+    valid = np.isfinite(d) & (d > 0)
+    with np.errstate(invalid="ignore"):
+        ru = np.clip((np.where(valid, d, F32(0.0)) - F32(3.0)) / F32(2.0), F32(0.0), F32(1.0))
+    u = F32(1.0) - c * (F32(1.0) - ru)
+    return np.where(valid, u, F32(1.0)).astype(np.float32)
+
+
+def output_gate(cur, refined, d, c, floor=0.1):
+    """v3.py:567-569: cur + g * (refined - cur), g = floor + (1.0 - floor) * u; the two Python-float constants are
+    rounded to fp32 by the tensor arithmetic."""
+    g = F32(floor) + F32(1.0 - floor) * lidar_uncertainty(d, c)
+    return (cur + g * (refined - cur)).astype(np.float32)
+
+
+def anchor_pull(logz, d, c, s, t, beta):
+    """v3.py:570-573 with _lidar_in_affine_frame's hard gate: logz + beta * gate * (log_d_aff - logz)."""
+    s_ = np.asarray(s, dtype=np.float32)[:, None, None]
+    t_ = np.asarray(t, dtype=np.float32)[:, None, None]
+    valid = np.isfinite(d) & (d > 0)
+    with np.errstate(invalid="ignore", over="ignore"):
+        daff = (d - t_) / np.maximum(s_, F32(1e-6))
+    ok = valid & (daff > F32(1e-4))
+    lda = np.where(ok, log_f32(np.maximum(np.where(ok, daff, F32(1.0)), F32(1e-4))), logz)
+    gate = c * ok.astype(np.float32)
+    return (logz + (F32(beta) * gate) * (lda - logz)).astype(np.float32)
+
+
 def step(points, lidar, conf, w, *, precision="int8", iters=10, trim=0.2, min_points=32, use_prompt=True,
-         soft_gate=False, final_fit=False, resolution=256.0, trace: Optional[dict] = None):
+         soft_gate=False, final_fit=False, resolution=256.0, output_gate_on=False, gate_floor=0.1, anchor=0.0,
+         trace: Optional[dict] = None):
     """Returns (refined points [B, H, W, 3], (s, t) prompt fit, (s, t) final fit or None)."""
     pts = np.array(points, dtype=np.float32, copy=True)
     B, H, W, _ = pts.shape
@@ -136,7 +169,16 @@ def step(points, lidar, conf, w, *, precision="int8", iters=10, trim=0.2, min_po
     blk_trace = [] if trace is not None else None
     x = (blocks_int8 if precision == "int8" else blocks_fp16)(x, nmap, w, blk_trace)
     delta = out_proj(x, w)
+    cur = pts[..., 2].copy()
     pts[..., 2] = pts[..., 2] + delta.reshape(B, H, W)
+    if output_gate_on or anchor > 0:
+        _, _, _, d_, c_ = prompt_inputs(pts, lidar, conf)
+    if output_gate_on:
+        pts[..., 2] = output_gate(cur, pts[..., 2], d_, c_, gate_floor)
+    if anchor > 0:
+        z, tg, m, _, _ = prompt_inputs(pts, lidar, conf)
+        sa = fit_f64(z, tg, m, iters, trim, min_points)
+        pts[..., 2] = anchor_pull(pts[..., 2], d_, c_, sa[0], sa[1], anchor)
     fin = None
     if final_fit:  # v3.py:768-778, at LiDAR resolution
         z, tg, m = final_inputs(pts, lidar, conf)

@@ -38,6 +38,7 @@ class RefinerConfig(C.Structure):
         ("B", i32), ("H", i32), ("W", i32), ("C", i32), ("n_blocks", i32), ("precision", i32),
         ("depth_resolution", f32), ("dh", i32), ("dw", i32), ("fit_iters", i32), ("fit_trim", f32),
         ("fit_min_points", i32), ("use_prompt", i32), ("soft_gate", i32), ("final_fit", i32), ("use_graph", i32),
+        ("output_gate", i32), ("output_gate_floor", f32), ("anchor", f32),
     ]
 
 

@@ -95,7 +95,8 @@ constexpr size_t kMaxGraphs = 4;
 // Residual blocks: conv1 (bias, SiLU, requantise) then conv2 (bias, skip, and either the next block's
 // LayerNorm/SiLU/quantise or, after the last block, out_proj and either the log-depth update of the point map or
 // the module's (M, 1) output). Expects x and q1 from the input stage.
-static int enqueue_blocks(pmg_refiner* r, const float* points, float* points_out, float* delta_out, hipStream_t s) {
+static int enqueue_blocks(pmg_refiner* r, const float* points, float* points_out, float* delta_out, hipStream_t s,
+                          const float* gate_lidar = nullptr, const float* gate_conf = nullptr) {
     const pmg_refiner_config& c = r->cfg;
     const int prec = c.precision == PMG_PREC_FP16 ? PMG_PREC_FP16 : PMG_PREC_INT8;
     const int64_t M = r->M;
@@ -144,6 +145,15 @@ static int enqueue_blocks(pmg_refiner* r, const float* points, float* points_out
             } else {
                 a2.points = points;
                 a2.points_out = points_out;
+                if (c.output_gate && gate_lidar) {
+                    a2.gate_lidar = gate_lidar;
+                    a2.gate_conf = gate_conf;
+                    a2.gate_dh = c.dh;
+                    a2.gate_dw = c.dw;
+                    // the reference's Python floats: floor + (1.0 - floor) * u, both constants rounded to fp32
+                    a2.gate_floor = c.output_gate_floor;
+                    a2.gate_scale = (float)(1.0 - (double)c.output_gate_floor);
+                }
             }
             if (int e = launch_conv_col(prec, a2, C, PMG_EPI_ROUT, s)) return e;
         }
@@ -212,7 +222,33 @@ static int enqueue_step(pmg_refiner* r, const float* points, float* points_out, 
     in.st = st;
     in.use_prompt = c.use_prompt;
     if (int e = launch_input_stage(in, f16, s)) return e;
-    if (int e = enqueue_blocks(r, points, points_out, nullptr, s)) return e;
+    if (int e = enqueue_blocks(r, points, points_out, nullptr, s, lidar, conf)) return e;
+
+    if (c.anchor > 0.0f) {
+        // v3.py:570-573: _lidar_in_affine_frame on the refined logz (the prompt fit's inputs), then the pull
+        float* st_a = r->st_scratch + 4 * c.B;
+        FitLaunch f{};
+        f.mode = 1;
+        f.logz = points_out + 2;
+        f.stride = 3;
+        f.lidar = lidar;
+        f.conf = conf;
+        f.B = c.B;
+        f.H = c.H;
+        f.W = c.W;
+        f.dh = c.dh;
+        f.dw = c.dw;
+        f.N = (int64_t)c.H * c.W;
+        f.iters = c.fit_iters;
+        f.trim = c.fit_trim;
+        f.min_points = c.fit_min_points;
+        f.st = st_a;
+        f.info = nullptr;
+        f.workspace = r->fit_ws[0];
+        f.workspace_bytes = r->fit_ws_bytes[0];
+        if (int e = launch_fit(f, s)) return e;
+        if (int e = launch_anchor(points_out, c.B, c.H, c.W, lidar, conf, c.dh, c.dw, st_a, c.anchor, s)) return e;
+    }
 
     if (c.final_fit) {
         // v3.py:768-778: area-pool the refined depth to the LiDAR grid, mask, fit.
@@ -302,7 +338,8 @@ pmg_refiner* pmg_refiner_create(const pmg_refiner_config* cfg) {
     if (c.B < 1 || c.H < 1 || c.W < 1 || (int64_t)c.B * c.H * c.W > INT_MAX / 27 || !supported_width(c.C) ||
         c.n_blocks < 1 || (c.precision != PMG_PREC_INT8 && c.precision != PMG_PREC_FP16) || c.dh < 1 || c.dw < 1 ||
         c.fit_iters < 0 || c.fit_iters > 64 || c.fit_min_points < 1 || !(c.fit_trim >= 0.0f && c.fit_trim < 1.0f) ||
-        (int64_t)c.H * c.W > ((int64_t)1 << 22)) {
+        (int64_t)c.H * c.W > ((int64_t)1 << 22) || !(c.output_gate_floor >= 0.0f && c.output_gate_floor <= 1.0f) ||
+        !(c.anchor >= 0.0f && c.anchor <= 1.0f)) {
         set_error("pmg_refiner_create: unsupported configuration");
         return nullptr;
     }
@@ -321,7 +358,7 @@ pmg_refiner* pmg_refiner_create(const pmg_refiner_config* cfg) {
     };
     const size_t o_zq = take(M * 4), o_zmin = take(c.B * 4), o_zmax = take(c.B * 4);
     const size_t o_x = take(M * c.C * 4), o_q1 = take(M * c.C * elt), o_q2 = take(M * c.C * elt);
-    const size_t o_st = take(4 * c.B * 4), o_f0 = take(r->fit_ws_bytes[0]), o_f1 = take(r->fit_ws_bytes[1]);
+    const size_t o_st = take(6 * c.B * 4), o_f0 = take(r->fit_ws_bytes[0]), o_f1 = take(r->fit_ws_bytes[1]);
     r->arena_bytes = off;
     if (hipMalloc(&r->arena, r->arena_bytes) != hipSuccess) {
         set_error("pmg_refiner_create: hipMalloc of " + std::to_string(r->arena_bytes) + " bytes failed");

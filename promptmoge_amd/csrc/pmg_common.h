@@ -115,6 +115,29 @@ __device__ inline void grid_barrier(unsigned* counter, unsigned index, unsigned 
     __syncthreads();
 }
 
+// The LiDAR depth and confidence/2 clamped to [0, 1] seen by pixel (b, i, j) of an H x W map: F.interpolate
+// mode='nearest' from dh x dw, source row floor(i * (dh / H)) (the scale in fp32), clamped to the last row
+// (v3.py:374-375, 389-390).
+__device__ inline void lidar_at(const float* lidar, const float* conf, int b, int i, int j, int H, int W, int dh,
+                                int dw, float& d, float& c) {
+    const float scy = (float)dh / (float)H, scx = (float)dw / (float)W;
+    int sy = (int)__builtin_floorf((float)i * scy);
+    int sx = (int)__builtin_floorf((float)j * scx);
+    sy = sy < dh - 1 ? sy : dh - 1;
+    sx = sx < dw - 1 ? sx : dw - 1;
+    const int64_t p = ((int64_t)b * dh + sy) * dw + sx;
+    d = lidar[p];
+    c = fmin_(fmax_(conf[p] / 2.0f, 0.0f), 1.0f);
+}
+
+// _lidar_uncertainty (v3.py:386-393) with range_uncertainty (prompt_stem.py:41-42, falloff 3 m -> 5 m):
+// u = 1 - c * (1 - clamp((d - 3) / 2, 0, 1)) where the LiDAR has a value, else 1.
+__device__ inline float lidar_uncertainty(float d, float c) {
+    const bool valid = __builtin_isfinite(d) && d > 0.0f;
+    const float ru = fmin_(fmax_((d - 3.0f) / 2.0f, 0.0f), 1.0f);
+    return valid ? 1.0f - c * (1.0f - ru) : 1.0f;
+}
+
 // Row layout shared by the fused epilogues and the row kernels: a wave covers 16 rows; lane l holds row l % 16
 // and, of its C channels, n = 16j + 4g + i with g = l / 16 (j < C/16, i < 4). Row reductions run in the "quad"
 // order: each lane sums its channels (j outer, i inner) from 0, then the four lane groups combine as

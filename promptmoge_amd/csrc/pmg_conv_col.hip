@@ -197,9 +197,19 @@ __device__ inline void col_epilogue(const ColConvArgs& a, const typename ColAcc<
             if (ok && g == 0) {
                 if (a.points) {  // _refine_logz: logz + out (v3.py:359)
                     const float p0 = a.points[mo * 3 + 0], p1 = a.points[mo * 3 + 1], p2 = a.points[mo * 3 + 2];
+                    float lz = p2 + d;
+                    if (a.gate_lidar) {  // output gate: cur + g * (refined - cur) (v3.py:565-569)
+                        const int HW = a.H * a.W;
+                        const int b = (int)(mo / HW), pix = (int)(mo - (int64_t)b * HW);
+                        const int i = pix / a.W, jj = pix - (pix / a.W) * a.W;
+                        float ld, lc;
+                        lidar_at(a.gate_lidar, a.gate_conf, b, i, jj, a.H, a.W, a.gate_dh, a.gate_dw, ld, lc);
+                        const float gu = a.gate_floor + a.gate_scale * lidar_uncertainty(ld, lc);
+                        lz = p2 + gu * (lz - p2);
+                    }
                     a.points_out[mo * 3 + 0] = p0;
                     a.points_out[mo * 3 + 1] = p1;
-                    a.points_out[mo * 3 + 2] = p2 + d;
+                    a.points_out[mo * 3 + 2] = lz;
                 } else {  // the refiner module's own output, (M, 1) (sparse_unet.py:258)
                     ((float*)a.out)[mo] = d;
                 }

@@ -99,7 +99,18 @@ struct ColConvArgs {
     const float* out_b;
     const float* points;
     float* points_out;
+    // PMG_EPI_ROUT with points: the refiner output gate (v3.py:565-569) when gate_lidar is set -- the update is
+    // scaled by g = gate_floor + gate_scale * u, u the LiDAR uncertainty of the pixel (lidar, conf [B][dh][dw])
+    const float* gate_lidar;
+    const float* gate_conf;
+    int gate_dh, gate_dw;
+    float gate_floor, gate_scale;
 };
 int launch_conv_col(int precision, const ColConvArgs& a, int C, int epi, hipStream_t s);
+
+// The elastic anchor (v3.py:570-573): logz of points [B][H][W][3] moves by beta * gate * (log_d_aff - logz), with
+// (log_d_aff, gate) the LiDAR in the affine frame of st [B][2] (hard gate, v3.py:376-380).
+int launch_anchor(float* points, int B, int H, int W, const float* lidar, const float* conf, int dh, int dw,
+                  const float* st, float beta, hipStream_t s);
 
 }  // namespace pmg

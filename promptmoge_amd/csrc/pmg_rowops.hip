@@ -84,14 +84,8 @@ struct InputArgs {
 };
 
 __device__ inline void prompt_feats(const InputArgs& a, int b, int i, int j, float logz, float& res, float& gate) {
-    const float scy = (float)a.dh / (float)a.H, scx = (float)a.dw / (float)a.W;
-    int sy = (int)__builtin_floorf((float)i * scy);
-    int sx = (int)__builtin_floorf((float)j * scx);
-    sy = sy < a.dh - 1 ? sy : a.dh - 1;
-    sx = sx < a.dw - 1 ? sx : a.dw - 1;
-    const int64_t p = ((int64_t)b * a.dh + sy) * a.dw + sx;
-    const float d = a.lidar[p];
-    const float c = fmin_(fmax_(a.conf[p] / 2.0f, 0.0f), 1.0f);
+    float d, c;
+    lidar_at(a.lidar, a.conf, b, i, j, a.H, a.W, a.dh, a.dw, d, c);
     const bool valid = __builtin_isfinite(d) && d > 0.0f;
     const float s = a.st[2 * b], t = a.st[2 * b + 1];
     const float daff = (d - t) / fmax_(s, 1e-6f);
@@ -249,6 +243,36 @@ __global__ void math_k(int op, const float* in, float* out, int64_t n) {
         out[i] = (float)silu_quant_i8(in[2 * i], in[2 * i + 1]);
     else
         out[i] = math_op(op, in[i]);
+}
+
+// One thread per pixel: the elastic anchor of the refined logz toward the LiDAR in its affine frame (v3.py:570-573,
+// _lidar_in_affine_frame 362-383 with the hard gate), fp32 in the reference's operation order.
+__global__ __launch_bounds__(256) void anchor_k(float* points, int B, int H, int W, const float* lidar,
+                                                const float* conf, int dh, int dw, const float* st, float beta) {
+    const int64_t m = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int HW = H * W;
+    if (m >= (int64_t)B * HW) return;
+    const int b = (int)(m / HW), pix = (int)(m - (int64_t)b * HW);
+    const int i = pix / W, j = pix - (pix / W) * W;
+    float d, c;
+    lidar_at(lidar, conf, b, i, j, H, W, dh, dw, d, c);
+    const float lz = points[m * 3 + 2];
+    const bool valid = __builtin_isfinite(d) && d > 0.0f;
+    const float s = st[2 * b], t = st[2 * b + 1];
+    const float daff = (d - t) / fmax_(s, 1e-6f);
+    const bool ok = valid && daff > 1e-4f;
+    const float lda = ok ? log_f32(fmax_(daff, 1e-4f)) : lz;
+    const float gate = c * (ok ? 1.0f : 0.0f);
+    points[m * 3 + 2] = lz + (beta * gate) * (lda - lz);
+}
+
+int launch_anchor(float* points, int B, int H, int W, const float* lidar, const float* conf, int dh, int dw,
+                  const float* st, float beta, hipStream_t s) {
+    const int64_t M = (int64_t)B * H * W;
+    if (M == 0) return PMG_OK;
+    hipLaunchKernelGGL(anchor_k, dim3((unsigned)((M + 255) / 256)), dim3(256), 0, s, points, B, H, W, lidar, conf, dh,
+                       dw, st, beta);
+    return check_launch("anchor_k");
 }
 
 }  // namespace pmg

@@ -66,12 +66,15 @@ class RefinerStep:
 
     points [B, H, W, 3] fp32 (x/z, y/z, logz) is refined into `out` (default in place); lidar, conf [B, dh, dw].
     Returns the prompt fit (s, t) [B, 2] and, if `final_fit`, the metric fit of the refined depth [B, 2].
+    `output_gate` / `output_gate_floor` and `anchor` are the refine loop's lidar_prompt options 'output_gate',
+    'output_gate_floor' and 'anchor' (v3.py:40-41, 565-573).
     """
 
     def __init__(self, weights: RefinerW, B: int, H: int, W: int, dh: Optional[int] = None,
                  dw: Optional[int] = None, *, precision: str = "int8", depth_resolution: float = 256.0,
                  fit_iters: int = 4, fit_trim: float = 0.2, fit_min_points: int = 32, use_prompt: bool = True,
-                 soft_gate: bool = False, final_fit: bool = False, use_graph: bool = True, device="cuda"):
+                 soft_gate: bool = False, final_fit: bool = False, use_graph: bool = True,
+                 output_gate: bool = False, output_gate_floor: float = 0.1, anchor: float = 0.0, device="cuda"):
         if precision not in ("int8", "fp16"):
             raise ValueError("precision must be 'int8' or 'fp16'")
         self.B, self.H, self.W = B, H, W
@@ -81,7 +84,8 @@ class RefinerStep:
         cfg = RefinerConfig(B, H, W, weights.C, len(weights.blocks),
                             _lib.PREC_INT8 if precision == "int8" else _lib.PREC_FP16, float(depth_resolution),
                             self.dh, self.dw, int(fit_iters), float(fit_trim), int(fit_min_points), int(use_prompt),
-                            int(soft_gate), int(final_fit), int(use_graph))
+                            int(soft_gate), int(final_fit), int(use_graph), int(output_gate),
+                            float(output_gate_floor), float(anchor))
         self._h = lib().pmg_refiner_create(C.byref(cfg))
         if not self._h:
             raise _lib.PmgError(_lib.PMG_E_INVALID, lib().pmg_last_error().decode())

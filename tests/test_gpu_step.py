@@ -17,14 +17,14 @@ from conftest import announce
 pytestmark = pytest.mark.gpu
 
 
-def _run(cfg, sc, w, *, B=1, use_graph=True, final_fit=False, reps=1, lidar=None):
+def _run(cfg, sc, w, *, B=1, use_graph=True, final_fit=False, reps=1, lidar=None, **kw):
     dev = torch.device("cuda:0")
     lidar, conf = (sc.lidar, sc.conf) if lidar is None else lidar
     pts = np.broadcast_to(sc.points, (B,) + sc.points.shape).copy()
     lid = np.broadcast_to(lidar, (B,) + lidar.shape).copy()
     cnf = np.broadcast_to(conf, (B,) + conf.shape).copy()
     step = RefinerStep(w, B, cfg.H, cfg.W, dh=lid.shape[-2], dw=lid.shape[-1], precision=cfg.precision,
-                       fit_iters=cfg.fit_iters, final_fit=final_fit, use_graph=use_graph)
+                       fit_iters=cfg.fit_iters, final_fit=final_fit, use_graph=use_graph, **kw)
     stream = torch.cuda.Stream()
     outs = []
     with torch.cuda.stream(stream):
@@ -76,6 +76,31 @@ def test_step_int8_lowres_lidar(gpu):
     d, dr = np.exp(P[..., 2].astype(np.float64)), np.exp(ref[..., 2].astype(np.float64))
     assert (np.abs(d - dr) / dr).max() < 1e-3
     assert abs(fin[0, 0] - fin_o[0][0]) <= 1e-5 * abs(fin_o[0][0]) and abs(fin[0, 1] - fin_o[1][0]) <= 1e-5
+
+
+@pytest.mark.parametrize("gate,anchor", [(True, 0.0), (False, 0.5), (True, 0.3)])
+def test_step_output_gate_and_anchor(gpu, gate, anchor):
+    """The refine loop's 'output_gate' (floor 0.1) and elastic 'anchor' options (v3.py:565-573) in the fused step:
+    refined depth within 1e-3 relative of the oracle (the anchor re-fits (s, t) on the refined depth, in fp64 sums
+    of another order); with the gate alone and a bit-identical prompt fit, the depth is bit-identical."""
+    announce(f"step int8 config=B output_gate={gate} anchor={anchor}")
+    cfg = spec.CONFIGS["B"]
+    sc = spec.make_scene(cfg)
+    w = spec.refiner_for(cfg, sc)
+    step, pts, lid, cnf, outs = _run(cfg, sc, w, final_fit=True, output_gate=gate, output_gate_floor=0.1,
+                                     anchor=anchor)
+    P, st, fin = outs[0]
+    ref, st_o, fin_o = orf.step(pts, lid, cnf, w, precision="int8", iters=cfg.fit_iters, final_fit=True,
+                                output_gate_on=gate, gate_floor=0.1, anchor=anchor)
+    plain, _, _ = orf.step(pts, lid, cnf, w, precision="int8", iters=cfg.fit_iters)
+    assert abs(st[0, 0] - st_o[0][0]) <= 1e-5 * abs(st_o[0][0]) and abs(st[0, 1] - st_o[1][0]) <= 1e-5
+    d, dr = np.exp(P[..., 2].astype(np.float64)), np.exp(ref[..., 2].astype(np.float64))
+    assert (np.abs(d - dr) / dr).max() < 1e-3
+    assert abs(fin[0, 0] - fin_o[0][0]) <= 1e-5 * abs(fin_o[0][0]) and abs(fin[0, 1] - fin_o[1][0]) <= 1e-5
+    # the options change the result (the test would not notice a step that ignores them)
+    assert np.abs(ref[..., 2] - plain[..., 2]).max() > 1e-4
+    if not anchor and st[0, 0] == st_o[0][0] and st[0, 1] == st_o[1][0]:
+        assert np.array_equal(P, ref)
 
 
 def test_step_fp16_teacher(gpu):

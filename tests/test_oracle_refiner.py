@@ -83,3 +83,53 @@ def test_weights_from_reference_state_dict():
             assert np.array_equal(getattr(a, f), getattr(b, f)), f
         assert a.clip1 == pytest.approx(b.clip1) and a.clip2 == pytest.approx(b.clip2)
     assert np.array_equal(got.out_w, w.out_w) and np.array_equal(got.in_w, w.in_w)
+
+
+# ---- output gate and elastic anchor (v3.py:565-573, 386-393) -------------------------------------------------
+def test_lidar_uncertainty_closed_form():
+    """u = 1 - c * (1 - clamp((d - 3) / 2, 0, 1)) where the LiDAR has a value, else 1 (prompt_stem.py:28-29)."""
+    d = np.array([[[2.0, 4.0, 6.0, 3.0, 5.0, 4.0, 0.0, np.nan, np.inf, -1.0]]], np.float32)
+    c = np.array([[[1.0, 1.0, 1.0, 1.0, 1.0, 0.5, 1.0, 1.0, 1.0, 1.0]]], np.float32)
+    u = rf.lidar_uncertainty(d, c)
+    np.testing.assert_array_equal(u[0, 0], np.float32([0.0, 0.5, 1.0, 0.0, 1.0, 0.75, 1.0, 1.0, 1.0, 1.0]))
+    # no confidence: full uncertainty whatever the range
+    assert np.all(rf.lidar_uncertainty(np.float32([[[1.0, 4.0, 9.0]]]), np.zeros((1, 1, 3), np.float32)) == 1.0)
+
+
+def test_output_gate_limits():
+    rng = np.random.default_rng(0)
+    cur = rng.normal(0.5, 0.3, (1, 4, 5)).astype(np.float32)
+    ref = (cur + rng.normal(0, 0.05, cur.shape)).astype(np.float32)
+    d = np.full(cur.shape, 2.0, np.float32)  # inside the 3 m knee: u = 1 - c
+    c1 = np.ones(cur.shape, np.float32)
+    # floor 0 and a confident close pixel (u = 0): no update at all
+    np.testing.assert_array_equal(rf.output_gate(cur, ref, d, c1, 0.0), cur)
+    # floor 1: the full update (up to the rounding of cur + (ref - cur))
+    np.testing.assert_allclose(rf.output_gate(cur, ref, d, c1, 1.0), ref, rtol=0, atol=1e-6)
+    # u = 1 (no confidence): the full update for any floor
+    np.testing.assert_allclose(rf.output_gate(cur, ref, d, np.zeros_like(c1), 0.1), ref, rtol=0, atol=1e-6)
+    # half-way: floor 0, c = 1, d = 4 m -> u = 0.5 -> cur + 0.5 (ref - cur)
+    out = rf.output_gate(cur, ref, np.full(cur.shape, 4.0, np.float32), c1, 0.0)
+    np.testing.assert_allclose(out, 0.5 * (cur.astype(np.float64) + ref), rtol=0, atol=1e-6)
+
+
+def test_anchor_pull_limits():
+    rng = np.random.default_rng(1)
+    logz = rng.normal(0.3, 0.2, (2, 3, 4)).astype(np.float32)
+    d = rng.uniform(1.0, 4.0, logz.shape).astype(np.float32)
+    c = np.ones(logz.shape, np.float32)
+    s, t = np.float32([1.3, 0.8]), np.float32([0.05, -0.02])
+    np.testing.assert_array_equal(rf.anchor_pull(logz, d, c, s, t, 0.0), logz)  # beta 0: off
+    # beta 1, full confidence: the LiDAR in the affine frame, log((d - t) / s), computed here in fp64
+    want = np.log((d.astype(np.float64) - t[:, None, None]) / s[:, None, None])
+    np.testing.assert_allclose(rf.anchor_pull(logz, d, c, s, t, 1.0), want, rtol=0, atol=2e-6)
+    # no LiDAR value or no confidence: the gate is 0
+    d2 = d.copy()
+    d2[0, 0, 0] = 0.0
+    c2 = c.copy()
+    c2[1, 2, 3] = 0.0
+    out = rf.anchor_pull(logz, d2, c2, s, t, 0.7)
+    assert out[0, 0, 0] == logz[0, 0, 0] and out[1, 2, 3] == logz[1, 2, 3]
+    # half strength: half-way between logz and the target
+    half = rf.anchor_pull(logz, d, c, s, t, 0.5)
+    np.testing.assert_allclose(half, 0.5 * (logz + want), rtol=0, atol=2e-6)
