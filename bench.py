@@ -19,7 +19,8 @@ captured HIP graph of that chain; the metric fit of the refined depth is timed s
     measured_peaks   this device's practical HBM copy bandwidth and int8 MFMA rate (pmg_probe_copy / _mfma_i8);
               `roofline.frac` is against the published 8 TB/s, `roofline.frac_measured` against the copy probe
     other_configs    one K-step frame of the fp16 teacher (T) and of the hi-res config (H, with nearest_fill); the
-              first U-Net level step of Model A (pool cache, mean pool, nearest upsampling: pool_L0)
+              first U-Net level step of Model A (pool cache, mean pool, nearest upsampling: pool_L0); the prompt
+              gauge infer applies after the loop, on Model A's depth and LiDAR (gauge_A)
 
 Other modes (used to produce the committed profiles):
     --kernels-only     launch each per-step kernel --kernel-reps times eagerly (plus a 64 MiB copy for counter
@@ -385,6 +386,26 @@ def pool_bench(stream, reps=20):
             "upsample_gbs": round((cfg.M * cfg.C * 4 * 2 + cfg.M * 4) / (up_ms * 1e-3) / 1e9, 1)}
 
 
+def gauge_bench(stream):
+    """The prompt gauge infer applies after the refine loop (gauge_poly=2, v3.py:841-853) on Model A's refined
+    depth with its 480x640 LiDAR prompt: pooled inputs, 3 IRLS rounds on one CU, the full-resolution correction."""
+    import numpy as np
+    import torch
+
+    from promptmoge_amd import ops, spec
+
+    dev = torch.device("cuda:0")
+    cfg = spec.CONFIGS["A"]
+    sc = spec.make_scene(cfg)
+    with torch.cuda.stream(stream):
+        depth = torch.from_numpy(np.exp(sc.points[..., 2].astype(np.float64)).astype(np.float32)[None]).to(dev)
+        lidar = torch.from_numpy(sc.lidar[None].copy()).to(dev)
+        conf = torch.from_numpy(sc.conf[None].copy()).to(dev)
+        ms = graph_ms(lambda: ops.gauge_poly(depth, lidar, conf, 2, 3), 10, stream)
+    return {"workload": f"A: prompt gauge, degree 2, 3 IRLS rounds, depth {cfg.H}x{cfg.W}, LiDAR {cfg.H}x{cfg.W}",
+            "ms": round(ms, 4)}
+
+
 def cpu_baseline(env):
     from oracle import refiner as orf
 
@@ -494,6 +515,7 @@ def main() -> int:
     others = None if args.no_others else {n: frame_bench(n, stream) for n in ("T", "H")}
     if others is not None:
         others["pool_L0"] = pool_bench(stream)
+        others["gauge_A"] = gauge_bench(stream)
     cpu = None if args.no_cpu else cpu_baseline(env)
 
     line = {

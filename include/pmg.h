@@ -279,6 +279,20 @@ size_t pmg_nearest_fill_workspace_bytes(int B, int h, int w);
 int pmg_nearest_fill(const float* depth, const float* conf, int B, int h, int w, float* depth_out, float* conf_out,
                      int32_t* src_index, void* workspace, size_t workspace_bytes, void* stream);
 
+/* pmg_gauge_poly -- replaces MoGeModel.prompt_gauge_poly (moge/model/v3.py:151-183), the per-frame prompt gauge
+ * that infer applies by default (gauge_poly=2, v3.py:841-853): corr[b] = exp(poly(u, v)) with (u, v) on
+ * linspace(-1, 1) grids, the polynomial (1, u, v) for degree 1 or (1, u, v, u^2, uv, v^2) for degree >= 2 fitted
+ * by `iters` IRLS rounds to log(max(lidar, 1e-3)) - log(max(z_lr, 1e-3)) on the pixels with conf >= 2, lidar > 0
+ * and z_lr > 0, z_lr the area-pooled valid (finite, > 0) depth; fewer than 200 such pixels or a singular /
+ * non-finite system give corr 1. depth: [B][H][W] fp32; lidar, conf: [B][h][w] fp32 (conf NULL: all 2);
+ * corr: [B][H][W] fp32 out; coef: [B][8] fp32 out (the coefficients in basis order, [7] = 1 if the frame was
+ * fitted, else 0). iters in [1, 64]. The workspace (pmg_gauge_poly_workspace_bytes) needs no initialisation.
+ */
+size_t pmg_gauge_poly_workspace_bytes(int B, int h, int w);
+int pmg_gauge_poly(const float* depth, int B, int H, int W, const float* lidar, const float* conf, int h, int w,
+                   int degree, int iters, float* corr, float* coef, void* workspace, size_t workspace_bytes,
+                   void* stream);
+
 /* ------------------------------------------------------------------------------------------------------------ *
  * The fused refiner step -- replaces one iteration of the refine loop (v3.py:547-576) for a single-level
  * refiner: prompt fit -> prompt residual/gate -> voxelise -> column neighbour map -> input_proj (+ prompt_proj)

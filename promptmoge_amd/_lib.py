@@ -91,6 +91,8 @@ SIGNATURES = {
     "pmg_fit_final": (i32, [vp, i64, vp, vp, vp, i32, i32, i32, i32, i32, i32, f32, i32, vp, vp, vp, sz, vp]),
     "pmg_nearest_fill_workspace_bytes": (sz, [i32, i32, i32]),
     "pmg_nearest_fill": (i32, [vp, vp, i32, i32, i32, vp, vp, vp, vp, sz, vp]),
+    "pmg_gauge_poly_workspace_bytes": (sz, [i32, i32, i32]),
+    "pmg_gauge_poly": (i32, [vp, i32, i32, i32, vp, vp, i32, i32, i32, i32, vp, vp, vp, sz, vp]),
     "pmg_refiner_create": (vp, [C.POINTER(RefinerConfig)]),
     "pmg_refiner_destroy": (None, [vp]),
     "pmg_refiner_set_weights": (i32, [vp, C.POINTER(RefinerWeights)]),

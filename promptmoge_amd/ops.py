@@ -17,7 +17,7 @@ __all__ = [
     "voxelize", "nmap_column", "nmap_hash", "row_order", "nmap_from_rows", "kmap_compact", "spconv_i8",
     "spconv_i8_ordered", "spconv_f16",
     "spconv_f32", "spconv_col", "ln_silu_quant", "ln_silu_f16", "fit_scale_shift", "fit_prompt", "fit_final",
-    "math_device",
+    "math_device", "gauge_poly",
     "nearest_fill",
     "EPI_ACC", "EPI_Q", "EPI_R", "EPI_BIAS", "EPI_SILU", "EPI_RLN", "EPI_ROUT", "EPI_QLIN",
 ]
@@ -445,3 +445,32 @@ def nearest_fill(depth: torch.Tensor, conf: Optional[torch.Tensor] = None, *, re
     if return_index:
         return d_out, c_out, idx
     return d_out, c_out
+
+
+def gauge_poly(depth: torch.Tensor, lidar: torch.Tensor, conf: Optional[torch.Tensor] = None, degree: int = 2,
+               iters: int = 3, *, return_coef: bool = False):
+    """MoGeModel.prompt_gauge_poly (moge/model/v3.py:151-183) on the GPU: the [B, H, W] correction exp(poly(u, v))
+    fitted by IRLS to log(prompt / area-pooled prediction) on confident prompt pixels (fewer than 200: 1).
+
+    depth [B, H, W] fp32; lidar (and conf, or None) [B, h, w] or [B, 1, h, w] fp32. With return_coef also the
+    per-frame coefficients [B, 8] (basis order (1, u, v, u^2, uv, v^2); [:, 7] is 1 where the frame was fitted).
+    """
+    depth = _dev(depth, "depth", torch.float32)
+    if depth.ndim != 3:
+        raise ValueError("depth must be [B, H, W]")
+    B, H, W = depth.shape
+    lidar = _dev(lidar, "lidar", torch.float32)
+    h, w = lidar.shape[-2:]
+    if lidar.numel() != B * h * w:
+        raise ValueError("lidar must be [B, h, w] or [B, 1, h, w]")
+    if conf is not None:
+        conf = _dev(conf, "conf", torch.float32)
+        if conf.numel() != B * h * w:
+            raise ValueError("conf must match lidar")
+    corr = torch.empty_like(depth)
+    coef = torch.empty((B, 8), dtype=torch.float32, device=depth.device)
+    ws_bytes = lib().pmg_gauge_poly_workspace_bytes(B, h, w)
+    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=depth.device)
+    call("pmg_gauge_poly", _p(depth), B, H, W, _p(lidar), _p(conf), h, w, int(degree), int(iters), _p(corr),
+         _p(coef), _p(ws), ws_bytes, _stream())
+    return (corr, coef) if return_coef else corr

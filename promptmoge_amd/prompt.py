@@ -1,6 +1,8 @@
 """Host-facing mirror of the reference's prompt preparation (promptmoge/model.py:61-72)."""
 from __future__ import annotations
 
+from typing import Optional
+
 import numpy as np
 import torch
 
@@ -37,3 +39,16 @@ def nearest_fill(depth, conf):
     filled = torch.gather(flat, 1, src).reshape(depth.shape)
     filled = torch.where(idx.reshape(depth.shape) >= 0, filled, depth)
     return filled, torch.where(valid | (idx < 0), conf, torch.ones_like(conf))
+
+
+def prompt_gauge_poly(depth: torch.Tensor, lidar: torch.Tensor, conf: Optional[torch.Tensor], degree: int = 2,
+                      iters: int = 3) -> torch.Tensor:
+    """Drop-in for MoGeModel.prompt_gauge_poly (moge/model/v3.py:151-183), computed on the GPU.
+
+    Same arguments and result: depth [B, H, W], lidar / conf [B, 1, h, w] or [B, h, w] (conf may be None); returns
+    the [B, H, W] multiplicative correction in depth's dtype. The least squares run in fp64 normal equations (the
+    reference: LAPACK on fp32), so the coefficients agree to rounding, not bit for bit.
+    """
+    corr = ops.gauge_poly(depth.float().contiguous(), lidar.float().contiguous(),
+                          None if conf is None else conf.float().contiguous(), degree, iters)
+    return corr.to(depth.dtype)

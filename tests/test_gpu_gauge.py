@@ -1,0 +1,104 @@
+"""GPU parity of the prompt gauge (pmg_gauge_poly, v3.py:152-183) against oracle/gauge.py on the same inputs.
+
+The correction and the coefficients must agree to 2e-5 (the least squares run in fp64 on both sides, in different
+forms, and the fp32 coefficients may round differently in the last bit); a frame with too few confident pixels
+is exactly 1."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import gauge as og
+from oracle.fit import area_pool
+from promptmoge_amd import ops, spec
+from promptmoge_amd.prompt import prompt_gauge_poly
+
+from conftest import announce
+
+pytestmark = pytest.mark.gpu
+
+
+def _gpu(depth, lidar, conf, degree=2, iters=3):
+    dev = torch.device("cuda:0")
+    d = torch.from_numpy(np.ascontiguousarray(depth)).to(dev)
+    l = torch.from_numpy(np.ascontiguousarray(lidar)).to(dev)
+    c = None if conf is None else torch.from_numpy(np.ascontiguousarray(conf)).to(dev)
+    corr, coef = ops.gauge_poly(d, l, c, degree, iters, return_coef=True)
+    torch.cuda.synchronize()
+    return corr.cpu().numpy(), coef.cpu().numpy()
+
+
+def _check(depth, lidar, conf, degree=2, iters=3):
+    corr, coef = _gpu(depth, lidar, conf, degree, iters)
+    want, coefs = og.gauge_poly(depth, lidar, conf, degree, iters, return_coef=True)
+    K = 6 if degree >= 2 else 3
+    for b, cb in enumerate(coefs):
+        if cb is None:
+            assert coef[b, 7] == 0.0 and np.all(corr[b] == 1.0)
+        else:
+            assert coef[b, 7] == 1.0
+            np.testing.assert_allclose(coef[b, :K], cb, rtol=0, atol=2e-5)
+    np.testing.assert_allclose(corr, want, rtol=2e-5, atol=0)
+    return corr, coefs
+
+
+def _scene_maps(cfg, seed, hw=None):
+    sc = spec.make_scene(cfg)
+    depth = np.exp(sc.points[..., 2].astype(np.float64)).astype(np.float32)[None]
+    lidar, conf = sc.lidar[None].copy(), sc.conf[None].copy()
+    if hw is not None:
+        lidar = area_pool(lidar, *hw)
+        conf = np.round(area_pool(conf, *hw)).astype(np.float32)
+    h, w = lidar.shape[-2:]
+    rng = np.random.default_rng(seed)
+    vv, uu = np.meshgrid(og.linspace_f32(h), og.linspace_f32(w), indexing="ij")
+    field = np.exp(0.04 * uu - 0.03 * vv + 0.05 * uu * vv + 0.02 * vv * vv)
+    lidar = (lidar * field * np.where(rng.random(lidar.shape) < 0.05, 1.4, 1.0)).astype(np.float32)
+    return depth, lidar, conf
+
+
+def test_gauge_recovers_polynomial(gpu):
+    announce("gauge: exact polynomial, B=2, 48x64 over 24x32")
+    rng = np.random.default_rng(0)
+    H, W, h, w = 48, 64, 24, 32
+    yy, xx = np.meshgrid(np.linspace(0, 1, H), np.linspace(0, 1, W), indexing="ij")
+    depth = np.stack([1.5 + 0.8 * xx + 0.4 * np.sin(3 * yy), 2.0 + 0.3 * yy]).astype(np.float32)
+    coef = rng.normal(0, 0.05, (2, 6))
+    vv, uu = np.meshgrid(og.linspace_f32(h), og.linspace_f32(w), indexing="ij")
+    A = og.basis(uu, vv, 2).astype(np.float64)
+    lidar = (area_pool(depth, h, w) * np.exp(np.einsum("hwk,bk->bhw", A, coef))).astype(np.float32)
+    _, coefs = _check(depth, lidar, np.full((2, h, w), 2.0, np.float32))
+    for b in range(2):
+        np.testing.assert_allclose(coefs[b], coef[b], rtol=0, atol=2e-5)
+
+
+@pytest.mark.parametrize("name,hw", [("B", None), ("B", (120, 160)), ("A", (192, 256))])
+def test_gauge_scene(gpu, name, hw):
+    announce(f"gauge: scene {name}, lidar {hw}")
+    depth, lidar, conf = _scene_maps(spec.CONFIGS[name], 5, hw)
+    corr, _ = _check(depth, lidar, conf)
+    assert np.abs(corr - 1.0).max() > 1e-3  # the fitted field is not the identity
+
+
+def test_gauge_degree1_conf_none_invalid_depth_and_skip(gpu):
+    announce("gauge: degree 1, conf None, invalid depth, a frame below 200 points")
+    depth, lidar, conf = _scene_maps(spec.CONFIGS["B"], 7, (60, 80))
+    depth = np.concatenate([depth, depth * np.float32(1.1)])
+    lidar = np.concatenate([lidar, lidar])
+    conf = np.concatenate([conf, np.zeros_like(conf)])
+    conf[1, :10, :10] = 2.0  # 100 confident pixels: the second frame is skipped
+    depth[0, :7, :9] = np.inf
+    depth[0, 20:25, 30:33] = 0.0
+    depth[0, 40, 41] = np.nan
+    corr, coefs = _check(depth, lidar, conf, degree=1)
+    assert coefs[1] is None and np.all(corr[1] == 1.0)
+    _check(depth[:1], lidar[:1], None)
+    _check(depth[:1], lidar[:1], conf[:1], iters=1)
+
+
+def test_gauge_reference_signature(gpu):
+    announce("gauge: prompt_gauge_poly with [B,1,h,w] inputs")
+    depth, lidar, conf = _scene_maps(spec.CONFIGS["B"], 9, (120, 160))
+    dev = torch.device("cuda:0")
+    out = prompt_gauge_poly(torch.from_numpy(depth).to(dev), torch.from_numpy(lidar[:, None]).to(dev),
+                            torch.from_numpy(conf[:, None]).to(dev))
+    np.testing.assert_allclose(out.cpu().numpy(), og.gauge_poly(depth, lidar, conf), rtol=2e-5, atol=0)
