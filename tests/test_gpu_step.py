@@ -103,6 +103,32 @@ def test_step_output_gate_and_anchor(gpu, gate, anchor):
         assert np.array_equal(P, ref)
 
 
+def test_step_batch_of_distinct_frames(gpu):
+    """B = 2 different scenes through one step (per-frame fits, batch-offset LiDAR lookups in the gate and the
+    anchor) against the oracle on the same batch."""
+    announce("step int8 B=2 distinct frames, output gate + anchor")
+    cfg = spec.CONFIGS["B"]
+    sc0, sc1 = spec.make_scene(cfg), spec.make_scene(cfg, seed=cfg.seed + 17)
+    w = spec.refiner_for(cfg, sc0)
+    dev = torch.device("cuda:0")
+    pts = np.stack([sc0.points, sc1.points])
+    lid, cnf = np.stack([sc0.lidar, sc1.lidar]), np.stack([sc0.conf, sc1.conf])
+    step = RefinerStep(w, 2, cfg.H, cfg.W, fit_iters=cfg.fit_iters, final_fit=True, output_gate=True, anchor=0.25)
+    with torch.cuda.stream(torch.cuda.Stream()):
+        P = torch.from_numpy(pts).to(dev)
+        st, fin = step(P, torch.from_numpy(lid).to(dev), torch.from_numpy(cnf).to(dev))
+        step.check()
+        got, st, fin = P.cpu().numpy(), st.cpu().numpy(), fin.cpu().numpy()
+    ref, st_o, fin_o = orf.step(pts, lid, cnf, w, precision="int8", iters=cfg.fit_iters, final_fit=True,
+                                output_gate_on=True, gate_floor=0.1, anchor=0.25)
+    for b in range(2):
+        assert abs(st[b, 0] - st_o[0][b]) <= 1e-5 * abs(st_o[0][b]) and abs(st[b, 1] - st_o[1][b]) <= 1e-5
+        assert abs(fin[b, 0] - fin_o[0][b]) <= 1e-5 * abs(fin_o[0][b]) and abs(fin[b, 1] - fin_o[1][b]) <= 1e-5
+    d, dr = np.exp(got[..., 2].astype(np.float64)), np.exp(ref[..., 2].astype(np.float64))
+    assert (np.abs(d - dr) / dr).max() < 1e-3
+    assert np.abs(pts[0, ..., 2] - pts[1, ..., 2]).max() > 0.1  # two different scenes
+
+
 def test_step_fp16_teacher(gpu):
     announce("step fp16 teacher (small)")
     cfg = spec.StepConfig("t", 120, 160, 130.0, 130.0, 80.0, 60.0, 64, 3, "fp16", seed=13)
