@@ -205,9 +205,10 @@ constexpr int kG2Waves = kG2Threads / 64;
 constexpr int kG2Tiles = 4;           // 16-row tiles per wave
 constexpr int kG2Chunk = kG2Waves * kG2Tiles * 16;  // 512 rows per block step
 
-// Generic-map int8 convolution for Ci = Co = C in {64, 128}: a persistent block per CU walks chunks of 512 output
-// rows (in `order` if given); each of its 8 waves owns 64 rows (4 tiles of 16) with 4 x C/16 int32 accumulator
-// tiles. The 27 taps run in fixed order in groups of GRP taps (4 at C = 64, 2 at C = 128: registers); the next
+// Generic-map int8 convolution for Ci = Co = C in {64, 128} (C = 64 launches spconv_g2r_k below instead): a
+// persistent block per CU walks chunks of 512 output rows (in `order` if given); each of its 8 waves owns 64 rows
+// (4 tiles of 16) with 4 x C/16 int32 accumulator tiles. The 27 taps run in fixed order in groups of GRP taps (4 at
+// C = 64, 2 at C = 128: registers); the next
 // group's weights are loaded into registers during this group and stored into the other LDS buffer, so the block
 // meets at one barrier per group. Each LDS weight operand feeds the wave's 4 tiles (4 MFMAs of 16 cycles) and the
 // next operand is read before they issue. A wave skips the MFMAs of taps none of its 4 tiles has; an absent
@@ -412,25 +413,194 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
     }
 }
 
+// Ci = Co = 64: every tap's weights fit in LDS (27 x 4 KB in operand order), so the block loads them once and
+// meets at no barrier afterwards -- each wave runs its chunks' 27 taps on its own, and a wave that skips a tap
+// (none of its tiles has it) gains the time instead of waiting for the others at the next group barrier. The tap
+// loop is that of spconv_g2_k without the weight staging: codes one tap ahead, map indices three taps ahead.
+template <int C, int EPI>
+__global__ __launch_bounds__(kG2Threads, 1) void spconv_g2r_k(ConvArgs a) {
+    constexpr int NB = C / 16, KS = C / 64, T = kG2Tiles;
+    constexpr int NF = NB * KS;
+    static_assert(C == 64, "resident weights: C = 64");
+    __shared__ __attribute__((aligned(16))) v4i s_w[27 * NF * 64];
+    __shared__ float s_k[2][C];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int M = (int)a.M;
+    const int64_t ntile = (a.M + 15) >> 4;
+    typedef const __attribute__((address_space(3))) v4i lds_v4i;
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, (int)(a.M * C), kBufWord3);
+    const __amdgpu_buffer_rsrc_t nr =
+        __builtin_amdgcn_make_buffer_rsrc((void*)a.nmap_t, (short)0, (int)(a.M * 27 * 4), kBufWord3);
+    for (int e = tid; e < 2 * C; e += kG2Threads) {
+        const int q = e / C, n = e - (e / C) * C;
+        const float* src = q == 0 ? a.w_scale : a.bias;
+        s_k[q][n] = src ? src[n] : 0.0f;
+    }
+    for (int e = tid; e < 27 * NF * 64; e += kG2Threads) {
+        const int f = e >> 6, l = e & 63;
+        const int v = f / NF, js = f - (f / NF) * NF;
+        const int j = js / KS, s2 = js - (js / KS) * KS;
+        s_w[e] = *(const v4i*)((const uint8_t*)a.w + ((l & 15) * 27) * C + 16 * (l >> 4) + ((16 * j * 27) + v) * C + 64 * s2);
+    }
+    __syncthreads();
+
+    const int nchunk = (M + kG2Chunk - 1) / kG2Chunk;
+    const int G = gridDim.x, b = blockIdx.x;
+    const int nx = G >= 8 ? 8 : 1;
+    const int x = b % nx, bi = b / nx, nbx = (G - x + nx - 1) / nx;
+    const int c0 = (int)((int64_t)nchunk * x / nx), c1 = (int)((int64_t)nchunk * (x + 1) / nx);
+    // each wave takes the block's chunks independently: wave wv of chunk ch owns rows [64 wv, 64 wv + 64)
+    for (int ch = c0 + bi; ch < c1; ch += nbx) {
+        const int pos0 = ch * kG2Chunk + wv * (16 * T) + r;
+        int roff[T];
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const int p = pos0 + 16 * t;
+            roff[t] = 4 * (a.order ? (p < M ? a.order[p] : 0) : p);
+        }
+        uint32_t wmask;
+        {
+            const int64_t tl = (int64_t)ch * (kG2Chunk / 16) + wv * T + (lane & (T - 1));
+            uint32_t mk = (lane < T && tl < ntile) ? a.tmask[tl] : 0u;
+#pragma unroll
+            for (int o = 1; o < T; o <<= 1) mk |= __shfl_xor(mk, o, 64);
+            wmask = (uint32_t)__builtin_amdgcn_readfirstlane((int)mk);
+        }
+        v4i acc[T][NB];
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+            for (int j = 0; j < NB; ++j) acc[t][j] = v4i{0, 0, 0, 0};
+        auto idx_load = [&](int v, int (&id)[T]) {
+            const int vo = (v < 27 ? v : 27) * M * 4;
+#pragma unroll
+            for (int t = 0; t < T; ++t) id[t] = __builtin_amdgcn_raw_buffer_load_b32(nr, roff[t], vo, 0);
+        };
+        auto gather = [&](const int (&id)[T], v4i (&xs)[T][KS]) {
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                const int off = id[t] >= 0 ? id[t] * C + 16 * g : (int)0x80000000;
+#pragma unroll
+                for (int s2 = 0; s2 < KS; ++s2) xs[t][s2] = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 64 * s2, 0);
+            }
+        };
+        auto mma_tap = [&](int v, const v4i (&xs)[T][KS]) {
+            const v4i* wb = s_w + v * NF * 64 + lane;
+            v4i wop = *(lds_v4i*)(wb);
+#pragma unroll
+            for (int q = 0; q < NF; ++q) {
+                const int s2 = q / NB, j = q - (q / NB) * NB;
+                v4i nxt = wop;
+                if (q + 1 < NF) {
+                    const int s3 = (q + 1) / NB, j3 = (q + 1) - ((q + 1) / NB) * NB;
+                    nxt = *(lds_v4i*)(wb + (j3 * KS + s3) * 64);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int t = 0; t < T; ++t)
+                    acc[t][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wop, xs[t][s2], acc[t][j], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                wop = nxt;
+            }
+        };
+        int I[2][T];
+        v4i X[2][T][KS];
+        {
+            int i0[T];
+            idx_load(0, i0);
+            idx_load(1, I[1]);
+            idx_load(2, I[0]);
+            gather(i0, X[0]);
+        }
+        auto tap = [&](auto Pc, int v) {
+            constexpr int p = decltype(Pc)::value;
+            gather(I[p ^ 1], X[p ^ 1]);
+            idx_load(v + 3, I[p ^ 1]);
+            __builtin_amdgcn_sched_barrier(0);
+            if (v < 27 && ((wmask >> v) & 1u)) mma_tap(v, X[p]);
+            __builtin_amdgcn_sched_barrier(0);
+        };
+#pragma unroll 1
+        for (int v = 0; v < 27; v += 2) {
+            tap(std::integral_constant<int, 0>{}, v);
+            tap(std::integral_constant<int, 1>{}, v + 1);
+        }
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            if (pos0 + 16 * t >= M) continue;
+            const int m = roff[t] >> 2;
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                const int64_t o = (int64_t)m * C + 16 * j + 4 * g;
+                if constexpr (EPI == PMG_EPI_ACC) {
+                    *(v4i*)((int32_t*)a.out + o) = acc[t][j];
+                } else {
+                    float y[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int n = 16 * j + 4 * g + i;
+                        float u = (float)acc[t][j][i] * a.a_scale;
+                        u = u * s_k[0][n];
+                        if (a.bias) u = u + s_k[1][n];
+                        y[i] = u;
+                    }
+                    if constexpr (EPI == PMG_EPI_Q) {
+                        store_silu_codes4(y, a.out_mult, (int8_t*)a.out + o);
+                    } else if constexpr (EPI == PMG_EPI_QLIN) {
+                        store_codes4(y, a.out_mult, (int8_t*)a.out + o);
+                    } else if constexpr (EPI == PMG_EPI_R) {
+                        const v4f sk = *(const v4f*)(a.skip + o);
+                        *(v4f*)((float*)a.out + o) = v4f{y[0] + sk[0], y[1] + sk[1], y[2] + sk[2], y[3] + sk[3]};
+                    } else {
+                        *(v4f*)((float*)a.out + o) = v4f{y[0], y[1], y[2], y[3]};
+                    }
+                }
+            }
+        }
+    }
+}
+
 template <int C>
-static int launch_g2(const ConvArgs& a, int epilogue, hipStream_t s) {
+static int launch_g2r(const ConvArgs& a, int epilogue, hipStream_t s) {
     static int cus = -1;
     if (cus < 0) cus = num_cus();
     const int64_t nchunk = (a.M + kG2Chunk - 1) / kG2Chunk;
     const unsigned grid = (unsigned)(nchunk < cus ? nchunk : cus);
     switch (epilogue) {
-        case PMG_EPI_ACC: hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_ACC>), dim3(grid), dim3(kG2Threads), 0, s, a); break;
-        case PMG_EPI_Q: hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_Q>), dim3(grid), dim3(kG2Threads), 0, s, a); break;
-        case PMG_EPI_QLIN:
-            hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_QLIN>), dim3(grid), dim3(kG2Threads), 0, s, a);
-            break;
-        case PMG_EPI_R: hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_R>), dim3(grid), dim3(kG2Threads), 0, s, a); break;
-        case PMG_EPI_BIAS:
-            hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_BIAS>), dim3(grid), dim3(kG2Threads), 0, s, a);
-            break;
+        case PMG_EPI_ACC: hipLaunchKernelGGL((spconv_g2r_k<C, PMG_EPI_ACC>), dim3(grid), dim3(kG2Threads), 0, s, a); break;
+        case PMG_EPI_Q: hipLaunchKernelGGL((spconv_g2r_k<C, PMG_EPI_Q>), dim3(grid), dim3(kG2Threads), 0, s, a); break;
+        case PMG_EPI_QLIN: hipLaunchKernelGGL((spconv_g2r_k<C, PMG_EPI_QLIN>), dim3(grid), dim3(kG2Threads), 0, s, a); break;
+        case PMG_EPI_R: hipLaunchKernelGGL((spconv_g2r_k<C, PMG_EPI_R>), dim3(grid), dim3(kG2Threads), 0, s, a); break;
+        case PMG_EPI_BIAS: hipLaunchKernelGGL((spconv_g2r_k<C, PMG_EPI_BIAS>), dim3(grid), dim3(kG2Threads), 0, s, a); break;
         default: return fail(PMG_E_INVALID, "spconv: epilogue not available for this precision");
     }
-    return check_launch("spconv_g2_k");
+    return check_launch("spconv_g2r_k");
+}
+
+template <int C>
+static int launch_g2(const ConvArgs& a, int epilogue, hipStream_t s) {
+    if constexpr (C == 64) {
+        return launch_g2r<64>(a, epilogue, s);
+    } else {
+        static int cus = -1;
+        if (cus < 0) cus = num_cus();
+        const int64_t nchunk = (a.M + kG2Chunk - 1) / kG2Chunk;
+        const unsigned grid = (unsigned)(nchunk < cus ? nchunk : cus);
+        switch (epilogue) {
+            case PMG_EPI_ACC: hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_ACC>), dim3(grid), dim3(kG2Threads), 0, s, a); break;
+            case PMG_EPI_Q: hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_Q>), dim3(grid), dim3(kG2Threads), 0, s, a); break;
+            case PMG_EPI_QLIN:
+                hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_QLIN>), dim3(grid), dim3(kG2Threads), 0, s, a);
+                break;
+            case PMG_EPI_R: hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_R>), dim3(grid), dim3(kG2Threads), 0, s, a); break;
+            case PMG_EPI_BIAS:
+                hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_BIAS>), dim3(grid), dim3(kG2Threads), 0, s, a);
+                break;
+            default: return fail(PMG_E_INVALID, "spconv: epilogue not available for this precision");
+        }
+        return check_launch("spconv_g2_k");
+    }
 }
 
 template <typename T>
