@@ -5,24 +5,25 @@
 //   gauge_inputs_k  one thread per LiDAR pixel: the area-pooled valid depth z_lr (the window sums of
 //                   where(ok, depth, 0) and of ok, each / height / width, as F.interpolate(mode='area')), the mask
 //                   conf >= 2 & lidar > 0 & z_lr > 0 and y = log(max(lidar, 1e-3)) - log(max(z_lr, 1e-3))
-//   gauge_fit_k     one 1024-thread block per frame runs the iterations: the weighted normal equations
-//                   (A w)^T (A w) c = (A w)^T (y w) summed in fp64 and solved by Gaussian elimination with partial
-//                   pivoting (the reference: LAPACK least squares on the same fp32 products), the residuals
-//                   r = y - A c in fp32, their exact lower median by a 4-pass radix select on the float bits (LDS
-//                   histograms), and the weights min(2 sc / max(|r|, 1e-6), 1), sc = 1.4826 median + 1e-4
+//   per IRLS round  gauge_sums_k (a grid of blocks per frame: fp64 partial sums of the weighted normal equations
+//                   (A w)^T (A w) c = (A w)^T (y w) over the confident pixels), gauge_solve_k (one wave per frame:
+//                   the partials in a fixed order, Gaussian elimination with partial pivoting; the reference runs
+//                   LAPACK least squares on the same fp32 products), and, for every round but the last, the exact
+//                   lower median of |y - A c| (fp32 residuals) by three radix passes over its bits (gauge_hist_k:
+//                   grid-wide 2048-bin histograms of the candidates; gauge_select_k: the bucket holding the rank)
+//                   and the weights min(2 sc / max(|r|, 1e-6), 1), sc = 1.4826 median + 1e-4 (gauge_weights_k)
 //   gauge_apply_k   one thread per output pixel: exp of the polynomial (a sequential fp32 sum over the basis)
 //
 // The basis is (1, u, v) or (1, u, v, u^2, uv, v^2) on torch.linspace(-1, 1, n) grids (the scalar rule: step
 // 2 / (n - 1) in fp32, start + step i for the first half, end - step (n - 1 - i) for the second). A frame with
-// fewer than 200 confident pixels, or a non-finite solution, gets the correction 1. The fit is latency-bound work
-// on one CU per frame: the LiDAR map is at most a few hundred thousand pixels and the loop runs 3 times.
+// fewer than 200 confident pixels, or a singular / non-finite system, gets the correction 1. The frame state (valid,
+// count, median search) lives in device memory, so the whole sequence runs without a host round trip.
 #include <climits>
 
 #include "pmg_common.h"
 
 namespace pmg {
 
-constexpr int kGaugeThreads = 1024;
 constexpr int kGaugeMinPoints = 200;
 constexpr int kGaugeMaxK = 6;
 
@@ -73,179 +74,243 @@ __global__ __launch_bounds__(256) void gauge_inputs_k(const float* __restrict__ 
     m_out[q] = (cf >= 2.0f && ld > 0.0f && z > 0.0f) ? 1 : 0;
 }
 
-// Sum of a double over the block (all threads get it); `red` holds one slot per wave.
-__device__ inline double block_sum_f64(double v, double* red) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    __syncthreads();  // `red` is free
-    if (lane == 0) red[wv] = v;
-    __syncthreads();
-    double s = 0.0;
-    for (int k = 0; k < kGaugeThreads / 64; ++k) s += red[k];  // fixed order: identical in every thread
-    return s;
+// ---- the IRLS rounds, spread over the GPU: per round a grid of blocks sums the weighted normal equations
+// (fp64 partials per block), one wave per frame reduces them in a fixed order and solves; then (all but the last
+// round) three radix-select passes over the residual bits (11 + 11 + 10 bits: a grid-wide histogram of the
+// candidates, then one block per frame picks the bucket holding the median's rank) and the new weights.
+constexpr int kGaugeBlk = 256;       // threads of the grid kernels
+constexpr int kGaugeMaxBlocks = 256; // blocks per frame
+constexpr int kGaugeBins = 2048;
+constexpr int kGaugeVals = 28;       // 21 normal-matrix entries + 6 right-hand sides + count (K = 6; fewer for 3)
+
+struct GaugeState {
+    uint32_t prefix;  // median bits found so far
+    uint32_t rank;    // rank of the median among the candidates with that prefix
+    int32_t count;    // confident pixels
+    int32_t valid;    // 1 while the frame has a finite solution
+};
+
+__device__ inline void gauge_range(int64_t N, int nblk, int blk, int64_t& n0, int64_t& n1) {
+    n0 = N * blk / nblk;
+    n1 = N * (blk + 1) / nblk;
 }
 
 template <int K>
-__global__ __launch_bounds__(kGaugeThreads) void gauge_fit_k(const float* __restrict__ y_all,
-                                                             const uint8_t* __restrict__ m_all, int h, int w,
-                                                             int iters, float* __restrict__ w_all,
-                                                             uint32_t* __restrict__ r_all, float* __restrict__ coef_out) {
-    constexpr int NG = K * (K + 1) / 2;  // normal-matrix entries (upper triangle)
-    __shared__ double s_red[kGaugeThreads / 64];
-    __shared__ double s_sys[K][K + 1];
-    __shared__ float s_coef[K];
-    __shared__ int s_state;  // 1: valid solution
-    __shared__ uint32_t s_hist[256];
-    __shared__ uint32_t s_sel[2];  // radix select: prefix, rank
-
-    const int tid = threadIdx.x;
-    const int64_t N = (int64_t)h * w;
-    const int64_t base = (int64_t)blockIdx.x * N;
-    const float* y = y_all + base;
-    const uint8_t* m = m_all + base;
-    float* wt = w_all + base;
-    uint32_t* rb = r_all + base;
-
-    auto basis_at = [&](int64_t n, float (&a)[kGaugeMaxK]) {
+__global__ __launch_bounds__(kGaugeBlk) void gauge_sums_k(const float* __restrict__ y_all,
+                                                          const uint8_t* __restrict__ m_all,
+                                                          const float* __restrict__ w_all, int h, int w, int first,
+                                                          const GaugeState* __restrict__ st, int nblk,
+                                                          double* __restrict__ partials) {
+    constexpr int NG = K * (K + 1) / 2;
+    __shared__ double s_red[kGaugeBlk / 64][kGaugeVals];
+    const int b = blockIdx.y, tid = threadIdx.x;
+    if (!first && !st[b].valid) return;
+    const int64_t N = (int64_t)h * w, base = (int64_t)b * N;
+    int64_t n0, n1;
+    gauge_range(N, nblk, blockIdx.x, n0, n1);
+    double G[NG + K + 1];
+#pragma unroll
+    for (int k = 0; k < NG + K + 1; ++k) G[k] = 0.0;
+    for (int64_t n = n0 + tid; n < n1; n += kGaugeBlk) {
+        if (!m_all[base + n]) continue;
+        float a[kGaugeMaxK];
         const int iy = (int)(n / w), ix = (int)(n - (int64_t)iy * w);
         gauge_basis(linspace_at(ix, w), linspace_at(iy, h), a);
-    };
-
-    int count = 0;
-    for (int it = 0; it < iters; ++it) {
-        // normal equations of lstsq(A * wgt[:, None], y * wgt) (v3.py:178), fp64 sums of the fp32 products
-        double G[NG], g[K];
+        const float wn = first ? 1.0f : w_all[base + n];
+        float wa[K];
 #pragma unroll
-        for (int k = 0; k < NG; ++k) G[k] = 0.0;
+        for (int k = 0; k < K; ++k) wa[k] = a[k] * wn;
+        const float wy = y_all[base + n] * wn;
+        int e = 0;
 #pragma unroll
-        for (int k = 0; k < K; ++k) g[k] = 0.0;
-        int cnt = 0;
-        for (int64_t n = tid; n < N; n += kGaugeThreads) {
-            if (!m[n]) continue;
-            float a[kGaugeMaxK];
-            basis_at(n, a);
-            const float wn = it == 0 ? 1.0f : wt[n];
-            float wa[K];
+        for (int i = 0; i < K; ++i)
 #pragma unroll
-            for (int k = 0; k < K; ++k) wa[k] = a[k] * wn;
-            const float wy = y[n] * wn;
-            int e = 0;
+            for (int j = i; j < K; ++j) G[e++] += (double)wa[i] * (double)wa[j];
 #pragma unroll
-            for (int i = 0; i < K; ++i) {
+        for (int i = 0; i < K; ++i) G[NG + i] += (double)wa[i] * (double)wy;
+        G[NG + K] += 1.0;
+    }
+    const int wv = tid >> 6, lane = tid & 63;
 #pragma unroll
-                for (int j = i; j < K; ++j) G[e++] += (double)wa[i] * (double)wa[j];
-                g[i] += (double)wa[i] * (double)wy;
-            }
-            ++cnt;
-        }
-        if (it == 0) count = (int)block_sum_f64((double)cnt, s_red);
-        if (count < kGaugeMinPoints) {  // v3.py:174-175: the frame keeps the correction 1
-            if (tid == 0) s_state = 0;
-            break;
-        }
-        {
-            int e = 0;
+    for (int k = 0; k < NG + K + 1; ++k) {
+        double v = G[k];
 #pragma unroll
-            for (int i = 0; i < K; ++i) {
-#pragma unroll
-                for (int j = i; j < K; ++j) {
-                    const double v = block_sum_f64(G[e++], s_red);
-                    if (tid == 0) s_sys[i][j] = s_sys[j][i] = v;
-                }
-                const double v = block_sum_f64(g[i], s_red);
-                if (tid == 0) s_sys[i][K] = v;
-            }
-        }
-        if (tid == 0) {
-            // Gaussian elimination with partial pivoting on [G | g]
-            bool okk = true;
-            for (int c = 0; c < K && okk; ++c) {
-                int p = c;
-                for (int r = c + 1; r < K; ++r)
-                    if (fabs(s_sys[r][c]) > fabs(s_sys[p][c])) p = r;
-                if (!(fabs(s_sys[p][c]) > 0.0)) {
-                    okk = false;
-                    break;
-                }
-                if (p != c)
-                    for (int k = 0; k <= K; ++k) {
-                        const double t = s_sys[c][k];
-                        s_sys[c][k] = s_sys[p][k];
-                        s_sys[p][k] = t;
-                    }
-                for (int r = c + 1; r < K; ++r) {
-                    const double f = s_sys[r][c] / s_sys[c][c];
-                    for (int k = c; k <= K; ++k) s_sys[r][k] -= f * s_sys[c][k];
-                }
-            }
-            double x[K];
-            for (int c = K - 1; c >= 0 && okk; --c) {
-                double s = s_sys[c][K];
-                for (int k = c + 1; k < K; ++k) s -= s_sys[c][k] * x[k];
-                x[c] = s / s_sys[c][c];
-            }
-            for (int k = 0; k < K && okk; ++k) {
-                s_coef[k] = (float)x[k];
-                okk = __builtin_isfinite(s_coef[k]);
-            }
-            s_state = okk ? 1 : 0;
-        }
-        __syncthreads();
-        if (!s_state || it + 1 == iters) break;  // the last weights are never used
-
-        // residuals |y - A c| (fp32, terms in basis order), then their lower median over the masked pixels
-        for (int64_t n = tid; n < N; n += kGaugeThreads) {
-            if (!m[n]) continue;
-            float a[kGaugeMaxK];
-            basis_at(n, a);
-            float p = 0.0f;
-#pragma unroll
-            for (int k = 0; k < K; ++k) p = p + a[k] * s_coef[k];
-            rb[n] = __float_as_uint(fabsf(y[n] - p));
-        }
-        if (tid == 0) {
-            s_sel[0] = 0u;
-            s_sel[1] = (uint32_t)((count - 1) / 2);  // torch.median: the lower middle element
-        }
-        for (int pass = 0; pass < 4; ++pass) {
-            const int sh = 24 - 8 * pass;
-            const uint32_t hmask = pass == 0 ? 0u : (0xffffffffu << (sh + 8));
-            if (tid < 256) s_hist[tid] = 0u;
-            __syncthreads();
-            const uint32_t prefix = s_sel[0];
-            for (int64_t n = tid; n < N; n += kGaugeThreads) {
-                if (!m[n]) continue;
-                const uint32_t v = rb[n];
-                if ((v & hmask) == prefix) atomicAdd(&s_hist[(v >> sh) & 0xffu], 1u);
-            }
-            __syncthreads();
-            if (tid == 0) {
-                uint32_t k = s_sel[1], cum = 0u;
-                int bkt = 0;
-                for (; bkt < 255; ++bkt) {
-                    if (cum + s_hist[bkt] > k) break;
-                    cum += s_hist[bkt];
-                }
-                s_sel[0] = prefix | ((uint32_t)bkt << sh);
-                s_sel[1] = k - cum;
-            }
-            __syncthreads();
-        }
-        const float med = __uint_as_float(s_sel[0]);
-        const float sc = 1.4826f * med + 1e-4f;
-        for (int64_t n = tid; n < N; n += kGaugeThreads) {
-            if (!m[n]) continue;
-            wt[n] = fmin_((2.0f * sc) / fmax_(__uint_as_float(rb[n]), 1e-6f), 1.0f);
-        }
-        __syncthreads();
+        for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+        if (lane == 0) s_red[wv][k] = v;
     }
     __syncthreads();
-    if (tid < 8) {
-        float v = 0.0f;
-        if (tid < K) v = s_state ? s_coef[tid] : 0.0f;
-        if (tid == 7) v = s_state ? 1.0f : 0.0f;
-        coef_out[blockIdx.x * 8 + tid] = v;
+    if (tid < NG + K + 1) {
+        double v = 0.0;
+        for (int q = 0; q < kGaugeBlk / 64; ++q) v += s_red[q][tid];
+        partials[((int64_t)b * nblk + blockIdx.x) * kGaugeVals + tid] = v;
+    }
+}
+
+// One wave per frame: the fixed-order reduction of the block partials, the count test, the solve (lane 0), and
+// the set-up of the median search; it also clears the frame's histogram for the first pass.
+template <int K>
+__global__ __launch_bounds__(64) void gauge_solve_k(const double* __restrict__ partials, int nblk, int first,
+                                                    GaugeState* __restrict__ st, float* __restrict__ coef,
+                                                    uint32_t* __restrict__ hist) {
+    constexpr int NG = K * (K + 1) / 2;
+    __shared__ double s_v[kGaugeVals];
+    const int b = blockIdx.x, lane = threadIdx.x;
+    for (int i = lane; i < kGaugeBins; i += 64) hist[(int64_t)b * kGaugeBins + i] = 0u;
+    if (!first && !st[b].valid) return;
+    if (lane < NG + K + 1) {
+        double v = 0.0;
+        for (int q = 0; q < nblk; ++q) v += partials[((int64_t)b * nblk + q) * kGaugeVals + lane];
+        s_v[lane] = v;
+    }
+    __syncthreads();
+    if (lane != 0) return;
+    const int count = (int)s_v[NG + K];
+    bool okk = count >= kGaugeMinPoints;  // v3.py:174-175: the frame keeps the correction 1
+    double A[K][K + 1];
+    {
+        int e = 0;
+        for (int i = 0; i < K; ++i) {
+            for (int j = i; j < K; ++j) {
+                A[i][j] = A[j][i] = s_v[e];
+                ++e;
+            }
+            A[i][K] = s_v[NG + i];
+        }
+    }
+    // Gaussian elimination with partial pivoting on [G | g]
+    for (int c = 0; c < K && okk; ++c) {
+        int p = c;
+        for (int r = c + 1; r < K; ++r)
+            if (fabs(A[r][c]) > fabs(A[p][c])) p = r;
+        if (!(fabs(A[p][c]) > 0.0)) {
+            okk = false;
+            break;
+        }
+        if (p != c)
+            for (int k = 0; k <= K; ++k) {
+                const double t = A[c][k];
+                A[c][k] = A[p][k];
+                A[p][k] = t;
+            }
+        for (int r = c + 1; r < K; ++r) {
+            const double f = A[r][c] / A[c][c];
+            for (int k = c; k <= K; ++k) A[r][k] -= f * A[c][k];
+        }
+    }
+    double x[K];
+    for (int c = K - 1; c >= 0 && okk; --c) {
+        double s = A[c][K];
+        for (int k = c + 1; k < K; ++k) s -= A[c][k] * x[k];
+        x[c] = s / A[c][c];
+    }
+    float cf[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int k = 0; k < K && okk; ++k) {
+        cf[k] = (float)x[k];
+        okk = __builtin_isfinite(cf[k]);
+    }
+    cf[7] = okk ? 1.0f : 0.0f;
+    for (int k = 0; k < 8; ++k) coef[b * 8 + k] = okk || k == 7 ? cf[k] : 0.0f;
+    GaugeState g;
+    g.prefix = 0u;
+    g.rank = okk ? (uint32_t)((count - 1) / 2) : 0u;  // torch.median: the lower middle element
+    g.count = count;
+    g.valid = okk ? 1 : 0;
+    st[b] = g;
+}
+
+// Radix pass `pass` (bits 31..21, 20..10, 9..0) of the median of |y - A c| over the confident pixels; pass 0 also
+// computes and keeps the residual bits (fp32, terms in basis order).
+template <int K>
+__global__ __launch_bounds__(kGaugeBlk) void gauge_hist_k(int pass, const float* __restrict__ y_all,
+                                                          const uint8_t* __restrict__ m_all, int h, int w,
+                                                          const float* __restrict__ coef,
+                                                          const GaugeState* __restrict__ st, int nblk,
+                                                          uint32_t* __restrict__ r_all, uint32_t* __restrict__ hist) {
+    __shared__ uint32_t s_h[kGaugeBins];
+    const int b = blockIdx.y, tid = threadIdx.x;
+    if (!st[b].valid) return;
+    for (int i = tid; i < kGaugeBins; i += kGaugeBlk) s_h[i] = 0u;
+    __syncthreads();
+    const int64_t N = (int64_t)h * w, base = (int64_t)b * N;
+    int64_t n0, n1;
+    gauge_range(N, nblk, blockIdx.x, n0, n1);
+    const int sh = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
+    const uint32_t bmask = pass == 2 ? 0x3ffu : 0x7ffu;
+    const uint32_t hmask = pass == 0 ? 0u : (pass == 1 ? 0xffe00000u : 0xfffffc00u);
+    const uint32_t prefix = st[b].prefix;
+    float c[kGaugeMaxK];
+#pragma unroll
+    for (int k = 0; k < kGaugeMaxK; ++k) c[k] = k < K ? coef[b * 8 + k] : 0.0f;
+    for (int64_t n = n0 + tid; n < n1; n += kGaugeBlk) {
+        if (!m_all[base + n]) continue;
+        uint32_t v;
+        if (pass == 0) {
+            float a[kGaugeMaxK];
+            const int iy = (int)(n / w), ix = (int)(n - (int64_t)iy * w);
+            gauge_basis(linspace_at(ix, w), linspace_at(iy, h), a);
+            float p = 0.0f;
+#pragma unroll
+            for (int k = 0; k < K; ++k) p = p + a[k] * c[k];
+            v = __float_as_uint(fabsf(y_all[base + n] - p));
+            r_all[base + n] = v;
+        } else {
+            v = r_all[base + n];
+        }
+        if ((v & hmask) == prefix) atomicAdd(&s_h[(v >> sh) & bmask], 1u);
+    }
+    __syncthreads();
+    uint32_t* hg = hist + (int64_t)b * kGaugeBins;
+    for (int i = tid; i < kGaugeBins; i += kGaugeBlk)
+        if (s_h[i]) atomicAdd(&hg[i], s_h[i]);
+}
+
+// One block per frame: the bucket of the pass that holds the rank; clears the histogram for the next pass.
+__global__ __launch_bounds__(kGaugeBlk) void gauge_select_k(int pass, GaugeState* __restrict__ st,
+                                                            uint32_t* __restrict__ hist) {
+    __shared__ uint32_t s_h[kGaugeBins];
+    __shared__ uint32_t s_part[kGaugeBlk];
+    const int b = blockIdx.x, tid = threadIdx.x;
+    uint32_t* hg = hist + (int64_t)b * kGaugeBins;
+    const bool valid = st[b].valid != 0;
+    constexpr int PER = kGaugeBins / kGaugeBlk;  // 8 bins per thread
+    uint32_t sum = 0u;
+    for (int k = 0; k < PER; ++k) {
+        const uint32_t v = valid ? hg[tid * PER + k] : 0u;
+        s_h[tid * PER + k] = v;
+        sum += v;
+    }
+    s_part[tid] = sum;
+    __syncthreads();
+    for (int i = tid; i < kGaugeBins; i += kGaugeBlk) hg[i] = 0u;
+    if (!valid || tid != 0) return;
+    const int sh = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
+    const int nb = pass == 2 ? 1024 : 2048;
+    uint32_t k = st[b].rank, cum = 0u;
+    int t = 0;
+    while (t < kGaugeBlk - 1 && cum + s_part[t] <= k) cum += s_part[t++];
+    int bkt = t * PER;
+    for (; bkt < nb - 1; ++bkt) {
+        if (cum + s_h[bkt] > k) break;
+        cum += s_h[bkt];
+    }
+    st[b].prefix |= (uint32_t)bkt << sh;
+    st[b].rank = k - cum;
+}
+
+__global__ __launch_bounds__(kGaugeBlk) void gauge_weights_k(const uint8_t* __restrict__ m_all, int h, int w,
+                                                             const GaugeState* __restrict__ st, int nblk,
+                                                             const uint32_t* __restrict__ r_all,
+                                                             float* __restrict__ w_all) {
+    const int b = blockIdx.y, tid = threadIdx.x;
+    if (!st[b].valid) return;
+    const int64_t N = (int64_t)h * w, base = (int64_t)b * N;
+    int64_t n0, n1;
+    gauge_range(N, nblk, blockIdx.x, n0, n1);
+    const float med = __uint_as_float(st[b].prefix);
+    const float sc = 1.4826f * med + 1e-4f;
+    for (int64_t n = n0 + tid; n < n1; n += kGaugeBlk) {
+        if (!m_all[base + n]) continue;
+        w_all[base + n] = fmin_((2.0f * sc) / fmax_(__uint_as_float(r_all[base + n]), 1e-6f), 1.0f);
     }
 }
 
@@ -275,12 +340,45 @@ __global__ __launch_bounds__(256) void gauge_apply_k(const float* __restrict__ c
 
 using namespace pmg;
 
+static int gauge_blocks(int64_t N) {
+    const int64_t nb = (N + 1023) / 1024;
+    return (int)(nb < 1 ? 1 : (nb > kGaugeMaxBlocks ? kGaugeMaxBlocks : nb));
+}
+
+template <int K>
+static int gauge_rounds(const float* y, const uint8_t* m, int B, int h, int w, int iters, float* wt, uint32_t* rb,
+                        double* partials, uint32_t* hist, GaugeState* st, float* coef, hipStream_t s) {
+    const int nblk = gauge_blocks((int64_t)h * w);
+    const dim3 grid((unsigned)nblk, (unsigned)B);
+    for (int it = 0; it < iters; ++it) {
+        const int first = it == 0;
+        hipLaunchKernelGGL(gauge_sums_k<K>, grid, dim3(kGaugeBlk), 0, s, y, m, wt, h, w, first, st, nblk, partials);
+        if (int e = check_launch("gauge_sums_k")) return e;
+        hipLaunchKernelGGL(gauge_solve_k<K>, dim3(B), dim3(64), 0, s, partials, nblk, first, st, coef, hist);
+        if (int e = check_launch("gauge_solve_k")) return e;
+        if (it + 1 == iters) break;  // the last weights are never used
+        for (int pass = 0; pass < 3; ++pass) {
+            hipLaunchKernelGGL(gauge_hist_k<K>, grid, dim3(kGaugeBlk), 0, s, pass, y, m, h, w, coef, st, nblk, rb,
+                               hist);
+            if (int e = check_launch("gauge_hist_k")) return e;
+            hipLaunchKernelGGL(gauge_select_k, dim3(B), dim3(kGaugeBlk), 0, s, pass, st, hist);
+            if (int e = check_launch("gauge_select_k")) return e;
+        }
+        hipLaunchKernelGGL(gauge_weights_k, grid, dim3(kGaugeBlk), 0, s, m, h, w, st, nblk, rb, wt);
+        if (int e = check_launch("gauge_weights_k")) return e;
+    }
+    return PMG_OK;
+}
+
 extern "C" {
 
 size_t pmg_gauge_poly_workspace_bytes(int B, int h, int w) {
     if (B < 1 || h < 1 || w < 1) return 0;
     const size_t n = (size_t)B * h * w;
-    return align256(n * 4) + align256(n) + align256(n * 4) + align256(n * 4);
+    const int nblk = gauge_blocks((int64_t)h * w);
+    return align256(n * 4) + align256(n) + align256(n * 4) + align256(n * 4) +
+           align256((size_t)B * nblk * kGaugeVals * sizeof(double)) + align256((size_t)B * kGaugeBins * 4) +
+           align256((size_t)B * sizeof(GaugeState));
 }
 
 int pmg_gauge_poly(const float* depth, int B, int H, int W, const float* lidar, const float* conf, int h, int w,
@@ -288,12 +386,13 @@ int pmg_gauge_poly(const float* depth, int B, int H, int W, const float* lidar, 
                    void* stream) {
     PMG_REQUIRE(depth && lidar && corr && coef, "null buffer");
     PMG_REQUIRE(B >= 1 && H >= 1 && W >= 1 && h >= 1 && w >= 1, "bad shape");
-    PMG_REQUIRE((int64_t)B * H * W < INT_MAX && (int64_t)B * h * w < INT_MAX, "map too large");
+    PMG_REQUIRE((int64_t)B * H * W < INT_MAX && (int64_t)B * h * w < INT_MAX && B <= 65535, "map too large");
     PMG_REQUIRE(degree >= 1, "degree must be >= 1");
     PMG_REQUIRE(iters >= 1 && iters <= 64, "iters must be in [1, 64]");
     PMG_REQUIRE(workspace && workspace_bytes >= pmg_gauge_poly_workspace_bytes(B, h, w), "workspace too small");
     hipStream_t s = (hipStream_t)stream;
     const int64_t n_lr = (int64_t)B * h * w, n_out = (int64_t)B * H * W;
+    const int nblk = gauge_blocks((int64_t)h * w);
     uint8_t* p = (uint8_t*)workspace;
     float* y = (float*)p;
     p += align256((size_t)n_lr * 4);
@@ -302,19 +401,21 @@ int pmg_gauge_poly(const float* depth, int B, int H, int W, const float* lidar, 
     float* wt = (float*)p;
     p += align256((size_t)n_lr * 4);
     uint32_t* rb = (uint32_t*)p;
+    p += align256((size_t)n_lr * 4);
+    double* partials = (double*)p;
+    p += align256((size_t)B * nblk * kGaugeVals * sizeof(double));
+    uint32_t* hist = (uint32_t*)p;
+    p += align256((size_t)B * kGaugeBins * 4);
+    GaugeState* st = (GaugeState*)p;
     hipLaunchKernelGGL(gauge_inputs_k, dim3((unsigned)((n_lr + 255) / 256)), dim3(256), 0, s, depth, lidar, conf, H, W,
                        h, w, n_lr, y, m);
     if (int e = check_launch("gauge_inputs_k")) return e;
     if (degree >= 2) {
-        hipLaunchKernelGGL(gauge_fit_k<6>, dim3(B), dim3(kGaugeThreads), 0, s, y, m, h, w, iters, wt, rb, coef);
-    } else {
-        hipLaunchKernelGGL(gauge_fit_k<3>, dim3(B), dim3(kGaugeThreads), 0, s, y, m, h, w, iters, wt, rb, coef);
-    }
-    if (int e = check_launch("gauge_fit_k")) return e;
-    if (degree >= 2) {
+        if (int e = gauge_rounds<6>(y, m, B, h, w, iters, wt, rb, partials, hist, st, coef, s)) return e;
         hipLaunchKernelGGL(gauge_apply_k<6>, dim3((unsigned)((n_out + 255) / 256)), dim3(256), 0, s, coef, H, W, n_out,
                            corr);
     } else {
+        if (int e = gauge_rounds<3>(y, m, B, h, w, iters, wt, rb, partials, hist, st, coef, s)) return e;
         hipLaunchKernelGGL(gauge_apply_k<3>, dim3((unsigned)((n_out + 255) / 256)), dim3(256), 0, s, coef, H, W, n_out,
                            corr);
     }
