@@ -95,3 +95,36 @@ def test_nearest_fill_rejected_on_host(libpmg):
     # workspace too small
     assert libpmg.pmg_nearest_fill(dummy, None, 1, 8, 8, dummy, None, None, dummy, ws - 1,
                                    None) == _lib.PMG_E_INVALID
+
+
+def test_gauge_rejected_on_host(libpmg):
+    dummy = C.c_void_p(16)
+    ws = libpmg.pmg_gauge_poly_workspace_bytes(2, 24, 32)
+    assert ws >= 2 * 24 * 32 * 13
+    assert libpmg.pmg_gauge_poly_workspace_bytes(0, 24, 32) == 0
+    args = lambda **k: dict(dict(depth=dummy, B=2, H=48, W=64, lidar=dummy, conf=None, h=24, w=32, degree=2, iters=3,
+                                 corr=dummy, coef=dummy, ws=dummy, wsb=ws), **k)
+    call = lambda a: libpmg.pmg_gauge_poly(a["depth"], a["B"], a["H"], a["W"], a["lidar"], a["conf"], a["h"], a["w"],
+                                           a["degree"], a["iters"], a["corr"], a["coef"], a["ws"], a["wsb"], None)
+    assert call(args(degree=0)) == _lib.PMG_E_INVALID           # degree must be >= 1
+    assert call(args(iters=0)) == _lib.PMG_E_INVALID            # the reference needs one lstsq round
+    assert call(args(wsb=ws - 1)) == _lib.PMG_E_INVALID         # workspace too small
+    assert call(args(corr=None)) == _lib.PMG_E_INVALID          # null output
+    assert call(args(h=0)) == _lib.PMG_E_INVALID
+
+
+def test_refiner_create_rejects_bad_gate_and_anchor(libpmg):
+    base = (1, 8, 8, 32, 1, 0, 256.0, 8, 8, 4, 0.2, 32, 1, 0, 0, 1)
+    for extra in [(1, 1.5, 0.0), (1, -0.1, 0.0), (0, 0.1, 1.5), (0, 0.1, -0.5)]:
+        cfg = _lib.RefinerConfig(*base, *extra)
+        assert not libpmg.pmg_refiner_create(C.byref(cfg))
+        assert b"unsupported" in libpmg.pmg_last_error()
+
+
+def test_python_ops_refuse_host_tensors():
+    import torch
+
+    from promptmoge_amd import ops
+
+    with pytest.raises(ValueError, match="GPU tensor"):
+        ops.gauge_poly(torch.ones(1, 8, 8), torch.ones(1, 4, 4))
