@@ -11,9 +11,9 @@
 // output rows. The number of output rows is written to device memory (the caller reads it once, as the
 // reference's int(...) does).
 //
-// Radix pass, over tiles of 4096 keys: pool_hist_k counts the tile's digits (LDS atomics), pool_scan_k (one
+// Radix pass, over tiles of 2048 keys: pool_hist_k counts the tile's digits (LDS atomics), pool_scan_k (one
 // block) turns the digit-major counts into each (digit, tile)'s output base, pool_scatter_k places the keys of
-// each tile in 16 rounds of 256: a key's rank among equal digits of its round comes from 9 wave ballots plus the
+// each tile in 8 rounds of 256: a key's rank among equal digits of its round comes from 9 wave ballots plus the
 // counts of the lower waves, so the pass is stable and deterministic.
 //
 // sparse_pool: one thread per (output row, 4 channels) sums its group's rows in seg_indices order -- input order,
@@ -26,8 +26,8 @@
 namespace pmg {
 
 constexpr int kPoolThreads = 256;
-constexpr int kPoolRounds = 16;
-constexpr int kPoolTile = kPoolThreads * kPoolRounds;  // 4096 keys per tile
+constexpr int kPoolRounds = 8;
+constexpr int kPoolTile = kPoolThreads * kPoolRounds;  // 2048 keys per tile
 
 struct PoolGeom {
     int64_t in[4];   // B, X, Y, Z of the input grid
@@ -68,27 +68,55 @@ __global__ __launch_bounds__(kPoolThreads) void pool_hist_k(const uint64_t* __re
 }
 
 // One block of 1024 threads: exclusive scan of n counts in place; the total goes to *total if given.
+// Exclusive scan of v[0, n) in place (and its total), one block: chunks of 8192 values are loaded coalesced into
+// LDS (all loads in flight at once), each thread scans 8 consecutive values, the 1024 thread sums are scanned by
+// wave shuffles and the 16 wave totals, and the chunk is stored back coalesced with the running carry.
 __global__ __launch_bounds__(1024) void pool_scan_k(uint32_t* v, int n, unsigned long long* total) {
-    __shared__ uint32_t part[1024];
-    const int per = (n + 1023) / 1024;
-    const int lo = threadIdx.x * per, hi = min(lo + per, n);
-    uint32_t s = 0;
-    for (int i = lo; i < hi; ++i) s += v[i];
-    part[threadIdx.x] = s;
-    __syncthreads();
-    for (int off = 1; off < 1024; off <<= 1) {
-        const uint32_t add = threadIdx.x >= off ? part[threadIdx.x - off] : 0u;
+    constexpr int PER = 8, CH = 1024 * PER;
+    __shared__ uint32_t s_v[CH];
+    __shared__ uint32_t part[16];
+    const int t = threadIdx.x;
+    uint32_t carry = 0u;
+    for (int base = 0; base < n; base += CH) {
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            const int i = base + k * 1024 + t;
+            s_v[k * 1024 + t] = i < n ? v[i] : 0u;
+        }
         __syncthreads();
-        part[threadIdx.x] += add;
+        uint32_t loc[PER], sum = 0u;
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            loc[k] = sum;
+            sum += s_v[t * PER + k];
+        }
+        // inclusive scan of the thread sums: within each wave by shuffles, then the 16 wave totals
+        uint32_t inc = sum;
+        const int lane = t & 63, wv = t >> 6;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const uint32_t y = __shfl_up(inc, off, 64);
+            if (lane >= off) inc += y;
+        }
+        if (lane == 63) part[wv] = inc;
         __syncthreads();
+        uint32_t wbase = 0u;
+        for (int q = 0; q < wv; ++q) wbase += part[q];
+        uint32_t ctot = 0u;
+        for (int q = 0; q < 16; ++q) ctot += part[q];
+        const uint32_t before = carry + wbase + inc - sum;
+#pragma unroll
+        for (int k = 0; k < PER; ++k) s_v[t * PER + k] = before + loc[k];
+        carry += ctot;
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            const int i = base + k * 1024 + t;
+            if (i < n) v[i] = s_v[k * 1024 + t];
+        }
+        __syncthreads();  // the next chunk overwrites s_v and part
     }
-    uint32_t run = part[threadIdx.x] - s;
-    for (int i = lo; i < hi; ++i) {
-        const uint32_t t = v[i];
-        v[i] = run;
-        run += t;
-    }
-    if (total && threadIdx.x == 1023) total[0] = part[1023];
+    if (total && t == 0) total[0] = carry;
 }
 
 // vals_in == nullptr: the value of key i is i (the first pass).
