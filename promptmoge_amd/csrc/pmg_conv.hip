@@ -656,7 +656,7 @@ int pmg_spconv_i8(const int8_t* x, const int32_t* nmap_t, const uint32_t* tile_m
     // The block-tiled kernel addresses x and the map through 32-bit buffer offsets.
     const bool fits32 = M * 27 * 4 < ((int64_t)1 << 31) && M * Ci < ((int64_t)1 << 31);
     if (Ci == Co && (Ci == 64 || Ci == 128) && fits32 && epilogue != PMG_EPI_SILU && aligned16(out) &&
-        (epilogue != PMG_EPI_R || aligned16(skip))) {
+        aligned16(x) && aligned16(w) && (epilogue != PMG_EPI_R || aligned16(skip))) {
         if (Ci == 64) return launch_g2<64>(a, epilogue, (hipStream_t)stream);
         return launch_g2<128>(a, epilogue, (hipStream_t)stream);
     }
@@ -674,8 +674,9 @@ int pmg_spconv_i8_ordered(const int8_t* x, const int32_t* nmap_t, const int32_t*
     PMG_REQUIRE((epilogue != PMG_EPI_Q && epilogue != PMG_EPI_QLIN) || out_mult > 0.0f, "out_mult must be positive");
     PMG_REQUIRE(Ci == Co && (Ci == 64 || Ci == 128), "pmg_spconv_i8_ordered: Ci = Co = 64 or 128");
     PMG_REQUIRE(M * 27 * 4 < ((int64_t)1 << 31) && M * Ci < ((int64_t)1 << 31), "pmg_spconv_i8_ordered: M too large");
-    PMG_REQUIRE(epilogue != PMG_EPI_SILU && aligned16(out) && (epilogue != PMG_EPI_R || aligned16(skip)),
-                "pmg_spconv_i8_ordered: unsupported epilogue or unaligned output");
+    PMG_REQUIRE(epilogue != PMG_EPI_SILU && aligned16(out) && aligned16(x) && aligned16(w) &&
+                    (epilogue != PMG_EPI_R || aligned16(skip)),
+                "pmg_spconv_i8_ordered: unsupported epilogue or unaligned x / w / output");
     if (M == 0) return PMG_OK;
     ConvArgs a{(const uint8_t*)x, nmap_t, order_tile_mask, (const uint8_t*)w, M, Co, Ci, Ci / 16,
                a_scale, w_scale, bias, out_mult, skip, out, order};
