@@ -16,8 +16,10 @@ Modules
   fill       nearest_fill (promptmoge/model.py:61-72): the exact EDT feature transform in two separable passes
   pool       build_pool_cache / sparse_pool / sparse_upsample (_core.py:339-505): perfect-partition pooling with
              sorted unique output keys, mean/sum in input order, nearest upsampling by parent
+  gauge      prompt_gauge_poly (v3.py:151-183): pooled inputs, IRLS with the lower median, exp(poly) correction
   refiner    the fused step (v3.py:346-383, 547-576; sparse_unet.py:176-258 single level; flex_sparse_blocks.py:70-75)
-             in the deployed int8 / fp16 arithmetic, and the reference's fp32 fake-quant (QAT) formulation
+             in the deployed int8 / fp16 arithmetic, and the reference's fp32 fake-quant (QAT) formulation; the refine
+             loop's output gate and elastic anchor (v3.py:565-573)
 
 What pins each function (golden vectors, closed forms, brute force, invariants) is listed in tests/test_oracle*.py.
 The reference ships no golden vectors or tests for this path.
