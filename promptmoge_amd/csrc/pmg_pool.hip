@@ -119,6 +119,76 @@ __global__ __launch_bounds__(1024) void pool_scan_k(uint32_t* v, int n, unsigned
     if (total && t == 0) total[0] = carry;
 }
 
+// Large scans run on a grid: pool_scan_chunk_k scans each 8192-value chunk in place (local exclusive values) and
+// writes its total to ctot[chunk]; the totals are scanned by pool_scan_k; pool_scan_add_k adds them back.
+__global__ __launch_bounds__(1024) void pool_scan_chunk_k(uint32_t* v, int n, uint32_t* ctot) {
+    constexpr int PER = 8, CH = 1024 * PER;
+    __shared__ uint32_t s_v[CH];
+    __shared__ uint32_t part[16];
+    const int t = threadIdx.x, base = blockIdx.x * CH;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const int i = base + k * 1024 + t;
+        s_v[k * 1024 + t] = i < n ? v[i] : 0u;
+    }
+    __syncthreads();
+    uint32_t loc[PER], sum = 0u;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        loc[k] = sum;
+        sum += s_v[t * PER + k];
+    }
+    uint32_t inc = sum;
+    const int lane = t & 63, wv = t >> 6;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t y = __shfl_up(inc, off, 64);
+        if (lane >= off) inc += y;
+    }
+    if (lane == 63) part[wv] = inc;
+    __syncthreads();
+    uint32_t wbase = 0u, ctot_ = 0u;
+    for (int q = 0; q < 16; ++q) {
+        wbase += q < wv ? part[q] : 0u;
+        ctot_ += part[q];
+    }
+    const uint32_t before = wbase + inc - sum;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) s_v[t * PER + k] = before + loc[k];
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const int i = base + k * 1024 + t;
+        if (i < n) v[i] = s_v[k * 1024 + t];
+    }
+    if (t == 0) ctot[blockIdx.x] = ctot_;
+}
+
+__global__ __launch_bounds__(1024) void pool_scan_add_k(uint32_t* v, int n, const uint32_t* ctot) {
+    constexpr int CH = 1024 * 8;
+    const uint32_t add = ctot[blockIdx.x];
+    for (int k = 0; k < 8; ++k) {
+        const int i = blockIdx.x * CH + k * 1024 + threadIdx.x;
+        if (i < n) v[i] += add;
+    }
+}
+
+// Exclusive scan of v[0, n) (and its total): one block for up to one chunk, else the three-kernel grid scan.
+static int pool_scan(uint32_t* v, int n, unsigned long long* total, uint32_t* ctot, hipStream_t s) {
+    constexpr int CH = 1024 * 8;
+    if (n <= CH) {
+        hipLaunchKernelGGL(pool_scan_k, dim3(1), dim3(1024), 0, s, v, n, total);
+        return check_launch("pool_scan_k");
+    }
+    const int nc = (n + CH - 1) / CH;
+    hipLaunchKernelGGL(pool_scan_chunk_k, dim3(nc), dim3(1024), 0, s, v, n, ctot);
+    if (int e = check_launch("pool_scan_chunk_k")) return e;
+    hipLaunchKernelGGL(pool_scan_k, dim3(1), dim3(1024), 0, s, ctot, nc, total);
+    if (int e = check_launch("pool_scan_k")) return e;
+    hipLaunchKernelGGL(pool_scan_add_k, dim3(nc), dim3(1024), 0, s, v, n, (const uint32_t*)ctot);
+    return check_launch("pool_scan_add_k");
+}
+
 // vals_in == nullptr: the value of key i is i (the first pass).
 __global__ __launch_bounds__(kPoolThreads) void pool_scatter_k(const uint64_t* __restrict__ keys_in,
                                                                const int32_t* __restrict__ vals_in, int64_t M,
@@ -292,7 +362,8 @@ size_t pmg_pool_cache_workspace_bytes(int64_t M) {
     if (M < 0) return 0;
     const size_t n = (size_t)(M > 0 ? M : 1);
     const size_t nt = (size_t)pool_tiles(M > 0 ? M : 1);
-    return 2 * pool_align(n * 8) + 2 * pool_align(n * 4) + pool_align(256 * nt * 4) + pool_align(nt * 4);
+    return 2 * pool_align(n * 8) + 2 * pool_align(n * 4) + pool_align(256 * nt * 4) + pool_align(nt * 4) +
+           pool_align((256 * nt / 8192 + 2) * 4);
 }
 
 int pmg_pool_cache(const int32_t* coords, int64_t M, const int64_t* sparse_shape, const int32_t* stride,
@@ -338,6 +409,8 @@ int pmg_pool_cache(const int32_t* coords, int64_t M, const int64_t* sparse_shape
     uint32_t* hist = (uint32_t*)p;
     p += pool_align(256 * (size_t)nt * 4);
     uint32_t* tcnt = (uint32_t*)p;
+    p += pool_align((size_t)nt * 4);
+    uint32_t* ctot = (uint32_t*)p;
 
     const unsigned g256 = (unsigned)((M + 255) / 256);
     hipLaunchKernelGGL(pool_keys_k, dim3(g256), dim3(256), 0, s, (const int4*)coords, M, pg, kb[0],
@@ -355,8 +428,7 @@ int pmg_pool_cache(const int32_t* coords, int64_t M, const int64_t* sparse_shape
         int32_t* vout = pass == npass - 1 ? seg_indices : vb[cur ^ 1];
         hipLaunchKernelGGL(pool_hist_k, dim3(nt), dim3(kPoolThreads), 0, s, kin, M, shift, nt, hist);
         if (int e = check_launch("pool_hist_k")) return e;
-        hipLaunchKernelGGL(pool_scan_k, dim3(1), dim3(1024), 0, s, hist, 256 * nt, (unsigned long long*)nullptr);
-        if (int e = check_launch("pool_scan_k")) return e;
+        if (int e = pool_scan(hist, 256 * nt, nullptr, ctot, s)) return e;
         hipLaunchKernelGGL(pool_scatter_k, dim3(nt), dim3(kPoolThreads), 0, s, kin, vin, M, shift, nt,
                            (const uint32_t*)hist, kout, vout);
         if (int e = check_launch("pool_scatter_k")) return e;
@@ -365,8 +437,7 @@ int pmg_pool_cache(const int32_t* coords, int64_t M, const int64_t* sparse_shape
     const uint64_t* sk = kb[cur];
     hipLaunchKernelGGL(pool_count_k, dim3(nt), dim3(kPoolThreads), 0, s, sk, M, tcnt);
     if (int e = check_launch("pool_count_k")) return e;
-    hipLaunchKernelGGL(pool_scan_k, dim3(1), dim3(1024), 0, s, tcnt, nt, (unsigned long long*)counts);
-    if (int e = check_launch("pool_scan_k")) return e;
+    if (int e = pool_scan(tcnt, nt, (unsigned long long*)counts, ctot, s)) return e;
     hipLaunchKernelGGL(pool_emit_k, dim3(nt), dim3(kPoolThreads), 0, s, sk, (const int32_t*)seg_indices, M,
                        (const uint32_t*)tcnt, pg, (const unsigned long long*)counts, parent, seg_offsets,
                        (int4*)out_coords);
