@@ -326,10 +326,10 @@ def calibrate(w: RefinerW, scene: Scene, crop: int = 96, pct: float = 99.95) -> 
     from an fp32 forward of the refiner on a central crop of `scene` (prompt features off). Calibration only: the
     arithmetic that is benchmarked and tested is elsewhere."""
     H, W, _ = scene.points.shape
-    h0, w0 = (H - crop) // 2, (W - crop) // 2
-    pts = scene.points[h0:h0 + crop, w0:w0 + crop].astype(np.float64)
+    Hc, Wc = min(crop, H), min(crop, W)  # the whole map when it is smaller than the crop
+    h0, w0 = (H - Hc) // 2, (W - Wc) // 2
+    pts = scene.points[h0:h0 + Hc, w0:w0 + Wc].astype(np.float64)
     z = np.rint(pts[..., 2].astype(np.float32) * np.float32(256.0)).astype(np.int64)
-    Hc = Wc = crop
     x = pts.reshape(-1, 3) @ w.in_w.T.astype(np.float64) + w.in_b
     # column stencil neighbour lists
     idx = np.arange(Hc * Wc).reshape(Hc, Wc)

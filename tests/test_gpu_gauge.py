@@ -102,3 +102,15 @@ def test_gauge_reference_signature(gpu):
     out = prompt_gauge_poly(torch.from_numpy(depth).to(dev), torch.from_numpy(lidar[:, None]).to(dev),
                             torch.from_numpy(conf[:, None]).to(dev))
     np.testing.assert_allclose(out.cpu().numpy(), og.gauge_poly(depth, lidar, conf), rtol=2e-5, atol=0)
+
+
+def test_gauge_three_frames_degree3_odd_grid(gpu):
+    """B = 3 different scenes, degree 3 (the same six-term basis as 2, v3.py:165-167), a 61 x 83 map over a 29 x 41
+    LiDAR grid (fractional area windows)."""
+    announce("gauge: B=3, degree 3, 61x83 over 29x41")
+    cfg = spec.StepConfig("odd", 61, 83, 70.0, 70.0, 41.0, 30.0, 32, 2, "int8", seed=23)
+    maps = [_scene_maps(cfg, 11 + k, (29, 41)) for k in range(3)]
+    depth = np.concatenate([m[0] for m in maps])
+    lidar = np.concatenate([m[1] for m in maps])
+    conf = np.concatenate([m[2] for m in maps])
+    _check(depth, lidar, conf, degree=3)

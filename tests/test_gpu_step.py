@@ -129,6 +129,35 @@ def test_step_batch_of_distinct_frames(gpu):
     assert np.abs(pts[0, ..., 2] - pts[1, ..., 2]).max() > 0.1  # two different scenes
 
 
+def test_step_odd_sizes(gpu):
+    """A 61 x 83 point map (no dimension a multiple of anything the kernels tile by), B = 3 frames, C = 32, a
+    29 x 41 LiDAR grid (fractional nearest / area windows), output gate and anchor on: every stage against the
+    oracle."""
+    announce("step int8 61x83 B=3 C=32, LiDAR 29x41, gate + anchor")
+    cfg = spec.StepConfig("odd", 61, 83, 70.0, 70.0, 41.0, 30.0, 32, 2, "int8", seed=23)
+    scs = [spec.make_scene(cfg, seed=23 + 5 * k) for k in range(3)]
+    w = spec.refiner_for(cfg, scs[0])
+    iy, ix = (np.arange(29) * cfg.H) // 29, (np.arange(41) * cfg.W) // 41
+    pts = np.stack([sc.points for sc in scs])
+    lid = np.stack([np.ascontiguousarray(sc.lidar[iy][:, ix]) for sc in scs])
+    cnf = np.stack([np.ascontiguousarray(sc.conf[iy][:, ix]) for sc in scs])
+    dev = torch.device("cuda:0")
+    step = RefinerStep(w, 3, cfg.H, cfg.W, dh=29, dw=41, fit_iters=cfg.fit_iters, final_fit=True, output_gate=True,
+                       output_gate_floor=0.2, anchor=0.4)
+    with torch.cuda.stream(torch.cuda.Stream()):
+        P = torch.from_numpy(pts).to(dev)
+        st, fin = step(P, torch.from_numpy(lid).to(dev), torch.from_numpy(cnf).to(dev))
+        step.check()
+        got, st, fin = P.cpu().numpy(), st.cpu().numpy(), fin.cpu().numpy()
+    ref, st_o, fin_o = orf.step(pts, lid, cnf, w, precision="int8", iters=cfg.fit_iters, final_fit=True,
+                                output_gate_on=True, gate_floor=0.2, anchor=0.4)
+    for b in range(3):
+        assert abs(st[b, 0] - st_o[0][b]) <= 1e-5 * abs(st_o[0][b]) and abs(st[b, 1] - st_o[1][b]) <= 1e-5
+        assert abs(fin[b, 0] - fin_o[0][b]) <= 1e-5 * abs(fin_o[0][b]) and abs(fin[b, 1] - fin_o[1][b]) <= 1e-5
+    d, dr = np.exp(got[..., 2].astype(np.float64)), np.exp(ref[..., 2].astype(np.float64))
+    assert (np.abs(d - dr) / dr).max() < 1e-3
+
+
 def test_step_fp16_teacher(gpu):
     announce("step fp16 teacher (small)")
     cfg = spec.StepConfig("t", 120, 160, 130.0, 130.0, 80.0, 60.0, 64, 3, "fp16", seed=13)
