@@ -128,3 +128,19 @@ def test_python_ops_refuse_host_tensors():
 
     with pytest.raises(ValueError, match="GPU tensor"):
         ops.gauge_poly(torch.ones(1, 8, 8), torch.ones(1, 4, 4))
+
+
+def test_header_compiles_as_plain_c(tmp_path):
+    """include/pmg.h is the C ABI a non-Python binding includes: it must compile as C99 with no C++ in it."""
+    import shutil
+    import subprocess
+
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("no C compiler")
+    src = tmp_path / "use_pmg.c"
+    src.write_text('#include "pmg.h"\nint main(void) { return pmg_version() == 0; }\n')
+    inc = Path(__file__).resolve().parents[1] / "include"
+    r = subprocess.run([gcc, "-std=c99", "-Wall", "-Wextra", "-Werror", "-fsyntax-only", f"-I{inc}", str(src)],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
