@@ -235,13 +235,17 @@ int pmg_ln_silu_f16(const float* x, int64_t M, int C, const float* gamma, const 
  * barriers, no host round trip.
  *   z, target: [B][N] fp32; mask: [B][N] uint8 (0/1); st: [B][2] fp32 (s, t) written on device.
  *   info (may be NULL): [B][5] int32 = (count, k, ok, threshold bits of the last trim round, device error flag:
- *   nonzero if a bounded device-wide wait expired, in which case (s, t) are not valid).
+ *   nonzero if a bounded device-wide wait expired -- the grid was not co-resident -- in which case (s, t) = NaN).
  *   workspace: pmg_fit_workspace_bytes(N, iters) bytes, zero-filled before its first use; every call leaves it
- *   ready for the next one (calls that share a workspace must be ordered, e.g. on one stream). After an expired
- *   wait (error flag set) zero-fill it again.
+ *   ready for the next one, also after an expired wait (calls that share a workspace must be ordered, e.g. on one
+ *   stream).
  * N <= 2^21 per batch item.
  * ------------------------------------------------------------------------------------------------------------ */
 size_t pmg_fit_workspace_bytes(int64_t N, int iters);
+/* Test hook (no counterpart in the reference): polls of one device-wide wait before it expires, for the fits
+ * enqueued after the call (0 restores the default, about 0.1 s). Returns the previous value. A tiny limit makes
+ * waits expire with every kernel still running to its end, so tests can exercise the error path. */
+unsigned pmg_debug_fit_spin_limit(unsigned polls);
 int pmg_fit_scale_shift(const float* z, const float* target, const uint8_t* mask, int B, int64_t N, int iters,
                         float trim, int min_points, float* st, int32_t* info, void* workspace,
                         size_t workspace_bytes, void* stream);

@@ -151,8 +151,12 @@ def anchor_pull(logz, d, c, s, t, beta):
 
 def step(points, lidar, conf, w, *, precision="int8", iters=10, trim=0.2, min_points=32, use_prompt=True,
          soft_gate=False, final_fit=False, resolution=256.0, output_gate_on=False, gate_floor=0.1, anchor=0.0,
-         trace: Optional[dict] = None):
-    """Returns (refined points [B, H, W, 3], (s, t) prompt fit, (s, t) final fit or None)."""
+         trace: Optional[dict] = None, st_given=None):
+    """Returns (refined points [B, H, W, 3], (s, t) prompt fit, (s, t) final fit or None).
+
+    st_given = (s [B], t [B]) replaces the prompt fit's result (the fit is then not run): a test that has checked a
+    device's fit against fit_f64 within its tolerance passes the device's (s, t) here, so that everything after the
+    fit is compared on identical inputs, bit for bit."""
     pts = np.array(points, dtype=np.float32, copy=True)
     B, H, W, _ = pts.shape
     M = B * H * W
@@ -160,7 +164,10 @@ def step(points, lidar, conf, w, *, precision="int8", iters=10, trim=0.2, min_po
     res = gate = None
     if use_prompt:
         z, tg, m, d, c = prompt_inputs(pts, lidar, conf)
-        st = fit_f64(z, tg, m, iters, trim, min_points)
+        if st_given is None:
+            st = fit_f64(z, tg, m, iters, trim, min_points)
+        else:
+            st = (np.asarray(st_given[0], np.float32).reshape(B), np.asarray(st_given[1], np.float32).reshape(B))
         r, g = prompt_feats(pts, d, c, st[0], st[1], soft_gate)
         res, gate = r.reshape(-1), g.reshape(-1)
     zq, coords, _, _ = voxelize(pts, resolution)

@@ -82,7 +82,11 @@ struct pmg_refiner {
 
 static size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
+// Destroys the cached graphs. A replay may still be running on the stream it was launched on, so the device is
+// synchronised first (this runs on eviction, new weights and destruction only).
 static void drop_graphs(pmg_refiner* r) {
+    if (r->graphs.empty()) return;
+    (void)hipDeviceSynchronize();
     for (auto& g : r->graphs) {
         hipGraphExecDestroy(g.exec);
         hipGraphDestroy(g.graph);
@@ -343,6 +347,18 @@ pmg_refiner* pmg_refiner_create(const pmg_refiner_config* cfg) {
         set_error("pmg_refiner_create: unsupported configuration");
         return nullptr;
     }
+    // the metric fit holds at most 2^21 elements per batch item: the prompt fit and the anchor's re-fit run on the
+    // H x W map, the final fit on the dh x dw LiDAR grid
+    if ((c.use_prompt || c.anchor > 0.0f) && (int64_t)c.H * c.W > kFitMaxElements) {
+        set_error("pmg_refiner_create: H*W = " + std::to_string((int64_t)c.H * c.W) +
+                  " exceeds the metric fit's 2^21 elements (use_prompt / anchor)");
+        return nullptr;
+    }
+    if (c.final_fit && (int64_t)c.dh * c.dw > kFitMaxElements) {
+        set_error("pmg_refiner_create: dh*dw = " + std::to_string((int64_t)c.dh * c.dw) +
+                  " exceeds the metric fit's 2^21 elements (final_fit)");
+        return nullptr;
+    }
     pmg_refiner* r = new pmg_refiner();
     r->cfg = c;
     r->M = (int64_t)c.B * c.H * c.W;
@@ -437,14 +453,18 @@ int pmg_refiner_forward(pmg_refiner* r, const float* feats, const int32_t* coord
 int pmg_refiner_check(pmg_refiner* r, void* stream) {
     PMG_REQUIRE(r, "null refiner");
     PMG_CHECK_HIP(hipStreamSynchronize((hipStream_t)stream));
-    int err[2] = {0, 0};
+    // each fit launch whose bounded wait expired has already restored its workspace and written NaN (s, t); the
+    // count it left in the workspace is reported once here and cleared
+    unsigned seen[2] = {0, 0};
     for (int k = 0; k < 2; ++k)
-        PMG_CHECK_HIP(hipMemcpy(&err[k], (uint8_t*)r->fit_ws[k] + 64, sizeof(int), hipMemcpyDeviceToHost));
-    if (err[0] || err[1]) {
-        // the fit's barrier state is undefined after an expired wait: start the workspaces over
-        for (int k = 0; k < 2; ++k) PMG_CHECK_HIP(hipMemset(r->fit_ws[k], 0, r->fit_ws_bytes[k]));
+        PMG_CHECK_HIP(hipMemcpy(&seen[k], (uint8_t*)r->fit_ws[k] + kFitErrSeenOffset, sizeof(unsigned),
+                                hipMemcpyDeviceToHost));
+    if (seen[0] || seen[1]) {
+        for (int k = 0; k < 2; ++k)
+            PMG_CHECK_HIP(hipMemset((uint8_t*)r->fit_ws[k] + kFitErrSeenOffset, 0, sizeof(unsigned)));
         PMG_CHECK_HIP(hipDeviceSynchronize());
-        return fail(PMG_E_DEVICE, "pmg_refiner_check: a device-wide wait in the metric fit expired");
+        return fail(PMG_E_DEVICE, "pmg_refiner_check: a device-wide wait in the metric fit expired (" +
+                                      std::to_string(seen[0] + seen[1]) + " launches)");
     }
     return PMG_OK;
 }

@@ -30,7 +30,10 @@
 //
 // Workspace: zero-filled once before its first use; the kernel leaves it reusable (the barrier flags and their
 // epoch only grow, histograms are cleared at the start of every launch, everything else is overwritten before it is
-// read).
+// read). A bounded wait that expires (the grid was not co-resident, e.g. another stream held CUs) sets the launch's
+// error flag; the launch then completes without waiting, the last block to finish reports the flag in info, writes
+// (s, t) = NaN, counts the failure in a sticky word (read by pmg_refiner_check) and returns the barrier state to its
+// initial zeros, so the next launch on the workspace starts clean.
 #include <climits>
 
 #include "pmg_common.h"
@@ -47,7 +50,10 @@ constexpr int kFitBins = 2048;
 constexpr int kCandCap = 32768;                        // candidates every block holds in LDS (128 KiB)
 constexpr uint32_t kInvalid = 0xffffffffu;             // residual key of a padding slot: above every residual
 constexpr int kFitTraceRounds = 64;
-constexpr size_t kFitHeader = 4096;                    // barrier, error flag, trace
+constexpr size_t kFitHeader = 4096;                    // barrier, error flag, trace, completion count
+constexpr size_t kFitErrOffset = 64;                   // the launch's error flag
+constexpr size_t kFitDoneOffset = 3904;                // finished blocks (after the trace, which ends below 3800)
+static_assert(kFitErrSeenOffset == 3968, "pmg_internal.h names the sticky failure count's offset");
 
 struct FitWs {
     unsigned* bar;        // [2]: the synchronisation epoch (the last flag value of the previous launch)
@@ -55,6 +61,8 @@ struct FitWs {
     int* err;
     uint32_t* trace;      // block 0's record: per round the selection path | candidates << 4 and the wall clock
                           // (100 MHz) at its end, per round the threshold bits; launch and first-solve times
+    unsigned* done;       // blocks of the current launch that have finished (the last one resets it to 0)
+    unsigned* err_seen;   // launches whose bounded wait expired since the owner last cleared it (sticky)
     uint64_t* partials;   // [2][kFitMaxBlocks][5] fp64 bit patterns
     unsigned* counts;     // [2][kFitMaxBlocks][2]: below, candidates
     unsigned* hist;       // [iters][3][kFitBins]
@@ -80,6 +88,7 @@ struct FitArgs {
     int b;  // batch item
     float* st;
     int32_t* info;
+    unsigned spin_limit;  // polls of one barrier wait before it gives up
     FitWs ws;
 };
 
@@ -90,7 +99,7 @@ struct FitArgs {
 // waiter; every data buffer exchanged across a barrier is double-buffered, so that block cannot overwrite what the
 // late waiter is about to read. Half the cost of a central arrival counter (no serialised read-modify-write, and
 // every waiter polls one line in parallel with the others).
-__device__ inline void fit_barrier(const FitWs& ws, unsigned nb, unsigned want) {
+__device__ inline void fit_barrier(const FitWs& ws, unsigned nb, unsigned want, unsigned spin_limit) {
     __syncthreads();
     if (threadIdx.x == 0) {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
@@ -101,7 +110,7 @@ __device__ inline void fit_barrier(const FitWs& ws, unsigned nb, unsigned want) 
         while ((int)(__hip_atomic_load(&ws.flags[threadIdx.x * 16], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) -
                      want) < 0) {
             __builtin_amdgcn_s_sleep(1);
-            if (++spins > (1u << 23)) {
+            if (++spins > spin_limit) {
                 __hip_atomic_store(ws.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 break;
             }
@@ -197,6 +206,7 @@ struct FitShared {
     unsigned bin, below;
     unsigned total_below, total_cand;
     uint32_t blo_last, bhi_last;  // bracket of the last stage
+    int last;                     // this block is the launch's last one to finish
 };
 
 // Finds, in a 2048-bin histogram, the bin holding the rank-th element (1-based); sets sh.bin and sh.below (the
@@ -400,7 +410,7 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
         FIT_MARK0(0);
         publish(v, 0u, 0u);
         FIT_MARK0(1);
-        fit_barrier(ws, nb, ++sync_seq);
+        fit_barrier(ws, nb, ++sync_seq, a.spin_limit);
         FIT_MARK0(2);
         double g[5];
         gather_partials(g);
@@ -474,7 +484,7 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
             }
             publish(v, packed_total >> 16, ncb);
             FIT_MARK(1);
-            fit_barrier(ws, nb, ++sync_seq);
+            fit_barrier(ws, nb, ++sync_seq, a.spin_limit);
             FIT_MARK(2);
             load_partials();
             // totals and region offsets, in block order
@@ -483,6 +493,11 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
                 const unsigned* c = ws.counts + ((size_t)(stage & 1) * kFitMaxBlocks + tid) * 2;
                 cb = __hip_atomic_load(&c[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 cc = __hip_atomic_load(&c[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                // a block publishes at most its own element count; the clamp only matters after an expired wait,
+                // when the counts may be another launch's, and keeps every candidate read inside this launch's
+                // regions
+                cb = cb < (unsigned)kFitPerBlock ? cb : (unsigned)kFitPerBlock;
+                cc = cc < (unsigned)kFitPerBlock ? cc : (unsigned)kFitPerBlock;
             }
             unsigned tb, tc;
             const unsigned offc = block_excl_scan2(cc, cb, sh.tmp2, tc, tb);
@@ -661,7 +676,7 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
                     unsigned* gh = ws.hist + ((int64_t)it * 3 + pass) * kFitBins;
                     for (int q = tid; q < kFitBins; q += kFitThreads)
                         if (sh.hist[q]) atomicAdd(&gh[q], sh.hist[q]);
-                    fit_barrier(ws, nb, ++sync_seq);
+                    fit_barrier(ws, nb, ++sync_seq, a.spin_limit);
                     find_bin(sh, rank, [&](int q) {
                         return __hip_atomic_load(&gh[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     });
@@ -697,7 +712,7 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
             unsigned* gh = ws.hist + ((int64_t)it * 3 + 2) * kFitBins;
             for (int q = tid; q < 1024; q += kFitThreads)
                 if (sh.hist[q]) atomicAdd(&gh[q], sh.hist[q]);
-            fit_barrier(ws, nb, ++sync_seq);
+            fit_barrier(ws, nb, ++sync_seq, a.spin_limit);
             find_bin(sh, rank, [&](int q) {
                 return __hip_atomic_load(&gh[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             });
@@ -715,7 +730,7 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
                 }
             }
             publish(v, 0u, 0u);
-            fit_barrier(ws, nb, ++sync_seq);
+            fit_barrier(ws, nb, ++sync_seq, a.spin_limit);
             double g[5];
             gather_partials(g);
             ++stage;
@@ -754,10 +769,39 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
         __hip_atomic_store(&ws.bar[2], sync_seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         a.st[2 * a.b] = s;
         a.st[2 * a.b + 1] = t;
-        if (a.info) {
-            a.info[5 * a.b + 3] = (int32_t)thr;
-            a.info[5 * a.b + 4] = __hip_atomic_load(ws.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (a.info) a.info[5 * a.b + 3] = (int32_t)thr;
+    }
+
+    // Completion. The last block to finish sees every block's writes; it reports the launch's error flag. After
+    // an expired wait the blocks may have passed different numbers of barriers, so their flags and the epoch no
+    // longer agree: it zeroes all of them (every flag line, not only this grid's, since the epoch restarts at 0),
+    // clears the flag, counts the failure and replaces (s, t), which raced, by NaN.
+    __syncthreads();
+    if (tid == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        const unsigned prev = __hip_atomic_fetch_add(ws.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        sh.last = prev == (unsigned)nb - 1u;
+        if (sh.last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    }
+    __syncthreads();
+    if (!sh.last) return;
+    const int err = __hip_atomic_load(ws.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (err) {
+        for (int q = tid; q < kFitMaxBlocks * 16; q += kFitThreads)
+            __hip_atomic_store(&ws.flags[q], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (tid == 0) {
+        if (err) {
+            const float nan = __builtin_nanf("");
+            a.st[2 * a.b] = nan;
+            a.st[2 * a.b + 1] = nan;
+            __hip_atomic_store(&ws.bar[2], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(ws.err, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_add(ws.err_seen, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
+        if (a.info) a.info[5 * a.b + 4] = err;
+        __hip_atomic_store(ws.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -780,6 +824,10 @@ size_t fit_workspace_bytes(int64_t N, int iters) {
            align256(2 * kFitMaxBlocks * 2 * sizeof(unsigned)) +
            align256(hist) + 3 * align256(cand);
 }
+
+// Polls of one barrier wait before it expires (~0.1 s at the default); lowered only by the test hook
+// pmg_debug_fit_spin_limit, so that tests can make waits expire with every kernel still exiting normally.
+static unsigned g_fit_spin_limit = 1u << 23;
 
 int launch_fit(const FitLaunch& f, hipStream_t s) {
     PMG_REQUIRE(f.N > 0 && f.N <= (int64_t)kFitMaxBlocks * kFitPerBlockMax, "N must be in [1, 2^21]");
@@ -807,8 +855,10 @@ int launch_fit(const FitLaunch& f, hipStream_t s) {
     uint8_t* p = (uint8_t*)f.workspace;
     FitWs ws;
     ws.bar = (unsigned*)p;
-    ws.err = (int*)(p + 64);
+    ws.err = (int*)(p + kFitErrOffset);
     ws.trace = (uint32_t*)(p + 128);
+    ws.done = (unsigned*)(p + kFitDoneOffset);
+    ws.err_seen = (unsigned*)(p + kFitErrSeenOffset);
     p += kFitHeader;
     ws.flags = (unsigned*)p;
     p += align256(kFitMaxBlocks * 64);
@@ -824,7 +874,8 @@ int launch_fit(const FitLaunch& f, hipStream_t s) {
     ws.c_t = (float*)(p + 2 * cand);
     for (int b = 0; b < f.B; ++b) {
         FitArgs a{f.mode, f.z, f.tg, f.mask, f.logz, f.stride, f.lidar, f.conf, f.H, f.W, f.dh, f.dw,
-                  f.N, f.iters, (float)(1.0 - (double)f.trim), f.min_points, b, f.st, f.info, ws};
+                  f.N, f.iters, (float)(1.0 - (double)f.trim), f.min_points, b, f.st, f.info,
+                  g_fit_spin_limit, ws};
         if (ept == 16)
             hipLaunchKernelGGL(fit_k<16>, dim3(nb), dim3(kFitThreads), 0, s, a);
         else
@@ -912,6 +963,12 @@ using namespace pmg;
 extern "C" {
 
 size_t pmg_fit_workspace_bytes(int64_t N, int iters) { return fit_workspace_bytes(N, iters); }
+
+unsigned pmg_debug_fit_spin_limit(unsigned polls) {
+    const unsigned prev = g_fit_spin_limit;
+    g_fit_spin_limit = polls ? polls : (1u << 23);
+    return prev;
+}
 
 size_t pmg_fit_final_workspace_bytes(int B, int dh, int dw, int iters) {
     if (B < 1 || dh < 1 || dw < 1) return 0;

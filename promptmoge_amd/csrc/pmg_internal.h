@@ -57,6 +57,10 @@ struct FitLaunch {
 };
 size_t fit_workspace_bytes(int64_t N, int iters);
 int launch_fit(const FitLaunch& f, hipStream_t s);
+// Byte offset, in a fit workspace, of the count of launches whose bounded wait expired (sticky until cleared).
+constexpr size_t kFitErrSeenOffset = 3968;
+// Elements per batch item the fit holds (256 blocks x 8192).
+constexpr int64_t kFitMaxElements = (int64_t)1 << 21;
 
 // The final metric fit at LiDAR resolution (v3.py:768-778): area-pooled depth, LiDAR mask, then the fit. The
 // workspace starts with the fit's own (error flag at byte 64), followed by the pooled depth and mask.

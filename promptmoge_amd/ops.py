@@ -349,7 +349,9 @@ def fit_scale_shift(z: torch.Tensor, target: torch.Tensor, mask: torch.Tensor, i
                     min_points: int = 32, differentiable: bool = False, *, return_info: bool = False):
     """fit_scale_shift (prompt_stem.py:211-240) on the GPU, same arguments: z, target, mask [B, ...] (flattened
     from dim 1). Returns s, t: [B] fp32 (and, with return_info, info [B, 5] int32 = count, k, ok, threshold bits,
-    error flag). The result carries no gradient; `differentiable=True` under grad mode is refused."""
+    error flag). A batch item whose device-wide wait expired (the grid could not run co-resident) gets s = t = NaN
+    and error flag 1; the workspace is ready for the next call either way. The result carries no gradient;
+    `differentiable=True` under grad mode is refused."""
     if differentiable and torch.is_grad_enabled() and z.requires_grad:
         raise NotImplementedError("the GPU metric fit is inference-only (differentiable=True needs autograd)")
     z = _dev(z.float().reshape(z.shape[0], -1).contiguous(), "z")

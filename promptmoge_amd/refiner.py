@@ -180,6 +180,7 @@ class FusedRefiner(torch.nn.Module):
         self.check_coords = check_coords
         self._weights = {}   # device -> DeviceWeights
         self._ctx = {}       # (device, B, H, W) -> refiner handle
+        self._io = {}        # (device, B, H, W) -> persistent input / output buffers of that context
 
     def _handle(self, device: torch.device, B: int, H: int, W: int):
         key = (device.index, B, H, W)
@@ -197,6 +198,14 @@ class FusedRefiner(torch.nn.Module):
                 raise _lib.PmgError(_lib.PMG_E_INVALID, lib().pmg_last_error().decode())
             call("pmg_refiner_set_weights", h, C.byref(dw.struct))
             self._ctx[key] = h
+            M = B * H * W
+            dev = torch.device("cuda", device.index)
+            self._io[key] = {
+                "feats": torch.empty((M, 3), dtype=torch.float32, device=dev),
+                "coords": torch.empty((M, 4), dtype=torch.int32, device=dev),
+                "prompt": torch.empty((M, 2), dtype=torch.float32, device=dev),
+                "out": torch.empty((M,), dtype=torch.float32, device=dev),
+            }
         return h
 
     def forward(self, feats: torch.Tensor, coords: Optional[torch.Tensor], shape, encoder_feature=None,
@@ -218,17 +227,26 @@ class FusedRefiner(torch.nn.Module):
             prompt_feats = prompt_feats.float().contiguous()
             if prompt_feats.shape != (M, 2):
                 raise ValueError("prompt_feats must be (M, 2)")
-        out = torch.empty((M, 1), dtype=torch.float32, device=feats.device)
         h = self._handle(feats.device, B, H, W)
-        p = lambda t: None if t is None else t.data_ptr()
-        call("pmg_refiner_forward", h, feats.data_ptr(), p(coords), p(prompt_feats), out.data_ptr(),
+        # The context replays one captured graph per (buffers, stream). The inputs are staged into the context's
+        # persistent buffers (a few MB of device copies on the same stream), so every call replays the same graph
+        # instead of capturing a new one for each fresh tensor; the result is copied out, so the caller owns it.
+        io = self._io[(feats.device.index, B, H, W)]
+        io["feats"].copy_(feats)
+        if coords is not None:
+            io["coords"].copy_(coords)
+        if prompt_feats is not None:
+            io["prompt"].copy_(prompt_feats)
+        call("pmg_refiner_forward", h, io["feats"].data_ptr(), io["coords"].data_ptr() if coords is not None else None,
+             io["prompt"].data_ptr() if prompt_feats is not None else None, io["out"].data_ptr(),
              C.c_void_p(torch.cuda.current_stream().cuda_stream))
-        return out
+        return io["out"].clone().view(M, 1)
 
     def close(self) -> None:
         for h in self._ctx.values():
             lib().pmg_refiner_destroy(h)
         self._ctx.clear()
+        self._io.clear()
 
     def __del__(self):
         try:

@@ -144,3 +144,27 @@ def test_header_compiles_as_plain_c(tmp_path):
     r = subprocess.run([gcc, "-std=c99", "-Wall", "-Wextra", "-Werror", "-fsyntax-only", f"-I{inc}", str(src)],
                        capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
+
+
+def test_refiner_create_rejects_maps_beyond_the_fit(libpmg):
+    """The metric fit holds 2^21 elements per batch item: a prompt fit (or anchor re-fit) over a larger H x W map,
+    or a final fit over a larger LiDAR grid, is refused when the context is created, not at every step."""
+    big = (1 << 21) + 2048  # 1025 x 2048 pixels
+    # (B, H, W, C, n_blocks, prec, res, dh, dw, iters, trim, min_points, use_prompt, soft, final_fit, graph)
+    cfg = _lib.RefinerConfig(1, 1025, 2048, 32, 1, 0, 256.0, 8, 8, 4, 0.2, 32, 1, 0, 0, 1)
+    assert big == 1025 * 2048
+    assert not libpmg.pmg_refiner_create(C.byref(cfg))
+    assert b"exceeds the metric fit" in libpmg.pmg_last_error() and b"use_prompt" in libpmg.pmg_last_error()
+    cfg = _lib.RefinerConfig(1, 1025, 2048, 32, 1, 0, 256.0, 8, 8, 4, 0.2, 32, 0, 0, 0, 1, 0, 0.1, 0.5)
+    assert not libpmg.pmg_refiner_create(C.byref(cfg))
+    assert b"anchor" in libpmg.pmg_last_error()
+    cfg = _lib.RefinerConfig(1, 64, 64, 32, 1, 0, 256.0, 1025, 2048, 4, 0.2, 32, 0, 0, 1, 1)
+    assert not libpmg.pmg_refiner_create(C.byref(cfg))
+    assert b"final_fit" in libpmg.pmg_last_error()
+
+
+def test_fit_spin_limit_hook_round_trips(libpmg):
+    prev = libpmg.pmg_debug_fit_spin_limit(7)
+    assert prev == 1 << 23
+    assert libpmg.pmg_debug_fit_spin_limit(0) == 7
+    assert libpmg.pmg_debug_fit_spin_limit(0) == 1 << 23

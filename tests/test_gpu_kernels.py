@@ -425,6 +425,36 @@ def test_fit_edge_cases(gpu):
         _close_st(s[b], tt[b], so[b], to[b])
 
 
+def test_fit_expired_wait_is_reported_and_does_not_leak(gpu, libpmg):
+    """A device-wide wait that expires -- forced from the host with a one-poll spin limit, so every kernel still runs
+    to its end -- is reported in info[:, 4] with (s, t) = NaN for that batch item, and does not leak: the next call
+    on the same workspace is exact again (the last block restores the barrier state)."""
+    announce("fit expired wait, then a clean call on the same workspace")
+    rng = np.random.default_rng(5)
+    B, N = 2, 300_000  # 74 blocks per item
+    z = rng.uniform(0.5, 6, size=(B, N)).astype(np.float32)
+    t = (1.3 * z + 0.05 + rng.normal(0, 0.01, size=(B, N))).astype(np.float32)
+    m = rng.random((B, N)) < 0.7
+    args = (_t(z, gpu), _t(t, gpu), _t(m, gpu))
+    s0, t0, i0 = (a.cpu().numpy() for a in ops.fit_scale_shift(*args, iters=10, return_info=True))
+    prev = libpmg.pmg_debug_fit_spin_limit(1)
+    try:
+        s1, t1, i1 = ops.fit_scale_shift(*args, iters=10, return_info=True)
+        torch.cuda.synchronize()
+    finally:
+        libpmg.pmg_debug_fit_spin_limit(prev)
+    s1, t1, i1 = s1.cpu().numpy(), t1.cpu().numpy(), i1.cpu().numpy()
+    assert i1[:, 4].any(), "one poll per wait: some wait must expire"
+    for b in range(B):
+        if i1[b, 4]:
+            assert np.isnan(s1[b]) and np.isnan(t1[b])
+        else:
+            assert s1[b] == s0[b] and t1[b] == t0[b]
+    s2, t2, i2 = (a.cpu().numpy() for a in ops.fit_scale_shift(*args, iters=10, return_info=True))
+    assert (i2[:, 4] == 0).all() and (i0[:, 4] == 0).all()
+    assert np.array_equal(s2, s0) and np.array_equal(t2, t0)
+
+
 @pytest.mark.parametrize("name", ["B", "A", "H"])
 def test_fit_prompt_scene(gpu, name):
     announce(f"fit prompt scene={name}")
