@@ -455,13 +455,16 @@ int pmg_refiner_check(pmg_refiner* r, void* stream) {
     PMG_CHECK_HIP(hipStreamSynchronize((hipStream_t)stream));
     // each fit launch whose bounded wait expired has already restored its workspace and written NaN (s, t); the
     // count it left in the workspace is reported once here and cleared
+    // (a context without a final fit holds only a stub there)
     unsigned seen[2] = {0, 0};
+    const bool has[2] = {r->fit_ws_bytes[0] > kFitErrSeenOffset, r->fit_ws_bytes[1] > kFitErrSeenOffset};
     for (int k = 0; k < 2; ++k)
-        PMG_CHECK_HIP(hipMemcpy(&seen[k], (uint8_t*)r->fit_ws[k] + kFitErrSeenOffset, sizeof(unsigned),
-                                hipMemcpyDeviceToHost));
+        if (has[k])
+            PMG_CHECK_HIP(hipMemcpy(&seen[k], (uint8_t*)r->fit_ws[k] + kFitErrSeenOffset, sizeof(unsigned),
+                                    hipMemcpyDeviceToHost));
     if (seen[0] || seen[1]) {
         for (int k = 0; k < 2; ++k)
-            PMG_CHECK_HIP(hipMemset((uint8_t*)r->fit_ws[k] + kFitErrSeenOffset, 0, sizeof(unsigned)));
+            if (has[k]) PMG_CHECK_HIP(hipMemset((uint8_t*)r->fit_ws[k] + kFitErrSeenOffset, 0, sizeof(unsigned)));
         PMG_CHECK_HIP(hipDeviceSynchronize());
         return fail(PMG_E_DEVICE, "pmg_refiner_check: a device-wide wait in the metric fit expired (" +
                                       std::to_string(seen[0] + seen[1]) + " launches)");
