@@ -242,6 +242,14 @@ int pmg_ln_silu_f16(const float* x, int64_t M, int C, const float* gamma, const 
  * N <= 2^21 per batch item.
  * ------------------------------------------------------------------------------------------------------------ */
 size_t pmg_fit_workspace_bytes(int64_t N, int iters);
+/* pmg_fit_scale_shift_static -- pmg_fit_scale_shift without a workspace argument and without allocating. It has
+ * no counterpart in the reference: it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops, harnesses that forbid hipMalloc). The workspace is a static 14 MiB device array that each
+ * GPU the library runs on holds until the process ends; it limits N to 2^19 per batch item and iters to 16 (larger
+ * sizes are refused with PMG_E_INVALID). Results are those of pmg_fit_scale_shift bit for bit. Every call on a GPU
+ * shares that GPU's array: calls that overlap on one GPU (other streams, other threads) race; order them. */
+int pmg_fit_scale_shift_static(const float* z, const float* target, const uint8_t* mask, int B, int64_t N, int iters,
+                               float trim, int min_points, float* st, int32_t* info, void* stream);
 /* Test hook (no counterpart in the reference): polls of one device-wide wait before it expires, for the fits
  * enqueued after the call (0 restores the default, about 0.1 s). Returns the previous value. A tiny limit makes
  * waits expire with every kernel still running to its end, so tests can exercise the error path. */

@@ -35,6 +35,7 @@
 // (s, t) = NaN, counts the failure in a sticky word (read by pmg_refiner_check) and returns the barrier state to its
 // initial zeros, so the next launch on the workspace starts clean.
 #include <climits>
+#include <mutex>
 
 #include "pmg_common.h"
 #include "pmg_internal.h"
@@ -956,6 +957,43 @@ int launch_final_fit(const FinalFit& f, hipStream_t s) {
     return launch_fit(g, s);
 }
 
+// ------------------------------------------------------------------------------------------------------------
+// Allocation-free fit: the workspace is a file-scope device array, one copy per GPU, instead of caller memory.
+// 14 MiB holds the workspace of N <= 2^19 elements per batch item at iters <= 16 (13.0 MB). Host code never uses
+// the array's name as an address: at a device's first call its address is looked up with hipGetSymbolAddress
+// (the device current), kept per device, and only that pointer reaches kernels.
+constexpr size_t kStaticFitBytes = (size_t)14 << 20;
+constexpr int kStaticFitMaxDevices = 64;
+static __device__ __align__(256) uint8_t scratch[kStaticFitBytes];
+
+__global__ void zero_words_k(uint32_t* p, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+static std::mutex g_static_fit_mu;
+static void* g_static_fit_ptr[kStaticFitMaxDevices];
+
+// The current device's scratch address. At the device's first call it also enqueues, on `s`, the clearing of the
+// part of the workspace the fit requires at zero before its first launch (the barrier epoch, error flag, completion
+// count and per-block flags; the rest is cleared or overwritten by every launch).
+static int static_fit_scratch(hipStream_t s, void** out) {
+    int dev = -1;
+    PMG_CHECK_HIP(hipGetDevice(&dev));
+    PMG_REQUIRE(dev >= 0 && dev < kStaticFitMaxDevices, "device index out of range for the static fit scratch");
+    std::lock_guard<std::mutex> lock(g_static_fit_mu);
+    if (!g_static_fit_ptr[dev]) {
+        void* p = nullptr;
+        PMG_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        const int64_t words = (int64_t)(kFitHeader + align256((size_t)kFitMaxBlocks * 64)) / 4;
+        hipLaunchKernelGGL(zero_words_k, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, s, (uint32_t*)p, words);
+        if (int e = check_launch("zero_words_k")) return e;
+        g_static_fit_ptr[dev] = p;
+    }
+    *out = g_static_fit_ptr[dev];
+    return PMG_OK;
+}
+
 }  // namespace pmg
 
 using namespace pmg;
@@ -963,6 +1001,35 @@ using namespace pmg;
 extern "C" {
 
 size_t pmg_fit_workspace_bytes(int64_t N, int iters) { return fit_workspace_bytes(N, iters); }
+
+int pmg_fit_scale_shift_static(const float* z, const float* target, const uint8_t* mask, int B, int64_t N, int iters,
+                               float trim, int min_points, float* st, int32_t* info, void* stream) {
+    PMG_REQUIRE(z && target && mask && st, "null buffer");
+    PMG_REQUIRE(B >= 1, "bad batch");
+    PMG_REQUIRE(N > 0 && N <= ((int64_t)1 << 19) && iters >= 0 && iters <= 16,
+                "pmg_fit_scale_shift_static: N = " + std::to_string(N) + ", iters = " + std::to_string(iters) +
+                    " exceed the static scratch (N <= 2^19 per batch item, iters <= 16); use pmg_fit_scale_shift "
+                    "with a caller workspace");
+    PMG_REQUIRE(fit_workspace_bytes(N, iters) <= kStaticFitBytes, "static fit scratch too small");
+    hipStream_t s = (hipStream_t)stream;
+    void* ws = nullptr;
+    if (int e = static_fit_scratch(s, &ws)) return e;
+    FitLaunch f{};
+    f.mode = 0;
+    f.z = z;
+    f.tg = target;
+    f.mask = mask;
+    f.B = B;
+    f.N = N;
+    f.iters = iters;
+    f.trim = trim;
+    f.min_points = min_points;
+    f.st = st;
+    f.info = info;
+    f.workspace = ws;
+    f.workspace_bytes = kStaticFitBytes;
+    return launch_fit(f, s);
+}
 
 unsigned pmg_debug_fit_spin_limit(unsigned polls) {
     const unsigned prev = g_fit_spin_limit;
