@@ -17,10 +17,15 @@ Modules
   pool       build_pool_cache / sparse_pool / sparse_upsample (_core.py:339-505): perfect-partition pooling with
              sorted unique output keys, mean/sum in input order, nearest upsampling by parent
   gauge      prompt_gauge_poly (v3.py:151-183): pooled inputs, IRLS with the lower median, exp(poly) correction
+  blocks     the int8 contract (qat.py:28-57, Refiner.swift:147-148), the residual block (flex_sparse_blocks.py:70-75)
+             and linear layers in three arithmetics: the reference's fp32, its QAT fake-quant, the deployed int8
   refiner    the fused step (v3.py:346-383, 547-576; sparse_unet.py:176-258 single level; flex_sparse_blocks.py:70-75)
              in the deployed int8 / fp16 arithmetic, and the reference's fp32 fake-quant (QAT) formulation; the refine
              loop's output gate and elastic anchor (v3.py:565-573)
+  unet       the multi-level Sparse3DUNet (sparse_unet.py:176-258; PoolDown / NearestUp, flex_sparse_blocks.py:78-105):
+             level structure, encoder conditioning, fuse_proj, per-level stages, in the three arithmetics
 
 What pins each function (golden vectors, closed forms, brute force, invariants) is listed in tests/test_oracle*.py.
-The reference ships no golden vectors or tests for this path.
+The reference ships no golden vectors or tests for this path; tests/golden/refiner_vectors.npz holds vectors its own
+modules produced (tests/golden/make_refiner_vectors.py), for the composition nothing else pins.
 """

@@ -23,31 +23,12 @@ from typing import Optional
 
 import numpy as np
 
-from .conv import conv_acc_int, conv_float, epilogue_q, epilogue_r
+from .blocks import (act_mult, act_scale, fake_quant, input_proj, layer_norm, out_proj, quantize_weight,
+                     resblock, silu)
+from .conv import conv_float
 from .fit import final_inputs, fit_f64, prompt_inputs
-from .numerics import F32, ln_silu, log_f32, quad_sum, quant_i8
+from .numerics import F32, ln_silu, log_f32
 from .structure import nmap_column, voxelize
-
-
-def quantize_weight(w: np.ndarray):
-    """WeightFakeQuant (qat.py:52-57) with _fake_quant (qat.py:35-36): s = max|W[co]| / 127 in fp32, clamped at
-    1e-12, q = clamp(round(W / s), -127, 127)."""
-    w = np.asarray(w, dtype=np.float32)
-    s = (np.abs(w).reshape(w.shape[0], -1).max(axis=1) / F32(127.0)).astype(np.float32)
-    s = np.maximum(s, F32(1e-12))
-    q = np.clip(np.rint(w / s.reshape((-1,) + (1,) * (w.ndim - 1))), -127, 127)
-    return q.astype(np.int8), s
-
-
-def act_scale(clip: float) -> np.float32:
-    """ActFakeQuant scale clip / QMAX in fp32, clamped at 1e-12 (qat.py:35, 98); the deployed dequantisation scale
-    aScale = clip / 127 (Refiner.swift:147)."""
-    return np.maximum(F32(clip) / F32(127.0), F32(1e-12))
-
-
-def act_mult(clip: float) -> np.float32:
-    """The deployed requantisation multiplier 127 / clip in fp32 (Refiner.swift:148)."""
-    return F32(127.0) / F32(clip)
 
 
 def prompt_feats(points, d, c, s, t, soft_gate=False):
@@ -66,39 +47,11 @@ def prompt_feats(points, d, c, s, t, soft_gate=False):
     return res.astype(np.float32), gate.astype(np.float32)
 
 
-def input_proj(f: np.ndarray, w, res=None, gate=None) -> np.ndarray:
-    """input_proj (+ prompt_proj), in the kernel's order: ((b + w0 f0) + w1 f1) + w2 f2 (+ ((pb + p0 r) + p1 g))."""
-    in_w, in_b = np.asarray(w.in_w, np.float32), np.asarray(w.in_b, np.float32)
-    y = in_b[None, :] + in_w[None, :, 0] * f[:, 0:1]
-    y = y + in_w[None, :, 1] * f[:, 1:2]
-    y = y + in_w[None, :, 2] * f[:, 2:3]
-    if res is not None:
-        pr_w, pr_b = np.asarray(w.pr_w, np.float32), np.asarray(w.pr_b, np.float32)
-        pp = pr_b[None, :] + pr_w[None, :, 0] * res[:, None]
-        pp = pp + pr_w[None, :, 1] * gate[:, None]
-        y = y + pp
-    return y.astype(np.float32)
-
-
-def out_proj(x: np.ndarray, w) -> np.ndarray:
-    """out_proj (C -> 1): bias + the quad-order sum of out_w * x (the PMG_EPI_ROUT epilogue)."""
-    ow = np.asarray(w.out_w, np.float32).reshape(1, -1)
-    return np.float32(w.out_b[0]) + quad_sum(ow * x.astype(np.float32))
-
-
 def blocks_int8(x, nmap, w, trace=None):
+    """The residual blocks in the deployed int8 arithmetic (blocks.resblock); trace receives each block's q1, acc1,
+    q2, acc2 and output x."""
     for blk in w.blocks:
-        q_w1, s_w1 = quantize_weight(blk.w1)
-        q_w2, s_w2 = quantize_weight(blk.w2)
-        a1, a2 = act_scale(blk.clip1), act_scale(blk.clip2)
-        m1, m2 = act_mult(blk.clip1), act_mult(blk.clip2)
-        q1 = quant_i8(ln_silu(x, blk.gamma, blk.beta), m1)
-        acc1 = conv_acc_int(q1, nmap, q_w1)
-        q2 = epilogue_q(acc1, a1, s_w1, blk.b1, m2)
-        acc2 = conv_acc_int(q2, nmap, q_w2)
-        x = epilogue_r(acc2, a2, s_w2, blk.b2, x)
-        if trace is not None:
-            trace.append(dict(q1=q1, acc1=acc1, q2=q2, acc2=acc2, x=x))
+        x = resblock(x, nmap, blk, "int8", trace)
     return x
 
 
@@ -196,33 +149,10 @@ def step(points, lidar, conf, w, *, precision="int8", iters=10, trim=0.2, min_po
 
 
 # ------------------------------------------------------------------------------------------------------------------
-def _ln_ref(x, gamma, beta, eps=1e-6):
-    mu = x.mean(axis=1, keepdims=True, dtype=np.float32)
-    var = ((x - mu) ** 2).mean(axis=1, keepdims=True, dtype=np.float32)
-    return ((x - mu) / np.sqrt(var + np.float32(eps)) * gamma + beta).astype(np.float32)
-
-
-def _silu_ref(x):
-    return (x / (np.float32(1.0) + np.exp(-x))).astype(np.float32)
-
-
-def _fake_quant(x, s):
-    """_fake_quant forward value (qat.py:35-36): clamp(round(x / s), -127, 127) * s."""
-    s = np.float32(s)
-    return (np.clip(np.rint(x.astype(np.float32) / s), -127, 127) * s).astype(np.float32)
-
-
 def blocks_fakequant(x, nmap, w):
     """The reference's fp32 formulation: _fallback conv on fake-quantised operands (qat.py:101-111, 52-57)."""
     for blk in w.blocks:
-        q_w1, s_w1 = quantize_weight(blk.w1)
-        q_w2, s_w2 = quantize_weight(blk.w2)
-        w1 = (q_w1.astype(np.float32) * s_w1.reshape(-1, 1, 1, 1, 1)).astype(np.float32)
-        w2 = (q_w2.astype(np.float32) * s_w2.reshape(-1, 1, 1, 1, 1)).astype(np.float32)
-        h = _fake_quant(_silu_ref(_ln_ref(x, blk.gamma, blk.beta)), act_scale(blk.clip1))
-        h = _silu_ref(conv_float(h, nmap, w1, blk.b1))
-        h = _fake_quant(h, act_scale(blk.clip2))
-        x = conv_float(h, nmap, w2, blk.b2) + x
+        x = resblock(x, nmap, blk, "fakequant")
     return x
 
 

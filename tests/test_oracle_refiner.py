@@ -15,6 +15,7 @@ import numpy as np
 import pytest
 
 from oracle import refiner as rf
+from oracle.blocks import resblock
 from promptmoge_amd import spec
 
 
@@ -49,10 +50,8 @@ def test_fp16_step_matches_fp32_reference():
     zq, _, _, _ = rf.voxelize(sc.points[None])
     nm = rf.nmap_column(zq)
     x = rf.input_proj(sc.points.reshape(-1, 3), w32, r.reshape(-1), g.reshape(-1))
-    for blk in w32.blocks:
-        h = rf._silu_ref(rf._ln_ref(x, blk.gamma, blk.beta))
-        h = rf._silu_ref(rf.conv_float(h, nm, blk.w1, blk.b1))
-        x = rf.conv_float(h, nm, blk.w2, blk.b2) + x
+    for blk in w32.blocks:  # the fp32 block, pinned against the reference's SparseResBlock3d (test_oracle_unet.py)
+        x = resblock(x, nm, blk, "fp32")
     ref = sc.points[..., 2] + (x @ w32.out_w.reshape(-1) + w32.out_b[0]).reshape(H, W)
     rel = np.abs(np.exp(pts[0, ..., 2].astype(np.float64)) - np.exp(ref.astype(np.float64))) / np.exp(ref)
     assert rel.max() < 1e-3, rel.max()
@@ -133,3 +132,92 @@ def test_anchor_pull_limits():
     # half strength: half-way between logz and the target
     half = rf.anchor_pull(logz, d, c, s, t, 0.5)
     np.testing.assert_allclose(half, 0.5 * (logz + want), rtol=0, atol=2e-6)
+
+
+# ------------------------------------------------------------------------------------------------ closed forms
+def _level0(C=16, seed=5, n_blocks=2):
+    cfg = spec.StepConfig("c", 24, 32, 30.0, 30.0, 16.0, 12.0, C, n_blocks, "int8", seed=seed)
+    sc = spec.make_scene(cfg)
+    w = spec.calibrate(spec.make_weights(C, n_blocks, seed=seed), sc, crop=32)
+    zq, _, _, _ = rf.voxelize(sc.points[None])
+    rng = np.random.default_rng(seed)
+    M = cfg.H * cfg.W
+    pf = np.stack([rng.normal(0, 0.05, M), rng.uniform(0, 1, M)], 1).astype(np.float32)
+    return cfg, sc, w, zq, pf
+
+
+def test_zero_conv2_blocks_are_the_identity():
+    """Every conv2 weight and bias zero: each SparseResBlock3d returns its input (skip only, flex_sparse_blocks.py:
+    75), so the module is out_proj(input_proj(f) + prompt_proj(pf)) (sparse_unet.py:189-192, 258), here checked
+    against an independent float64 evaluation."""
+    cfg, sc, w, zq, pf = _level0()
+    w0 = dataclasses.replace(w, blocks=[dataclasses.replace(b, w2=np.zeros_like(b.w2), b2=np.zeros_like(b.b2))
+                                        for b in w.blocks])
+    f = sc.points.reshape(-1, 3)
+    got = rf.forward(f, zq, cfg.H, cfg.W, w0, pf, precision="int8")
+    f64 = lambda a: np.asarray(a, np.float64)
+    x = f @ f64(w.in_w).T + f64(w.in_b) + pf @ f64(w.pr_w).T + f64(w.pr_b)
+    ref = x @ f64(w.out_w).reshape(-1) + f64(w.out_b)[0]
+    assert np.abs(got - ref).max() <= 1e-5 * np.abs(ref).max()
+    # and the blocks do act when conv2 is not zero
+    assert np.abs(rf.forward(f, zq, cfg.H, cfg.W, w, pf, precision="int8") - ref).max() > 1e-3
+
+
+def test_constant_layernorm_and_centre_tap_conv1():
+    """gamma = 0, beta = b: LayerNorm returns b in every row, so conv1's input codes are quant(silu(b), 127/clip1)
+    in every row; with only the centre tap of conv1 non-zero (v = 13, the voxel itself, present in every row),
+    acc1[m, n] = sum_c W[n, 13, c] * q[c] for every m."""
+    cfg, sc, w, zq, pf = _level0(n_blocks=1)
+    b = w.blocks[0]
+    rng = np.random.default_rng(7)
+    beta = rng.normal(0, 1.0, b.beta.shape).astype(np.float32)
+    w1 = np.zeros_like(b.w1)
+    w1[:, 1, 1, 1, :] = rng.normal(0, 0.05, (b.w1.shape[0], b.w1.shape[-1]))
+    wc = dataclasses.replace(w, blocks=[dataclasses.replace(b, gamma=np.zeros_like(b.gamma), beta=beta, w1=w1)])
+    trace = {}
+    rf.step(sc.points[None], sc.lidar[None], sc.conf[None], wc, precision="int8", iters=4, trace=trace)
+    blk = trace["blocks"][0]
+    from oracle.numerics import silu_f32
+    codes = np.clip(np.rint(silu_f32(beta) * (np.float32(127) / np.float32(b.clip1))), -127, 127).astype(np.int64)
+    assert (blk["q1"] == codes[None, :]).all()
+    q, _ = rf.quantize_weight(w1)
+    expect = q.reshape(q.shape[0], 27, -1)[:, 13, :].astype(np.int64) @ codes
+    assert (blk["acc1"] == expect[None, :]).all()
+
+
+def test_prompt_features_hand_built():
+    """_lidar_in_affine_frame's residual and gate (v3.py:371-383) and the channel order [residual, gate]
+    (v3.py:552-554) on hand-built pixels, (s, t) = (2, 0.5): d_aff = (d - t) / max(s, 1e-6)."""
+    logz = np.array([[0.3, -0.2, 0.1, 0.7, 0.05, 1.1]], np.float32)
+    pts = np.zeros((1, 1, 6, 3), np.float32)
+    pts[..., 2] = logz
+    d = np.array([[[2.5, 0.5 + 2e-5, 0.0, np.nan, 4.5, 2.5]]], np.float32)   # d_aff 1, 1e-5, -, -, 2, 1
+    c = np.array([[[1.0, 1.0, 1.0, 1.0, 0.5, 0.0]]], np.float32)
+    res, gate = rf.prompt_feats(pts, d, c, [2.0], [0.5])
+    ok = np.array([1, 0, 0, 0, 1, 1], bool)
+    lda = np.where(ok, np.log(np.maximum(np.where(ok, (d[0, 0] - 0.5) / 2.0, 1.0), 1e-4)), logz[0])
+    g = c[0, 0] * ok
+    np.testing.assert_allclose(gate[0, 0], g, rtol=0, atol=0)
+    np.testing.assert_allclose(res[0, 0], (lda - logz[0]) * g, rtol=1e-6, atol=1e-7)
+    assert res[0, 0, 1] == 0 and res[0, 0, 2] == 0 and res[0, 0, 3] == 0      # d_aff <= 1e-4, d = 0, d = NaN
+    assert res[0, 0, 5] == 0 and gate[0, 0, 5] == 0                          # conf 0: no gate
+    _, soft = rf.prompt_feats(pts, d, c, [2.0], [0.5], soft_gate=True)
+    np.testing.assert_allclose(soft[0, 0], (np.float32(0.15) + np.float32(0.85) * c[0, 0]) * ok, rtol=0, atol=0)
+    # a vanishing scale is clamped at 1e-6 (v3.py:375): d_aff = (2.5 - 0.5) / 1e-6
+    r2, _ = rf.prompt_feats(pts, d, c, [1e-9], [0.5])
+    assert abs(r2[0, 0, 0] - (np.log(2.0 / 1e-6) - 0.3)) < 1e-4
+    # the step feeds [residual, gate] to prompt_proj in that order: swapping the two columns changes the module
+    cfg, sc, w, zq, pf = _level0(n_blocks=1)
+    f = sc.points.reshape(-1, 3)
+    a = rf.forward(f, zq, cfg.H, cfg.W, w, pf)
+    b = rf.forward(f, zq, cfg.H, cfg.W, w, pf[:, ::-1].copy())
+    assert np.abs(a - b).max() > 1e-4
+
+
+def test_zero_out_proj_adds_its_bias():
+    """out_proj zero with bias delta: the refined log depth is logz + delta exactly (_refine_logz, v3.py:359)."""
+    cfg, sc, w, zq, pf = _level0()
+    wz = dataclasses.replace(w, out_w=np.zeros_like(w.out_w), out_b=np.array([0.125], np.float32))
+    pts, _, _ = rf.step(sc.points[None], sc.lidar[None], sc.conf[None], wz, precision="int8", iters=4)
+    assert np.array_equal(pts[..., 2], sc.points[None, ..., 2] + np.float32(0.125))
+    assert np.array_equal(pts[..., :2], sc.points[None, ..., :2])
