@@ -389,6 +389,80 @@ int pmg_refiner_check(pmg_refiner* r, void* stream);
  * last block), 4 q1 (the last block's conv1 input codes), 5 q2 (its conv2 input codes). NULL for any other id. */
 const void* pmg_refiner_buffer(pmg_refiner* r, int id);
 
+/* ------------------------------------------------------------------------------------------------------------ *
+ * The multi-level refiner -- Sparse3DUNet (moge/model/modules/sparse_unet.py:17-258) in the deployed int8
+ * arithmetic (qat.py:1-16; the device engine's sequence Refiner.swift:224-292, Refiner.metal:133-322): input_proj
+ * (+ prompt_proj) -> per level: SparseResBlock3d stage, PoolDown (mean pool, int8 linear) -> encoder conditioning
+ * (encoder_fuse on the token grid + encoder_bias_map, gathered by column) -> fuse_proj (int8 linear, SiLU, int8
+ * linear) -> bottleneck stage -> per level: NearestUp (int8 linear at the coarse level, upsample, + skip), stage ->
+ * out_proj. Level structure: level 0 = one voxel per pixel (raster order); level k+1 = the stride-2 perfect-partition
+ * pool of level k (flex_sparse_blocks.py:78-90, _core.py:339-395), voxels in (b, i, j, z) order; submanifold maps per
+ * level (_core.py:269-304). Every level is built and sized on the device: no host synchronisation, the forward is
+ * captured into a HIP graph per (buffers, stream). Buffers are allocated for B*H*W voxels on every level.
+ * ------------------------------------------------------------------------------------------------------------ */
+typedef struct {
+    int B, H, W;            /* point map; level 0 = B*H*W voxels; H, W multiples of 2^(levels-1) */
+    int levels;             /* len(model_channels), 2 .. 8; downsample factors 2 (encoder_downsample 2^(levels-1)) */
+    int channels[8];        /* model_channels: level 0 in {16, 32, 48, 64, 128}; others in {16, 32, 48, 64, 96,
+                               128, 192, 256} */
+    int enc_blocks[8];      /* encoder_blocks_per_level (down_stages[k]) */
+    int dec_blocks[8];      /* decoder_blocks_per_level: dec_blocks[i] is up_stages[i], at level levels-2-i; the last
+                               (level 0) needs >= 1 block (out_proj runs in its last convolution's epilogue) */
+    int bottleneck_blocks;
+    int enc_channels;       /* encoder_fuse in_features (multiple of 16) */
+    float depth_resolution; /* refiner_depth_resolution (v3.py:29): keys when no coords are given */
+    int use_graph;
+} pmg_unet_config;
+
+typedef struct {
+    const int8_t* w;      /* [N][K] int8, nn.Linear's (out, in) layout */
+    const float* w_scale; /* [N] per-output-channel weight scale */
+    const float* bias;    /* [N] */
+    float a_scale;        /* clip/127 of the input activation */
+    float q_mult;         /* 127/clip: quantises the input */
+} pmg_linear_weights;
+
+typedef struct {
+    const float* in_w;  /* input_proj [C0][3], [C0] */
+    const float* in_b;
+    const float* pr_w;  /* prompt_proj [C0][2], [C0], or both NULL */
+    const float* pr_b;
+    const float* out_w; /* out_proj [C0], [1] */
+    const float* out_b;
+    int n_blocks;       /* sum(enc_blocks) + bottleneck_blocks + sum(dec_blocks) */
+    const pmg_block_weights* blocks;   /* host array in module order: down_stages[0..L-1], bottleneck_stage,
+                                          up_stages[0..L-2]; conv weights [C][27][C] int8 */
+    int n_linears;      /* 2 (levels - 1) + 3 */
+    const pmg_linear_weights* linears; /* host array: downsample_blocks[0..L-2].linear, encoder_fuse, fuse_proj.0,
+                                          fuse_proj.2, upsample_blocks[0..L-2].linear */
+} pmg_unet_weights;
+
+typedef struct pmg_unet pmg_unet;
+
+pmg_unet* pmg_unet_create(const pmg_unet_config* cfg);
+void pmg_unet_destroy(pmg_unet* u);
+/* Bytes of the context's device workspace (allocated by pmg_unet_create). */
+size_t pmg_unet_workspace_bytes(const pmg_unet* u);
+/* Voxel capacity of every level (B*H*W). */
+int64_t pmg_unet_capacity(const pmg_unet* u);
+int pmg_unet_set_weights(pmg_unet* u, const pmg_unet_weights* w);
+/* Sparse3DUNet.forward (sparse_unet.py:176-258), the call _refine_logz makes (v3.py:356-357): feats [M][3] fp32 (the
+ * point map reshaped, v3.py:342), M = B*H*W in raster order; coords [M][4] int32 (b, i, j, z) as _voxelize builds
+ * them (v3.py:337-340) or NULL to voxelise feats[:, 2] with depth_resolution; prompt_feats [M][2] or NULL (no
+ * prompt_proj, sparse_unet.py:191); encoder_feature [B][enc_channels][H/ds][W/ds] fp32 (ds = 2^(levels-1));
+ * encoder_bias_map [B][C_{L-1}][H/ds][W/ds] fp32 or NULL (sparse_unet.py:235-239); out [M] fp32. */
+int pmg_unet_forward(pmg_unet* u, const float* feats, const int32_t* coords, const float* prompt_feats,
+                     const float* encoder_feature, const float* encoder_bias_map, float* out, void* stream);
+/* Device buffers of the last forward, for parity tests: PMG_UNET_COUNTS int64 [levels] voxels per level;
+ * PMG_UNET_COORDS [cap][4] int32 of `level`; PMG_UNET_PARENT [cap] int32, level -> level + 1; PMG_UNET_NMAP
+ * [27][cap] int32 and PMG_UNET_TILE_MASK [cap/16] (levels >= 1); PMG_UNET_COL_OFFSETS the column CSR
+ * [B*H_k*W_k + 1] int32 (levels >= 1); PMG_UNET_DOWN [cap][C] fp32, the down stage's output at `level`;
+ * PMG_UNET_UP [cap][C] fp32, the up stage's (the bottleneck's at the deepest level); PMG_UNET_ENC_TOKENS
+ * [B*(H/ds)*(W/ds)][C_{L-1}] fp32, encoder_fuse + bias map per token. NULL for an id the level does not have. */
+enum { PMG_UNET_COUNTS = 0, PMG_UNET_COORDS = 1, PMG_UNET_PARENT = 2, PMG_UNET_NMAP = 3, PMG_UNET_TILE_MASK = 4,
+       PMG_UNET_DOWN = 5, PMG_UNET_UP = 6, PMG_UNET_ENC_TOKENS = 7, PMG_UNET_COL_OFFSETS = 8 };
+const void* pmg_unet_buffer(pmg_unet* u, int id, int level);
+
 #ifdef __cplusplus
 }
 #endif

@@ -128,6 +128,8 @@ def forward(feats, levels: List[Level], w, encoder_feature, prompt_feats=None, e
         t = L - 2 - i
         lin = linear(x, w.up[i], mode, record, f"upsample_blocks.{i}.linear")   # flex_sparse_blocks.py:99-105
         x = (sparse_upsample(lin, levels[t + 1].parent) + skips[t]).astype(np.float32)
+        if tr is not None:
+            tr[f"dec{i}_in"] = x
         bt = [] if tr is not None else None
         for j, blk in enumerate(w.dec[i]):
             x = resblock(x, levels[t].nmap, blk, mode, bt, record, f"up_stages.{i}.{j}")

@@ -49,12 +49,35 @@ class BlockWeights(C.Structure):
     ]
 
 
+class UNetConfig(C.Structure):
+    _fields_ = [
+        ("B", i32), ("H", i32), ("W", i32), ("levels", i32), ("channels", i32 * 8), ("enc_blocks", i32 * 8),
+        ("dec_blocks", i32 * 8), ("bottleneck_blocks", i32), ("enc_channels", i32), ("depth_resolution", f32),
+        ("use_graph", i32),
+    ]
+
+
+class LinearWeights(C.Structure):
+    _fields_ = [("w", vp), ("w_scale", vp), ("bias", vp), ("a_scale", f32), ("q_mult", f32)]
+
+
 class RefinerWeights(C.Structure):
     _fields_ = [
         ("in_w", vp), ("in_b", vp), ("pr_w", vp), ("pr_b", vp), ("out_w", vp), ("out_b", vp),
         ("n_blocks", i32), ("blocks", C.POINTER(BlockWeights)),
     ]
 
+
+class UNetWeights(C.Structure):
+    _fields_ = [
+        ("in_w", vp), ("in_b", vp), ("pr_w", vp), ("pr_b", vp), ("out_w", vp), ("out_b", vp),
+        ("n_blocks", i32), ("blocks", C.POINTER(BlockWeights)), ("n_linears", i32),
+        ("linears", C.POINTER(LinearWeights)),
+    ]
+
+
+UNET_COUNTS, UNET_COORDS, UNET_PARENT, UNET_NMAP, UNET_TILE_MASK, UNET_DOWN, UNET_UP, UNET_ENC_TOKENS, \
+    UNET_COL_OFFSETS = range(9)
 
 # name -> (restype, argtypes)
 SIGNATURES = {
@@ -102,6 +125,13 @@ SIGNATURES = {
     "pmg_refiner_forward": (i32, [vp, vp, vp, vp, vp, vp]),
     "pmg_refiner_check": (i32, [vp, vp]),
     "pmg_refiner_buffer": (vp, [vp, i32]),
+    "pmg_unet_create": (vp, [C.POINTER(UNetConfig)]),
+    "pmg_unet_destroy": (None, [vp]),
+    "pmg_unet_workspace_bytes": (sz, [vp]),
+    "pmg_unet_capacity": (i64, [vp]),
+    "pmg_unet_set_weights": (i32, [vp, C.POINTER(UNetWeights)]),
+    "pmg_unet_forward": (i32, [vp, vp, vp, vp, vp, vp, vp, vp]),
+    "pmg_unet_buffer": (vp, [vp, i32, i32]),
 }
 
 _lib: C.CDLL | None = None

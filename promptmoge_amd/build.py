@@ -21,7 +21,7 @@ HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 BUILD = HERE / "_build"
 LIB = HERE / "libpmg.so"
-SOURCES = ["pmg_api.hip", "pmg_structure.hip", "pmg_conv.hip", "pmg_conv_col.hip", "pmg_rowops.hip", "pmg_fit.hip", "pmg_fill.hip", "pmg_order.hip", "pmg_probe.hip", "pmg_pool.hip", "pmg_gauge.hip"]
+SOURCES = ["pmg_api.hip", "pmg_structure.hip", "pmg_conv.hip", "pmg_conv_col.hip", "pmg_rowops.hip", "pmg_fit.hip", "pmg_fill.hip", "pmg_order.hip", "pmg_probe.hip", "pmg_pool.hip", "pmg_gauge.hip", "pmg_unet.hip"]
 ARCH = "gfx950"
 
 FLAGS = [

@@ -14,6 +14,7 @@
 #include <vector>
 
 #include "pmg_common.h"
+#include "pmg_graph.h"
 #include "pmg_internal.h"
 
 namespace pmg {
@@ -72,29 +73,10 @@ struct pmg_refiner {
 
     // Captured steps and forwards, keyed by (kind, buffers..., stream); a ping-pong of two point buffers over K
     // steps uses two entries.
-    struct Graph {
-        const void* key[8];
-        hipGraph_t graph;
-        hipGraphExec_t exec;
-    };
-    std::vector<Graph> graphs;
+    GraphCache graphs;
 };
 
 static size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
-
-// Destroys the cached graphs. A replay may still be running on the stream it was launched on, so the device is
-// synchronised first (this runs on eviction, new weights and destruction only).
-static void drop_graphs(pmg_refiner* r) {
-    if (r->graphs.empty()) return;
-    (void)hipDeviceSynchronize();
-    for (auto& g : r->graphs) {
-        hipGraphExecDestroy(g.exec);
-        hipGraphDestroy(g.graph);
-    }
-    r->graphs.clear();
-}
-
-constexpr size_t kMaxGraphs = 4;
 
 // Residual blocks: conv1 (bias, SiLU, requantise) then conv2 (bias, skip, and either the next block's
 // LayerNorm/SiLU/quantise or, after the last block, out_proj and either the log-depth update of the point map or
@@ -292,41 +274,6 @@ static int enqueue_forward(pmg_refiner* r, const float* feats, const int32_t* co
     return enqueue_blocks(r, nullptr, nullptr, delta_out, s);
 }
 
-// Runs `enqueue` on `s` through the refiner's graph cache: captured the first time a key is seen, replayed after.
-// The legacy default stream cannot be captured; on it (or with use_graph off) the work is enqueued eagerly.
-template <typename F>
-static int run_cached(pmg_refiner* r, const void* const (&key)[8], hipStream_t s, F&& enqueue) {
-    if (!r->cfg.use_graph || s == nullptr) return enqueue();
-    for (auto& g : r->graphs)
-        if (std::memcmp(g.key, key, sizeof key) == 0) {
-            PMG_CHECK_HIP(hipGraphLaunch(g.exec, s));
-            return PMG_OK;
-        }
-    if (r->graphs.size() >= kMaxGraphs) drop_graphs(r);
-    PMG_CHECK_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-    const int e = enqueue();
-    hipGraph_t graph = nullptr;
-    const hipError_t ce = hipStreamEndCapture(s, &graph);
-    if (e) {
-        if (graph) hipGraphDestroy(graph);
-        return e;
-    }
-    if (ce != hipSuccess) return fail(PMG_E_HIP, std::string("hipStreamEndCapture: ") + hipGetErrorString(ce));
-    hipGraphExec_t exec = nullptr;
-    const hipError_t ie = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
-    if (ie != hipSuccess) {
-        hipGraphDestroy(graph);
-        return fail(PMG_E_HIP, std::string("hipGraphInstantiate: ") + hipGetErrorString(ie));
-    }
-    pmg_refiner::Graph g{};
-    std::memcpy(g.key, key, sizeof key);
-    g.graph = graph;
-    g.exec = exec;
-    r->graphs.push_back(g);
-    PMG_CHECK_HIP(hipGraphLaunch(exec, s));
-    return PMG_OK;
-}
-
 extern "C" {
 
 const char* pmg_last_error(void) { return g_last_error.c_str(); }
@@ -402,7 +349,7 @@ pmg_refiner* pmg_refiner_create(const pmg_refiner_config* cfg) {
 
 void pmg_refiner_destroy(pmg_refiner* r) {
     if (!r) return;
-    drop_graphs(r);
+    r->graphs.clear();
     if (r->arena) hipFree(r->arena);
     delete r;
 }
@@ -426,7 +373,7 @@ int pmg_refiner_set_weights(pmg_refiner* r, const pmg_refiner_weights* w) {
     r->blocks.assign(w->blocks, w->blocks + w->n_blocks);
     r->w.blocks = nullptr;
     r->have_weights = true;
-    drop_graphs(r);
+    r->graphs.clear();
     return PMG_OK;
 }
 
@@ -437,7 +384,7 @@ int pmg_refiner_step(pmg_refiner* r, const float* points, float* points_out, con
     PMG_REQUIRE((!r->cfg.use_prompt && !r->cfg.final_fit) || (lidar && conf), "LiDAR inputs required");
     hipStream_t s = (hipStream_t)stream;
     const void* const key[8] = {(const void*)1, points, points_out, lidar, conf, st_prompt, st_final, stream};
-    return run_cached(r, key, s, [&] { return enqueue_step(r, points, points_out, lidar, conf, st_prompt, st_final, s); });
+    return r->graphs.run(key, s, r->cfg.use_graph, [&] { return enqueue_step(r, points, points_out, lidar, conf, st_prompt, st_final, s); });
 }
 
 int pmg_refiner_forward(pmg_refiner* r, const float* feats, const int32_t* coords, const float* prompt_feats,
@@ -447,7 +394,7 @@ int pmg_refiner_forward(pmg_refiner* r, const float* feats, const int32_t* coord
     PMG_REQUIRE(!prompt_feats || (r->w.pr_w && r->w.pr_b), "prompt_feats given but the refiner has no prompt_proj");
     hipStream_t s = (hipStream_t)stream;
     const void* const key[8] = {(const void*)2, feats, coords, prompt_feats, out, nullptr, nullptr, stream};
-    return run_cached(r, key, s, [&] { return enqueue_forward(r, feats, coords, prompt_feats, out, s); });
+    return r->graphs.run(key, s, r->cfg.use_graph, [&] { return enqueue_forward(r, feats, coords, prompt_feats, out, s); });
 }
 
 int pmg_refiner_check(pmg_refiner* r, void* stream) {

@@ -19,6 +19,7 @@
 #include <type_traits>
 
 #include "pmg_common.h"
+#include "pmg_internal.h"
 
 namespace pmg {
 
@@ -38,6 +39,8 @@ struct ConvArgs {
     const float* skip;
     void* out;
     const int32_t* order;  // rows in processing order (tile masks follow it), or NULL for 0 .. M-1
+    const int64_t* m_dev;  // spconv_k: the row count on the device (<= M, which is then the map's row stride and
+                           // the grid's capacity), or NULL for M rows
 };
 
 template <typename T>
@@ -112,7 +115,9 @@ __global__ __launch_bounds__(256) void spconv_k(ConvArgs a) {
     __shared__ int8_t taps_s[4][32];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int64_t tile = (int64_t)blockIdx.x * 4 + wv;
-    const int64_t ntile = (a.M + 15) >> 4;
+    const int64_t Mr = a.m_dev ? *a.m_dev : a.M;  // rows; a.M is the map's row stride
+    if ((int64_t)blockIdx.x * 64 >= Mr) return;   // the whole block lies beyond the rows (device-sized grids)
+    const int64_t ntile = (Mr + 15) >> 4;
     const uint32_t mask = tile < ntile ? a.tmask[tile] : 0u;
     if (lane < 27 && ((mask >> lane) & 1u)) taps_s[wv][__popc(mask & ((1u << lane) - 1u))] = (int8_t)lane;
     __syncthreads();
@@ -121,7 +126,7 @@ __global__ __launch_bounds__(256) void spconv_k(ConvArgs a) {
     const int r = lane & 15, g = lane >> 4;
     const int64_t m0 = tile * 16;
     const int64_t row = m0 + r;
-    const bool row_ok = row < a.M;
+    const bool row_ok = row < Mr;
     const int n0 = blockIdx.y * 16 * NB;
 
     typename Acc<T>::type acc[NB];
@@ -137,7 +142,7 @@ __global__ __launch_bounds__(256) void spconv_k(ConvArgs a) {
             const int c = q - t * a.nchunk;
             const int v = taps_s[wv][t];
             const int idx = row_ok ? a.nmap_t[(int64_t)v * a.M + row] : -1;
-            if (idx >= 0 && idx < a.M) av = *(const v4i*)(a.x + (int64_t)idx * a.row_bytes + c * 16);
+            if (idx >= 0 && idx < Mr) av = *(const v4i*)(a.x + (int64_t)idx * a.row_bytes + c * 16);
 #pragma unroll
             for (int j = 0; j < NB; ++j)
                 bv[j] = *(const v4i*)(a.w + ((int64_t)(n0 + 16 * j + r) * 27 + v) * a.row_bytes + c * 16);
@@ -155,7 +160,7 @@ __global__ __launch_bounds__(256) void spconv_k(ConvArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int64_t m = m0 + 4 * g + i;
-            if (m < a.M) epilogue<T, EPI>(a, m, n, acc[j], i);
+            if (m < Mr) epilogue<T, EPI>(a, m, n, acc[j], i);
         }
     }
 }
@@ -600,6 +605,39 @@ static int launch_g2(const ConvArgs& a, int epilogue, hipStream_t s) {
             default: return fail(PMG_E_INVALID, "spconv: epilogue not available for this precision");
         }
         return check_launch("spconv_g2_k");
+    }
+}
+
+int launch_conv_i8_dev(const DevConv& d, hipStream_t s) {
+    PMG_REQUIRE(d.x && d.nmap_t && d.tile_mask && d.w && d.out && d.m_dev, "null buffer");
+    PMG_REQUIRE(d.Ci % 16 == 0 && d.Co % 16 == 0 && d.Ci > 0 && d.Co > 0, "channels must be multiples of 16");
+    PMG_REQUIRE(d.epilogue == PMG_EPI_Q || d.epilogue == PMG_EPI_R || d.epilogue == PMG_EPI_BIAS ||
+                    d.epilogue == PMG_EPI_ACC,
+                "unsupported epilogue");
+    PMG_REQUIRE(d.epilogue != PMG_EPI_R || d.skip, "skip required");
+    if (d.cap == 0) return PMG_OK;
+    ConvArgs a{};
+    a.x = (const uint8_t*)d.x;
+    a.nmap_t = d.nmap_t;
+    a.tmask = d.tile_mask;
+    a.w = (const uint8_t*)d.w;
+    a.M = d.cap;
+    a.Co = d.Co;
+    a.row_bytes = d.Ci;
+    a.nchunk = d.Ci / 16;
+    a.a_scale = d.a_scale;
+    a.w_scale = d.w_scale;
+    a.bias = d.bias;
+    a.out_mult = d.out_mult;
+    a.skip = d.skip;
+    a.out = d.out;
+    a.m_dev = d.m_dev;
+    const int nb = pick_nb(d.Co);
+    switch (d.epilogue) {
+        case PMG_EPI_Q: return launch_nb<int8_t, PMG_EPI_Q>(a, nb, s);
+        case PMG_EPI_R: return launch_nb<int8_t, PMG_EPI_R>(a, nb, s);
+        case PMG_EPI_BIAS: return launch_nb<int8_t, PMG_EPI_BIAS>(a, nb, s);
+        default: return launch_nb<int8_t, PMG_EPI_ACC>(a, nb, s);
     }
 }
 

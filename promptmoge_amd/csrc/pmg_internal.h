@@ -117,4 +117,24 @@ int launch_conv_col(int precision, const ColConvArgs& a, int C, int epi, hipStre
 int launch_anchor(float* points, int B, int H, int W, const float* lidar, const float* conf, int dh, int dw,
                   const float* st, float beta, hipStream_t s);
 
+// int8 submanifold conv on a device-sized level (generic map, spconv_k): rows m < *m_dev of a capacity-`cap` level;
+// nmap_t is [27][cap] and tile_mask covers the rows. Epilogues ACC, BIAS, Q (SiLU requantise), R (+ skip).
+struct DevConv {
+    const int8_t* x;
+    const int32_t* nmap_t;
+    const uint32_t* tile_mask;
+    int64_t cap;
+    const int64_t* m_dev;
+    int Ci, Co;
+    const int8_t* w;  // [Co][27][Ci]
+    int epilogue;
+    float a_scale;
+    const float* w_scale;
+    const float* bias;
+    float out_mult;
+    const float* skip;
+    void* out;
+};
+int launch_conv_i8_dev(const DevConv& d, hipStream_t s);
+
 }  // namespace pmg

@@ -1,0 +1,1023 @@
+// The multi-level sparse U-Net refiner (Sparse3DUNet, moge/model/modules/sparse_unet.py:17-258) in the deployed
+// int8 arithmetic, every level built and sized on the device.
+//
+// Structure. Level 0 holds one voxel per pixel in raster (b, i, j) order (MoGeModel._voxelize, v3.py:305-344).
+// Level k+1 is PoolDown's perfect-partition pool of level k, stride 2 on (i, j, z) (flex_sparse_blocks.py:78-90;
+// _core.py:339-395). Every level's voxels are in (b, i, j, z) order -- the order of _linearise on the pooled shape,
+// i.e. the reference's sorted unique output keys -- so a level is a set of columns (b, i, j), each holding its
+// voxels with increasing z: a column CSR. A coarse column merges the z / 2 lists of its (up to) four child columns:
+// one thread per coarse column counts the distinct values, a two-kernel scan places the columns, and the same
+// merge then writes the coarse voxels and each child's parent. The children of a coarse voxel in increasing row
+// order are the matching runs of its child columns in raster order, the order of the reference's index_add_. This
+// is the per-column design of the reference's device engine (Structure.metal:87-215) without its host-side sizing:
+// the voxel count of every level stays on the device, buffers are allocated for the level-0 count (an upper bound
+// of every level), and every later kernel reads the count. Submanifold maps of levels >= 1: per voxel, the 9
+// neighbouring columns are scanned for z - 1, z, z + 1 (the result of _build_submanifold_nmap_sorted,
+// _core.py:298-304), tap-major [27][capacity] with 16-row tile masks.
+//
+// Layers (int8 contract qat.py:1-16; the deployed engine's sequence, Refiner.swift:224-292, Refiner.metal:133-322):
+//   level-0 blocks         the map-free column convolutions (pmg_conv_col.hip) with the next LayerNorm fused
+//   blocks at levels >= 1  generic-map MFMA conv with the device row count (spconv_k) + a row LayerNorm kernel
+//   PoolDown               children's fp32 mean (row order, / count) quantised in one kernel, then an int8 GEMM
+//   encoder conditioning   per token: quantise-transpose of the planar feature, int8 GEMM (+ the planar bias map),
+//                          gathered per voxel by its column in the concat-quantise of fuse_proj.0's input
+//   fuse_proj              int8 GEMM + SiLU + requantise, int8 GEMM
+//   NearestUp              quantise, int8 GEMM at the coarse level, then parent gather + skip + next LayerNorm
+//   out_proj               in the epilogue of the last level-0 conv
+#include <climits>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "pmg_common.h"
+#include "pmg_graph.h"
+#include "pmg_internal.h"
+
+namespace pmg {
+
+constexpr int kScanTile = 2048;  // columns per block of the column scan (256 threads x 8)
+constexpr int kMaxLevels = 8;
+
+// ---------------------------------------------------------------------------------------------------------------
+// Level structure.
+
+// Level-0 coordinates (b, i, j, zq - zmin[b]) (v3.py:333-340), and the level-0 keys zq.
+__global__ __launch_bounds__(256) void level0_coords_k(const int32_t* __restrict__ zq, const int32_t* __restrict__ zmin,
+                                                       int H, int W, int64_t M, int4* __restrict__ coords) {
+    const int64_t m = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (m >= M) return;
+    const int64_t HW = (int64_t)H * W;
+    const int b = (int)(m / HW);
+    const int p = (int)(m - (int64_t)b * HW);
+    coords[m] = make_int4(b, p / W, p % W, zq[m] - zmin[b]);
+}
+
+// Voxels of column c of a level: [off[c], off[c + 1]); level 0 (off NULL) holds voxel c in column c.
+__device__ inline void col_range(const int32_t* off, int64_t c, int32_t& lo, int32_t& hi) {
+    if (off) {
+        lo = off[c];
+        hi = off[c + 1];
+    } else {
+        lo = (int32_t)c;
+        hi = lo + 1;
+    }
+}
+
+struct PoolGeom {
+    const int4* coords;   // fine level [cap][4]
+    const int32_t* off;   // fine column CSR [B * Hf * Wf + 1], or NULL (level 0)
+    int B, Hf, Wf;        // fine column grid
+    int Hc, Wc;           // coarse column grid: ceil(Hf / 2), ceil(Wf / 2)
+};
+
+// The (up to) four child columns of coarse column C = (b, I, J), in raster order: (2I, 2J), (2I, 2J+1),
+// (2I+1, 2J), (2I+1, 2J+1); those outside the fine grid are empty.
+__device__ inline void child_ranges(const PoolGeom& g, int64_t C, int32_t (&lo)[4], int32_t (&hi)[4]) {
+    const int64_t per = (int64_t)g.Hc * g.Wc;
+    const int b = (int)(C / per);
+    const int rem = (int)(C - (int64_t)b * per);
+    const int I = rem / g.Wc, J = rem - (rem / g.Wc) * g.Wc;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int i = 2 * I + (q >> 1), j = 2 * J + (q & 1);
+        if (i < g.Hf && j < g.Wf) {
+            col_range(g.off, ((int64_t)b * g.Hf + i) * g.Wf + j, lo[q], hi[q]);
+        } else {
+            lo[q] = 0;
+            hi[q] = 0;
+        }
+    }
+}
+
+// The smallest z / 2 at the heads of the four lists (INT_MAX when all are exhausted). z >= 0, so z >> 1 = floor.
+__device__ inline int merge_min(const int4* coords, const int32_t (&h)[4], const int32_t (&e)[4]) {
+    int mn = INT_MAX;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        if (h[q] < e[q]) {
+            const int z = coords[h[q]].w >> 1;
+            mn = z < mn ? z : mn;
+        }
+    return mn;
+}
+
+__global__ __launch_bounds__(256) void pool_count_k(PoolGeom g, int64_t ncols, int32_t* __restrict__ cnt) {
+    const int64_t C = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (C >= ncols) return;
+    int32_t h[4], e[4];
+    child_ranges(g, C, h, e);
+    int n = 0;
+    for (;;) {
+        const int mn = merge_min(g.coords, h, e);
+        if (mn == INT_MAX) break;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            while (h[q] < e[q] && (g.coords[h[q]].w >> 1) == mn) ++h[q];
+        ++n;
+    }
+    cnt[C] = n;
+}
+
+// Exclusive scan of cnt in tiles of kScanTile: excl[c] = sum of the tile's counts before c, tile_sum[t] = total.
+__global__ __launch_bounds__(256) void scan_tiles_k(const int32_t* __restrict__ cnt, int64_t n,
+                                                    int32_t* __restrict__ excl, int32_t* __restrict__ tile_sum) {
+    __shared__ int32_t wsum[4];
+    const int64_t base = (int64_t)blockIdx.x * kScanTile + threadIdx.x * 8;
+    int32_t v[8], s = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        v[k] = base + k < n ? cnt[base + k] : 0;
+        s += v[k];
+    }
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const uint32_t incl = wave_incl_scan_u32((uint32_t)s);
+    if (lane == 63) wsum[w] = (int32_t)incl;
+    __syncthreads();
+    int32_t before = 0;
+    for (int k = 0; k < w; ++k) before += wsum[k];
+    int32_t run = before + (int32_t)incl - s;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        if (base + k < n) excl[base + k] = run;
+        run += v[k];
+    }
+    if (threadIdx.x == 255) tile_sum[blockIdx.x] = before + (int32_t)incl;
+}
+
+// One block: tile_sum -> exclusive tile offsets (in place); the grand total is the level's voxel count (count,
+// int64) and the end of its column CSR (off[ncols]).
+__global__ __launch_bounds__(1024) void scan_top_k(int32_t* __restrict__ tile_sum, int ntiles, int64_t* count,
+                                                   int32_t* off_end) {
+    __shared__ int32_t wsum[16];
+    const int per = (ntiles + 1023) / 1024;
+    const int b0 = threadIdx.x * per;
+    int32_t s = 0;
+    for (int k = 0; k < per; ++k)
+        if (b0 + k < ntiles) s += tile_sum[b0 + k];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const uint32_t incl = wave_incl_scan_u32((uint32_t)s);
+    if (lane == 63) wsum[w] = (int32_t)incl;
+    __syncthreads();
+    int32_t before = 0;
+    for (int k = 0; k < w; ++k) before += wsum[k];
+    int32_t run = before + (int32_t)incl - s;
+    __syncthreads();
+    for (int k = 0; k < per; ++k)
+        if (b0 + k < ntiles) {
+            const int32_t t = tile_sum[b0 + k];
+            tile_sum[b0 + k] = run;
+            run += t;
+        }
+    if (threadIdx.x == 1023) {
+        const int32_t total = before + (int32_t)incl;
+        *count = total;
+        *off_end = total;
+    }
+}
+
+// Writes the coarse voxels of column C (coordinates and the column's CSR start) and the parent of every child.
+__global__ __launch_bounds__(256) void pool_emit_k(PoolGeom g, int64_t ncols, const int32_t* __restrict__ excl,
+                                                   const int32_t* __restrict__ tile_off, int4* __restrict__ coords_c,
+                                                   int32_t* __restrict__ off_c, int32_t* __restrict__ parent) {
+    const int64_t C = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (C >= ncols) return;
+    const int32_t base = excl[C] + tile_off[C / kScanTile];
+    off_c[C] = base;
+    const int64_t per = (int64_t)g.Hc * g.Wc;
+    const int b = (int)(C / per);
+    const int rem = (int)(C - (int64_t)b * per);
+    const int I = rem / g.Wc, J = rem - (rem / g.Wc) * g.Wc;
+    int32_t h[4], e[4];
+    child_ranges(g, C, h, e);
+    int32_t o = base;
+    for (;;) {
+        const int mn = merge_min(g.coords, h, e);
+        if (mn == INT_MAX) break;
+        coords_c[o] = make_int4(b, I, J, mn);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            while (h[q] < e[q] && (g.coords[h[q]].w >> 1) == mn) parent[h[q]++] = o;
+        ++o;
+    }
+}
+
+// The submanifold map of a level >= 1: nmap_t[v][o] = the row of (b, i + di, j + dj, z + dz) or -1, tap
+// v = (di+1)*9 + (dj+1)*3 + (dz+1) (_core.py:65-82), found in the 9 neighbouring columns; 16-row tile masks.
+__global__ __launch_bounds__(256) void nmap_level_k(const int4* __restrict__ coords, const int32_t* __restrict__ off,
+                                                    const int64_t* __restrict__ count, int H, int W, int64_t cap,
+                                                    int32_t* __restrict__ nmap_t, uint32_t* __restrict__ tile_mask) {
+    const int64_t M = *count;
+    if ((int64_t)blockIdx.x * 256 >= M) return;  // whole block beyond the level
+    const int64_t o = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    uint32_t rmask = 0;
+    if (o < M) {
+        const int4 c = coords[o];
+#pragma unroll
+        for (int di = -1; di <= 1; ++di)
+#pragma unroll
+            for (int dj = -1; dj <= 1; ++dj) {
+                int32_t f[3] = {-1, -1, -1};
+                const int i = c.y + di, j = c.z + dj;
+                if (i >= 0 && i < H && j >= 0 && j < W) {
+                    const int64_t col = ((int64_t)c.x * H + i) * W + j;
+                    const int32_t lo = off[col], hi = off[col + 1];
+                    for (int32_t p = lo; p < hi; ++p) {
+                        const int z = coords[p].w;
+                        if (z > c.w + 1) break;
+                        if (z >= c.w - 1) f[z - (c.w - 1)] = p;
+                    }
+                }
+#pragma unroll
+                for (int dz = 0; dz < 3; ++dz) {
+                    const int v = (di + 1) * 9 + (dj + 1) * 3 + dz;
+                    nmap_t[(int64_t)v * cap + o] = f[dz];
+                    rmask |= (f[dz] >= 0 ? 1u : 0u) << v;
+                }
+            }
+    }
+#pragma unroll
+    for (int sh = 1; sh < 16; sh <<= 1) rmask |= __shfl_xor(rmask, sh, 16);
+    if ((o & 15) == 0 && o < M) tile_mask[o >> 4] = rmask;
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Row kernels on device-sized levels.
+
+// PoolDown's mean (sparse_pool 'mean', _core.py:464-476: fp32 sums in input row order from 0, divided by the
+// child count) of coarse voxel o, quantised for the pool linear: codes = clamp(rint(mean * mult)). Threads per row
+// = C / 4 (a float4 each).
+__global__ __launch_bounds__(256) void pool_quant_k(const float* __restrict__ x, int C, PoolGeom g,
+                                                    const int4* __restrict__ coords_c, const int64_t* __restrict__ count,
+                                                    float mult, int8_t* __restrict__ codes) {
+    const int tpr = C >> 2;
+    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t o = gid / tpr;
+    const int cq = (int)(gid - o * tpr);
+    if (o >= *count) return;
+    const int4 oc = coords_c[o];
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    int n = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int i = 2 * oc.y + (q >> 1), j = 2 * oc.z + (q & 1);
+        if (i >= g.Hf || j >= g.Wf) continue;
+        int32_t lo, hi;
+        col_range(g.off, ((int64_t)oc.x * g.Hf + i) * g.Wf + j, lo, hi);
+        for (int32_t p = lo; p < hi; ++p) {
+            const int z = g.coords[p].w >> 1;
+            if (z > oc.w) break;
+            if (z == oc.w) {
+                const float4 v = *(const float4*)(x + (int64_t)p * C + 4 * cq);
+                acc.x = acc.x + v.x;
+                acc.y = acc.y + v.y;
+                acc.z = acc.z + v.z;
+                acc.w = acc.w + v.w;
+                ++n;
+            }
+        }
+    }
+    const float cnt = (float)n;
+    const float h[4] = {acc.x / cnt, acc.y / cnt, acc.z / cnt, acc.w / cnt};
+    store_codes4(h, mult, codes + o * C + 4 * cq);
+}
+
+// codes = clamp(rint(x * mult)) of a device-sized [rows][C] fp32 array (the input of NearestUp's linear).
+__global__ __launch_bounds__(256) void quant_rows_k(const float* __restrict__ x, int C, const int64_t* __restrict__ count,
+                                                    float mult, int8_t* __restrict__ codes) {
+    const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;  // group of 4
+    if (q * 4 >= *count * C) return;
+    const float4 v = *(const float4*)(x + q * 4);
+    const float h[4] = {v.x, v.y, v.z, v.w};
+    store_codes4(h, mult, codes + q * 4);
+}
+
+// Row LayerNorm / SiLU / quantise in the 16-rows-per-wave layout of the fused epilogues (lane (r, g) holds
+// channels 16j + 4g + i of row r; quad-order sums), on a device-sized level:
+//   UP = false: codes = quant(silu(LN(x))) of x
+//   UP = true:  y = lin[parent[m]] + skip[m] (NearestUp + the U-Net's skip add, sparse_unet.py:251-254), written
+//               to y_out, then (gamma non-NULL) codes of y
+template <int C, bool UP>
+__global__ __launch_bounds__(256) void rows_ln_k(const float* __restrict__ x, const int32_t* __restrict__ parent,
+                                                 const float* __restrict__ skip, const int64_t* __restrict__ count,
+                                                 const float* __restrict__ gamma, const float* __restrict__ beta,
+                                                 float eps, float mult, float* __restrict__ y_out,
+                                                 int8_t* __restrict__ codes) {
+    constexpr int NB = C / 16;
+    const int64_t M = *count;
+    if ((int64_t)blockIdx.x * 64 >= M) return;
+    const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+    const int64_t m = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 16 + r;
+    const bool ok = m < M;
+    const int64_t mo = ok ? m : 0;
+    float y[NB][4];
+    const int64_t src = UP ? (int64_t)parent[mo] : mo;
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+        const float4 v = *(const float4*)(x + src * C + 16 * j + 4 * g);
+        y[j][0] = v.x;
+        y[j][1] = v.y;
+        y[j][2] = v.z;
+        y[j][3] = v.w;
+        if constexpr (UP) {
+            const float4 k = *(const float4*)(skip + mo * C + 16 * j + 4 * g);
+            y[j][0] = y[j][0] + k.x;
+            y[j][1] = y[j][1] + k.y;
+            y[j][2] = y[j][2] + k.z;
+            y[j][3] = y[j][3] + k.w;
+            if (ok) *(float4*)(y_out + mo * C + 16 * j + 4 * g) = make_float4(y[j][0], y[j][1], y[j][2], y[j][3]);
+        }
+    }
+    if (!gamma) return;
+    ln_silu_quad<NB, false>(y, gamma, beta, eps, g);
+    if (!ok) return;
+    uint32_t pk[NB];
+    silu_codes_packed<NB>(y, mult, pk);
+#pragma unroll
+    for (int j = 0; j < NB; ++j) *(uint32_t*)(codes + mo * C + 16 * j + 4 * g) = pk[j];
+}
+
+// The encoder feature, planar [B][K][RC] fp32, into int8 rows [B * RC][K] = clamp(rint(v * mult)): 64 x 64 tiles
+// transposed through LDS (loads along the token index, stores along the channel).
+__global__ __launch_bounds__(256) void enc_quant_k(const float* __restrict__ planar, int K, int64_t RC, float mult,
+                                                   int8_t* __restrict__ codes) {
+    __shared__ int8_t tile[64][64 + 4];
+    const int b = blockIdx.z;
+    const int64_t t0 = (int64_t)blockIdx.x * 64;
+    const int k0 = blockIdx.y * 64;
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int kk = ty + 4 * r;
+        const int64_t t = t0 + tx;
+        float v = 0.0f;
+        if (t < RC && k0 + kk < K) v = planar[((int64_t)b * K + k0 + kk) * RC + t];
+        tile[kk][tx] = quant_i8(v, mult);
+    }
+    __syncthreads();
+    const int tt = threadIdx.x >> 2, kc = (threadIdx.x & 3) * 16;
+    const int64_t t = t0 + tt;
+    if (t >= RC || k0 + kc >= K) return;
+    uint32_t w[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        w[u] = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[u] |= (uint32_t)(uint8_t)tile[kc + 4 * u + i][tt] << (8 * i);
+    }
+    *(uint4*)(codes + ((int64_t)b * RC + t) * K + k0 + kc) = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// fuse_proj.0's input: cat([x, enc_tok[token of the voxel's column]]) quantised with one scale (sparse_unet.py:
+// 240; the deployed concat_q8, Refiner.metal:285-300). Token of (b, i, j) = (b * R + i) * Cc + j.
+__global__ __launch_bounds__(256) void concat_quant_k(const float* __restrict__ x, const float* __restrict__ enc_tok,
+                                                      const int4* __restrict__ coords, const int64_t* __restrict__ count,
+                                                      int C, int R, int Cc, float mult, int8_t* __restrict__ codes) {
+    const int tpr = C >> 1;  // 2C channels, 4 per thread
+    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t o = gid / tpr;
+    const int cq = (int)(gid - o * tpr);
+    if (o >= *count) return;
+    const int c = 4 * cq;
+    const float* src;
+    if (c < C) {
+        src = x + o * C + c;
+    } else {
+        const int4 v = coords[o];
+        src = enc_tok + (((int64_t)v.x * R + v.y) * Cc + v.z) * C + (c - C);
+    }
+    const float4 v = *(const float4*)src;
+    const float h[4] = {v.x, v.y, v.z, v.w};
+    store_codes4(h, mult, codes + o * 2 * C + c);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// int8 dense GEMM on MFMA (nn.Linear on int8 codes, the deployed dg8 kernels, Refiner.metal:173-250):
+//   out[m][n] = (acc * a_scale) * w_scale[n] + bias[n] (+ planar_add[b][n][rc], m = b * RC + rc)      EPI_BIAS
+//   codes[m][n] = quant(silu(...), out_mult)                                                           EPI_Q
+// acc = sum_k A[m][k] * W[n][k] exact in int32; A [rows][K] int8 codes, W [N][K] int8 (nn.Linear's layout).
+// One wave per 16 rows x 16 NB columns, v_mfma_i32_16x16x64_i8 over the K chunks with the operand layout of
+// spconv_k (lane l: row / column l % 16, 16-byte chunk l / 16 of each 64-byte step).
+struct GemmArgs {
+    const int8_t* a;
+    const int8_t* w;
+    int64_t rows_cap;
+    const int64_t* rows_dev;  // rows on the device, or NULL for rows_cap
+    int K, N;
+    float a_scale;
+    const float* w_scale;
+    const float* bias;
+    float out_mult;
+    void* out;
+    const float* planar_add;
+    int64_t planar_rc;
+};
+
+template <int NB, int EPI>
+__global__ __launch_bounds__(256) void gemm_i8_k(GemmArgs g) {
+    const int64_t rows = g.rows_dev ? *g.rows_dev : g.rows_cap;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int64_t m0 = ((int64_t)blockIdx.x * 4 + wv) * 16;
+    if (m0 >= rows) return;
+    const int r = lane & 15, gq = lane >> 4;
+    const int64_t row = m0 + r;
+    const bool row_ok = row < rows;
+    const int n0 = blockIdx.y * 16 * NB;
+    const int nchunk = g.K >> 4;
+    v4i acc[NB];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) acc[j] = v4i{0, 0, 0, 0};
+    for (int q0 = 0; q0 < nchunk; q0 += 4) {
+        const int q = q0 + gq;
+        v4i av = {0, 0, 0, 0};
+        v4i bv[NB];
+        if (q < nchunk) {
+            if (row_ok) av = *(const v4i*)(g.a + row * g.K + q * 16);
+#pragma unroll
+            for (int j = 0; j < NB; ++j) bv[j] = *(const v4i*)(g.w + (int64_t)(n0 + 16 * j + r) * g.K + q * 16);
+        } else {
+#pragma unroll
+            for (int j = 0; j < NB; ++j) bv[j] = v4i{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int j = 0; j < NB; ++j) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv[j], acc[j], 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+        const int n = n0 + 16 * j + r;
+        const float ws = g.w_scale[n], bs = g.bias ? g.bias[n] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int64_t m = m0 + 4 * gq + i;
+            if (m >= rows) continue;
+            float y = (float)acc[j][i] * g.a_scale;
+            y = y * ws;
+            if (g.bias) y = y + bs;
+            if constexpr (EPI == PMG_EPI_Q) {
+                ((int8_t*)g.out)[m * g.N + n] = silu_quant_i8(y, g.out_mult);
+            } else {
+                if (g.planar_add) {
+                    const int64_t b = m / g.planar_rc, rc = m - b * g.planar_rc;
+                    y = y + g.planar_add[(b * g.N + n) * g.planar_rc + rc];
+                }
+                ((float*)g.out)[m * g.N + n] = y;
+            }
+        }
+    }
+}
+
+static int launch_gemm(const GemmArgs& g, int epi, hipStream_t s) {
+    PMG_REQUIRE(g.K % 16 == 0 && g.N % 16 == 0 && g.K > 0 && g.N > 0, "GEMM sizes must be multiples of 16");
+    if (g.rows_cap == 0) return PMG_OK;
+    const int b = g.N / 16;
+    const int nb = b % 4 == 0 ? 4 : (b % 2 == 0 ? 2 : 1);
+    const dim3 grid((unsigned)((g.rows_cap + 63) / 64), (unsigned)(g.N / (16 * nb)));
+#define PMG_GEMM_CASE(NBV)                                                                       \
+    if (nb == NBV) {                                                                             \
+        if (epi == PMG_EPI_Q)                                                                    \
+            hipLaunchKernelGGL((gemm_i8_k<NBV, PMG_EPI_Q>), grid, dim3(256), 0, s, g);           \
+        else                                                                                     \
+            hipLaunchKernelGGL((gemm_i8_k<NBV, PMG_EPI_BIAS>), grid, dim3(256), 0, s, g);        \
+    }
+    PMG_GEMM_CASE(4)
+    PMG_GEMM_CASE(2)
+    PMG_GEMM_CASE(1)
+#undef PMG_GEMM_CASE
+    return check_launch("gemm_i8_k");
+}
+
+#define PMG_LN_SWITCH(C, BODY)                                                                  \
+    switch (C) {                                                                                \
+        case 16: { constexpr int CC = 16; BODY; break; }                                       \
+        case 32: { constexpr int CC = 32; BODY; break; }                                       \
+        case 48: { constexpr int CC = 48; BODY; break; }                                       \
+        case 64: { constexpr int CC = 64; BODY; break; }                                       \
+        case 96: { constexpr int CC = 96; BODY; break; }                                       \
+        case 128: { constexpr int CC = 128; BODY; break; }                                     \
+        case 192: { constexpr int CC = 192; BODY; break; }                                     \
+        case 256: { constexpr int CC = 256; BODY; break; }                                     \
+        default: return fail(PMG_E_INVALID, "unsupported level width " + std::to_string(C));   \
+    }
+
+static bool unet_width(int C) {
+    return C == 16 || C == 32 || C == 48 || C == 64 || C == 96 || C == 128 || C == 192 || C == 256;
+}
+static bool col_width(int C) { return C == 16 || C == 32 || C == 48 || C == 64 || C == 128; }
+
+static int launch_rows_ln(bool up, int C, const float* x, const int32_t* parent, const float* skip,
+                          const int64_t* count, int64_t cap, const float* gamma, const float* beta, float mult,
+                          float* y_out, int8_t* codes, hipStream_t s) {
+    if (cap == 0) return PMG_OK;
+    const dim3 grid((unsigned)((cap + 63) / 64));
+    if (up) {
+        PMG_LN_SWITCH(C, hipLaunchKernelGGL((rows_ln_k<CC, true>), grid, dim3(256), 0, s, x, parent, skip, count,
+                                            gamma, beta, 1e-6f, mult, y_out, codes));
+    } else {
+        PMG_LN_SWITCH(C, hipLaunchKernelGGL((rows_ln_k<CC, false>), grid, dim3(256), 0, s, x, parent, skip, count,
+                                            gamma, beta, 1e-6f, mult, y_out, codes));
+    }
+    return check_launch("rows_ln_k");
+}
+
+}  // namespace pmg
+
+using namespace pmg;
+
+// ---------------------------------------------------------------------------------------------------------------
+// The U-Net context: one arena holding every level's structure and activations at the level-0 capacity.
+struct pmg_unet {
+    pmg_unet_config cfg{};
+    int L = 0;
+    int64_t cap = 0;              // level-0 voxels = B * H * W, the capacity of every level
+    int Hk[kMaxLevels], Wk[kMaxLevels];
+    int64_t ncols[kMaxLevels];    // B * Hk * Wk
+    int R = 0, Cc = 0;            // encoder token grid
+    int64_t T = 0;                // tokens B * R * Cc
+    int Cmax = 0;
+
+    void* arena = nullptr;
+    size_t arena_bytes = 0;
+    int64_t* counts = nullptr;    // [L] voxels per level (device)
+    int32_t* zq0 = nullptr;       // level-0 keys [cap]
+    int32_t* zmin = nullptr;      // [B] (and zmax [B])
+    int4* coords0 = nullptr;      // level-0 coordinates when not given
+    int4* coords[kMaxLevels] = {};      // [cap] (level 0: the caller's or coords0)
+    int32_t* off[kMaxLevels] = {};      // column CSR [ncols + 1] (level 0: NULL)
+    int32_t* parent[kMaxLevels] = {};   // level k -> k + 1 [cap]
+    int32_t* nmap_t[kMaxLevels] = {};   // [27][cap] (levels >= 1)
+    uint32_t* tmask[kMaxLevels] = {};   // [cap / 16 + 1]
+    float* xd[kMaxLevels] = {};         // down-stage stream = skip [cap][C_k]
+    float* xu[kMaxLevels] = {};         // up-stage stream [cap][C_k] (k < L - 1)
+    float* xb = nullptr;                // bottleneck stream [cap][C_L]
+    int32_t* scan_cnt = nullptr;        // [max ncols]
+    int32_t* scan_excl = nullptr;       // [max ncols]
+    int32_t* scan_tiles = nullptr;      // [max ncols / kScanTile + 1]
+    int8_t* q1 = nullptr;               // [cap][Cmax]
+    int8_t* q2 = nullptr;
+    int8_t* codes = nullptr;            // linear inputs [cap][max(2 C_L, Cmax)]
+    int8_t* codes2 = nullptr;           // fuse_proj.2 input [cap][C_L]
+    float* lin = nullptr;               // NearestUp linear output [cap][Cmax]
+    int8_t* enc_codes = nullptr;        // [T][enc_channels]
+    float* enc_tok = nullptr;           // [T][C_L]
+
+    bool have_weights = false;
+    const float* in_w = nullptr;
+    const float* in_b = nullptr;
+    const float* pr_w = nullptr;
+    const float* pr_b = nullptr;
+    const float* out_w = nullptr;
+    const float* out_b = nullptr;
+    std::vector<pmg_block_weights> down[kMaxLevels], dec[kMaxLevels], bott;
+    std::vector<pmg_linear_weights> pool, up;
+    pmg_linear_weights enc{}, fuse0{}, fuse2{};
+
+    GraphCache graphs;
+};
+
+static size_t ualign(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// One residual block on level k (flex_sparse_blocks.py:70-75) whose conv1 input codes are in u->q1 and whose stream
+// is x (updated in place). After conv2: the next block's LayerNorm codes (level 0: fused RLN epilogue; else the row
+// kernel), nothing, or (last level-0 block of the network) out_proj into delta.
+static int enqueue_block(pmg_unet* u, int k, const pmg_block_weights& bk, const pmg_block_weights* next, float* x,
+                         float* delta, hipStream_t s) {
+    const int C = u->cfg.channels[k];
+    if (k == 0) {
+        ColConvArgs a1{};
+        a1.x = u->q1;
+        a1.zq = u->zq0;
+        a1.w = bk.w1;
+        a1.M = u->cap;
+        a1.H = u->cfg.H;
+        a1.W = u->cfg.W;
+        a1.a_scale = bk.a1_scale;
+        a1.w_scale = bk.w1_scale;
+        a1.bias = bk.b1;
+        a1.out_mult = bk.q2_mult;
+        a1.out = u->q2;
+        if (int e = launch_conv_col(PMG_PREC_INT8, a1, C, PMG_EPI_Q, s)) return e;
+        ColConvArgs a2{};
+        a2.x = u->q2;
+        a2.zq = u->zq0;
+        a2.w = bk.w2;
+        a2.M = u->cap;
+        a2.H = u->cfg.H;
+        a2.W = u->cfg.W;
+        a2.a_scale = bk.a2_scale;
+        a2.w_scale = bk.w2_scale;
+        a2.bias = bk.b2;
+        a2.skip = x;
+        a2.out = x;
+        if (next) {
+            a2.ln_gamma = next->ln_gamma;
+            a2.ln_beta = next->ln_beta;
+            a2.ln_eps = 1e-6f;
+            a2.next_mult = next->q1_mult;
+            a2.next_q = u->q1;
+            return launch_conv_col(PMG_PREC_INT8, a2, C, PMG_EPI_RLN, s);
+        }
+        if (delta) {
+            a2.out_w = u->out_w;
+            a2.out_b = u->out_b;
+            a2.out = delta;
+            return launch_conv_col(PMG_PREC_INT8, a2, C, PMG_EPI_ROUT, s);
+        }
+        return launch_conv_col(PMG_PREC_INT8, a2, C, PMG_EPI_R, s);
+    }
+    DevConv c1{};
+    c1.x = u->q1;
+    c1.nmap_t = u->nmap_t[k];
+    c1.tile_mask = u->tmask[k];
+    c1.cap = u->cap;
+    c1.m_dev = u->counts + k;
+    c1.Ci = C;
+    c1.Co = C;
+    c1.w = (const int8_t*)bk.w1;
+    c1.epilogue = PMG_EPI_Q;
+    c1.a_scale = bk.a1_scale;
+    c1.w_scale = bk.w1_scale;
+    c1.bias = bk.b1;
+    c1.out_mult = bk.q2_mult;
+    c1.out = u->q2;
+    if (int e = launch_conv_i8_dev(c1, s)) return e;
+    DevConv c2 = c1;
+    c2.x = u->q2;
+    c2.w = (const int8_t*)bk.w2;
+    c2.epilogue = PMG_EPI_R;
+    c2.a_scale = bk.a2_scale;
+    c2.w_scale = bk.w2_scale;
+    c2.bias = bk.b2;
+    c2.skip = x;
+    c2.out = x;
+    if (int e = launch_conv_i8_dev(c2, s)) return e;
+    if (next)
+        return launch_rows_ln(false, C, x, nullptr, nullptr, u->counts + k, u->cap, next->ln_gamma, next->ln_beta,
+                              next->q1_mult, nullptr, u->q1, s);
+    return PMG_OK;
+}
+
+// A stage of blocks on level k over stream x, whose first block's input codes are already in q1.
+static int enqueue_stage(pmg_unet* u, int k, const std::vector<pmg_block_weights>& st, float* x, float* delta,
+                         hipStream_t s) {
+    for (size_t j = 0; j < st.size(); ++j) {
+        const pmg_block_weights* next = j + 1 < st.size() ? &st[j + 1] : nullptr;
+        if (int e = enqueue_block(u, k, st[j], next, x, next ? nullptr : delta, s)) return e;
+    }
+    return PMG_OK;
+}
+
+static int ln_codes(pmg_unet* u, int k, const float* x, const pmg_block_weights& b, hipStream_t s) {
+    return launch_rows_ln(false, u->cfg.channels[k], x, nullptr, nullptr, u->counts + k, u->cap, b.ln_gamma,
+                          b.ln_beta, b.q1_mult, nullptr, u->q1, s);
+}
+
+static int linear(pmg_unet* u, const int8_t* a, const int64_t* rows_dev, int64_t rows_cap, int K,
+                  const pmg_linear_weights& lw, int N, int epi, float out_mult, void* out, const float* planar,
+                  hipStream_t s) {
+    GemmArgs g{a, lw.w, rows_cap, rows_dev, K, N, lw.a_scale, lw.w_scale, lw.bias, out_mult, out, planar,
+               (int64_t)u->R * u->Cc};
+    return launch_gemm(g, epi, s);
+}
+
+// The level structure (levels 1 .. L-1) from the level-0 coordinates.
+static int enqueue_structure(pmg_unet* u, hipStream_t s) {
+    for (int k = 0; k + 1 < u->L; ++k) {
+        PoolGeom g{u->coords[k], u->off[k], u->cfg.B, u->Hk[k], u->Wk[k], u->Hk[k + 1], u->Wk[k + 1]};
+        const int64_t nc = u->ncols[k + 1];
+        const unsigned gb = (unsigned)((nc + 255) / 256);
+        hipLaunchKernelGGL(pool_count_k, dim3(gb), dim3(256), 0, s, g, nc, u->scan_cnt);
+        if (int e = check_launch("pool_count_k")) return e;
+        const int ntiles = (int)((nc + kScanTile - 1) / kScanTile);
+        hipLaunchKernelGGL(scan_tiles_k, dim3((unsigned)ntiles), dim3(256), 0, s, u->scan_cnt, nc, u->scan_excl,
+                           u->scan_tiles);
+        if (int e = check_launch("scan_tiles_k")) return e;
+        hipLaunchKernelGGL(scan_top_k, dim3(1), dim3(1024), 0, s, u->scan_tiles, ntiles, u->counts + k + 1,
+                           u->off[k + 1] + nc);
+        if (int e = check_launch("scan_top_k")) return e;
+        hipLaunchKernelGGL(pool_emit_k, dim3(gb), dim3(256), 0, s, g, nc, u->scan_excl, u->scan_tiles,
+                           u->coords[k + 1], u->off[k + 1], u->parent[k]);
+        if (int e = check_launch("pool_emit_k")) return e;
+        hipLaunchKernelGGL(nmap_level_k, dim3((unsigned)((u->cap + 255) / 256)), dim3(256), 0, s, u->coords[k + 1],
+                           u->off[k + 1], u->counts + k + 1, u->Hk[k + 1], u->Wk[k + 1], u->cap, u->nmap_t[k + 1],
+                           u->tmask[k + 1]);
+        if (int e = check_launch("nmap_level_k")) return e;
+    }
+    return PMG_OK;
+}
+
+// Sparse3DUNet.forward (sparse_unet.py:176-258) on level-0 voxels; out [cap] = the (M, 1) output.
+static int enqueue_unet(pmg_unet* u, const float* feats, const int32_t* coords, const float* prompt,
+                        const float* enc_feat, const float* enc_bias, float* out, hipStream_t s) {
+    const pmg_unet_config& c = u->cfg;
+    const int L = u->L;
+    const int64_t cap = u->cap;
+    // level 0: keys and coordinates (the caller's, or _voxelize's from the log depth)
+    const int32_t* zkeys = nullptr;
+    if (coords) {
+        u->coords[0] = (int4*)coords;
+        zkeys = coords + 3;
+    } else {
+        if (int e = pmg_voxelize(feats + 2, 3, c.B, c.H, c.W, c.depth_resolution, u->zq0, u->zmin, u->zmin + c.B, s))
+            return e;
+        hipLaunchKernelGGL(level0_coords_k, dim3((unsigned)((cap + 255) / 256)), dim3(256), 0, s, u->zq0, u->zmin,
+                           c.H, c.W, cap, u->coords0);
+        if (int e = check_launch("level0_coords_k")) return e;
+        u->coords[0] = u->coords0;
+        zkeys = (const int32_t*)u->coords0 + 3;
+    }
+    // input_proj (+ prompt_proj), the level-0 keys, and the first block's codes (sparse_unet.py:189-192)
+    const pmg_block_weights* first = !u->down[0].empty() ? &u->down[0][0] : nullptr;
+    InputStage in{};
+    in.points = feats;
+    in.B = c.B;
+    in.H = c.H;
+    in.W = c.W;
+    in.C = c.channels[0];
+    in.dh = c.H;
+    in.dw = c.W;
+    in.in_w = u->in_w;
+    in.in_b = u->in_b;
+    in.pr_w = u->pr_w;
+    in.pr_b = u->pr_b;
+    in.x_out = u->xd[0];
+    in.gamma = first ? first->ln_gamma : u->in_b;  // without a level-0 block the codes are not read
+    in.beta = first ? first->ln_beta : u->in_b;
+    in.eps = 1e-6f;
+    in.out_mult = first ? first->q1_mult : 1.0f;
+    in.q_out = u->q1;
+    in.resolution = c.depth_resolution;
+    in.zq_out = u->zq0;
+    in.prompt_in = prompt;
+    in.use_prompt = prompt != nullptr;
+    in.zkeys = zkeys;
+    in.zkey_stride = 4;
+    if (int e = launch_input_stage(in, false, s)) return e;
+    if (int e = enqueue_structure(u, s)) return e;
+
+    // down stages and PoolDown (sparse_unet.py:223-231; flex_sparse_blocks.py:85-90)
+    for (int k = 0; k < L; ++k) {
+        if (int e = enqueue_stage(u, k, u->down[k], u->xd[k], nullptr, s)) return e;
+        if (k + 1 == L) break;
+        const int Ck = c.channels[k], Cn = c.channels[k + 1];
+        PoolGeom g{u->coords[k], u->off[k], c.B, u->Hk[k], u->Wk[k], u->Hk[k + 1], u->Wk[k + 1]};
+        const int64_t thr = cap * (Ck / 4);
+        hipLaunchKernelGGL(pool_quant_k, dim3((unsigned)((thr + 255) / 256)), dim3(256), 0, s, u->xd[k], Ck, g,
+                           u->coords[k + 1], u->counts + k + 1, u->pool[k].q_mult, u->codes);
+        if (int e = check_launch("pool_quant_k")) return e;
+        if (int e = linear(u, u->codes, u->counts + k + 1, cap, Ck, u->pool[k], Cn, PMG_EPI_BIAS, 0.0f, u->xd[k + 1],
+                           nullptr, s))
+            return e;
+        if (!u->down[k + 1].empty())
+            if (int e = ln_codes(u, k + 1, u->xd[k + 1], u->down[k + 1][0], s)) return e;
+    }
+
+    // encoder conditioning and fuse_proj at the deepest level (sparse_unet.py:233-240)
+    const int top = L - 1, CL = c.channels[top];
+    {
+        const dim3 grid((unsigned)(((int64_t)u->R * u->Cc + 63) / 64), (unsigned)((c.enc_channels + 63) / 64),
+                        (unsigned)c.B);
+        hipLaunchKernelGGL(enc_quant_k, grid, dim3(256), 0, s, enc_feat, c.enc_channels, (int64_t)u->R * u->Cc,
+                           u->enc.q_mult, u->enc_codes);
+        if (int e = check_launch("enc_quant_k")) return e;
+        if (int e = linear(u, u->enc_codes, nullptr, u->T, c.enc_channels, u->enc, CL, PMG_EPI_BIAS, 0.0f,
+                           u->enc_tok, enc_bias, s))
+            return e;
+        const int64_t thr = cap * (CL / 2);
+        hipLaunchKernelGGL(concat_quant_k, dim3((unsigned)((thr + 255) / 256)), dim3(256), 0, s, u->xd[top],
+                           u->enc_tok, u->coords[top], u->counts + top, CL, u->R, u->Cc, u->fuse0.q_mult, u->codes);
+        if (int e = check_launch("concat_quant_k")) return e;
+        if (int e = linear(u, u->codes, u->counts + top, cap, 2 * CL, u->fuse0, CL, PMG_EPI_Q, u->fuse2.q_mult,
+                           u->codes2, nullptr, s))
+            return e;
+        if (int e = linear(u, u->codes2, u->counts + top, cap, CL, u->fuse2, CL, PMG_EPI_BIAS, 0.0f, u->xb, nullptr,
+                           s))
+            return e;
+    }
+    // bottleneck (sparse_unet.py:244-247)
+    if (!u->bott.empty()) {
+        if (int e = ln_codes(u, top, u->xb, u->bott[0], s)) return e;
+        if (int e = enqueue_stage(u, top, u->bott, u->xb, nullptr, s)) return e;
+    }
+    // NearestUp + skip + up stages (sparse_unet.py:249-256; flex_sparse_blocks.py:99-105)
+    float* cur = u->xb;
+    for (int i = 0; i + 1 < L; ++i) {
+        const int t = L - 2 - i;
+        const int Cs = c.channels[t + 1], Ct = c.channels[t];
+        hipLaunchKernelGGL(quant_rows_k, dim3((unsigned)((cap * Cs / 4 + 255) / 256)), dim3(256), 0, s, cur, Cs,
+                           u->counts + t + 1, u->up[i].q_mult, u->codes);
+        if (int e = check_launch("quant_rows_k")) return e;
+        if (int e = linear(u, u->codes, u->counts + t + 1, cap, Cs, u->up[i], Ct, PMG_EPI_BIAS, 0.0f, u->lin,
+                           nullptr, s))
+            return e;
+        const pmg_block_weights* fb = !u->dec[i].empty() ? &u->dec[i][0] : nullptr;
+        if (int e = launch_rows_ln(true, Ct, u->lin, u->parent[t], u->xd[t], u->counts + t, cap,
+                                   fb ? fb->ln_gamma : nullptr, fb ? fb->ln_beta : nullptr, fb ? fb->q1_mult : 1.0f,
+                                   u->xu[t], u->q1, s))
+            return e;
+        if (int e = enqueue_stage(u, t, u->dec[i], u->xu[t], t == 0 ? out : nullptr, s)) return e;
+        cur = u->xu[t];
+    }
+    return PMG_OK;
+}
+
+extern "C" {
+
+pmg_unet* pmg_unet_create(const pmg_unet_config* cfg) {
+    if (!cfg) {
+        set_error("pmg_unet_create: null config");
+        return nullptr;
+    }
+    const pmg_unet_config& c = *cfg;
+    const int L = c.levels;
+    std::string why;
+    if (L < 2 || L > kMaxLevels) why = "levels must be in [2, 8] (sparse_unet.py:52)";
+    else if (c.B < 1 || c.H < 1 || c.W < 1 || (int64_t)c.B * c.H * c.W > INT_MAX / 32)
+        why = "bad point-map size";
+    else if (c.enc_channels < 16 || c.enc_channels % 16 != 0) why = "enc_channels must be a positive multiple of 16";
+    else if (c.bottleneck_blocks < 0) why = "bottleneck_blocks must be >= 0";
+    else {
+        const int ds = 1 << (L - 1);
+        if (c.H % ds != 0 || c.W % ds != 0)
+            why = "H and W must be multiples of the encoder downsampling 2^(levels-1) (sparse_unet.py:187)";
+        if (!col_width(c.channels[0])) why = "level-0 width must be 16, 32, 48, 64 or 128";
+        for (int k = 0; k < L && why.empty(); ++k) {
+            if (!unet_width(c.channels[k])) why = "level widths must be 16, 32, 48, 64, 96, 128, 192 or 256";
+            if (c.enc_blocks[k] < 0 || c.enc_blocks[k] > 16) why = "enc_blocks must be in [0, 16]";
+            if (k + 1 < L && (c.dec_blocks[k] < 0 || c.dec_blocks[k] > 16)) why = "dec_blocks must be in [0, 16]";
+        }
+        if (why.empty() && c.dec_blocks[L - 2] < 1)
+            why = "the last up stage (level 0) needs a block: out_proj runs in its last convolution's epilogue";
+    }
+    if (!why.empty()) {
+        set_error("pmg_unet_create: " + why);
+        return nullptr;
+    }
+    pmg_unet* u = new pmg_unet();
+    u->cfg = c;
+    u->L = L;
+    u->cap = (int64_t)c.B * c.H * c.W;
+    u->Hk[0] = c.H;
+    u->Wk[0] = c.W;
+    for (int k = 1; k < L; ++k) {
+        u->Hk[k] = (u->Hk[k - 1] + 1) / 2;
+        u->Wk[k] = (u->Wk[k - 1] + 1) / 2;
+    }
+    int64_t maxcols = 1;
+    for (int k = 0; k < L; ++k) {
+        u->ncols[k] = (int64_t)c.B * u->Hk[k] * u->Wk[k];
+        if (k > 0 && u->ncols[k] > maxcols) maxcols = u->ncols[k];
+        if (c.channels[k] > u->Cmax) u->Cmax = c.channels[k];
+    }
+    u->R = u->Hk[L - 1];
+    u->Cc = u->Wk[L - 1];
+    u->T = (int64_t)c.B * u->R * u->Cc;
+    const int CL = c.channels[L - 1];
+    const int64_t cap = u->cap;
+    size_t off = 0;
+    std::vector<std::pair<void**, size_t>> plan;
+    auto take = [&](void** p, size_t bytes) { plan.push_back({p, bytes}); };
+    take((void**)&u->counts, sizeof(int64_t) * kMaxLevels);
+    take((void**)&u->zq0, 4 * cap);
+    take((void**)&u->zmin, 8 * c.B);
+    take((void**)&u->coords0, 16 * cap);
+    for (int k = 0; k < L; ++k) {
+        if (k > 0) {
+            take((void**)&u->coords[k], 16 * cap);
+            take((void**)&u->off[k], 4 * (u->ncols[k] + 1));
+            take((void**)&u->nmap_t[k], (size_t)27 * 4 * cap);
+            take((void**)&u->tmask[k], 4 * (cap / 16 + 1));
+        }
+        if (k + 1 < L) {
+            take((void**)&u->parent[k], 4 * cap);
+            take((void**)&u->xu[k], (size_t)4 * cap * c.channels[k]);
+        }
+        take((void**)&u->xd[k], (size_t)4 * cap * c.channels[k]);
+    }
+    take((void**)&u->xb, (size_t)4 * cap * CL);
+    take((void**)&u->scan_cnt, 4 * maxcols);
+    take((void**)&u->scan_excl, 4 * maxcols);
+    take((void**)&u->scan_tiles, 4 * (maxcols / kScanTile + 2));
+    take((void**)&u->q1, (size_t)cap * u->Cmax);
+    take((void**)&u->q2, (size_t)cap * u->Cmax);
+    take((void**)&u->codes, (size_t)cap * (2 * CL > u->Cmax ? 2 * CL : u->Cmax));
+    take((void**)&u->codes2, (size_t)cap * CL);
+    take((void**)&u->lin, (size_t)4 * cap * u->Cmax);
+    take((void**)&u->enc_codes, (size_t)u->T * c.enc_channels);
+    take((void**)&u->enc_tok, (size_t)4 * u->T * CL);
+    for (auto& p : plan) off += ualign(p.second);
+    u->arena_bytes = off;
+    if (hipMalloc(&u->arena, u->arena_bytes) != hipSuccess) {
+        set_error("pmg_unet_create: hipMalloc of " + std::to_string(u->arena_bytes) + " bytes failed");
+        delete u;
+        return nullptr;
+    }
+    if (hipMemset(u->arena, 0, u->arena_bytes) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+        set_error("pmg_unet_create: clearing the workspace failed");
+        (void)hipFree(u->arena);
+        delete u;
+        return nullptr;
+    }
+    uint8_t* a = (uint8_t*)u->arena;
+    off = 0;
+    for (auto& p : plan) {
+        *p.first = a + off;
+        off += ualign(p.second);
+    }
+    // level 0 holds cap voxels: its count is known, every other is written by the structure kernels
+    if (hipMemcpy(u->counts, &u->cap, sizeof(int64_t), hipMemcpyHostToDevice) != hipSuccess) {
+        set_error("pmg_unet_create: initialising the level counts failed");
+        (void)hipFree(u->arena);
+        delete u;
+        return nullptr;
+    }
+    return u;
+}
+
+void pmg_unet_destroy(pmg_unet* u) {
+    if (!u) return;
+    u->graphs.clear();
+    if (u->arena) (void)hipFree(u->arena);
+    delete u;
+}
+
+size_t pmg_unet_workspace_bytes(const pmg_unet* u) { return u ? u->arena_bytes : 0; }
+
+int pmg_unet_set_weights(pmg_unet* u, const pmg_unet_weights* w) {
+    PMG_REQUIRE(u && w, "null argument");
+    const pmg_unet_config& c = u->cfg;
+    const int L = u->L;
+    int nb = 0;
+    for (int k = 0; k < L; ++k) nb += c.enc_blocks[k];
+    nb += c.bottleneck_blocks;
+    for (int k = 0; k + 1 < L; ++k) nb += c.dec_blocks[k];
+    PMG_REQUIRE(w->n_blocks == nb && w->blocks, "block count mismatch: expected " + std::to_string(nb));
+    PMG_REQUIRE(w->n_linears == 2 * (L - 1) + 3 && w->linears, "linear count mismatch: expected " +
+                                                                 std::to_string(2 * (L - 1) + 3));
+    PMG_REQUIRE(w->in_w && w->in_b && w->out_w && w->out_b, "missing projection weights");
+    PMG_REQUIRE((w->pr_w == nullptr) == (w->pr_b == nullptr), "prompt_proj needs weight and bias");
+    for (int i = 0; i < nb; ++i) {
+        const pmg_block_weights& b = w->blocks[i];
+        PMG_REQUIRE(b.ln_gamma && b.ln_beta && b.w1 && b.b1 && b.w2 && b.b2 && b.w1_scale && b.w2_scale,
+                    "missing block weights");
+        PMG_REQUIRE(aligned16(b.w1) && aligned16(b.w2), "conv weights must be 16-byte aligned");
+        PMG_REQUIRE(b.a1_scale > 0.0f && b.a2_scale > 0.0f && b.q1_mult > 0.0f && b.q2_mult > 0.0f,
+                    "int8 blocks need positive activation scales");
+    }
+    for (int i = 0; i < w->n_linears; ++i) {
+        const pmg_linear_weights& l = w->linears[i];
+        PMG_REQUIRE(l.w && l.w_scale && l.bias && aligned16(l.w), "missing or misaligned linear weights");
+        PMG_REQUIRE(l.a_scale > 0.0f && l.q_mult > 0.0f, "linears need positive activation scales");
+    }
+    u->in_w = w->in_w;
+    u->in_b = w->in_b;
+    u->pr_w = w->pr_w;
+    u->pr_b = w->pr_b;
+    u->out_w = w->out_w;
+    u->out_b = w->out_b;
+    int q = 0;
+    for (int k = 0; k < L; ++k) u->down[k].assign(w->blocks + q, w->blocks + q + c.enc_blocks[k]), q += c.enc_blocks[k];
+    u->bott.assign(w->blocks + q, w->blocks + q + c.bottleneck_blocks);
+    q += c.bottleneck_blocks;
+    for (int i = 0; i + 1 < L; ++i) u->dec[i].assign(w->blocks + q, w->blocks + q + c.dec_blocks[i]), q += c.dec_blocks[i];
+    u->pool.assign(w->linears, w->linears + (L - 1));
+    u->enc = w->linears[L - 1];
+    u->fuse0 = w->linears[L];
+    u->fuse2 = w->linears[L + 1];
+    u->up.assign(w->linears + L + 2, w->linears + 2 * L + 1);
+    u->have_weights = true;
+    u->graphs.clear();
+    return PMG_OK;
+}
+
+int pmg_unet_forward(pmg_unet* u, const float* feats, const int32_t* coords, const float* prompt_feats,
+                     const float* encoder_feature, const float* encoder_bias_map, float* out, void* stream) {
+    PMG_REQUIRE(u && u->have_weights, "weights not set");
+    PMG_REQUIRE(feats && encoder_feature && out, "null buffer");
+    PMG_REQUIRE(!prompt_feats || u->pr_w, "prompt_feats given but the refiner has no prompt_proj");
+    PMG_REQUIRE(!coords || aligned16(coords), "coords must be 16-byte aligned");
+    hipStream_t s = (hipStream_t)stream;
+    const void* const key[8] = {feats, coords, prompt_feats, encoder_feature, encoder_bias_map, out, stream,
+                                (const void*)3};
+    return u->graphs.run(key, s, u->cfg.use_graph != 0, [&] {
+        return enqueue_unet(u, feats, coords, prompt_feats, encoder_feature, encoder_bias_map, out, s);
+    });
+}
+
+const void* pmg_unet_buffer(pmg_unet* u, int id, int level) {
+    if (!u || level < 0 || level >= u->L) return nullptr;
+    switch (id) {
+        case PMG_UNET_COUNTS: return u->counts;
+        case PMG_UNET_COORDS: return u->coords[level];
+        case PMG_UNET_PARENT: return level + 1 < u->L ? u->parent[level] : nullptr;
+        case PMG_UNET_NMAP: return level > 0 ? u->nmap_t[level] : nullptr;
+        case PMG_UNET_TILE_MASK: return level > 0 ? u->tmask[level] : nullptr;
+        case PMG_UNET_DOWN: return u->xd[level];
+        case PMG_UNET_UP: return level + 1 < u->L ? u->xu[level] : u->xb;
+        case PMG_UNET_ENC_TOKENS: return u->enc_tok;
+        case PMG_UNET_COL_OFFSETS: return level > 0 ? u->off[level] : nullptr;
+        default: return nullptr;
+    }
+}
+
+int64_t pmg_unet_capacity(const pmg_unet* u) { return u ? u->cap : 0; }
+
+}  // extern "C"

@@ -1,0 +1,218 @@
+"""The multi-level int8 refiner on the GPU, behind Sparse3DUNet.forward's signature.
+
+`UNetRefiner` is an nn.Module with the forward of Sparse3DUNet (moge/model/modules/sparse_unet.py:176-258),
+`forward(feats, coords, shape, encoder_feature, prompt_feats=None, encoder_bias_map=None) -> (M, 1)`, the call
+`_refine_logz` makes (v3.py:356-357): `model.refiner = UNetRefiner.from_state_dict(model.refiner.state_dict())`
+(or `refiner=` there). It runs the whole U-Net -- level structure, per-level maps, int8 convolutions and linears,
+encoder conditioning -- in libpmg (`pmg_unet_*`, csrc/pmg_unet.hip) as one captured HIP graph with no host
+synchronisation. The voxels must be level 0 as _voxelize builds them (v3.py:305-344): one per pixel in raster order.
+
+Weights come from a Sparse3DUNet state dict (plain or QAT), from the Metal engine's refiner.bin / refiner.json
+export, or from promptmoge_amd.unet_weights.make_unet_weights; the arithmetic is the deployed int8 contract
+(qat.py:1-16): per-output-channel int8 weights, per-tensor int8 activations with the layer's clip, int32
+accumulation. Inference only.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from typing import Dict, Optional, Sequence
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._lib import BlockWeights, LinearWeights, UNetConfig, UNetWeights, call, lib
+from .spec import act_mult, act_scale
+from .unet_weights import UNetW, load_refiner_bin, quantized, unet_from_state_dict
+
+
+class UNetDeviceWeights:
+    """A UNetW on the GPU in the layouts the kernels read: conv weights int8 (Co, 3, 3, 3, Ci), linear weights int8
+    (N, K), per-output-channel fp32 scales, fp32 biases / LayerNorm affine, activation scales from the clips."""
+
+    def __init__(self, w: UNetW, device):
+        t = lambda a, dt=torch.float32: torch.as_tensor(np.ascontiguousarray(a)).to(device=device, dtype=dt)
+        self.keep = []
+
+        def dev(a, dt=torch.float32):
+            x = t(a, dt)
+            self.keep.append(x)
+            return x.data_ptr()
+
+        self.in_w, self.in_b = dev(w.in_w), dev(w.in_b)
+        self.pr_w = dev(w.pr_w) if w.pr_w is not None else None
+        self.pr_b = dev(w.pr_b) if w.pr_b is not None else None
+        self.out_w, self.out_b = dev(np.asarray(w.out_w).reshape(-1)), dev(np.asarray(w.out_b).reshape(-1))
+        blocks = [b for st in w.down for b in st] + list(w.bott) + [b for st in w.dec for b in st]
+        self._blocks = (BlockWeights * max(len(blocks), 1))()
+        for k, b in enumerate(blocks):
+            q1, s1 = quantized(b.w1)
+            q2, s2 = quantized(b.w2)
+            self._blocks[k] = BlockWeights(
+                dev(b.gamma), dev(b.beta), dev(q1, torch.int8), dev(s1), dev(b.b1), float(act_scale(b.clip1)),
+                float(act_mult(b.clip1)), dev(q2, torch.int8), dev(s2), dev(b.b2), float(act_scale(b.clip2)),
+                float(act_mult(b.clip2)))
+        linears = list(w.pool) + [w.enc, w.fuse0, w.fuse2] + list(w.up)
+        self._linears = (LinearWeights * len(linears))()
+        for k, l in enumerate(linears):
+            q, s = quantized(l.w)
+            self._linears[k] = LinearWeights(dev(q, torch.int8), dev(s), dev(l.b), float(act_scale(l.clip)),
+                                             float(act_mult(l.clip)))
+        self.struct = UNetWeights(self.in_w, self.in_b, self.pr_w, self.pr_b, self.out_w, self.out_b, len(blocks),
+                                  C.cast(self._blocks, C.POINTER(BlockWeights)), len(linears),
+                                  C.cast(self._linears, C.POINTER(LinearWeights)))
+
+
+class UNetRefiner(torch.nn.Module):
+    """Sparse3DUNet on the GPU in the deployed int8 arithmetic (see the module docstring)."""
+
+    def __init__(self, weights: UNetW, *, depth_resolution: float = 256.0, use_graph: bool = True,
+                 check_coords: bool = True):
+        super().__init__()
+        if any(f != 2 for f in weights.factors):
+            raise ValueError("downsample factors other than 2 are not supported (MoGe's refiners use 2)")
+        self.host_weights = weights
+        self.depth_resolution = float(depth_resolution)
+        self.use_graph = use_graph
+        self.check_coords = check_coords
+        self._weights: Dict[int, UNetDeviceWeights] = {}
+        self._ctx: Dict[tuple, int] = {}
+        self._io: Dict[tuple, dict] = {}
+
+    @classmethod
+    def from_state_dict(cls, sd, factors: Optional[Sequence[int]] = None, clips=None, **kw) -> "UNetRefiner":
+        """From a Sparse3DUNet (QAT) state dict (unet_weights.unet_from_state_dict)."""
+        return cls(unet_from_state_dict(sd, factors, clips), **kw)
+
+    @classmethod
+    def from_refiner_bin(cls, directory, **kw):
+        """From the Metal engine's refiner.bin / refiner.json (promptmoge/export/refiner.py:28-110). Returns
+        (module, uv_bias [C_L, R, C] or None): uv_bias is the encoder bias map of every frame of that grid."""
+        w, man, uv = load_refiner_bin(directory)
+        return cls(w, depth_resolution=float(man.get("depth_resolution", 256.0)), **kw), uv
+
+    def _config(self, B: int, H: int, W: int) -> UNetConfig:
+        w = self.host_weights
+        L = w.levels
+        pad = lambda xs: (_lib.i32 * 8)(*(list(xs) + [0] * (8 - len(xs))))
+        return UNetConfig(B, H, W, L, pad(w.channels), pad([len(s) for s in w.down]), pad([len(s) for s in w.dec]),
+                          len(w.bott), int(w.enc_channels), self.depth_resolution, int(self.use_graph))
+
+    def _handle(self, device: torch.device, B: int, H: int, W: int):
+        key = (device.index, B, H, W)
+        h = self._ctx.get(key)
+        if h is None:
+            dw = self._weights.get(device.index)
+            if dw is None:
+                dw = self._weights[device.index] = UNetDeviceWeights(self.host_weights, device)
+            cfg = self._config(B, H, W)
+            h = lib().pmg_unet_create(C.byref(cfg))
+            if not h:
+                raise _lib.PmgError(_lib.PMG_E_INVALID, lib().pmg_last_error().decode())
+            call("pmg_unet_set_weights", h, C.byref(dw.struct))
+            self._ctx[key] = h
+            M = B * H * W
+            w = self.host_weights
+            ds = 2 ** (w.levels - 1)
+            dev = torch.device("cuda", device.index)
+            self._io[key] = {
+                "feats": torch.empty((M, 3), dtype=torch.float32, device=dev),
+                "coords": torch.empty((M, 4), dtype=torch.int32, device=dev),
+                "prompt": torch.empty((M, 2), dtype=torch.float32, device=dev),
+                "enc": torch.empty((B, w.enc_channels, H // ds, W // ds), dtype=torch.float32, device=dev),
+                "bias": torch.empty((B, w.channels[-1], H // ds, W // ds), dtype=torch.float32, device=dev),
+                "out": torch.empty((M,), dtype=torch.float32, device=dev),
+            }
+        return h
+
+    def forward(self, feats: torch.Tensor, coords: Optional[torch.Tensor], shape, encoder_feature: torch.Tensor,
+                prompt_feats: Optional[torch.Tensor] = None,
+                encoder_bias_map: Optional[torch.Tensor] = None) -> torch.Tensor:
+        if torch.is_grad_enabled() and feats.requires_grad:
+            raise NotImplementedError("UNetRefiner is inference-only")
+        w = self.host_weights
+        B, H, W = int(shape[0]), int(shape[1]), int(shape[2])
+        M = B * H * W
+        ds = 2 ** (w.levels - 1)
+        if feats.shape != (M, 3) or not feats.is_cuda:
+            raise ValueError(f"feats must be a GPU tensor (M, 3) with M = B*H*W = {M} (level-0 voxels)")
+        # sparse_unet.py:185-187: the point map is encoder_downsample times the encoder grid
+        if encoder_feature.ndim != 4 or encoder_feature.shape[0] != B or encoder_feature.shape[1] != w.enc_channels \
+                or H != encoder_feature.shape[2] * ds or W != encoder_feature.shape[3] * ds:
+            raise ValueError(f"encoder_feature must be [B, {w.enc_channels}, H/{ds}, W/{ds}]")
+        if coords is not None:
+            coords = coords.to(torch.int32)
+            if coords.shape != (M, 4):
+                raise ValueError("coords must be (M, 4)")
+            if self.check_coords and not _is_raster(coords, B, H, W):
+                raise ValueError("coords are not level-0 raster order (one voxel per pixel, _voxelize)")
+        if prompt_feats is not None and prompt_feats.shape != (M, 2):
+            raise ValueError("prompt_feats must be (M, 2)")
+        if encoder_bias_map is not None and encoder_bias_map.shape != (B, w.channels[-1], H // ds, W // ds):
+            raise ValueError(f"encoder_bias_map must be [B, {w.channels[-1]}, H/{ds}, W/{ds}]")
+        h = self._handle(feats.device, B, H, W)
+        # inputs staged into the context's persistent buffers, so every call replays one captured graph
+        io = self._io[(feats.device.index, B, H, W)]
+        io["feats"].copy_(feats)
+        io["enc"].copy_(encoder_feature)
+        if coords is not None:
+            io["coords"].copy_(coords)
+        if prompt_feats is not None:
+            io["prompt"].copy_(prompt_feats)
+        if encoder_bias_map is not None:
+            io["bias"].copy_(encoder_bias_map)
+        p = lambda name, on: io[name].data_ptr() if on else None
+        call("pmg_unet_forward", h, io["feats"].data_ptr(), p("coords", coords is not None),
+             p("prompt", prompt_feats is not None), io["enc"].data_ptr(), p("bias", encoder_bias_map is not None),
+             io["out"].data_ptr(), C.c_void_p(torch.cuda.current_stream().cuda_stream))
+        return io["out"].clone().view(M, 1)
+
+    def buffer(self, which: str, level: int, shape=None) -> torch.Tensor:
+        """A copy of a device buffer of the last forward (parity tests): counts, coords, parent, nmap, tile_mask,
+        col_offsets, down, up, enc_tokens (see pmg_unet_buffer)."""
+        if len(self._ctx) != 1:
+            raise RuntimeError("buffer() needs exactly one context")
+        key, h = next(iter(self._ctx.items()))
+        B, H, W = key[1:]
+        w = self.host_weights
+        cap = B * H * W
+        ids = {"counts": (_lib.UNET_COUNTS, (w.levels,), torch.int64),
+               "coords": (_lib.UNET_COORDS, (cap, 4), torch.int32),
+               "parent": (_lib.UNET_PARENT, (cap,), torch.int32),
+               "nmap": (_lib.UNET_NMAP, (27, cap), torch.int32),
+               "tile_mask": (_lib.UNET_TILE_MASK, ((cap + 15) // 16,), torch.int32),
+               "down": (_lib.UNET_DOWN, (cap, w.channels[level]), torch.float32),
+               "up": (_lib.UNET_UP, (cap, w.channels[level]), torch.float32),
+               "enc_tokens": (_lib.UNET_ENC_TOKENS,
+                              (B * (H >> (w.levels - 1)) * (W >> (w.levels - 1)), w.channels[-1]), torch.float32)}
+        if which == "col_offsets":
+            n = B * -(-H // 2 ** level) * -(-W // 2 ** level) + 1
+            ids["col_offsets"] = (_lib.UNET_COL_OFFSETS, (n,), torch.int32)
+        bid, shp, dt = ids[which]
+        ptr = lib().pmg_unet_buffer(h, bid, level)
+        if not ptr:
+            raise ValueError(f"level {level} has no {which}")
+        out = torch.empty(shape or shp, dtype=dt, device=torch.device("cuda", key[0]))
+        from .refiner import _copy_device
+
+        _copy_device(out.data_ptr(), ptr, out.numel() * out.element_size(), torch.cuda.current_stream().cuda_stream)
+        return out
+
+    def close(self) -> None:
+        for h in self._ctx.values():
+            lib().pmg_unet_destroy(h)
+        self._ctx.clear()
+        self._io.clear()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # interpreter shutdown: the library handle may already be gone
+            pass
+
+
+def _is_raster(coords: torch.Tensor, B: int, H: int, W: int) -> bool:
+    """coords[:, :3] == (b, i, j) in raster order, the test of _is_one_voxel_per_column (_core.py:249-266)."""
+    m = torch.arange(B * H * W, device=coords.device, dtype=torch.int32)
+    ref = torch.stack([m // (H * W), (m // W) % H, m % W], dim=1)
+    return bool(torch.equal(coords[:, :3], ref))

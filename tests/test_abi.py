@@ -168,3 +168,23 @@ def test_fit_spin_limit_hook_round_trips(libpmg):
     assert prev == 1 << 23
     assert libpmg.pmg_debug_fit_spin_limit(0) == 7
     assert libpmg.pmg_debug_fit_spin_limit(0) == 1 << 23
+
+
+def test_unet_create_rejects_bad_config(libpmg):
+    """pmg_unet_create validates on the host, before any allocation (sparse_unet.py:52, 187 and the kernels'
+    widths)."""
+    def cfg(**kw):
+        d = dict(B=1, H=64, W=96, levels=3, channels=[16, 32, 32], enc_blocks=[1, 1, 1], dec_blocks=[1, 1], bott=1,
+                 enc=32)
+        d.update(kw)
+        pad = lambda xs: (C.c_int * 8)(*(list(xs) + [0] * (8 - len(xs))))
+        return _lib.UNetConfig(d["B"], d["H"], d["W"], d["levels"], pad(d["channels"]), pad(d["enc_blocks"]),
+                               pad(d["dec_blocks"]), d["bott"], d["enc"], 256.0, 1)
+    for bad, msg in [(dict(levels=1), b"levels"), (dict(H=62), b"multiples"), (dict(channels=[24, 32, 32]), b"level-0"),
+                     (dict(channels=[16, 40, 32]), b"widths"), (dict(dec_blocks=[1, 0]), b"last up stage"),
+                     (dict(enc=20), b"enc_channels")]:
+        c = cfg(**bad)
+        assert not libpmg.pmg_unet_create(C.byref(c)), bad
+        assert msg in libpmg.pmg_last_error(), (bad, libpmg.pmg_last_error())
+    assert libpmg.pmg_unet_forward(None, None, None, None, None, None, None, None) == _lib.PMG_E_INVALID
+    assert libpmg.pmg_unet_buffer(None, 0, 0) is None and libpmg.pmg_unet_capacity(None) == 0
