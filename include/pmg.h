@@ -276,6 +276,13 @@ int pmg_fit_final(const float* logz, int64_t stride, const float* lidar, const f
                   int B, int H, int W, int dh, int dw, int iters, float trim, int min_points, float* st, int32_t* info,
                   void* workspace, size_t workspace_bytes, void* stream);
 
+/* pmg_post_depth -- the metric depth after the final fit (post_depth, MetricFit.metal:200-211; v3.py:776):
+ * depth[b,i,j] = s[b] * exp(logz[b,i,j]) + t[b] in fp32, +inf where mask[b,i,j] == 0 (mask [B][H][W] uint8, the
+ * model's mask, or NULL: all pixels) or where that depth is not > 0. logz with element stride `stride` (3 for the
+ * point map); st [B][2] (the final fit's output, read on the device); depth [B][H][W] fp32. */
+int pmg_post_depth(const float* logz, int64_t stride, const uint8_t* mask, int B, int H, int W, const float* st,
+                   float* depth, void* stream);
+
 /* ------------------------------------------------------------------------------------------------------------ *
  * (5) LiDAR prompt fill.
  *

@@ -15,7 +15,7 @@ from __future__ import annotations
 import numpy as np
 
 from .conv import conv_acc_int, conv_float, dequant, epilogue_q, epilogue_r
-from .numerics import F32, ln_silu, quad_sum, quant_i8
+from .numerics import F32, ln_silu, quad_sum, quant_i8, rowwise
 
 
 # ------------------------------------------------------------------------------------------------- int8 contract
@@ -138,11 +138,12 @@ def resblock(x, nmap, blk, mode: str, trace=None, record=None, path=None):
     if mode == "int8":
         q_w1, s_w1 = quantize_weight(blk.w1)
         q_w2, s_w2 = quantize_weight(blk.w2)
-        q1 = quant_i8(ln_silu(x, blk.gamma, blk.beta), act_mult(blk.clip1))
+        x = np.asarray(x, np.float32)
+        q1 = rowwise(lambda xb: quant_i8(ln_silu(xb, blk.gamma, blk.beta), act_mult(blk.clip1)), x)
         acc1 = conv_acc_int(q1, nmap, q_w1)
-        q2 = epilogue_q(acc1, act_scale(blk.clip1), s_w1, blk.b1, act_mult(blk.clip2))
+        q2 = rowwise(lambda ab: epilogue_q(ab, act_scale(blk.clip1), s_w1, blk.b1, act_mult(blk.clip2)), acc1)
         acc2 = conv_acc_int(q2, nmap, q_w2)
-        out = epilogue_r(acc2, act_scale(blk.clip2), s_w2, blk.b2, x)
+        out = rowwise(lambda ab, xb: epilogue_r(ab, act_scale(blk.clip2), s_w2, blk.b2, xb), acc2, x)
         if trace is not None:
             trace.append(dict(q1=q1, acc1=acc1, q2=q2, acc2=acc2, x=out))
         return out

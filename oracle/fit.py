@@ -136,3 +136,18 @@ def final_inputs(points, lidar, conf, mask_binary=None):
     if mask_binary is not None:
         mask &= area_pool(np.asarray(mask_binary, dtype=np.float32), dh, dw) > F32(0.99)
     return z.reshape(B, -1), lidar.reshape(B, -1), mask.reshape(B, -1)
+
+
+def post_depth(points, st, mask=None):
+    """post_depth (MetricFit.metal:200-211; v3.py:776): d = s * exp(logz) + t in fp32 per frame; +inf where the mask
+    is false or d <= 0. points [B, H, W, 3], st (s [B], t [B]), mask [B, H, W] or None."""
+    from .numerics import exp_f32
+
+    logz = np.asarray(points, np.float32)[..., 2]
+    s = np.asarray(st[0], np.float32).reshape(-1, 1, 1)
+    t = np.asarray(st[1], np.float32).reshape(-1, 1, 1)
+    d = (s * exp_f32(logz) + t).astype(np.float32)
+    ok = d > 0
+    if mask is not None:
+        ok &= np.asarray(mask, bool)
+    return np.where(ok, d, np.float32(np.inf)).astype(np.float32)

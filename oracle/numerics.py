@@ -23,6 +23,44 @@ C3, C5, C7, C9 = _f(0x3EAAAAAB), _f(0x3E4CCCCD), _f(0x3E124925), _f(0x3DE38E39)
 SQRT2 = _f(0x3FB504F3)
 
 
+_BLOCK = 1 << 16
+
+
+def _blocked(fn):
+    """Evaluates an elementwise function in blocks of 65536 elements (each block's many passes stay in cache); the
+    result is the same, element by element."""
+    def run(x):
+        x = np.asarray(x, dtype=np.float32)
+        if x.size <= _BLOCK:
+            return fn(x)
+        flat = np.ascontiguousarray(x).reshape(-1)
+        out = np.empty_like(flat)
+        for i in range(0, flat.size, _BLOCK):
+            out[i:i + _BLOCK] = fn(flat[i:i + _BLOCK])
+        return out.reshape(x.shape)
+
+    run.__doc__ = fn.__doc__
+    run.__name__ = fn.__name__
+    return run
+
+
+def rowwise(fn, *arrays, block: int = 8192):
+    """fn(*row_blocks) over blocks of `block` rows of arrays sharing their first dimension (None passes through),
+    on a few threads, results concatenated: for row-independent fn the result of fn(*arrays), element by element."""
+    import concurrent.futures as cf
+    import os
+
+    n = next(a.shape[0] for a in arrays if a is not None)
+    if n <= block:
+        return fn(*arrays)
+    starts = list(range(0, n, block))
+    part = lambda r0: fn(*[a if a is None else a[r0:r0 + block] for a in arrays])
+    with cf.ThreadPoolExecutor(max(1, min(8, os.cpu_count() or 1))) as ex:
+        outs = list(ex.map(part, starts))
+    return np.concatenate(outs)
+
+
+@_blocked
 def exp_f32(x) -> np.ndarray:
     """Cody-Waite reduction, degree-7 Horner polynomial, exponent-field scaling (pmg_math.h exp_f32)."""
     x = np.asarray(x, dtype=np.float32)
@@ -43,6 +81,7 @@ def exp_f32(x) -> np.ndarray:
     return out.astype(np.float32)
 
 
+@_blocked
 def log_f32(x) -> np.ndarray:
     """log(x) = e*ln2 + 2 atanh((m-1)/(m+1)) for positive normal x (pmg_math.h log_f32)."""
     x = np.asarray(x, dtype=np.float32)

@@ -27,7 +27,7 @@ from .blocks import (act_mult, act_scale, fake_quant, input_proj, layer_norm, ou
                      resblock, silu)
 from .conv import conv_float
 from .fit import final_inputs, fit_f64, prompt_inputs
-from .numerics import F32, ln_silu, log_f32
+from .numerics import F32, ln_silu, log_f32, rowwise
 from .structure import nmap_column, voxelize
 
 
@@ -60,10 +60,10 @@ def blocks_fp16(x, nmap, w, trace=None):
     from .numerics import silu_f32
 
     for blk in w.blocks:
-        h1 = ln_silu(x, blk.gamma, blk.beta).astype(np.float16)
+        h1 = rowwise(lambda xb: ln_silu(xb, blk.gamma, blk.beta).astype(np.float16), x)
         y1 = conv_float(h1.astype(np.float64), nmap, np.asarray(blk.w1, np.float16).astype(np.float64),
                         dtype=np.float64).astype(np.float32)
-        h2 = silu_f32(y1 + np.asarray(blk.b1, np.float32)).astype(np.float16)
+        h2 = rowwise(lambda yb: silu_f32(yb + np.asarray(blk.b1, np.float32)).astype(np.float16), y1)
         y2 = conv_float(h2.astype(np.float64), nmap, np.asarray(blk.w2, np.float16).astype(np.float64),
                         dtype=np.float64).astype(np.float32)
         x = (y2 + np.asarray(blk.b2, np.float32)) + x

@@ -113,6 +113,7 @@ SIGNATURES = {
     "pmg_fit_scale_shift": (i32, [vp, vp, vp, i32, i64, i32, f32, i32, vp, vp, vp, sz, vp]),
     "pmg_fit_prompt": (i32, [vp, i64, vp, vp, i32, i32, i32, i32, i32, i32, f32, i32, vp, vp, vp, sz, vp]),
     "pmg_fit_final_workspace_bytes": (sz, [i32, i32, i32, i32]),
+    "pmg_post_depth": (i32, [vp, i64, vp, i32, i32, i32, vp, vp, vp]),
     "pmg_fit_final": (i32, [vp, i64, vp, vp, vp, i32, i32, i32, i32, i32, i32, f32, i32, vp, vp, vp, sz, vp]),
     "pmg_nearest_fill_workspace_bytes": (sz, [i32, i32, i32]),
     "pmg_nearest_fill": (i32, [vp, vp, i32, i32, i32, vp, vp, vp, vp, sz, vp]),

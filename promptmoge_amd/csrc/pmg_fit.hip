@@ -921,6 +921,19 @@ __global__ __launch_bounds__(256) void final_inputs_k(const float* __restrict__ 
     m_out[q] = m ? 1 : 0;
 }
 
+// post_depth (MetricFit.metal:200-211; v3.py:776 depth = s * z + t): the metric depth of every pixel from the refined
+// log depth and the final fit of its frame, d = s * exp(logz) + t in fp32; +inf where the mask is 0 or d <= 0.
+__global__ __launch_bounds__(256) void post_depth_k(const float* __restrict__ logz, int64_t stride,
+                                                    const uint8_t* __restrict__ mask, int64_t HW, int64_t n,
+                                                    const float* __restrict__ st, float* __restrict__ depth) {
+    const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (p >= n) return;
+    const int64_t b = p / HW;
+    const float d = st[2 * b] * exp_f32(logz[p * stride]) + st[2 * b + 1];
+    const bool ok = (mask == nullptr || mask[p] != 0) && d > 0.0f;
+    depth[p] = ok ? d : __builtin_inff();
+}
+
 size_t final_fit_workspace_bytes(int B, int dh, int dw, int iters) {
     const size_t n = (size_t)B * dh * dw;
     return align256(fit_workspace_bytes((int64_t)dh * dw, iters)) + align256(n * sizeof(float)) + align256(n);
@@ -1089,6 +1102,16 @@ int pmg_fit_prompt(const float* logz, int64_t stride, const float* lidar, const 
     f.workspace = workspace;
     f.workspace_bytes = workspace_bytes;
     return launch_fit(f, (hipStream_t)stream);
+}
+
+int pmg_post_depth(const float* logz, int64_t stride, const uint8_t* mask, int B, int H, int W, const float* st,
+                   float* depth, void* stream) {
+    PMG_REQUIRE(logz && st && depth, "null buffer");
+    PMG_REQUIRE(B >= 1 && H >= 1 && W >= 1 && stride >= 1, "bad shape");
+    const int64_t HW = (int64_t)H * W, n = (int64_t)B * HW;
+    hipLaunchKernelGGL(post_depth_k, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, logz,
+                       stride, mask, HW, n, st, depth);
+    return check_launch("post_depth_k");
 }
 
 int pmg_fit_final(const float* logz, int64_t stride, const float* lidar, const float* conf, const uint8_t* mask_binary,

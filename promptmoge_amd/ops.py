@@ -17,6 +17,7 @@ __all__ = [
     "voxelize", "nmap_column", "nmap_hash", "row_order", "nmap_from_rows", "kmap_compact", "spconv_i8",
     "spconv_i8_ordered", "spconv_f16",
     "spconv_f32", "spconv_col", "ln_silu_quant", "ln_silu_f16", "fit_scale_shift", "fit_prompt", "fit_final",
+    "post_depth",
     "math_device", "gauge_poly",
     "nearest_fill",
     "EPI_ACC", "EPI_Q", "EPI_R", "EPI_BIAS", "EPI_SILU", "EPI_RLN", "EPI_ROUT", "EPI_QLIN",
@@ -411,6 +412,27 @@ def fit_final(points: torch.Tensor, lidar: torch.Tensor, conf: torch.Tensor, mas
     if return_info:
         return st[:, 0], st[:, 1], info
     return st[:, 0], st[:, 1]
+
+def post_depth(points: torch.Tensor, st: torch.Tensor, mask: Optional[torch.Tensor] = None,
+               out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """post_depth (MetricFit.metal:200-211; v3.py:776): metric depth s * exp(logz) + t of the point map
+    [B, H, W, 3] with the per-frame final fit st [B, 2] (read on the device, no synchronisation); +inf where mask
+    [B, H, W] (bool / uint8, optional) is false or the depth is not positive. Returns [B, H, W] fp32."""
+    points = _dev(points, "points", torch.float32)
+    st = _dev(st.float().contiguous(), "st")
+    B, H, W, _ = points.shape
+    if st.shape != (B, 2):
+        raise ValueError("st must be [B, 2]")
+    m8 = None
+    if mask is not None:
+        m8 = _dev(mask.to(torch.uint8).contiguous(), "mask")
+        if m8.numel() != B * H * W:
+            raise ValueError("mask must be [B, H, W]")
+    if out is None:
+        out = torch.empty((B, H, W), dtype=torch.float32, device=points.device)
+    call("pmg_post_depth", points.data_ptr() + 8, 3, _p(m8), B, H, W, _p(st), _p(out), _stream())
+    return out
+
 
 def nearest_fill(depth: torch.Tensor, conf: Optional[torch.Tensor] = None, *, return_index: bool = False,
                  out: Optional[Tuple[torch.Tensor, Optional[torch.Tensor]]] = None):

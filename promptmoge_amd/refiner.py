@@ -67,16 +67,23 @@ class RefinerStep:
     points [B, H, W, 3] fp32 (x/z, y/z, logz) is refined into `out` (default in place); lidar, conf [B, dh, dw].
     Returns the prompt fit (s, t) [B, 2] and, if `final_fit`, the metric fit of the refined depth [B, 2].
     `output_gate` / `output_gate_floor` and `anchor` are the refine loop's lidar_prompt options 'output_gate',
-    'output_gate_floor' and 'anchor' (v3.py:40-41, 565-573).
+    'output_gate_floor' and 'anchor' (v3.py:40-41, 565-573). With `post_depth` (and `final_fit`) every call also
+    writes the metric depth s * exp(logz) + t of the refined map into `self.depth` [B, H, W] (+inf where not > 0;
+    MetricFit.metal:200-211).
     """
 
     def __init__(self, weights: RefinerW, B: int, H: int, W: int, dh: Optional[int] = None,
                  dw: Optional[int] = None, *, precision: str = "int8", depth_resolution: float = 256.0,
                  fit_iters: int = 4, fit_trim: float = 0.2, fit_min_points: int = 32, use_prompt: bool = True,
                  soft_gate: bool = False, final_fit: bool = False, use_graph: bool = True,
-                 output_gate: bool = False, output_gate_floor: float = 0.1, anchor: float = 0.0, device="cuda"):
+                 output_gate: bool = False, output_gate_floor: float = 0.1, anchor: float = 0.0,
+                 post_depth: bool = False, device="cuda"):
         if precision not in ("int8", "fp16"):
             raise ValueError("precision must be 'int8' or 'fp16'")
+        if post_depth and not final_fit:
+            raise ValueError("post_depth needs final_fit")
+        self.post_depth = post_depth
+        self.depth = torch.empty((B, H, W), dtype=torch.float32, device=device) if post_depth else None
         self.B, self.H, self.W = B, H, W
         self.dh, self.dw = dh or H, dw or W
         self.final_fit = final_fit
@@ -119,6 +126,9 @@ class RefinerStep:
         stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
         call("pmg_refiner_step", self._h, points.data_ptr(), out.data_ptr(), lidar.data_ptr(), conf.data_ptr(),
              self.st_prompt.data_ptr(), self.st_final.data_ptr() if self.final_fit else None, stream)
+        if self.post_depth:  # the metric depth of the refined map, MetricFit.metal:200-211 (self.depth)
+            call("pmg_post_depth", out.data_ptr() + 8, 3, None, self.B, self.H, self.W, self.st_final.data_ptr(),
+                 self.depth.data_ptr(), stream)
         return self.st_prompt, (self.st_final if self.final_fit else None)
 
     def check(self) -> None:

@@ -120,11 +120,12 @@ def nearest_fill(depth: np.ndarray, conf: np.ndarray):
     return depth[tuple(idx)], np.where(valid, conf, 1).astype(conf.dtype)
 
 
-def make_scene(cfg: StepConfig, seed: Optional[int] = None) -> Scene:
+def make_scene(cfg: StepConfig, seed: Optional[int] = None, fill: bool = True) -> Scene:
     """Ray-cast piecewise-planar room (6-10 planes, depth clipped to [0.5, 6] m) plus sigma = 5 mm Gaussian noise:
     that depth map is the LiDAR prompt (same resolution, 3 % gross outliers, i.i.d. confidence in {0, 1, 2} with
     P = (0.1, 0.2, 0.7)) and, mapped into an affine frame (depth ~= 1.3 * exp(logz) + 0.05), the network's point
-    map (x/z, y/z, logz) that the refiner voxelises."""
+    map (x/z, y/z, logz) that the refiner voxelises. With holes (config H) the LiDAR is nearest-filled here unless
+    fill=False, which returns it with the holes at 0 (for a device-side fill)."""
     rng = np.random.default_rng(cfg.seed if seed is None else seed)
     H, W = cfg.H, cfg.W
     dx = (np.arange(W) - cfg.cx) / cfg.fx
@@ -141,7 +142,8 @@ def make_scene(cfg: StepConfig, seed: Optional[int] = None) -> Scene:
     if cfg.holes > 0:
         hole = rng.random(D.shape) < cfg.holes
         lidar = np.where(hole, 0.0, lidar)
-        lidar, conf = nearest_fill(lidar, conf)
+        if fill:
+            lidar, conf = nearest_fill(lidar, conf)
     d_net = (D_obs - T0) / S0
     points = np.stack(
         [np.broadcast_to(dx[None, :], (H, W)), np.broadcast_to(dy[:, None], (H, W)), np.log(d_net)], axis=-1

@@ -578,3 +578,29 @@ def test_conv_col_f16(gpu, C):
     assert (np.abs(got - ref) <= bound + 1e-6).all()
     h = ops.spconv_col(_t(x, gpu), zq, _t(w, gpu), ops.EPI_Q, bias=_t(b, gpu)).cpu().numpy()
     assert np.array_equal(h.view(np.uint16), onm.silu_f32((got + b).astype(np.float32)).astype(np.float16).view(np.uint16))
+
+
+def test_post_depth_after_final_fit(gpu):
+    """post_depth (MetricFit.metal:200-211) on the device's final fit: bit-exact against the oracle given the same
+    (s, t), +inf off the mask; and the fused step's post_depth option writes the same map."""
+    from oracle.fit import post_depth as o_post_depth
+    from promptmoge_amd.refiner import RefinerStep
+
+    announce("post_depth after the final fit, config B")
+    cfg, sc = _scene("B")
+    pts = np.stack([sc.points, sc.points * np.float32(1.01)])
+    lid, cnf = np.stack([sc.lidar, sc.lidar]), np.stack([sc.conf, sc.conf])
+    mask = np.random.default_rng(3).random(pts.shape[:3]) < 0.9
+    P = _t(pts, gpu)
+    s, t = ops.fit_final(P, _t(lid, gpu), _t(cnf, gpu), iters=10)
+    st = torch.stack([s, t], 1)
+    d = ops.post_depth(P, st, _t(mask, gpu)).cpu().numpy()
+    st_h = st.cpu().numpy()
+    ref = o_post_depth(pts, (st_h[:, 0], st_h[:, 1]), mask)
+    assert np.array_equal(d, ref) and np.isinf(d[~mask]).all()
+    w = spec.refiner_for(cfg, sc)
+    step = RefinerStep(w, 1, cfg.H, cfg.W, fit_iters=10, final_fit=True, post_depth=True)
+    Q = _t(sc.points[None], gpu)
+    _, fin = step(Q, _t(sc.lidar[None], gpu), _t(sc.conf[None], gpu))
+    fh = fin.cpu().numpy()
+    assert np.array_equal(step.depth.cpu().numpy(), o_post_depth(Q.cpu().numpy(), (fh[:, 0], fh[:, 1])))

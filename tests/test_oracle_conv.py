@@ -51,3 +51,20 @@ def test_epilogues_closed_form():
     silu = lambda v: v / (1 + np.exp(-v))
     expect = [int(np.clip(np.rint(silu(float(v)) * 8.0), -127, 127)) for v in y[0]]
     assert q.tolist()[0] == expect  # 12.5 -> 99.99..; -11.5 -> ~0; -2 -> -1.9 -> -2 (=-0.238/0.125); saturates
+
+
+def test_conv_on_a_subset_of_rows():
+    """A map of some rows (the sampled-row checks of large sets) gathers from all of x: the result is those rows
+    of the full convolution, for the generic and the column-stencil map, integer and float."""
+    rng = np.random.default_rng(4)
+    z = rng.integers(0, 4, size=(1, 12, 14))
+    nm = st.nmap_column(z)
+    x = rng.integers(-127, 128, size=(nm.shape[0], 32)).astype(np.int8)
+    w = rng.integers(-127, 128, size=(16, 3, 3, 3, 32)).astype(np.int8)
+    rows = np.sort(rng.choice(nm.shape[0], 40, replace=False))
+    full = cv.conv_acc_int(x, nm, w)
+    assert np.array_equal(cv.conv_acc_int(x, nm[rows], w), full[rows])
+    f = cv.conv_float(x.astype(np.float64), nm, w.astype(np.float64), dtype=np.float64)
+    assert np.array_equal(cv.conv_float(x.astype(np.float64), nm[rows], w.astype(np.float64), dtype=np.float64),
+                          f[rows])
+    assert np.array_equal(f, full.astype(np.float64))

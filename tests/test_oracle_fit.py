@@ -98,3 +98,21 @@ def test_final_inputs_mask_rules():
     mb = np.ones((1, H, W), bool)
     mb[0, 0, 0] = False                              # 8/9 of the first 3x3 window: 0.889 <= 0.99
     assert fit.final_inputs(pts, lidar, conf, mb)[2].tolist() == [[False, False, False, False]]
+
+
+def test_post_depth_closed_forms():
+    """post_depth (MetricFit.metal:200-211): s = 1, t = 0 gives exp(logz); a shift that makes the depth <= 0 and a
+    false mask give +inf; two frames use their own (s, t)."""
+    from oracle.fit import post_depth
+    from oracle.numerics import exp_f32
+
+    rng = np.random.default_rng(0)
+    pts = rng.normal(0, 0.5, (2, 5, 7, 3)).astype(np.float32)
+    d = post_depth(pts, ([1.0, 2.0], [0.0, -1.0]))
+    assert np.array_equal(d[0], exp_f32(pts[0, ..., 2]))
+    e = np.float32(2.0) * exp_f32(pts[1, ..., 2]) - np.float32(1.0)
+    assert np.array_equal(d[1], np.where(e > 0, e, np.inf).astype(np.float32))
+    assert np.isinf(d[1]).any() and np.isfinite(d[1]).any()
+    mask = rng.random((2, 5, 7)) < 0.5
+    dm = post_depth(pts, ([1.0, 2.0], [0.0, -1.0]), mask)
+    assert np.isinf(dm[~mask]).all() and np.array_equal(dm[mask], d[mask])
