@@ -284,16 +284,22 @@ __global__ __launch_bounds__(kColThreads) void spconv_col_k(ColConvArgs a) {
         }
     };
 
-    const int nseg = (M + kSeg - 1) / kSeg;
-    int seg = blockIdx.x;
+    // XCD-aware segment order (as spconv_colv_k): one contiguous band of segments per XCD (block b runs on XCD
+    // b % 8), dealt round-robin to that XCD's blocks, so the image rows a band's windows share stay in its L2.
+    const int nx = gridDim.x < 8 ? (int)gridDim.x : 8;
+    const int xcd = (int)blockIdx.x % nx, ib = (int)blockIdx.x / nx;
+    const int nbx = ((int)gridDim.x - xcd + nx - 1) / nx;
+    const int nseg_all = (M + kSeg - 1) / kSeg;
+    const int nseg = (int)((int64_t)nseg_all * (xcd + 1) / nx);  // end of this XCD's band
+    int seg = (int)((int64_t)nseg_all * xcd / nx) + ib;
     if (seg < nseg) {
         fetch(seg);
         commit(0);
     }
-    for (int it = 0; seg < nseg; seg += gridDim.x, ++it) {
+    for (int it = 0; seg < nseg; seg += nbx, ++it) {
         const int buf = NBUF == 2 ? (it & 1) : 0;
         const int s0 = seg * kSeg;
-        const int nxt = seg + gridDim.x;
+        const int nxt = seg + nbx;
         __syncthreads();  // window `buf` (and the weights) visible to all waves
         if constexpr (NBUF == 2) {
             if (nxt < nseg) fetch(nxt);  // in flight during this segment's compute (issued after the barrier,
@@ -637,13 +643,21 @@ __global__ __launch_bounds__(128 * WG, 1) void spconv_colv_k(ColConvArgs a) {
     const lds_int* zcb = (lds_int*)zbuf + lr0 + kWin + 1;
     const lds_u8* wb = (lds_u8*)s_w + lane * 16;
 
-    // this group's segments: first, first + stride, ...; group 0 has at least as many as group 1
+    // this group's segments: first, first + stride, ...; group 0 has at least as many as group 1. XCD-aware: block
+    // b runs on XCD b % 8 (workgroups are dispatched round-robin over the XCDs), and the segments -- consecutive
+    // pixels in raster order -- are split into one contiguous band per XCD, dealt round-robin to that XCD's groups.
+    // A segment's window reads the image rows above and below it too, i.e. rows of neighbouring segments of the
+    // same band, so each row comes from HBM about once into its XCD's L2 instead of once per XCD that reads it.
     const int nseg = (M + kSeg - 1) / kSeg;
-    const int stride = 2 * (int)gridDim.x;
-    const int first = 2 * (int)blockIdx.x + grp;
-    const int nk = first < nseg ? (nseg - 1 - first) / stride + 1 : 0;
-    const int first0 = 2 * (int)blockIdx.x;
-    const int nk0 = first0 < nseg ? (nseg - 1 - first0) / stride + 1 : 0;
+    const int nx = gridDim.x < 8 ? (int)gridDim.x : 8;
+    const int xcd = (int)blockIdx.x % nx, ib = (int)blockIdx.x / nx;
+    const int nbx = ((int)gridDim.x - xcd + nx - 1) / nx;  // blocks on this XCD
+    const int seg_lo = (int)((int64_t)nseg * xcd / nx), seg_hi = (int)((int64_t)nseg * (xcd + 1) / nx);
+    const int stride = 2 * nbx;
+    const int first = seg_lo + 2 * ib + grp;
+    const int nk = first < seg_hi ? (seg_hi - 1 - first) / stride + 1 : 0;
+    const int first0 = seg_lo + 2 * ib;
+    const int nk0 = first0 < seg_hi ? (seg_hi - 1 - first0) / stride + 1 : 0;
 
     if (nk > 0) fetch(first);
 #pragma unroll
