@@ -406,27 +406,44 @@ def gauge_bench(stream):
             "ms": round(ms, 4)}
 
 
-def cpu_baseline(env):
-    from oracle import refiner as orf
-
+def _cpu_model() -> str:
     try:
-        from threadpoolctl import threadpool_info
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
-        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
-    except Exception:
-        threads = os.cpu_count() or 1
+
+def cpu_baseline(env):
+    """The reference's CPU path (the _fallback flex_gemm ops, QAT fake quantisation, kthvalue fit) restated op for op
+    in torch (oracle/torch_port.py), on all the host's cores: 1 warm-up, median of 5 steps of the workload."""
+    import torch
+
+    from oracle import torch_port
+
     cfg, sc, w = env["cfg"], env["sc"], env["w"]
-    run = lambda: orf.step_fakequant(sc.points[None], sc.lidar[None], sc.conf[None], w, iters=cfg.fit_iters)
-    run()
-    ts = []
-    for _ in range(5):
-        t0 = time.perf_counter()
+    nproc = os.cpu_count() or 1
+    prev = torch.get_num_threads()
+    torch.set_num_threads(nproc)
+    try:
+        run = lambda: torch_port.step(sc.points[None], sc.lidar[None], sc.conf[None], w, iters=cfg.fit_iters)
         run()
-        ts.append(time.perf_counter() - t0)
+        ts = []
+        for _ in range(5):
+            t0 = time.perf_counter()
+            run()
+            ts.append(time.perf_counter() - t0)
+        threads = torch.get_num_threads()
+    finally:
+        torch.set_num_threads(prev)
     tc = statistics.median(ts)
     return {"value": round(cfg.M / tc, 1), "unit": "voxels/s", "cores": int(threads), "kind": "port",
-            "sample": f"1 warm-up + median of 5 steps of config {cfg.name} ({cfg.M} voxels each), NumPy restatement "
-                      f"of the _fallback path (BLAS {threads} threads, elementwise work 1 thread)",
+            "nproc": nproc, "threads": int(threads), "cpu_model": _cpu_model(),
+            "sample": f"1 warm-up + median of 5 steps of config {cfg.name} ({cfg.M} voxels each): the reference's "
+                      f"_fallback path restated op for op in torch on the CPU (per-tap index_select / mm / "
+                      f"index_add_, QAT fake quantisation, kthvalue fit), torch.set_num_threads({nproc})",
             "ms_per_step": round(tc * 1e3, 1)}
 
 

@@ -221,3 +221,17 @@ def test_zero_out_proj_adds_its_bias():
     pts, _, _ = rf.step(sc.points[None], sc.lidar[None], sc.conf[None], wz, precision="int8", iters=4)
     assert np.array_equal(pts[..., 2], sc.points[None, ..., 2] + np.float32(0.125))
     assert np.array_equal(pts[..., :2], sc.points[None, ..., :2])
+
+
+def test_torch_cpu_port_matches_fakequant_oracle():
+    """The CPU baseline (oracle/torch_port.py: the _fallback path in torch) computes the oracle's fake-quant step:
+    the same model in another fp32 order, so the same statistical bounds as the int8 comparison above."""
+    from oracle import torch_port
+
+    sc, w = _small("int8", 16, 3)
+    got = torch_port.step(sc.points[None], sc.lidar[None], sc.conf[None], w, iters=10)
+    ref = rf.step_fakequant(sc.points[None], sc.lidar[None], sc.conf[None], w, iters=10)
+    d, dr = np.exp(got[..., 2].astype(np.float64)), np.exp(ref[..., 2].astype(np.float64))
+    rel = np.abs(d - dr) / dr
+    assert np.median(rel) < 1e-6 and rel.mean() < 1e-4 and (rel > 1e-3).mean() < 5e-3, (rel.mean(), rel.max())
+    assert np.abs(got[..., 2] - sc.points[None, ..., 2]).mean() > 1e-3
