@@ -288,6 +288,89 @@ def microbench(stream):
     return micro
 
 
+def fit_trace(args):
+    """The metric fit's own per-round record: block 0 of fit_k writes, into the workspace header, the wall clock
+    (100 MHz) at the launch, after the first solve and after every trim round, with the round's selection path
+    (0 bracket, 1 bracket missed -> radix, 2 radix, 3 radix + third pass), its candidate count, and the number of
+    rounds run (the loop stops at a fixed point). Prints one line per round for the prompt fit and the final fit of
+    the configuration (the last of 20 runs each)."""
+    import numpy as np
+    import torch
+
+    from promptmoge_amd import ops
+
+    env = setup(args.config)
+    cfg = env["cfg"]
+    P, L, Cf = env["P"], env["L"], env["Cf"]
+    names = {0: "bracket", 1: "bracket missed -> radix", 2: "radix", 3: "radix + third pass"}
+    with torch.cuda.stream(env["stream"]):
+        for name, run in (("prompt fit", lambda: ops.fit_prompt(P, L, Cf, iters=cfg.fit_iters)),
+                          ("final fit", lambda: ops.fit_final(P, L, Cf, iters=cfg.fit_iters))):
+            for _ in range(20):
+                run()
+            torch.cuda.synchronize()
+            ws = next(iter(ops._FIT_WS.values()))
+            tr = ws[128:128 + 4096].cpu().numpy().view(np.uint32)
+            t0, t1 = int(tr[129]), int(tr[128])
+            print(f"# {name}, config {cfg.name} ({cfg.H}x{cfg.W}, iters {cfg.fit_iters}); times in us from the launch")
+            print(f"load + first solve {((t1 - t0) & 0xffffffff) / 100.0:8.2f}")
+            prev = t1
+            for it in range(int(tr[130])):
+                t = int(tr[2 * it + 1])
+                dt = ((t - prev) & 0xffffffff) / 100.0
+                print(f"round {it:2d} {dt:8.2f}  path {names.get(int(tr[2 * it]) & 15, '?'):24s} "
+                      f"candidates {int(tr[2 * it]) >> 4}")
+                prev = t
+            print(f"total (block 0) {((prev - t0) & 0xffffffff) / 100.0:8.2f}", flush=True)
+    return 0
+
+
+def unet_bench(stream, reps=20):
+    """The multi-level int8 refiner (UNetRefiner, pmg_unet_*) at Model A's size: a 5-level Sparse3DUNet with
+    channels [32, 64, 128, 256, 256], one block per stage, encoder 1024 channels on the 30 x 40 token grid, prompt
+    features and encoder bias map; one forward = level structure + maps + all layers (one captured graph)."""
+    import numpy as np
+    import torch
+
+    from promptmoge_amd import spec
+    from promptmoge_amd import unet_weights as uw
+    from promptmoge_amd.unet import UNetRefiner
+
+    cfg = spec.CONFIGS["A"]
+    sc = spec.make_scene(cfg)
+    H, W = cfg.H, cfg.W
+    w = uw.make_unet_weights([32, 64, 128, 256, 256], 1024, seed=1)
+    for layer in w.quantised_layers().values():  # clips of the right scale for these weights (timing only)
+        if hasattr(layer, "clip1"):
+            layer.clip1, layer.clip2 = 3.0, 2.0
+        else:
+            layer.clip = 3.0
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(0)
+    M = H * W
+    with torch.cuda.stream(stream):
+        feats = torch.from_numpy(sc.points.reshape(M, 3).copy()).to(dev)
+        enc = torch.from_numpy(rng.normal(0, 1, (1, 1024, H // 16, W // 16)).astype(np.float32)).to(dev)
+        bias = torch.from_numpy(rng.normal(0, 0.1, (1, 256, H // 16, W // 16)).astype(np.float32)).to(dev)
+        pf = torch.from_numpy(np.stack([rng.normal(0, 0.05, M), rng.uniform(0, 1, M)], 1).astype(np.float32)).to(dev)
+        mod = UNetRefiner(w)
+        shape = torch.Size([1, H, W, 1024, 3])
+        for _ in range(3):
+            mod(feats, None, shape, enc, prompt_feats=pf, encoder_bias_map=bias)
+        torch.cuda.synchronize()
+        counts = [int(c) for c in mod.buffer("counts", 0).cpu()]
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            mod(feats, None, shape, enc, prompt_feats=pf, encoder_bias_map=bias)
+        e1.record(stream)
+        torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    return {"workload": "A-shape 5-level int8 Sparse3DUNet [32, 64, 128, 256, 256], 1 block per stage, encoder 1024 "
+                        "x 30x40 tokens, prompt + bias map; forward incl. level structure (keys from depth)",
+            "voxels_per_level": counts, "ms": round(ms, 4), "voxels_per_s": round(M / (ms * 1e-3), 1)}
+
+
 def frame_bench(name, stream, reps=10):
     """One frame of a K-step configuration: K refine steps (each with its prompt fit, voxel keys and stencil
     rebuilt, v3.py:537-578) and the final metric fit after the last one. H also times the GPU nearest_fill of its
@@ -458,6 +541,10 @@ def main() -> int:
     ap.add_argument("--no-others", action="store_true", help="skip the K-step T and H frame timings")
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--kernels-only", action="store_true")
+    ap.add_argument("--fit-trace", action="store_true",
+                    help="print the metric fit's per-round phase trace (prompt and final fit of config A)")
+    ap.add_argument("--micro-only", action="store_true",
+                    help="run only the 1M-voxel map and conv microbench (for counter collection) and print it")
     ap.add_argument("--write-traffic", nargs=3, metavar=("OUT", "FETCH_DIR", "WRITE_DIR"))
     args = ap.parse_args()
     if args.write_traffic:
@@ -473,6 +560,11 @@ def main() -> int:
     sys.path.insert(0, ROOT)
     if args.kernels_only:
         return kernels_only(args)
+    if args.fit_trace:
+        return fit_trace(args)
+    if args.micro_only:
+        print(json.dumps({"conv_microbench": microbench(torch.cuda.Stream())}), flush=True)
+        return 0
     from promptmoge_amd.refiner import RefinerStep
 
     env = setup(args.config)
@@ -533,6 +625,7 @@ def main() -> int:
     if others is not None:
         others["pool_L0"] = pool_bench(stream)
         others["gauge_A"] = gauge_bench(stream)
+        others["unet_A"] = unet_bench(stream)
     cpu = None if args.no_cpu else cpu_baseline(env)
 
     line = {

@@ -425,7 +425,9 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
     uint32_t lo = 0, hi = 0;
 
     // A fit that falls back to (1, 0) never changes (s, t): its trim rounds cannot affect the result.
+    int rounds = 0;  // trim rounds run (the loop stops early at a fixed point)
     for (int it = 0; it < (sh.ok ? a.iters : 0); ++it) {
+        rounds = it + 1;
         // The element values and mask bits are loop-invariant; hiding that from the compiler keeps it from hoisting
         // their fp64 products and per-element lane masks out of the loop into hundreds of extra registers.
 #pragma unroll
@@ -771,6 +773,7 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
         a.st[2 * a.b] = s;
         a.st[2 * a.b + 1] = t;
         if (a.info) a.info[5 * a.b + 3] = (int32_t)thr;
+        ws.trace[2 * kFitTraceRounds + 2] = (uint32_t)rounds;
     }
 
     // Completion. The last block to finish sees every block's writes; it reports the launch's error flag. After
