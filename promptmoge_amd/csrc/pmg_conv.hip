@@ -218,37 +218,52 @@ constexpr int kG2Chunk = kG2Waves * kG2Tiles * 16;  // 512 rows per block step
 // meets at one barrier per group. Each LDS weight operand feeds the wave's 4 tiles (4 MFMAs of 16 cycles) and the
 // next operand is read before they issue. A wave skips the MFMAs of taps none of its 4 tiles has; an absent
 // neighbour (index -1), and every index of such a tap, becomes an out-of-range buffer offset, which loads zeros.
-template <int C, int EPI>
+//
+// NB < C / 16 splits the output channels into slices of 16 NB, one per blockIdx.y (Co = 256: 8 column blocks of 16
+// at a time, which is what fits the registers), and T sets the rows per wave (16 T; chunks of 128 T rows). With
+// a.m_dev the row count is read on the device: a.M is then the capacity, the row stride of the map. PF = how many
+// weight operands ahead a wave reads from LDS; RS = 4 gathers codes three taps ahead instead of one and requests
+// a group's weights a whole group ahead (a few hundred rows per block, as on the coarse levels of a U-Net, leave
+// each tap waiting on both otherwise).
+template <int C, int EPI, int NB = C / 16, int T = kG2Tiles, int PF = 1, int RS = 2>
 __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
     constexpr int GRP = C == 64 ? 4 : 2;
-    constexpr int NB = C / 16, KS = C / 64, T = kG2Tiles;
+    constexpr int KS = C / 64;
     constexpr int NF = NB * KS;                          // 1 KB operand fragments per tap
     constexpr int WPT = GRP * NF / kG2Waves;             // fragments staged per wave per group
     constexpr int NG = (27 + GRP - 1) / GRP;             // tap groups; taps >= 27 of the last one are empty
     constexpr int NG2 = (NG + 1) / 2;                    // loop trips of two groups (one per LDS buffer)
-    static_assert(C == 64 || C == 128, "C must be 64 or 128");
+    constexpr int CHUNK = kG2Waves * T * 16;             // rows per block step
+    constexpr int NS = 16 * NB;                          // output channels of the block
+    static_assert(C == 64 || C == 128 || C == 256, "C must be 64, 128 or 256");
     static_assert(GRP * NF % kG2Waves == 0, "staging split");
+    static_assert(T == 1 || T == 2 || T == 4, "tiles per wave");
+    static_assert(RS == 2 || RS == 4, "ring slots: the tap parity or v mod 4 of a trip");
+    constexpr int GD = RS - 1;                           // gather distance in taps
 
     __shared__ __attribute__((aligned(16))) v4i s_w[2][GRP * NF * 64];
-    __shared__ float s_k[2][C];
+    __shared__ float s_k[2][NS];
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int r = lane & 15, g = lane >> 4;
-    const int M = (int)a.M;
-    const int64_t ntile = (a.M + 15) >> 4;
+    const int S = (int)a.M;                               // map row stride (the capacity)
+    const int M = a.m_dev ? (int)*a.m_dev : S;            // rows
+    const int64_t ntile = (M + 15) >> 4;
+    const int Co = NS == C ? C : a.Co;
+    const int n0 = NS == C ? 0 : (int)blockIdx.y * NS;    // first output channel of the block
     typedef const __attribute__((address_space(3))) v4i lds_v4i;
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, (int)(a.M * C), kBufWord3);
     const __amdgpu_buffer_rsrc_t nr =
         __builtin_amdgcn_make_buffer_rsrc((void*)a.nmap_t, (short)0, (int)(a.M * 27 * 4), kBufWord3);
-    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc((void*)a.w, (short)0, C * 27 * C, kBufWord3);
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc((void*)a.w, (short)0, Co * 27 * C, kBufWord3);
 
-    for (int e = tid; e < 2 * C; e += kG2Threads) {
-        const int q = e / C, n = e - (e / C) * C;
+    for (int e = tid; e < 2 * NS; e += kG2Threads) {
+        const int q = e / NS, n = e - (e / NS) * NS;
         const float* src = q == 0 ? a.w_scale : a.bias;
-        s_k[q][n] = src ? src[n] : 0.0f;
+        s_k[q][n] = src ? src[n0 + n] : 0.0f;
     }
 
-    const int nchunk = (M + kG2Chunk - 1) / kG2Chunk;
+    const int nchunk = (M + CHUNK - 1) / CHUNK;
     const int G = gridDim.x, b = blockIdx.x;
     const int nx = G >= 8 ? 8 : 1;
     const int x = b % nx, bi = b / nx, nbx = (G - x + nx - 1) / nx;
@@ -258,7 +273,7 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
     // the gathers). Fragment f = wv + 8k of the group is tap slot q = f / NF, operand js = f % NF = (j, s), and
     // lane l holds W[16j + (l & 15)][v][64s + 16(l >> 4) .. +16] of the [Co][27][Ci] tensor; taps >= 27 load zeros
     // (out-of-range buffer offset).
-    const int wlane = (r * 27) * C + 16 * g;
+    const int wlane = ((n0 + r) * 27) * C + 16 * g;
     // staged in PARTS pieces of WPP fragments per wave, one piece per tap of the group where that divides evenly
     // (C = 128: 8 registers held for one tap instead of 16 for the whole group)
     constexpr int PARTS = WPT % GRP == 0 ? GRP : 1, WPP = WPT / PARTS;
@@ -279,16 +294,17 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
     };
 
     for (int ch = c0 + bi; ch < c1; ch += nbx) {
-        const int pos0 = ch * kG2Chunk + wv * (16 * T) + r;
+        const int pos0 = ch * CHUNK + wv * (16 * T) + r;
+        // map offset of each tile's row; rows beyond M get an out-of-range offset (their indices load as 0)
         int roff[T];
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             const int p = pos0 + 16 * t;
-            roff[t] = 4 * (a.order ? (p < M ? a.order[p] : 0) : p);
+            roff[t] = p < M ? 4 * (a.order ? a.order[p] : p) : (int)0x80000000;
         }
         uint32_t wmask;
         {
-            const int64_t tl = (int64_t)ch * (kG2Chunk / 16) + wv * T + (lane & (T - 1));
+            const int64_t tl = (int64_t)ch * (CHUNK / 16) + wv * T + (lane & (T - 1));
             uint32_t mk = (lane < T && tl < ntile) ? a.tmask[tl] : 0u;
 #pragma unroll
             for (int o = 1; o < T; o <<= 1) mk |= __shfl_xor(mk, o, 64);
@@ -303,7 +319,7 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
         // map indices of tap v (taps >= 27: out-of-range, zeros); gathers of the rows they name (absent: zeros).
         // Every load is issued unconditionally, so the compiler's vmcnt waits stay exact.
         auto idx_load = [&](int v, int (&id)[T]) {
-            const int vo = (v < 27 ? v : 27) * M * 4;
+            const int vo = (v < 27 ? v : 27) * S * 4;
 #pragma unroll
             for (int t = 0; t < T; ++t) id[t] = __builtin_amdgcn_raw_buffer_load_b32(nr, roff[t], vo, 0);
         };
@@ -315,63 +331,84 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
                 for (int s2 = 0; s2 < KS; ++s2) xs[t][s2] = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 64 * s2, 0);
             }
         };
+        // operand q of the tap is (s2, j) = (q / NB, q % NB), read PF operands ahead of its MFMAs
         auto mma_tap = [&](const v4i* wslot, const v4i (&xs)[T][KS]) {
             const v4i* wb = wslot + lane;
-            v4i wop = *(lds_v4i*)(wb);
+            v4i wop[PF];
+#pragma unroll
+            for (int k = 0; k < PF; ++k) wop[k] = *(lds_v4i*)(wb + ((k % NB) * KS + k / NB) * 64);
 #pragma unroll
             for (int q = 0; q < NF; ++q) {
                 const int s2 = q / NB, j = q - (q / NB) * NB;
-                v4i nxt = wop;
-                if (q + 1 < NF) {
-                    const int s3 = (q + 1) / NB, j3 = (q + 1) - ((q + 1) / NB) * NB;
-                    nxt = *(lds_v4i*)(wb + (j3 * KS + s3) * 64);
+                const v4i cur = wop[q % PF];
+                if (q + PF < NF) {
+                    const int s3 = (q + PF) / NB, j3 = (q + PF) - ((q + PF) / NB) * NB;
+                    wop[q % PF] = *(lds_v4i*)(wb + (j3 * KS + s3) * 64);
                 }
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int t = 0; t < T; ++t)
-                    acc[t][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wop, xs[t][s2], acc[t][j], 0, 0, 0);
+                    acc[t][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(cur, xs[t][s2], acc[t][j], 0, 0, 0);
                 __builtin_amdgcn_sched_barrier(0);
-                wop = nxt;
             }
         };
 
-        int I[2][T];  // indices three taps ahead: tap v+3 reuses the slot that tap v+1's gather just read
-        v4i X[2][T][KS];
+        // Rings of RS slots (tap u in slot u mod RS): the codes of tap u are gathered GD = RS - 1 taps ahead of its
+        // MFMAs and its map indices two taps before that; an index slot is reloaded once its gather has read it.
+        int I[RS][T];
+        v4i X[RS][T][KS];
 #pragma unroll
         for (int part = 0; part < PARTS; ++part) {
             v4i st[WPP];
             w_load(0, part, st);
             w_store(s_w[0], part, st);
         }
-        {
+        if constexpr (RS == 2) {
             int i0[T];
             idx_load(0, i0);
             idx_load(1, I[1]);
             idx_load(2, I[0]);
             gather(i0, X[0]);
+        } else {
+#pragma unroll
+            for (int u = 0; u < RS; ++u) idx_load(u, I[u]);
+#pragma unroll
+            for (int u = 0; u < GD; ++u) gather(I[u], X[u]);
+            idx_load(RS, I[0]);
         }
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's weight stores are in LDS
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
 
         // One group: weights of the next group are loaded at its start and stored into the other buffer at its end
-        // (every wave left that buffer at the last barrier); per tap v, the codes of tap v+1 and the indices of
-        // tap v+3 are requested before tap v's MFMAs. H = the buffer (group parity), compile-time, so the X and I
-        // ring slots are too.
+        // (every wave left that buffer at the last barrier); per tap v, the codes of tap v+GD and the indices of
+        // tap v+GD+2 are requested before tap v's MFMAs. H = the buffer (group parity), compile-time, so the X and
+        // I ring slots are too.
         auto group = [&](auto Hc, int grp) {
             constexpr int H = decltype(Hc)::value;
+            v4i sta[RS == 2 ? 1 : PARTS][WPP];  // RS = 4: the next group's weights, all requested at its start
 #pragma unroll
             for (int q = 0; q < GRP; ++q) {
                 const int v = GRP * grp + q;
                 const int p = (GRP * H + q) & 3;  // v mod 4 (GRP * grp = 4 * trip + GRP * H)
                 v4i st[WPP];
-                if (q < PARTS) w_load(grp + 1, q, st);
-                gather(I[(p + 1) & 1], X[(p + 1) & 1]);
-                idx_load(v + 3, I[(p + 1) & 1]);
+                if constexpr (RS == 2) {
+                    if (q < PARTS) w_load(grp + 1, q, st);
+                } else if (q == 0) {
+#pragma unroll
+                    for (int pp = 0; pp < PARTS; ++pp) w_load(grp + 1, pp, sta[pp]);
+                }
+                gather(I[(p + GD) % RS], X[(p + GD) % RS]);
+                idx_load(v + GD + 2, I[(p + GD + 2) % RS]);
                 __builtin_amdgcn_sched_barrier(0);
-                if (v < 27 && ((wmask >> v) & 1u)) mma_tap(s_w[H] + q * NF * 64, X[p & 1]);
+                if (v < 27 && ((wmask >> v) & 1u)) mma_tap(s_w[H] + q * NF * 64, X[p % RS]);
                 __builtin_amdgcn_sched_barrier(0);
-                if (q < PARTS) w_store(s_w[H ^ 1], q, st);
+                if constexpr (RS == 2) {
+                    if (q < PARTS) w_store(s_w[H ^ 1], q, st);
+                } else if (q == GRP - 1) {
+#pragma unroll
+                    for (int pp = 0; pp < PARTS; ++pp) w_store(s_w[H ^ 1], pp, sta[pp]);
+                }
             }
             __builtin_amdgcn_s_waitcnt(0xc07f);
             __builtin_amdgcn_s_barrier();
@@ -389,7 +426,7 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
             const int m = roff[t] >> 2;
 #pragma unroll
             for (int j = 0; j < NB; ++j) {
-                const int64_t o = (int64_t)m * C + 16 * j + 4 * g;
+                const int64_t o = (int64_t)m * Co + n0 + 16 * j + 4 * g;
                 if constexpr (EPI == PMG_EPI_ACC) {
                     *(v4i*)((int32_t*)a.out + o) = acc[t][j];
                 } else {
@@ -422,17 +459,19 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
 // meets at no barrier afterwards -- each wave runs its chunks' 27 taps on its own, and a wave that skips a tap
 // (none of its tiles has it) gains the time instead of waiting for the others at the next group barrier. The tap
 // loop is that of spconv_g2_k without the weight staging: codes one tap ahead, map indices three taps ahead.
-template <int C, int EPI>
+template <int C, int EPI, int T = kG2Tiles, int PF = 1>
 __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2r_k(ConvArgs a) {
-    constexpr int NB = C / 16, KS = C / 64, T = kG2Tiles;
+    constexpr int NB = C / 16, KS = C / 64;
     constexpr int NF = NB * KS;
+    constexpr int CHUNK = kG2Waves * T * 16;
     static_assert(C == 64, "resident weights: C = 64");
     __shared__ __attribute__((aligned(16))) v4i s_w[27 * NF * 64];
     __shared__ float s_k[2][C];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int r = lane & 15, g = lane >> 4;
-    const int M = (int)a.M;
-    const int64_t ntile = (a.M + 15) >> 4;
+    const int S = (int)a.M;                     // map row stride (the capacity)
+    const int M = a.m_dev ? (int)*a.m_dev : S;  // rows
+    const int64_t ntile = (M + 15) >> 4;
     typedef const __attribute__((address_space(3))) v4i lds_v4i;
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, (int)(a.M * C), kBufWord3);
     const __amdgpu_buffer_rsrc_t nr =
@@ -450,23 +489,23 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2r_k(ConvArgs a) {
     }
     __syncthreads();
 
-    const int nchunk = (M + kG2Chunk - 1) / kG2Chunk;
+    const int nchunk = (M + CHUNK - 1) / CHUNK;
     const int G = gridDim.x, b = blockIdx.x;
     const int nx = G >= 8 ? 8 : 1;
     const int x = b % nx, bi = b / nx, nbx = (G - x + nx - 1) / nx;
     const int c0 = (int)((int64_t)nchunk * x / nx), c1 = (int)((int64_t)nchunk * (x + 1) / nx);
     // each wave takes the block's chunks independently: wave wv of chunk ch owns rows [64 wv, 64 wv + 64)
     for (int ch = c0 + bi; ch < c1; ch += nbx) {
-        const int pos0 = ch * kG2Chunk + wv * (16 * T) + r;
-        int roff[T];
+        const int pos0 = ch * CHUNK + wv * (16 * T) + r;
+        int roff[T];  // rows beyond M: out-of-range map offset (indices load as 0)
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             const int p = pos0 + 16 * t;
-            roff[t] = 4 * (a.order ? (p < M ? a.order[p] : 0) : p);
+            roff[t] = p < M ? 4 * (a.order ? a.order[p] : p) : (int)0x80000000;
         }
         uint32_t wmask;
         {
-            const int64_t tl = (int64_t)ch * (kG2Chunk / 16) + wv * T + (lane & (T - 1));
+            const int64_t tl = (int64_t)ch * (CHUNK / 16) + wv * T + (lane & (T - 1));
             uint32_t mk = (lane < T && tl < ntile) ? a.tmask[tl] : 0u;
 #pragma unroll
             for (int o = 1; o < T; o <<= 1) mk |= __shfl_xor(mk, o, 64);
@@ -478,7 +517,7 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2r_k(ConvArgs a) {
 #pragma unroll
             for (int j = 0; j < NB; ++j) acc[t][j] = v4i{0, 0, 0, 0};
         auto idx_load = [&](int v, int (&id)[T]) {
-            const int vo = (v < 27 ? v : 27) * M * 4;
+            const int vo = (v < 27 ? v : 27) * S * 4;
 #pragma unroll
             for (int t = 0; t < T; ++t) id[t] = __builtin_amdgcn_raw_buffer_load_b32(nr, roff[t], vo, 0);
         };
@@ -492,21 +531,22 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2r_k(ConvArgs a) {
         };
         auto mma_tap = [&](int v, const v4i (&xs)[T][KS]) {
             const v4i* wb = s_w + v * NF * 64 + lane;
-            v4i wop = *(lds_v4i*)(wb);
+            v4i wop[PF];
+#pragma unroll
+            for (int k = 0; k < PF; ++k) wop[k] = *(lds_v4i*)(wb + ((k % NB) * KS + k / NB) * 64);
 #pragma unroll
             for (int q = 0; q < NF; ++q) {
                 const int s2 = q / NB, j = q - (q / NB) * NB;
-                v4i nxt = wop;
-                if (q + 1 < NF) {
-                    const int s3 = (q + 1) / NB, j3 = (q + 1) - ((q + 1) / NB) * NB;
-                    nxt = *(lds_v4i*)(wb + (j3 * KS + s3) * 64);
+                const v4i cur = wop[q % PF];
+                if (q + PF < NF) {
+                    const int s3 = (q + PF) / NB, j3 = (q + PF) - ((q + PF) / NB) * NB;
+                    wop[q % PF] = *(lds_v4i*)(wb + (j3 * KS + s3) * 64);
                 }
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int t = 0; t < T; ++t)
-                    acc[t][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wop, xs[t][s2], acc[t][j], 0, 0, 0);
+                    acc[t][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(cur, xs[t][s2], acc[t][j], 0, 0, 0);
                 __builtin_amdgcn_sched_barrier(0);
-                wop = nxt;
             }
         };
         int I[2][T];
@@ -608,6 +648,36 @@ static int launch_g2(const ConvArgs& a, int epilogue, hipStream_t s) {
     }
 }
 
+// Device-sized launches of the staged kernels (Ci = Co = C): the grid covers the capacity's chunks, at most one
+// block per CU in x (blockIdx.y: the output-channel slice), and every block reads the row count and takes its XCD
+// band's share of the chunks that hold rows; the others return at once.
+template <int C, int NB, int T, int PF, int RS>
+static int launch_g2_dev(const ConvArgs& a, int epilogue, hipStream_t s) {
+    static int cus = -1;
+    if (cus < 0) cus = num_cus();
+    constexpr int CHUNK = kG2Waves * T * 16;
+    const int64_t nchunk = (a.M + CHUNK - 1) / CHUNK;
+    const dim3 grid((unsigned)(nchunk < cus ? nchunk : cus), (unsigned)(a.Co / (16 * NB)));
+    if constexpr (C == 64) {
+        static_assert(NB == 4, "C = 64 keeps all 64 output channels");
+        switch (epilogue) {
+            case PMG_EPI_ACC: hipLaunchKernelGGL((spconv_g2r_k<C, PMG_EPI_ACC, T, PF>), grid, dim3(kG2Threads), 0, s, a); break;
+            case PMG_EPI_Q: hipLaunchKernelGGL((spconv_g2r_k<C, PMG_EPI_Q, T, PF>), grid, dim3(kG2Threads), 0, s, a); break;
+            case PMG_EPI_R: hipLaunchKernelGGL((spconv_g2r_k<C, PMG_EPI_R, T, PF>), grid, dim3(kG2Threads), 0, s, a); break;
+            default: hipLaunchKernelGGL((spconv_g2r_k<C, PMG_EPI_BIAS, T, PF>), grid, dim3(kG2Threads), 0, s, a); break;
+        }
+        return check_launch("spconv_g2r_k");
+    } else {
+        switch (epilogue) {
+            case PMG_EPI_ACC: hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_ACC, NB, T, PF, RS>), grid, dim3(kG2Threads), 0, s, a); break;
+            case PMG_EPI_Q: hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_Q, NB, T, PF, RS>), grid, dim3(kG2Threads), 0, s, a); break;
+            case PMG_EPI_R: hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_R, NB, T, PF, RS>), grid, dim3(kG2Threads), 0, s, a); break;
+            default: hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_BIAS, NB, T, PF, RS>), grid, dim3(kG2Threads), 0, s, a); break;
+        }
+        return check_launch("spconv_g2_k");
+    }
+}
+
 int launch_conv_i8_dev(const DevConv& d, hipStream_t s) {
     PMG_REQUIRE(d.x && d.nmap_t && d.tile_mask && d.w && d.out && d.m_dev, "null buffer");
     PMG_REQUIRE(d.Ci % 16 == 0 && d.Co % 16 == 0 && d.Ci > 0 && d.Co > 0, "channels must be multiples of 16");
@@ -632,6 +702,13 @@ int launch_conv_i8_dev(const DevConv& d, hipStream_t s) {
     a.skip = d.skip;
     a.out = d.out;
     a.m_dev = d.m_dev;
+    // the staged kernels' buffer offsets are 32-bit
+    const bool fits32 = d.cap * 27 * 4 < ((int64_t)1 << 31) && d.cap * d.Ci < ((int64_t)1 << 31);
+    if (fits32 && d.Ci == d.Co) {
+        if (d.Ci == 64) return launch_g2_dev<64, 4, 2, 2, 2>(a, d.epilogue, s);
+        if (d.Ci == 128) return launch_g2_dev<128, 8, 2, 3, 4>(a, d.epilogue, s);
+        if (d.Ci == 256) return launch_g2_dev<256, 8, 1, 3, 4>(a, d.epilogue, s);
+    }
     const int nb = pick_nb(d.Co);
     switch (d.epilogue) {
         case PMG_EPI_Q: return launch_nb<int8_t, PMG_EPI_Q>(a, nb, s);
