@@ -101,7 +101,7 @@ __device__ inline void epilogue(const ConvArgs& a, int64_t m, int n, typename Ac
             if (a.bias) y = y + a.bias[n];
         }
         if constexpr (EPI == PMG_EPI_SILU) {
-            ((_Float16*)a.out)[o] = (_Float16)silu_f32(y);
+            ((_Float16*)a.out)[o] = (_Float16)silu_fast(y);
         } else if constexpr (EPI == PMG_EPI_R) {
             ((float*)a.out)[o] = y + a.skip[o];
         } else {

@@ -21,7 +21,8 @@
 //
 // Epilogues (one pass over the output):
 //   ACC    raw accumulator (int32 / fp32), for parity
-//   Q      int8: clamp(rint(silu(acc*a_scale*w_scale + bias) * out_mult), +-127);  fp16: half(silu(acc + bias))
+//   Q      int8: clamp(rint(silu(acc*a_scale*w_scale + bias) * out_mult), +-127);  fp16: half(silu(acc + bias)),
+//          SiLU by the hardware exp2/reciprocal (silu_fast: within one fp16 ulp of the exact form)
 //   R      x_new = dequant(acc) + skip                                   (fp32 residual stream)
 //   RLN    R, stores x_new, then the next block's LayerNorm -> SiLU -> int8 codes (or fp16), so the residual block
 //          needs no separate normalisation pass (flex_sparse_blocks.py:230-234)
@@ -159,7 +160,7 @@ __device__ inline void col_epilogue(const ColConvArgs& a, const typename ColAcc<
                     typedef _Float16 h4 __attribute__((ext_vector_type(4)));
                     h4 hv;
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) hv[i] = (_Float16)silu_f32(y[j][i]);
+                    for (int i = 0; i < 4; ++i) hv[i] = (_Float16)silu_fast(y[j][i]);
                     *(h4*)((_Float16*)a.out + o) = hv;
                 }
             }
@@ -223,6 +224,7 @@ __global__ __launch_bounds__(kColThreads) void spconv_col_k(ColConvArgs a) {
     typedef ColGeom<T, C> G;
     constexpr int ROWB = G::ROWB, NCH = G::NCH, NB = C / 16, NBUF = G::NBUF;
     constexpr bool WLDS = G::WLDS;
+    static_assert(NCH <= 4 || NCH % 4 == 0, "a tap's chunks must fill whole MFMA steps");
     typedef typename ColAcc<T>::type acc_t;
 
     __shared__ __attribute__((aligned(16))) uint8_t s_w[WLDS ? G::WBYTES : 16];
@@ -458,25 +460,294 @@ __global__ __launch_bounds__(kColThreads) void spconv_col_k(ColConvArgs a) {
     }
 }
 
+// Weights beyond LDS residency (int8 C = 128, fp16 C = 48 / 64: 124-442 KB): the same segments and windows, with
+// the taps staged. The block walks the union of its 8 waves' active taps in ascending order; each tap's weights
+// (C x 27 x Ci -> C x Ci) are staged once per block into LDS in MFMA operand order -- lane (r, g) of fragment
+// (s, j) holds W[16j + r][v][chunk 4s + g], zero where 4s + g is past the row (the K padding of C = 48 in fp16) --
+// and feed all eight waves, where the resident-weight kernel above would read every operand from L2 once per wave
+// and MFMA step. Tap t + 1's weights are written while tap t's MFMAs run (two LDS buffers, one barrier per tap);
+// their global loads are issued two taps ahead. A wave whose rows lack a tap skips its MFMAs. The next segment's
+// window is loaded into registers during the taps (after the epilogue at C/16 > 4, where registers run out) and
+// written once every wave has left the current one.
+template <typename T, int C, int EPI, int WV>
+__global__ __launch_bounds__(64 * WV) void spconv_cols_k(ColConvArgs a) {
+    constexpr int kThreads = 64 * WV, kSegS = 32 * WV, kWinS = kSegS + 2;
+    constexpr int ROWB = C * (int)sizeof(T), NCH = ROWB / 16, NB = C / 16;
+    constexpr int XBYTES = 3 * kWinS * ROWB;
+    constexpr int PF = (3 * kWinS * NCH + kThreads - 1) / kThreads;  // window chunks per thread
+    constexpr int PFZ = (3 * kWinS + kThreads - 1) / kThreads;       // window keys per thread
+    constexpr int SPT = (NCH + 3) / 4;       // MFMA steps per tap; lane group g of step s takes chunk 4s + g
+    constexpr int FR = SPT * NB;             // 1 KB operand fragments per tap
+    constexpr int WPT = (FR * 64 + kThreads - 1) / kThreads;  // staged 16-byte pieces per thread per tap
+    // the next window is prefetched during the taps where the registers allow (up to 64 output channels)
+    constexpr bool kPre = NB <= 4;
+    typedef typename ColAcc<T>::type acc_t;
+    static_assert(XBYTES + 2 * FR * 1024 + 3 * kWinS * 4 + 64 <= 160 * 1024, "window and two taps must fit LDS");
+
+    __shared__ __attribute__((aligned(16))) v4i s_w[2][FR * 64];
+    __shared__ __attribute__((aligned(16))) uint8_t s_x[XBYTES];
+    __shared__ int s_z[3 * kWinS];
+    __shared__ __attribute__((aligned(16))) uint8_t s_zero[16];
+    __shared__ uint32_t s_uni[WV];
+
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int M = (int)a.M;
+    const int H = a.H, W = a.W;
+    const int HW = H * W;
+    const uint8_t* __restrict__ xg = (const uint8_t*)a.x;
+    const uint8_t* __restrict__ wg = (const uint8_t*)a.w;
+    if (tid == 0) *(v4i*)s_zero = v4i{0, 0, 0, 0};
+
+    // staged weights of tap v (v < 0: none) into registers; piece e = tid + k * kThreads is lane e % 64 of
+    // fragment f = e / 64 = s * NB + j
+    auto w_load = [&](int v, v4i (&st)[WPT]) {
+#pragma unroll
+        for (int k = 0; k < WPT; ++k) {
+            const int e = tid + k * kThreads;
+            const int f = e >> 6, l = e & 63;
+            const int s2 = f / NB, j = f - (f / NB) * NB;
+            const int ch = 4 * s2 + (l >> 4);
+            st[k] = v4i{0, 0, 0, 0};
+            if (v >= 0 && e < FR * 64 && ch < NCH)
+                st[k] = *(const v4i*)(wg + ((int64_t)(16 * j + (l & 15)) * 27 + v) * ROWB + ch * 16);
+        }
+    };
+    auto w_store = [&](int buf, const v4i (&st)[WPT]) {
+#pragma unroll
+        for (int k = 0; k < WPT; ++k) {
+            const int e = tid + k * kThreads;
+            if (e < FR * 64) s_w[buf][e] = st[k];
+        }
+    };
+
+    v4i pf[PF];
+    int pfz[PFZ];
+    auto fetch = [&](int sg) {
+        const int s0 = sg * kSegS;
+#pragma unroll
+        for (int k = 0; k < PF; ++k) {
+            const int e = tid + k * kThreads;
+            pf[k] = v4i{0, 0, 0, 0};
+            if (e < 3 * kWinS * NCH) {
+                const int d = e / (kWinS * NCH);
+                const int rem = e - d * (kWinS * NCH);
+                const int q = rem / NCH, c = rem - (rem / NCH) * NCH;
+                const int p = s0 + (d - 1) * W - 1 + q;
+                if (p >= 0 && p < M) pf[k] = *(const v4i*)(xg + (int64_t)p * ROWB + c * 16);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < PFZ; ++k) {
+            const int e = tid + k * kThreads;
+            pfz[k] = kZFar;
+            if (e < 3 * kWinS) {
+                const int d = e / kWinS, q = e - (e / kWinS) * kWinS;
+                const int p = s0 + (d - 1) * W - 1 + q;
+                if (p >= 0 && p < M) pfz[k] = a.zq[p];
+            }
+        }
+    };
+    auto commit = [&]() {
+#pragma unroll
+        for (int k = 0; k < PF; ++k) {
+            const int e = tid + k * kThreads;
+            if (e < 3 * kWinS * NCH) ((v4i*)s_x)[e] = pf[k];
+        }
+#pragma unroll
+        for (int k = 0; k < PFZ; ++k) {
+            const int e = tid + k * kThreads;
+            if (e < 3 * kWinS) s_z[e] = pfz[k];
+        }
+    };
+
+    // XCD-aware segment order, as in spconv_col_k
+    const int nx = gridDim.x < 8 ? (int)gridDim.x : 8;
+    const int xcd = (int)blockIdx.x % nx, ib = (int)blockIdx.x / nx;
+    const int nbx = ((int)gridDim.x - xcd + nx - 1) / nx;
+    const int nseg_all = (M + kSegS - 1) / kSegS;
+    const int nseg = (int)((int64_t)nseg_all * (xcd + 1) / nx);
+    int seg = (int)((int64_t)nseg_all * xcd / nx) + ib;
+    if (seg < nseg) {
+        fetch(seg);
+        commit();
+    }
+    typedef const __attribute__((address_space(3))) uint8_t* lds_ptr;
+    typedef const __attribute__((address_space(3))) v4i lds_v4i;
+    for (; seg < nseg; seg += nbx) {
+        const int s0 = seg * kSegS;
+        const int nxt = seg + nbx;
+        __syncthreads();  // window visible; every wave has left the previous segment's weight buffers
+
+        // ---- 27-bit tap masks of the wave's 32 rows (lane l < 32: row l), the wave's union and the block's
+        uint32_t mk = 0;
+        {
+            const int lr = 32 * wv + (lane & 31);
+            const int m = s0 + lr;
+            if (lane < 32 && m < M) {
+                const int pix = m % HW;
+                const int i = pix / W, j = pix - (pix / W) * W;
+                const int zc = s_z[kWinS + lr + 1];
+#pragma unroll
+                for (int di = 0; di < 3; ++di)
+#pragma unroll
+                    for (int dj = 0; dj < 3; ++dj) {
+                        const bool in = (unsigned)(i + di - 1) < (unsigned)H && (unsigned)(j + dj - 1) < (unsigned)W;
+                        const int64_t dz = (int64_t)s_z[di * kWinS + lr + dj] - zc;
+                        const bool hit = in && dz >= -1 && dz <= 1;
+                        mk |= (hit ? 1u : 0u) << (di * 9 + dj * 3 + (int)(dz + 1 < 0 ? 0 : (dz + 1 > 2 ? 2 : dz + 1)));
+                    }
+            }
+        }
+        uint32_t uni = mk;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) uni |= __shfl_xor(uni, o, 64);
+        uni = sgpr(uni);
+        const uint32_t mrow0 = __shfl(mk, r, 64), mrow1 = __shfl(mk, 16 + r, 64);
+        if (lane == 0) s_uni[wv] = uni;
+        __syncthreads();
+        uint32_t bu = 0;
+#pragma unroll
+        for (int w2 = 0; w2 < WV; ++w2) bu |= s_uni[w2];
+        bu = sgpr(bu);
+
+        acc_t acc[2][NB];
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int j = 0; j < NB; ++j) acc[rb][j] = acc_t{0, 0, 0, 0};
+
+        // operand addresses: lane-constant LDS offsets plus a wave-uniform offset per (tap, step); a lane whose
+        // row lacks the tap, or whose chunk is padding, reads the zero slot
+        const int lr0 = 32 * wv + r;
+        const lds_ptr xbase = (lds_ptr)s_x + (lr0 * ROWB + g * 16);
+        const lds_ptr zslot = (lds_ptr)s_zero;
+
+        // tap sequence: ascending bits of bu, -1 after the last
+        uint32_t rem = bu;
+        auto pop = [&]() {
+            const int v = rem ? (int)__builtin_ctz(rem) : -1;
+            rem = rem ? rem & (rem - 1) : 0u;
+            return v;
+        };
+        const int ntap = __builtin_popcount(bu);
+        int v0 = pop(), v1 = pop(), v2 = pop();
+        v4i wa[WPT], wb[WPT];
+        w_load(v0, wa);
+        w_load(v1, wb);
+        w_store(0, wa);
+        __syncthreads();
+
+        // The next window is requested right after the segment's last weight load: the memory counter completes
+        // in order, so a window requested earlier would hold up every later weight store behind it.
+        bool fetched = !kPre || nxt >= nseg;
+        auto tap = [&](int buf, int v, const v4i (&wnext)[WPT], v4i (&wlater)[WPT], int vlater) {
+            // the weights two taps ahead are requested before this tap's matrix work
+            w_load(vlater, wlater);
+            if (!fetched && vlater < 0) {
+                fetch(nxt);
+                fetched = true;
+            }
+            if ((uni >> v) & 1u) {
+                const int xo = ((v / 9) * kWinS + (v / 3) % 3) * ROWB;
+                const bool h0 = (mrow0 >> v) & 1u, h1 = (mrow1 >> v) & 1u;
+                // every operand of the tap is requested before its first MFMA (LDS returns in order, so the MFMAs
+                // of step 0 wait only for step 0's reads)
+                v4i x0[SPT], x1[SPT], wo[SPT][NB];
+#pragma unroll
+                for (int s2 = 0; s2 < SPT; ++s2) {
+                    const bool on = 4 * s2 + g < NCH;
+                    const lds_ptr p0 = h0 && on ? xbase + (xo + s2 * 64) : zslot;
+                    const lds_ptr p1 = h1 && on ? xbase + (xo + 16 * ROWB + s2 * 64) : zslot;
+                    x0[s2] = *(const __attribute__((address_space(3))) v4i*)p0;
+                    x1[s2] = *(const __attribute__((address_space(3))) v4i*)p1;
+#pragma unroll
+                    for (int j = 0; j < NB; ++j) wo[s2][j] = *(lds_v4i*)(&s_w[buf][(s2 * NB + j) * 64 + lane]);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int s2 = 0; s2 < SPT; ++s2)
+#pragma unroll
+                    for (int j = 0; j < NB; ++j) {
+                        mma_col(acc[0][j], wo[s2][j], x0[s2], T{});
+                        mma_col(acc[1][j], wo[s2][j], x1[s2], T{});
+                    }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            w_store(buf ^ 1, wnext);
+            __syncthreads();
+        };
+        // two taps per trip so the buffer and register-set indices are compile-time
+        for (int t = 0; t < ntap; t += 2) {
+            tap(0, v0, wb, wa, v2);
+            v0 = v1;
+            v1 = v2;
+            v2 = pop();
+            if (t + 1 >= ntap) break;
+            tap(1, v0, wa, wb, v2);
+            v0 = v1;
+            v1 = v2;
+            v2 = pop();
+        }
+
+        if (!fetched) fetch(nxt);  // at most two taps: every weight load came before the loop
+
+        // ---- epilogue
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) {
+            v4f sk[NB];
+            if constexpr (EPI == PMG_EPI_R || EPI == PMG_EPI_RLN || EPI == PMG_EPI_ROUT)
+                load_skip<C>(a, s0 + 32 * wv + 16 * rb + r, M, g, sk);
+            col_epilogue<T, C, EPI>(a, acc[rb], s0 + 32 * wv + 16 * rb + r, M, g, epi_global(a), sk);
+        }
+
+        // ---- the next window: written once every wave has left this one
+        if (nxt < nseg) {
+            if constexpr (!kPre) fetch(nxt);
+            __syncthreads();
+            commit();
+        }
+    }
+}
+
 template <typename T, int C, int EPI>
 static int launch_col3(const ColConvArgs& a, hipStream_t s) {
     if constexpr (!ColGeom<T, C>::FITS) {
         return fail(PMG_E_INVALID, "pmg_spconv_col: this precision/width does not fit the LDS window");
     } else {
         const int64_t nseg = (a.M + kSeg - 1) / kSeg;
-        static int per_cu = -1;
-        if (per_cu < 0) {
-            int n = 0;
-            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, spconv_col_k<T, C, EPI>, kColThreads, 0) !=
-                    hipSuccess ||
-                n < 1)
-                n = 1;
-            per_cu = n;
+        if constexpr (!ColGeom<T, C>::WLDS) {
+            // 8-wave blocks of 256-voxel segments, one per CU (LDS)
+            constexpr int WV = 8;
+            const int64_t nseg4 = (a.M + 32 * WV - 1) / (32 * WV);
+            static int per_cu = -1;
+            if (per_cu < 0) {
+                int n = 0;
+                if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, spconv_cols_k<T, C, EPI, WV>, 64 * WV, 0) !=
+                        hipSuccess ||
+                    n < 1)
+                    n = 1;
+                per_cu = n;
+            }
+            int64_t grid = (int64_t)per_cu * num_cus();
+            if (grid > nseg4) grid = nseg4;
+            hipLaunchKernelGGL((spconv_cols_k<T, C, EPI, WV>), dim3((unsigned)grid), dim3(64 * WV), 0, s, a);
+            return check_launch("spconv_cols_k");
+        } else {
+            static int per_cu = -1;
+            if (per_cu < 0) {
+                int n = 0;
+                if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, spconv_col_k<T, C, EPI>, kColThreads, 0) !=
+                        hipSuccess ||
+                    n < 1)
+                    n = 1;
+                per_cu = n;
+            }
+            int64_t grid = (int64_t)per_cu * num_cus();
+            if (grid > nseg) grid = nseg;
+            hipLaunchKernelGGL((spconv_col_k<T, C, EPI>), dim3((unsigned)grid), dim3(kColThreads), 0, s, a);
+            return check_launch("spconv_col_k");
         }
-        int64_t grid = (int64_t)per_cu * num_cus();
-        if (grid > nseg) grid = nseg;
-        hipLaunchKernelGGL((spconv_col_k<T, C, EPI>), dim3((unsigned)grid), dim3(kColThreads), 0, s, a);
-        return check_launch("spconv_col_k");
     }
 }
 
