@@ -546,6 +546,8 @@ def main() -> int:
     ap.add_argument("--micro-only", action="store_true",
                     help="run only the 1M-voxel map and conv microbench (for counter collection) and print it")
     ap.add_argument("--write-traffic", nargs=3, metavar=("OUT", "FETCH_DIR", "WRITE_DIR"))
+    ap.add_argument("--other", choices=["T", "H", "unet_A"],
+                    help="time only this other configuration (K-step frame, or the multi-level U-Net) and print it")
     args = ap.parse_args()
     if args.write_traffic:
         write_traffic(*args.write_traffic)
@@ -564,6 +566,11 @@ def main() -> int:
         return fit_trace(args)
     if args.micro_only:
         print(json.dumps({"conv_microbench": microbench(torch.cuda.Stream())}), flush=True)
+        return 0
+    if args.other:
+        s = torch.cuda.Stream()
+        res = unet_bench(s) if args.other == "unet_A" else frame_bench(args.other, s)
+        print(json.dumps({args.other: res}), flush=True)
         return 0
     from promptmoge_amd.refiner import RefinerStep
 

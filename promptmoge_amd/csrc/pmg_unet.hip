@@ -17,7 +17,9 @@
 //
 // Layers (int8 contract qat.py:1-16; the deployed engine's sequence, Refiner.swift:224-292, Refiner.metal:133-322):
 //   level-0 blocks         the map-free column convolutions (pmg_conv_col.hip) with the next LayerNorm fused
-//   blocks at levels >= 1  generic-map MFMA conv with the device row count (spconv_k) + a row LayerNorm kernel
+//   blocks at levels >= 1  generic-map MFMA conv with the device row count (launch_conv_i8_dev: the weight-staged
+//                          spconv_g2_k / spconv_g2r_k at C = 64 / 128 / 256, spconv_k otherwise) + a row
+//                          LayerNorm kernel
 //   PoolDown               children's fp32 mean (row order, / count) quantised in one kernel, then an int8 GEMM
 //   encoder conditioning   per token: quantise-transpose of the planar feature, int8 GEMM (+ the planar bias map),
 //                          gathered per voxel by its column in the concat-quantise of fuse_proj.0's input
