@@ -114,24 +114,20 @@ __device__ inline void col_epilogue(const ColConvArgs& a, const typename ColAcc<
         for (int j = 0; j < NB; ++j)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int n = 16 * j + 4 * g + i;
-                // the bias of an LDS-staged constant set is zero-filled when absent, so it is read unconditionally
-                // and the add is a select rather than a branch
-                float b = 0.0f;
-                if constexpr (std::is_same<P, const float*>::value) {
-                    if (k.has_bias) b = k.bs[n];
-                } else {
-                    b = k.bs[n];
-                }
-                float t;
                 if constexpr (sizeof(T) == 1) {
-                    t = (float)acc[j][i] * a.a_scale;
-                    t = t * k.ws[n];
+                    const float t = (float)acc[j][i] * a.a_scale;
+                    y[j][i] = t * k.ws[16 * j + 4 * g + i];
                 } else {
-                    t = acc[j][i];
+                    y[j][i] = acc[j][i];
                 }
-                y[j][i] = k.has_bias ? t + b : t;
             }
+        // the bias in one branch, uniform over the launch, instead of a select per element
+        if (k.has_bias) {
+#pragma unroll
+            for (int j = 0; j < NB; ++j)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) y[j][i] = y[j][i] + k.bs[16 * j + 4 * g + i];
+        }
     }
     if constexpr (EPI == PMG_EPI_ACC) {
         if (ok) {
@@ -779,12 +775,13 @@ static int launch_col2(const ColConvArgs& a, int epi, hipStream_t s) {
 // reduction runs over K = 8 offsets x 3 taps x C + C instead of 27 x C: the four lane groups of an MFMA operand
 // (16 K-values each) take four different offsets -- group G = 0 takes offsets 0..3, G = 1 offsets 5..8 -- and one
 // MFMA step covers (tap dz, channel chunk c) of all four: lane group g supplies chunk c of its offset's neighbour
-// row, zeroed (v_cndmask) unless that neighbour's dz is the step's. Per 16-channel output block that is
-// 6 * C/16 + 1 steps (the last one the centre tap, lane groups >= C/16 zero) instead of 27 with up to 75 % K
-// padding: 19 instead of 27 MFMAs at C = 48, 13 at C = 32. Each lane reads its offset's codes once per group
-// (one ds_read_b128 per chunk and tile) and keeps them for the three dz steps; the next group's codes are read
-// into the registers of chunks already done. The weights of a step are one conflict-free 16-byte read per lane
-// from LDS, laid out in the MFMA operand order, read two steps ahead, and each read feeds the TT tiles' MFMAs.
+// row, or zeros unless that neighbour's dz is the step's. Per 16-channel output block that is 6 * C/16 + 1 steps
+// (the first one the centre tap, lane groups >= C/16 zero) instead of 27 with up to 75 % K padding: 19 instead of
+// 27 MFMAs at C = 48, 13 at C = 32. A lane reads its step operand per tile straight from LDS, from its neighbour row
+// or, when that neighbour is not the step's tap, from a 16-byte zero slot (one address select instead of zeroing
+// four registers: the matrix phase shares its SIMD's VALU with the other group's epilogue). The weights of a step
+// are one conflict-free 16-byte read per lane from LDS, laid out in the MFMA operand order; both operands are read
+// two steps ahead, and each weight read feeds the TT tiles' MFMAs.
 // The weights stay in LDS for the whole block; per-channel epilogue constants are staged in LDS too, so the
 // epilogue issues no dependent global loads.
 template <int C, int TT, int WG>
@@ -819,6 +816,7 @@ __global__ __launch_bounds__(128 * WG, 1) void spconv_colv_k(ColConvArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t s_x[2][G::XBYTES];
     __shared__ int s_z[2][G::ZWORDS];
     __shared__ float s_k[5][C];  // w_scale, bias, ln gamma, ln beta, out_w
+    __shared__ __attribute__((aligned(16))) v4i s_zx;  // the operand of a neighbour that is not the step's tap
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int grp = wv / WG, wq = wv - grp * WG, gtid = tid - grp * GT;
@@ -937,7 +935,8 @@ __global__ __launch_bounds__(128 * WG, 1) void spconv_colv_k(ColConvArgs a) {
         if (e < WCH) ((v4i*)s_w)[e] = wtmp[k];
     }
     if (nk > 0) commit();
-    __syncthreads();  // weights, constants and both groups' first windows visible
+    if (tid == 0) s_zx = v4i{0, 0, 0, 0};
+    __syncthreads();  // weights, constants, the zero slot and both groups' first windows visible
 
     constexpr bool kRes = EPI == PMG_EPI_R || EPI == PMG_EPI_RLN || EPI == PMG_EPI_ROUT;
     constexpr bool kSkipEarly = TT * NB <= 8;  // else the residual inputs would not fit in registers beside the MFMAs
@@ -980,60 +979,51 @@ __global__ __launch_bounds__(128 * WG, 1) void spconv_colv_k(ColConvArgs a) {
                     for (int j = 0; j < NB; ++j) w[j] = *(lds_v4i*)(wb + (st * NB + j) * 1024);
                 };
                 v4i Wt[3][NB];
-                v4i X[NCH][TT];  // codes of the current group's offsets
-                int zz[TT], dz[TT];
-                load_w(0, Wt[0]);
-                load_w(1, Wt[1]);
+                // Each step's codes are read from LDS per tile, two steps ahead like the weights: the lane's offset
+                // row, chunk c, when that neighbour is the step's tap dz, else the zero slot -- one address select
+                // per tile and step instead of zeroing 16 bytes (4 selects) per tile and step.
+                int dzg[2][TT];
 #pragma unroll
                 for (int t = 0; t < TT; ++t) {
-                    const v4i xc = *(lds_v4i*)(xcb + 16 * t * ROWB);
-                    X[0][t] = kin ? xc : v4i{0, 0, 0, 0};
+                    const int z0 = zg0[16 * t], z1 = zg1[16 * t];
+                    const bool in0 = (unsigned)(pi[t] + ri0) < (unsigned)H && (unsigned)(pj[t] + rj0) < (unsigned)W;
+                    const bool in1 = (unsigned)(pi[t] + ri1) < (unsigned)H && (unsigned)(pj[t] + rj1) < (unsigned)W;
+                    dzg[0][t] = in0 ? z0 - zc[t] + 1 : 3;  // 0, 1, 2: tap dz - 1; anything else: none
+                    dzg[1][t] = in1 ? z1 - zc[t] + 1 : 3;
                 }
+                const lds_u8* zs = (lds_u8*)&s_zx;
+                auto load_x = [&](int st, v4i (&xm)[TT]) {  // st compile-time after unrolling
 #pragma unroll
-                for (int t = 0; t < TT; ++t) zz[t] = zg0[16 * t];
+                    for (int t = 0; t < TT; ++t) {
+                        const lds_u8* p;
+                        if (st == 0) {  // the centre: the row itself, lanes g >= NCH are K padding
+                            p = kin ? xcb + 16 * t * ROWB : zs;
+                        } else {
+                            const int u = st - 1, gi = u / (3 * NCH), d = (u / NCH) % 3, c = u % NCH;
+                            p = dzg[gi][t] == d ? (gi == 0 ? xg0 : xg1) + (16 * t * ROWB + 16 * c) : zs;
+                        }
+                        xm[t] = *(lds_v4i*)p;
+                    }
+                };
+                v4i XM[3][TT];
+                load_w(0, Wt[0]);
+                load_x(0, XM[0]);
+                load_w(1, Wt[1]);
+                load_x(1, XM[1]);
 #pragma unroll
                 for (int st = 0; st < NSTEP; ++st) {
-                    const int u = st - 1, gi = u / (3 * NCH), d = (u / NCH) % 3, c = u % NCH;
-                    if (st + 2 < NSTEP) load_w(st + 2, Wt[(st + 2) % 3]);
-                    if (st == 1 + 2 * NCH) {  // group 1's keys, one dz pass ahead
-#pragma unroll
-                        for (int t = 0; t < TT; ++t) zz[t] = zg1[16 * t];
+                    if (st + 2 < NSTEP) {
+                        load_w(st + 2, Wt[(st + 2) % 3]);
+                        load_x(st + 2, XM[(st + 2) % 3]);
                     }
                     __builtin_amdgcn_sched_barrier(0);
-                    v4i xm[TT];
-                    if (st == 0) {
-#pragma unroll
-                        for (int t = 0; t < TT; ++t) xm[t] = X[0][t];
-                    } else {
-                        if (d == 0 && c == 0) {
-                            const int ri = gi == 0 ? ri0 : ri1, rj = gi == 0 ? rj0 : rj1;
-#pragma unroll
-                            for (int t = 0; t < TT; ++t) {
-                                const bool in =
-                                    (unsigned)(pi[t] + ri) < (unsigned)H && (unsigned)(pj[t] + rj) < (unsigned)W;
-                                dz[t] = in ? zz[t] - zc[t] + 1 : 3;  // 0, 1, 2: tap dz - 1; anything else: none
-                            }
-                        }
-#pragma unroll
-                        for (int t = 0; t < TT; ++t) xm[t] = dz[t] == d ? X[c][t] : v4i{0, 0, 0, 0};
-                    }
 #pragma unroll
                     for (int j = 0; j < NB; ++j)
 #pragma unroll
                         for (int t = 0; t < TT; ++t)
-                            acc[t][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(Wt[st % 3][j], xm[t], acc[t][j], 0, 0, 0);
+                            acc[t][j] =
+                                __builtin_amdgcn_mfma_i32_16x16x64_i8(Wt[st % 3][j], XM[st % 3][t], acc[t][j], 0, 0, 0);
                     __builtin_amdgcn_sched_barrier(0);
-                    // codes of the next group: after the centre, group 0's; during group 0's last dz pass, group
-                    // 1's chunk c into the registers of group 0's chunk c
-                    if (st == 0) {
-#pragma unroll
-                        for (int cc = 0; cc < NCH; ++cc)
-#pragma unroll
-                            for (int t = 0; t < TT; ++t) X[cc][t] = *(lds_v4i*)(xg0 + 16 * t * ROWB + 16 * cc);
-                    } else if (gi == 0 && d == 2) {
-#pragma unroll
-                        for (int t = 0; t < TT; ++t) X[c][t] = *(lds_v4i*)(xg1 + 16 * t * ROWB + 16 * c);
-                    }
                 }
             }
         } else if (kk < nk) {
