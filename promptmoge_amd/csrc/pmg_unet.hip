@@ -245,6 +245,15 @@ __global__ __launch_bounds__(256) void nmap_level_k(const int4* __restrict__ coo
 // ---------------------------------------------------------------------------------------------------------------
 // Row kernels on device-sized levels.
 
+// The row kernels below walk a level's rows in grid-stride loops over the count on the device: their grids are
+// capped (row_grid), so a coarse level of a few thousand rows does not launch the capacity's hundreds of
+// thousands of threads only to have them exit.
+constexpr int64_t kRowBlocksMax = 4096;  // 16 blocks of 256 threads per CU
+static unsigned row_grid(int64_t threads_cap) {
+    const int64_t b = (threads_cap + 255) / 256;
+    return (unsigned)(b < 1 ? 1 : (b < kRowBlocksMax ? b : kRowBlocksMax));
+}
+
 // PoolDown's mean (sparse_pool 'mean', _core.py:464-476: fp32 sums in input row order from 0, divided by the
 // child count) of coarse voxel o, quantised for the pool linear: codes = clamp(rint(mean * mult)). Threads per row
 // = C / 4 (a float4 each).
@@ -252,45 +261,47 @@ __global__ __launch_bounds__(256) void pool_quant_k(const float* __restrict__ x,
                                                     const int4* __restrict__ coords_c, const int64_t* __restrict__ count,
                                                     float mult, int8_t* __restrict__ codes) {
     const int tpr = C >> 2;
-    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int64_t o = gid / tpr;
-    const int cq = (int)(gid - o * tpr);
-    if (o >= *count) return;
-    const int4 oc = coords_c[o];
-    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    int n = 0;
+    const int64_t items = *count * tpr;
+    for (int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x; gid < items; gid += (int64_t)gridDim.x * 256) {
+        const int64_t o = gid / tpr;
+        const int cq = (int)(gid - o * tpr);
+        const int4 oc = coords_c[o];
+        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        int n = 0;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int i = 2 * oc.y + (q >> 1), j = 2 * oc.z + (q & 1);
-        if (i >= g.Hf || j >= g.Wf) continue;
-        int32_t lo, hi;
-        col_range(g.off, ((int64_t)oc.x * g.Hf + i) * g.Wf + j, lo, hi);
-        for (int32_t p = lo; p < hi; ++p) {
-            const int z = g.coords[p].w >> 1;
-            if (z > oc.w) break;
-            if (z == oc.w) {
-                const float4 v = *(const float4*)(x + (int64_t)p * C + 4 * cq);
-                acc.x = acc.x + v.x;
-                acc.y = acc.y + v.y;
-                acc.z = acc.z + v.z;
-                acc.w = acc.w + v.w;
-                ++n;
+        for (int q = 0; q < 4; ++q) {
+            const int i = 2 * oc.y + (q >> 1), j = 2 * oc.z + (q & 1);
+            if (i >= g.Hf || j >= g.Wf) continue;
+            int32_t lo, hi;
+            col_range(g.off, ((int64_t)oc.x * g.Hf + i) * g.Wf + j, lo, hi);
+            for (int32_t p = lo; p < hi; ++p) {
+                const int z = g.coords[p].w >> 1;
+                if (z > oc.w) break;
+                if (z == oc.w) {
+                    const float4 v = *(const float4*)(x + (int64_t)p * C + 4 * cq);
+                    acc.x = acc.x + v.x;
+                    acc.y = acc.y + v.y;
+                    acc.z = acc.z + v.z;
+                    acc.w = acc.w + v.w;
+                    ++n;
+                }
             }
         }
+        const float cnt = (float)n;
+        const float h[4] = {acc.x / cnt, acc.y / cnt, acc.z / cnt, acc.w / cnt};
+        store_codes4(h, mult, codes + o * C + 4 * cq);
     }
-    const float cnt = (float)n;
-    const float h[4] = {acc.x / cnt, acc.y / cnt, acc.z / cnt, acc.w / cnt};
-    store_codes4(h, mult, codes + o * C + 4 * cq);
 }
 
 // codes = clamp(rint(x * mult)) of a device-sized [rows][C] fp32 array (the input of NearestUp's linear).
 __global__ __launch_bounds__(256) void quant_rows_k(const float* __restrict__ x, int C, const int64_t* __restrict__ count,
                                                     float mult, int8_t* __restrict__ codes) {
-    const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;  // group of 4
-    if (q * 4 >= *count * C) return;
-    const float4 v = *(const float4*)(x + q * 4);
-    const float h[4] = {v.x, v.y, v.z, v.w};
-    store_codes4(h, mult, codes + q * 4);
+    const int64_t groups = *count * C / 4;  // groups of 4 values
+    for (int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x; q < groups; q += (int64_t)gridDim.x * 256) {
+        const float4 v = *(const float4*)(x + q * 4);
+        const float h[4] = {v.x, v.y, v.z, v.w};
+        store_codes4(h, mult, codes + q * 4);
+    }
 }
 
 // Row LayerNorm / SiLU / quantise in the 16-rows-per-wave layout of the fused epilogues (lane (r, g) holds
@@ -306,36 +317,39 @@ __global__ __launch_bounds__(256) void rows_ln_k(const float* __restrict__ x, co
                                                  int8_t* __restrict__ codes) {
     constexpr int NB = C / 16;
     const int64_t M = *count;
-    if ((int64_t)blockIdx.x * 64 >= M) return;
     const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
-    const int64_t m = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 16 + r;
-    const bool ok = m < M;
-    const int64_t mo = ok ? m : 0;
-    float y[NB][4];
-    const int64_t src = UP ? (int64_t)parent[mo] : mo;
+    // blocks of 64 rows, grid-stride (every lane of a wave runs each trip: the LayerNorm sums cross lanes)
+    for (int64_t blk = blockIdx.x; blk * 64 < M; blk += gridDim.x) {
+        const int64_t m = (blk * 4 + (threadIdx.x >> 6)) * 16 + r;
+        const bool ok = m < M;
+        const int64_t mo = ok ? m : 0;
+        float y[NB][4];
+        const int64_t src = UP ? (int64_t)parent[mo] : mo;
 #pragma unroll
-    for (int j = 0; j < NB; ++j) {
-        const float4 v = *(const float4*)(x + src * C + 16 * j + 4 * g);
-        y[j][0] = v.x;
-        y[j][1] = v.y;
-        y[j][2] = v.z;
-        y[j][3] = v.w;
-        if constexpr (UP) {
-            const float4 k = *(const float4*)(skip + mo * C + 16 * j + 4 * g);
-            y[j][0] = y[j][0] + k.x;
-            y[j][1] = y[j][1] + k.y;
-            y[j][2] = y[j][2] + k.z;
-            y[j][3] = y[j][3] + k.w;
-            if (ok) *(float4*)(y_out + mo * C + 16 * j + 4 * g) = make_float4(y[j][0], y[j][1], y[j][2], y[j][3]);
+        for (int j = 0; j < NB; ++j) {
+            const float4 v = *(const float4*)(x + src * C + 16 * j + 4 * g);
+            y[j][0] = v.x;
+            y[j][1] = v.y;
+            y[j][2] = v.z;
+            y[j][3] = v.w;
+            if constexpr (UP) {
+                const float4 k = *(const float4*)(skip + mo * C + 16 * j + 4 * g);
+                y[j][0] = y[j][0] + k.x;
+                y[j][1] = y[j][1] + k.y;
+                y[j][2] = y[j][2] + k.z;
+                y[j][3] = y[j][3] + k.w;
+                if (ok) *(float4*)(y_out + mo * C + 16 * j + 4 * g) = make_float4(y[j][0], y[j][1], y[j][2], y[j][3]);
+            }
+        }
+        if (!gamma) continue;
+        ln_silu_quad<NB, false>(y, gamma, beta, eps, g);
+        uint32_t pk[NB];
+        silu_codes_packed<NB>(y, mult, pk);
+        if (ok) {
+#pragma unroll
+            for (int j = 0; j < NB; ++j) *(uint32_t*)(codes + mo * C + 16 * j + 4 * g) = pk[j];
         }
     }
-    if (!gamma) return;
-    ln_silu_quad<NB, false>(y, gamma, beta, eps, g);
-    if (!ok) return;
-    uint32_t pk[NB];
-    silu_codes_packed<NB>(y, mult, pk);
-#pragma unroll
-    for (int j = 0; j < NB; ++j) *(uint32_t*)(codes + mo * C + 16 * j + 4 * g) = pk[j];
 }
 
 // The encoder feature, planar [B][K][RC] fp32, into int8 rows [B * RC][K] = clamp(rint(v * mult)): 64 x 64 tiles
@@ -375,21 +389,21 @@ __global__ __launch_bounds__(256) void concat_quant_k(const float* __restrict__ 
                                                       const int4* __restrict__ coords, const int64_t* __restrict__ count,
                                                       int C, int R, int Cc, float mult, int8_t* __restrict__ codes) {
     const int tpr = C >> 1;  // 2C channels, 4 per thread
-    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int64_t o = gid / tpr;
-    const int cq = (int)(gid - o * tpr);
-    if (o >= *count) return;
-    const int c = 4 * cq;
-    const float* src;
-    if (c < C) {
-        src = x + o * C + c;
-    } else {
-        const int4 v = coords[o];
-        src = enc_tok + (((int64_t)v.x * R + v.y) * Cc + v.z) * C + (c - C);
+    const int64_t items = *count * tpr;
+    for (int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x; gid < items; gid += (int64_t)gridDim.x * 256) {
+        const int64_t o = gid / tpr;
+        const int c = 4 * (int)(gid - o * tpr);
+        const float* src;
+        if (c < C) {
+            src = x + o * C + c;
+        } else {
+            const int4 v = coords[o];
+            src = enc_tok + (((int64_t)v.x * R + v.y) * Cc + v.z) * C + (c - C);
+        }
+        const float4 v = *(const float4*)src;
+        const float h[4] = {v.x, v.y, v.z, v.w};
+        store_codes4(h, mult, codes + o * 2 * C + c);
     }
-    const float4 v = *(const float4*)src;
-    const float h[4] = {v.x, v.y, v.z, v.w};
-    store_codes4(h, mult, codes + o * 2 * C + c);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -418,50 +432,65 @@ template <int NB, int EPI>
 __global__ __launch_bounds__(256) void gemm_i8_k(GemmArgs g) {
     const int64_t rows = g.rows_dev ? *g.rows_dev : g.rows_cap;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int64_t m0 = ((int64_t)blockIdx.x * 4 + wv) * 16;
-    if (m0 >= rows) return;
     const int r = lane & 15, gq = lane >> 4;
-    const int64_t row = m0 + r;
-    const bool row_ok = row < rows;
     const int n0 = blockIdx.y * 16 * NB;
     const int nchunk = g.K >> 4;
-    v4i acc[NB];
+    // blocks of 64 rows (16 per wave), grid-stride over the rows on the device
+    for (int64_t mb = blockIdx.x; mb * 64 < rows; mb += gridDim.x) {
+        const int64_t m0 = (mb * 4 + wv) * 16;
+        if (m0 >= rows) break;
+        const int64_t row = m0 + r;
+        const bool row_ok = row < rows;
+        v4i acc[NB];
 #pragma unroll
-    for (int j = 0; j < NB; ++j) acc[j] = v4i{0, 0, 0, 0};
-    for (int q0 = 0; q0 < nchunk; q0 += 4) {
-        const int q = q0 + gq;
-        v4i av = {0, 0, 0, 0};
-        v4i bv[NB];
-        if (q < nchunk) {
-            if (row_ok) av = *(const v4i*)(g.a + row * g.K + q * 16);
+        for (int j = 0; j < NB; ++j) acc[j] = v4i{0, 0, 0, 0};
+        // K in steps of 4 chunks (one per lane group), the next step's operands requested before this step's
+        // MFMAs. Loads are unconditional (a clamped address; the padding chunks and rows past the end are zeroed
+        // when used), so the memory waits name exactly the step they need.
+        const int64_t arow = (row_ok ? row : 0) * g.K;
+        auto load = [&](int q0, v4i& av, v4i (&bv)[NB]) {
+            const int q = q0 + gq < nchunk ? q0 + gq : nchunk - 1;
+            av = *(const v4i*)(g.a + arow + q * 16);
 #pragma unroll
             for (int j = 0; j < NB; ++j) bv[j] = *(const v4i*)(g.w + (int64_t)(n0 + 16 * j + r) * g.K + q * 16);
-        } else {
+        };
+        auto mma = [&](int q0, const v4i& av, const v4i (&bv)[NB]) {
+            const bool on = q0 + gq < nchunk;
+            const v4i z = {0, 0, 0, 0};
+            const v4i a = on && row_ok ? av : z;
 #pragma unroll
-            for (int j = 0; j < NB; ++j) bv[j] = v4i{0, 0, 0, 0};
+            for (int j = 0; j < NB; ++j)
+                acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, on ? bv[j] : z, acc[j], 0, 0, 0);
+        };
+        v4i a0, a1, b0[NB], b1[NB];
+        load(0, a0, b0);
+        for (int q0 = 0; q0 < nchunk; q0 += 8) {
+            if (q0 + 4 < nchunk) load(q0 + 4, a1, b1);
+            mma(q0, a0, b0);
+            if (q0 + 4 >= nchunk) break;
+            if (q0 + 8 < nchunk) load(q0 + 8, a0, b0);
+            mma(q0 + 4, a1, b1);
         }
 #pragma unroll
-        for (int j = 0; j < NB; ++j) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv[j], acc[j], 0, 0, 0);
-    }
+        for (int j = 0; j < NB; ++j) {
+            const int n = n0 + 16 * j + r;
+            const float ws = g.w_scale[n], bs = g.bias ? g.bias[n] : 0.0f;
 #pragma unroll
-    for (int j = 0; j < NB; ++j) {
-        const int n = n0 + 16 * j + r;
-        const float ws = g.w_scale[n], bs = g.bias ? g.bias[n] : 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int64_t m = m0 + 4 * gq + i;
-            if (m >= rows) continue;
-            float y = (float)acc[j][i] * g.a_scale;
-            y = y * ws;
-            if (g.bias) y = y + bs;
-            if constexpr (EPI == PMG_EPI_Q) {
-                ((int8_t*)g.out)[m * g.N + n] = silu_quant_i8(y, g.out_mult);
-            } else {
-                if (g.planar_add) {
-                    const int64_t b = m / g.planar_rc, rc = m - b * g.planar_rc;
-                    y = y + g.planar_add[(b * g.N + n) * g.planar_rc + rc];
+            for (int i = 0; i < 4; ++i) {
+                const int64_t m = m0 + 4 * gq + i;
+                if (m >= rows) continue;
+                float y = (float)acc[j][i] * g.a_scale;
+                y = y * ws;
+                if (g.bias) y = y + bs;
+                if constexpr (EPI == PMG_EPI_Q) {
+                    ((int8_t*)g.out)[m * g.N + n] = silu_quant_i8(y, g.out_mult);
+                } else {
+                    if (g.planar_add) {
+                        const int64_t b = m / g.planar_rc, rc = m - b * g.planar_rc;
+                        y = y + g.planar_add[(b * g.N + n) * g.planar_rc + rc];
+                    }
+                    ((float*)g.out)[m * g.N + n] = y;
                 }
-                ((float*)g.out)[m * g.N + n] = y;
             }
         }
     }
@@ -472,7 +501,11 @@ static int launch_gemm(const GemmArgs& g, int epi, hipStream_t s) {
     if (g.rows_cap == 0) return PMG_OK;
     const int b = g.N / 16;
     const int nb = b % 4 == 0 ? 4 : (b % 2 == 0 ? 2 : 1);
-    const dim3 grid((unsigned)((g.rows_cap + 63) / 64), (unsigned)(g.N / (16 * nb)));
+    const unsigned gy = (unsigned)(g.N / (16 * nb));
+    int64_t gx = (g.rows_cap + 63) / 64;
+    const int64_t gx_max = kRowBlocksMax / gy > 0 ? kRowBlocksMax / gy : 1;  // device-sized rows: grid-stride
+    if (g.rows_dev && gx > gx_max) gx = gx_max;
+    const dim3 grid((unsigned)gx, gy);
 #define PMG_GEMM_CASE(NBV)                                                                       \
     if (nb == NBV) {                                                                             \
         if (epi == PMG_EPI_Q)                                                                    \
@@ -509,7 +542,7 @@ static int launch_rows_ln(bool up, int C, const float* x, const int32_t* parent,
                           const int64_t* count, int64_t cap, const float* gamma, const float* beta, float mult,
                           float* y_out, int8_t* codes, hipStream_t s) {
     if (cap == 0) return PMG_OK;
-    const dim3 grid((unsigned)((cap + 63) / 64));
+    const dim3 grid(row_grid(cap * 4));  // 64 rows (256 threads) per block, grid-stride
     if (up) {
         PMG_LN_SWITCH(C, hipLaunchKernelGGL((rows_ln_k<CC, true>), grid, dim3(256), 0, s, x, parent, skip, count,
                                             gamma, beta, 1e-6f, mult, y_out, codes));
@@ -761,8 +794,7 @@ static int enqueue_unet(pmg_unet* u, const float* feats, const int32_t* coords, 
         if (k + 1 == L) break;
         const int Ck = c.channels[k], Cn = c.channels[k + 1];
         PoolGeom g{u->coords[k], u->off[k], c.B, u->Hk[k], u->Wk[k], u->Hk[k + 1], u->Wk[k + 1]};
-        const int64_t thr = cap * (Ck / 4);
-        hipLaunchKernelGGL(pool_quant_k, dim3((unsigned)((thr + 255) / 256)), dim3(256), 0, s, u->xd[k], Ck, g,
+        hipLaunchKernelGGL(pool_quant_k, dim3(row_grid(cap * (Ck / 4))), dim3(256), 0, s, u->xd[k], Ck, g,
                            u->coords[k + 1], u->counts + k + 1, u->pool[k].q_mult, u->codes);
         if (int e = check_launch("pool_quant_k")) return e;
         if (int e = linear(u, u->codes, u->counts + k + 1, cap, Ck, u->pool[k], Cn, PMG_EPI_BIAS, 0.0f, u->xd[k + 1],
@@ -783,8 +815,7 @@ static int enqueue_unet(pmg_unet* u, const float* feats, const int32_t* coords, 
         if (int e = linear(u, u->enc_codes, nullptr, u->T, c.enc_channels, u->enc, CL, PMG_EPI_BIAS, 0.0f,
                            u->enc_tok, enc_bias, s))
             return e;
-        const int64_t thr = cap * (CL / 2);
-        hipLaunchKernelGGL(concat_quant_k, dim3((unsigned)((thr + 255) / 256)), dim3(256), 0, s, u->xd[top],
+        hipLaunchKernelGGL(concat_quant_k, dim3(row_grid(cap * (CL / 2))), dim3(256), 0, s, u->xd[top],
                            u->enc_tok, u->coords[top], u->counts + top, CL, u->R, u->Cc, u->fuse0.q_mult, u->codes);
         if (int e = check_launch("concat_quant_k")) return e;
         if (int e = linear(u, u->codes, u->counts + top, cap, 2 * CL, u->fuse0, CL, PMG_EPI_Q, u->fuse2.q_mult,
@@ -804,7 +835,7 @@ static int enqueue_unet(pmg_unet* u, const float* feats, const int32_t* coords, 
     for (int i = 0; i + 1 < L; ++i) {
         const int t = L - 2 - i;
         const int Cs = c.channels[t + 1], Ct = c.channels[t];
-        hipLaunchKernelGGL(quant_rows_k, dim3((unsigned)((cap * Cs / 4 + 255) / 256)), dim3(256), 0, s, cur, Cs,
+        hipLaunchKernelGGL(quant_rows_k, dim3(row_grid(cap * Cs / 4)), dim3(256), 0, s, cur, Cs,
                            u->counts + t + 1, u->up[i].q_mult, u->codes);
         if (int e = check_launch("quant_rows_k")) return e;
         if (int e = linear(u, u->codes, u->counts + t + 1, cap, Cs, u->up[i], Ct, PMG_EPI_BIAS, 0.0f, u->lin,
