@@ -549,27 +549,43 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2r_k(ConvArgs a) {
                 __builtin_amdgcn_sched_barrier(0);
             }
         };
+        // The wave walks only its own active taps (no barrier binds it to the block's union): a scalar queue holds
+        // the taps of this step and the next three (27 after the last: out-of-range indices, zeros, no MFMAs).
+        uint32_t rem = wmask;
+        auto pop = [&]() {
+            const int v = rem ? (int)__builtin_ctz(rem) : 27;
+            rem = rem ? rem & (rem - 1) : 0u;
+            return v;
+        };
+        const int ntap = __builtin_popcount(wmask);
+        int v0 = pop(), v1 = pop(), v2 = pop(), v3 = pop();
         int I[2][T];
         v4i X[2][T][KS];
         {
             int i0[T];
-            idx_load(0, i0);
-            idx_load(1, I[1]);
-            idx_load(2, I[0]);
+            idx_load(v0, i0);
+            idx_load(v1, I[1]);
+            idx_load(v2, I[0]);
             gather(i0, X[0]);
         }
-        auto tap = [&](auto Pc, int v) {
+        // step k: the codes of tap k+1 (indices loaded two steps ago) and the indices of tap k+3 are requested,
+        // then tap k's MFMAs run
+        auto tap = [&](auto Pc) {
             constexpr int p = decltype(Pc)::value;
             gather(I[p ^ 1], X[p ^ 1]);
-            idx_load(v + 3, I[p ^ 1]);
+            idx_load(v3, I[p ^ 1]);
             __builtin_amdgcn_sched_barrier(0);
-            if (v < 27 && ((wmask >> v) & 1u)) mma_tap(v, X[p]);
+            if (v0 < 27) mma_tap(v0, X[p]);
             __builtin_amdgcn_sched_barrier(0);
+            v0 = v1;
+            v1 = v2;
+            v2 = v3;
+            v3 = pop();
         };
 #pragma unroll 1
-        for (int v = 0; v < 27; v += 2) {
-            tap(std::integral_constant<int, 0>{}, v);
-            tap(std::integral_constant<int, 1>{}, v + 1);
+        for (int k = 0; k < ntap; k += 2) {
+            tap(std::integral_constant<int, 0>{});
+            tap(std::integral_constant<int, 1>{});
         }
 #pragma unroll
         for (int t = 0; t < T; ++t) {
