@@ -41,7 +41,69 @@ struct ConvArgs {
     const int32_t* order;  // rows in processing order (tile masks follow it), or NULL for 0 .. M-1
     const int64_t* m_dev;  // spconv_k: the row count on the device (<= M, which is then the map's row stride and
                            // the grid's capacity), or NULL for M rows
+    int32_t* part;         // device-sized spconv_g2_k: int32 partial sums of a tap split ([Z][rows][Co]), or NULL
 };
+
+// Tap split of the device-sized weight-staged convolution: when a level has few chunks (a coarse U-Net level of a
+// few thousand rows keeps a handful of CUs busy for 27 dependent taps), each (chunk, range of taps) is a unit of
+// its own and stores exact int32 partial sums; split_epilogue_k, the next launch on the stream, adds them in order
+// and applies the epilogue. (Finishing in the last unit to arrive instead needs an agent-scope release per unit,
+// an L2 write-back on CDNA: measured slower than the second launch.) The factor follows from the row count on the
+// device: as many units as fit one round of blocks.
+constexpr int kSplitUnits = 256;  // units aimed at (chunks x output slices x Z): one block per CU of MI355X
+constexpr int kSplitMax = 9;
+__host__ __device__ inline int split_factor(int nchunk, int nslice) {
+    const int cs = nchunk * nslice;
+    const int z = cs > 0 ? kSplitUnits / cs : 1;
+    return z < 1 ? 1 : (z > kSplitMax ? kSplitMax : z);
+}
+
+// Row m, output channels c .. c+3 of a tap-split launch: the Z partial sums added in order (int32: exact, the
+// unsplit accumulator) and the epilogue of the device-sized convolution in the same arithmetic.
+template <int EPI>
+__device__ inline void split_finish(const ConvArgs& a, int Z, int M, int64_t m, int c) {
+    const int Co = a.Co;
+    v4i acc = *(const v4i*)(a.part + m * Co + c);
+    for (int z = 1; z < Z; ++z) acc += *(const v4i*)(a.part + ((int64_t)z * M + m) * Co + c);
+    const int64_t o = m * Co + c;
+    if constexpr (EPI == PMG_EPI_ACC) {
+        *(v4i*)((int32_t*)a.out + o) = acc;
+    } else {
+        float y[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float u = (float)acc[i] * a.a_scale;
+            u = u * a.w_scale[c + i];
+            if (a.bias) u = u + a.bias[c + i];
+            y[i] = u;
+        }
+        if constexpr (EPI == PMG_EPI_Q) {
+            store_silu_codes4(y, a.out_mult, (int8_t*)a.out + o);
+        } else if constexpr (EPI == PMG_EPI_QLIN) {
+            store_codes4(y, a.out_mult, (int8_t*)a.out + o);
+        } else if constexpr (EPI == PMG_EPI_R) {
+            const v4f sk = *(const v4f*)(a.skip + o);
+            *(v4f*)((float*)a.out + o) = v4f{y[0] + sk[0], y[1] + sk[1], y[2] + sk[2], y[3] + sk[3]};
+        } else {
+            *(v4f*)((float*)a.out + o) = v4f{y[0], y[1], y[2], y[3]};
+        }
+    }
+}
+
+// The second launch of a tap split: the row count and Z read again on the device exactly as spconv_g2_k reads
+// them (CHUNK rows per chunk, nslice output slices); nothing to do when that launch did not split.
+template <int EPI, int CHUNK>
+__global__ __launch_bounds__(256) void split_epilogue_k(ConvArgs a, int nslice) {
+    const int M = (int)*a.m_dev;
+    const int Z = split_factor((M + CHUNK - 1) / CHUNK, nslice);
+    if (Z < 2) return;
+    const int Q4 = a.Co / 4;
+    const int64_t total = (int64_t)M * Q4;
+    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+        const int64_t m = e / Q4;
+        split_finish<EPI>(a, Z, M, m, 4 * (int)(e - m * Q4));
+    }
+}
 
 template <typename T>
 struct Acc;
@@ -240,6 +302,7 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
     static_assert(T == 1 || T == 2 || T == 4, "tiles per wave");
     static_assert(RS == 2 || RS == 4, "ring slots: the tap parity or v mod 4 of a trip");
     constexpr int GD = RS - 1;                           // gather distance in taps
+    constexpr bool kDev = RS == 4;                       // the device-sized launch (tap split allowed)
 
     __shared__ __attribute__((aligned(16))) v4i s_w[2][GRP * NF * 64];
     __shared__ float s_k[2][NS];
@@ -264,15 +327,20 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
     }
 
     const int nchunk = (M + CHUNK - 1) / CHUNK;
+    // units: (chunk, z) with z the z-th of Z ranges of taps; Z = 1 (a unit is a chunk, all 27 taps) unless this is
+    // a device-sized launch with a partials buffer and few chunks
+    const int Z = kDev && a.part ? split_factor(nchunk, (int)gridDim.y) : 1;
+    const int nunit = nchunk * Z;
     const int G = gridDim.x, b = blockIdx.x;
     const int nx = G >= 8 ? 8 : 1;
     const int x = b % nx, bi = b / nx, nbx = (G - x + nx - 1) / nx;
-    const int c0 = (int)((int64_t)nchunk * x / nx), c1 = (int)((int64_t)nchunk * (x + 1) / nx);
+    const int c0 = (int)((int64_t)nunit * x / nx), c1 = (int)((int64_t)nunit * (x + 1) / nx);
+    int t0 = 0, t1 = 27;  // the unit's taps [t0, t1)
 
     // Weights of group grp through registers into LDS (no LDS DMA: the compiler then keeps exact vmcnt waits for
     // the gathers). Fragment f = wv + 8k of the group is tap slot q = f / NF, operand js = f % NF = (j, s), and
-    // lane l holds W[16j + (l & 15)][v][64s + 16(l >> 4) .. +16] of the [Co][27][Ci] tensor; taps >= 27 load zeros
-    // (out-of-range buffer offset).
+    // lane l holds W[16j + (l & 15)][v][64s + 16(l >> 4) .. +16] of the [Co][27][Ci] tensor; taps >= t1 load
+    // zeros (out-of-range buffer offset).
     const int wlane = ((n0 + r) * 27) * C + 16 * g;
     // staged in PARTS pieces of WPP fragments per wave, one piece per tap of the group where that divides evenly
     // (C = 128: 8 registers held for one tap instead of 16 for the whole group)
@@ -283,8 +351,8 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
             const int f = wv + kG2Waves * (part * WPP + kk);
             const int q = f / NF, js = f - (f / NF) * NF;
             const int j = js / KS, s2 = js - (js / KS) * KS;
-            const int v = GRP * grp + q;
-            const int off = v < 27 ? wlane + ((16 * j * 27) + v) * C + 64 * s2 : (int)0x80000000;
+            const int v = t0 + GRP * grp + q;
+            const int off = v < t1 ? wlane + ((16 * j * 27) + v) * C + 64 * s2 : (int)0x80000000;
             st[kk] = __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 0);
         }
     };
@@ -293,7 +361,13 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
         for (int kk = 0; kk < WPP; ++kk) dst[(wv + kG2Waves * (part * WPP + kk)) * 64 + lane] = st[kk];
     };
 
-    for (int ch = c0 + bi; ch < c1; ch += nbx) {
+    for (int un = c0 + bi; un < c1; un += nbx) {
+        const int ch = Z == 1 ? un : un / Z, z = un - ch * Z;
+        if constexpr (kDev) {
+            t0 = 27 * z / Z;
+            t1 = 27 * (z + 1) / Z;
+        }
+        const int trips = kDev ? (t1 - t0 + 3) / 4 : NG2;  // trips of 4 taps (two groups)
         const int pos0 = ch * CHUNK + wv * (16 * T) + r;
         // map offset of each tile's row; rows beyond M get an out-of-range offset (their indices load as 0)
         int roff[T];
@@ -316,10 +390,10 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
 #pragma unroll
             for (int j = 0; j < NB; ++j) acc[t][j] = v4i{0, 0, 0, 0};
 
-        // map indices of tap v (taps >= 27: out-of-range, zeros); gathers of the rows they name (absent: zeros).
+        // map indices of tap v (taps >= t1: out-of-range, zeros); gathers of the rows they name (absent: zeros).
         // Every load is issued unconditionally, so the compiler's vmcnt waits stay exact.
         auto idx_load = [&](int v, int (&id)[T]) {
-            const int vo = (v < 27 ? v : 27) * S * 4;
+            const int vo = (v < t1 ? v : 27) * S * 4;
 #pragma unroll
             for (int t = 0; t < T; ++t) id[t] = __builtin_amdgcn_raw_buffer_load_b32(nr, roff[t], vo, 0);
         };
@@ -371,10 +445,10 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
             gather(i0, X[0]);
         } else {
 #pragma unroll
-            for (int u = 0; u < RS; ++u) idx_load(u, I[u]);
+            for (int u = 0; u < RS; ++u) idx_load(t0 + u, I[u]);
 #pragma unroll
             for (int u = 0; u < GD; ++u) gather(I[u], X[u]);
-            idx_load(RS, I[0]);
+            idx_load(t0 + RS, I[0]);
         }
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's weight stores are in LDS
         __builtin_amdgcn_s_barrier();
@@ -389,8 +463,8 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
             v4i sta[RS == 2 ? 1 : PARTS][WPP];  // RS = 4: the next group's weights, all requested at its start
 #pragma unroll
             for (int q = 0; q < GRP; ++q) {
-                const int v = GRP * grp + q;
-                const int p = (GRP * H + q) & 3;  // v mod 4 (GRP * grp = 4 * trip + GRP * H)
+                const int v = t0 + GRP * grp + q;
+                const int p = (GRP * H + q) & 3;  // (v - t0) mod 4 (GRP * grp = 4 * trip + GRP * H)
                 v4i st[WPP];
                 if constexpr (RS == 2) {
                     if (q < PARTS) w_load(grp + 1, q, st);
@@ -401,7 +475,7 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
                 gather(I[(p + GD) % RS], X[(p + GD) % RS]);
                 idx_load(v + GD + 2, I[(p + GD + 2) % RS]);
                 __builtin_amdgcn_sched_barrier(0);
-                if (v < 27 && ((wmask >> v) & 1u)) mma_tap(s_w[H] + q * NF * 64, X[p % RS]);
+                if (v < t1 && ((wmask >> v) & 1u)) mma_tap(s_w[H] + q * NF * 64, X[p % RS]);
                 __builtin_amdgcn_sched_barrier(0);
                 if constexpr (RS == 2) {
                     if (q < PARTS) w_store(s_w[H ^ 1], q, st);
@@ -415,11 +489,22 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
             __builtin_amdgcn_sched_barrier(0);
         };
 #pragma unroll 1
-        for (int it = 0; it < NG2; ++it) {
+        for (int it = 0; it < trips; ++it) {
             group(std::integral_constant<int, 0>{}, 2 * it);
             group(std::integral_constant<int, 1>{}, 2 * it + 1);
         }
 
+        if (kDev && Z > 1) {  // a tap range: the exact partial sums, [Z][M][Co]
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                if (pos0 + 16 * t >= M) continue;
+                const int m = roff[t] >> 2;
+#pragma unroll
+                for (int j = 0; j < NB; ++j)
+                    *(v4i*)(a.part + ((int64_t)z * M + m) * Co + n0 + 16 * j + 4 * g) = acc[t][j];
+            }
+            continue;  // split_epilogue_k adds the Z partials and applies the epilogue
+        }
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             if (pos0 + 16 * t >= M) continue;
@@ -676,6 +761,7 @@ static int launch_g2_dev(const ConvArgs& a, int epilogue, hipStream_t s) {
     const dim3 grid((unsigned)(nchunk < cus ? nchunk : cus), (unsigned)(a.Co / (16 * NB)));
     if constexpr (C == 64) {
         static_assert(NB == 4, "C = 64 keeps all 64 output channels");
+        static_assert(RS == 2, "the resident-weight kernel has no tap split");
         switch (epilogue) {
             case PMG_EPI_ACC: hipLaunchKernelGGL((spconv_g2r_k<C, PMG_EPI_ACC, T, PF>), grid, dim3(kG2Threads), 0, s, a); break;
             case PMG_EPI_Q: hipLaunchKernelGGL((spconv_g2r_k<C, PMG_EPI_Q, T, PF>), grid, dim3(kG2Threads), 0, s, a); break;
@@ -692,6 +778,34 @@ static int launch_g2_dev(const ConvArgs& a, int epilogue, hipStream_t s) {
         }
         return check_launch("spconv_g2_k");
     }
+}
+
+// A device-sized weight-staged launch with the tap split allowed when the partials buffer holds its largest case
+// (Z * rows * Co * 4 bytes: at most kSplitUnits * chunk * Co / slices * 4, since Z * chunks * slices <= kSplitUnits),
+// followed by split_epilogue_k.
+template <int C, int NB, int T, int PF>
+static int launch_g2_dev_split(ConvArgs a, int epilogue, int32_t* part, int64_t part_bytes, hipStream_t s) {
+    constexpr int CHUNK = kG2Waves * T * 16;
+    const int64_t need = (int64_t)kSplitUnits * CHUNK * (16 * NB) * 4;
+    a.part = part && part_bytes >= need ? part : nullptr;
+    const int rc = launch_g2_dev<C, NB, T, PF, 4>(a, epilogue, s);
+    if (rc || !a.part) return rc;
+    const int nslice = a.Co / (16 * NB);
+    const int64_t blocks = (a.M * (a.Co / 4) + 255) / 256;
+    const dim3 grid((unsigned)(blocks < 1024 ? blocks : 1024));
+    switch (epilogue) {
+        case PMG_EPI_ACC: hipLaunchKernelGGL((split_epilogue_k<PMG_EPI_ACC, CHUNK>), grid, dim3(256), 0, s, a, nslice); break;
+        case PMG_EPI_Q: hipLaunchKernelGGL((split_epilogue_k<PMG_EPI_Q, CHUNK>), grid, dim3(256), 0, s, a, nslice); break;
+        case PMG_EPI_R: hipLaunchKernelGGL((split_epilogue_k<PMG_EPI_R, CHUNK>), grid, dim3(256), 0, s, a, nslice); break;
+        default: hipLaunchKernelGGL((split_epilogue_k<PMG_EPI_BIAS, CHUNK>), grid, dim3(256), 0, s, a, nslice); break;
+    }
+    return check_launch("split_epilogue_k");
+}
+
+int64_t conv_split_bytes(int C) {
+    if (C == 128) return (int64_t)kSplitUnits * (kG2Waves * 2 * 16) * 128 * 4;
+    if (C == 256) return (int64_t)kSplitUnits * (kG2Waves * 1 * 16) * 128 * 4;
+    return 0;
 }
 
 int launch_conv_i8_dev(const DevConv& d, hipStream_t s) {
@@ -722,8 +836,8 @@ int launch_conv_i8_dev(const DevConv& d, hipStream_t s) {
     const bool fits32 = d.cap * 27 * 4 < ((int64_t)1 << 31) && d.cap * d.Ci < ((int64_t)1 << 31);
     if (fits32 && d.Ci == d.Co) {
         if (d.Ci == 64) return launch_g2_dev<64, 4, 2, 2, 2>(a, d.epilogue, s);
-        if (d.Ci == 128) return launch_g2_dev<128, 8, 2, 3, 4>(a, d.epilogue, s);
-        if (d.Ci == 256) return launch_g2_dev<256, 8, 1, 3, 4>(a, d.epilogue, s);
+        if (d.Ci == 128) return launch_g2_dev_split<128, 8, 2, 3>(a, d.epilogue, d.part, d.part_bytes, s);
+        if (d.Ci == 256) return launch_g2_dev_split<256, 8, 1, 3>(a, d.epilogue, d.part, d.part_bytes, s);
     }
     const int nb = pick_nb(d.Co);
     switch (d.epilogue) {

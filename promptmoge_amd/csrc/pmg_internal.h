@@ -117,8 +117,10 @@ int launch_conv_col(int precision, const ColConvArgs& a, int C, int epi, hipStre
 int launch_anchor(float* points, int B, int H, int W, const float* lidar, const float* conf, int dh, int dw,
                   const float* st, float beta, hipStream_t s);
 
-// int8 submanifold conv on a device-sized level (generic map, spconv_k): rows m < *m_dev of a capacity-`cap` level;
-// nmap_t is [27][cap] and tile_mask covers the rows. Epilogues ACC, BIAS, Q (SiLU requantise), R (+ skip).
+// int8 submanifold conv on a device-sized level (generic map): rows m < *m_dev of a capacity-`cap` level; nmap_t is
+// [27][cap] and tile_mask covers the rows. Epilogues ACC, BIAS, Q (SiLU requantise), R (+ skip). With a partials
+// buffer of conv_split_bytes(C) bytes (C = 128, 256), a level with few rows splits its taps over more blocks and a
+// second launch adds the partial sums (launches on one stream may share the buffer).
 struct DevConv {
     const int8_t* x;
     const int32_t* nmap_t;
@@ -134,7 +136,10 @@ struct DevConv {
     float out_mult;
     const float* skip;
     void* out;
+    int32_t* part;       // tap-split partial sums, or NULL
+    int64_t part_bytes;
 };
 int launch_conv_i8_dev(const DevConv& d, hipStream_t s);
+int64_t conv_split_bytes(int C);  // partials buffer of a width's tap split (0: no split at that width)
 
 }  // namespace pmg

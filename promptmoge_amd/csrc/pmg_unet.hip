@@ -593,6 +593,8 @@ struct pmg_unet {
     float* lin = nullptr;               // NearestUp linear output [cap][Cmax]
     int8_t* enc_codes = nullptr;        // [T][enc_channels]
     float* enc_tok = nullptr;           // [T][C_L]
+    int32_t* part = nullptr;            // tap-split partial sums of the coarsest level's convolutions
+    int64_t part_bytes = 0;
 
     bool have_weights = false;
     const float* in_w = nullptr;
@@ -673,6 +675,12 @@ static int enqueue_block(pmg_unet* u, int k, const pmg_block_weights& bk, const 
     c1.bias = bk.b1;
     c1.out_mult = bk.q2_mult;
     c1.out = u->q2;
+    // the tap split (a second launch) only at the coarsest level: the capacity does not bound a level's rows, and
+    // at the finer levels, with too many rows to split, that launch would only cost its dispatch
+    if (k == u->L - 1 && k > 0) {
+        c1.part = u->part;
+        c1.part_bytes = u->part_bytes;
+    }
     if (int e = launch_conv_i8_dev(c1, s)) return e;
     DevConv c2 = c1;
     c2.x = u->q2;
@@ -936,6 +944,8 @@ pmg_unet* pmg_unet_create(const pmg_unet_config* cfg) {
     take((void**)&u->lin, (size_t)4 * cap * u->Cmax);
     take((void**)&u->enc_codes, (size_t)u->T * c.enc_channels);
     take((void**)&u->enc_tok, (size_t)4 * u->T * CL);
+    if (L > 1) u->part_bytes = conv_split_bytes(c.channels[L - 1]);
+    if (u->part_bytes > 0) take((void**)&u->part, (size_t)u->part_bytes);
     for (auto& p : plan) off += ualign(p.second);
     u->arena_bytes = off;
     if (hipMalloc(&u->arena, u->arena_bytes) != hipSuccess) {
