@@ -268,23 +268,33 @@ def microbench(stream):
     with torch.cuda.stream(stream):
         cd = torch.from_numpy(coords).to(dev)
         shape = (1, 1024, 1024, 1024)
-        ntu, tmu, _ = ops.nmap_hash(cd, shape)
+        ntu, tmu, nru, rmu = ops.nmap_hash(cd, shape, rows=True, row_mask=True)
         torch.cuda.synchronize()
-        hash_ms = graph_ms(lambda: ops.nmap_hash(cd, shape), 5, stream)
+        hash_ms = graph_ms(lambda: ops.nmap_hash(cd, shape, row_mask=True), 5, stream)
+        # the map's processing order (rows sorted by tap mask, the map permuted into it): built once per map, like
+        # the map itself, and read by every convolution on it
+        order, otm, nmo = ops.row_order(rmu, nru)
+        torch.cuda.synchronize()
+        order_ms = graph_ms(lambda: ops.row_order(rmu, nru), 5, stream)
         pu = int((ntu >= 0).sum().item())
         M = coords.shape[0]
         micro = {"voxels": int(M), "pairs": pu, "mean_active_taps": round(pu / M, 3), "hash_map_ms": round(hash_ms, 4),
-                 "hash_map_gbs": round((16 * M + 108 * M) / (hash_ms * 1e-3) / 1e9, 1)}
+                 "hash_map_gbs": round((16 * M + 108 * M) / (hash_ms * 1e-3) / 1e9, 1),
+                 "row_order_ms": round(order_ms, 4)}
         g = torch.Generator(device="cpu").manual_seed(5)
         for Cm in (64, 128):
             xm = torch.randint(-127, 128, (M, Cm), generator=g, dtype=torch.int8).to(dev)
             wm = torch.randint(-127, 128, (Cm, 3, 3, 3, Cm), generator=g, dtype=torch.int8).to(dev)
             sm = torch.full((Cm,), 1e-4, device=dev)
             om = torch.empty((M, Cm), dtype=torch.int8, device=dev)
-            # the microbenchmark's epilogue: per-channel requantisation q = clamp(rint(acc * m[n]), +-127)
-            t = graph_ms(lambda: ops.spconv_i8(xm, ntu, tmu, wm, ops.EPI_QLIN, w_scale=sm, out=om), 5, stream)
+            # the microbenchmark's epilogue: per-channel requantisation q = clamp(rint(acc * m[n]), +-127); rows in
+            # the map's processing order (the caller's order timed beside it)
+            t = graph_ms(lambda: ops.spconv_i8_ordered(xm, nmo, order, otm, wm, ops.EPI_QLIN, w_scale=sm, out=om),
+                         5, stream)
+            t_u = graph_ms(lambda: ops.spconv_i8(xm, ntu, tmu, wm, ops.EPI_QLIN, w_scale=sm, out=om), 5, stream)
             tops = 2 * Cm * Cm * pu / (t * 1e-3) / 1e12
-            micro[f"C{Cm}"] = {"ms": round(t, 4), "tops": round(tops, 2), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
+            micro[f"C{Cm}"] = {"ms": round(t, 4), "tops": round(tops, 2), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+                               "ms_caller_order": round(t_u, 4)}
     return micro
 
 

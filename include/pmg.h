@@ -91,14 +91,16 @@ int pmg_nmap_hash(const int32_t* coords, int64_t M, const int64_t* sparse_shape_
                   size_t workspace_bytes, void* stream);
 
 /* pmg_row_order -- a processing order for pmg_spconv_i8_ordered (no counterpart in the reference; it changes no
- * result): within each window of 4096 consecutive rows, the rows sorted, stably, by the top 16 bits of their
- * 27-bit tap mask (row_mask [M], bit v = tap v present, as pmg_nmap_hash writes it), so that 16-row tiles share
- * their taps while each window keeps its rows' neighbourhood. order [M] int32 = row indices (order[i] lies in
- * the window of i); order_tile_mask [ceil(M/16)] = the union of the tap masks of order[16t .. 16t+15]. The
- * workspace is not used (pmg_row_order_workspace_bytes returns a nominal 256 bytes). */
+ * result): the rows sorted, stably, by their 27-bit tap mask (row_mask [M], bit v = tap v present, as
+ * pmg_nmap_hash writes it), so that the tiles and chunks of the convolution run few taps while rows of one
+ * neighbourhood pattern keep the caller's order. order [M] int32 = row indices in processing order;
+ * order_tile_mask [ceil(M/16)] = the union of the tap masks of order[16t .. 16t+15]; nmap_o [27][M] (optional,
+ * with nmap_rows, the row-major (M, 27) map pmg_nmap_hash writes) = the tap-major map in processing order,
+ * nmap_o[v][p] = nmap_rows[order[p]][v] -- the map pmg_spconv_i8_ordered reads. Workspace:
+ * pmg_row_order_workspace_bytes(M) (any contents). M < 2^31. */
 size_t pmg_row_order_workspace_bytes(int64_t M);
-int pmg_row_order(const uint32_t* row_mask, int64_t M, int32_t* order, uint32_t* order_tile_mask, void* workspace,
-                  size_t workspace_bytes, void* stream);
+int pmg_row_order(const uint32_t* row_mask, const int32_t* nmap_rows, int64_t M, int32_t* order,
+                  uint32_t* order_tile_mask, int32_t* nmap_o, void* workspace, size_t workspace_bytes, void* stream);
 
 /* pmg_pool_cache -- build_pool_cache (promptmoge/_fallback/flex_gemm/_core.py:339-395) for the perfect-partition
  * pool MoGe uses (kernel == stride, padding 0), output coordinates not given: the output voxels are the distinct
@@ -166,9 +168,11 @@ enum { PMG_EPI_ACC = 0, PMG_EPI_Q = 1, PMG_EPI_R = 2, PMG_EPI_BIAS = 3, PMG_EPI_
 int pmg_spconv_i8(const int8_t* x, const int32_t* nmap_t, const uint32_t* tile_mask, int64_t M, int Ci, int Co,
                   const int8_t* w, int epilogue, float a_scale, const float* w_scale, const float* bias,
                   float out_mult, const float* skip, void* out, void* stream);
-/* pmg_spconv_i8 with the rows processed in `order` (pmg_row_order) and tile masks of that order: the same
- * results, with the MFMA work of each tile limited to its rows' taps. Ci = Co = 64 or 128. */
-int pmg_spconv_i8_ordered(const int8_t* x, const int32_t* nmap_t, const int32_t* order,
+/* pmg_spconv_i8 with the rows processed in `order` (pmg_row_order): nmap_o is the map in processing order
+ * (pmg_row_order's nmap_o) and order_tile_mask its tile masks; output row order[p] is computed from map column p.
+ * The same results as pmg_spconv_i8 on the caller's map, with each chunk of rows running only its rows' taps.
+ * Ci = Co = 64 or 128. */
+int pmg_spconv_i8_ordered(const int8_t* x, const int32_t* nmap_o, const int32_t* order,
                           const uint32_t* order_tile_mask, int64_t M, int Ci, int Co, const int8_t* w, int epilogue,
                           float a_scale, const float* w_scale, const float* bias, float out_mult, const float* skip,
                           void* out, void* stream);

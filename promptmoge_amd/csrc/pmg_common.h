@@ -212,16 +212,18 @@ __device__ inline int8_t silu_quant_i8(float y, float mult) {
     return (int8_t)(int)q;
 }
 
-// Stores the lane's 4 channels of block j of row m as int8 codes (quant by mult) or fp16.
-__device__ inline void store_codes4(const float (&h)[4], float mult, int8_t* q) {
+// The int8 codes (quant by mult) of 4 channels, packed into a word (channel i in byte i).
+__device__ inline uint32_t pack_codes4(const float (&h)[4], float mult) {
     uint32_t pk = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) pk |= (uint32_t)(uint8_t)quant_i8(h[i], mult) << (8 * i);
-    *(uint32_t*)q = pk;
+    return pk;
 }
-// As store_codes4 for silu(t): the codes of silu of the 4 pre-activations t (silu_quant_i8 with one branch to the
+// Stores the lane's 4 channels of block j of row m as int8 codes (quant by mult) or fp16.
+__device__ inline void store_codes4(const float (&h)[4], float mult, int8_t* q) { *(uint32_t*)q = pack_codes4(h, mult); }
+// As pack_codes4 for silu(t): the codes of silu of the 4 pre-activations t (silu_quant_i8 with one branch to the
 // exact evaluation per 4 values).
-__device__ inline void store_silu_codes4(const float (&t)[4], float mult, int8_t* q) {
+__device__ inline uint32_t pack_silu_codes4(const float (&t)[4], float mult) {
     float c[4];
     bool u[4], any = false;
 #pragma unroll
@@ -237,7 +239,26 @@ __device__ inline void store_silu_codes4(const float (&t)[4], float mult, int8_t
     uint32_t pk = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) pk |= (uint32_t)(uint8_t)(int)c[i] << (8 * i);
-    *(uint32_t*)q = pk;
+    return pk;
+}
+__device__ inline void store_silu_codes4(const float (&t)[4], float mult, int8_t* q) {
+    *(uint32_t*)q = pack_silu_codes4(t, mult);
+}
+
+// A 4 x 4 transpose of words between the four 16-lane groups of a wave: on entry word k of lane group g is
+// element (k, g), on exit it holds element (g, k) (two v_permlane32_swap, two v_permlane16_swap; lanes keep their
+// position within the group). With word k of lane (r, g) holding the 4 codes of channels 16k + 4g .. +3 of row r
+// (the MFMA output layout of a 64-channel block), lane (r, g) then holds channels 16g .. 16g + 15 in words 0..3:
+// 16 contiguous bytes, so a row of the block is stored by four 16-byte lanes instead of sixteen 4-byte ones.
+__device__ inline void lane_groups_transpose4(uint32_t (&w)[4]) {
+    const auto a = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
+    const auto b = __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false);
+    const auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
+    const auto d = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
+    w[0] = c[0];
+    w[1] = c[1];
+    w[2] = d[0];
+    w[3] = d[1];
 }
 // silu_quant_i8 of NB x 4 values, packed four codes to a word, with one branch to the exact evaluation for all of
 // them (so the fast evaluations of the NB x 4 values can interleave).

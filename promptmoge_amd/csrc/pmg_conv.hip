@@ -38,7 +38,8 @@ struct ConvArgs {
     float out_mult;
     const float* skip;
     void* out;
-    const int32_t* order;  // rows in processing order (tile masks follow it), or NULL for 0 .. M-1
+    const int32_t* order;  // output row of each processing position, or NULL for 0 .. M-1; the map's columns and
+                           // the tile masks are in processing order
     const int64_t* m_dev;  // spconv_k: the row count on the device (<= M, which is then the map's row stride and
                            // the grid's capacity), or NULL for M rows
     int32_t* part;         // device-sized spconv_g2_k: int32 partial sums of a tap split ([Z][rows][Co]), or NULL
@@ -266,6 +267,49 @@ static int pick_nb(int Co) {
 // gather made the waits at the join conservative). Counters show the kernel limited by the L1 path of the gathers
 // (texture data unit busy 75 % at C = 128, most of it waiting on the cache; each 512-row chunk gathers ~27 times
 // its own rows), not by the gather latency: a three-tap-deep gather ring at C = 64 was no faster.
+// Code epilogues (Q: SiLU requant, QLIN: linear requant) of a wave's T tiles of 16 rows x 16 NB channels: the
+// dequantised accumulators (a_scale, per-channel scale and bias from LDS) packed into words of 4 codes, regrouped
+// between the lanes of each row (lane_groups_transpose4) and stored as one 16-byte vector per lane and 64-channel
+// block. Rows at or beyond M compute but do not store (the transpose needs every lane of the wave).
+template <int EPI, int T, int NB>
+__device__ inline void store_tile_codes(const ConvArgs& a, const v4i (&acc)[T][NB], const float* s_scale,
+                                        const float* s_bias, const int (&orow)[T], int pos0, int M, int Co, int n0,
+                                        int g) {
+    static_assert(NB % 4 == 0, "64-channel blocks");
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        uint32_t w[NB];
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            float y[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int n = 16 * j + 4 * g + i;
+                float u = (float)acc[t][j][i] * a.a_scale;
+                u = u * s_scale[n];
+                if (a.bias) u = u + s_bias[n];
+                y[i] = u;
+            }
+            w[j] = EPI == PMG_EPI_Q ? pack_silu_codes4(y, a.out_mult) : pack_codes4(y, a.out_mult);
+        }
+#pragma unroll
+        for (int h = 0; h < NB / 4; ++h) {
+            uint32_t q[4] = {w[4 * h], w[4 * h + 1], w[4 * h + 2], w[4 * h + 3]};
+            lane_groups_transpose4(q);
+            if (pos0 + 16 * t < M)
+                *(v4i*)((int8_t*)a.out + (int64_t)orow[t] * Co + n0 + 64 * h + 16 * g) =
+                    v4i{(int)q[0], (int)q[1], (int)q[2], (int)q[3]};
+        }
+    }
+}
+
+// Host-sized generic-map launches deal groups of kXcdGroup consecutive chunks round-robin over the 8 XCDs (block b
+// runs on XCD b % 8): neighbouring chunks (rows that share neighbours) stay on one XCD's L2, and the work evens out
+// where it varies along the row order (rows sorted by tap mask; measured at C = 128 on the 1M-voxel surface set:
+// 0.369 ms with one contiguous band per XCD, 0.324 ms dealt in groups of 16). Device-sized launches (a few chunks)
+// keep one contiguous band per XCD.
+constexpr int kXcdGroup = 16;
+
 constexpr int kBufWord3 = 0x00020000;  // buffer descriptor word 3 for raw (untyped) loads on gfx9
 constexpr int kG2Threads = 512;       // 8 waves: two per SIMD, 256 registers each
 constexpr int kG2Waves = kG2Threads / 64;
@@ -287,7 +331,7 @@ constexpr int kG2Chunk = kG2Waves * kG2Tiles * 16;  // 512 rows per block step
 // weight operands ahead a wave reads from LDS; RS = 4 gathers codes three taps ahead instead of one and requests
 // a group's weights a whole group ahead (a few hundred rows per block, as on the coarse levels of a U-Net, leave
 // each tap waiting on both otherwise).
-template <int C, int EPI, int NB = C / 16, int T = kG2Tiles, int PF = 1, int RS = 2>
+template <int C, int EPI, int NB = C / 16, int T = kG2Tiles, int PF = 1, int RS = 2, bool DEV = (RS == 4)>
 __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
     constexpr int GRP = C == 64 ? 4 : 2;
     constexpr int KS = C / 64;
@@ -302,10 +346,11 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
     static_assert(T == 1 || T == 2 || T == 4, "tiles per wave");
     static_assert(RS == 2 || RS == 4, "ring slots: the tap parity or v mod 4 of a trip");
     constexpr int GD = RS - 1;                           // gather distance in taps
-    constexpr bool kDev = RS == 4;                       // the device-sized launch (tap split allowed)
+    constexpr bool kDev = DEV;                           // the device-sized launch (tap split allowed)
 
     __shared__ __attribute__((aligned(16))) v4i s_w[2][GRP * NF * 64];
     __shared__ float s_k[2][NS];
+    __shared__ uint32_t s_um[kG2Waves];  // each wave's tap mask, for the chunk's union
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int r = lane & 15, g = lane >> 4;
@@ -345,13 +390,18 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
     // staged in PARTS pieces of WPP fragments per wave, one piece per tap of the group where that divides evenly
     // (C = 128: 8 registers held for one tap instead of 16 for the whole group)
     constexpr int PARTS = WPT % GRP == 0 ? GRP : 1, WPP = WPT / PARTS;
-    auto w_load = [&](int grp, int part, v4i (&st)[WPP]) {
+    // Union walk: the block runs only the taps that some row of its chunk has, in ascending order (a map in
+    // mask-sorted row order leaves ~12 of 27 per 512-row chunk). Each tap slot of a group is then one staging
+    // part, and three scalar cursors pop the union's taps for the weight loads, the index loads and the MFMAs.
+    constexpr bool UW = !kDev && PARTS == GRP;
+    // With the union walk (UW) a part is one tap slot and `vt` names its tap (27: none, zeros).
+    auto w_load = [&](int grp, int part, v4i (&st)[WPP], int vt) {
 #pragma unroll
         for (int kk = 0; kk < WPP; ++kk) {
             const int f = wv + kG2Waves * (part * WPP + kk);
             const int q = f / NF, js = f - (f / NF) * NF;
             const int j = js / KS, s2 = js - (js / KS) * KS;
-            const int v = t0 + GRP * grp + q;
+            const int v = UW ? vt : t0 + GRP * grp + q;
             const int off = v < t1 ? wlane + ((16 * j * 27) + v) * C + 64 * s2 : (int)0x80000000;
             st[kk] = __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 0);
         }
@@ -361,20 +411,25 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
         for (int kk = 0; kk < WPP; ++kk) dst[(wv + kG2Waves * (part * WPP + kk)) * 64 + lane] = st[kk];
     };
 
-    for (int un = c0 + bi; un < c1; un += nbx) {
+    constexpr int gi = kDev ? 0 : kXcdGroup;
+    for (int kq = bi;; kq += nbx) {
+        const int un = gi ? ((kq / gi) * nx + x) * gi + kq % gi : c0 + kq;
+        if (un >= (gi ? nunit : c1)) break;
         const int ch = Z == 1 ? un : un / Z, z = un - ch * Z;
         if constexpr (kDev) {
             t0 = 27 * z / Z;
             t1 = 27 * (z + 1) / Z;
         }
-        const int trips = kDev ? (t1 - t0 + 3) / 4 : NG2;  // trips of 4 taps (two groups)
+        int trips = kDev ? (t1 - t0 + 3) / 4 : NG2;  // trips of 4 taps (two groups)
         const int pos0 = ch * CHUNK + wv * (16 * T) + r;
-        // map offset of each tile's row; rows beyond M get an out-of-range offset (their indices load as 0)
-        int roff[T];
+        // map column of each tile's row (a map in processing order) and the row its outputs go to; rows beyond M
+        // get an out-of-range map offset (their indices load as 0)
+        int roff[T], orow[T];
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             const int p = pos0 + 16 * t;
-            roff[t] = p < M ? 4 * (a.order ? a.order[p] : p) : (int)0x80000000;
+            roff[t] = p < M ? 4 * p : (int)0x80000000;
+            orow[t] = p < M && a.order ? a.order[p] : p;
         }
         uint32_t wmask;
         {
@@ -384,6 +439,26 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
             for (int o = 1; o < T; o <<= 1) mk |= __shfl_xor(mk, o, 64);
             wmask = (uint32_t)__builtin_amdgcn_readfirstlane((int)mk);
         }
+        // the chunk's tap union: every wave publishes its mask; the previous chunk's readers have all passed at
+        // least one group barrier since (trips >= 1)
+        uint32_t cw = 0, ci = 0, cm = 0;  // cursors: weight loads, index loads, MFMAs
+        if constexpr (UW) {
+            if (lane == 0) s_um[wv] = wmask;
+            __builtin_amdgcn_s_waitcnt(0xc07f);
+            __builtin_amdgcn_s_barrier();
+            uint32_t um = 0;
+#pragma unroll
+            for (int k = 0; k < kG2Waves; ++k) um |= s_um[k];
+            um = (uint32_t)__builtin_amdgcn_readfirstlane((int)um);
+            const int ntap = __builtin_popcount(um);
+            trips = ntap > 0 ? (ntap + 3) / 4 : 1;
+            cw = ci = cm = um;
+        }
+        auto pop = [](uint32_t& rem) {
+            const int v = rem ? (int)__builtin_ctz(rem) : 27;
+            rem = rem ? rem & (rem - 1) : 0u;
+            return v;
+        };
         v4i acc[T][NB];
 #pragma unroll
         for (int t = 0; t < T; ++t)
@@ -434,21 +509,21 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
 #pragma unroll
         for (int part = 0; part < PARTS; ++part) {
             v4i st[WPP];
-            w_load(0, part, st);
+            w_load(0, part, st, UW ? pop(cw) : 0);
             w_store(s_w[0], part, st);
         }
         if constexpr (RS == 2) {
             int i0[T];
-            idx_load(0, i0);
-            idx_load(1, I[1]);
-            idx_load(2, I[0]);
+            idx_load(UW ? pop(ci) : 0, i0);
+            idx_load(UW ? pop(ci) : 1, I[1]);
+            idx_load(UW ? pop(ci) : 2, I[0]);
             gather(i0, X[0]);
         } else {
 #pragma unroll
-            for (int u = 0; u < RS; ++u) idx_load(t0 + u, I[u]);
+            for (int u = 0; u < RS; ++u) idx_load(UW ? pop(ci) : t0 + u, I[u]);
 #pragma unroll
             for (int u = 0; u < GD; ++u) gather(I[u], X[u]);
-            idx_load(t0 + RS, I[0]);
+            idx_load(UW ? pop(ci) : t0 + RS, I[0]);
         }
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's weight stores are in LDS
         __builtin_amdgcn_s_barrier();
@@ -463,17 +538,17 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
             v4i sta[RS == 2 ? 1 : PARTS][WPP];  // RS = 4: the next group's weights, all requested at its start
 #pragma unroll
             for (int q = 0; q < GRP; ++q) {
-                const int v = t0 + GRP * grp + q;
+                const int v = UW ? pop(cm) : t0 + GRP * grp + q;
                 const int p = (GRP * H + q) & 3;  // (v - t0) mod 4 (GRP * grp = 4 * trip + GRP * H)
                 v4i st[WPP];
                 if constexpr (RS == 2) {
-                    if (q < PARTS) w_load(grp + 1, q, st);
+                    if (q < PARTS) w_load(grp + 1, q, st, UW ? pop(cw) : 0);
                 } else if (q == 0) {
 #pragma unroll
-                    for (int pp = 0; pp < PARTS; ++pp) w_load(grp + 1, pp, sta[pp]);
+                    for (int pp = 0; pp < PARTS; ++pp) w_load(grp + 1, pp, sta[pp], UW ? pop(cw) : 0);
                 }
                 gather(I[(p + GD) % RS], X[(p + GD) % RS]);
-                idx_load(v + GD + 2, I[(p + GD + 2) % RS]);
+                idx_load(UW ? pop(ci) : v + GD + 2, I[(p + GD + 2) % RS]);
                 __builtin_amdgcn_sched_barrier(0);
                 if (v < t1 && ((wmask >> v) & 1u)) mma_tap(s_w[H] + q * NF * 64, X[p % RS]);
                 __builtin_amdgcn_sched_barrier(0);
@@ -498,17 +573,21 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
 #pragma unroll
             for (int t = 0; t < T; ++t) {
                 if (pos0 + 16 * t >= M) continue;
-                const int m = roff[t] >> 2;
+                const int m = orow[t];
 #pragma unroll
                 for (int j = 0; j < NB; ++j)
                     *(v4i*)(a.part + ((int64_t)z * M + m) * Co + n0 + 16 * j + 4 * g) = acc[t][j];
             }
             continue;  // split_epilogue_k adds the Z partials and applies the epilogue
         }
+        if constexpr (EPI == PMG_EPI_Q || EPI == PMG_EPI_QLIN) {
+            store_tile_codes<EPI, T, NB>(a, acc, s_k[0], s_k[1], orow, pos0, M, Co, n0, g);
+            continue;
+        }
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             if (pos0 + 16 * t >= M) continue;
-            const int m = roff[t] >> 2;
+            const int m = orow[t];
 #pragma unroll
             for (int j = 0; j < NB; ++j) {
                 const int64_t o = (int64_t)m * Co + n0 + 16 * j + 4 * g;
@@ -541,15 +620,22 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
 }
 
 // Ci = Co = 64: every tap's weights fit in LDS (27 x 4 KB in operand order), so the block loads them once and
-// meets at no barrier afterwards -- each wave runs its chunks' 27 taps on its own, and a wave that skips a tap
-// (none of its tiles has it) gains the time instead of waiting for the others at the next group barrier. The tap
-// loop is that of spconv_g2_k without the weight staging: codes one tap ahead, map indices three taps ahead.
-template <int C, int EPI, int T = kG2Tiles, int PF = 1>
-__global__ __launch_bounds__(kG2Threads, 1) void spconv_g2r_k(ConvArgs a) {
+// meets at no barrier afterwards -- each wave runs its chunks' taps on its own, and a wave that skips a tap (none
+// of its tiles has it) gains the time instead of waiting for the others at the next group barrier. The tap loop
+// is that of spconv_g2_k without the weight staging: a ring of RS slots gathers the codes RS - 1 taps ahead of
+// their MFMAs and the map indices two taps before that. NWV waves per block (NWV = 16: four per SIMD, fewer
+// registers each): each wave spends most of a tap waiting for its gathers, so more waves and deeper rings keep
+// more of them in flight.
+template <int C, int EPI, int T = kG2Tiles, int PF = 1, int RS = 2, int NWV = kG2Waves>
+__global__ __launch_bounds__(64 * NWV, 1) void spconv_g2r_k(ConvArgs a) {
     constexpr int NB = C / 16, KS = C / 64;
     constexpr int NF = NB * KS;
-    constexpr int CHUNK = kG2Waves * T * 16;
+    constexpr int CHUNK = NWV * T * 16;
+    constexpr int NTH = 64 * NWV;
+    constexpr int GD = RS - 1;                 // gather distance in taps
+    constexpr int UNR = RS % 2 == 0 ? RS : 2 * RS;  // steps per loop trip: the X ring (RS) and the index pair (2)
     static_assert(C == 64, "resident weights: C = 64");
+    static_assert(RS >= 2 && RS <= 4, "ring slots");
     __shared__ __attribute__((aligned(16))) v4i s_w[27 * NF * 64];
     __shared__ float s_k[2][C];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -561,12 +647,12 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2r_k(ConvArgs a) {
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, (int)(a.M * C), kBufWord3);
     const __amdgpu_buffer_rsrc_t nr =
         __builtin_amdgcn_make_buffer_rsrc((void*)a.nmap_t, (short)0, (int)(a.M * 27 * 4), kBufWord3);
-    for (int e = tid; e < 2 * C; e += kG2Threads) {
+    for (int e = tid; e < 2 * C; e += NTH) {
         const int q = e / C, n = e - (e / C) * C;
         const float* src = q == 0 ? a.w_scale : a.bias;
         s_k[q][n] = src ? src[n] : 0.0f;
     }
-    for (int e = tid; e < 27 * NF * 64; e += kG2Threads) {
+    for (int e = tid; e < 27 * NF * 64; e += NTH) {
         const int f = e >> 6, l = e & 63;
         const int v = f / NF, js = f - (f / NF) * NF;
         const int j = js / KS, s2 = js - (js / KS) * KS;
@@ -579,14 +665,18 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2r_k(ConvArgs a) {
     const int nx = G >= 8 ? 8 : 1;
     const int x = b % nx, bi = b / nx, nbx = (G - x + nx - 1) / nx;
     const int c0 = (int)((int64_t)nchunk * x / nx), c1 = (int)((int64_t)nchunk * (x + 1) / nx);
-    // each wave takes the block's chunks independently: wave wv of chunk ch owns rows [64 wv, 64 wv + 64)
-    for (int ch = c0 + bi; ch < c1; ch += nbx) {
+    // each wave takes the block's chunks independently: wave wv of chunk ch owns rows [16 T wv, 16 T (wv + 1))
+    const int gi = a.m_dev ? 0 : kXcdGroup;
+    for (int kq = bi;; kq += nbx) {
+        const int ch = gi ? ((kq / gi) * nx + x) * gi + kq % gi : c0 + kq;
+        if (ch >= (gi ? nchunk : c1)) break;
         const int pos0 = ch * CHUNK + wv * (16 * T) + r;
-        int roff[T];  // rows beyond M: out-of-range map offset (indices load as 0)
+        int roff[T], orow[T];  // map column (processing order) and output row; rows beyond M: out-of-range offset
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             const int p = pos0 + 16 * t;
-            roff[t] = p < M ? 4 * (a.order ? a.order[p] : p) : (int)0x80000000;
+            roff[t] = p < M ? 4 * p : (int)0x80000000;
+            orow[t] = p < M && a.order ? a.order[p] : p;
         }
         uint32_t wmask;
         {
@@ -635,7 +725,7 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2r_k(ConvArgs a) {
             }
         };
         // The wave walks only its own active taps (no barrier binds it to the block's union): a scalar queue holds
-        // the taps of this step and the next three (27 after the last: out-of-range indices, zeros, no MFMAs).
+        // the taps of this step and the next GD + 2 (27 after the last: out-of-range indices, zeros, no MFMAs).
         uint32_t rem = wmask;
         auto pop = [&]() {
             const int v = rem ? (int)__builtin_ctz(rem) : 27;
@@ -643,39 +733,54 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2r_k(ConvArgs a) {
             return v;
         };
         const int ntap = __builtin_popcount(wmask);
-        int v0 = pop(), v1 = pop(), v2 = pop(), v3 = pop();
+        int q[GD + 3];
+#pragma unroll
+        for (int u = 0; u < GD + 3; ++u) q[u] = pop();
         int I[2][T];
-        v4i X[2][T][KS];
-        {
-            int i0[T];
-            idx_load(v0, i0);
-            idx_load(v1, I[1]);
-            idx_load(v2, I[0]);
-            gather(i0, X[0]);
+        v4i X[RS][T][KS];
+#pragma unroll
+        for (int u = 0; u < GD; ++u) {
+            int iu[T];
+            idx_load(q[u], iu);
+            gather(iu, X[u]);
         }
-        // step k: the codes of tap k+1 (indices loaded two steps ago) and the indices of tap k+3 are requested,
-        // then tap k's MFMAs run
-        auto tap = [&](auto Pc) {
-            constexpr int p = decltype(Pc)::value;
-            gather(I[p ^ 1], X[p ^ 1]);
-            idx_load(v3, I[p ^ 1]);
+        idx_load(q[GD], I[GD & 1]);
+        idx_load(q[GD + 1], I[(GD + 1) & 1]);
+        // step k: the codes of tap k+GD (indices loaded two steps ago) and the indices of tap k+GD+2 are
+        // requested, then tap k's MFMAs run
+        auto tap = [&](auto Kc) {
+            constexpr int k = decltype(Kc)::value;
+            constexpr int xs = (k + GD) % RS, is = (k + GD) & 1;
+            gather(I[is], X[xs]);
+            idx_load(q[GD + 2], I[is]);
             __builtin_amdgcn_sched_barrier(0);
-            if (v0 < 27) mma_tap(v0, X[p]);
+            if (q[0] < 27) mma_tap(q[0], X[k % RS]);
             __builtin_amdgcn_sched_barrier(0);
-            v0 = v1;
-            v1 = v2;
-            v2 = v3;
-            v3 = pop();
+#pragma unroll
+            for (int u = 0; u < GD + 2; ++u) q[u] = q[u + 1];
+            q[GD + 2] = pop();
         };
 #pragma unroll 1
-        for (int k = 0; k < ntap; k += 2) {
+        for (int k = 0; k < ntap; k += UNR) {
             tap(std::integral_constant<int, 0>{});
             tap(std::integral_constant<int, 1>{});
+            if constexpr (UNR > 2) {
+                tap(std::integral_constant<int, 2>{});
+                tap(std::integral_constant<int, 3>{});
+            }
+            if constexpr (UNR > 4) {
+                tap(std::integral_constant<int, 4>{});
+                tap(std::integral_constant<int, 5>{});
+            }
+        }
+        if constexpr (EPI == PMG_EPI_Q || EPI == PMG_EPI_QLIN) {
+            store_tile_codes<EPI, T, NB>(a, acc, s_k[0], s_k[1], orow, pos0, M, C, 0, g);
+            continue;
         }
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             if (pos0 + 16 * t >= M) continue;
-            const int m = roff[t] >> 2;
+            const int m = orow[t];
 #pragma unroll
             for (int j = 0; j < NB; ++j) {
                 const int64_t o = (int64_t)m * C + 16 * j + 4 * g;
@@ -707,22 +812,29 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2r_k(ConvArgs a) {
     }
 }
 
+// The host-sized C = 64 launch: 16-row tiles per wave, gather ring slots, waves per block.
+constexpr int kG2rT = 4, kG2rRS = 2, kG2rWaves = 8;
+
 template <int C>
 static int launch_g2r(const ConvArgs& a, int epilogue, hipStream_t s) {
     static int cus = -1;
     if (cus < 0) cus = num_cus();
-    const int64_t nchunk = (a.M + kG2Chunk - 1) / kG2Chunk;
-    const unsigned grid = (unsigned)(nchunk < cus ? nchunk : cus);
+    constexpr int T = kG2rT, RS = kG2rRS, NWV = kG2rWaves, CHUNK = NWV * T * 16;
+    const int64_t nchunk = (a.M + CHUNK - 1) / CHUNK;
+    const dim3 grid((unsigned)(nchunk < cus ? nchunk : cus)), blk(64 * NWV);
     switch (epilogue) {
-        case PMG_EPI_ACC: hipLaunchKernelGGL((spconv_g2r_k<C, PMG_EPI_ACC>), dim3(grid), dim3(kG2Threads), 0, s, a); break;
-        case PMG_EPI_Q: hipLaunchKernelGGL((spconv_g2r_k<C, PMG_EPI_Q>), dim3(grid), dim3(kG2Threads), 0, s, a); break;
-        case PMG_EPI_QLIN: hipLaunchKernelGGL((spconv_g2r_k<C, PMG_EPI_QLIN>), dim3(grid), dim3(kG2Threads), 0, s, a); break;
-        case PMG_EPI_R: hipLaunchKernelGGL((spconv_g2r_k<C, PMG_EPI_R>), dim3(grid), dim3(kG2Threads), 0, s, a); break;
-        case PMG_EPI_BIAS: hipLaunchKernelGGL((spconv_g2r_k<C, PMG_EPI_BIAS>), dim3(grid), dim3(kG2Threads), 0, s, a); break;
+        case PMG_EPI_ACC: hipLaunchKernelGGL((spconv_g2r_k<C, PMG_EPI_ACC, T, 1, RS, NWV>), grid, blk, 0, s, a); break;
+        case PMG_EPI_Q: hipLaunchKernelGGL((spconv_g2r_k<C, PMG_EPI_Q, T, 1, RS, NWV>), grid, blk, 0, s, a); break;
+        case PMG_EPI_QLIN: hipLaunchKernelGGL((spconv_g2r_k<C, PMG_EPI_QLIN, T, 1, RS, NWV>), grid, blk, 0, s, a); break;
+        case PMG_EPI_R: hipLaunchKernelGGL((spconv_g2r_k<C, PMG_EPI_R, T, 1, RS, NWV>), grid, blk, 0, s, a); break;
+        case PMG_EPI_BIAS: hipLaunchKernelGGL((spconv_g2r_k<C, PMG_EPI_BIAS, T, 1, RS, NWV>), grid, blk, 0, s, a); break;
         default: return fail(PMG_E_INVALID, "spconv: epilogue not available for this precision");
     }
     return check_launch("spconv_g2r_k");
 }
+
+// The host-sized C = 128 launch: 16-row tiles per wave and gather ring slots.
+constexpr int kG2T128 = 4, kG2RS128 = 2;
 
 template <int C>
 static int launch_g2(const ConvArgs& a, int epilogue, hipStream_t s) {
@@ -731,18 +843,15 @@ static int launch_g2(const ConvArgs& a, int epilogue, hipStream_t s) {
     } else {
         static int cus = -1;
         if (cus < 0) cus = num_cus();
-        const int64_t nchunk = (a.M + kG2Chunk - 1) / kG2Chunk;
-        const unsigned grid = (unsigned)(nchunk < cus ? nchunk : cus);
+        constexpr int T = kG2T128, RS = kG2RS128, CHUNK = kG2Waves * T * 16;
+        const int64_t nchunk = (a.M + CHUNK - 1) / CHUNK;
+        const dim3 grid((unsigned)(nchunk < cus ? nchunk : cus)), blk(kG2Threads);
         switch (epilogue) {
-            case PMG_EPI_ACC: hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_ACC>), dim3(grid), dim3(kG2Threads), 0, s, a); break;
-            case PMG_EPI_Q: hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_Q>), dim3(grid), dim3(kG2Threads), 0, s, a); break;
-            case PMG_EPI_QLIN:
-                hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_QLIN>), dim3(grid), dim3(kG2Threads), 0, s, a);
-                break;
-            case PMG_EPI_R: hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_R>), dim3(grid), dim3(kG2Threads), 0, s, a); break;
-            case PMG_EPI_BIAS:
-                hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_BIAS>), dim3(grid), dim3(kG2Threads), 0, s, a);
-                break;
+            case PMG_EPI_ACC: hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_ACC, C / 16, T, 1, RS, false>), grid, blk, 0, s, a); break;
+            case PMG_EPI_Q: hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_Q, C / 16, T, 1, RS, false>), grid, blk, 0, s, a); break;
+            case PMG_EPI_QLIN: hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_QLIN, C / 16, T, 1, RS, false>), grid, blk, 0, s, a); break;
+            case PMG_EPI_R: hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_R, C / 16, T, 1, RS, false>), grid, blk, 0, s, a); break;
+            case PMG_EPI_BIAS: hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_BIAS, C / 16, T, 1, RS, false>), grid, blk, 0, s, a); break;
             default: return fail(PMG_E_INVALID, "spconv: epilogue not available for this precision");
         }
         return check_launch("spconv_g2_k");
@@ -908,11 +1017,11 @@ int pmg_spconv_i8(const int8_t* x, const int32_t* nmap_t, const uint32_t* tile_m
     return conv_common<int8_t>(a, Ci, epilogue, (hipStream_t)stream);
 }
 
-int pmg_spconv_i8_ordered(const int8_t* x, const int32_t* nmap_t, const int32_t* order, const uint32_t* order_tile_mask,
+int pmg_spconv_i8_ordered(const int8_t* x, const int32_t* nmap_o, const int32_t* order, const uint32_t* order_tile_mask,
                           int64_t M, int Ci, int Co, const int8_t* w, int epilogue, float a_scale,
                           const float* w_scale, const float* bias, float out_mult, const float* skip, void* out,
                           void* stream) {
-    if (int e = validate(x, nmap_t, order_tile_mask, M, Ci, Co, w, out, 1, "pmg_spconv_i8_ordered")) return e;
+    if (int e = validate(x, nmap_o, order_tile_mask, M, Ci, Co, w, out, 1, "pmg_spconv_i8_ordered")) return e;
     PMG_REQUIRE(order, "null order");
     PMG_REQUIRE(epilogue == PMG_EPI_ACC || w_scale, "w_scale required");
     PMG_REQUIRE(epilogue != PMG_EPI_R || skip, "skip required");
@@ -923,7 +1032,7 @@ int pmg_spconv_i8_ordered(const int8_t* x, const int32_t* nmap_t, const int32_t*
                     (epilogue != PMG_EPI_R || aligned16(skip)),
                 "pmg_spconv_i8_ordered: unsupported epilogue or unaligned x / w / output");
     if (M == 0) return PMG_OK;
-    ConvArgs a{(const uint8_t*)x, nmap_t, order_tile_mask, (const uint8_t*)w, M, Co, Ci, Ci / 16,
+    ConvArgs a{(const uint8_t*)x, nmap_o, order_tile_mask, (const uint8_t*)w, M, Co, Ci, Ci / 16,
                a_scale, w_scale, bias, out_mult, skip, out, order};
     if (Ci == 64) return launch_g2<64>(a, epilogue, (hipStream_t)stream);
     return launch_g2<128>(a, epilogue, (hipStream_t)stream);

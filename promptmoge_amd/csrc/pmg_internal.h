@@ -142,4 +142,19 @@ struct DevConv {
 int launch_conv_i8_dev(const DevConv& d, hipStream_t s);
 int64_t conv_split_bytes(int C);  // partials buffer of a width's tap split (0: no split at that width)
 
+// Stable LSD radix sort of (uint64 key, int32 value) pairs over the keys' low `bits` bits, 8 bits per pass
+// (pmg_pool.hip): the caller writes the keys into keys[0]; the first pass takes value i for key i; the sorted
+// values go to vals_final and the sorted keys are in keys[sorted]. Workspace: radix_sort_workspace_bytes(M).
+struct RadixBufs {
+    uint64_t* keys[2];
+    int32_t* vals[2];
+    uint32_t* hist;
+    uint32_t* tcnt;
+    uint32_t* ctot;
+    int sorted;
+};
+size_t radix_sort_workspace_bytes(int64_t M);
+RadixBufs radix_bufs(void* workspace, int64_t M);
+int radix_sort_pairs(RadixBufs& r, int64_t M, int bits, int32_t* vals_final, hipStream_t s);
+
 }  // namespace pmg

@@ -1,104 +1,49 @@
-// Row order for the generic-map convolution: rows sorted by their tap mask within windows of consecutive rows.
+// Row order for the generic-map convolution: rows stably sorted by their 27-bit tap mask.
 //
-// The block-tiled convolution multiplies every 16-row tile by the weights of each tap any of its rows has. In the
-// caller's row order (e.g. lexicographic coordinates of surfaces) 16 consecutive rows together use ~25 of the 27
-// taps while each row uses ~13. Sorting the rows of each window of 4096 consecutive rows by their tap mask -- by
-// its top 16 bits (taps 11..26), which keeps rows of one surface orientation together -- brings a tile's taps down
-// to ~17, while the window keeps the rows (and the neighbours they gather) spatially local. A global sort gets the
-// tiles to ~13.5 taps but scatters every chunk's neighbours over the whole volume. The order changes no result:
-// each output row is computed from its own map row alone.
+// The block-tiled convolution runs, for each chunk of 512 output rows, the taps that any row of the chunk has,
+// and each wave multiplies its 16-row tiles by the weights of each tap one of its rows has. In the caller's row
+// order (e.g. lexicographic coordinates of surfaces) 512 consecutive rows use ~27 of the 27 taps and 64 rows ~25,
+// while a row uses ~10-13. Sorted by the whole mask, rows with one neighbourhood pattern are consecutive: a chunk
+// then uses ~12 taps and a wave ~10 on the 1M-voxel surface set. The sort is stable, so the rows of one pattern
+// stay in the caller's (spatial) order and a chunk's gathers stay local within its pattern. The order changes no
+// result: each output row is computed from its own map row alone.
 //
-// One block per window, entirely in LDS: a stable LSD radix sort with two 8-bit digits. Per digit: a histogram
-// (LDS atomics; counts do not depend on order), an exclusive scan of the 256 counts, and 16 rounds of 256 keys in
-// window order, where the rank of a key among equal digits comes from 9 wave ballots (the lanes whose digit
-// matches on every bit) plus the counts of the lower waves -- so the sort is stable and deterministic. The keys
-// keep the full mask, so the per-tile union of the sorted masks is a contiguous OR.
+// Three steps: the masks become 64-bit keys; a stable LSD radix sort (the pool cache's, four 8-bit passes) gives
+// the order; one kernel writes the tile unions of the sorted masks and the tap-major map in processing order
+// (column p is the caller's row order[p]), so the convolution reads its map coalesced and only its output rows
+// are scattered. The map comes from the row-major (M, 27) layout: each position reads one 108-byte row, where the
+// tap-major layout would cost 27 scattered 4-byte reads.
 #include <climits>
 
 #include "pmg_common.h"
+#include "pmg_internal.h"
 
 namespace pmg {
 
-constexpr int kOrdThreads = 256;
-constexpr int kOrdRounds = 16;
-constexpr int kOrdWindow = kOrdThreads * kOrdRounds;  // 4096 rows per window (one block)
-constexpr int kOrdShift = 11;                         // the sort key is mask >> 11 (taps 11..26)
+__global__ __launch_bounds__(256) void order_keys_k(const uint32_t* __restrict__ row_mask, int64_t M,
+                                                    uint64_t* __restrict__ keys) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < M) keys[i] = (uint64_t)(row_mask[i] & 0x7ffffffu);
+}
 
-__global__ __launch_bounds__(kOrdThreads) void order_window_k(const uint32_t* __restrict__ row_mask, int64_t M,
-                                                              int32_t* __restrict__ order,
-                                                              uint32_t* __restrict__ tile_mask) {
-    constexpr int NW = kOrdThreads / 64;
-    __shared__ uint32_t s_key[2][kOrdWindow];
-    __shared__ int32_t s_val[2][kOrdWindow];
-    __shared__ uint32_t s_run[256];
-    __shared__ uint32_t s_cnt[NW][256];
-    __shared__ uint32_t s_tmp[256];
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int64_t base = (int64_t)blockIdx.x * kOrdWindow;
-    const int n = (int)(M - base < kOrdWindow ? M - base : kOrdWindow);
-    for (int i = tid; i < kOrdWindow; i += kOrdThreads) {
-        s_key[0][i] = i < n ? row_mask[base + i] : 0u;
-        s_val[0][i] = (int32_t)(base + i);
-    }
-    const uint64_t below = (1ull << lane) - 1ull;
-    for (int pass = 0; pass < 2; ++pass) {
-        const int src = pass & 1, dst = src ^ 1;
-        const int sh = kOrdShift + 8 * pass;
-        // digit counts, then their exclusive scan (Hillis-Steele over the 256 digits, one per thread)
-        s_run[tid] = 0;
-        __syncthreads();
-        for (int i = tid; i < n; i += kOrdThreads) atomicAdd(&s_run[(s_key[src][i] >> sh) & 0xffu], 1u);
-        __syncthreads();
-        const uint32_t c = s_run[tid];
-        s_tmp[tid] = c;
-        __syncthreads();
-        for (int off = 1; off < 256; off <<= 1) {
-            const uint32_t add = tid >= off ? s_tmp[tid - off] : 0u;
-            __syncthreads();
-            s_tmp[tid] += add;
-            __syncthreads();
-        }
-        s_run[tid] = s_tmp[tid] - c;  // start of digit tid
-        __syncthreads();
-        for (int k = 0; k < kOrdRounds; ++k) {
-            const int i = k * kOrdThreads + tid;
-            const bool ok = i < n;
-            const uint32_t key = s_key[src][i];
-            const int32_t val = s_val[src][i];
-            const uint32_t d = ok ? (key >> sh) & 0xffu : 256u;  // 256 matches no real digit
-            uint64_t peers = __ballot(ok);
-#pragma unroll
-            for (int b = 0; b < 9; ++b) {
-                const uint64_t bb = __ballot((d >> b) & 1u);
-                peers &= ((d >> b) & 1u) ? bb : ~bb;
-            }
-            for (int e = lane; e < 256; e += 64) s_cnt[w][e] = 0;
-            __syncthreads();
-            const uint32_t rank = (uint32_t)__popcll(peers & below);
-            if (ok && rank == 0) s_cnt[w][d] = (uint32_t)__popcll(peers);
-            __syncthreads();
-            if (ok) {
-                uint32_t pos = s_run[d] + rank;
-                for (int q = 0; q < w; ++q) pos += s_cnt[q][d];
-                s_key[dst][pos] = key;
-                s_val[dst][pos] = val;
-            }
-            __syncthreads();
-            uint32_t add = 0;
-#pragma unroll
-            for (int q = 0; q < NW; ++q) add += s_cnt[q][tid];
-            s_run[tid] += add;
-            __syncthreads();  // the next round clears s_cnt and reads s_run
-        }
-    }
-    // after two passes the sorted window is in buffer 0
-    for (int i = tid; i < n; i += kOrdThreads) order[base + i] = s_val[0][i];
-    // tile unions: the window starts on a tile boundary (4096 = 256 tiles)
-    for (int t = tid; t * 16 < n; t += kOrdThreads) {
+// One thread per processing position p: the permuted map column, and (every 16th thread) the tile union of
+// the 16 sorted masks starting at p.
+__global__ __launch_bounds__(256) void order_finish_k(const uint64_t* __restrict__ sorted_keys,
+                                                      const int32_t* __restrict__ order,
+                                                      const int32_t* __restrict__ nmap_rows, int64_t M,
+                                                      uint32_t* __restrict__ tile_mask, int32_t* __restrict__ nmap_o) {
+    const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (p >= M) return;
+    if ((p & 15) == 0) {
         uint32_t m = 0;
-        const int e = t * 16 + 16 < n ? t * 16 + 16 : n;
-        for (int i = t * 16; i < e; ++i) m |= s_key[0][i];
-        tile_mask[base / 16 + t] = m;
+        const int64_t e = p + 16 < M ? p + 16 : M;
+        for (int64_t i = p; i < e; ++i) m |= (uint32_t)sorted_keys[i];
+        tile_mask[p >> 4] = m;
+    }
+    if (nmap_o) {
+        const int64_t r = order[p];
+#pragma unroll 9
+        for (int v = 0; v < 27; ++v) nmap_o[v * M + p] = nmap_rows[r * 27 + v];
     }
 }
 
@@ -108,20 +53,26 @@ using namespace pmg;
 
 extern "C" {
 
-size_t pmg_row_order_workspace_bytes(int64_t M) { return M < 0 ? 0 : 256; }
+size_t pmg_row_order_workspace_bytes(int64_t M) { return M < 0 ? 0 : radix_sort_workspace_bytes(M); }
 
-int pmg_row_order(const uint32_t* row_mask, int64_t M, int32_t* order, uint32_t* order_tile_mask, void* workspace,
-                  size_t workspace_bytes, void* stream) {
-    PMG_REQUIRE(row_mask && order && order_tile_mask, "null buffer");
-    PMG_REQUIRE(M >= 0 && M < ((int64_t)1 << 31), "bad voxel count");
-    (void)workspace;
-    (void)workspace_bytes;
+int pmg_row_order(const uint32_t* row_mask, const int32_t* nmap_rows, int64_t M, int32_t* order,
+                  uint32_t* order_tile_mask, int32_t* nmap_o, void* workspace, size_t workspace_bytes, void* stream) {
+    PMG_REQUIRE(row_mask && order && order_tile_mask && workspace, "null buffer");
+    PMG_REQUIRE(!nmap_o == !nmap_rows, "nmap_rows and nmap_o go together");
+    PMG_REQUIRE(!nmap_o || nmap_o != nmap_rows, "the permuted map needs its own buffer");
+    PMG_REQUIRE(M >= 0 && M < ((int64_t)1 << 31) && M * 27 < ((int64_t)1 << 62), "bad voxel count");
+    PMG_REQUIRE((M + 2047) / 2048 * 256 <= INT_MAX, "too many voxels");
+    PMG_REQUIRE(workspace_bytes >= pmg_row_order_workspace_bytes(M), "workspace too small");
     if (M == 0) return PMG_OK;
-    const int64_t nwin = (M + kOrdWindow - 1) / kOrdWindow;
-    PMG_REQUIRE(nwin <= INT_MAX, "too many voxels");
-    hipLaunchKernelGGL(order_window_k, dim3((unsigned)nwin), dim3(kOrdThreads), 0, (hipStream_t)stream, row_mask, M,
-                       order, order_tile_mask);
-    return check_launch("order_window_k");
+    hipStream_t s = (hipStream_t)stream;
+    RadixBufs rb = radix_bufs(workspace, M);
+    const unsigned g = (unsigned)((M + 255) / 256);
+    hipLaunchKernelGGL(order_keys_k, dim3(g), dim3(256), 0, s, row_mask, M, rb.keys[0]);
+    if (int e = check_launch("order_keys_k")) return e;
+    if (int e = radix_sort_pairs(rb, M, 27, order, s)) return e;
+    hipLaunchKernelGGL(order_finish_k, dim3(g), dim3(256), 0, s, (const uint64_t*)rb.keys[rb.sorted],
+                       (const int32_t*)order, nmap_rows, M, order_tile_mask, nmap_o);
+    return check_launch("order_finish_k");
 }
 
 }  // extern "C"

@@ -22,6 +22,7 @@
 #include <climits>
 
 #include "pmg_common.h"
+#include "pmg_internal.h"
 
 namespace pmg {
 
@@ -352,19 +353,61 @@ static size_t pool_align(size_t x) { return (x + 255) & ~(size_t)255; }
 
 static int64_t pool_tiles(int64_t M) { return (M + kPoolTile - 1) / kPoolTile; }
 
+size_t radix_sort_workspace_bytes(int64_t M) {
+    const size_t n = (size_t)(M > 0 ? M : 1);
+    const size_t nt = (size_t)pool_tiles(M > 0 ? M : 1);
+    return 2 * pool_align(n * 8) + 2 * pool_align(n * 4) + pool_align(256 * nt * 4) + pool_align(nt * 4) +
+           pool_align((256 * nt / 8192 + 2) * 4);
+}
+
+RadixBufs radix_bufs(void* workspace, int64_t M) {
+    const size_t n = (size_t)(M > 0 ? M : 1);
+    const size_t nt = (size_t)pool_tiles(M > 0 ? M : 1);
+    char* p = (char*)workspace;
+    RadixBufs r;
+    r.keys[0] = (uint64_t*)p;
+    r.keys[1] = (uint64_t*)(p + pool_align(n * 8));
+    p += 2 * pool_align(n * 8);
+    r.vals[0] = (int32_t*)p;
+    r.vals[1] = (int32_t*)(p + pool_align(n * 4));
+    p += 2 * pool_align(n * 4);
+    r.hist = (uint32_t*)p;
+    p += pool_align(256 * nt * 4);
+    r.tcnt = (uint32_t*)p;
+    p += pool_align(nt * 4);
+    r.ctot = (uint32_t*)p;
+    return r;
+}
+
+int radix_sort_pairs(RadixBufs& r, int64_t M, int bits, int32_t* vals_final, hipStream_t s) {
+    const int nt = (int)pool_tiles(M);
+    const int npass = (bits + 7) / 8;
+    int cur = 0;
+    for (int pass = 0; pass < npass; ++pass) {
+        const int shift = 8 * pass;
+        const uint64_t* kin = r.keys[cur];
+        const int32_t* vin = pass == 0 ? nullptr : r.vals[cur];
+        uint64_t* kout = r.keys[cur ^ 1];
+        int32_t* vout = pass == npass - 1 ? vals_final : r.vals[cur ^ 1];
+        hipLaunchKernelGGL(pool_hist_k, dim3(nt), dim3(kPoolThreads), 0, s, kin, M, shift, nt, r.hist);
+        if (int e = check_launch("pool_hist_k")) return e;
+        if (int e = pool_scan(r.hist, 256 * nt, nullptr, r.ctot, s)) return e;
+        hipLaunchKernelGGL(pool_scatter_k, dim3(nt), dim3(kPoolThreads), 0, s, kin, vin, M, shift, nt,
+                           (const uint32_t*)r.hist, kout, vout);
+        if (int e = check_launch("pool_scatter_k")) return e;
+        cur ^= 1;
+    }
+    r.sorted = cur;
+    return PMG_OK;
+}
+
 }  // namespace pmg
 
 using namespace pmg;
 
 extern "C" {
 
-size_t pmg_pool_cache_workspace_bytes(int64_t M) {
-    if (M < 0) return 0;
-    const size_t n = (size_t)(M > 0 ? M : 1);
-    const size_t nt = (size_t)pool_tiles(M > 0 ? M : 1);
-    return 2 * pool_align(n * 8) + 2 * pool_align(n * 4) + pool_align(256 * nt * 4) + pool_align(nt * 4) +
-           pool_align((256 * nt / 8192 + 2) * 4);
-}
+size_t pmg_pool_cache_workspace_bytes(int64_t M) { return M < 0 ? 0 : radix_sort_workspace_bytes(M); }
 
 int pmg_pool_cache(const int32_t* coords, int64_t M, const int64_t* sparse_shape, const int32_t* stride,
                    const int64_t* out_sparse_shape, int32_t* out_coords, int32_t* parent, int32_t* seg_indices,
@@ -399,42 +442,19 @@ int pmg_pool_cache(const int32_t* coords, int64_t M, const int64_t* sparse_shape
         fill_u32(seg_offsets, 0u, 2, s);
         return check_launch("fill_u32");
     }
-    const size_t n = (size_t)M;
     const int nt = (int)pool_tiles(M);
-    char* p = (char*)workspace;
-    uint64_t* kb[2] = {(uint64_t*)p, (uint64_t*)(p + pool_align(n * 8))};
-    p += 2 * pool_align(n * 8);
-    int32_t* vb[2] = {(int32_t*)p, (int32_t*)(p + pool_align(n * 4))};
-    p += 2 * pool_align(n * 4);
-    uint32_t* hist = (uint32_t*)p;
-    p += pool_align(256 * (size_t)nt * 4);
-    uint32_t* tcnt = (uint32_t*)p;
-    p += pool_align((size_t)nt * 4);
-    uint32_t* ctot = (uint32_t*)p;
+    RadixBufs rb = radix_bufs(workspace, M);
+    uint32_t* tcnt = rb.tcnt;
+    uint32_t* ctot = rb.ctot;
 
     const unsigned g256 = (unsigned)((M + 255) / 256);
-    hipLaunchKernelGGL(pool_keys_k, dim3(g256), dim3(256), 0, s, (const int4*)coords, M, pg, kb[0],
+    hipLaunchKernelGGL(pool_keys_k, dim3(g256), dim3(256), 0, s, (const int4*)coords, M, pg, rb.keys[0],
                        (unsigned long long*)counts);
     if (int e = check_launch("pool_keys_k")) return e;
     // stable LSD radix sort of (key, row) over the significant bits of the output-grid keys
     const int bits = total > 1 ? 64 - __builtin_clzll(total - 1) : 1;
-    const int npass = (bits + 7) / 8;
-    int cur = 0;
-    for (int pass = 0; pass < npass; ++pass) {
-        const int shift = 8 * pass;
-        const uint64_t* kin = kb[cur];
-        const int32_t* vin = pass == 0 ? nullptr : vb[cur];
-        uint64_t* kout = kb[cur ^ 1];
-        int32_t* vout = pass == npass - 1 ? seg_indices : vb[cur ^ 1];
-        hipLaunchKernelGGL(pool_hist_k, dim3(nt), dim3(kPoolThreads), 0, s, kin, M, shift, nt, hist);
-        if (int e = check_launch("pool_hist_k")) return e;
-        if (int e = pool_scan(hist, 256 * nt, nullptr, ctot, s)) return e;
-        hipLaunchKernelGGL(pool_scatter_k, dim3(nt), dim3(kPoolThreads), 0, s, kin, vin, M, shift, nt,
-                           (const uint32_t*)hist, kout, vout);
-        if (int e = check_launch("pool_scatter_k")) return e;
-        cur ^= 1;
-    }
-    const uint64_t* sk = kb[cur];
+    if (int e = radix_sort_pairs(rb, M, bits, seg_indices, s)) return e;
+    const uint64_t* sk = rb.keys[rb.sorted];
     hipLaunchKernelGGL(pool_count_k, dim3(nt), dim3(kPoolThreads), 0, s, sk, M, tcnt);
     if (int e = check_launch("pool_count_k")) return e;
     if (int e = pool_scan(tcnt, nt, (unsigned long long*)counts, ctot, s)) return e;

@@ -113,17 +113,25 @@ def nmap_hash(coords: torch.Tensor, sparse_shape: Sequence[int], *, taps: bool =
     return (nt, tm, nr, rm) if row_mask else (nt, tm, nr)
 
 
-def row_order(row_mask: torch.Tensor):
-    """Processing order for spconv_i8_ordered: rows stably sorted by the top 16 bits of their tap mask, and the
-    tile masks [ceil(M/16)] of that order. Returns (order [M] int32, order_tile_mask)."""
+def row_order(row_mask: torch.Tensor, nmap_rows: Optional[torch.Tensor] = None):
+    """Processing order for spconv_i8_ordered: rows stably sorted by their 27-bit tap mask, the tile masks
+    [ceil(M/16)] of that order and, given the row-major map (nmap_hash(rows=True)), the tap-major map in that
+    order (the map spconv_i8_ordered reads). Returns (order [M] int32, order_tile_mask, nmap_o [27, M] | None)."""
     row_mask = _dev(row_mask, "row_mask", torch.int32)
     M = row_mask.shape[0]
-    order = torch.empty((M,), dtype=torch.int32, device=row_mask.device)
-    otm = torch.empty(((M + 15) // 16,), dtype=torch.int32, device=row_mask.device)
+    dev = row_mask.device
+    order = torch.empty((M,), dtype=torch.int32, device=dev)
+    otm = torch.empty(((M + 15) // 16,), dtype=torch.int32, device=dev)
+    nmo = None
+    if nmap_rows is not None:
+        nmap_rows = _dev(nmap_rows, "nmap_rows", torch.int32)
+        if tuple(nmap_rows.shape) != (M, 27) or not nmap_rows.is_contiguous():
+            raise ValueError("nmap_rows must be a contiguous (M, 27) map")
+        nmo = torch.empty((27, M), dtype=torch.int32, device=dev)
     ws_bytes = lib().pmg_row_order_workspace_bytes(M)
-    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=row_mask.device)
-    call("pmg_row_order", _p(row_mask), M, _p(order), _p(otm), _p(ws), ws_bytes, _stream())
-    return order, otm
+    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
+    call("pmg_row_order", _p(row_mask), _p(nmap_rows), M, _p(order), _p(otm), _p(nmo), _p(ws), ws_bytes, _stream())
+    return order, otm, nmo
 
 
 def pool_cache(coords: torch.Tensor, sparse_shape: Sequence[int], stride: Sequence[int],
@@ -232,12 +240,13 @@ def spconv_i8(x: torch.Tensor, nmap_t: torch.Tensor, tile_mask: torch.Tensor, w:
     return out
 
 
-def spconv_i8_ordered(x: torch.Tensor, nmap_t: torch.Tensor, order: torch.Tensor, order_tile_mask: torch.Tensor,
+def spconv_i8_ordered(x: torch.Tensor, nmap_o: torch.Tensor, order: torch.Tensor, order_tile_mask: torch.Tensor,
                       w: torch.Tensor, epilogue: int = EPI_ACC, *, a_scale: float = 1.0,
                       w_scale: Optional[torch.Tensor] = None, bias: Optional[torch.Tensor] = None,
                       out_mult: float = 1.0, skip: Optional[torch.Tensor] = None,
                       out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """spconv_i8 with rows processed in `order` (row_order): identical results, less MFMA work. Ci = Co = 64, 128."""
+    """spconv_i8 with rows processed in `order`, reading the map permuted into that order (row_order's nmap_o):
+    identical results, fewer taps per chunk of rows. Ci = Co = 64, 128."""
     x = _dev(x, "x", torch.int8)
     w = _dev(w, "w", torch.int8)
     order = _dev(order, "order", torch.int32)
@@ -247,7 +256,7 @@ def spconv_i8_ordered(x: torch.Tensor, nmap_t: torch.Tensor, order: torch.Tensor
         raise ValueError("weight must be (Co, 3, 3, 3, Ci)")
     if out is None:
         out = _conv_out(M, Co, epilogue, "i8", x.device)
-    call("pmg_spconv_i8_ordered", _p(x), _p(nmap_t), _p(order), _p(order_tile_mask), M, Ci, Co, _p(w), epilogue,
+    call("pmg_spconv_i8_ordered", _p(x), _p(nmap_o), _p(order), _p(order_tile_mask), M, Ci, Co, _p(w), epilogue,
          float(a_scale), _p(w_scale), _p(bias), float(out_mult), _p(skip), _p(out), _stream())
     return out
 

@@ -5,8 +5,9 @@
   H  int8, 756 x 1008, C = 64, K = 3, planes + thin cylinders, 20 % LiDAR holes filled on the device
      (nearest_fill): the fill bit-exact, each prompt fit and the final fit within 1e-5, and -- given the device's
      (s, t) -- the refined point map bit-exact at every step
-  U  the 1M-voxel conv microbench set: the hash map bit-exact against the sorted map over all 27 x 1M entries, and
-     the int8 convolution with per-channel requantisation bit-exact on 65,536 sampled rows at C = 64 and 128
+  U  the 1M-voxel conv microbench set: the hash map bit-exact against the sorted map over all 27 x 1M entries, the
+     int8 convolution with per-channel requantisation bit-exact on 65,536 sampled rows at C = 64 and 128, and the
+     benchmarked mask-sorted (ordered) convolution identical to it on every row
 """
 import numpy as np
 import pytest
@@ -87,7 +88,7 @@ def test_microbench_set_map_and_conv(gpu, C):
     coords = spec.make_voxels(1_000_000, 1024, seed=21)
     M = coords.shape[0]
     shape = (1, 1024, 1024, 1024)
-    nt, tm, _ = ops.nmap_hash(torch.from_numpy(coords).to(gpu), shape)
+    nt, tm, nr, rm = ops.nmap_hash(torch.from_numpy(coords).to(gpu), shape, rows=True, row_mask=True)
     nmap = ost.nmap_sorted(coords, shape)
     assert np.array_equal(nt.cpu().numpy().T, nmap)
     assert np.array_equal(tm.cpu().numpy().view(np.uint32), ost.tile_masks(nmap))
@@ -105,3 +106,8 @@ def test_microbench_set_map_and_conv(gpu, C):
     plain = np.clip(np.rint(acc.astype(np.float32) * mult[None, :]), -127, 127).astype(np.int8)
     assert np.array_equal(ref, plain)
     assert (ref != 0).mean() > 0.3  # the codes are not all zero
+    # the benchmarked path: rows in mask-sorted order, the map permuted into it -- identical codes for every row
+    order, otm, nmo = ops.row_order(rm, nr)
+    qo = ops.spconv_i8_ordered(torch.from_numpy(x).to(gpu), nmo, order, otm, torch.from_numpy(w).to(gpu),
+                               ops.EPI_QLIN, a_scale=1.0, w_scale=torch.from_numpy(mult).to(gpu), out_mult=1.0)
+    assert np.array_equal(qo.cpu().numpy(), q)

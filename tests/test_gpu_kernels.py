@@ -236,38 +236,41 @@ def test_conv_int8_generic_map(gpu):
 
 
 def test_row_order_is_a_stable_sort_by_mask(gpu):
-    """pmg_row_order: within each window of 4096 consecutive rows, a permutation sorting the rows stably by the top
-    16 bits of their tap mask, with the tile unions of that order; the hash's row masks are the bits of its map
-    rows. 200k rows end in a ragged window."""
+    """pmg_row_order: a permutation sorting the rows stably by their whole 27-bit tap mask, the tile unions of that
+    order, and the tap-major map permuted into it; the hash's row masks are the bits of its map rows. 200,001 rows
+    end in a ragged tile and a ragged radix tile."""
     announce("row order 200k surface voxels")
-    coords = spec.make_voxels(200_000, grid=512, seed=5)
+    coords = spec.make_voxels(200_001, grid=512, seed=5)
     shape = (1, 512, 512, 512)
     nt, tm, nr, rm = ops.nmap_hash(_t(coords, gpu), shape, rows=True, row_mask=True)
-    order, otm = ops.row_order(rm)
+    order, otm, nmo = ops.row_order(rm, nr)
     torch.cuda.synchronize()
     rows = nr.cpu().numpy()
     masks = ((rows >= 0).astype(np.uint64) << np.arange(27, dtype=np.uint64)).sum(1).astype(np.uint32)
     assert np.array_equal(rm.cpu().numpy().view(np.uint32), masks)
-    win = 4096
-    expect = np.concatenate([s + np.argsort(masks[s:s + win] >> 11, kind="stable")
-                             for s in range(0, len(masks), win)])
-    assert len(masks) % win != 0
+    expect = np.argsort(masks, kind="stable")
     assert np.array_equal(order.cpu().numpy(), expect)
     m = masks[expect]
+    assert np.all(m[1:] >= m[:-1]) and len(m) % 16 != 0
     pad = np.zeros(((len(m) + 15) // 16) * 16, np.uint32)
     pad[:len(m)] = m
     assert np.array_equal(otm.cpu().numpy().view(np.uint32), np.bitwise_or.reduce(pad.reshape(-1, 16), axis=1))
+    assert np.array_equal(nmo.cpu().numpy(), nt.cpu().numpy()[:, expect])
+    # without a map: the same order and tile masks
+    o2, otm2, none = ops.row_order(rm)
+    assert none is None and torch.equal(o2, order) and torch.equal(otm2, otm)
 
 
 @pytest.mark.parametrize("C", [64, 128])
 def test_conv_int8_ordered_matches_unordered(gpu, C):
-    """The ordered convolution gives bit-identical results to the plain one (accumulators and every epilogue)."""
+    """The ordered convolution (map permuted into the mask-sorted order, outputs scattered back) gives
+    bit-identical results to the plain one (accumulators and every epilogue) and to the oracle."""
     announce(f"conv int8 ordered C={C}")
     rng = np.random.default_rng(C + 1)
     coords = spec.make_voxels(70_001, grid=256, seed=4)
     shape = (1, 256, 256, 256)
-    nt, tm, _, rm = ops.nmap_hash(_t(coords, gpu), shape, row_mask=True)
-    order, otm = ops.row_order(rm)
+    nt, tm, nr, rm = ops.nmap_hash(_t(coords, gpu), shape, rows=True, row_mask=True)
+    order, otm, nmo = ops.row_order(rm, nr)
     M = coords.shape[0]
     x = _t(rng.integers(-127, 128, size=(M, C)).astype(np.int8), gpu)
     w = _t(rng.integers(-127, 128, size=(C, 3, 3, 3, C)).astype(np.int8), gpu)
@@ -278,11 +281,11 @@ def test_conv_int8_ordered_matches_unordered(gpu, C):
     for epi, extra in ((ops.EPI_ACC, {}), (ops.EPI_Q, {}), (ops.EPI_R, {"skip": skip}), (ops.EPI_BIAS, {}),
                        (ops.EPI_QLIN, {})):
         a = ops.spconv_i8(x, nt, tm, w, epi, **kw, **extra)
-        o = ops.spconv_i8_ordered(x, nt, order, otm, w, epi, **kw, **extra)
+        o = ops.spconv_i8_ordered(x, nmo, order, otm, w, epi, **kw, **extra)
         torch.cuda.synchronize()
         assert torch.equal(a, o), epi
     nm = ost.nmap_sorted(coords, shape)
-    assert np.array_equal(ops.spconv_i8_ordered(x, nt, order, otm, w).cpu().numpy(),
+    assert np.array_equal(ops.spconv_i8_ordered(x, nmo, order, otm, w).cpu().numpy(),
                           ocv.conv_acc_int(x.cpu().numpy(), nm, w.cpu().numpy()))
 
 
