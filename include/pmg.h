@@ -91,15 +91,16 @@ int pmg_nmap_hash(const int32_t* coords, int64_t M, const int64_t* sparse_shape_
                   size_t workspace_bytes, void* stream);
 
 /* pmg_row_order -- a processing order for pmg_spconv_i8_ordered (no counterpart in the reference; it changes no
- * result): the rows sorted, stably, by their 27-bit tap mask (row_mask [M], bit v = tap v present, as
- * pmg_nmap_hash writes it), so that the tiles and chunks of the convolution run few taps while rows of one
+ * result): within each window of `window` consecutive rows (0: one window), the rows sorted, stably, by their
+ * 27-bit tap mask (row_mask [M], bit v = tap v present, as pmg_nmap_hash writes it), so that the tiles and chunks
+ * of the convolution run few taps while a window's rows stay in one part of the volume and rows of one
  * neighbourhood pattern keep the caller's order. order [M] int32 = row indices in processing order;
  * order_tile_mask [ceil(M/16)] = the union of the tap masks of order[16t .. 16t+15]; nmap_o [27][M] (optional,
  * with nmap_rows, the row-major (M, 27) map pmg_nmap_hash writes) = the tap-major map in processing order,
  * nmap_o[v][p] = nmap_rows[order[p]][v] -- the map pmg_spconv_i8_ordered reads. Workspace:
  * pmg_row_order_workspace_bytes(M) (any contents). M < 2^31. */
 size_t pmg_row_order_workspace_bytes(int64_t M);
-int pmg_row_order(const uint32_t* row_mask, const int32_t* nmap_rows, int64_t M, int32_t* order,
+int pmg_row_order(const uint32_t* row_mask, const int32_t* nmap_rows, int64_t M, int64_t window, int32_t* order,
                   uint32_t* order_tile_mask, int32_t* nmap_o, void* workspace, size_t workspace_bytes, void* stream);
 
 /* pmg_pool_cache -- build_pool_cache (promptmoge/_fallback/flex_gemm/_core.py:339-395) for the perfect-partition

@@ -96,7 +96,7 @@ SIGNATURES = {
     "pmg_sparse_pool": (i32, [vp, i64, i32, vp, vp, i64, i32, vp, vp]),
     "pmg_sparse_upsample": (i32, [vp, i64, vp, i64, vp, vp]),
     "pmg_row_order_workspace_bytes": (sz, [i64]),
-    "pmg_row_order": (i32, [vp, vp, i64, vp, vp, vp, vp, sz, vp]),
+    "pmg_row_order": (i32, [vp, vp, i64, i64, vp, vp, vp, vp, sz, vp]),
     "pmg_nmap_from_rows": (i32, [vp, i64, vp, vp, vp]),
     "pmg_kmap_workspace_bytes": (sz, [i64]),
     "pmg_kmap_compact": (i32, [vp, i64, vp, vp, vp, i64, vp, sz, vp]),

@@ -113,10 +113,14 @@ def nmap_hash(coords: torch.Tensor, sparse_shape: Sequence[int], *, taps: bool =
     return (nt, tm, nr, rm) if row_mask else (nt, tm, nr)
 
 
-def row_order(row_mask: torch.Tensor, nmap_rows: Optional[torch.Tensor] = None):
-    """Processing order for spconv_i8_ordered: rows stably sorted by their 27-bit tap mask, the tile masks
-    [ceil(M/16)] of that order and, given the row-major map (nmap_hash(rows=True)), the tap-major map in that
-    order (the map spconv_i8_ordered reads). Returns (order [M] int32, order_tile_mask, nmap_o [27, M] | None)."""
+ROW_ORDER_WINDOW = 1 << 18
+
+
+def row_order(row_mask: torch.Tensor, nmap_rows: Optional[torch.Tensor] = None, window: int = ROW_ORDER_WINDOW):
+    """Processing order for spconv_i8_ordered: within windows of `window` consecutive rows (0: one window), rows
+    stably sorted by their 27-bit tap mask; the tile masks [ceil(M/16)] of that order and, given the row-major map
+    (nmap_hash(rows=True)), the tap-major map in that order (the map spconv_i8_ordered reads).
+    Returns (order [M] int32, order_tile_mask, nmap_o [27, M] | None)."""
     row_mask = _dev(row_mask, "row_mask", torch.int32)
     M = row_mask.shape[0]
     dev = row_mask.device
@@ -130,7 +134,7 @@ def row_order(row_mask: torch.Tensor, nmap_rows: Optional[torch.Tensor] = None):
         nmo = torch.empty((27, M), dtype=torch.int32, device=dev)
     ws_bytes = lib().pmg_row_order_workspace_bytes(M)
     ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
-    call("pmg_row_order", _p(row_mask), _p(nmap_rows), M, _p(order), _p(otm), _p(nmo), _p(ws), ws_bytes, _stream())
+    call("pmg_row_order", _p(row_mask), _p(nmap_rows), M, int(window), _p(order), _p(otm), _p(nmo), _p(ws), ws_bytes, _stream())
     return order, otm, nmo
 
 

@@ -236,29 +236,33 @@ def test_conv_int8_generic_map(gpu):
 
 
 def test_row_order_is_a_stable_sort_by_mask(gpu):
-    """pmg_row_order: a permutation sorting the rows stably by their whole 27-bit tap mask, the tile unions of that
-    order, and the tap-major map permuted into it; the hash's row masks are the bits of its map rows. 200,001 rows
-    end in a ragged tile and a ragged radix tile."""
+    """pmg_row_order: a permutation sorting the rows of each window stably by their whole 27-bit tap mask, the tile
+    unions of that order, and the tap-major map permuted into it; the hash's row masks are the bits of its map rows.
+    200,001 rows end in a ragged window, a ragged tile and a ragged radix tile."""
     announce("row order 200k surface voxels")
     coords = spec.make_voxels(200_001, grid=512, seed=5)
     shape = (1, 512, 512, 512)
     nt, tm, nr, rm = ops.nmap_hash(_t(coords, gpu), shape, rows=True, row_mask=True)
-    order, otm, nmo = ops.row_order(rm, nr)
+    order, otm, nmo = ops.row_order(rm, nr, window=65536)
     torch.cuda.synchronize()
     rows = nr.cpu().numpy()
     masks = ((rows >= 0).astype(np.uint64) << np.arange(27, dtype=np.uint64)).sum(1).astype(np.uint32)
     assert np.array_equal(rm.cpu().numpy().view(np.uint32), masks)
-    expect = np.argsort(masks, kind="stable")
+    win = 65536
+    expect = np.concatenate([s + np.argsort(masks[s:s + win], kind="stable") for s in range(0, len(masks), win)])
     assert np.array_equal(order.cpu().numpy(), expect)
     m = masks[expect]
-    assert np.all(m[1:] >= m[:-1]) and len(m) % 16 != 0
+    assert np.all(m[1:win] >= m[:win - 1]) and len(m) % 16 != 0 and len(m) % win != 0
     pad = np.zeros(((len(m) + 15) // 16) * 16, np.uint32)
     pad[:len(m)] = m
     assert np.array_equal(otm.cpu().numpy().view(np.uint32), np.bitwise_or.reduce(pad.reshape(-1, 16), axis=1))
     assert np.array_equal(nmo.cpu().numpy(), nt.cpu().numpy()[:, expect])
     # without a map: the same order and tile masks
-    o2, otm2, none = ops.row_order(rm)
+    o2, otm2, none = ops.row_order(rm, window=65536)
     assert none is None and torch.equal(o2, order) and torch.equal(otm2, otm)
+    # one window: the whole set sorted by mask
+    o3, _, _ = ops.row_order(rm, window=0)
+    assert np.array_equal(o3.cpu().numpy(), np.argsort(masks, kind="stable"))
 
 
 @pytest.mark.parametrize("C", [64, 128])
