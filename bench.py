@@ -303,7 +303,7 @@ def fit_trace(args):
     (100 MHz) at the launch, after the first solve and after every trim round, with the round's selection path
     (0 bracket, 1 bracket missed -> radix, 2 radix, 3 radix + third pass), its candidate count, and the number of
     rounds run (the loop stops at a fixed point). Prints one line per round for the prompt fit and the final fit of
-    the configuration (the last of 20 runs each)."""
+    the configuration, on its input point map and on the map one refiner step made (the last of 20 runs each)."""
     import numpy as np
     import torch
 
@@ -311,11 +311,15 @@ def fit_trace(args):
 
     env = setup(args.config)
     cfg = env["cfg"]
-    P, L, Cf = env["P"], env["L"], env["Cf"]
+    P, L, Cf, Pr = env["P"], env["L"], env["Cf"], env["Pout"]
     names = {0: "bracket", 1: "bracket missed -> radix", 2: "radix", 3: "radix + third pass"}
     with torch.cuda.stream(env["stream"]):
+        # on the input point map, and on the map one refiner step made (what the final fit and the prompt fits of
+        # later steps see)
         for name, run in (("prompt fit", lambda: ops.fit_prompt(P, L, Cf, iters=cfg.fit_iters)),
-                          ("final fit", lambda: ops.fit_final(P, L, Cf, iters=cfg.fit_iters))):
+                          ("final fit", lambda: ops.fit_final(P, L, Cf, iters=cfg.fit_iters)),
+                          ("prompt fit on the refined map", lambda: ops.fit_prompt(Pr, L, Cf, iters=cfg.fit_iters)),
+                          ("final fit on the refined map", lambda: ops.fit_final(Pr, L, Cf, iters=cfg.fit_iters))):
             for _ in range(20):
                 run()
             torch.cuda.synchronize()
