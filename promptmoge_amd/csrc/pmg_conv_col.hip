@@ -456,33 +456,35 @@ __global__ __launch_bounds__(kColThreads) void spconv_col_k(ColConvArgs a) {
     }
 }
 
-// Weights beyond LDS residency (int8 C = 128, fp16 C = 48 / 64: 124-442 KB): the same segments and windows, with
-// the taps staged. The block walks the union of its 8 waves' active taps in ascending order; each tap's weights
-// (C x 27 x Ci -> C x Ci) are staged once per block into LDS in MFMA operand order -- lane (r, g) of fragment
-// (s, j) holds W[16j + r][v][chunk 4s + g], zero where 4s + g is past the row (the K padding of C = 48 in fp16) --
-// and feed all eight waves, where the resident-weight kernel above would read every operand from L2 once per wave
-// and MFMA step. Tap t + 1's weights are written while tap t's MFMAs run (two LDS buffers, one barrier per tap);
-// their global loads are issued two taps ahead. A wave whose rows lack a tap skips its MFMAs. The next segment's
-// window is loaded into registers during the taps (after the epilogue at C/16 > 4, where registers run out) and
-// written once every wave has left the current one.
+// Weights beyond LDS residency (int8 C = 128, fp16 C = 48 / 64: 124-442 KB): the taps staged, on 2-D tiles. A
+// block takes tiles of WV image rows x 32 columns (wave w: row w, two 16-voxel MFMA tiles) and keeps the tile's
+// window -- (WV + 2) x 34 pixels, codes and keys -- in LDS: 1.3 x the tile's pixels where a 256-voxel run of one
+// image row needs a 3 x 258 window (2.3 x less window traffic), so two windows fit beside the staged weights and
+// the next tile's window is loaded during this tile's taps and epilogue. The block walks the union of its waves'
+// active taps in ascending order; each tap's weights (C x 27 x Ci -> C x Ci) are staged once per block into LDS in
+// MFMA operand order -- lane (r, g) of fragment (s, j) holds W[16j + r][v][chunk 4s + g], zero where 4s + g is
+// past the row (the K padding of C = 48 in fp16) -- and feed all the waves. Tap t + 1's weights are written while
+// tap t's MFMAs run (two LDS buffers, one barrier per tap); their global loads are issued two taps ahead, and the
+// next window right after the tile's last weight load (the memory counter completes in order, so a window
+// requested earlier would hold every later weight store behind it). A wave whose rows lack a tap skips its MFMAs.
 template <typename T, int C, int EPI, int WV>
 __global__ __launch_bounds__(64 * WV) void spconv_cols_k(ColConvArgs a) {
-    constexpr int kThreads = 64 * WV, kSegS = 32 * WV, kWinS = kSegS + 2;
+    constexpr int kThreads = 64 * WV;
+    constexpr int TC = 32, WR = WV + 2, WC = TC + 2, WPIX = WR * WC;  // tile columns; window rows, columns
     constexpr int ROWB = C * (int)sizeof(T), NCH = ROWB / 16, NB = C / 16;
-    constexpr int XBYTES = 3 * kWinS * ROWB;
-    constexpr int PF = (3 * kWinS * NCH + kThreads - 1) / kThreads;  // window chunks per thread
-    constexpr int PFZ = (3 * kWinS + kThreads - 1) / kThreads;       // window keys per thread
+    constexpr int XBYTES = WPIX * ROWB;
+    constexpr int PF = (WPIX * NCH + kThreads - 1) / kThreads;  // window chunks per thread
+    constexpr int PFZ = (WPIX + kThreads - 1) / kThreads;       // window keys per thread
     constexpr int SPT = (NCH + 3) / 4;       // MFMA steps per tap; lane group g of step s takes chunk 4s + g
     constexpr int FR = SPT * NB;             // 1 KB operand fragments per tap
     constexpr int WPT = (FR * 64 + kThreads - 1) / kThreads;  // staged 16-byte pieces per thread per tap
-    // the next window is prefetched during the taps where the registers allow (up to 64 output channels)
     constexpr bool kPre = NB <= 4;
     typedef typename ColAcc<T>::type acc_t;
-    static_assert(XBYTES + 2 * FR * 1024 + 3 * kWinS * 4 + 64 <= 160 * 1024, "window and two taps must fit LDS");
+    static_assert(2 * XBYTES + 2 * FR * 1024 + 2 * WPIX * 4 + 64 <= 160 * 1024, "two windows and two taps must fit LDS");
 
     __shared__ __attribute__((aligned(16))) v4i s_w[2][FR * 64];
-    __shared__ __attribute__((aligned(16))) uint8_t s_x[XBYTES];
-    __shared__ int s_z[3 * kWinS];
+    __shared__ __attribute__((aligned(16))) uint8_t s_x[2][XBYTES];
+    __shared__ int s_z[2][WPIX];
     __shared__ __attribute__((aligned(16))) uint8_t s_zero[16];
     __shared__ uint32_t s_uni[WV];
 
@@ -491,6 +493,7 @@ __global__ __launch_bounds__(64 * WV) void spconv_cols_k(ColConvArgs a) {
     const int M = (int)a.M;
     const int H = a.H, W = a.W;
     const int HW = H * W;
+    const int th = (H + WV - 1) / WV, tw = (W + TC - 1) / TC;  // tiles per frame: th x tw
     const uint8_t* __restrict__ xg = (const uint8_t*)a.x;
     const uint8_t* __restrict__ wg = (const uint8_t*)a.w;
     if (tid == 0) *(v4i*)s_zero = v4i{0, 0, 0, 0};
@@ -517,79 +520,93 @@ __global__ __launch_bounds__(64 * WV) void spconv_cols_k(ColConvArgs a) {
         }
     };
 
+    // tile t of the batch: frame b, image rows i0 .. i0 + WV - 1, columns j0 .. j0 + TC - 1
+    auto tile_origin = [&](int t, int& b, int& i0, int& j0) {
+        b = t / (th * tw);
+        const int q = t - b * (th * tw);
+        i0 = (q / tw) * WV;
+        j0 = (q - (q / tw) * tw) * TC;
+    };
+    // Window of tile t: slot (wr, wc) holds pixel (i0 - 1 + wr, j0 - 1 + wc) of the frame; slots outside the frame
+    // hold zero codes and a key no voxel matches. Rows of 34 pixels are contiguous in memory (coalesced loads).
     v4i pf[PF];
     int pfz[PFZ];
-    auto fetch = [&](int sg) {
-        const int s0 = sg * kSegS;
+    auto fetch = [&](int t) {
+        int b, i0, j0;
+        tile_origin(t, b, i0, j0);
+        const int64_t fb = (int64_t)b * HW;
 #pragma unroll
         for (int k = 0; k < PF; ++k) {
             const int e = tid + k * kThreads;
             pf[k] = v4i{0, 0, 0, 0};
-            if (e < 3 * kWinS * NCH) {
-                const int d = e / (kWinS * NCH);
-                const int rem = e - d * (kWinS * NCH);
-                const int q = rem / NCH, c = rem - (rem / NCH) * NCH;
-                const int p = s0 + (d - 1) * W - 1 + q;
-                if (p >= 0 && p < M) pf[k] = *(const v4i*)(xg + (int64_t)p * ROWB + c * 16);
+            if (e < WPIX * NCH) {
+                const int px = e / NCH, c = e - (e / NCH) * NCH;
+                const int i = i0 - 1 + px / WC, j = j0 - 1 + (px - (px / WC) * WC);
+                if ((unsigned)i < (unsigned)H && (unsigned)j < (unsigned)W)
+                    pf[k] = *(const v4i*)(xg + (fb + (int64_t)i * W + j) * ROWB + c * 16);
             }
         }
 #pragma unroll
         for (int k = 0; k < PFZ; ++k) {
             const int e = tid + k * kThreads;
             pfz[k] = kZFar;
-            if (e < 3 * kWinS) {
-                const int d = e / kWinS, q = e - (e / kWinS) * kWinS;
-                const int p = s0 + (d - 1) * W - 1 + q;
-                if (p >= 0 && p < M) pfz[k] = a.zq[p];
+            if (e < WPIX) {
+                const int i = i0 - 1 + e / WC, j = j0 - 1 + (e - (e / WC) * WC);
+                if ((unsigned)i < (unsigned)H && (unsigned)j < (unsigned)W) pfz[k] = a.zq[fb + (int64_t)i * W + j];
             }
         }
     };
-    auto commit = [&]() {
+    auto commit = [&](int buf) {
 #pragma unroll
         for (int k = 0; k < PF; ++k) {
             const int e = tid + k * kThreads;
-            if (e < 3 * kWinS * NCH) ((v4i*)s_x)[e] = pf[k];
+            if (e < WPIX * NCH) ((v4i*)s_x[buf])[e] = pf[k];
         }
 #pragma unroll
         for (int k = 0; k < PFZ; ++k) {
             const int e = tid + k * kThreads;
-            if (e < 3 * kWinS) s_z[e] = pfz[k];
+            if (e < WPIX) s_z[buf][e] = pfz[k];
         }
     };
 
-    // XCD-aware segment order, as in spconv_col_k
+    // XCD-aware tile order: one contiguous band of tiles (raster order) per XCD (block b runs on XCD b % 8), dealt
+    // round-robin to that XCD's blocks, so the rows and columns neighbouring tiles share stay in its L2.
     const int nx = gridDim.x < 8 ? (int)gridDim.x : 8;
     const int xcd = (int)blockIdx.x % nx, ib = (int)blockIdx.x / nx;
     const int nbx = ((int)gridDim.x - xcd + nx - 1) / nx;
-    const int nseg_all = (M + kSegS - 1) / kSegS;
-    const int nseg = (int)((int64_t)nseg_all * (xcd + 1) / nx);
-    int seg = (int)((int64_t)nseg_all * xcd / nx) + ib;
-    if (seg < nseg) {
-        fetch(seg);
-        commit();
+    const int ntile = (M / HW) * th * tw;  // M = frames x H x W
+    const int tend = (int)((int64_t)ntile * (xcd + 1) / nx);  // end of this XCD's band
+    int tile = (int)((int64_t)ntile * xcd / nx) + ib;
+    if (tile < tend) {
+        fetch(tile);
+        commit(0);
     }
     typedef const __attribute__((address_space(3))) uint8_t* lds_ptr;
     typedef const __attribute__((address_space(3))) v4i lds_v4i;
-    for (; seg < nseg; seg += nbx) {
-        const int s0 = seg * kSegS;
-        const int nxt = seg + nbx;
-        __syncthreads();  // window visible; every wave has left the previous segment's weight buffers
+    for (int it = 0; tile < tend; tile += nbx, ++it) {
+        const int xb = it & 1;  // this tile's window buffer
+        const int nxt = tile + nbx;
+        int b, i0, j0;
+        tile_origin(tile, b, i0, j0);
+        __syncthreads();  // window visible; every wave has left the previous tile's window and weight buffers
+        const uint8_t* const sx = s_x[xb];
+        const int* const sz = s_z[xb];
 
-        // ---- 27-bit tap masks of the wave's 32 rows (lane l < 32: row l), the wave's union and the block's
+        // ---- 27-bit tap masks of the wave's 32 voxels (lane l < 32: column l of row wv), the wave's union and the
+        // block's
+        const int i = i0 + wv;
         uint32_t mk = 0;
         {
-            const int lr = 32 * wv + (lane & 31);
-            const int m = s0 + lr;
-            if (lane < 32 && m < M) {
-                const int pix = m % HW;
-                const int i = pix / W, j = pix - (pix / W) * W;
-                const int zc = s_z[kWinS + lr + 1];
+            const int lr = lane & 31;
+            const int j = j0 + lr;
+            if (lane < 32 && i < H && j < W) {
+                const int zc = sz[(wv + 1) * WC + lr + 1];
 #pragma unroll
                 for (int di = 0; di < 3; ++di)
 #pragma unroll
                     for (int dj = 0; dj < 3; ++dj) {
                         const bool in = (unsigned)(i + di - 1) < (unsigned)H && (unsigned)(j + dj - 1) < (unsigned)W;
-                        const int64_t dz = (int64_t)s_z[di * kWinS + lr + dj] - zc;
+                        const int64_t dz = (int64_t)sz[(wv + di) * WC + lr + dj] - zc;
                         const bool hit = in && dz >= -1 && dz <= 1;
                         mk |= (hit ? 1u : 0u) << (di * 9 + dj * 3 + (int)(dz + 1 < 0 ? 0 : (dz + 1 > 2 ? 2 : dz + 1)));
                     }
@@ -614,9 +631,9 @@ __global__ __launch_bounds__(64 * WV) void spconv_cols_k(ColConvArgs a) {
             for (int j = 0; j < NB; ++j) acc[rb][j] = acc_t{0, 0, 0, 0};
 
         // operand addresses: lane-constant LDS offsets plus a wave-uniform offset per (tap, step); a lane whose
-        // row lacks the tap, or whose chunk is padding, reads the zero slot
-        const int lr0 = 32 * wv + r;
-        const lds_ptr xbase = (lds_ptr)s_x + (lr0 * ROWB + g * 16);
+        // voxel lacks the tap, or whose chunk is padding, reads the zero slot. Window slot of the neighbour (di, dj)
+        // of column c of row wv: (wv + di) * WC + c + dj.
+        const lds_ptr xbase = (lds_ptr)sx + ((wv * WC + r) * ROWB + g * 16);
         const lds_ptr zslot = (lds_ptr)s_zero;
 
         // tap sequence: ascending bits of bu, -1 after the last
@@ -634,9 +651,9 @@ __global__ __launch_bounds__(64 * WV) void spconv_cols_k(ColConvArgs a) {
         w_store(0, wa);
         __syncthreads();
 
-        // The next window is requested right after the segment's last weight load: the memory counter completes
-        // in order, so a window requested earlier would hold up every later weight store behind it.
-        bool fetched = !kPre || nxt >= nseg;
+        // (the next window is requested during the taps up to 64 output channels; beyond, the registers of its
+        // pieces would spill, and it is requested after the epilogue)
+        bool fetched = nxt >= tend || !kPre;
         auto tap = [&](int buf, int v, const v4i (&wnext)[WPT], v4i (&wlater)[WPT], int vlater) {
             // the weights two taps ahead are requested before this tap's matrix work
             w_load(vlater, wlater);
@@ -645,7 +662,7 @@ __global__ __launch_bounds__(64 * WV) void spconv_cols_k(ColConvArgs a) {
                 fetched = true;
             }
             if ((uni >> v) & 1u) {
-                const int xo = ((v / 9) * kWinS + (v / 3) % 3) * ROWB;
+                const int xo = ((v / 9) * WC + (v / 3) % 3) * ROWB;
                 const bool h0 = (mrow0 >> v) & 1u, h1 = (mrow1 >> v) & 1u;
                 // every operand of the tap is requested before its first MFMA (LDS returns in order, so the MFMAs
                 // of step 0 wait only for step 0's reads)
@@ -686,22 +703,22 @@ __global__ __launch_bounds__(64 * WV) void spconv_cols_k(ColConvArgs a) {
             v2 = pop();
         }
 
-        if (!fetched) fetch(nxt);  // at most two taps: every weight load came before the loop
+        if (kPre && !fetched) fetch(nxt);  // at most two taps: every weight load came before the loop
 
-        // ---- epilogue
+        // ---- epilogue: voxel of row wv, column 16 rb + r (M: outside the frame, nothing stored)
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb) {
+            const int j = j0 + 16 * rb + r;
+            const int m = i < H && j < W ? b * HW + i * W + j : M;
             v4f sk[NB];
-            if constexpr (EPI == PMG_EPI_R || EPI == PMG_EPI_RLN || EPI == PMG_EPI_ROUT)
-                load_skip<C>(a, s0 + 32 * wv + 16 * rb + r, M, g, sk);
-            col_epilogue<T, C, EPI>(a, acc[rb], s0 + 32 * wv + 16 * rb + r, M, g, epi_global(a), sk);
+            if constexpr (EPI == PMG_EPI_R || EPI == PMG_EPI_RLN || EPI == PMG_EPI_ROUT) load_skip<C>(a, m, M, g, sk);
+            col_epilogue<T, C, EPI>(a, acc[rb], m, M, g, epi_global(a), sk);
         }
 
-        // ---- the next window: written once every wave has left this one
-        if (nxt < nseg) {
+        // ---- the next tile's window into the other buffer (every wave left it before this tile began)
+        if (nxt < tend) {
             if constexpr (!kPre) fetch(nxt);
-            __syncthreads();
-            commit();
+            commit(xb ^ 1);
         }
     }
 }
@@ -713,9 +730,10 @@ static int launch_col3(const ColConvArgs& a, hipStream_t s) {
     } else {
         const int64_t nseg = (a.M + kSeg - 1) / kSeg;
         if constexpr (!ColGeom<T, C>::WLDS) {
-            // 8-wave blocks of 256-voxel segments, one per CU (LDS)
+            // 8-wave blocks of 8 x 32-voxel tiles, one per CU (LDS)
             constexpr int WV = 8;
-            const int64_t nseg4 = (a.M + 32 * WV - 1) / (32 * WV);
+            const int64_t HW = (int64_t)a.H * a.W;
+            const int64_t nseg4 = (a.M / HW) * ((a.H + WV - 1) / WV) * ((a.W + 31) / 32);
             static int per_cu = -1;
             if (per_cu < 0) {
                 int n = 0;

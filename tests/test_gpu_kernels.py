@@ -599,6 +599,31 @@ def test_conv_col_f16(gpu, C):
     _assert_f16_ulp(h, onm.silu_f32((got + b).astype(np.float32)).astype(np.float16))
 
 
+@pytest.mark.parametrize("prec,C", [("int8", 128), ("fp16", 64), ("fp16", 48)])
+def test_conv_col_staged_ragged_tiles(gpu, prec, C):
+    """The staged-weight level-0 convolution works on tiles of 8 image rows x 32 columns: a 61 x 83 frame (neither
+    a multiple of the tile) in a batch of three, against the dense oracle (int8 bit-exact, fp16 within its
+    accumulation bound)."""
+    announce(f"conv col staged {prec} C={C} 61x83 x3")
+    rng = np.random.default_rng(300 + C)
+    pts, zq_o, nm, zq = _col_setup(gpu, H=61, W=83, seed=11, B=3)
+    M = nm.shape[0]
+    if prec == "int8":
+        x = rng.integers(-127, 128, size=(M, C)).astype(np.int8)
+        w = rng.integers(-127, 128, size=(C, 3, 3, 3, C)).astype(np.int8)
+        acc = ops.spconv_col(_t(x, gpu), zq, _t(w, gpu), ops.EPI_ACC)
+        assert np.array_equal(acc.cpu().numpy(), ocv.conv_acc_int(x, nm, w))
+    else:
+        x = rng.normal(size=(M, C)).astype(np.float16)
+        w = rng.normal(0, 0.05, size=(C, 3, 3, 3, C)).astype(np.float16)
+        ref = ocv.conv_float(x.astype(np.float64), nm, w.astype(np.float64), dtype=np.float64)
+        got = ops.spconv_col(_t(x, gpu), zq, _t(w, gpu), ops.EPI_ACC).cpu().numpy()
+        bound = 27 * C * 2 ** -23 * ocv.conv_float(np.abs(x.astype(np.float64)), nm, np.abs(w.astype(np.float64)),
+                                                    dtype=np.float64)
+        assert (np.abs(got - ref) <= bound + 1e-6).all()
+    assert (nm >= 0).sum(1).mean() > 1.5  # the scene has neighbours, not only centre taps
+
+
 def test_post_depth_after_final_fit(gpu):
     """post_depth (MetricFit.metal:200-211) on the device's final fit: bit-exact against the oracle given the same
     (s, t), +inf off the mask; and the fused step's post_depth option writes the same map."""
