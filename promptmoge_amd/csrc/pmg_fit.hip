@@ -195,7 +195,7 @@ __device__ inline unsigned block_excl_scan2(unsigned a, unsigned b, uint2* tmp, 
 #endif
 struct FitShared {
     unsigned hist[kFitBins];
-    uint32_t cand[kCandCap];
+    alignas(16) uint32_t cand[kCandCap];
     unsigned off[kFitMaxBlocks + 1];
     double red[5][kFitWaves];
     unsigned tmp[kFitWaves];
@@ -203,7 +203,6 @@ struct FitShared {
     float s, t;
     long long kk;
     int ok;
-    int same;  // the last solve reproduced the previous (s, t) bit for bit
     unsigned bin, below;
     unsigned total_below, total_cand;
     uint32_t blo_last, bhi_last;  // bracket of the last stage
@@ -359,36 +358,50 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
         }
     };
     float s = 1.0f, t = 0.0f;
-    // Closed-form weighted LS on the global sums (prompt_stem.py:222-232); thread 0 decides, all threads read.
+    bool same = false;  // the last solve reproduced the previous (s, t) bit for bit
+    // Closed-form weighted LS on the global sums (prompt_stem.py:222-232). The first solve: thread 0 also decides
+    // the fallback and k, all threads read. Later solves: every thread holds the same sums (fixed-order block
+    // reductions), so each computes the same (s, t) with the same fp64 operations and no broadcast is needed.
+    auto ls = [&](const double (&g)[5], bool ok, float& ns, float& nt) {
+        const double n = g[0], sx = g[1], sy = g[2], sxx = g[3], sxy = g[4];
+        const double nn = n > 1.0 ? n : 1.0;
+        const double den = nn * sxx - sx * sx;
+        const double sn = den > 1e-12 ? (nn * sxy - sx * sy) / (den > 1e-12 ? den : 1e-12) : 1.0;
+        const double tn = (sy - sn * sx) / nn;
+        ns = s;
+        nt = t;
+        if (ok) {
+            ns = (float)sn;
+            nt = (float)tn;
+        }
+    };
     auto solve = [&](const double (&g)[5], bool first) {
+        if (!first) {
+            float ns, nt;
+            ls(g, sh.ok != 0, ns, nt);
+            same = f2u(ns) == f2u(s) && f2u(nt) == f2u(t);
+            s = ns;
+            t = nt;
+            return;
+        }
         if (tid == 0) {
-            const double n = g[0], sx = g[1], sy = g[2], sxx = g[3], sxy = g[4];
-            if (first) {
-                const int64_t count = (int64_t)n;
-                sh.ok = count >= a.min_points;
-                int64_t k = (int64_t)(a.keep * (float)count);
-                if (k < a.min_points) k = a.min_points;
-                sh.kk = k < a.N ? k : a.N;
-                if (a.info && b == 0) {
-                    a.info[5 * a.b + 0] = (int32_t)count;
-                    a.info[5 * a.b + 1] = (int32_t)k;
-                    a.info[5 * a.b + 2] = sh.ok;
-                }
+            const int64_t count = (int64_t)g[0];
+            sh.ok = count >= a.min_points;
+            int64_t k = (int64_t)(a.keep * (float)count);
+            if (k < a.min_points) k = a.min_points;
+            sh.kk = k < a.N ? k : a.N;
+            if (a.info && b == 0) {
+                a.info[5 * a.b + 0] = (int32_t)count;
+                a.info[5 * a.b + 1] = (int32_t)k;
+                a.info[5 * a.b + 2] = sh.ok;
             }
-            const double nn = n > 1.0 ? n : 1.0;
-            const double den = nn * sxx - sx * sx;
-            const double sn = den > 1e-12 ? (nn * sxy - sx * sy) / (den > 1e-12 ? den : 1e-12) : 1.0;
-            const double tn = (sy - sn * sx) / nn;
-            float ns = s, nt = t;
-            if (sh.ok) {
-                ns = (float)sn;
-                nt = (float)tn;
-            }
-            sh.same = f2u(ns) == f2u(s) && f2u(nt) == f2u(t);
+            float ns, nt;
+            ls(g, sh.ok != 0, ns, nt);
             sh.s = ns;
             sh.t = nt;
         }
         __syncthreads();
+        same = false;
         s = sh.s;
         t = sh.t;
         __syncthreads();
@@ -575,7 +588,21 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
                 if ((unsigned)tid < total) {
                     const uint32_t key = sh.cand[tid] & 0x7fffffffu;
                     unsigned less = 0, eq = 0;
-                    for (unsigned g = 0; g < total; ++g) {
+                    // four keys per 16-byte LDS read and four reads in flight per trip: one 4-byte read per trip
+                    // waited out its latency every time (107 candidates took 5.6 us)
+                    const unsigned t4 = total & ~3u;
+#pragma unroll 4
+                    for (unsigned g = 0; g < t4; g += 4) {
+                        const uint4 q = *(const uint4*)&sh.cand[g];
+                        const uint32_t kq[4] = {q.x & 0x7fffffffu, q.y & 0x7fffffffu, q.z & 0x7fffffffu,
+                                                q.w & 0x7fffffffu};
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            less += kq[e] < key ? 1u : 0u;
+                            eq += kq[e] == key ? 1u : 0u;
+                        }
+                    }
+                    for (unsigned g = t4; g < total; ++g) {
                         const uint32_t kg = sh.cand[g] & 0x7fffffffu;
                         less += kg < key ? 1u : 0u;
                         eq += kg == key ? 1u : 0u;
@@ -765,7 +792,7 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
         // Fixed point: when a round reproduces the previous (s, t) bit for bit, the next round sees the same
         // residuals, hence the same k-th value, weights and sums, so every remaining round -- and the final
         // solve -- returns exactly these (s, t). Stopping here gives the bit-identical result.
-        if (sh.same) break;
+        if (same) break;
     }
 
     if (b == 0 && tid == 0) {
