@@ -331,17 +331,21 @@ constexpr int kG2Chunk = kG2Waves * kG2Tiles * 16;  // 512 rows per block step
 // weight operands ahead a wave reads from LDS; RS = 4 gathers codes three taps ahead instead of one and requests
 // a group's weights a whole group ahead (a few hundred rows per block, as on the coarse levels of a U-Net, leave
 // each tap waiting on both otherwise).
-template <int C, int EPI, int NB = C / 16, int T = kG2Tiles, int PF = 1, int RS = 2, bool DEV = (RS == 4)>
+template <int C, int EPI, int NB = C / 16, int T = kG2Tiles, int PF = 1, int RS = 2, bool DEV = (RS == 4),
+          typename E = int8_t>
 __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
-    constexpr int GRP = C == 64 ? 4 : 2;
-    constexpr int KS = C / 64;
+    constexpr int RB = C * (int)sizeof(E);               // row bytes: the kernel moves 64-byte K chunks of any type
+    constexpr int GRP = RB == 64 ? 4 : 2;
+    constexpr int KS = RB / 64;
     constexpr int NF = NB * KS;                          // 1 KB operand fragments per tap
     constexpr int WPT = GRP * NF / kG2Waves;             // fragments staged per wave per group
     constexpr int NG = (27 + GRP - 1) / GRP;             // tap groups; taps >= 27 of the last one are empty
     constexpr int NG2 = (NG + 1) / 2;                    // loop trips of two groups (one per LDS buffer)
     constexpr int CHUNK = kG2Waves * T * 16;             // rows per block step
     constexpr int NS = 16 * NB;                          // output channels of the block
-    static_assert(C == 64 || C == 128 || C == 256, "C must be 64, 128 or 256");
+    static_assert(RB == 64 || RB == 128 || RB == 256, "rows of 64, 128 or 256 bytes");
+    static_assert(sizeof(E) == 1 || !DEV, "device-sized launches are int8");
+    typedef typename Acc<E>::type acc_t;
     static_assert(GRP * NF % kG2Waves == 0, "staging split");
     static_assert(T == 1 || T == 2 || T == 4, "tiles per wave");
     static_assert(RS == 2 || RS == 4, "ring slots: the tap parity or v mod 4 of a trip");
@@ -360,10 +364,10 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
     const int Co = NS == C ? C : a.Co;
     const int n0 = NS == C ? 0 : (int)blockIdx.y * NS;    // first output channel of the block
     typedef const __attribute__((address_space(3))) v4i lds_v4i;
-    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, (int)(a.M * C), kBufWord3);
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, (int)(a.M * RB), kBufWord3);
     const __amdgpu_buffer_rsrc_t nr =
         __builtin_amdgcn_make_buffer_rsrc((void*)a.nmap_t, (short)0, (int)(a.M * 27 * 4), kBufWord3);
-    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc((void*)a.w, (short)0, Co * 27 * C, kBufWord3);
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc((void*)a.w, (short)0, Co * 27 * RB, kBufWord3);
 
     for (int e = tid; e < 2 * NS; e += kG2Threads) {
         const int q = e / NS, n = e - (e / NS) * NS;
@@ -386,7 +390,7 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
     // the gathers). Fragment f = wv + 8k of the group is tap slot q = f / NF, operand js = f % NF = (j, s), and
     // lane l holds W[16j + (l & 15)][v][64s + 16(l >> 4) .. +16] of the [Co][27][Ci] tensor; taps >= t1 load
     // zeros (out-of-range buffer offset).
-    const int wlane = ((n0 + r) * 27) * C + 16 * g;
+    const int wlane = ((n0 + r) * 27) * RB + 16 * g;
     // staged in PARTS pieces of WPP fragments per wave, one piece per tap of the group where that divides evenly
     // (C = 128: 8 registers held for one tap instead of 16 for the whole group)
     constexpr int PARTS = WPT % GRP == 0 ? GRP : 1, WPP = WPT / PARTS;
@@ -402,7 +406,7 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
             const int q = f / NF, js = f - (f / NF) * NF;
             const int j = js / KS, s2 = js - (js / KS) * KS;
             const int v = UW ? vt : t0 + GRP * grp + q;
-            const int off = v < t1 ? wlane + ((16 * j * 27) + v) * C + 64 * s2 : (int)0x80000000;
+            const int off = v < t1 ? wlane + ((16 * j * 27) + v) * RB + 64 * s2 : (int)0x80000000;
             st[kk] = __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 0);
         }
     };
@@ -459,11 +463,11 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
             rem = rem ? rem & (rem - 1) : 0u;
             return v;
         };
-        v4i acc[T][NB];
+        acc_t acc[T][NB];
 #pragma unroll
         for (int t = 0; t < T; ++t)
 #pragma unroll
-            for (int j = 0; j < NB; ++j) acc[t][j] = v4i{0, 0, 0, 0};
+            for (int j = 0; j < NB; ++j) acc[t][j] = acc_t{0, 0, 0, 0};
 
         // map indices of tap v (taps >= t1: out-of-range, zeros); gathers of the rows they name (absent: zeros).
         // Every load is issued unconditionally, so the compiler's vmcnt waits stay exact.
@@ -475,7 +479,7 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
         auto gather = [&](const int (&id)[T], v4i (&xs)[T][KS]) {
 #pragma unroll
             for (int t = 0; t < T; ++t) {
-                const int off = id[t] >= 0 ? id[t] * C + 16 * g : (int)0x80000000;
+                const int off = id[t] >= 0 ? id[t] * RB + 16 * g : (int)0x80000000;
 #pragma unroll
                 for (int s2 = 0; s2 < KS; ++s2) xs[t][s2] = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 64 * s2, 0);
             }
@@ -497,7 +501,7 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int t = 0; t < T; ++t)
-                    acc[t][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(cur, xs[t][s2], acc[t][j], 0, 0, 0);
+                    mma(acc[t][j], cur, xs[t][s2], E{});
                 __builtin_amdgcn_sched_barrier(0);
             }
         };
@@ -569,7 +573,8 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
             group(std::integral_constant<int, 1>{}, 2 * it + 1);
         }
 
-        if (kDev && Z > 1) {  // a tap range: the exact partial sums, [Z][M][Co]
+        if constexpr (kDev) {
+            if (Z > 1) {  // a tap range: the exact partial sums, [Z][M][Co]
 #pragma unroll
             for (int t = 0; t < T; ++t) {
                 if (pos0 + 16 * t >= M) continue;
@@ -579,39 +584,66 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
                     *(v4i*)(a.part + ((int64_t)z * M + m) * Co + n0 + 16 * j + 4 * g) = acc[t][j];
             }
             continue;  // split_epilogue_k adds the Z partials and applies the epilogue
+            }
         }
-        if constexpr (EPI == PMG_EPI_Q || EPI == PMG_EPI_QLIN) {
-            store_tile_codes<EPI, T, NB>(a, acc, s_k[0], s_k[1], orow, pos0, M, Co, n0, g);
-            continue;
-        }
+        if constexpr (sizeof(E) != 1) {  // fp16 / fp32 features: fp32 accumulators, bias from LDS
 #pragma unroll
-        for (int t = 0; t < T; ++t) {
-            if (pos0 + 16 * t >= M) continue;
-            const int m = orow[t];
+            for (int t = 0; t < T; ++t) {
+                if (pos0 + 16 * t >= M) continue;
+                const int m = orow[t];
 #pragma unroll
-            for (int j = 0; j < NB; ++j) {
-                const int64_t o = (int64_t)m * Co + n0 + 16 * j + 4 * g;
-                if constexpr (EPI == PMG_EPI_ACC) {
-                    *(v4i*)((int32_t*)a.out + o) = acc[t][j];
-                } else {
+                for (int j = 0; j < NB; ++j) {
+                    const int64_t o = (int64_t)m * Co + n0 + 16 * j + 4 * g;
                     float y[4];
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        const int n = 16 * j + 4 * g + i;
-                        float u = (float)acc[t][j][i] * a.a_scale;
-                        u = u * s_k[0][n];
-                        if (a.bias) u = u + s_k[1][n];
-                        y[i] = u;
+                        y[i] = acc[t][j][i];
+                        if constexpr (EPI != PMG_EPI_ACC) {
+                            if (a.bias) y[i] = y[i] + s_k[1][16 * j + 4 * g + i];
+                        }
                     }
-                    if constexpr (EPI == PMG_EPI_Q) {
-                        store_silu_codes4(y, a.out_mult, (int8_t*)a.out + o);
-                    } else if constexpr (EPI == PMG_EPI_QLIN) {
-                        store_codes4(y, a.out_mult, (int8_t*)a.out + o);
+                    if constexpr (EPI == PMG_EPI_SILU) {
+                        typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+                        h4 hv;
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) hv[i] = (_Float16)silu_fast(y[i]);
+                        *(h4*)((_Float16*)a.out + o) = hv;
                     } else if constexpr (EPI == PMG_EPI_R) {
                         const v4f sk = *(const v4f*)(a.skip + o);
                         *(v4f*)((float*)a.out + o) = v4f{y[0] + sk[0], y[1] + sk[1], y[2] + sk[2], y[3] + sk[3]};
                     } else {
                         *(v4f*)((float*)a.out + o) = v4f{y[0], y[1], y[2], y[3]};
+                    }
+                }
+            }
+        } else if constexpr (EPI == PMG_EPI_Q || EPI == PMG_EPI_QLIN) {
+            store_tile_codes<EPI, T, NB>(a, acc, s_k[0], s_k[1], orow, pos0, M, Co, n0, g);
+        } else {
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                if (pos0 + 16 * t >= M) continue;
+                const int m = orow[t];
+#pragma unroll
+                for (int j = 0; j < NB; ++j) {
+                    const int64_t o = (int64_t)m * Co + n0 + 16 * j + 4 * g;
+                    if constexpr (EPI == PMG_EPI_ACC) {
+                        *(v4i*)((int32_t*)a.out + o) = acc[t][j];
+                    } else {
+                        float y[4];
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const int n = 16 * j + 4 * g + i;
+                            float u = (float)acc[t][j][i] * a.a_scale;
+                            u = u * s_k[0][n];
+                            if (a.bias) u = u + s_k[1][n];
+                            y[i] = u;
+                        }
+                        if constexpr (EPI == PMG_EPI_R) {
+                            const v4f sk = *(const v4f*)(a.skip + o);
+                            *(v4f*)((float*)a.out + o) = v4f{y[0] + sk[0], y[1] + sk[1], y[2] + sk[2], y[3] + sk[3]};
+                        } else {
+                            *(v4f*)((float*)a.out + o) = v4f{y[0], y[1], y[2], y[3]};
+                        }
                     }
                 }
             }
@@ -858,6 +890,40 @@ static int launch_g2(const ConvArgs& a, int epilogue, hipStream_t s) {
     }
 }
 
+// fp16 / fp32 features, Ci = Co = C with rows of 64, 128 or 256 bytes: the weight-staged kernel on K chunks of 32
+// halves (v_mfma_f32_16x16x32_f16) or 16 floats (four v_mfma_f32_16x16x4f32), fp32 accumulators. Rows of 256
+// bytes hold 16 tiles of accumulators per wave at T = 4, so they run T = 2.
+template <typename E, int C>
+static int launch_g2f(const ConvArgs& a, int epilogue, hipStream_t s) {
+    static int cus = -1;
+    if (cus < 0) cus = num_cus();
+    constexpr int T = C * (int)sizeof(E) == 256 ? 2 : 4, CHUNK = kG2Waves * T * 16;
+    const int64_t nchunk = (a.M + CHUNK - 1) / CHUNK;
+    const dim3 grid((unsigned)(nchunk < cus ? nchunk : cus)), blk(kG2Threads);
+    switch (epilogue) {
+        case PMG_EPI_ACC: hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_ACC, C / 16, T, 1, 2, false, E>), grid, blk, 0, s, a); break;
+        case PMG_EPI_BIAS: hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_BIAS, C / 16, T, 1, 2, false, E>), grid, blk, 0, s, a); break;
+        case PMG_EPI_R: hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_R, C / 16, T, 1, 2, false, E>), grid, blk, 0, s, a); break;
+        case PMG_EPI_SILU:
+            if constexpr (sizeof(E) == 2) {
+                hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_SILU, C / 16, T, 1, 2, false, E>), grid, blk, 0, s, a);
+                break;
+            }
+            [[fallthrough]];
+        default: return fail(PMG_E_INVALID, "spconv: epilogue not available for this precision");
+    }
+    return check_launch("spconv_g2_k");
+}
+
+// Whether the fp staged kernel takes this convolution: Ci = Co >= 32 with rows of 64 - 256 bytes (fp16 32, 64,
+// 128; fp32 32, 64), 32-bit buffer offsets and aligned vectors.
+static bool g2f_fits(const ConvArgs& a, int Ci, int elt, int epilogue) {
+    const int rb = Ci * elt;
+    return Ci == a.Co && Ci >= 32 && Ci % 16 == 0 && (rb == 64 || rb == 128 || rb == 256) &&
+           a.M * 27 * 4 < ((int64_t)1 << 31) && a.M * rb < ((int64_t)1 << 31) && aligned16(a.out) &&
+           (epilogue != PMG_EPI_R || aligned16(a.skip));
+}
+
 // Device-sized launches of the staged kernels (Ci = Co = C): the grid covers the capacity's chunks, at most one
 // block per CU in x (blockIdx.y: the output-channel slice), and every block reads the row count and takes its XCD
 // band's share of the chunks that hold rows; the others return at once.
@@ -1045,6 +1111,11 @@ int pmg_spconv_f16(const uint16_t* x, const int32_t* nmap_t, const uint32_t* til
     if (M == 0) return PMG_OK;
     ConvArgs a{(const uint8_t*)x, nmap_t, tile_mask, (const uint8_t*)w, M, Co, Ci * 2, Ci * 2 / 16,
                1.0f, nullptr, bias, 1.0f, skip, out};
+    if (g2f_fits(a, Ci, 2, epilogue)) {
+        if (Ci == 32) return launch_g2f<_Float16, 32>(a, epilogue, (hipStream_t)stream);
+        if (Ci == 64) return launch_g2f<_Float16, 64>(a, epilogue, (hipStream_t)stream);
+        return launch_g2f<_Float16, 128>(a, epilogue, (hipStream_t)stream);
+    }
     return conv_common<_Float16>(a, Ci, epilogue, (hipStream_t)stream);
 }
 
@@ -1055,6 +1126,10 @@ int pmg_spconv_f32(const float* x, const int32_t* nmap_t, const uint32_t* tile_m
     if (M == 0) return PMG_OK;
     ConvArgs a{(const uint8_t*)x, nmap_t, tile_mask, (const uint8_t*)w, M, Co, Ci * 4, Ci * 4 / 16,
                1.0f, nullptr, bias, 1.0f, nullptr, out};
+    if (g2f_fits(a, Ci, 4, epilogue)) {
+        if (Ci == 32) return launch_g2f<float, 32>(a, epilogue, (hipStream_t)stream);
+        return launch_g2f<float, 64>(a, epilogue, (hipStream_t)stream);
+    }
     return conv_common<float>(a, Ci, epilogue, (hipStream_t)stream);
 }
 

@@ -323,7 +323,7 @@ def test_conv_int8_epilogues(gpu, C):
     assert np.array_equal(out_m.cpu().numpy(), expect)
 
 
-@pytest.mark.parametrize("C", [32, 64])
+@pytest.mark.parametrize("C", [32, 48, 64, 128])
 def test_conv_f16(gpu, C):
     announce(f"conv fp16 C={C}")
     rng = np.random.default_rng(100 + C)
@@ -341,19 +341,31 @@ def test_conv_f16(gpu, C):
     h = ops.spconv_f16(_t(x, gpu), nt, tm, _t(w, gpu), ops.EPI_SILU, bias=_t(b, gpu)).cpu().numpy()
     hr = onm.silu_f32((got + b).astype(np.float32)).astype(np.float16)  # from the kernel's own accumulator
     _assert_f16_ulp(h, hr)
+    # bias and residual epilogues: fp32 additions to the same accumulator
+    yb = ops.spconv_f16(_t(x, gpu), nt, tm, _t(w, gpu), ops.EPI_BIAS, bias=_t(b, gpu)).cpu().numpy()
+    assert np.array_equal(yb, got + b)
+    skip = rng.normal(size=(M, C)).astype(np.float32)
+    yr = ops.spconv_f16(_t(x, gpu), nt, tm, _t(w, gpu), ops.EPI_R, bias=_t(b, gpu), skip=_t(skip, gpu)).cpu().numpy()
+    assert np.array_equal(yr, (got + b) + skip)
 
 
-def test_conv_f32(gpu):
-    announce("conv fp32")
-    rng = np.random.default_rng(7)
+@pytest.mark.parametrize("Ci,Co", [(24, 32), (32, 32), (64, 64)])
+def test_conv_f32(gpu, Ci, Co):
+    announce(f"conv fp32 {Ci}->{Co}")
+    rng = np.random.default_rng(7 + Ci)
     nm, nt, tm = _map_from_scene(gpu)
     M = nm.shape[0]
-    x = rng.normal(size=(M, 24)).astype(np.float32)
-    w = rng.normal(0, 0.05, size=(32, 3, 3, 3, 24)).astype(np.float32)
-    b = rng.normal(size=32).astype(np.float32)
+    x = rng.normal(size=(M, Ci)).astype(np.float32)
+    w = rng.normal(0, 0.05, size=(Co, 3, 3, 3, Ci)).astype(np.float32)
+    b = rng.normal(size=Co).astype(np.float32)
     got = ops.spconv_f32(_t(x, gpu), nt, tm, _t(w, gpu), _t(b, gpu)).cpu().numpy()
     ref = ocv.conv_float(x.astype(np.float64), nm, w.astype(np.float64), b.astype(np.float64), dtype=np.float64)
-    assert np.abs(got - ref).max() < 1e-4
+    # fp32 accumulation: error bound ~ n_terms * eps32 * sum|terms| (+ the bias)
+    bound = 27 * Ci * 2 ** -23 * ocv.conv_float(np.abs(x.astype(np.float64)), nm, np.abs(w.astype(np.float64)),
+                                                 np.abs(b.astype(np.float64)), dtype=np.float64)
+    assert (np.abs(got - ref) <= bound + 1e-6).all()
+    acc = ops.spconv_f32(_t(x, gpu), nt, tm, _t(w, gpu)).cpu().numpy()
+    assert np.array_equal(got, acc + b)
 
 
 # ---------------------------------------------------------------------------------------------------------- row ops
