@@ -181,6 +181,11 @@ int pmg_spconv_f16(const uint16_t* x, const int32_t* nmap_t, const uint32_t* til
                    const uint16_t* w, int epilogue, const float* bias, const float* skip, void* out, void* stream);
 int pmg_spconv_f32(const float* x, const int32_t* nmap_t, const uint32_t* tile_mask, int64_t M, int Ci, int Co,
                    const float* w, int epilogue, const float* bias, float* out, void* stream);
+/* bf16 features and weights (the refiner under bf16 autocast, sparse_unet.py:155-158, through
+ * submanifold_conv, _core.py:399-441): bf16 MFMA with fp32 accumulation, fp32 output; epilogues ACC, BIAS and R.
+ * ABI version 4. */
+int pmg_spconv_bf16(const uint16_t* x, const int32_t* nmap_t, const uint32_t* tile_mask, int64_t M, int Ci, int Co,
+                    const uint16_t* w, int epilogue, const float* bias, const float* skip, float* out, void* stream);
 
 /* pmg_spconv_col -- the level-0 convolution computed straight from the voxel keys zq [B][H][W] (pmg_voxelize),
  * with the column-stencil neighbourhood of _build_submanifold_nmap_column (_core.py:269-295) derived on the fly

@@ -103,6 +103,7 @@ SIGNATURES = {
     "pmg_spconv_i8": (i32, [vp, vp, vp, i64, i32, i32, vp, i32, f32, vp, vp, f32, vp, vp, vp]),
     "pmg_spconv_i8_ordered": (i32, [vp, vp, vp, vp, i64, i32, i32, vp, i32, f32, vp, vp, f32, vp, vp, vp]),
     "pmg_spconv_f16": (i32, [vp, vp, vp, i64, i32, i32, vp, i32, vp, vp, vp, vp]),
+    "pmg_spconv_bf16": (i32, [vp, vp, vp, i64, i32, i32, vp, i32, vp, vp, vp, vp]),
     "pmg_spconv_f32": (i32, [vp, vp, vp, i64, i32, i32, vp, i32, vp, vp, vp]),
     "pmg_spconv_col": (i32, [i32, vp, vp, i32, i32, i32, i32, vp, i32, C.c_void_p, vp]),
     "pmg_ln_silu_quant": (i32, [vp, i64, i32, vp, vp, f32, f32, vp, vp]),

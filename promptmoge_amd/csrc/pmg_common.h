@@ -40,6 +40,7 @@ int num_cus();
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
 // ---------------------------------------------------------------------------------------------------------------
 // Wave-level reductions (64 lanes), deterministic butterfly order.

@@ -120,6 +120,10 @@ template <>
 struct Acc<float> {
     typedef v4f type;
 };
+template <>
+struct Acc<__bf16> {
+    typedef v4f type;
+};
 
 __device__ inline void mma(v4i& acc, const v4i& a, const v4i& b, int8_t) {
     acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc, 0, 0, 0);
@@ -127,6 +131,10 @@ __device__ inline void mma(v4i& acc, const v4i& a, const v4i& b, int8_t) {
 __device__ inline void mma(v4f& acc, const v4i& a, const v4i& b, _Float16) {
     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, a), __builtin_bit_cast(v8h, b), acc, 0,
                                                   0, 0);
+}
+__device__ inline void mma(v4f& acc, const v4i& a, const v4i& b, __bf16) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, a), __builtin_bit_cast(v8bf, b), acc, 0,
+                                                   0, 0);
 }
 __device__ inline void mma(v4f& acc, const v4i& a, const v4i& b, float) {
     const v4f af = __builtin_bit_cast(v4f, a), bf = __builtin_bit_cast(v4f, b);
@@ -890,9 +898,9 @@ static int launch_g2(const ConvArgs& a, int epilogue, hipStream_t s) {
     }
 }
 
-// fp16 / fp32 features, Ci = Co = C with rows of 64, 128 or 256 bytes: the weight-staged kernel on K chunks of 32
-// halves (v_mfma_f32_16x16x32_f16) or 16 floats (four v_mfma_f32_16x16x4f32), fp32 accumulators. Rows of 256
-// bytes hold 16 tiles of accumulators per wave at T = 4, so they run T = 2.
+// fp16 / bf16 / fp32 features, Ci = Co = C with rows of 64, 128 or 256 bytes: the weight-staged kernel on K chunks
+// of 32 halves (v_mfma_f32_16x16x32_f16 / _bf16) or 16 floats (four v_mfma_f32_16x16x4f32), fp32 accumulators.
+// Rows of 256 bytes hold 16 tiles of accumulators per wave at T = 4, so they run T = 2.
 template <typename E, int C>
 static int launch_g2f(const ConvArgs& a, int epilogue, hipStream_t s) {
     static int cus = -1;
@@ -905,7 +913,7 @@ static int launch_g2f(const ConvArgs& a, int epilogue, hipStream_t s) {
         case PMG_EPI_BIAS: hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_BIAS, C / 16, T, 1, 2, false, E>), grid, blk, 0, s, a); break;
         case PMG_EPI_R: hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_R, C / 16, T, 1, 2, false, E>), grid, blk, 0, s, a); break;
         case PMG_EPI_SILU:
-            if constexpr (sizeof(E) == 2) {
+            if constexpr (std::is_same<E, _Float16>::value) {
                 hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_SILU, C / 16, T, 1, 2, false, E>), grid, blk, 0, s, a);
                 break;
             }
@@ -915,8 +923,8 @@ static int launch_g2f(const ConvArgs& a, int epilogue, hipStream_t s) {
     return check_launch("spconv_g2_k");
 }
 
-// Whether the fp staged kernel takes this convolution: Ci = Co >= 32 with rows of 64 - 256 bytes (fp16 32, 64,
-// 128; fp32 32, 64), 32-bit buffer offsets and aligned vectors.
+// Whether the fp staged kernel takes this convolution: Ci = Co >= 32 with rows of 64 - 256 bytes (fp16 / bf16 32,
+// 64, 128; fp32 32, 64), 32-bit buffer offsets and aligned vectors.
 static bool g2f_fits(const ConvArgs& a, int Ci, int elt, int epilogue) {
     const int rb = Ci * elt;
     return Ci == a.Co && Ci >= 32 && Ci % 16 == 0 && (rb == 64 || rb == 128 || rb == 256) &&
@@ -1037,7 +1045,7 @@ static int conv_common(const ConvArgs& a, int Ci, int epilogue, hipStream_t s) {
             if constexpr (sizeof(T) == 1) return launch_nb<T, PMG_EPI_QLIN>(a, nb, s);
             break;
         case PMG_EPI_SILU:
-            if constexpr (sizeof(T) == 2) return launch_nb<T, PMG_EPI_SILU>(a, nb, s);
+            if constexpr (std::is_same<T, _Float16>::value) return launch_nb<T, PMG_EPI_SILU>(a, nb, s);
             break;
     }
     (void)Ci;
@@ -1117,6 +1125,23 @@ int pmg_spconv_f16(const uint16_t* x, const int32_t* nmap_t, const uint32_t* til
         return launch_g2f<_Float16, 128>(a, epilogue, (hipStream_t)stream);
     }
     return conv_common<_Float16>(a, Ci, epilogue, (hipStream_t)stream);
+}
+
+int pmg_spconv_bf16(const uint16_t* x, const int32_t* nmap_t, const uint32_t* tile_mask, int64_t M, int Ci, int Co,
+                    const uint16_t* w, int epilogue, const float* bias, const float* skip, float* out, void* stream) {
+    if (int e = validate(x, nmap_t, tile_mask, M, Ci, Co, w, out, 2, "pmg_spconv_bf16")) return e;
+    PMG_REQUIRE(epilogue == PMG_EPI_ACC || epilogue == PMG_EPI_BIAS || epilogue == PMG_EPI_R,
+                "bf16 supports the ACC, BIAS and R epilogues");
+    PMG_REQUIRE(epilogue != PMG_EPI_R || skip, "skip required");
+    if (M == 0) return PMG_OK;
+    ConvArgs a{(const uint8_t*)x, nmap_t, tile_mask, (const uint8_t*)w, M, Co, Ci * 2, Ci * 2 / 16,
+               1.0f, nullptr, bias, 1.0f, skip, out};
+    if (g2f_fits(a, Ci, 2, epilogue)) {
+        if (Ci == 32) return launch_g2f<__bf16, 32>(a, epilogue, (hipStream_t)stream);
+        if (Ci == 64) return launch_g2f<__bf16, 64>(a, epilogue, (hipStream_t)stream);
+        return launch_g2f<__bf16, 128>(a, epilogue, (hipStream_t)stream);
+    }
+    return conv_common<__bf16>(a, Ci, epilogue, (hipStream_t)stream);
 }
 
 int pmg_spconv_f32(const float* x, const int32_t* nmap_t, const uint32_t* tile_mask, int64_t M, int Ci, int Co,

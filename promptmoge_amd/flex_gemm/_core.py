@@ -214,8 +214,9 @@ def submanifold_conv(feats: Tensor, coords: Tensor, shape: torch.Size, weight: T
     """out[m] = bias + sum_v W[:, v, :] @ feats[nmap[m, v]] (the cross-correlation of F.conv3d restricted to the
     active set), weight (Co, 3, 3, 3, Ci) -> (out (M, Co) in feats' dtype, neighbor_cache) (_core.py:399-441).
 
-    fp32 features run the fp32 MFMA kernel (exact fp32 products, fp32 accumulation), fp16 the fp16 MFMA kernel with
-    fp32 accumulation, bf16 is computed in fp32 and rounded back. Forward only: the kernels have no backward."""
+    fp32 features run the fp32 MFMA kernel (exact fp32 products, fp32 accumulation), fp16 and bf16 the fp16 / bf16
+    MFMA kernels with fp32 accumulation (bf16 results rounded back from fp32). Forward only: the kernels have no
+    backward."""
     kernel_size = tuple(weight.shape[1:-1])
     D = len(kernel_size)
     sparse_shape = tuple(shape[: coords.shape[1]])
@@ -243,7 +244,13 @@ def submanifold_conv(feats: Tensor, coords: Tensor, shape: torch.Size, weight: T
         bk = None if b is None else _pad_to(b, 0, 16).contiguous()
         out = _ops.spconv_f16(x, neighbor_cache.nmap_t, neighbor_cache.tile_mask, wk,
                               _ops.EPI_BIAS if bk is not None else _ops.EPI_ACC, bias=bk)
-    elif feats.dtype in (torch.float32, torch.bfloat16):
+    elif feats.dtype == torch.bfloat16:
+        x = _pad_to(feats.detach().contiguous(), 1, 8)
+        wk = _pad_to(_pad_to(w.to(torch.bfloat16), 2, 8), 0, 16).contiguous()
+        bk = None if b is None else _pad_to(b, 0, 16).contiguous()
+        out = _ops.spconv_bf16(x, neighbor_cache.nmap_t, neighbor_cache.tile_mask, wk,
+                               _ops.EPI_BIAS if bk is not None else _ops.EPI_ACC, bias=bk)
+    elif feats.dtype == torch.float32:
         x = _pad_to(feats.detach().float().contiguous(), 1, 4)
         wk = _pad_to(_pad_to(w.float(), 2, 4), 0, 16).contiguous()
         bk = None if b is None else _pad_to(b, 0, 16).contiguous()

@@ -15,7 +15,7 @@ from ._lib import EPI_ACC, EPI_BIAS, EPI_Q, EPI_QLIN, EPI_R, EPI_RLN, EPI_ROUT, 
 
 __all__ = [
     "voxelize", "nmap_column", "nmap_hash", "row_order", "nmap_from_rows", "kmap_compact", "spconv_i8",
-    "spconv_i8_ordered", "spconv_f16",
+    "spconv_i8_ordered", "spconv_f16", "spconv_bf16",
     "spconv_f32", "spconv_col", "ln_silu_quant", "ln_silu_f16", "fit_scale_shift", "fit_prompt", "fit_final",
     "post_depth",
     "math_device", "gauge_poly",
@@ -277,6 +277,24 @@ def spconv_f16(x: torch.Tensor, nmap_t: torch.Tensor, tile_mask: torch.Tensor, w
     if out is None:
         out = _conv_out(M, Co, epilogue, "f16", x.device)
     call("pmg_spconv_f16", _p(x), _p(nmap_t), _p(tile_mask), M, Ci, Co, _p(w), epilogue, _p(bias), _p(skip), _p(out),
+         _stream())
+    return out
+
+
+def spconv_bf16(x: torch.Tensor, nmap_t: torch.Tensor, tile_mask: torch.Tensor, w: torch.Tensor,
+                epilogue: int = EPI_ACC, *, bias: Optional[torch.Tensor] = None, skip: Optional[torch.Tensor] = None,
+                out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """bf16 features (M, Ci) and weights (Co, 3, 3, 3, Ci): bf16 MFMA, fp32 accumulation, fp32 output (M, Co);
+    epilogues ACC, BIAS (+ bias) and R (+ bias + skip)."""
+    x = _dev(x, "x", torch.bfloat16)
+    w = _dev(w, "w", torch.bfloat16)
+    M, Ci = x.shape
+    Co = w.shape[0]
+    if w.numel() != Co * 27 * Ci:
+        raise ValueError("weight must be (Co, 3, 3, 3, Ci)")
+    if out is None:
+        out = torch.empty((M, Co), dtype=torch.float32, device=x.device)
+    call("pmg_spconv_bf16", _p(x), _p(nmap_t), _p(tile_mask), M, Ci, Co, _p(w), epilogue, _p(bias), _p(skip), _p(out),
          _stream())
     return out
 

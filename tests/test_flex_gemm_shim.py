@@ -117,7 +117,7 @@ def test_cache_generic_uses_hash(gpu):
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype,ci,co", [(torch.float32, 32, 48), (torch.float32, 6, 10), (torch.float16, 64, 64),
                                          (torch.bfloat16, 16, 32), (torch.float32, 64, 64), (torch.float16, 32, 32),
-                                         (torch.float16, 128, 128)])
+                                         (torch.float16, 128, 128), (torch.bfloat16, 64, 64)])
 def test_submanifold_conv_matches_oracle(gpu, dtype, ci, co):
     announce(f"flex_gemm conv {dtype} {ci}->{co}")
     coords, shape = _level0(seed=ci + co)

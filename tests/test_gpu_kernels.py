@@ -349,6 +349,29 @@ def test_conv_f16(gpu, C):
     assert np.array_equal(yr, (got + b) + skip)
 
 
+@pytest.mark.parametrize("C", [32, 48, 64, 128])
+def test_conv_bf16(gpu, C):
+    announce(f"conv bf16 C={C}")
+    g = torch.Generator().manual_seed(300 + C)
+    nm, nt, tm = _map_from_scene(gpu)
+    M = nm.shape[0]
+    x = torch.randn(M, C, generator=g).bfloat16()
+    w = (torch.randn(C, 3, 3, 3, C, generator=g) * 0.05).bfloat16()
+    b = (torch.randn(C, generator=g) * 0.05).float()
+    xs, ws = x.float().numpy().astype(np.float64), w.float().numpy().astype(np.float64)
+    ref = ocv.conv_float(xs, nm, ws, dtype=np.float64)
+    got = ops.spconv_bf16(x.to(gpu), nt, tm, w.to(gpu), ops.EPI_ACC).cpu().numpy()
+    # fp32 accumulation of exact bf16 products: error bound ~ n_terms * eps32 * sum|terms|
+    bound = 27 * C * 2 ** -23 * ocv.conv_float(np.abs(xs), nm, np.abs(ws), dtype=np.float64)
+    assert (np.abs(got - ref) <= bound + 1e-6).all()
+    bn = b.numpy()
+    yb = ops.spconv_bf16(x.to(gpu), nt, tm, w.to(gpu), ops.EPI_BIAS, bias=b.to(gpu)).cpu().numpy()
+    assert np.array_equal(yb, got + bn)
+    skip = torch.randn(M, C, generator=g)
+    yr = ops.spconv_bf16(x.to(gpu), nt, tm, w.to(gpu), ops.EPI_R, bias=b.to(gpu), skip=skip.to(gpu)).cpu().numpy()
+    assert np.array_equal(yr, (got + bn) + skip.numpy())
+
+
 @pytest.mark.parametrize("Ci,Co", [(24, 32), (32, 32), (64, 64)])
 def test_conv_f32(gpu, Ci, Co):
     announce(f"conv fp32 {Ci}->{Co}")
