@@ -16,7 +16,8 @@ captured HIP graph of that chain; the metric fit of the refined depth is timed s
     cpu_baseline  the oracle's restatement of the reference's CPU path (_fallback conv on fake-quantised operands,
               fit_scale_shift with an exact k-th selection) timed on this host: 1 warm-up + median of 5 Model-A steps
     conv_microbench  isolated int8 conv on 1,000,000 surface voxels in 1024^3, C = 64 and 128; beside
-              it the same map through the flex_gemm shim's fp16 convolution (fp16_C64 / fp16_C128)
+              it the same map through the flex_gemm shim's fp16 and bf16 convolutions (fp16_C64 ... bf16_C128;
+              the dense bf16 peak equals fp16's)
     measured_peaks   this device's practical HBM copy bandwidth and int8 MFMA rate (pmg_probe_copy / _mfma_i8);
               `roofline.frac` is against the published 8 TB/s, `roofline.frac_measured` against the copy probe
     other_configs    one K-step frame of the fp16 teacher (T) and of the hi-res config (H, with nearest_fill); the
@@ -297,16 +298,17 @@ def microbench(stream):
             tops = 2 * Cm * Cm * pu / (t * 1e-3) / 1e12
             micro[f"C{Cm}"] = {"ms": round(t, 4), "tops": round(tops, 2), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
                                "ms_caller_order": round(t_u, 4)}
-        # the same map through the flex_gemm shim's fp16 path (SubmanifoldConv3d on fp16 features: fp16 MFMA,
-        # fp32 accumulators, caller's row order)
-        for Cm in (64, 128):
-            xh = (torch.randn(M, Cm, generator=g) * 0.5).half().to(dev)
-            wh = (torch.randn(Cm, 3, 3, 3, Cm, generator=g) * 0.05).half().to(dev)
-            oh = torch.empty((M, Cm), dtype=torch.float32, device=dev)
-            t = graph_ms(lambda: ops.spconv_f16(xh, ntu, tmu, wh, ops.EPI_ACC, out=oh), 5, stream)
-            tf = 2 * Cm * Cm * pu / (t * 1e-3) / 1e12
-            micro[f"fp16_C{Cm}"] = {"ms": round(t, 4), "tflops": round(tf, 2),
-                                    "frac_fp16_peak": round(tf / FP16_PEAK_TFLOPS, 4)}
+        # the same map through the flex_gemm shim's fp16 and bf16 paths (SubmanifoldConv3d on fp16 / bf16
+        # features: fp16 / bf16 MFMA, fp32 accumulators, caller's row order)
+        for name, dt, conv in (("fp16", torch.float16, ops.spconv_f16), ("bf16", torch.bfloat16, ops.spconv_bf16)):
+            for Cm in (64, 128):
+                xh = (torch.randn(M, Cm, generator=g) * 0.5).to(dt).to(dev)
+                wh = (torch.randn(Cm, 3, 3, 3, Cm, generator=g) * 0.05).to(dt).to(dev)
+                oh = torch.empty((M, Cm), dtype=torch.float32, device=dev)
+                t = graph_ms(lambda: conv(xh, ntu, tmu, wh, ops.EPI_ACC, out=oh), 5, stream)
+                tf = 2 * Cm * Cm * pu / (t * 1e-3) / 1e12
+                micro[f"{name}_C{Cm}"] = {"ms": round(t, 4), "tflops": round(tf, 2),
+                                          "frac_fp16_peak": round(tf / FP16_PEAK_TFLOPS, 4)}
     return micro
 
 
