@@ -527,35 +527,50 @@ def _cpu_model() -> str:
     return "unknown"
 
 
+def _cpu_time(cfg, sc, w, reps=5):
+    """Median seconds of `reps` CPU steps (after one warm-up) of the torch restatement of the _fallback path."""
+    from oracle import torch_port
+
+    run = lambda: torch_port.step(sc.points[None], sc.lidar[None], sc.conf[None], w, iters=cfg.fit_iters)
+    run()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        run()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
 def cpu_baseline(env):
     """The reference's CPU path (the _fallback flex_gemm ops, QAT fake quantisation, kthvalue fit) restated op for op
-    in torch (oracle/torch_port.py), on all the host's cores: 1 warm-up, median of 5 steps of the workload."""
+    in torch (oracle/torch_port.py), on all the host's cores: 1 warm-up, median of 5 steps of the workload (the
+    top-level figures), and the same for config B (the reference's own CPU case)."""
     import torch
 
-    from oracle import torch_port
+    from promptmoge_amd import spec
 
     cfg, sc, w = env["cfg"], env["sc"], env["w"]
     nproc = os.cpu_count() or 1
     prev = torch.get_num_threads()
     torch.set_num_threads(nproc)
     try:
-        run = lambda: torch_port.step(sc.points[None], sc.lidar[None], sc.conf[None], w, iters=cfg.fit_iters)
-        run()
-        ts = []
-        for _ in range(5):
-            t0 = time.perf_counter()
-            run()
-            ts.append(time.perf_counter() - t0)
+        tc = _cpu_time(cfg, sc, w)
+        cfg_b = spec.CONFIGS["B"]
+        sc_b = spec.make_scene(cfg_b)
+        tb = _cpu_time(cfg_b, sc_b, spec.refiner_for(cfg_b, sc_b))
         threads = torch.get_num_threads()
     finally:
         torch.set_num_threads(prev)
-    tc = statistics.median(ts)
+    what = ("the reference's _fallback path restated op for op in torch on the CPU (per-tap index_select / mm / "
+            f"index_add_, QAT fake quantisation, kthvalue fit), torch.set_num_threads({nproc})")
     return {"value": round(cfg.M / tc, 1), "unit": "voxels/s", "cores": int(threads), "kind": "port",
             "nproc": nproc, "threads": int(threads), "cpu_model": _cpu_model(),
-            "sample": f"1 warm-up + median of 5 steps of config {cfg.name} ({cfg.M} voxels each): the reference's "
-                      f"_fallback path restated op for op in torch on the CPU (per-tap index_select / mm / "
-                      f"index_add_, QAT fake quantisation, kthvalue fit), torch.set_num_threads({nproc})",
-            "ms_per_step": round(tc * 1e3, 1)}
+            "sample": f"1 warm-up + median of 5 steps of config {cfg.name} ({cfg.M} voxels each): {what}",
+            "ms_per_step": round(tc * 1e3, 1),
+            "configs": {"B": {"workload": f"B: {cfg_b.H}x{cfg_b.W} int8 refiner step K=1, C={cfg_b.C}, "
+                                          f"{2 * cfg_b.n_blocks} conv layers, fit iters {cfg_b.fit_iters}",
+                              "value": round(cfg_b.M / tb, 1), "unit": "voxels/s", "ms_per_step": round(tb * 1e3, 1),
+                              "sample": f"1 warm-up + median of 5 steps ({cfg_b.M} voxels each)"}}}
 
 
 def main() -> int:

@@ -20,12 +20,23 @@ from .numerics import F32, exp_f32
 
 
 def _resid(s, t, z, tg, mask):
+    """r = |s*z + t - target| / target.clamp_min(1e-3), +inf off the mask (prompt_stem.py:233-234)."""
     e = np.float32(s) * z
     e = e + np.float32(t)
     e = e - tg
     with np.errstate(divide="ignore", invalid="ignore"):
         r = np.abs(e) / np.maximum(tg, F32(1e-3))
     return np.where(mask, r, F32(np.inf)).astype(np.float32)
+
+
+def _kth(r, kk):
+    """torch.kthvalue(r, kk).values: the kk-th smallest, 1-indexed (prompt_stem.py:238)."""
+    return np.partition(r, kk - 1)[kk - 1]
+
+
+def _keep(mask, r, thr):
+    """w = mask & (r <= thr) (prompt_stem.py:239): every residual tied with the threshold is kept."""
+    return mask & (r <= thr)
 
 
 def _fit_one(z, tg, mask, iters, trim, min_points, acc):
@@ -53,8 +64,8 @@ def _fit_one(z, tg, mask, iters, trim, min_points, acc):
         if it == iters:
             break
         r = _resid(s, t, z, tg, mask)
-        thr = np.partition(r, kk - 1)[kk - 1]                # torch.kthvalue (1-indexed k)
-        w = mask & (r <= thr)
+        thr = _kth(r, kk)
+        w = _keep(mask, r, thr)
     return s, t, dict(count=count, k=k, ok=ok, thr=thr)
 
 

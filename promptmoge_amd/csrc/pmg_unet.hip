@@ -54,6 +54,13 @@ __global__ __launch_bounds__(256) void level0_coords_k(const int32_t* __restrict
     coords[m] = make_int4(b, p / W, p % W, zq[m] - zmin[b]);
 }
 
+// The caller's level-0 coordinates copied into the context's own buffer, so that level 0's coordinates always live
+// at one address (also across replays of graphs captured with and without given coordinates).
+__global__ __launch_bounds__(256) void copy_coords_k(const int4* __restrict__ src, int64_t M, int4* __restrict__ dst) {
+    const int64_t m = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (m < M) dst[m] = src[m];
+}
+
 // Voxels of column c of a level: [off[c], off[c + 1]); level 0 (off NULL) holds voxel c in column c.
 __device__ inline void col_range(const int32_t* off, int64_t c, int32_t& lo, int32_t& hi) {
     if (off) {
@@ -754,19 +761,19 @@ static int enqueue_unet(pmg_unet* u, const float* feats, const int32_t* coords, 
     const int L = u->L;
     const int64_t cap = u->cap;
     // level 0: keys and coordinates (the caller's, or _voxelize's from the log depth)
-    const int32_t* zkeys = nullptr;
     if (coords) {
-        u->coords[0] = (int4*)coords;
-        zkeys = coords + 3;
+        hipLaunchKernelGGL(copy_coords_k, dim3((unsigned)((cap + 255) / 256)), dim3(256), 0, s, (const int4*)coords,
+                           cap, u->coords0);
+        if (int e = check_launch("copy_coords_k")) return e;
     } else {
         if (int e = pmg_voxelize(feats + 2, 3, c.B, c.H, c.W, c.depth_resolution, u->zq0, u->zmin, u->zmin + c.B, s))
             return e;
         hipLaunchKernelGGL(level0_coords_k, dim3((unsigned)((cap + 255) / 256)), dim3(256), 0, s, u->zq0, u->zmin,
                            c.H, c.W, cap, u->coords0);
         if (int e = check_launch("level0_coords_k")) return e;
-        u->coords[0] = u->coords0;
-        zkeys = (const int32_t*)u->coords0 + 3;
     }
+    u->coords[0] = u->coords0;
+    const int32_t* zkeys = (const int32_t*)u->coords0 + 3;
     // input_proj (+ prompt_proj), the level-0 keys, and the first block's codes (sparse_unet.py:189-192)
     const pmg_block_weights* first = !u->down[0].empty() ? &u->down[0][0] : nullptr;
     InputStage in{};

@@ -37,9 +37,13 @@ class DeviceWeights:
         self.pr_w, self.pr_b = t(w.pr_w), t(w.pr_b)
         self.out_w, self.out_b = t(w.out_w), t(w.out_b)
         self.blocks = []
-        for b in w.blocks:
+        for k, b in enumerate(w.blocks):
             d = {"gamma": t(b.gamma), "beta": t(b.beta), "b1": t(b.b1), "b2": t(b.b2)}
             if precision == "int8":
+                for name, c in (("conv1", b.clip1), ("conv2", b.clip2)):
+                    if not np.isfinite(c) or c <= 0:
+                        raise ValueError(f"block {k} {name}: the int8 refiner needs a positive activation clip, "
+                                         f"got {c} (a state dict without aq_*.clip entries needs `clips`)")
                 q1, s1 = quantize_weight(b.w1)
                 q2, s2 = quantize_weight(b.w2)
                 d.update(w1=t(q1, torch.int8), s1=t(s1), w2=t(q2, torch.int8), s2=t(s2),

@@ -276,7 +276,8 @@ def weights_from_state_dict(sd, stages=("down_stages.0", "bottleneck_stage"), cl
     (flex_sparse_blocks.py:50-75) under each stage prefix `<stage>.<k>.`: norm1, conv1, conv2 (weights
     (Co, 3, 3, 3, Ci), nn/__init__.py:30). QAT-wrapped weights are read from `.parametrizations.weight.original`
     (torch.nn.utils.parametrize, qat.py:111); activation clips from the quantisers' `aq_<module_path>.clip`
-    buffers (qat.py:76, 112-115), or from `clips` = {module path: clip}. Tensors may be torch tensors or arrays."""
+    buffers (qat.py:76, 112-115), or from `clips` = {module path: clip}; a clip found in neither is NaN, which the
+    int8 refiner refuses (naming the layer). Tensors may be torch tensors or arrays."""
     f32 = lambda t: np.asarray(t.detach().cpu().float().numpy() if hasattr(t, "detach") else t, dtype=np.float32)
 
     def get(name: str):
@@ -294,7 +295,7 @@ def weights_from_state_dict(sd, stages=("down_stages.0", "bottleneck_stage"), cl
         key = "aq_" + path.replace(".", "_") + ".clip"
         if key in sd:
             return float(f32(sd[key]))
-        return 1.0
+        return float("nan")  # unknown: the fp16 / fp32 refiner never reads it, the int8 one refuses it
 
     in_w, in_b = get("input_proj.weight"), get("input_proj.bias")
     C = in_w.shape[0]

@@ -71,6 +71,12 @@ class UNetRefiner(torch.nn.Module):
         super().__init__()
         if any(f != 2 for f in weights.factors):
             raise ValueError("downsample factors other than 2 are not supported (MoGe's refiners use 2)")
+        wide = [c for c in weights.channels if c not in (16, 32, 48, 64, 96, 128, 192, 256)]
+        if wide or weights.channels[0] not in (16, 32, 48, 64, 128):
+            # the deployed int8 refiners are the narrowed 32 64 128 256 256 (train.py:124); the stock 512-wide
+            # refiner is the fp16 teacher, which runs through the flex_gemm shim
+            raise ValueError(f"UNetRefiner (int8) takes level widths 16, 32, 48, 64, 96, 128, 192, 256 (level 0: 16, "
+                             f"32, 48, 64, 128); got {weights.channels}")
         self.host_weights = weights
         self.depth_resolution = float(depth_resolution)
         self.use_graph = use_graph

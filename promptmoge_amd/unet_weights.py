@@ -6,7 +6,8 @@ the SparseResBlock3d stages (flex_sparse_blocks.py:50-75), the PoolDown / Neares
 bottleneck stage, and the activation clip of every quantised layer's input (qat.py:60-98).
 
 Sources:
-  unet_from_state_dict   a Sparse3DUNet state dict, plain or QAT (`.parametrizations.weight.original`, `aq_*.clip`)
+  unet_from_state_dict   a Sparse3DUNet state dict, QAT (`.parametrizations.weight.original`, `aq_*.clip`) or plain
+                         with the activation clips given
   load_refiner_bin       the Metal engine's export, refiner.bin + refiner.json (promptmoge/export/refiner.py:28-110):
                          int8 weights with their per-output-channel scales are kept exactly as stored (QuantW)
   make_unet_weights      seeded synthetic weights (no checkpoint is available offline)
@@ -111,7 +112,9 @@ def unet_from_state_dict(sd, factors: Optional[Sequence[int]] = None,
     """A Sparse3DUNet's weights from its state dict, under the reference's parameter names (sparse_unet.py:81-150,
     flex_sparse_blocks.py:50-105). QAT checkpoints store masters under `.parametrizations.weight.original`
     (torch.nn.utils.parametrize, qat.py:111) and clips in `aq_<module path with '_'>.clip` (qat.py:112-115);
-    `clips` ({module path: clip}) overrides them. `factors` defaults to Sparse3DUNet's [2] * (levels - 1)."""
+    `clips` ({module path: clip}) overrides them. A quantised layer (qat.py:118-138) with neither raises
+    ValueError naming it, so a plain (non-QAT) state dict needs `clips`. `factors` defaults to Sparse3DUNet's
+    [2] * (levels - 1)."""
     f32 = lambda t: np.asarray(t.detach().cpu().float().numpy() if hasattr(t, "detach") else t, dtype=F32)
 
     def has(name):
@@ -131,7 +134,12 @@ def unet_from_state_dict(sd, factors: Optional[Sequence[int]] = None,
         if clips is not None and path in clips:
             return float(clips[path])
         key = "aq_" + path.replace(".", "_") + ".clip"
-        return float(f32(sd[key])) if key in sd else 1.0
+        if key not in sd:
+            # the int8 refiner needs every quantised layer's activation clip (export/refiner.py asserts that the
+            # observer ran); a default would silently saturate that layer's input
+            raise ValueError(f"{path}: quantised layer without an activation clip ({key} is not in the state dict "
+                             f"and `clips` does not name it)")
+        return float(f32(sd[key]))
 
     def blocks(prefix):
         out, j = [], 0

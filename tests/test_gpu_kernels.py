@@ -463,6 +463,24 @@ def test_fit_selection_paths(gpu, case):
     assert s2.item() == s[0] and t2.item() == tt[0]
 
 
+@pytest.mark.parametrize("case", ["relative_rule", "clamp", "ties"])
+def test_fit_trim_rule_closed_form(gpu, case):
+    """The hand-built trimming cases (tests/fit_cases.py): after one trim the device keeps exactly the subset the rule
+    of prompt_stem.py:233-239 keeps (relative residual, 1e-3 clamp, k-th smallest, r <= thr), so (s, t) equal that
+    subset's least-squares line (np.polyfit in float64). Two batch items: the case, and the case reversed."""
+    import fit_cases as fc
+
+    announce(f"fit trim rule {case}")
+    z, tg, kept = getattr(fc, f"{case}_case")()[:3]
+    zz = np.stack([z, z[::-1]])
+    tt = np.stack([tg, tg[::-1]])
+    m = np.ones_like(zz, bool)
+    s, t_ = ops.fit_scale_shift(_t(zz, gpu), _t(tt, gpu), _t(m, gpu), iters=1)
+    es, et = fc.lstsq_st(z, tg, kept)
+    for b in range(2):
+        assert abs(float(s[b]) - es) < 2e-6 and abs(float(t_[b]) - et) < 2e-6, (b, float(s[b]), es, float(t_[b]), et)
+
+
 def test_fit_edge_cases(gpu):
     announce("fit edge cases")
     z = np.full((3, 5000), 2.0, np.float32)

@@ -24,6 +24,8 @@ CASES = {
     "small3": ([16, 32, 32], [1, 2, 1], [2, 1], 1, 2, 32, 48, 32, 3),
     "wide4": ([32, 64, 128, 256], [1, 1, 1, 1], [1, 1, 1], 1, 1, 64, 96, 64, 5),
     "modelB5": ([32, 64, 128, 256, 256], [1, 1, 1, 1, 1], [1, 1, 1, 1], 1, 1, 240, 320, 1024, 7),
+    # the widths that take the generic spconv_k and rows_ln_k<48 / 96 / 192> at levels >= 1
+    "odd3": ([48, 96, 192], [1, 1, 1], [1, 1], 1, 1, 48, 64, 48, 13),
 }
 
 
@@ -117,6 +119,13 @@ def test_unet_keys_from_depth_and_graph_replay(gpu):
     torch.cuda.synchronize()
     assert np.array_equal(a.cpu().numpy(), b.cpu().numpy())
     assert np.array_equal(a.cpu().numpy(), c.cpu().numpy())
+    # level 0's coordinates live at one address whichever graph ran last: a replay of the given-coordinates graph
+    # after the from-depth one exposes the coordinates it was given
+    tc2 = tc.clone()
+    tc2[:, 3] += 1
+    mod(tf, tc2, shape, te, prompt_feats=tp, encoder_bias_map=tb)
+    torch.cuda.synchronize()
+    assert np.array_equal(mod.buffer("coords", 0).cpu().numpy()[:M], tc2.cpu().numpy())
     ref_d = ou.forward(pts.reshape(M, 3), levels, w, enc, None, None, mode="int8")
     assert np.array_equal(d.cpu().numpy()[:, 0], ref_d)
     assert np.abs(a.cpu().numpy() - d.cpu().numpy()).max() > 1e-4

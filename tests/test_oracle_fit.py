@@ -1,10 +1,14 @@
-"""Pins the oracle's fit_scale_shift restatement: exact-linear recovery, trimming of outliers above the kept
-quantile, the < min_points fallback, the degenerate constant-z case, the k formula, and agreement of the fp64-sum
-form with the reference's literal fp32 form."""
+"""Pins the oracle's fit_scale_shift restatement: exact-linear recovery, the trimming rule (relative residual with its
+1e-3 clamp, the k-th smallest, r <= thr at ties) on hand-built sets whose kept subset is known in closed form,
+trimming of outliers above the kept quantile, the < min_points fallback, the degenerate constant-z case, the k
+formula, and agreement of the fp64-sum form with the reference's literal fp32 form. A mutation test plants the
+plausible misreadings of the rule in the oracle and checks that the hand-built cases catch each of them."""
 import numpy as np
 import pytest
 
+import fit_cases as fc
 from oracle import fit
+from oracle.numerics import F32
 
 
 # The literal fp32 form loses ~1e-5 to the cancellation in n*sxx - sx^2 (the reason the kernel sums in fp64), so its
@@ -116,3 +120,103 @@ def test_post_depth_closed_forms():
     mask = rng.random((2, 5, 7)) < 0.5
     dm = post_depth(pts, ([1.0, 2.0], [0.0, -1.0]), mask)
     assert np.isinf(dm[~mask]).all() and np.array_equal(dm[mask], d[mask])
+
+
+# ----------------------------------------------------------------------------- the trimming rule, prompt_stem.py:233-239
+FORMS = [(fit.fit_f64, 2e-6), (fit.fit_f32, 2e-6)]
+
+
+def _solve(form, z, tg, iters=1):
+    s_, t_, info = form(z[None], tg[None], np.ones((1, z.size), bool), iters=iters, return_info=True)
+    return float(s_[0]), float(t_[0]), info[0]
+
+
+@pytest.mark.parametrize("form,tol", FORMS)
+def test_trim_keeps_the_kth_relative_residual(form, tol):
+    """relative_rule_case: the first trim keeps the 31 inliers and Q+; the result is their least-squares line, which
+    is 6e-3 away from the line 2z + 0.25 that an absolute residual, a residual over z, the (k+1)-th, or r < thr
+    would give."""
+    z, tg, kept, line = fc.relative_rule_case()
+    s_, t_, info = _solve(form, z, tg)
+    es, et = fc.lstsq_st(z, tg, kept)
+    assert info["k"] == 32 and len(kept) == 32
+    assert abs(s_ - es) < tol and abs(t_ - et) < tol
+    assert abs(es - line[0]) > 5e-3 and abs(et - line[1]) > 5e-4      # the misreadings' answer is far away
+
+
+@pytest.mark.parametrize("form,tol", FORMS)
+def test_trim_denominator_is_clamped_at_1e_3(form, tol):
+    """clamp_case: a target of 3 * 2^-12 < 1e-3 is divided by 1e-3, which ranks it before the pair point at z = 2;
+    without the clamp the other point is kept and the line moves by 5e-3 in s and 0.027 in t."""
+    z, tg, kept, wrong = fc.clamp_case()
+    s_, t_, _ = _solve(form, z, tg)
+    es, et = fc.lstsq_st(z, tg, kept)
+    ws, wt = fc.lstsq_st(z, tg, wrong)
+    assert abs(s_ - es) < tol and abs(t_ - et) < tol
+    assert abs(ws - es) > 1e-3 and abs(wt - et) > 1e-2
+
+
+@pytest.mark.parametrize("form,tol", FORMS)
+def test_trim_keeps_every_tie_at_the_threshold(form, tol):
+    """ties_case: the k-th residual is shared by two identical points; r <= thr keeps both (k + 1 points)."""
+    z, tg, kept = fc.ties_case()
+    s_, t_, info = _solve(form, z, tg)
+    es, et = fc.lstsq_st(z, tg, kept)
+    assert info["k"] == 36 and len(kept) == 37
+    assert abs(s_ - es) < tol and abs(t_ - et) < tol
+    assert abs(es - 2.0) > 1e-3
+
+
+def _pins_hold():
+    try:
+        for form, tol in FORMS:
+            test_trim_keeps_the_kth_relative_residual(form, tol)
+            test_trim_denominator_is_clamped_at_1e_3(form, tol)
+            test_trim_keeps_every_tie_at_the_threshold(form, tol)
+    except AssertionError:
+        return False
+    return True
+
+
+def _resid_absolute(s, t, z, tg, mask):
+    e = np.abs(np.float32(s) * z + np.float32(t) - tg)
+    return np.where(mask, e, F32(np.inf)).astype(np.float32)
+
+
+def _resid_over_z(s, t, z, tg, mask):
+    e = np.abs(np.float32(s) * z + np.float32(t) - tg) / np.maximum(z, F32(1e-3))
+    return np.where(mask, e, F32(np.inf)).astype(np.float32)
+
+
+def _resid_unclamped(s, t, z, tg, mask):
+    with np.errstate(divide="ignore", invalid="ignore"):
+        e = np.abs(np.float32(s) * z + np.float32(t) - tg) / tg
+    return np.where(mask, e, F32(np.inf)).astype(np.float32)
+
+
+def _resid_clamp_1e_4(s, t, z, tg, mask):
+    e = np.abs(np.float32(s) * z + np.float32(t) - tg) / np.maximum(tg, F32(1e-4))
+    return np.where(mask, e, F32(np.inf)).astype(np.float32)
+
+
+MUTATIONS = {
+    "absolute residual": ("_resid", _resid_absolute),
+    "residual over z": ("_resid", _resid_over_z),
+    "no 1e-3 clamp": ("_resid", _resid_unclamped),
+    "clamp at 1e-4": ("_resid", _resid_clamp_1e_4),
+    "k-th one late": ("_kth", lambda r, kk: np.partition(r, kk)[kk]),
+    "k-th one early": ("_kth", lambda r, kk: np.partition(r, kk - 2)[kk - 2]),
+    "r < thr": ("_keep", lambda mask, r, thr: mask & (r < thr)),
+}
+
+
+def test_pins_hold_on_the_oracle():
+    assert _pins_hold()
+
+
+@pytest.mark.parametrize("name", sorted(MUTATIONS))
+def test_each_misreading_of_the_trim_fails_a_pin(monkeypatch, name):
+    """Plants one misreading of prompt_stem.py:233-239 in the CPU oracle; the hand-built cases must reject it."""
+    attr, fn = MUTATIONS[name]
+    monkeypatch.setattr(fit, attr, fn)
+    assert not _pins_hold(), f"the pins do not detect: {name}"

@@ -84,6 +84,30 @@ def test_weights_from_reference_state_dict():
     assert np.array_equal(got.out_w, w.out_w) and np.array_equal(got.in_w, w.in_w)
 
 
+def test_int8_refiner_refuses_missing_clips():
+    """weights_from_state_dict leaves a clip it cannot find as NaN (the fp16 refiner never reads it); building the
+    int8 device weights from it raises, naming the layer."""
+    import torch
+    from promptmoge_amd import spec
+    from promptmoge_amd.refiner import DeviceWeights
+
+    w = spec.make_weights(16, 2, seed=1)
+    sd = {"input_proj.weight": w.in_w, "input_proj.bias": w.in_b, "out_proj.weight": w.out_w,
+          "out_proj.bias": w.out_b}
+    for k, b in enumerate(w.blocks):
+        p = f"down_stages.0.{k}"
+        sd.update({f"{p}.norm1.weight": b.gamma, f"{p}.norm1.bias": b.beta, f"{p}.conv1.weight": b.w1,
+                   f"{p}.conv1.bias": b.b1, f"{p}.conv2.weight": b.w2, f"{p}.conv2.bias": b.b2})
+    got = spec.weights_from_state_dict(sd, stages=("down_stages.0",))
+    assert np.isnan(got.blocks[0].clip1)
+    with pytest.raises(ValueError, match="block 0 conv1"):
+        DeviceWeights(got, "int8", device="cpu")
+    clips = {f"down_stages.0.{k}.conv{i}": 2.0 for k in range(2) for i in (1, 2)}
+    ok = spec.weights_from_state_dict(sd, stages=("down_stages.0",), clips=clips)
+    DeviceWeights(ok, "int8", device="cpu")
+    DeviceWeights(got, "fp16", device="cpu")
+
+
 # ---- output gate and elastic anchor (v3.py:565-573, 386-393) -------------------------------------------------
 def test_lidar_uncertainty_closed_form():
     """u = 1 - c * (1 - clamp((d - 3) / 2, 0, 1)) where the LiDAR has a value, else 1 (prompt_stem.py:28-29)."""

@@ -127,6 +127,19 @@ def _synthetic(channels=(16, 32, 32), seed=3, B=2, H=16, W=24, enc_c=32):
     return w, levels, pts.reshape(M, 3), enc, pf, bias
 
 
+def test_state_dict_without_clips_is_refused():
+    """A plain state dict carries no aq_*.clip entries; without `clips` the reader refuses it and names the first
+    quantised layer it meets, instead of assuming a clip (which would saturate that layer's int8 input)."""
+    _, _, sd, clips = _golden_unet()
+    with pytest.raises(ValueError, match="activation clip"):
+        uw.unet_from_state_dict(sd, factors=[2, 2])
+    partial = dict(clips)
+    missing = sorted(partial)[0]
+    del partial[missing]
+    with pytest.raises(ValueError, match=missing.replace(".", r"\.")):
+        uw.unet_from_state_dict(sd, factors=[2, 2], clips=partial)
+
+
 def test_int8_unet_matches_fakequant_statistically():
     """The deployed int8 arithmetic and the QAT fake-quant formulation evaluate one quantised model in different
     fp32 orders: a value within an ulp of a rounding tie may take the neighbouring code and propagate. Median error
@@ -196,3 +209,13 @@ def test_refiner_bin_round_trip(tmp_path):
     o1 = ou.forward(feats, levels, w1, enc, pf, bias, mode="int8")
     o2 = ou.forward(feats, levels, w2, enc, pf, bias, mode="int8")
     assert np.array_equal(o1, o2)
+
+
+def test_unet_refiner_refuses_widths_beyond_256():
+    """The int8 U-Net runs widths up to 256 (the deployed 32 64 128 256 256 refiners, train.py:124); the stock
+    512-wide refiner is refused when the module is built, before any device work."""
+    from promptmoge_amd.unet import UNetRefiner
+
+    w = uw.make_unet_weights([16, 32, 512], 32, seed=0)
+    with pytest.raises(ValueError, match="level widths"):
+        UNetRefiner(w)
