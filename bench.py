@@ -399,6 +399,56 @@ def unet_bench(stream, reps=20):
             "voxels_per_level": counts, "ms": round(ms, 4), "voxels_per_s": round(M / (ms * 1e-3), 1)}
 
 
+def unet_step_bench(stream, reps=20):
+    """One fused refine step with the multi-level int8 refiner (UNetStep, pmg_unet_step) at Model A's size: prompt
+    fit (10 rounds) -> residual/gate -> voxelise -> the 5-level U-Net of unet_bench -> logz + delta -> final metric
+    fit (10 rounds) -> post_depth, one captured graph on the stream (the inputs resident, in place)."""
+    import numpy as np
+    import torch
+
+    from promptmoge_amd import spec
+    from promptmoge_amd import unet_weights as uw
+    from promptmoge_amd.unet import UNetStep
+
+    cfg = spec.CONFIGS["A"]
+    sc = spec.make_scene(cfg)
+    H, W = cfg.H, cfg.W
+    w = uw.make_unet_weights([32, 64, 128, 256, 256], 1024, seed=1)
+    for layer in w.quantised_layers().values():  # clips of the right scale for these weights (timing only)
+        if hasattr(layer, "clip1"):
+            layer.clip1, layer.clip2 = 3.0, 2.0
+        else:
+            layer.clip = 3.0
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(0)
+    res = {"workload": "A-shape 5-level int8 refine step: prompt fit + residual/gate + voxelise + Sparse3DUNet "
+                       "[32, 64, 128, 256, 256] (1 block per stage, encoder 1024 x 30x40, bias map) + logz update "
+                       "+ final metric fit + post_depth, fit iters 10, one captured graph"}
+    with torch.cuda.stream(stream):
+        P0 = torch.from_numpy(sc.points[None].copy()).to(dev)
+        L = torch.from_numpy(sc.lidar[None].copy()).to(dev)
+        Cf = torch.from_numpy(sc.conf[None].copy()).to(dev)
+        enc = torch.from_numpy(rng.normal(0, 1, (1, 1024, H // 16, W // 16)).astype(np.float32)).to(dev)
+        bias = torch.from_numpy(rng.normal(0, 0.1, (1, 256, H // 16, W // 16)).astype(np.float32)).to(dev)
+        out = torch.empty_like(P0)
+        for key, final in (("ms", True), ("ms_without_final_fit", False)):
+            step = UNetStep(w, 1, H, W, fit_iters=cfg.fit_iters, final_fit=final, post_depth=final, device=dev)
+            for _ in range(3):
+                step(P0, L, Cf, enc, bias, out=out)
+            step.check()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(reps):
+                step(P0, L, Cf, enc, bias, out=out)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            step.check()
+            res[key] = round(e0.elapsed_time(e1) / reps, 4)
+            step.close()
+    res["voxels_per_s"] = round(H * W / (res["ms"] * 1e-3), 1)
+    return res
+
+
 def frame_bench(name, stream, reps=10):
     """One frame of a K-step configuration: K refine steps (each with its prompt fit, voxel keys and stencil
     rebuilt, v3.py:537-578) and the final metric fit after the last one. H also times the GPU nearest_fill of its
@@ -589,7 +639,7 @@ def main() -> int:
     ap.add_argument("--micro-only", action="store_true",
                     help="run only the 1M-voxel map and conv microbench (for counter collection) and print it")
     ap.add_argument("--write-traffic", nargs=3, metavar=("OUT", "FETCH_DIR", "WRITE_DIR"))
-    ap.add_argument("--other", choices=["T", "H", "unet_A"],
+    ap.add_argument("--other", choices=["T", "H", "unet_A", "unet_A_step"],
                     help="time only this other configuration (K-step frame, or the multi-level U-Net) and print it")
     args = ap.parse_args()
     if args.write_traffic:
@@ -612,7 +662,8 @@ def main() -> int:
         return 0
     if args.other:
         s = torch.cuda.Stream()
-        res = unet_bench(s) if args.other == "unet_A" else frame_bench(args.other, s)
+        res = {"unet_A": unet_bench, "unet_A_step": unet_step_bench}.get(args.other, lambda st: frame_bench(
+            args.other, st))(s)
         print(json.dumps({args.other: res}), flush=True)
         return 0
     from promptmoge_amd.refiner import RefinerStep
@@ -676,6 +727,7 @@ def main() -> int:
         others["pool_L0"] = pool_bench(stream)
         others["gauge_A"] = gauge_bench(stream)
         others["unet_A"] = unet_bench(stream)
+        others["unet_A_step"] = unet_step_bench(stream)
     cpu = None if args.no_cpu else cpu_baseline(env)
 
     line = {

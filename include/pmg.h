@@ -477,8 +477,46 @@ int pmg_unet_forward(pmg_unet* u, const float* feats, const int32_t* coords, con
  * PMG_UNET_UP [cap][C] fp32, the up stage's (the bottleneck's at the deepest level); PMG_UNET_ENC_TOKENS
  * [B*(H/ds)*(W/ds)][C_{L-1}] fp32, encoder_fuse + bias map per token. NULL for an id the level does not have. */
 enum { PMG_UNET_COUNTS = 0, PMG_UNET_COORDS = 1, PMG_UNET_PARENT = 2, PMG_UNET_NMAP = 3, PMG_UNET_TILE_MASK = 4,
-       PMG_UNET_DOWN = 5, PMG_UNET_UP = 6, PMG_UNET_ENC_TOKENS = 7, PMG_UNET_COL_OFFSETS = 8 };
+       PMG_UNET_DOWN = 5, PMG_UNET_UP = 6, PMG_UNET_ENC_TOKENS = 7, PMG_UNET_COL_OFFSETS = 8, PMG_UNET_STEP_ST = 9 };
+/* PMG_UNET_STEP_ST (any level): [3][B][2] fp32, the last pmg_unet_step's prompt, final and anchor fits (s, t) (the
+ * prompt and final rows are written there only when the caller passes no st_prompt / st_final). */
 const void* pmg_unet_buffer(pmg_unet* u, int id, int level);
+
+/* ------------------------------------------------------------------------------------------------------------ *
+ * One refine-loop step with the multi-level refiner: the body of the loop at moge/model/v3.py:547-576 around
+ * _refine_logz (v3.py:346-360) with Sparse3DUNet (sparse_unet.py:176-258), in the device engine's order
+ * (Refiner.swift:224-292) -- prompt fit (fit_scale_shift of _lidar_in_affine_frame, v3.py:362-378) -> per-voxel
+ * (residual, gate) prompt features (v3.py:548-555) -> _voxelize (v3.py:305-344) -> level structure -> the U-Net ->
+ * logz + out_proj (v3.py:359), optionally through the output gate (v3.py:565-569) -> optionally the elastic anchor
+ * (v3.py:570-573) -> optionally the final metric fit at LiDAR resolution (v3.py:768-778) and post_depth
+ * (MetricFit.metal:200-211). One stream, no host synchronisation, one captured HIP graph per (buffers, stream).
+ * ------------------------------------------------------------------------------------------------------------ */
+typedef struct {
+    int dh, dw;              /* LiDAR map size */
+    int fit_iters;           /* trim rounds of each fit (0 .. 64) */
+    float fit_trim;          /* 0.2 */
+    int fit_min_points;      /* 32 */
+    int use_prompt;          /* prompt fit + (residual, gate) through prompt_proj; 0: no prompt features */
+    int soft_gate;           /* soft_residual_gate (v3.py:379-382) */
+    int output_gate;         /* refiner_output_gate (v3.py:565-569) */
+    float output_gate_floor; /* 0.1 */
+    float anchor;            /* anchor_strength beta in [0, 1] (v3.py:570-573); 0 = off */
+    int final_fit;           /* the metric fit of the refined depth at LiDAR resolution */
+} pmg_unet_step_config;
+
+/* Sets the step options and allocates the step's own workspace (the fits'); captured steps are dropped. Call it
+ * before the first pmg_unet_step and again to change the options; pmg_unet_step itself allocates nothing. */
+int pmg_unet_step_prepare(pmg_unet* u, const pmg_unet_step_config* cfg);
+/* points: [B][H][W][3] (x/z, y/z, logz) fp32; points_out: the same map with the refined logz (may alias points:
+ * the loop's `current_coord = cat(xy, refined_logz)`, v3.py:574); lidar, conf: [B][dh][dw] fp32;
+ * encoder_feature [B][enc_channels][H/ds][W/ds], encoder_bias_map [B][C_{L-1}][H/ds][W/ds] or NULL (as for
+ * pmg_unet_forward); st_prompt, st_final: [B][2] or NULL; depth: [B][H][W] fp32 post_depth of the refined map with
+ * the final fit's (s, t) (+inf where not > 0), or NULL (needs final_fit). */
+int pmg_unet_step(pmg_unet* u, const float* points, float* points_out, const float* lidar, const float* conf,
+                  const float* encoder_feature, const float* encoder_bias_map, float* st_prompt, float* st_final,
+                  float* depth, void* stream);
+/* Synchronises `stream`; reports (PMG_E_DEVICE) and clears a device-wide wait of a step's metric fit that expired. */
+int pmg_unet_check(pmg_unet* u, void* stream);
 
 #ifdef __cplusplus
 }

@@ -169,3 +169,62 @@ def calibrate(w, levels, feats, encoder_feature, prompt_feats=None, encoder_bias
         else:
             layer.clip = pc(rec[path])
     return out
+
+
+# ------------------------------------------------------------------------------------------------- refine step
+def step(points, lidar, conf, w, encoder_feature, encoder_bias_map=None, *, iters=10, trim=0.2, min_points=32,
+         use_prompt=True, soft_gate=False, final_fit=False, post_depth=False, resolution=256.0,
+         output_gate_on=False, gate_floor=0.1, anchor=0.0, st_given=None, st_anchor_given=None,
+         trace: Optional[dict] = None):
+    """One refine-loop step with the multi-level refiner (v3.py:547-576): prompt fit of _lidar_in_affine_frame
+    (v3.py:362-378), the (residual, gate) prompt features (v3.py:548-555), _refine_logz (v3.py:346-360) with this
+    Sparse3DUNet, logz + out, the output gate (v3.py:565-569), the elastic anchor (v3.py:570-573), the final metric
+    fit at LiDAR resolution (v3.py:768-778) and post_depth (MetricFit.metal:200-211). The int8 arithmetic of
+    `forward`; the steps around it are oracle/refiner.py's.
+
+    st_given / st_anchor_given = (s [B], t [B]) replace the prompt / anchor fit's result (that fit is then not run),
+    so that a device whose fit was checked against fit_f64 within its tolerance is compared on identical inputs
+    after it. Returns (points [B, H, W, 3], prompt (s, t) or None, final (s, t) or None, depth [B, H, W] or None)."""
+    from .fit import final_inputs, fit_f64, prompt_inputs
+    from .fit import post_depth as post_depth_fn
+    from .refiner import anchor_pull, output_gate, prompt_feats
+
+    pts = np.array(points, dtype=np.float32, copy=True)
+    B, H, W, _ = pts.shape
+    st = None
+    pf = None
+    if use_prompt:
+        z, tg, m, d, c = prompt_inputs(pts, lidar, conf)
+        if st_given is None:
+            st = fit_f64(z, tg, m, iters, trim, min_points)
+        else:
+            st = (np.asarray(st_given[0], np.float32).reshape(B), np.asarray(st_given[1], np.float32).reshape(B))
+        r, g = prompt_feats(pts, d, c, st[0], st[1], soft_gate)
+        pf = np.stack([r.reshape(-1), g.reshape(-1)], 1)
+    delta, levels = forward_from_points(pts, w, encoder_feature, pf, encoder_bias_map, "int8", resolution, trace)
+    cur = pts[..., 2].copy()
+    pts[..., 2] = pts[..., 2] + delta.reshape(B, H, W)
+    if output_gate_on or anchor > 0:
+        _, _, _, d_, c_ = prompt_inputs(pts, lidar, conf)
+    if output_gate_on:
+        pts[..., 2] = output_gate(cur, pts[..., 2], d_, c_, gate_floor)
+    if trace is not None:
+        trace["before_anchor"] = pts.copy()
+    if anchor > 0:
+        if st_anchor_given is None:
+            z, tg, m, _, _ = prompt_inputs(pts, lidar, conf)
+            sa = fit_f64(z, tg, m, iters, trim, min_points)
+        else:
+            sa = (np.asarray(st_anchor_given[0], np.float32).reshape(B),
+                  np.asarray(st_anchor_given[1], np.float32).reshape(B))
+        pts[..., 2] = anchor_pull(pts[..., 2], d_, c_, sa[0], sa[1], anchor)
+    fin = depth = None
+    if final_fit:
+        z, tg, m = final_inputs(pts, lidar, conf)
+        fin = fit_f64(z, tg, m, iters, trim, min_points)
+        if post_depth:
+            depth = post_depth_fn(pts, fin)
+    if trace is not None:
+        trace["levels"] = levels
+        trace["prompt_feats"] = pf
+    return pts, st, fin, depth

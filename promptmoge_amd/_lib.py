@@ -57,6 +57,14 @@ class UNetConfig(C.Structure):
     ]
 
 
+class UNetStepConfig(C.Structure):
+    _fields_ = [
+        ("dh", i32), ("dw", i32), ("fit_iters", i32), ("fit_trim", f32), ("fit_min_points", i32),
+        ("use_prompt", i32), ("soft_gate", i32), ("output_gate", i32), ("output_gate_floor", f32), ("anchor", f32),
+        ("final_fit", i32),
+    ]
+
+
 class LinearWeights(C.Structure):
     _fields_ = [("w", vp), ("w_scale", vp), ("bias", vp), ("a_scale", f32), ("q_mult", f32)]
 
@@ -77,7 +85,7 @@ class UNetWeights(C.Structure):
 
 
 UNET_COUNTS, UNET_COORDS, UNET_PARENT, UNET_NMAP, UNET_TILE_MASK, UNET_DOWN, UNET_UP, UNET_ENC_TOKENS, \
-    UNET_COL_OFFSETS = range(9)
+    UNET_COL_OFFSETS, UNET_STEP_ST = range(10)
 
 # name -> (restype, argtypes)
 SIGNATURES = {
@@ -134,6 +142,9 @@ SIGNATURES = {
     "pmg_unet_set_weights": (i32, [vp, C.POINTER(UNetWeights)]),
     "pmg_unet_forward": (i32, [vp, vp, vp, vp, vp, vp, vp, vp]),
     "pmg_unet_buffer": (vp, [vp, i32, i32]),
+    "pmg_unet_step_prepare": (i32, [vp, C.POINTER(UNetStepConfig)]),
+    "pmg_unet_step": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]),
+    "pmg_unet_check": (i32, [vp, vp]),
 }
 
 _lib: C.CDLL | None = None

@@ -383,7 +383,7 @@ int pmg_refiner_step(pmg_refiner* r, const float* points, float* points_out, con
     PMG_REQUIRE(points && points_out, "null points");
     PMG_REQUIRE((!r->cfg.use_prompt && !r->cfg.final_fit) || (lidar && conf), "LiDAR inputs required");
     hipStream_t s = (hipStream_t)stream;
-    const void* const key[8] = {(const void*)1, points, points_out, lidar, conf, st_prompt, st_final, stream};
+    const void* const key[kGraphKey] = {(const void*)1, points, points_out, lidar, conf, st_prompt, st_final, stream};
     return r->graphs.run(key, s, r->cfg.use_graph, [&] { return enqueue_step(r, points, points_out, lidar, conf, st_prompt, st_final, s); });
 }
 
@@ -393,7 +393,7 @@ int pmg_refiner_forward(pmg_refiner* r, const float* feats, const int32_t* coord
     PMG_REQUIRE(feats && out, "null buffer");
     PMG_REQUIRE(!prompt_feats || (r->w.pr_w && r->w.pr_b), "prompt_feats given but the refiner has no prompt_proj");
     hipStream_t s = (hipStream_t)stream;
-    const void* const key[8] = {(const void*)2, feats, coords, prompt_feats, out, nullptr, nullptr, stream};
+    const void* const key[kGraphKey] = {(const void*)2, feats, coords, prompt_feats, out, nullptr, nullptr, stream};
     return r->graphs.run(key, s, r->cfg.use_graph, [&] { return enqueue_forward(r, feats, coords, prompt_feats, out, s); });
 }
 

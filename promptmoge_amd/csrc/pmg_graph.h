@@ -10,9 +10,12 @@
 
 namespace pmg {
 
+// A key is the sequence's kind tag, its buffers and the stream, padded with nullptr.
+constexpr int kGraphKey = 12;
+
 struct GraphCache {
     struct Entry {
-        const void* key[8];
+        const void* key[kGraphKey];
         hipGraph_t graph;
         hipGraphExec_t exec;
     };
@@ -34,7 +37,7 @@ struct GraphCache {
     // Runs `enqueue` on `s`: captured into a graph the first time `key` is seen, replayed after. The legacy default
     // stream cannot be captured; on it (or with use_graph off) the work is enqueued eagerly.
     template <typename F>
-    int run(const void* const (&key)[8], hipStream_t s, bool use_graph, F&& enqueue) {
+    int run(const void* const (&key)[kGraphKey], hipStream_t s, bool use_graph, F&& enqueue) {
         if (!use_graph || s == nullptr) return enqueue();
         for (auto& g : entries)
             if (std::memcmp(g.key, key, sizeof key) == 0) {

@@ -603,6 +603,15 @@ struct pmg_unet {
     int32_t* part = nullptr;            // tap-split partial sums of the coarsest level's convolutions
     int64_t part_bytes = 0;
 
+    // pmg_unet_step: its own workspace (the prompt / anchor fit, the final fit, the fits' (s, t)), allocated by
+    // pmg_unet_step_prepare
+    bool step_ready = false;
+    pmg_unet_step_config scfg{};
+    void* step_arena = nullptr;
+    void* fit_ws[2] = {nullptr, nullptr};  // prompt (and anchor) fit, final fit
+    size_t fit_ws_bytes[2] = {0, 0};
+    float* st_scratch = nullptr;           // [3][B][2]: prompt, final, anchor (s, t)
+
     bool have_weights = false;
     const float* in_w = nullptr;
     const float* in_b = nullptr;
@@ -619,11 +628,24 @@ struct pmg_unet {
 
 static size_t ualign(size_t v) { return (v + 255) & ~(size_t)255; }
 
+// Where the network's last convolution (a level-0 block) puts out_proj: the module's (M, 1) output `delta`
+// (sparse_unet.py:258), or -- the refine step -- logz + delta into the point map points_out (v3.py:359), scaled by the
+// output gate when gate_lidar is set (v3.py:565-569).
+struct UnetOut {
+    float* delta = nullptr;
+    const float* points = nullptr;
+    float* points_out = nullptr;
+    const float* gate_lidar = nullptr;
+    const float* gate_conf = nullptr;
+    int gate_dh = 0, gate_dw = 0;
+    float gate_floor = 0.0f, gate_scale = 0.0f;
+};
+
 // One residual block on level k (flex_sparse_blocks.py:70-75) whose conv1 input codes are in u->q1 and whose stream
 // is x (updated in place). After conv2: the next block's LayerNorm codes (level 0: fused RLN epilogue; else the row
-// kernel), nothing, or (last level-0 block of the network) out_proj into delta.
+// kernel), nothing, or (last level-0 block of the network) out_proj into `rout`.
 static int enqueue_block(pmg_unet* u, int k, const pmg_block_weights& bk, const pmg_block_weights* next, float* x,
-                         float* delta, hipStream_t s) {
+                         const UnetOut* rout, hipStream_t s) {
     const int C = u->cfg.channels[k];
     if (k == 0) {
         ColConvArgs a1{};
@@ -659,10 +681,21 @@ static int enqueue_block(pmg_unet* u, int k, const pmg_block_weights& bk, const 
             a2.next_q = u->q1;
             return launch_conv_col(PMG_PREC_INT8, a2, C, PMG_EPI_RLN, s);
         }
-        if (delta) {
+        if (rout) {
             a2.out_w = u->out_w;
             a2.out_b = u->out_b;
-            a2.out = delta;
+            if (rout->delta) {
+                a2.out = rout->delta;
+            } else {
+                a2.points = rout->points;
+                a2.points_out = rout->points_out;
+                a2.gate_lidar = rout->gate_lidar;
+                a2.gate_conf = rout->gate_conf;
+                a2.gate_dh = rout->gate_dh;
+                a2.gate_dw = rout->gate_dw;
+                a2.gate_floor = rout->gate_floor;
+                a2.gate_scale = rout->gate_scale;
+            }
             return launch_conv_col(PMG_PREC_INT8, a2, C, PMG_EPI_ROUT, s);
         }
         return launch_conv_col(PMG_PREC_INT8, a2, C, PMG_EPI_R, s);
@@ -706,11 +739,11 @@ static int enqueue_block(pmg_unet* u, int k, const pmg_block_weights& bk, const 
 }
 
 // A stage of blocks on level k over stream x, whose first block's input codes are already in q1.
-static int enqueue_stage(pmg_unet* u, int k, const std::vector<pmg_block_weights>& st, float* x, float* delta,
+static int enqueue_stage(pmg_unet* u, int k, const std::vector<pmg_block_weights>& st, float* x, const UnetOut* rout,
                          hipStream_t s) {
     for (size_t j = 0; j < st.size(); ++j) {
         const pmg_block_weights* next = j + 1 < st.size() ? &st[j + 1] : nullptr;
-        if (int e = enqueue_block(u, k, st[j], next, x, next ? nullptr : delta, s)) return e;
+        if (int e = enqueue_block(u, k, st[j], next, x, next ? nullptr : rout, s)) return e;
     }
     return PMG_OK;
 }
@@ -754,9 +787,21 @@ static int enqueue_structure(pmg_unet* u, hipStream_t s) {
     return PMG_OK;
 }
 
-// Sparse3DUNet.forward (sparse_unet.py:176-258) on level-0 voxels; out [cap] = the (M, 1) output.
+// The prompt features of the refine step, computed per voxel in the input stage from the LiDAR in the affine frame of
+// the prompt fit's (s, t) (v3.py:548-555, 362-383).
+struct UnetPrompt {
+    const float* lidar = nullptr;
+    const float* conf = nullptr;
+    int dh = 0, dw = 0;
+    const float* st = nullptr;
+    int soft_gate = 0;
+};
+
+// Sparse3DUNet.forward (sparse_unet.py:176-258) on level-0 voxels; out_proj goes to `rout`. The prompt features are
+// the given `prompt` [M][2], or computed from `lp` (the refine step), or absent.
 static int enqueue_unet(pmg_unet* u, const float* feats, const int32_t* coords, const float* prompt,
-                        const float* enc_feat, const float* enc_bias, float* out, hipStream_t s) {
+                        const UnetPrompt* lp, const float* enc_feat, const float* enc_bias, const UnetOut& rout,
+                        hipStream_t s) {
     const pmg_unet_config& c = u->cfg;
     const int L = u->L;
     const int64_t cap = u->cap;
@@ -798,6 +843,15 @@ static int enqueue_unet(pmg_unet* u, const float* feats, const int32_t* coords, 
     in.zq_out = u->zq0;
     in.prompt_in = prompt;
     in.use_prompt = prompt != nullptr;
+    if (lp && lp->st) {
+        in.lidar = lp->lidar;
+        in.conf = lp->conf;
+        in.dh = lp->dh;
+        in.dw = lp->dw;
+        in.st = lp->st;
+        in.soft_gate = lp->soft_gate;
+        in.use_prompt = 1;
+    }
     in.zkeys = zkeys;
     in.zkey_stride = 4;
     if (int e = launch_input_stage(in, false, s)) return e;
@@ -861,8 +915,95 @@ static int enqueue_unet(pmg_unet* u, const float* feats, const int32_t* coords, 
                                    fb ? fb->ln_gamma : nullptr, fb ? fb->ln_beta : nullptr, fb ? fb->q1_mult : 1.0f,
                                    u->xu[t], u->q1, s))
             return e;
-        if (int e = enqueue_stage(u, t, u->dec[i], u->xu[t], t == 0 ? out : nullptr, s)) return e;
+        if (int e = enqueue_stage(u, t, u->dec[i], u->xu[t], t == 0 ? &rout : nullptr, s)) return e;
         cur = u->xu[t];
+    }
+    return PMG_OK;
+}
+
+// One refine-loop step with the multi-level refiner (v3.py:547-576, the device engine's order Refiner.swift:224-292):
+// prompt fit -> (residual, gate) prompt features -> _voxelize -> structure -> Sparse3DUNet -> logz + delta (output
+// gate) -> elastic anchor -> final metric fit -> post_depth. points_out may alias points.
+static int enqueue_unet_step(pmg_unet* u, const float* points, float* points_out, const float* lidar,
+                             const float* conf, const float* enc_feat, const float* enc_bias, float* st_prompt,
+                             float* st_final, float* depth, hipStream_t s) {
+    const pmg_unet_config& c = u->cfg;
+    const pmg_unet_step_config& q = u->scfg;
+    const int B = c.B;
+    float* const st_p = st_prompt ? st_prompt : u->st_scratch;
+    float* const st_f = st_final ? st_final : u->st_scratch + 2 * B;
+    float* const st_a = u->st_scratch + 4 * B;
+    auto prompt_fit = [&](const float* pts, float* st) {
+        FitLaunch f{};
+        f.mode = 1;
+        f.logz = pts + 2;
+        f.stride = 3;
+        f.lidar = lidar;
+        f.conf = conf;
+        f.B = B;
+        f.H = c.H;
+        f.W = c.W;
+        f.dh = q.dh;
+        f.dw = q.dw;
+        f.N = (int64_t)c.H * c.W;
+        f.iters = q.fit_iters;
+        f.trim = q.fit_trim;
+        f.min_points = q.fit_min_points;
+        f.st = st;
+        f.info = nullptr;
+        f.workspace = u->fit_ws[0];
+        f.workspace_bytes = u->fit_ws_bytes[0];
+        return launch_fit(f, s);
+    };
+    UnetPrompt lp{};
+    if (q.use_prompt) {
+        if (int e = prompt_fit(points, st_p)) return e;
+        lp.lidar = lidar;
+        lp.conf = conf;
+        lp.dh = q.dh;
+        lp.dw = q.dw;
+        lp.st = st_p;
+        lp.soft_gate = q.soft_gate;
+    }
+    UnetOut rout{};
+    rout.points = points;
+    rout.points_out = points_out;
+    if (q.output_gate) {
+        rout.gate_lidar = lidar;
+        rout.gate_conf = conf;
+        rout.gate_dh = q.dh;
+        rout.gate_dw = q.dw;
+        rout.gate_floor = q.output_gate_floor;  // floor + (1.0 - floor) * u with both constants rounded to fp32
+        rout.gate_scale = (float)(1.0 - (double)q.output_gate_floor);
+    }
+    if (int e = enqueue_unet(u, points, nullptr, nullptr, q.use_prompt ? &lp : nullptr, enc_feat, enc_bias, rout, s))
+        return e;
+    if (q.anchor > 0.0f) {  // v3.py:570-573: re-fit on the refined depth, then the pull toward the LiDAR
+        if (int e = prompt_fit(points_out, st_a)) return e;
+        if (int e = launch_anchor(points_out, B, c.H, c.W, lidar, conf, q.dh, q.dw, st_a, q.anchor, s)) return e;
+    }
+    if (q.final_fit) {  // v3.py:768-778
+        FinalFit f{};
+        f.logz = points_out + 2;
+        f.stride = 3;
+        f.lidar = lidar;
+        f.conf = conf;
+        f.mask_binary = nullptr;
+        f.B = B;
+        f.H = c.H;
+        f.W = c.W;
+        f.dh = q.dh;
+        f.dw = q.dw;
+        f.iters = q.fit_iters;
+        f.trim = q.fit_trim;
+        f.min_points = q.fit_min_points;
+        f.st = st_f;
+        f.info = nullptr;
+        f.workspace = u->fit_ws[1];
+        f.workspace_bytes = u->fit_ws_bytes[1];
+        if (int e = launch_final_fit(f, s)) return e;
+        if (depth)  // MetricFit.metal:200-211 (v3.py:776)
+            if (int e = pmg_post_depth(points_out + 2, 3, nullptr, B, c.H, c.W, st_f, depth, s)) return e;
     }
     return PMG_OK;
 }
@@ -985,6 +1126,7 @@ pmg_unet* pmg_unet_create(const pmg_unet_config* cfg) {
 void pmg_unet_destroy(pmg_unet* u) {
     if (!u) return;
     u->graphs.clear();
+    if (u->step_arena) (void)hipFree(u->step_arena);
     if (u->arena) (void)hipFree(u->arena);
     delete u;
 }
@@ -1045,11 +1187,89 @@ int pmg_unet_forward(pmg_unet* u, const float* feats, const int32_t* coords, con
     PMG_REQUIRE(!prompt_feats || u->pr_w, "prompt_feats given but the refiner has no prompt_proj");
     PMG_REQUIRE(!coords || aligned16(coords), "coords must be 16-byte aligned");
     hipStream_t s = (hipStream_t)stream;
-    const void* const key[8] = {feats, coords, prompt_feats, encoder_feature, encoder_bias_map, out, stream,
-                                (const void*)3};
+    const void* const key[kGraphKey] = {(const void*)3, feats, coords, prompt_feats, encoder_feature, encoder_bias_map,
+                                        out, stream};
+    UnetOut rout{};
+    rout.delta = out;
     return u->graphs.run(key, s, u->cfg.use_graph != 0, [&] {
-        return enqueue_unet(u, feats, coords, prompt_feats, encoder_feature, encoder_bias_map, out, s);
+        return enqueue_unet(u, feats, coords, prompt_feats, nullptr, encoder_feature, encoder_bias_map, rout, s);
     });
+}
+
+int pmg_unet_step_prepare(pmg_unet* u, const pmg_unet_step_config* sc) {
+    PMG_REQUIRE(u && sc, "null argument");
+    const pmg_unet_step_config& q = *sc;
+    const pmg_unet_config& c = u->cfg;
+    PMG_REQUIRE(q.dh >= 1 && q.dw >= 1, "bad LiDAR size");
+    PMG_REQUIRE(q.fit_iters >= 0 && q.fit_iters <= 64 && q.fit_min_points >= 1 && q.fit_trim >= 0.0f &&
+                    q.fit_trim < 1.0f,
+                "bad fit parameters");
+    PMG_REQUIRE(q.output_gate_floor >= 0.0f && q.output_gate_floor <= 1.0f, "output_gate_floor must be in [0, 1]");
+    PMG_REQUIRE(q.anchor >= 0.0f && q.anchor <= 1.0f, "anchor must be in [0, 1]");
+    PMG_REQUIRE(!(q.use_prompt || q.anchor > 0.0f) || (int64_t)c.H * c.W <= kFitMaxElements,
+                "H*W exceeds the metric fit's 2^21 elements (use_prompt / anchor)");
+    PMG_REQUIRE(!q.final_fit || (int64_t)q.dh * q.dw <= kFitMaxElements,
+                "dh*dw exceeds the metric fit's 2^21 elements (final_fit)");
+    u->graphs.clear();  // (synchronises) captured steps use the old workspace
+    if (u->step_arena) {
+        (void)hipFree(u->step_arena);
+        u->step_arena = nullptr;
+    }
+    u->step_ready = false;
+    u->fit_ws_bytes[0] = ualign(fit_workspace_bytes((int64_t)c.H * c.W, q.fit_iters));
+    u->fit_ws_bytes[1] = q.final_fit ? ualign(final_fit_workspace_bytes(c.B, q.dh, q.dw, q.fit_iters)) : 256;
+    const size_t st_bytes = ualign(6 * sizeof(float) * (size_t)c.B);
+    const size_t bytes = u->fit_ws_bytes[0] + u->fit_ws_bytes[1] + st_bytes;
+    if (hipMalloc(&u->step_arena, bytes) != hipSuccess) {
+        u->step_arena = nullptr;
+        return fail(PMG_E_HIP, "pmg_unet_step_prepare: hipMalloc of " + std::to_string(bytes) + " bytes failed");
+    }
+    PMG_CHECK_HIP(hipMemset(u->step_arena, 0, bytes));  // the fits' workspaces start zero-filled
+    PMG_CHECK_HIP(hipDeviceSynchronize());
+    uint8_t* a = (uint8_t*)u->step_arena;
+    u->fit_ws[0] = a;
+    u->fit_ws[1] = a + u->fit_ws_bytes[0];
+    u->st_scratch = (float*)(a + u->fit_ws_bytes[0] + u->fit_ws_bytes[1]);
+    u->scfg = q;
+    u->step_ready = true;
+    return PMG_OK;
+}
+
+int pmg_unet_step(pmg_unet* u, const float* points, float* points_out, const float* lidar, const float* conf,
+                  const float* encoder_feature, const float* encoder_bias_map, float* st_prompt, float* st_final,
+                  float* depth, void* stream) {
+    PMG_REQUIRE(u && u->have_weights, "weights not set");
+    PMG_REQUIRE(u->step_ready, "pmg_unet_step_prepare has not run");
+    PMG_REQUIRE(points && points_out && lidar && conf && encoder_feature, "null buffer");
+    PMG_REQUIRE(!u->scfg.use_prompt || u->pr_w, "use_prompt needs prompt_proj weights");
+    PMG_REQUIRE(!depth || u->scfg.final_fit, "post_depth (depth) needs final_fit");
+    hipStream_t s = (hipStream_t)stream;
+    const void* const key[kGraphKey] = {(const void*)4, points, points_out, lidar, conf, encoder_feature,
+                                        encoder_bias_map, st_prompt, st_final, depth, stream};
+    return u->graphs.run(key, s, u->cfg.use_graph != 0, [&] {
+        return enqueue_unet_step(u, points, points_out, lidar, conf, encoder_feature, encoder_bias_map, st_prompt,
+                                 st_final, depth, s);
+    });
+}
+
+int pmg_unet_check(pmg_unet* u, void* stream) {
+    PMG_REQUIRE(u, "null context");
+    PMG_CHECK_HIP(hipStreamSynchronize((hipStream_t)stream));
+    if (!u->step_ready) return PMG_OK;
+    unsigned seen[2] = {0, 0};
+    const bool has[2] = {u->fit_ws_bytes[0] > kFitErrSeenOffset, u->fit_ws_bytes[1] > kFitErrSeenOffset};
+    for (int k = 0; k < 2; ++k)
+        if (has[k])
+            PMG_CHECK_HIP(hipMemcpy(&seen[k], (uint8_t*)u->fit_ws[k] + kFitErrSeenOffset, sizeof(unsigned),
+                                    hipMemcpyDeviceToHost));
+    if (seen[0] || seen[1]) {
+        for (int k = 0; k < 2; ++k)
+            if (has[k]) PMG_CHECK_HIP(hipMemset((uint8_t*)u->fit_ws[k] + kFitErrSeenOffset, 0, sizeof(unsigned)));
+        PMG_CHECK_HIP(hipDeviceSynchronize());
+        return fail(PMG_E_DEVICE, "pmg_unet_check: a device-wide wait in the metric fit expired (" +
+                                      std::to_string(seen[0] + seen[1]) + " launches)");
+    }
+    return PMG_OK;
 }
 
 const void* pmg_unet_buffer(pmg_unet* u, int id, int level) {
@@ -1064,6 +1284,7 @@ const void* pmg_unet_buffer(pmg_unet* u, int id, int level) {
         case PMG_UNET_UP: return level + 1 < u->L ? u->xu[level] : u->xb;
         case PMG_UNET_ENC_TOKENS: return u->enc_tok;
         case PMG_UNET_COL_OFFSETS: return level > 0 ? u->off[level] : nullptr;
+        case PMG_UNET_STEP_ST: return u->step_ready ? u->st_scratch : nullptr;
         default: return nullptr;
     }
 }

@@ -7,6 +7,10 @@
 encoder conditioning -- in libpmg (`pmg_unet_*`, csrc/pmg_unet.hip) as one captured HIP graph with no host
 synchronisation. The voxels must be level 0 as _voxelize builds them (v3.py:305-344): one per pixel in raster order.
 
+`UNetStep` is one whole refine-loop step with that refiner (v3.py:547-576): prompt fit, (residual, gate) prompt
+features, _voxelize, the U-Net, logz + delta (output gate), elastic anchor, final metric fit and post_depth, one
+captured graph on the device (`pmg_unet_step`), with no host round trip between them.
+
 Weights come from a Sparse3DUNet state dict (plain or QAT), from the Metal engine's refiner.bin / refiner.json
 export, or from promptmoge_amd.unet_weights.make_unet_weights; the arithmetic is the deployed int8 contract
 (qat.py:1-16): per-output-channel int8 weights, per-tensor int8 activations with the layer's clip, int32
@@ -21,7 +25,7 @@ import numpy as np
 import torch
 
 from . import _lib
-from ._lib import BlockWeights, LinearWeights, UNetConfig, UNetWeights, call, lib
+from ._lib import BlockWeights, LinearWeights, UNetConfig, UNetStepConfig, UNetWeights, call, lib
 from .spec import act_mult, act_scale
 from .unet_weights import UNetW, load_refiner_bin, quantized, unet_from_state_dict
 
@@ -215,6 +219,111 @@ class UNetRefiner(torch.nn.Module):
             self.close()
         except Exception:  # interpreter shutdown: the library handle may already be gone
             pass
+
+
+class UNetStep:
+    """One refine-loop step with the multi-level int8 refiner, fused on the GPU (pmg_unet_step).
+
+    points [B, H, W, 3] fp32 (x/z, y/z, logz) is refined into `out` (default in place); lidar, conf [B, dh, dw];
+    encoder_feature [B, C_enc, H/ds, W/ds] and encoder_bias_map [B, C_{L-1}, H/ds, W/ds] (or None) as for
+    Sparse3DUNet.forward. Returns the prompt fit (s, t) [B, 2] (None without the prompt) and, with `final_fit`, the
+    metric fit of the refined depth [B, 2]. The options are the refine loop's: `use_prompt` (use_refiner_residual,
+    v3.py:548-555) with `soft_gate`, `output_gate` / `output_gate_floor` and `anchor` (v3.py:565-573), `fit_iters`,
+    `fit_trim`, `fit_min_points` (fit_scale_shift's); with `post_depth` (and `final_fit`) every call also writes
+    s * exp(logz) + t of the refined map into `self.depth` [B, H, W] (+inf where not > 0; MetricFit.metal:200-211).
+    Inference only; the step allocates nothing after construction.
+    """
+
+    def __init__(self, weights, B: int, H: int, W: int, dh: Optional[int] = None, dw: Optional[int] = None, *,
+                 depth_resolution: float = 256.0, fit_iters: int = 4, fit_trim: float = 0.2, fit_min_points: int = 32,
+                 use_prompt: bool = True, soft_gate: bool = False, output_gate: bool = False,
+                 output_gate_floor: float = 0.1, anchor: float = 0.0, final_fit: bool = False,
+                 post_depth: bool = False, use_graph: bool = True, device="cuda"):
+        mod = weights if isinstance(weights, UNetRefiner) else UNetRefiner(weights, depth_resolution=depth_resolution)
+        w = mod.host_weights
+        if post_depth and not final_fit:
+            raise ValueError("post_depth needs final_fit")
+        if use_prompt and w.pr_w is None:
+            raise ValueError("use_prompt needs a refiner with prompt_proj")
+        ds = 2 ** (w.levels - 1)
+        if H % ds or W % ds:
+            raise ValueError(f"H and W must be multiples of the encoder downsampling {ds} (sparse_unet.py:187)")
+        self.device = torch.device(device)
+        if self.device.index is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
+        self.B, self.H, self.W = B, H, W
+        self.dh, self.dw = dh or H, dw or W
+        self.use_prompt, self.final_fit, self.post_depth = use_prompt, final_fit, post_depth
+        self.host_weights = w
+        self.weights = UNetDeviceWeights(w, self.device)
+        pad = lambda xs: (_lib.i32 * 8)(*(list(xs) + [0] * (8 - len(xs))))
+        cfg = UNetConfig(B, H, W, w.levels, pad(w.channels), pad([len(st) for st in w.down]),
+                         pad([len(st) for st in w.dec]), len(w.bott), int(w.enc_channels), float(mod.depth_resolution),
+                         int(use_graph))
+        with torch.cuda.device(self.device):
+            self.h = lib().pmg_unet_create(C.byref(cfg))
+            if not self.h:
+                raise _lib.PmgError(_lib.PMG_E_INVALID, lib().pmg_last_error().decode())
+            call("pmg_unet_set_weights", self.h, C.byref(self.weights.struct))
+            scfg = UNetStepConfig(self.dh, self.dw, int(fit_iters), float(fit_trim), int(fit_min_points),
+                                  int(use_prompt), int(soft_gate), int(output_gate), float(output_gate_floor),
+                                  float(anchor), int(final_fit))
+            call("pmg_unet_step_prepare", self.h, C.byref(scfg))
+        self.st_prompt = torch.zeros((B, 2), dtype=torch.float32, device=self.device)
+        self.st_final = torch.zeros((B, 2), dtype=torch.float32, device=self.device)
+        self.depth = torch.empty((B, H, W), dtype=torch.float32, device=self.device) if post_depth else None
+
+    def __call__(self, points: torch.Tensor, lidar: torch.Tensor, conf: torch.Tensor, encoder_feature: torch.Tensor,
+                 encoder_bias_map: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None):
+        w = self.host_weights
+        B, H, W = self.B, self.H, self.W
+        ds = 2 ** (w.levels - 1)
+        need = lambda t, shape, name: _need(t, shape, name, self.device)
+        need(points, (B, H, W, 3), "points")
+        need(lidar, (B, self.dh, self.dw), "lidar")
+        need(conf, (B, self.dh, self.dw), "conf")
+        need(encoder_feature, (B, w.enc_channels, H // ds, W // ds), "encoder_feature")
+        if encoder_bias_map is not None:
+            need(encoder_bias_map, (B, w.channels[-1], H // ds, W // ds), "encoder_bias_map")
+        out = points if out is None else out
+        need(out, (B, H, W, 3), "out")
+        p = lambda t: None if t is None else t.data_ptr()
+        call("pmg_unet_step", self.h, points.data_ptr(), out.data_ptr(), lidar.data_ptr(), conf.data_ptr(),
+             encoder_feature.data_ptr(), p(encoder_bias_map), self.st_prompt.data_ptr(), self.st_final.data_ptr(),
+             p(self.depth), C.c_void_p(torch.cuda.current_stream(self.device).cuda_stream))
+        return (self.st_prompt if self.use_prompt else None), (self.st_final if self.final_fit else None)
+
+    def anchor_fit(self) -> torch.Tensor:
+        """A copy of the last step's anchor re-fit (s, t) [B, 2] (for parity tests)."""
+        ptr = lib().pmg_unet_buffer(self.h, _lib.UNET_STEP_ST, 0)
+        out = torch.empty((self.B, 2), dtype=torch.float32, device=self.device)
+        from .refiner import _copy_device
+
+        _copy_device(out.data_ptr(), ptr + 4 * 4 * self.B, 8 * self.B,
+                     torch.cuda.current_stream(self.device).cuda_stream)
+        return out
+
+    def check(self) -> None:
+        """Synchronises the stream; raises if a metric fit's device-wide wait expired in a step since the last
+        check."""
+        call("pmg_unet_check", self.h, C.c_void_p(torch.cuda.current_stream(self.device).cuda_stream))
+
+    def close(self) -> None:
+        if getattr(self, "h", None):
+            lib().pmg_unet_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # interpreter shutdown: the library handle may already be gone
+            pass
+
+
+def _need(t: torch.Tensor, shape, name: str, device: torch.device) -> None:
+    if t.dtype != torch.float32 or tuple(t.shape) != tuple(shape) or not t.is_contiguous() or t.device != device:
+        raise ValueError(f"{name} must be a contiguous float32 tensor {tuple(shape)} on {device}, got "
+                         f"{t.dtype} {tuple(t.shape)} on {t.device}")
 
 
 def _is_raster(coords: torch.Tensor, B: int, H: int, W: int) -> bool:
