@@ -317,7 +317,9 @@ def fit_trace(args):
     (100 MHz) at the launch, after the first solve and after every trim round, with the round's selection path
     (0 bracket, 1 bracket missed -> radix, 2 radix, 3 radix + third pass), its candidate count, and the number of
     rounds run (the loop stops at a fixed point). Prints one line per round for the prompt fit and the final fit of
-    the configuration, on its input point map and on the map one refiner step made (the last of 20 runs each)."""
+    the configuration, on its input point map and on the map one refiner step made (the last of 20 runs each). A
+    library built with PMG_FIT_PHASE_TRACE=1 (python -m promptmoge_amd.build) also records the phases of each
+    round, which are printed after it."""
     import numpy as np
     import torch
 
@@ -346,8 +348,15 @@ def fit_trace(args):
             for it in range(int(tr[130])):
                 t = int(tr[2 * it + 1])
                 dt = ((t - prev) & 0xffffffff) / 100.0
-                print(f"round {it:2d} {dt:8.2f}  path {names.get(int(tr[2 * it]) & 15, '?'):24s} "
-                      f"candidates {int(tr[2 * it]) >> 4}")
+                line = (f"round {it:2d} {dt:8.2f}  path {names.get(int(tr[2 * it]) & 15, '?'):24s} "
+                        f"candidates {int(tr[2 * it]) >> 4}")
+                mk = [int(v) for v in tr[256 + it * 8: 256 + it * 8 + 7]]
+                if it < 32 and any(mk):  # phase marks: a library built with PMG_FIT_PHASE_TRACE=1
+                    d = [((mk[k + 1] - mk[k]) & 0xffffffff) / 100.0 for k in range(6)]
+                    line += (f"  | before stage {((mk[0] - prev) & 0xffffffff) / 100.0:.2f} publish {d[0]:.2f} "
+                             f"barrier {d[1]:.2f} totals {d[2]:.2f} candload {d[3]:.2f} select {d[4]:.2f} "
+                             f"solve {d[5]:.2f}")
+                print(line)
                 prev = t
             print(f"total (block 0) {((prev - t0) & 0xffffffff) / 100.0:8.2f}", flush=True)
     return 0

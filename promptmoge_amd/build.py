@@ -8,6 +8,7 @@ Every translation unit is compiled with
                                                  NumPy restatement);
   -fhip-fp32-correctly-rounded-divide-sqrt       IEEE division and square root in device code;
   -Xclang -target-feature -Xclang -packed-fp32-ops   no packed fp32 instructions are generated.
+With PMG_FIT_PHASE_TRACE=1 in the environment the metric fit is compiled with its phase marks (profiling only).
 """
 from __future__ import annotations
 
@@ -43,7 +44,10 @@ def _hipcc() -> str:
 
 def _compile(src: str) -> Path:
     obj = BUILD / (Path(src).stem + ".o")
-    cmd = [_hipcc(), *FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
+    extra = []
+    if src == "pmg_fit.hip" and os.environ.get("PMG_FIT_PHASE_TRACE") == "1":
+        extra = ["-DPMG_FIT_PHASE_TRACE"]  # the metric fit records its per-round phases (profiling builds only)
+    cmd = [_hipcc(), *FLAGS, *extra, "-c", str(CSRC / src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{r.stdout}\n{r.stderr}")
