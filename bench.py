@@ -362,10 +362,11 @@ def fit_trace(args):
     return 0
 
 
-def unet_bench(stream, reps=20):
-    """The multi-level int8 refiner (UNetRefiner, pmg_unet_*) at Model A's size: a 5-level Sparse3DUNet with
-    channels [32, 64, 128, 256, 256], one block per stage, encoder 1024 channels on the 30 x 40 token grid, prompt
-    features and encoder bias map; one forward = level structure + maps + all layers (one captured graph)."""
+def unet_bench(stream, reps=20, channels=(32, 64, 128, 256, 256), precision="int8"):
+    """The multi-level refiner (UNetRefiner, pmg_unet_*) at Model A's size: a 5-level Sparse3DUNet with the deployed
+    int8 channels [32, 64, 128, 256, 256] (or the fp16 teacher's stock [32, 64, 128, 256, 512]), one block per
+    stage, encoder 1024 channels on the 30 x 40 token grid, prompt features and encoder bias map; one forward =
+    level structure + maps + all layers (one captured graph)."""
     import numpy as np
     import torch
 
@@ -376,7 +377,7 @@ def unet_bench(stream, reps=20):
     cfg = spec.CONFIGS["A"]
     sc = spec.make_scene(cfg)
     H, W = cfg.H, cfg.W
-    w = uw.make_unet_weights([32, 64, 128, 256, 256], 1024, seed=1)
+    w = uw.make_unet_weights(list(channels), 1024, seed=1)
     for layer in w.quantised_layers().values():  # clips of the right scale for these weights (timing only)
         if hasattr(layer, "clip1"):
             layer.clip1, layer.clip2 = 3.0, 2.0
@@ -388,9 +389,9 @@ def unet_bench(stream, reps=20):
     with torch.cuda.stream(stream):
         feats = torch.from_numpy(sc.points.reshape(M, 3).copy()).to(dev)
         enc = torch.from_numpy(rng.normal(0, 1, (1, 1024, H // 16, W // 16)).astype(np.float32)).to(dev)
-        bias = torch.from_numpy(rng.normal(0, 0.1, (1, 256, H // 16, W // 16)).astype(np.float32)).to(dev)
+        bias = torch.from_numpy(rng.normal(0, 0.1, (1, channels[-1], H // 16, W // 16)).astype(np.float32)).to(dev)
         pf = torch.from_numpy(np.stack([rng.normal(0, 0.05, M), rng.uniform(0, 1, M)], 1).astype(np.float32)).to(dev)
-        mod = UNetRefiner(w)
+        mod = UNetRefiner(w, precision=precision)
         shape = torch.Size([1, H, W, 1024, 3])
         for _ in range(3):
             mod(feats, None, shape, enc, prompt_feats=pf, encoder_bias_map=bias)
@@ -403,8 +404,8 @@ def unet_bench(stream, reps=20):
         e1.record(stream)
         torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / reps
-    return {"workload": "A-shape 5-level int8 Sparse3DUNet [32, 64, 128, 256, 256], 1 block per stage, encoder 1024 "
-                        "x 30x40 tokens, prompt + bias map; forward incl. level structure (keys from depth)",
+    return {"workload": f"A-shape 5-level {precision} Sparse3DUNet {list(channels)}, 1 block per stage, encoder "
+                        f"1024 x 30x40 tokens, prompt + bias map; forward incl. level structure (keys from depth)",
             "voxels_per_level": counts, "ms": round(ms, 4), "voxels_per_s": round(M / (ms * 1e-3), 1)}
 
 
@@ -648,7 +649,7 @@ def main() -> int:
     ap.add_argument("--micro-only", action="store_true",
                     help="run only the 1M-voxel map and conv microbench (for counter collection) and print it")
     ap.add_argument("--write-traffic", nargs=3, metavar=("OUT", "FETCH_DIR", "WRITE_DIR"))
-    ap.add_argument("--other", choices=["T", "H", "unet_A", "unet_A_step"],
+    ap.add_argument("--other", choices=["T", "H", "unet_A", "unet_A_step", "unet_T"],
                     help="time only this other configuration (K-step frame, or the multi-level U-Net) and print it")
     args = ap.parse_args()
     if args.write_traffic:
@@ -671,8 +672,9 @@ def main() -> int:
         return 0
     if args.other:
         s = torch.cuda.Stream()
-        res = {"unet_A": unet_bench, "unet_A_step": unet_step_bench}.get(args.other, lambda st: frame_bench(
-            args.other, st))(s)
+        res = {"unet_A": unet_bench, "unet_A_step": unet_step_bench,
+               "unet_T": lambda st: unet_bench(st, channels=(32, 64, 128, 256, 512), precision="fp16")}.get(
+            args.other, lambda st: frame_bench(args.other, st))(s)
         print(json.dumps({args.other: res}), flush=True)
         return 0
     from promptmoge_amd.refiner import RefinerStep
@@ -737,6 +739,7 @@ def main() -> int:
         others["gauge_A"] = gauge_bench(stream)
         others["unet_A"] = unet_bench(stream)
         others["unet_A_step"] = unet_step_bench(stream)
+        others["unet_T"] = unet_bench(stream, channels=(32, 64, 128, 256, 512), precision="fp16")
     cpu = None if args.no_cpu else cpu_baseline(env)
 
     line = {

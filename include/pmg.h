@@ -429,14 +429,17 @@ typedef struct {
     int enc_channels;       /* encoder_fuse in_features (multiple of 16) */
     float depth_resolution; /* refiner_depth_resolution (v3.py:29): keys when no coords are given */
     int use_graph;
+    int precision;          /* PMG_PREC_INT8 (the deployed refiners) or PMG_PREC_FP16 (the teacher, PromptMoGe-L:
+                               fp16 activations and weights in every conv and linear, fp32 accumulation, fp32
+                               residual streams; level widths up to 512, level 0 16 .. 64) */
 } pmg_unet_config;
 
 typedef struct {
-    const int8_t* w;      /* [N][K] int8, nn.Linear's (out, in) layout */
-    const float* w_scale; /* [N] per-output-channel weight scale */
+    const void* w;        /* [N][K], nn.Linear's (out, in) layout: int8, or fp16 with PMG_PREC_FP16 */
+    const float* w_scale; /* [N] per-output-channel weight scale (int8 only) */
     const float* bias;    /* [N] */
-    float a_scale;        /* clip/127 of the input activation */
-    float q_mult;         /* 127/clip: quantises the input */
+    float a_scale;        /* clip/127 of the input activation (int8 only) */
+    float q_mult;         /* 127/clip: quantises the input (int8 only) */
 } pmg_linear_weights;
 
 typedef struct {
@@ -448,7 +451,8 @@ typedef struct {
     const float* out_b;
     int n_blocks;       /* sum(enc_blocks) + bottleneck_blocks + sum(dec_blocks) */
     const pmg_block_weights* blocks;   /* host array in module order: down_stages[0..L-1], bottleneck_stage,
-                                          up_stages[0..L-2]; conv weights [C][27][C] int8 */
+                                          up_stages[0..L-2]; conv weights [C][27][C] int8 (fp16: fp16, and the
+                                          scales and clips are not read) */
     int n_linears;      /* 2 (levels - 1) + 3 */
     const pmg_linear_weights* linears; /* host array: downsample_blocks[0..L-2].linear, encoder_fuse, fuse_proj.0,
                                           fuse_proj.2, upsample_blocks[0..L-2].linear */

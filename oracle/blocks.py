@@ -9,6 +9,12 @@ Arithmetics ("mode"):
   "int8"       the deployed integer arithmetic (SparseConvInt8.metal:1-154, Refiner.metal:75-131, 133-322): int8 codes
                clamp(rint(y * 127/clip)), exact int32 accumulation, (acc * a_scale) * w_scale[n] + bias[n] in fp32,
                LayerNorm in the kernels' fixed "quad" summation order, exp/log/SiLU bit-reproducible (numerics.py)
+  "fp16"       the teacher (PromptMoGe-L) in half precision: every conv and linear on fp16 operands (activations and
+               weights rounded to fp16) with fp32 accumulation (here fp64, then rounded; `acc=np.float32` sums in
+               fp32 instead, another order of the same arithmetic), LayerNorm + SiLU in fp32
+               (quad order) rounded to fp16 as conv1's input, SiLU of conv1 rounded to fp16 as conv2's input, the
+               residual stream, pooling, upsampling, input_proj and out_proj in fp32 (the single-level teacher's
+               contract, refiner.blocks_fp16, extended to the U-Net's linears)
 """
 from __future__ import annotations
 
@@ -99,9 +105,10 @@ def out_proj(x: np.ndarray, w) -> np.ndarray:
     return np.float32(np.asarray(w.out_b).reshape(-1)[0]) + quad_sum(ow * x.astype(np.float32))
 
 
-def linear(x, lin, mode: str, record=None, path=None):
+def linear(x, lin, mode: str, record=None, path=None, acc=np.float64):
     """nn.Linear, out = x @ W^T + b, in the requested arithmetic; `lin` has w (out, in), b, clip. int8: the input
-    codes quant_i8(x, 127/clip), then linear_codes. `record` receives the input under `path`."""
+    codes quant_i8(x, 127/clip), then linear_codes; fp16: linear_f16 with sums in `acc`. `record` receives the input
+    under `path`."""
     x = np.asarray(x, np.float32)
     if record is not None:
         record[path] = x
@@ -110,7 +117,27 @@ def linear(x, lin, mode: str, record=None, path=None):
     if mode == "fakequant":
         return (fake_quant(x, lin.clip) @ fake_quant_weight(lin.w).T + np.asarray(lin.b, np.float32)).astype(
             np.float32)
+    if mode == "fp16":
+        return linear_f16(x, lin, acc=acc)
     return linear_codes(quant_i8(x, act_mult(lin.clip)), lin)
+
+
+def f16(x):
+    """Rounded to fp16 (round to nearest even), as float64."""
+    return np.asarray(x, np.float32).astype(np.float16).astype(np.float64)
+
+
+def linear_f16(x, lin, silu_out: bool = False, acc=np.float64):
+    """The teacher's linear: fp16(x) @ fp16(W)^T summed in `acc` (fp64: exactly; fp32: another summation, the spread
+    a kernel's own fp32 order may show), rounded to fp32, + b in fp32; with silu_out, SiLU of that, rounded to fp16
+    (fuse_proj.0 into fuse_proj.2's input)."""
+    y = (f16(x).astype(acc) @ f16(lin.w).astype(acc).T).astype(np.float32) + np.asarray(lin.b, np.float32)
+    y = y.astype(np.float32)
+    if silu_out:
+        from .numerics import silu_f32
+
+        return silu_f32(y).astype(np.float16).astype(np.float32)
+    return y
 
 
 def linear_codes(codes, lin):
@@ -130,7 +157,7 @@ def linear_silu_codes(x, lin, out_clip):
     return epilogue_q(acc, act_scale(lin.clip), s, lin.b, act_mult(out_clip))
 
 
-def resblock(x, nmap, blk, mode: str, trace=None, record=None, path=None):
+def resblock(x, nmap, blk, mode: str, trace=None, record=None, path=None, acc=np.float64):
     """SparseResBlock3d.forward (flex_sparse_blocks.py:70-75): h = silu(norm1(x)); conv1; silu; conv2; + x (the
     identity skip: the block keeps its width). `blk` has gamma, beta, w1, b1, w2, b2, clip1, clip2; nmap (M, 27).
     `trace` (a list) receives the block's codes / accumulators (int8) or output; `record` (fp32 / fakequant) the
@@ -146,6 +173,18 @@ def resblock(x, nmap, blk, mode: str, trace=None, record=None, path=None):
         out = rowwise(lambda ab, xb: epilogue_r(ab, act_scale(blk.clip2), s_w2, blk.b2, xb), acc2, x)
         if trace is not None:
             trace.append(dict(q1=q1, acc1=acc1, q2=q2, acc2=acc2, x=out))
+        return out
+    if mode == "fp16":
+        from .numerics import silu_f32
+
+        x = np.asarray(x, np.float32)
+        h1 = rowwise(lambda xb: ln_silu(xb, blk.gamma, blk.beta).astype(np.float16), x)
+        y1 = conv_float(h1.astype(acc), nmap, f16(blk.w1).astype(acc), dtype=acc).astype(np.float32)
+        h2 = rowwise(lambda yb: silu_f32(yb + np.asarray(blk.b1, np.float32)).astype(np.float16), y1)
+        y2 = conv_float(h2.astype(acc), nmap, f16(blk.w2).astype(acc), dtype=acc).astype(np.float32)
+        out = ((y2 + np.asarray(blk.b2, np.float32)) + x).astype(np.float32)
+        if trace is not None:
+            trace.append(dict(h1=h1, h2=h2, x=out))
         return out
     w1, w2 = np.asarray(blk.w1, np.float32), np.asarray(blk.w2, np.float32)
     h = silu(layer_norm(x, blk.gamma, blk.beta))

@@ -3,9 +3,9 @@
 Sparse3DUNet.forward (moge/model/modules/sparse_unet.py:176-258) with SparseResBlock3d, PoolDown and NearestUp
 (moge/model/modules/flex_sparse_blocks.py:50-105) over the _fallback flex_gemm structure (submanifold maps,
 perfect-partition pooling, nearest upsampling; promptmoge/_fallback/flex_gemm/_core.py:269-505). One composition in
-the three arithmetics of oracle/blocks.py: "fp32" (the reference module), "fakequant" (the module under
-enable_refiner_qat, qat.py:118-138) and "int8" (the deployed integer arithmetic, in the GPU kernels' fp32 op order;
-the device engine's sequence, Refiner.swift:224-292 and Refiner.metal:133-322).
+the four arithmetics of oracle/blocks.py: "fp32" (the reference module), "fakequant" (the module under
+enable_refiner_qat, qat.py:118-138), "int8" (the deployed integer arithmetic, in the GPU kernels' fp32 op order;
+the device engine's sequence, Refiner.swift:224-292 and Refiner.metal:133-322) and "fp16" (the teacher).
 
 Weights: any object with the attributes of promptmoge_amd.unet.UNetW (duck-typed). Linear layers are objects with
 `w` (out, in), `b` (out,) and `clip` (the activation clip of their input; unused in "fp32").
@@ -16,7 +16,7 @@ from typing import List, Optional, Sequence
 
 import numpy as np
 
-from .blocks import input_proj, linear, linear_codes, linear_silu_codes, out_proj, resblock, silu
+from .blocks import input_proj, linear, linear_codes, linear_f16, linear_silu_codes, out_proj, resblock, silu
 from .pool import pool_cache, sparse_pool, sparse_upsample
 from .structure import nmap_column, nmap_sorted, voxelize
 
@@ -67,16 +67,18 @@ def sample_rows(planar: np.ndarray, coords: np.ndarray) -> np.ndarray:
 
 # ------------------------------------------------------------------------------------------------- forward
 def forward(feats, levels: List[Level], w, encoder_feature, prompt_feats=None, encoder_bias_map=None,
-            mode: str = "int8", trace: Optional[dict] = None, record: Optional[dict] = None) -> np.ndarray:
+            mode: str = "int8", trace: Optional[dict] = None, record: Optional[dict] = None,
+            acc=np.float64) -> np.ndarray:
     """Sparse3DUNet.forward (sparse_unet.py:176-258) on a built structure. Returns (M0,) (out_channels = 1).
 
     feats (M0, 3) fp32; encoder_feature [B, C_enc, H/16, W/16]; prompt_feats (M0, 2) or None; encoder_bias_map
     [B, C_L, H/16, W/16] or None. trace (optional dict) receives per-stage results (int8: also block codes);
-    record (fp32 / fakequant) the input of every quantised layer under its module path (qat.py:118-138)."""
+    record (fp32 / fakequant) the input of every quantised layer under its module path (qat.py:118-138). acc: the
+    sums of the fp16 mode's convolutions and linears (fp64 exact; fp32 another order)."""
     L = len(levels)
     assert len(w.down) == L and len(w.pool) == L - 1 and len(w.up) == L - 1 and len(w.dec) == L - 1
     feats = np.asarray(feats, np.float32)
-    if mode == "int8":
+    if mode in ("int8", "fp16"):
         res = gate = None
         if prompt_feats is not None:
             pf = np.asarray(prompt_feats, np.float32)
@@ -93,7 +95,7 @@ def forward(feats, levels: List[Level], w, encoder_feature, prompt_feats=None, e
     for k in range(L):                                                          # sparse_unet.py:223-231
         bt = [] if tr is not None else None
         for j, blk in enumerate(w.down[k]):
-            x = resblock(x, levels[k].nmap, blk, mode, bt, record, f"down_stages.{k}.{j}")
+            x = resblock(x, levels[k].nmap, blk, mode, bt, record, f"down_stages.{k}.{j}", acc)
         if tr is not None:
             tr[f"down{k}"] = x
             tr[f"down{k}_blocks"] = bt
@@ -101,11 +103,11 @@ def forward(feats, levels: List[Level], w, encoder_feature, prompt_feats=None, e
             skips.append(x)
             nxt = levels[k + 1]
             pooled = sparse_pool(x, nxt.parent, nxt.M, "mean")                 # flex_sparse_blocks.py:85-90
-            x = linear(pooled, w.pool[k], mode, record, f"downsample_blocks.{k}.linear")
+            x = linear(pooled, w.pool[k], mode, record, f"downsample_blocks.{k}.linear", acc)
             if tr is not None:
                 tr[f"pool{k}"] = x
     top = levels[L - 1]
-    enc = linear(sample_rows(encoder_feature, top.coords), w.enc, mode, record, "encoder_fuse")  # :233-234
+    enc = linear(sample_rows(encoder_feature, top.coords), w.enc, mode, record, "encoder_fuse", acc)  # :233-234
     if tr is not None:
         tr["enc_lin"] = enc
     if encoder_bias_map is not None:
@@ -113,6 +115,8 @@ def forward(feats, levels: List[Level], w, encoder_feature, prompt_feats=None, e
     cat = np.concatenate([x, enc], axis=1)
     if mode == "int8":                                                          # :240
         x = linear_codes(linear_silu_codes(cat, w.fuse0, w.fuse2.clip), w.fuse2)
+    elif mode == "fp16":
+        x = linear_f16(linear_f16(cat, w.fuse0, silu_out=True, acc=acc), w.fuse2, acc=acc)
     else:
         x = linear(silu(linear(cat, w.fuse0, mode, record, "fuse_proj.0")), w.fuse2, mode, record, "fuse_proj.2")
     if tr is not None:
@@ -120,23 +124,23 @@ def forward(feats, levels: List[Level], w, encoder_feature, prompt_feats=None, e
         tr["fuse"] = x
     bt = [] if tr is not None else None
     for j, blk in enumerate(w.bott):                                            # :244-247
-        x = resblock(x, top.nmap, blk, mode, bt, record, f"bottleneck_stage.{j}")
+        x = resblock(x, top.nmap, blk, mode, bt, record, f"bottleneck_stage.{j}", acc)
     if tr is not None:
         tr["bott"] = x
         tr["bott_blocks"] = bt
     for i in range(L - 1):                                                      # :249-256
         t = L - 2 - i
-        lin = linear(x, w.up[i], mode, record, f"upsample_blocks.{i}.linear")   # flex_sparse_blocks.py:99-105
+        lin = linear(x, w.up[i], mode, record, f"upsample_blocks.{i}.linear", acc)  # flex_sparse_blocks.py:99-105
         x = (sparse_upsample(lin, levels[t + 1].parent) + skips[t]).astype(np.float32)
         if tr is not None:
             tr[f"dec{i}_in"] = x
         bt = [] if tr is not None else None
         for j, blk in enumerate(w.dec[i]):
-            x = resblock(x, levels[t].nmap, blk, mode, bt, record, f"up_stages.{i}.{j}")
+            x = resblock(x, levels[t].nmap, blk, mode, bt, record, f"up_stages.{i}.{j}", acc)
         if tr is not None:
             tr[f"dec{i}"] = x
             tr[f"dec{i}_blocks"] = bt
-    if mode == "int8":
+    if mode in ("int8", "fp16"):
         return out_proj(x, w)                                                   # :258
     return (x @ np.asarray(w.out_w, np.float32).reshape(1, -1).T).reshape(-1) + np.float32(np.asarray(w.out_b)[0])
 

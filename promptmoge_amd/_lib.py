@@ -53,7 +53,7 @@ class UNetConfig(C.Structure):
     _fields_ = [
         ("B", i32), ("H", i32), ("W", i32), ("levels", i32), ("channels", i32 * 8), ("enc_blocks", i32 * 8),
         ("dec_blocks", i32 * 8), ("bottleneck_blocks", i32), ("enc_channels", i32), ("depth_resolution", f32),
-        ("use_graph", i32),
+        ("use_graph", i32), ("precision", i32),
     ]
 
 

@@ -343,7 +343,8 @@ template <int C, int EPI, int NB = C / 16, int T = kG2Tiles, int PF = 1, int RS 
           typename E = int8_t>
 __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
     constexpr int RB = C * (int)sizeof(E);               // row bytes: the kernel moves 64-byte K chunks of any type
-    constexpr int GRP = RB == 64 ? 4 : 2;
+    // taps per LDS buffer: GRP taps of NF 1 KB fragments each, two buffers within the LDS
+    constexpr int GRP = RB == 64 ? 4 : (RB * NB <= 2048 ? 2 : 1);
     constexpr int KS = RB / 64;
     constexpr int NF = NB * KS;                          // 1 KB operand fragments per tap
     constexpr int WPT = GRP * NF / kG2Waves;             // fragments staged per wave per group
@@ -351,7 +352,8 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
     constexpr int NG2 = (NG + 1) / 2;                    // loop trips of two groups (one per LDS buffer)
     constexpr int CHUNK = kG2Waves * T * 16;             // rows per block step
     constexpr int NS = 16 * NB;                          // output channels of the block
-    static_assert(RB == 64 || RB == 128 || RB == 256, "rows of 64, 128 or 256 bytes");
+    static_assert(RB == 64 || RB == 128 || RB == 256 || RB == 512 || RB == 1024, "rows of 64 .. 1024 bytes");
+    static_assert(2 * GRP * NB * (RB / 64) <= 128, "two LDS buffers of GRP taps' weights");
     static_assert(sizeof(E) == 1 || !DEV, "device-sized launches are int8");
     typedef typename Acc<E>::type acc_t;
     static_assert(GRP * NF % kG2Waves == 0, "staging split");
@@ -463,7 +465,7 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
             for (int k = 0; k < kG2Waves; ++k) um |= s_um[k];
             um = (uint32_t)__builtin_amdgcn_readfirstlane((int)um);
             const int ntap = __builtin_popcount(um);
-            trips = ntap > 0 ? (ntap + 3) / 4 : 1;
+            trips = ntap > 0 ? (ntap + 2 * GRP - 1) / (2 * GRP) : 1;  // two groups of GRP taps per trip
             cw = ci = cm = um;
         }
         auto pop = [](uint32_t& rem) {
@@ -898,23 +900,27 @@ static int launch_g2(const ConvArgs& a, int epilogue, hipStream_t s) {
     }
 }
 
-// fp16 / bf16 / fp32 features, Ci = Co = C with rows of 64, 128 or 256 bytes: the weight-staged kernel on K chunks
-// of 32 halves (v_mfma_f32_16x16x32_f16 / _bf16) or 16 floats (four v_mfma_f32_16x16x4f32), fp32 accumulators.
-// Rows of 256 bytes hold 16 tiles of accumulators per wave at T = 4, so they run T = 2.
+// fp16 / bf16 / fp32 features, Ci = Co = C with rows of 64 - 1024 bytes: the weight-staged kernel on K chunks of 32
+// halves (v_mfma_f32_16x16x32_f16 / _bf16) or 16 floats (four v_mfma_f32_16x16x4f32), fp32 accumulators. Rows of
+// 256 bytes hold 16 tiles of accumulators per wave at T = 4, so they run T = 2; rows of 512 and 1024 bytes (fp16
+// C = 256, 512) split the output channels into slices of 64 (blockIdx.y: a tap's weights fit the LDS buffers) and
+// run T = 2 and 1 (the gathered rows of the two ring slots fill the registers).
 template <typename E, int C>
 static int launch_g2f(const ConvArgs& a, int epilogue, hipStream_t s) {
     static int cus = -1;
     if (cus < 0) cus = num_cus();
-    constexpr int T = C * (int)sizeof(E) == 256 ? 2 : 4, CHUNK = kG2Waves * T * 16;
+    constexpr int RB = C * (int)sizeof(E);
+    constexpr int NB = RB <= 256 ? C / 16 : 4;
+    constexpr int T = RB <= 128 ? 4 : (RB <= 512 ? 2 : 1), CHUNK = kG2Waves * T * 16;
     const int64_t nchunk = (a.M + CHUNK - 1) / CHUNK;
-    const dim3 grid((unsigned)(nchunk < cus ? nchunk : cus)), blk(kG2Threads);
+    const dim3 grid((unsigned)(nchunk < cus ? nchunk : cus), (unsigned)(C / (16 * NB))), blk(kG2Threads);
     switch (epilogue) {
-        case PMG_EPI_ACC: hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_ACC, C / 16, T, 1, 2, false, E>), grid, blk, 0, s, a); break;
-        case PMG_EPI_BIAS: hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_BIAS, C / 16, T, 1, 2, false, E>), grid, blk, 0, s, a); break;
-        case PMG_EPI_R: hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_R, C / 16, T, 1, 2, false, E>), grid, blk, 0, s, a); break;
+        case PMG_EPI_ACC: hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_ACC, NB, T, 1, 2, false, E>), grid, blk, 0, s, a); break;
+        case PMG_EPI_BIAS: hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_BIAS, NB, T, 1, 2, false, E>), grid, blk, 0, s, a); break;
+        case PMG_EPI_R: hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_R, NB, T, 1, 2, false, E>), grid, blk, 0, s, a); break;
         case PMG_EPI_SILU:
             if constexpr (std::is_same<E, _Float16>::value) {
-                hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_SILU, C / 16, T, 1, 2, false, E>), grid, blk, 0, s, a);
+                hipLaunchKernelGGL((spconv_g2_k<C, PMG_EPI_SILU, NB, T, 1, 2, false, E>), grid, blk, 0, s, a);
                 break;
             }
             [[fallthrough]];
@@ -924,10 +930,12 @@ static int launch_g2f(const ConvArgs& a, int epilogue, hipStream_t s) {
 }
 
 // Whether the fp staged kernel takes this convolution: Ci = Co >= 32 with rows of 64 - 256 bytes (fp16 / bf16 32,
-// 64, 128; fp32 32, 64), 32-bit buffer offsets and aligned vectors.
+// 64, 128; fp32 32, 64), or fp16 / bf16 rows of 512 or 1024 bytes (C = 256, 512: slices of 64 output channels),
+// 32-bit buffer offsets and aligned vectors.
 static bool g2f_fits(const ConvArgs& a, int Ci, int elt, int epilogue) {
     const int rb = Ci * elt;
-    return Ci == a.Co && Ci >= 32 && Ci % 16 == 0 && (rb == 64 || rb == 128 || rb == 256) &&
+    return Ci == a.Co && Ci >= 32 && Ci % 16 == 0 &&
+           (rb == 64 || rb == 128 || rb == 256 || (elt == 2 && (rb == 512 || rb == 1024))) &&
            a.M * 27 * 4 < ((int64_t)1 << 31) && a.M * rb < ((int64_t)1 << 31) && aligned16(a.out) &&
            (epilogue != PMG_EPI_R || aligned16(a.skip));
 }
@@ -1032,6 +1040,45 @@ int launch_conv_i8_dev(const DevConv& d, hipStream_t s) {
 }
 
 template <typename T>
+static int conv_common(const ConvArgs& a, int Ci, int epilogue, hipStream_t s);
+
+// The fp16 teacher's convolution on a device-sized level (the int8 one's counterpart): x and w fp16, fp32
+// accumulation; epilogues SILU (bias, SiLU, fp16 out: conv1), R (bias + skip, fp32: conv2), BIAS, ACC. The
+// weight-staged kernel takes Ci = Co = 32, 64, 128 (it reads the row count on the device); other widths the generic
+// one-wave-per-16-rows kernel.
+int launch_conv_f16_dev(const DevConv& d, hipStream_t s) {
+    PMG_REQUIRE(d.x && d.nmap_t && d.tile_mask && d.w && d.out && d.m_dev, "null buffer");
+    PMG_REQUIRE(d.Ci % 16 == 0 && d.Co % 16 == 0 && d.Ci > 0 && d.Co > 0, "channels must be multiples of 16");
+    PMG_REQUIRE(d.epilogue == PMG_EPI_SILU || d.epilogue == PMG_EPI_R || d.epilogue == PMG_EPI_BIAS ||
+                    d.epilogue == PMG_EPI_ACC,
+                "unsupported epilogue");
+    PMG_REQUIRE(d.epilogue != PMG_EPI_R || d.skip, "skip required");
+    if (d.cap == 0) return PMG_OK;
+    ConvArgs a{};
+    a.x = (const uint8_t*)d.x;
+    a.nmap_t = d.nmap_t;
+    a.tmask = d.tile_mask;
+    a.w = (const uint8_t*)d.w;
+    a.M = d.cap;
+    a.Co = d.Co;
+    a.row_bytes = 2 * d.Ci;
+    a.nchunk = 2 * d.Ci / 16;
+    a.a_scale = 1.0f;
+    a.bias = d.bias;
+    a.skip = d.skip;
+    a.out = d.out;
+    a.m_dev = d.m_dev;
+    if (g2f_fits(a, d.Ci, 2, d.epilogue)) {
+        if (d.Ci == 32) return launch_g2f<_Float16, 32>(a, d.epilogue, s);
+        if (d.Ci == 64) return launch_g2f<_Float16, 64>(a, d.epilogue, s);
+        if (d.Ci == 128) return launch_g2f<_Float16, 128>(a, d.epilogue, s);
+        if (d.Ci == 256) return launch_g2f<_Float16, 256>(a, d.epilogue, s);
+        return launch_g2f<_Float16, 512>(a, d.epilogue, s);
+    }
+    return conv_common<_Float16>(a, d.Ci, d.epilogue, s);
+}
+
+template <typename T>
 static int conv_common(const ConvArgs& a, int Ci, int epilogue, hipStream_t s) {
     const int nb = pick_nb(a.Co);
     switch (epilogue) {
@@ -1122,7 +1169,9 @@ int pmg_spconv_f16(const uint16_t* x, const int32_t* nmap_t, const uint32_t* til
     if (g2f_fits(a, Ci, 2, epilogue)) {
         if (Ci == 32) return launch_g2f<_Float16, 32>(a, epilogue, (hipStream_t)stream);
         if (Ci == 64) return launch_g2f<_Float16, 64>(a, epilogue, (hipStream_t)stream);
-        return launch_g2f<_Float16, 128>(a, epilogue, (hipStream_t)stream);
+        if (Ci == 128) return launch_g2f<_Float16, 128>(a, epilogue, (hipStream_t)stream);
+        if (Ci == 256) return launch_g2f<_Float16, 256>(a, epilogue, (hipStream_t)stream);
+        return launch_g2f<_Float16, 512>(a, epilogue, (hipStream_t)stream);
     }
     return conv_common<_Float16>(a, Ci, epilogue, (hipStream_t)stream);
 }
@@ -1139,7 +1188,9 @@ int pmg_spconv_bf16(const uint16_t* x, const int32_t* nmap_t, const uint32_t* ti
     if (g2f_fits(a, Ci, 2, epilogue)) {
         if (Ci == 32) return launch_g2f<__bf16, 32>(a, epilogue, (hipStream_t)stream);
         if (Ci == 64) return launch_g2f<__bf16, 64>(a, epilogue, (hipStream_t)stream);
-        return launch_g2f<__bf16, 128>(a, epilogue, (hipStream_t)stream);
+        if (Ci == 128) return launch_g2f<__bf16, 128>(a, epilogue, (hipStream_t)stream);
+        if (Ci == 256) return launch_g2f<__bf16, 256>(a, epilogue, (hipStream_t)stream);
+        return launch_g2f<__bf16, 512>(a, epilogue, (hipStream_t)stream);
     }
     return conv_common<__bf16>(a, Ci, epilogue, (hipStream_t)stream);
 }

@@ -140,6 +140,9 @@ struct DevConv {
     int64_t part_bytes;
 };
 int launch_conv_i8_dev(const DevConv& d, hipStream_t s);
+// The same for the fp16 teacher: x, w fp16 (the int8_t pointers hold fp16 data), fp32 accumulation, epilogues SILU
+// (bias + SiLU to fp16), R, BIAS, ACC; no tap split.
+int launch_conv_f16_dev(const DevConv& d, hipStream_t s);
 int64_t conv_split_bytes(int C);  // partials buffer of a width's tap split (0: no split at that width)
 
 // Stable LSD radix sort of (uint64 key, int32 value) pairs over the keys' low `bits` bits, 8 bits per pass

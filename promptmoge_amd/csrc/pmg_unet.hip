@@ -261,12 +261,18 @@ static unsigned row_grid(int64_t threads_cap) {
     return (unsigned)(b < 1 ? 1 : (b < kRowBlocksMax ? b : kRowBlocksMax));
 }
 
+// A linear's or convolution's input activations, in the network's arithmetic: int8 codes clamp(rint(v * mult)), or
+// fp16 (the teacher; mult unused).
+__device__ inline void put4(int8_t* dst, const float (&h)[4], float mult) { store_codes4(h, mult, dst); }
+__device__ inline void put4(_Float16* dst, const float (&h)[4], float) { store_half4(h, dst); }
+
 // PoolDown's mean (sparse_pool 'mean', _core.py:464-476: fp32 sums in input row order from 0, divided by the
-// child count) of coarse voxel o, quantised for the pool linear: codes = clamp(rint(mean * mult)). Threads per row
-// = C / 4 (a float4 each).
+// child count) of coarse voxel o, as the pool linear's input (codes = clamp(rint(mean * mult)), or fp16). Threads
+// per row = C / 4 (a float4 each).
+template <typename O>
 __global__ __launch_bounds__(256) void pool_quant_k(const float* __restrict__ x, int C, PoolGeom g,
                                                     const int4* __restrict__ coords_c, const int64_t* __restrict__ count,
-                                                    float mult, int8_t* __restrict__ codes) {
+                                                    float mult, O* __restrict__ codes) {
     const int tpr = C >> 2;
     const int64_t items = *count * tpr;
     for (int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x; gid < items; gid += (int64_t)gridDim.x * 256) {
@@ -296,18 +302,19 @@ __global__ __launch_bounds__(256) void pool_quant_k(const float* __restrict__ x,
         }
         const float cnt = (float)n;
         const float h[4] = {acc.x / cnt, acc.y / cnt, acc.z / cnt, acc.w / cnt};
-        store_codes4(h, mult, codes + o * C + 4 * cq);
+        put4(codes + o * C + 4 * cq, h, mult);
     }
 }
 
-// codes = clamp(rint(x * mult)) of a device-sized [rows][C] fp32 array (the input of NearestUp's linear).
+// The input of NearestUp's linear from a device-sized [rows][C] fp32 array: codes = clamp(rint(x * mult)), or fp16.
+template <typename O>
 __global__ __launch_bounds__(256) void quant_rows_k(const float* __restrict__ x, int C, const int64_t* __restrict__ count,
-                                                    float mult, int8_t* __restrict__ codes) {
+                                                    float mult, O* __restrict__ codes) {
     const int64_t groups = *count * C / 4;  // groups of 4 values
     for (int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x; q < groups; q += (int64_t)gridDim.x * 256) {
         const float4 v = *(const float4*)(x + q * 4);
         const float h[4] = {v.x, v.y, v.z, v.w};
-        store_codes4(h, mult, codes + q * 4);
+        put4(codes + q * 4, h, mult);
     }
 }
 
@@ -316,12 +323,13 @@ __global__ __launch_bounds__(256) void quant_rows_k(const float* __restrict__ x,
 //   UP = false: codes = quant(silu(LN(x))) of x
 //   UP = true:  y = lin[parent[m]] + skip[m] (NearestUp + the U-Net's skip add, sparse_unet.py:251-254), written
 //               to y_out, then (gamma non-NULL) codes of y
-template <int C, bool UP>
+// The codes are int8 (O = int8_t: SiLU inside the requantisation) or fp16 (O = _Float16: silu_fast, rounded).
+template <int C, bool UP, typename O>
 __global__ __launch_bounds__(256) void rows_ln_k(const float* __restrict__ x, const int32_t* __restrict__ parent,
                                                  const float* __restrict__ skip, const int64_t* __restrict__ count,
                                                  const float* __restrict__ gamma, const float* __restrict__ beta,
                                                  float eps, float mult, float* __restrict__ y_out,
-                                                 int8_t* __restrict__ codes) {
+                                                 O* __restrict__ codes) {
     constexpr int NB = C / 16;
     const int64_t M = *count;
     const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
@@ -349,21 +357,33 @@ __global__ __launch_bounds__(256) void rows_ln_k(const float* __restrict__ x, co
             }
         }
         if (!gamma) continue;
-        ln_silu_quad<NB, false>(y, gamma, beta, eps, g);
-        uint32_t pk[NB];
-        silu_codes_packed<NB>(y, mult, pk);
-        if (ok) {
+        if constexpr (sizeof(O) == 1) {
+            ln_silu_quad<NB, false>(y, gamma, beta, eps, g);
+            uint32_t pk[NB];
+            silu_codes_packed<NB>(y, mult, pk);
+            if (ok) {
 #pragma unroll
-            for (int j = 0; j < NB; ++j) *(uint32_t*)(codes + mo * C + 16 * j + 4 * g) = pk[j];
+                for (int j = 0; j < NB; ++j) *(uint32_t*)(codes + mo * C + 16 * j + 4 * g) = pk[j];
+            }
+        } else {
+            ln_silu_quad<NB, true>(y, gamma, beta, eps, g);
+            if (ok) {
+#pragma unroll
+                for (int j = 0; j < NB; ++j) store_half4(y[j], codes + mo * C + 16 * j + 4 * g);
+            }
         }
     }
 }
 
-// The encoder feature, planar [B][K][RC] fp32, into int8 rows [B * RC][K] = clamp(rint(v * mult)): 64 x 64 tiles
-// transposed through LDS (loads along the token index, stores along the channel).
+// The encoder feature, planar [B][K][RC] fp32, into token rows [B * RC][K] (int8 clamp(rint(v * mult)), or fp16):
+// 64 x 64 tiles transposed through LDS (loads along the token index, stores along the channel).
+__device__ inline int8_t to_act(float v, float mult, int8_t) { return quant_i8(v, mult); }
+__device__ inline _Float16 to_act(float v, float, _Float16) { return (_Float16)v; }
+
+template <typename O>
 __global__ __launch_bounds__(256) void enc_quant_k(const float* __restrict__ planar, int K, int64_t RC, float mult,
-                                                   int8_t* __restrict__ codes) {
-    __shared__ int8_t tile[64][64 + 4];
+                                                   O* __restrict__ codes) {
+    __shared__ O tile[64][64 + 4];
     const int b = blockIdx.z;
     const int64_t t0 = (int64_t)blockIdx.x * 64;
     const int k0 = blockIdx.y * 64;
@@ -374,27 +394,41 @@ __global__ __launch_bounds__(256) void enc_quant_k(const float* __restrict__ pla
         const int64_t t = t0 + tx;
         float v = 0.0f;
         if (t < RC && k0 + kk < K) v = planar[((int64_t)b * K + k0 + kk) * RC + t];
-        tile[kk][tx] = quant_i8(v, mult);
+        tile[kk][tx] = to_act(v, mult, O{});
     }
     __syncthreads();
     const int tt = threadIdx.x >> 2, kc = (threadIdx.x & 3) * 16;
     const int64_t t = t0 + tt;
     if (t >= RC || k0 + kc >= K) return;
-    uint32_t w[4];
+    O* const dst = codes + ((int64_t)b * RC + t) * K + k0 + kc;
+    if constexpr (sizeof(O) == 1) {
+        uint32_t w[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-        w[u] = 0;
+        for (int u = 0; u < 4; ++u) {
+            w[u] = 0;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) w[u] |= (uint32_t)(uint8_t)tile[kc + 4 * u + i][tt] << (8 * i);
+            for (int i = 0; i < 4; ++i) w[u] |= (uint32_t)(uint8_t)tile[kc + 4 * u + i][tt] << (8 * i);
+        }
+        *(uint4*)dst = make_uint4(w[0], w[1], w[2], w[3]);
+    } else {
+        typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+        h8 v0, v1;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            v0[i] = tile[kc + i][tt];
+            v1[i] = tile[kc + 8 + i][tt];
+        }
+        *(h8*)dst = v0;
+        *(h8*)(dst + 8) = v1;
     }
-    *(uint4*)(codes + ((int64_t)b * RC + t) * K + k0 + kc) = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
 // fuse_proj.0's input: cat([x, enc_tok[token of the voxel's column]]) quantised with one scale (sparse_unet.py:
 // 240; the deployed concat_q8, Refiner.metal:285-300). Token of (b, i, j) = (b * R + i) * Cc + j.
+template <typename O>
 __global__ __launch_bounds__(256) void concat_quant_k(const float* __restrict__ x, const float* __restrict__ enc_tok,
                                                       const int4* __restrict__ coords, const int64_t* __restrict__ count,
-                                                      int C, int R, int Cc, float mult, int8_t* __restrict__ codes) {
+                                                      int C, int R, int Cc, float mult, O* __restrict__ codes) {
     const int tpr = C >> 1;  // 2C channels, 4 per thread
     const int64_t items = *count * tpr;
     for (int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x; gid < items; gid += (int64_t)gridDim.x * 256) {
@@ -409,20 +443,22 @@ __global__ __launch_bounds__(256) void concat_quant_k(const float* __restrict__ 
         }
         const float4 v = *(const float4*)src;
         const float h[4] = {v.x, v.y, v.z, v.w};
-        store_codes4(h, mult, codes + o * 2 * C + c);
+        put4(codes + o * 2 * C + c, h, mult);
     }
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// int8 dense GEMM on MFMA (nn.Linear on int8 codes, the deployed dg8 kernels, Refiner.metal:173-250):
+// Dense GEMM on MFMA (nn.Linear; in int8 the deployed dg8 kernels, Refiner.metal:173-250):
 //   out[m][n] = (acc * a_scale) * w_scale[n] + bias[n] (+ planar_add[b][n][rc], m = b * RC + rc)      EPI_BIAS
 //   codes[m][n] = quant(silu(...), out_mult)                                                           EPI_Q
 // acc = sum_k A[m][k] * W[n][k] exact in int32; A [rows][K] int8 codes, W [N][K] int8 (nn.Linear's layout).
-// One wave per 16 rows x 16 NB columns, v_mfma_i32_16x16x64_i8 over the K chunks with the operand layout of
-// spconv_k (lane l: row / column l % 16, 16-byte chunk l / 16 of each 64-byte step).
+// The teacher (E = _Float16): fp16 A and W, fp32 accumulation (v_mfma_f32_16x16x32_f16), out = acc + bias[n]
+// (+ planar_add), or SiLU of it rounded to fp16 (EPI_Q). One wave per 16 rows x 16 NB columns, MFMAs over the
+// 16-byte K chunks with the operand layout of spconv_k (lane l: row / column l % 16, chunk l / 16 of each 64-byte
+// step).
 struct GemmArgs {
-    const int8_t* a;
-    const int8_t* w;
+    const void* a;
+    const void* w;
     int64_t rows_cap;
     const int64_t* rows_dev;  // rows on the device, or NULL for rows_cap
     int K, N;
@@ -435,39 +471,50 @@ struct GemmArgs {
     int64_t planar_rc;
 };
 
-template <int NB, int EPI>
+__device__ inline void gemm_mma(v4i& acc, const v4i& a, const v4i& b, int8_t) {
+    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc, 0, 0, 0);
+}
+__device__ inline void gemm_mma(v4f& acc, const v4i& a, const v4i& b, _Float16) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, a), __builtin_bit_cast(v8h, b), acc, 0, 0,
+                                                  0);
+}
+
+template <int NB, int EPI, typename E = int8_t>
 __global__ __launch_bounds__(256) void gemm_i8_k(GemmArgs g) {
+    typedef typename std::conditional<sizeof(E) == 1, v4i, v4f>::type acc_t;
     const int64_t rows = g.rows_dev ? *g.rows_dev : g.rows_cap;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int r = lane & 15, gq = lane >> 4;
     const int n0 = blockIdx.y * 16 * NB;
-    const int nchunk = g.K >> 4;
+    const int rowb = g.K * (int)sizeof(E);  // bytes per row of A and W
+    const int nchunk = rowb >> 4;
+    const uint8_t* const ga = (const uint8_t*)g.a;
+    const uint8_t* const gw = (const uint8_t*)g.w;
     // blocks of 64 rows (16 per wave), grid-stride over the rows on the device
     for (int64_t mb = blockIdx.x; mb * 64 < rows; mb += gridDim.x) {
         const int64_t m0 = (mb * 4 + wv) * 16;
         if (m0 >= rows) break;
         const int64_t row = m0 + r;
         const bool row_ok = row < rows;
-        v4i acc[NB];
+        acc_t acc[NB];
 #pragma unroll
-        for (int j = 0; j < NB; ++j) acc[j] = v4i{0, 0, 0, 0};
+        for (int j = 0; j < NB; ++j) acc[j] = acc_t{0, 0, 0, 0};
         // K in steps of 4 chunks (one per lane group), the next step's operands requested before this step's
         // MFMAs. Loads are unconditional (a clamped address; the padding chunks and rows past the end are zeroed
         // when used), so the memory waits name exactly the step they need.
-        const int64_t arow = (row_ok ? row : 0) * g.K;
+        const int64_t arow = (row_ok ? row : 0) * rowb;
         auto load = [&](int q0, v4i& av, v4i (&bv)[NB]) {
             const int q = q0 + gq < nchunk ? q0 + gq : nchunk - 1;
-            av = *(const v4i*)(g.a + arow + q * 16);
+            av = *(const v4i*)(ga + arow + q * 16);
 #pragma unroll
-            for (int j = 0; j < NB; ++j) bv[j] = *(const v4i*)(g.w + (int64_t)(n0 + 16 * j + r) * g.K + q * 16);
+            for (int j = 0; j < NB; ++j) bv[j] = *(const v4i*)(gw + (int64_t)(n0 + 16 * j + r) * rowb + q * 16);
         };
         auto mma = [&](int q0, const v4i& av, const v4i (&bv)[NB]) {
             const bool on = q0 + gq < nchunk;
             const v4i z = {0, 0, 0, 0};
             const v4i a = on && row_ok ? av : z;
 #pragma unroll
-            for (int j = 0; j < NB; ++j)
-                acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, on ? bv[j] : z, acc[j], 0, 0, 0);
+            for (int j = 0; j < NB; ++j) gemm_mma(acc[j], a, on ? bv[j] : z, E{});
         };
         v4i a0, a1, b0[NB], b1[NB];
         load(0, a0, b0);
@@ -481,16 +528,24 @@ __global__ __launch_bounds__(256) void gemm_i8_k(GemmArgs g) {
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
             const int n = n0 + 16 * j + r;
-            const float ws = g.w_scale[n], bs = g.bias ? g.bias[n] : 0.0f;
+            const float ws = sizeof(E) == 1 ? g.w_scale[n] : 1.0f, bs = g.bias ? g.bias[n] : 0.0f;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int64_t m = m0 + 4 * gq + i;
                 if (m >= rows) continue;
-                float y = (float)acc[j][i] * g.a_scale;
-                y = y * ws;
+                float y;
+                if constexpr (sizeof(E) == 1) {
+                    y = (float)acc[j][i] * g.a_scale;
+                    y = y * ws;
+                } else {
+                    y = acc[j][i];
+                }
                 if (g.bias) y = y + bs;
                 if constexpr (EPI == PMG_EPI_Q) {
-                    ((int8_t*)g.out)[m * g.N + n] = silu_quant_i8(y, g.out_mult);
+                    if constexpr (sizeof(E) == 1)
+                        ((int8_t*)g.out)[m * g.N + n] = silu_quant_i8(y, g.out_mult);
+                    else
+                        ((_Float16*)g.out)[m * g.N + n] = (_Float16)silu_fast(y);
                 } else {
                     if (g.planar_add) {
                         const int64_t b = m / g.planar_rc, rc = m - b * g.planar_rc;
@@ -503,7 +558,7 @@ __global__ __launch_bounds__(256) void gemm_i8_k(GemmArgs g) {
     }
 }
 
-static int launch_gemm(const GemmArgs& g, int epi, hipStream_t s) {
+static int launch_gemm(const GemmArgs& g, int epi, bool f16, hipStream_t s) {
     PMG_REQUIRE(g.K % 16 == 0 && g.N % 16 == 0 && g.K > 0 && g.N > 0, "GEMM sizes must be multiples of 16");
     if (g.rows_cap == 0) return PMG_OK;
     const int b = g.N / 16;
@@ -513,12 +568,18 @@ static int launch_gemm(const GemmArgs& g, int epi, hipStream_t s) {
     const int64_t gx_max = kRowBlocksMax / gy > 0 ? kRowBlocksMax / gy : 1;  // device-sized rows: grid-stride
     if (g.rows_dev && gx > gx_max) gx = gx_max;
     const dim3 grid((unsigned)gx, gy);
-#define PMG_GEMM_CASE(NBV)                                                                       \
-    if (nb == NBV) {                                                                             \
-        if (epi == PMG_EPI_Q)                                                                    \
-            hipLaunchKernelGGL((gemm_i8_k<NBV, PMG_EPI_Q>), grid, dim3(256), 0, s, g);           \
-        else                                                                                     \
-            hipLaunchKernelGGL((gemm_i8_k<NBV, PMG_EPI_BIAS>), grid, dim3(256), 0, s, g);        \
+#define PMG_GEMM_CASE(NBV)                                                                                \
+    if (nb == NBV) {                                                                                      \
+        if (f16) {                                                                                        \
+            if (epi == PMG_EPI_Q)                                                                         \
+                hipLaunchKernelGGL((gemm_i8_k<NBV, PMG_EPI_Q, _Float16>), grid, dim3(256), 0, s, g);      \
+            else                                                                                          \
+                hipLaunchKernelGGL((gemm_i8_k<NBV, PMG_EPI_BIAS, _Float16>), grid, dim3(256), 0, s, g);   \
+        } else if (epi == PMG_EPI_Q) {                                                                    \
+            hipLaunchKernelGGL((gemm_i8_k<NBV, PMG_EPI_Q>), grid, dim3(256), 0, s, g);                    \
+        } else {                                                                                          \
+            hipLaunchKernelGGL((gemm_i8_k<NBV, PMG_EPI_BIAS>), grid, dim3(256), 0, s, g);                 \
+        }                                                                                                 \
     }
     PMG_GEMM_CASE(4)
     PMG_GEMM_CASE(2)
@@ -537,25 +598,44 @@ static int launch_gemm(const GemmArgs& g, int epi, hipStream_t s) {
         case 128: { constexpr int CC = 128; BODY; break; }                                     \
         case 192: { constexpr int CC = 192; BODY; break; }                                     \
         case 256: { constexpr int CC = 256; BODY; break; }                                     \
+        case 512: { constexpr int CC = 512; BODY; break; }                                     \
         default: return fail(PMG_E_INVALID, "unsupported level width " + std::to_string(C));   \
     }
 
-static bool unet_width(int C) {
-    return C == 16 || C == 32 || C == 48 || C == 64 || C == 96 || C == 128 || C == 192 || C == 256;
+// Level widths: int8 16 .. 256 (the deployed refiners); the fp16 teacher also 512 (the stock refiner's deepest
+// level, train.py:124), on the generic convolution. Level 0: the map-free convolutions' widths.
+static bool unet_width(int C, int prec) {
+    return C == 16 || C == 32 || C == 48 || C == 64 || C == 96 || C == 128 || C == 192 || C == 256 ||
+           (prec == PMG_PREC_FP16 && C == 512);
 }
-static bool col_width(int C) { return C == 16 || C == 32 || C == 48 || C == 64 || C == 128; }
+static bool col_width(int C, int prec) {
+    return C == 16 || C == 32 || C == 48 || C == 64 || (prec == PMG_PREC_INT8 && C == 128);
+}
 
 static int launch_rows_ln(bool up, int C, const float* x, const int32_t* parent, const float* skip,
                           const int64_t* count, int64_t cap, const float* gamma, const float* beta, float mult,
-                          float* y_out, int8_t* codes, hipStream_t s) {
+                          float* y_out, void* codes, bool f16, hipStream_t s) {
     if (cap == 0) return PMG_OK;
     const dim3 grid(row_grid(cap * 4));  // 64 rows (256 threads) per block, grid-stride
-    if (up) {
-        PMG_LN_SWITCH(C, hipLaunchKernelGGL((rows_ln_k<CC, true>), grid, dim3(256), 0, s, x, parent, skip, count,
-                                            gamma, beta, 1e-6f, mult, y_out, codes));
+    if (f16) {
+        _Float16* c16 = (_Float16*)codes;
+        if (up) {
+            PMG_LN_SWITCH(C, hipLaunchKernelGGL((rows_ln_k<CC, true, _Float16>), grid, dim3(256), 0, s, x, parent,
+                                                skip, count, gamma, beta, 1e-6f, mult, y_out, c16));
+        } else {
+            PMG_LN_SWITCH(C, hipLaunchKernelGGL((rows_ln_k<CC, false, _Float16>), grid, dim3(256), 0, s, x, parent,
+                                                skip, count, gamma, beta, 1e-6f, mult, y_out, c16));
+        }
     } else {
-        PMG_LN_SWITCH(C, hipLaunchKernelGGL((rows_ln_k<CC, false>), grid, dim3(256), 0, s, x, parent, skip, count,
-                                            gamma, beta, 1e-6f, mult, y_out, codes));
+        int8_t* c8 = (int8_t*)codes;
+        if (C > 256) return fail(PMG_E_INVALID, "int8 level widths end at 256");
+        if (up) {
+            PMG_LN_SWITCH(C, hipLaunchKernelGGL((rows_ln_k<CC, true, int8_t>), grid, dim3(256), 0, s, x, parent,
+                                                skip, count, gamma, beta, 1e-6f, mult, y_out, c8));
+        } else {
+            PMG_LN_SWITCH(C, hipLaunchKernelGGL((rows_ln_k<CC, false, int8_t>), grid, dim3(256), 0, s, x, parent,
+                                                skip, count, gamma, beta, 1e-6f, mult, y_out, c8));
+        }
     }
     return check_launch("rows_ln_k");
 }
@@ -593,12 +673,13 @@ struct pmg_unet {
     int32_t* scan_cnt = nullptr;        // [max ncols]
     int32_t* scan_excl = nullptr;       // [max ncols]
     int32_t* scan_tiles = nullptr;      // [max ncols / kScanTile + 1]
-    int8_t* q1 = nullptr;               // [cap][Cmax]
-    int8_t* q2 = nullptr;
-    int8_t* codes = nullptr;            // linear inputs [cap][max(2 C_L, Cmax)]
-    int8_t* codes2 = nullptr;           // fuse_proj.2 input [cap][C_L]
+    // activations entering a convolution or a linear: int8 codes, or fp16 (the teacher)
+    void* q1 = nullptr;                 // [cap][Cmax]
+    void* q2 = nullptr;
+    void* codes = nullptr;              // linear inputs [cap][max(2 C_L, Cmax)]
+    void* codes2 = nullptr;             // fuse_proj.2 input [cap][C_L]
     float* lin = nullptr;               // NearestUp linear output [cap][Cmax]
-    int8_t* enc_codes = nullptr;        // [T][enc_channels]
+    void* enc_codes = nullptr;          // [T][enc_channels]
     float* enc_tok = nullptr;           // [T][C_L]
     int32_t* part = nullptr;            // tap-split partial sums of the coarsest level's convolutions
     int64_t part_bytes = 0;
@@ -647,6 +728,8 @@ struct UnetOut {
 static int enqueue_block(pmg_unet* u, int k, const pmg_block_weights& bk, const pmg_block_weights* next, float* x,
                          const UnetOut* rout, hipStream_t s) {
     const int C = u->cfg.channels[k];
+    const bool f16 = u->cfg.precision == PMG_PREC_FP16;
+    const int prec = f16 ? PMG_PREC_FP16 : PMG_PREC_INT8;
     if (k == 0) {
         ColConvArgs a1{};
         a1.x = u->q1;
@@ -660,7 +743,7 @@ static int enqueue_block(pmg_unet* u, int k, const pmg_block_weights& bk, const 
         a1.bias = bk.b1;
         a1.out_mult = bk.q2_mult;
         a1.out = u->q2;
-        if (int e = launch_conv_col(PMG_PREC_INT8, a1, C, PMG_EPI_Q, s)) return e;
+        if (int e = launch_conv_col(prec, a1, C, PMG_EPI_Q, s)) return e;
         ColConvArgs a2{};
         a2.x = u->q2;
         a2.zq = u->zq0;
@@ -679,7 +762,7 @@ static int enqueue_block(pmg_unet* u, int k, const pmg_block_weights& bk, const 
             a2.ln_eps = 1e-6f;
             a2.next_mult = next->q1_mult;
             a2.next_q = u->q1;
-            return launch_conv_col(PMG_PREC_INT8, a2, C, PMG_EPI_RLN, s);
+            return launch_conv_col(prec, a2, C, PMG_EPI_RLN, s);
         }
         if (rout) {
             a2.out_w = u->out_w;
@@ -696,12 +779,12 @@ static int enqueue_block(pmg_unet* u, int k, const pmg_block_weights& bk, const 
                 a2.gate_floor = rout->gate_floor;
                 a2.gate_scale = rout->gate_scale;
             }
-            return launch_conv_col(PMG_PREC_INT8, a2, C, PMG_EPI_ROUT, s);
+            return launch_conv_col(prec, a2, C, PMG_EPI_ROUT, s);
         }
-        return launch_conv_col(PMG_PREC_INT8, a2, C, PMG_EPI_R, s);
+        return launch_conv_col(prec, a2, C, PMG_EPI_R, s);
     }
     DevConv c1{};
-    c1.x = u->q1;
+    c1.x = (const int8_t*)u->q1;
     c1.nmap_t = u->nmap_t[k];
     c1.tile_mask = u->tmask[k];
     c1.cap = u->cap;
@@ -709,7 +792,7 @@ static int enqueue_block(pmg_unet* u, int k, const pmg_block_weights& bk, const 
     c1.Ci = C;
     c1.Co = C;
     c1.w = (const int8_t*)bk.w1;
-    c1.epilogue = PMG_EPI_Q;
+    c1.epilogue = f16 ? PMG_EPI_SILU : PMG_EPI_Q;
     c1.a_scale = bk.a1_scale;
     c1.w_scale = bk.w1_scale;
     c1.bias = bk.b1;
@@ -717,13 +800,14 @@ static int enqueue_block(pmg_unet* u, int k, const pmg_block_weights& bk, const 
     c1.out = u->q2;
     // the tap split (a second launch) only at the coarsest level: the capacity does not bound a level's rows, and
     // at the finer levels, with too many rows to split, that launch would only cost its dispatch
-    if (k == u->L - 1 && k > 0) {
+    if (k == u->L - 1 && k > 0 && !f16) {
         c1.part = u->part;
         c1.part_bytes = u->part_bytes;
     }
-    if (int e = launch_conv_i8_dev(c1, s)) return e;
+    auto conv = [&](const DevConv& d) { return f16 ? launch_conv_f16_dev(d, s) : launch_conv_i8_dev(d, s); };
+    if (int e = conv(c1)) return e;
     DevConv c2 = c1;
-    c2.x = u->q2;
+    c2.x = (const int8_t*)u->q2;
     c2.w = (const int8_t*)bk.w2;
     c2.epilogue = PMG_EPI_R;
     c2.a_scale = bk.a2_scale;
@@ -731,10 +815,10 @@ static int enqueue_block(pmg_unet* u, int k, const pmg_block_weights& bk, const 
     c2.bias = bk.b2;
     c2.skip = x;
     c2.out = x;
-    if (int e = launch_conv_i8_dev(c2, s)) return e;
+    if (int e = conv(c2)) return e;
     if (next)
         return launch_rows_ln(false, C, x, nullptr, nullptr, u->counts + k, u->cap, next->ln_gamma, next->ln_beta,
-                              next->q1_mult, nullptr, u->q1, s);
+                              next->q1_mult, nullptr, u->q1, f16, s);
     return PMG_OK;
 }
 
@@ -750,15 +834,15 @@ static int enqueue_stage(pmg_unet* u, int k, const std::vector<pmg_block_weights
 
 static int ln_codes(pmg_unet* u, int k, const float* x, const pmg_block_weights& b, hipStream_t s) {
     return launch_rows_ln(false, u->cfg.channels[k], x, nullptr, nullptr, u->counts + k, u->cap, b.ln_gamma,
-                          b.ln_beta, b.q1_mult, nullptr, u->q1, s);
+                          b.ln_beta, b.q1_mult, nullptr, u->q1, u->cfg.precision == PMG_PREC_FP16, s);
 }
 
-static int linear(pmg_unet* u, const int8_t* a, const int64_t* rows_dev, int64_t rows_cap, int K,
+static int linear(pmg_unet* u, const void* a, const int64_t* rows_dev, int64_t rows_cap, int K,
                   const pmg_linear_weights& lw, int N, int epi, float out_mult, void* out, const float* planar,
                   hipStream_t s) {
     GemmArgs g{a, lw.w, rows_cap, rows_dev, K, N, lw.a_scale, lw.w_scale, lw.bias, out_mult, out, planar,
                (int64_t)u->R * u->Cc};
-    return launch_gemm(g, epi, s);
+    return launch_gemm(g, epi, u->cfg.precision == PMG_PREC_FP16, s);
 }
 
 // The level structure (levels 1 .. L-1) from the level-0 coordinates.
@@ -854,7 +938,8 @@ static int enqueue_unet(pmg_unet* u, const float* feats, const int32_t* coords, 
     }
     in.zkeys = zkeys;
     in.zkey_stride = 4;
-    if (int e = launch_input_stage(in, false, s)) return e;
+    const bool f16 = c.precision == PMG_PREC_FP16;
+    if (int e = launch_input_stage(in, f16, s)) return e;
     if (int e = enqueue_structure(u, s)) return e;
 
     // down stages and PoolDown (sparse_unet.py:223-231; flex_sparse_blocks.py:85-90)
@@ -863,8 +948,12 @@ static int enqueue_unet(pmg_unet* u, const float* feats, const int32_t* coords, 
         if (k + 1 == L) break;
         const int Ck = c.channels[k], Cn = c.channels[k + 1];
         PoolGeom g{u->coords[k], u->off[k], c.B, u->Hk[k], u->Wk[k], u->Hk[k + 1], u->Wk[k + 1]};
-        hipLaunchKernelGGL(pool_quant_k, dim3(row_grid(cap * (Ck / 4))), dim3(256), 0, s, u->xd[k], Ck, g,
-                           u->coords[k + 1], u->counts + k + 1, u->pool[k].q_mult, u->codes);
+        if (f16)
+            hipLaunchKernelGGL(pool_quant_k<_Float16>, dim3(row_grid(cap * (Ck / 4))), dim3(256), 0, s, u->xd[k], Ck,
+                               g, u->coords[k + 1], u->counts + k + 1, 1.0f, (_Float16*)u->codes);
+        else
+            hipLaunchKernelGGL(pool_quant_k<int8_t>, dim3(row_grid(cap * (Ck / 4))), dim3(256), 0, s, u->xd[k], Ck,
+                               g, u->coords[k + 1], u->counts + k + 1, u->pool[k].q_mult, (int8_t*)u->codes);
         if (int e = check_launch("pool_quant_k")) return e;
         if (int e = linear(u, u->codes, u->counts + k + 1, cap, Ck, u->pool[k], Cn, PMG_EPI_BIAS, 0.0f, u->xd[k + 1],
                            nullptr, s))
@@ -878,14 +967,24 @@ static int enqueue_unet(pmg_unet* u, const float* feats, const int32_t* coords, 
     {
         const dim3 grid((unsigned)(((int64_t)u->R * u->Cc + 63) / 64), (unsigned)((c.enc_channels + 63) / 64),
                         (unsigned)c.B);
-        hipLaunchKernelGGL(enc_quant_k, grid, dim3(256), 0, s, enc_feat, c.enc_channels, (int64_t)u->R * u->Cc,
-                           u->enc.q_mult, u->enc_codes);
+        if (f16)
+            hipLaunchKernelGGL(enc_quant_k<_Float16>, grid, dim3(256), 0, s, enc_feat, c.enc_channels,
+                               (int64_t)u->R * u->Cc, 1.0f, (_Float16*)u->enc_codes);
+        else
+            hipLaunchKernelGGL(enc_quant_k<int8_t>, grid, dim3(256), 0, s, enc_feat, c.enc_channels,
+                               (int64_t)u->R * u->Cc, u->enc.q_mult, (int8_t*)u->enc_codes);
         if (int e = check_launch("enc_quant_k")) return e;
         if (int e = linear(u, u->enc_codes, nullptr, u->T, c.enc_channels, u->enc, CL, PMG_EPI_BIAS, 0.0f,
                            u->enc_tok, enc_bias, s))
             return e;
-        hipLaunchKernelGGL(concat_quant_k, dim3(row_grid(cap * (CL / 2))), dim3(256), 0, s, u->xd[top],
-                           u->enc_tok, u->coords[top], u->counts + top, CL, u->R, u->Cc, u->fuse0.q_mult, u->codes);
+        if (f16)
+            hipLaunchKernelGGL(concat_quant_k<_Float16>, dim3(row_grid(cap * (CL / 2))), dim3(256), 0, s,
+                               u->xd[top], u->enc_tok, u->coords[top], u->counts + top, CL, u->R, u->Cc, 1.0f,
+                               (_Float16*)u->codes);
+        else
+            hipLaunchKernelGGL(concat_quant_k<int8_t>, dim3(row_grid(cap * (CL / 2))), dim3(256), 0, s,
+                               u->xd[top], u->enc_tok, u->coords[top], u->counts + top, CL, u->R, u->Cc,
+                               u->fuse0.q_mult, (int8_t*)u->codes);
         if (int e = check_launch("concat_quant_k")) return e;
         if (int e = linear(u, u->codes, u->counts + top, cap, 2 * CL, u->fuse0, CL, PMG_EPI_Q, u->fuse2.q_mult,
                            u->codes2, nullptr, s))
@@ -904,8 +1003,12 @@ static int enqueue_unet(pmg_unet* u, const float* feats, const int32_t* coords, 
     for (int i = 0; i + 1 < L; ++i) {
         const int t = L - 2 - i;
         const int Cs = c.channels[t + 1], Ct = c.channels[t];
-        hipLaunchKernelGGL(quant_rows_k, dim3(row_grid(cap * Cs / 4)), dim3(256), 0, s, cur, Cs,
-                           u->counts + t + 1, u->up[i].q_mult, u->codes);
+        if (f16)
+            hipLaunchKernelGGL(quant_rows_k<_Float16>, dim3(row_grid(cap * Cs / 4)), dim3(256), 0, s, cur, Cs,
+                               u->counts + t + 1, 1.0f, (_Float16*)u->codes);
+        else
+            hipLaunchKernelGGL(quant_rows_k<int8_t>, dim3(row_grid(cap * Cs / 4)), dim3(256), 0, s, cur, Cs,
+                               u->counts + t + 1, u->up[i].q_mult, (int8_t*)u->codes);
         if (int e = check_launch("quant_rows_k")) return e;
         if (int e = linear(u, u->codes, u->counts + t + 1, cap, Cs, u->up[i], Ct, PMG_EPI_BIAS, 0.0f, u->lin,
                            nullptr, s))
@@ -913,7 +1016,7 @@ static int enqueue_unet(pmg_unet* u, const float* feats, const int32_t* coords, 
         const pmg_block_weights* fb = !u->dec[i].empty() ? &u->dec[i][0] : nullptr;
         if (int e = launch_rows_ln(true, Ct, u->lin, u->parent[t], u->xd[t], u->counts + t, cap,
                                    fb ? fb->ln_gamma : nullptr, fb ? fb->ln_beta : nullptr, fb ? fb->q1_mult : 1.0f,
-                                   u->xu[t], u->q1, s))
+                                   u->xu[t], u->q1, f16, s))
             return e;
         if (int e = enqueue_stage(u, t, u->dec[i], u->xu[t], t == 0 ? &rout : nullptr, s)) return e;
         cur = u->xu[t];
@@ -1021,15 +1124,20 @@ pmg_unet* pmg_unet_create(const pmg_unet_config* cfg) {
     if (L < 2 || L > kMaxLevels) why = "levels must be in [2, 8] (sparse_unet.py:52)";
     else if (c.B < 1 || c.H < 1 || c.W < 1 || (int64_t)c.B * c.H * c.W > INT_MAX / 32)
         why = "bad point-map size";
+    else if (c.precision != PMG_PREC_INT8 && c.precision != PMG_PREC_FP16) why = "precision must be int8 or fp16";
     else if (c.enc_channels < 16 || c.enc_channels % 16 != 0) why = "enc_channels must be a positive multiple of 16";
     else if (c.bottleneck_blocks < 0) why = "bottleneck_blocks must be >= 0";
     else {
         const int ds = 1 << (L - 1);
         if (c.H % ds != 0 || c.W % ds != 0)
             why = "H and W must be multiples of the encoder downsampling 2^(levels-1) (sparse_unet.py:187)";
-        if (!col_width(c.channels[0])) why = "level-0 width must be 16, 32, 48, 64 or 128";
+        if (!col_width(c.channels[0], c.precision))
+            why = c.precision == PMG_PREC_FP16 ? "fp16 level-0 width must be 16, 32, 48 or 64"
+                                               : "level-0 width must be 16, 32, 48, 64 or 128";
         for (int k = 0; k < L && why.empty(); ++k) {
-            if (!unet_width(c.channels[k])) why = "level widths must be 16, 32, 48, 64, 96, 128, 192 or 256";
+            if (!unet_width(c.channels[k], c.precision))
+                why = c.precision == PMG_PREC_FP16 ? "fp16 level widths must be 16, 32, 48, 64, 96, 128, 192, 256 or 512"
+                                                   : "level widths must be 16, 32, 48, 64, 96, 128, 192 or 256";
             if (c.enc_blocks[k] < 0 || c.enc_blocks[k] > 16) why = "enc_blocks must be in [0, 16]";
             if (k + 1 < L && (c.dec_blocks[k] < 0 || c.dec_blocks[k] > 16)) why = "dec_blocks must be in [0, 16]";
         }
@@ -1085,14 +1193,15 @@ pmg_unet* pmg_unet_create(const pmg_unet_config* cfg) {
     take((void**)&u->scan_cnt, 4 * maxcols);
     take((void**)&u->scan_excl, 4 * maxcols);
     take((void**)&u->scan_tiles, 4 * (maxcols / kScanTile + 2));
-    take((void**)&u->q1, (size_t)cap * u->Cmax);
-    take((void**)&u->q2, (size_t)cap * u->Cmax);
-    take((void**)&u->codes, (size_t)cap * (2 * CL > u->Cmax ? 2 * CL : u->Cmax));
-    take((void**)&u->codes2, (size_t)cap * CL);
+    const size_t elt = c.precision == PMG_PREC_FP16 ? 2 : 1;
+    take((void**)&u->q1, elt * cap * u->Cmax);
+    take((void**)&u->q2, elt * cap * u->Cmax);
+    take((void**)&u->codes, elt * cap * (2 * CL > u->Cmax ? 2 * CL : u->Cmax));
+    take((void**)&u->codes2, elt * cap * CL);
     take((void**)&u->lin, (size_t)4 * cap * u->Cmax);
-    take((void**)&u->enc_codes, (size_t)u->T * c.enc_channels);
+    take((void**)&u->enc_codes, elt * u->T * c.enc_channels);
     take((void**)&u->enc_tok, (size_t)4 * u->T * CL);
-    if (L > 1) u->part_bytes = conv_split_bytes(c.channels[L - 1]);
+    if (L > 1 && c.precision != PMG_PREC_FP16) u->part_bytes = conv_split_bytes(c.channels[L - 1]);
     if (u->part_bytes > 0) take((void**)&u->part, (size_t)u->part_bytes);
     for (auto& p : plan) off += ualign(p.second);
     u->arena_bytes = off;
@@ -1146,18 +1255,19 @@ int pmg_unet_set_weights(pmg_unet* u, const pmg_unet_weights* w) {
                                                                  std::to_string(2 * (L - 1) + 3));
     PMG_REQUIRE(w->in_w && w->in_b && w->out_w && w->out_b, "missing projection weights");
     PMG_REQUIRE((w->pr_w == nullptr) == (w->pr_b == nullptr), "prompt_proj needs weight and bias");
+    const bool i8 = c.precision == PMG_PREC_INT8;
     for (int i = 0; i < nb; ++i) {
         const pmg_block_weights& b = w->blocks[i];
-        PMG_REQUIRE(b.ln_gamma && b.ln_beta && b.w1 && b.b1 && b.w2 && b.b2 && b.w1_scale && b.w2_scale,
+        PMG_REQUIRE(b.ln_gamma && b.ln_beta && b.w1 && b.b1 && b.w2 && b.b2 && (!i8 || (b.w1_scale && b.w2_scale)),
                     "missing block weights");
         PMG_REQUIRE(aligned16(b.w1) && aligned16(b.w2), "conv weights must be 16-byte aligned");
-        PMG_REQUIRE(b.a1_scale > 0.0f && b.a2_scale > 0.0f && b.q1_mult > 0.0f && b.q2_mult > 0.0f,
+        PMG_REQUIRE(!i8 || (b.a1_scale > 0.0f && b.a2_scale > 0.0f && b.q1_mult > 0.0f && b.q2_mult > 0.0f),
                     "int8 blocks need positive activation scales");
     }
     for (int i = 0; i < w->n_linears; ++i) {
         const pmg_linear_weights& l = w->linears[i];
-        PMG_REQUIRE(l.w && l.w_scale && l.bias && aligned16(l.w), "missing or misaligned linear weights");
-        PMG_REQUIRE(l.a_scale > 0.0f && l.q_mult > 0.0f, "linears need positive activation scales");
+        PMG_REQUIRE(l.w && (!i8 || l.w_scale) && l.bias && aligned16(l.w), "missing or misaligned linear weights");
+        PMG_REQUIRE(!i8 || (l.a_scale > 0.0f && l.q_mult > 0.0f), "linears need positive activation scales");
     }
     u->in_w = w->in_w;
     u->in_b = w->in_b;

@@ -1,4 +1,4 @@
-"""The multi-level int8 refiner on the GPU, behind Sparse3DUNet.forward's signature.
+"""The multi-level refiner on the GPU (int8, or the fp16 teacher), behind Sparse3DUNet.forward's signature.
 
 `UNetRefiner` is an nn.Module with the forward of Sparse3DUNet (moge/model/modules/sparse_unet.py:176-258),
 `forward(feats, coords, shape, encoder_feature, prompt_feats=None, encoder_bias_map=None) -> (M, 1)`, the call
@@ -14,7 +14,9 @@ captured graph on the device (`pmg_unet_step`), with no host round trip between 
 Weights come from a Sparse3DUNet state dict (plain or QAT), from the Metal engine's refiner.bin / refiner.json
 export, or from promptmoge_amd.unet_weights.make_unet_weights; the arithmetic is the deployed int8 contract
 (qat.py:1-16): per-output-channel int8 weights, per-tensor int8 activations with the layer's clip, int32
-accumulation. Inference only.
+accumulation -- or, with precision="fp16", the teacher's (PromptMoGe-L, e.g. the stock 32 64 128 256 512 refiner,
+train.py:124): fp16 activations and weights in every convolution and linear, fp32 accumulation, fp32 residual
+streams, LayerNorm and SiLU in fp32. Inference only.
 """
 from __future__ import annotations
 
@@ -32,9 +34,10 @@ from .unet_weights import UNetW, load_refiner_bin, quantized, unet_from_state_di
 
 class UNetDeviceWeights:
     """A UNetW on the GPU in the layouts the kernels read: conv weights int8 (Co, 3, 3, 3, Ci), linear weights int8
-    (N, K), per-output-channel fp32 scales, fp32 biases / LayerNorm affine, activation scales from the clips."""
+    (N, K), per-output-channel fp32 scales, fp32 biases / LayerNorm affine, activation scales from the clips; with
+    precision "fp16" (the teacher) the conv and linear weights in fp16 and no scales or clips."""
 
-    def __init__(self, w: UNetW, device):
+    def __init__(self, w: UNetW, device, precision: str = "int8"):
         t = lambda a, dt=torch.float32: torch.as_tensor(np.ascontiguousarray(a)).to(device=device, dtype=dt)
         self.keep = []
 
@@ -49,7 +52,13 @@ class UNetDeviceWeights:
         self.out_w, self.out_b = dev(np.asarray(w.out_w).reshape(-1)), dev(np.asarray(w.out_b).reshape(-1))
         blocks = [b for st in w.down for b in st] + list(w.bott) + [b for st in w.dec for b in st]
         self._blocks = (BlockWeights * max(len(blocks), 1))()
+        f16 = precision == "fp16"
+        h = lambda a: dev(np.asarray(a, np.float32), torch.float16)
         for k, b in enumerate(blocks):
+            if f16:
+                self._blocks[k] = BlockWeights(dev(b.gamma), dev(b.beta), h(b.w1), None, dev(b.b1), 1.0, 1.0, h(b.w2),
+                                               None, dev(b.b2), 1.0, 1.0)
+                continue
             q1, s1 = quantized(b.w1)
             q2, s2 = quantized(b.w2)
             self._blocks[k] = BlockWeights(
@@ -59,6 +68,9 @@ class UNetDeviceWeights:
         linears = list(w.pool) + [w.enc, w.fuse0, w.fuse2] + list(w.up)
         self._linears = (LinearWeights * len(linears))()
         for k, l in enumerate(linears):
+            if f16:
+                self._linears[k] = LinearWeights(h(l.w), None, dev(l.b), 1.0, 1.0)
+                continue
             q, s = quantized(l.w)
             self._linears[k] = LinearWeights(dev(q, torch.int8), dev(s), dev(l.b), float(act_scale(l.clip)),
                                              float(act_mult(l.clip)))
@@ -68,19 +80,29 @@ class UNetDeviceWeights:
 
 
 class UNetRefiner(torch.nn.Module):
-    """Sparse3DUNet on the GPU in the deployed int8 arithmetic (see the module docstring)."""
+    """Sparse3DUNet on the GPU in the deployed int8 arithmetic, or (precision="fp16") in the teacher's half
+    precision (see the module docstring)."""
 
     def __init__(self, weights: UNetW, *, depth_resolution: float = 256.0, use_graph: bool = True,
-                 check_coords: bool = True):
+                 check_coords: bool = True, precision: str = "int8"):
         super().__init__()
         if any(f != 2 for f in weights.factors):
             raise ValueError("downsample factors other than 2 are not supported (MoGe's refiners use 2)")
-        wide = [c for c in weights.channels if c not in (16, 32, 48, 64, 96, 128, 192, 256)]
-        if wide or weights.channels[0] not in (16, 32, 48, 64, 128):
-            # the deployed int8 refiners are the narrowed 32 64 128 256 256 (train.py:124); the stock 512-wide
-            # refiner is the fp16 teacher, which runs through the flex_gemm shim
-            raise ValueError(f"UNetRefiner (int8) takes level widths 16, 32, 48, 64, 96, 128, 192, 256 (level 0: 16, "
-                             f"32, 48, 64, 128); got {weights.channels}")
+        if precision not in ("int8", "fp16"):
+            raise ValueError("precision must be 'int8' or 'fp16'")
+        if precision == "int8":
+            wide = [c for c in weights.channels if c not in (16, 32, 48, 64, 96, 128, 192, 256)]
+            if wide or weights.channels[0] not in (16, 32, 48, 64, 128):
+                # the deployed int8 refiners are the narrowed 32 64 128 256 256 (train.py:124); the stock 512-wide
+                # refiner is the teacher, which runs in fp16 (precision="fp16")
+                raise ValueError(f"UNetRefiner (int8) takes level widths 16, 32, 48, 64, 96, 128, 192, 256 (level 0: "
+                                 f"16, 32, 48, 64, 128); got {weights.channels}")
+        else:
+            wide = [c for c in weights.channels if c not in (16, 32, 48, 64, 96, 128, 192, 256, 512)]
+            if wide or weights.channels[0] not in (16, 32, 48, 64):
+                raise ValueError(f"UNetRefiner (fp16) takes level widths 16, 32, 48, 64, 96, 128, 192, 256, 512 "
+                                 f"(level 0: 16, 32, 48, 64); got {weights.channels}")
+        self.precision = precision
         self.host_weights = weights
         self.depth_resolution = float(depth_resolution)
         self.use_graph = use_graph
@@ -106,7 +128,8 @@ class UNetRefiner(torch.nn.Module):
         L = w.levels
         pad = lambda xs: (_lib.i32 * 8)(*(list(xs) + [0] * (8 - len(xs))))
         return UNetConfig(B, H, W, L, pad(w.channels), pad([len(s) for s in w.down]), pad([len(s) for s in w.dec]),
-                          len(w.bott), int(w.enc_channels), self.depth_resolution, int(self.use_graph))
+                          len(w.bott), int(w.enc_channels), self.depth_resolution, int(self.use_graph),
+                          _lib.PREC_FP16 if self.precision == "fp16" else _lib.PREC_INT8)
 
     def _handle(self, device: torch.device, B: int, H: int, W: int):
         key = (device.index, B, H, W)
@@ -114,7 +137,7 @@ class UNetRefiner(torch.nn.Module):
         if h is None:
             dw = self._weights.get(device.index)
             if dw is None:
-                dw = self._weights[device.index] = UNetDeviceWeights(self.host_weights, device)
+                dw = self._weights[device.index] = UNetDeviceWeights(self.host_weights, device, self.precision)
             cfg = self._config(B, H, W)
             h = lib().pmg_unet_create(C.byref(cfg))
             if not h:
@@ -222,7 +245,8 @@ class UNetRefiner(torch.nn.Module):
 
 
 class UNetStep:
-    """One refine-loop step with the multi-level int8 refiner, fused on the GPU (pmg_unet_step).
+    """One refine-loop step with the multi-level refiner (int8, or the fp16 teacher), fused on the GPU
+    (pmg_unet_step).
 
     points [B, H, W, 3] fp32 (x/z, y/z, logz) is refined into `out` (default in place); lidar, conf [B, dh, dw];
     encoder_feature [B, C_enc, H/ds, W/ds] and encoder_bias_map [B, C_{L-1}, H/ds, W/ds] (or None) as for
@@ -235,11 +259,12 @@ class UNetStep:
     """
 
     def __init__(self, weights, B: int, H: int, W: int, dh: Optional[int] = None, dw: Optional[int] = None, *,
-                 depth_resolution: float = 256.0, fit_iters: int = 4, fit_trim: float = 0.2, fit_min_points: int = 32,
+                 depth_resolution: float = 256.0, precision: str = "int8", fit_iters: int = 4, fit_trim: float = 0.2, fit_min_points: int = 32,
                  use_prompt: bool = True, soft_gate: bool = False, output_gate: bool = False,
                  output_gate_floor: float = 0.1, anchor: float = 0.0, final_fit: bool = False,
                  post_depth: bool = False, use_graph: bool = True, device="cuda"):
-        mod = weights if isinstance(weights, UNetRefiner) else UNetRefiner(weights, depth_resolution=depth_resolution)
+        mod = weights if isinstance(weights, UNetRefiner) else UNetRefiner(weights, depth_resolution=depth_resolution,
+                                                                           precision=precision)
         w = mod.host_weights
         if post_depth and not final_fit:
             raise ValueError("post_depth needs final_fit")
@@ -255,11 +280,11 @@ class UNetStep:
         self.dh, self.dw = dh or H, dw or W
         self.use_prompt, self.final_fit, self.post_depth = use_prompt, final_fit, post_depth
         self.host_weights = w
-        self.weights = UNetDeviceWeights(w, self.device)
+        self.weights = UNetDeviceWeights(w, self.device, mod.precision)
         pad = lambda xs: (_lib.i32 * 8)(*(list(xs) + [0] * (8 - len(xs))))
         cfg = UNetConfig(B, H, W, w.levels, pad(w.channels), pad([len(st) for st in w.down]),
                          pad([len(st) for st in w.dec]), len(w.bott), int(w.enc_channels), float(mod.depth_resolution),
-                         int(use_graph))
+                         int(use_graph), _lib.PREC_FP16 if mod.precision == "fp16" else _lib.PREC_INT8)
         with torch.cuda.device(self.device):
             self.h = lib().pmg_unet_create(C.byref(cfg))
             if not self.h:

@@ -149,3 +149,72 @@ def test_unet_from_refiner_bin(gpu, tmp_path):
               prompt_feats=_t(pf, gpu), encoder_bias_map=_t(bmap, gpu))
     ref = ou.forward(pts.reshape(M, 3), levels, w2, enc, pf, bmap, mode="int8")
     assert np.array_equal(out.cpu().numpy()[:, 0], ref)
+
+
+# ---- the fp16 teacher (PromptMoGe-L): oracle/blocks.py "fp16" arithmetic ------------------------------------------
+F16_CASES = {
+    # name: (channels, enc_blocks, dec_blocks, bottleneck, B, H, W, enc_channels, seed)
+    "teacher5_small": ([32, 64, 128, 256, 512], [1, 1, 1, 1, 1], [1, 1, 1, 1], 1, 1, 64, 96, 64, 5),
+    "teacher5_240x320": ([32, 64, 128, 256, 512], [1, 1, 1, 1, 1], [1, 1, 1, 1], 1, 1, 240, 320, 256, 5),
+    "f16_3lv_b2": ([16, 32, 64], [1, 2, 1], [2, 1], 1, 2, 32, 48, 32, 3),
+}
+
+
+def _rms(a):
+    return float(np.sqrt(np.mean(np.square(np.asarray(a, np.float64)))))
+
+
+@pytest.mark.parametrize("name", list(F16_CASES))
+def test_unet_fp16_matches_oracle(gpu, name):
+    """The stock 512-wide teacher U-Net (train.py:124) natively in fp16, against oracle/unet.py's "fp16" arithmetic
+    (fp16 activations and weights in every conv and linear, fp32 accumulation, fp32 streams). The level structure is
+    bit for bit. The values cannot be: the device sums in its MFMA order, and a different fp32 summation order moves
+    fp16 roundings by one ulp, which the next LayerNorm and the wide coarse layers amplify (on these weights the
+    oracle summed in fp32 instead of fp64 lands 1e-3 RMS away from itself at the output). So:
+      * level 0's stream, before much amplification, within 1e-5 RMS of the oracle -- a tenth of what rounding to
+        fp16 changes there (the fp32 module) -- so the device computes the teacher's fp16 arithmetic;
+      * every level's stream and the (M, 1) output within three times that summation-order spread (RMS) of the
+        oracle, and four times it at the worst element: the device differs from the oracle in two independent ways
+        of that size -- its summation order, and its SiLU (hardware exp2 / reciprocal, within one fp16 ulp of the
+        oracle's before the rounding) -- where the fp32-summed oracle differs in one."""
+    announce(f"unet fp16 forward case={name}")
+    channels, eb, db, bb, B, H, W, enc_c, seed = F16_CASES[name]
+    L = len(channels)
+    ds = 2 ** (L - 1)
+    w = uw.make_unet_weights(channels, enc_c, enc_blocks=eb, dec_blocks=db, bottleneck_blocks=bb, seed=seed)
+    cfg = spec.StepConfig("u", H, W, 0.9 * W, 0.9 * W, W / 2, H / 2, channels[0], 1, "int8", seed=seed)
+    pts = np.stack([spec.make_scene(cfg, seed=seed + 11 * b).points for b in range(B)])
+    rng = np.random.default_rng(seed)
+    enc = rng.normal(0, 1, (B, enc_c, H // ds, W // ds)).astype(np.float32)
+    bias = rng.normal(0, 0.1, (B, channels[-1], H // ds, W // ds)).astype(np.float32)
+    M = B * H * W
+    pf = np.stack([rng.normal(0, 0.05, M), rng.uniform(0, 1, M)], 1).astype(np.float32)
+    zq, coords, zext, _ = ost.voxelize(pts)
+    levels = ou.build_levels(coords, (B, H, W, zext), w.factors, zkeys=zq)
+    mod = UNetRefiner(w, precision="fp16")
+    shape = torch.Size([B, H, W, zext, 3])
+    tf, tc, te, tb, tp = (_t(a, gpu) for a in (pts.reshape(M, 3), coords, enc, bias, pf))
+    out = mod(tf, tc, shape, te, prompt_feats=tp, encoder_bias_map=tb)
+    out2 = mod(tf, None, shape, te, prompt_feats=tp, encoder_bias_map=tb)  # keys from the depth, another graph
+    torch.cuda.synchronize()
+    counts = mod.buffer("counts", 0).cpu().numpy()
+    assert [int(c) for c in counts] == [lv.M for lv in levels]
+    for k in range(1, L):
+        assert np.array_equal(mod.buffer("coords", k).cpu().numpy()[:levels[k].M], levels[k].coords), k
+    assert np.array_equal(out.cpu().numpy(), out2.cpu().numpy())
+    tr, tr_alt, tr32 = {}, {}, {}
+    ref = ou.forward(pts.reshape(M, 3), levels, w, enc, pf, bias, mode="fp16", trace=tr)
+    alt = ou.forward(pts.reshape(M, 3), levels, w, enc, pf, bias, mode="fp16", trace=tr_alt, acc=np.float32)
+    ou.forward(pts.reshape(M, 3), levels, w, enc, pf, bias, mode="fp32", trace=tr32)
+    d0 = mod.buffer("down", 0).cpu().numpy()[:M]
+    r0 = tr["down0"]
+    assert _rms(d0 - r0) <= 1e-5 * _rms(r0) and _rms(d0 - r0) <= 0.1 * _rms(tr32["down0"] - r0), (
+        _rms(d0 - r0) / _rms(r0), _rms(tr32["down0"] - r0) / _rms(r0))
+    pairs = [(mod.buffer("down", k).cpu().numpy()[:levels[k].M], tr[f"down{k}"], tr_alt[f"down{k}"], f"down{k}")
+             for k in range(L)]
+    pairs.append((out.cpu().numpy()[:, 0], ref, alt, "out"))
+    for got, r, a, what in pairs:
+        spread, spread_max = _rms(a - r), float(np.abs(a - r).max())
+        err, err_max = _rms(got - r), float(np.abs(got - r).max())
+        assert err <= 3 * spread + 1e-6 * _rms(r) and err_max <= 4 * spread_max + 1e-6 * float(np.abs(r).max()), (
+            what, err / _rms(r), spread / _rms(r), err_max, spread_max)
