@@ -113,8 +113,10 @@ class UNetRefiner(torch.nn.Module):
 
     @classmethod
     def from_state_dict(cls, sd, factors: Optional[Sequence[int]] = None, clips=None, **kw) -> "UNetRefiner":
-        """From a Sparse3DUNet (QAT) state dict (unet_weights.unet_from_state_dict)."""
-        return cls(unet_from_state_dict(sd, factors, clips), **kw)
+        """From a Sparse3DUNet state dict (unet_weights.unet_from_state_dict): QAT, or plain with `clips`; with
+        precision="fp16" (the teacher) any plain state dict, no clips needed."""
+        f16 = kw.get("precision", "int8") == "fp16"
+        return cls(unet_from_state_dict(sd, factors, clips, require_clips=not f16), **kw)
 
     @classmethod
     def from_refiner_bin(cls, directory, **kw):

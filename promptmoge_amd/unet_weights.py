@@ -108,12 +108,13 @@ class UNetW:
 
 # ------------------------------------------------------------------------------------------------ state dict
 def unet_from_state_dict(sd, factors: Optional[Sequence[int]] = None,
-                         clips: Optional[Dict[str, float]] = None) -> UNetW:
+                         clips: Optional[Dict[str, float]] = None, require_clips: bool = True) -> UNetW:
     """A Sparse3DUNet's weights from its state dict, under the reference's parameter names (sparse_unet.py:81-150,
     flex_sparse_blocks.py:50-105). QAT checkpoints store masters under `.parametrizations.weight.original`
     (torch.nn.utils.parametrize, qat.py:111) and clips in `aq_<module path with '_'>.clip` (qat.py:112-115);
     `clips` ({module path: clip}) overrides them. A quantised layer (qat.py:118-138) with neither raises
-    ValueError naming it, so a plain (non-QAT) state dict needs `clips`. `factors` defaults to Sparse3DUNet's
+    ValueError naming it, so a plain (non-QAT) state dict needs `clips` -- unless `require_clips` is False (the
+    fp16 teacher, which quantises nothing: the missing clips are then NaN). `factors` defaults to Sparse3DUNet's
     [2] * (levels - 1)."""
     f32 = lambda t: np.asarray(t.detach().cpu().float().numpy() if hasattr(t, "detach") else t, dtype=F32)
 
@@ -135,6 +136,8 @@ def unet_from_state_dict(sd, factors: Optional[Sequence[int]] = None,
             return float(clips[path])
         key = "aq_" + path.replace(".", "_") + ".clip"
         if key not in sd:
+            if not require_clips:
+                return float("nan")
             # the int8 refiner needs every quantised layer's activation clip (export/refiner.py asserts that the
             # observer ran); a default would silently saturate that layer's input
             raise ValueError(f"{path}: quantised layer without an activation clip ({key} is not in the state dict "

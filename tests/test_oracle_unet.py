@@ -219,3 +219,15 @@ def test_unet_refiner_refuses_widths_beyond_256():
     w = uw.make_unet_weights([16, 32, 512], 32, seed=0)
     with pytest.raises(ValueError, match="level widths"):
         UNetRefiner(w)
+
+
+def test_teacher_state_dict_needs_no_clips():
+    """The fp16 teacher quantises nothing: its plain state dict loads without clips (they are left NaN), and the
+    int8 reader still refuses the same dict."""
+    from promptmoge_amd.unet import UNetRefiner
+
+    _, _, sd, _ = _golden_unet()
+    mod = UNetRefiner.from_state_dict(sd, factors=[2, 2], precision="fp16")
+    assert mod.precision == "fp16" and np.isnan(mod.host_weights.enc.clip)
+    with pytest.raises(ValueError, match="activation clip"):
+        UNetRefiner.from_state_dict(sd, factors=[2, 2])
