@@ -222,12 +222,11 @@ def test_unet_refiner_refuses_widths_beyond_256():
 
 
 def test_teacher_state_dict_needs_no_clips():
-    """The fp16 teacher quantises nothing: its plain state dict loads without clips (they are left NaN), and the
-    int8 reader still refuses the same dict."""
-    from promptmoge_amd.unet import UNetRefiner
-
+    """The fp16 teacher quantises nothing: its plain state dict loads without clips (they are left NaN; the
+    reference module's own golden state dict, whose 8-wide level 0 the device does not take, so the reader is
+    called directly), and the int8 reader still refuses the same dict."""
     _, _, sd, _ = _golden_unet()
-    mod = UNetRefiner.from_state_dict(sd, factors=[2, 2], precision="fp16")
-    assert mod.precision == "fp16" and np.isnan(mod.host_weights.enc.clip)
+    w = uw.unet_from_state_dict(sd, factors=[2, 2], require_clips=False)
+    assert w.channels == [8, 16, 16] and np.isnan(w.enc.clip) and np.isnan(w.down[0][0].clip1)
     with pytest.raises(ValueError, match="activation clip"):
-        UNetRefiner.from_state_dict(sd, factors=[2, 2])
+        uw.unet_from_state_dict(sd, factors=[2, 2])
