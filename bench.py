@@ -46,6 +46,12 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
 FP16_PEAK_TFLOPS = 2500.0
+# mask-sort window of the microbench's row order per width (0: the whole map). Measured on the 1M-voxel set: C = 64
+# (the resident-weight kernel, each wave walks its own taps) runs 0.110 ms at 2^18 rows against 0.123 ms at one
+# window (smaller windows keep its gathers in L2); C = 128 (the block walks its chunk's tap union between weight
+# staging barriers) runs 0.305 ms at one window against 0.324 ms at 2^18 and 0.37-0.39 ms at 2^14-2^15 (the union
+# of a 512-row chunk grows from 11.6 taps at one window to 16.0 at 2^16 and 19.7 at 2^14).
+ORDER_WINDOW = {64: 1 << 18, 128: 0}
 METRIC = "refiner step latency ms + active voxels/s at 480×640; int8 conv TOPS (% peak)"
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_modelA.txt")
 CALIB_BYTES = 64 << 20  # the calibration copy: 64 MiB read + 64 MiB written
@@ -274,18 +280,19 @@ def microbench(stream):
         ntu, tmu, nru, rmu = ops.nmap_hash(cd, shape, rows=True, row_mask=True)
         torch.cuda.synchronize()
         hash_ms = graph_ms(lambda: ops.nmap_hash(cd, shape, row_mask=True), 5, stream)
-        # the map's processing order (rows sorted by tap mask, the map permuted into it): built once per map, like
-        # the map itself, and read by every convolution on it
-        order, otm, nmo = ops.row_order(rmu, nru)
-        torch.cuda.synchronize()
-        order_ms = graph_ms(lambda: ops.row_order(rmu, nru), 5, stream)
         pu = int((ntu >= 0).sum().item())
         M = coords.shape[0]
         micro = {"voxels": int(M), "pairs": pu, "mean_active_taps": round(pu / M, 3), "hash_map_ms": round(hash_ms, 4),
-                 "hash_map_gbs": round((16 * M + 108 * M) / (hash_ms * 1e-3) / 1e9, 1),
-                 "row_order_ms": round(order_ms, 4)}
+                 "hash_map_gbs": round((16 * M + 108 * M) / (hash_ms * 1e-3) / 1e9, 1)}
         g = torch.Generator(device="cpu").manual_seed(5)
         for Cm in (64, 128):
+            # the map's processing order for this width (rows sorted by tap mask within windows of ORDER_WINDOW[Cm]
+            # rows, the map permuted into it): built once per map, like the map itself, and read by every
+            # convolution of that width on it; its build time is reported beside the convolution's
+            win = ORDER_WINDOW[Cm]
+            order, otm, nmo = ops.row_order(rmu, nru, window=win)
+            torch.cuda.synchronize()
+            order_ms = graph_ms(lambda: ops.row_order(rmu, nru, window=win), 5, stream)
             xm = torch.randint(-127, 128, (M, Cm), generator=g, dtype=torch.int8).to(dev)
             wm = torch.randint(-127, 128, (Cm, 3, 3, 3, Cm), generator=g, dtype=torch.int8).to(dev)
             sm = torch.full((Cm,), 1e-4, device=dev)
@@ -296,8 +303,15 @@ def microbench(stream):
                          5, stream)
             t_u = graph_ms(lambda: ops.spconv_i8(xm, ntu, tmu, wm, ops.EPI_QLIN, w_scale=sm, out=om), 5, stream)
             tops = 2 * Cm * Cm * pu / (t * 1e-3) / 1e12
+            gain = t_u - t
             micro[f"C{Cm}"] = {"ms": round(t, 4), "tops": round(tops, 2), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
-                               "ms_caller_order": round(t_u, 4)}
+                               "ms_caller_order": round(t_u, 4), "order_window": win or M,
+                               "row_order_ms": round(order_ms, 4),
+                               # one convolution on a fresh map, its order built first
+                               "ms_with_order_build": round(t + order_ms, 4),
+                               # convolutions of this width on one map that repay the order's build
+                               "order_break_even_convs": round(order_ms / gain, 1) if gain > 0 else None}
+            del order, otm, nmo
         # the same map through the flex_gemm shim's fp16 and bf16 paths (SubmanifoldConv3d on fp16 / bf16
         # features: fp16 / bf16 MFMA, fp32 accumulators, caller's row order)
         for name, dt, conv in (("fp16", torch.float16, ops.spconv_f16), ("bf16", torch.bfloat16, ops.spconv_bf16)):
