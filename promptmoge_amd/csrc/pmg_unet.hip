@@ -6,8 +6,9 @@
 // _core.py:339-395). Every level's voxels are in (b, i, j, z) order -- the order of _linearise on the pooled shape,
 // i.e. the reference's sorted unique output keys -- so a level is a set of columns (b, i, j), each holding its
 // voxels with increasing z: a column CSR. A coarse column merges the z / 2 lists of its (up to) four child columns:
-// one thread per coarse column counts the distinct values, a two-kernel scan places the columns, and the same
-// merge then writes the coarse voxels and each child's parent. The children of a coarse voxel in increasing row
+// one thread per coarse column counts the distinct values and scans them within its block of 256 columns, and the
+// same merge then writes the coarse voxels and each child's parent, each block starting after the totals of the
+// blocks before it. The children of a coarse voxel in increasing row
 // order are the matching runs of its child columns in raster order, the order of the reference's index_add_. This
 // is the per-column design of the reference's device engine (Structure.metal:87-215) without its host-side sizing:
 // the voxel count of every level stays on the device, buffers are allocated for the level-0 count (an upper bound
@@ -37,7 +38,6 @@
 
 namespace pmg {
 
-constexpr int kScanTile = 2048;  // columns per block of the column scan (256 threads x 8)
 constexpr int kMaxLevels = 8;
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -110,88 +110,59 @@ __device__ inline int merge_min(const int4* coords, const int32_t (&h)[4], const
     return mn;
 }
 
-__global__ __launch_bounds__(256) void pool_count_k(PoolGeom g, int64_t ncols, int32_t* __restrict__ cnt) {
-    const int64_t C = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (C >= ncols) return;
-    int32_t h[4], e[4];
-    child_ranges(g, C, h, e);
-    int n = 0;
-    for (;;) {
-        const int mn = merge_min(g.coords, h, e);
-        if (mn == INT_MAX) break;
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            while (h[q] < e[q] && (g.coords[h[q]].w >> 1) == mn) ++h[q];
-        ++n;
-    }
-    cnt[C] = n;
-}
-
-// Exclusive scan of cnt in tiles of kScanTile: excl[c] = sum of the tile's counts before c, tile_sum[t] = total.
-__global__ __launch_bounds__(256) void scan_tiles_k(const int32_t* __restrict__ cnt, int64_t n,
-                                                    int32_t* __restrict__ excl, int32_t* __restrict__ tile_sum) {
+// One thread per coarse column: its voxel count (the distinct z / 2 of its child columns), and the exclusive scan
+// of the counts within the block's 256 columns (excl) with the block's total (tile_sum).
+__global__ __launch_bounds__(256) void pool_count_k(PoolGeom g, int64_t ncols, int32_t* __restrict__ excl,
+                                                    int32_t* __restrict__ tile_sum) {
     __shared__ int32_t wsum[4];
-    const int64_t base = (int64_t)blockIdx.x * kScanTile + threadIdx.x * 8;
-    int32_t v[8], s = 0;
+    const int64_t C = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    int n = 0;
+    if (C < ncols) {
+        int32_t h[4], e[4];
+        child_ranges(g, C, h, e);
+        for (;;) {
+            const int mn = merge_min(g.coords, h, e);
+            if (mn == INT_MAX) break;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        v[k] = base + k < n ? cnt[base + k] : 0;
-        s += v[k];
+            for (int q = 0; q < 4; ++q)
+                while (h[q] < e[q] && (g.coords[h[q]].w >> 1) == mn) ++h[q];
+            ++n;
+        }
     }
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const uint32_t incl = wave_incl_scan_u32((uint32_t)s);
+    const uint32_t incl = wave_incl_scan_u32((uint32_t)n);
     if (lane == 63) wsum[w] = (int32_t)incl;
     __syncthreads();
     int32_t before = 0;
     for (int k = 0; k < w; ++k) before += wsum[k];
-    int32_t run = before + (int32_t)incl - s;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        if (base + k < n) excl[base + k] = run;
-        run += v[k];
-    }
+    if (C < ncols) excl[C] = before + (int32_t)incl - n;
     if (threadIdx.x == 255) tile_sum[blockIdx.x] = before + (int32_t)incl;
 }
 
-// One block: tile_sum -> exclusive tile offsets (in place); the grand total is the level's voxel count (count,
-// int64) and the end of its column CSR (off[ncols]).
-__global__ __launch_bounds__(1024) void scan_top_k(int32_t* __restrict__ tile_sum, int ntiles, int64_t* count,
-                                                   int32_t* off_end) {
-    __shared__ int32_t wsum[16];
-    const int per = (ntiles + 1023) / 1024;
-    const int b0 = threadIdx.x * per;
-    int32_t s = 0;
-    for (int k = 0; k < per; ++k)
-        if (b0 + k < ntiles) s += tile_sum[b0 + k];
+// Writes the coarse voxels of column C (coordinates and the column's CSR start) and the parent of every child. The
+// block's first row is the sum of the tile totals of the blocks before it (pool_count_k's tiling: 256 columns per
+// block); the last block also writes the level's voxel count and the end of its column CSR.
+__global__ __launch_bounds__(256) void pool_emit_k(PoolGeom g, int64_t ncols, const int32_t* __restrict__ excl,
+                                                   const int32_t* __restrict__ tile_sum, int64_t* __restrict__ count,
+                                                   int4* __restrict__ coords_c, int32_t* __restrict__ off_c,
+                                                   int32_t* __restrict__ parent) {
+    __shared__ int32_t wsum[4];
+    int32_t t = 0;
+    for (int64_t q = threadIdx.x; q < (int64_t)blockIdx.x; q += 256) t += tile_sum[q];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const uint32_t incl = wave_incl_scan_u32((uint32_t)s);
+    const uint32_t incl = wave_incl_scan_u32((uint32_t)t);
     if (lane == 63) wsum[w] = (int32_t)incl;
     __syncthreads();
-    int32_t before = 0;
-    for (int k = 0; k < w; ++k) before += wsum[k];
-    int32_t run = before + (int32_t)incl - s;
-    __syncthreads();
-    for (int k = 0; k < per; ++k)
-        if (b0 + k < ntiles) {
-            const int32_t t = tile_sum[b0 + k];
-            tile_sum[b0 + k] = run;
-            run += t;
-        }
-    if (threadIdx.x == 1023) {
-        const int32_t total = before + (int32_t)incl;
-        *count = total;
-        *off_end = total;
-    }
-}
-
-// Writes the coarse voxels of column C (coordinates and the column's CSR start) and the parent of every child.
-__global__ __launch_bounds__(256) void pool_emit_k(PoolGeom g, int64_t ncols, const int32_t* __restrict__ excl,
-                                                   const int32_t* __restrict__ tile_off, int4* __restrict__ coords_c,
-                                                   int32_t* __restrict__ off_c, int32_t* __restrict__ parent) {
+    const int32_t tile0 = wsum[0] + wsum[1] + wsum[2] + wsum[3];
     const int64_t C = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (C >= ncols) return;
-    const int32_t base = excl[C] + tile_off[C / kScanTile];
+    const int32_t base = excl[C] + tile0;
     off_c[C] = base;
+    if (C == ncols - 1) {  // the last column: the level's total
+        const int32_t total = tile0 + tile_sum[blockIdx.x];
+        *count = total;
+        off_c[ncols] = total;
+    }
     const int64_t per = (int64_t)g.Hc * g.Wc;
     const int b = (int)(C / per);
     const int rem = (int)(C - (int64_t)b * per);
@@ -670,9 +641,8 @@ struct pmg_unet {
     float* xd[kMaxLevels] = {};         // down-stage stream = skip [cap][C_k]
     float* xu[kMaxLevels] = {};         // up-stage stream [cap][C_k] (k < L - 1)
     float* xb = nullptr;                // bottleneck stream [cap][C_L]
-    int32_t* scan_cnt = nullptr;        // [max ncols]
-    int32_t* scan_excl = nullptr;       // [max ncols]
-    int32_t* scan_tiles = nullptr;      // [max ncols / kScanTile + 1]
+    int32_t* scan_excl = nullptr;       // [max ncols]: a column's first row within its block of 256 columns
+    int32_t* scan_tiles = nullptr;      // [max ncols / 256 + 1]: each block's voxel total
     // activations entering a convolution or a linear: int8 codes, or fp16 (the teacher)
     void* q1 = nullptr;                 // [cap][Cmax]
     void* q2 = nullptr;
@@ -851,17 +821,10 @@ static int enqueue_structure(pmg_unet* u, hipStream_t s) {
         PoolGeom g{u->coords[k], u->off[k], u->cfg.B, u->Hk[k], u->Wk[k], u->Hk[k + 1], u->Wk[k + 1]};
         const int64_t nc = u->ncols[k + 1];
         const unsigned gb = (unsigned)((nc + 255) / 256);
-        hipLaunchKernelGGL(pool_count_k, dim3(gb), dim3(256), 0, s, g, nc, u->scan_cnt);
+        hipLaunchKernelGGL(pool_count_k, dim3(gb), dim3(256), 0, s, g, nc, u->scan_excl, u->scan_tiles);
         if (int e = check_launch("pool_count_k")) return e;
-        const int ntiles = (int)((nc + kScanTile - 1) / kScanTile);
-        hipLaunchKernelGGL(scan_tiles_k, dim3((unsigned)ntiles), dim3(256), 0, s, u->scan_cnt, nc, u->scan_excl,
-                           u->scan_tiles);
-        if (int e = check_launch("scan_tiles_k")) return e;
-        hipLaunchKernelGGL(scan_top_k, dim3(1), dim3(1024), 0, s, u->scan_tiles, ntiles, u->counts + k + 1,
-                           u->off[k + 1] + nc);
-        if (int e = check_launch("scan_top_k")) return e;
         hipLaunchKernelGGL(pool_emit_k, dim3(gb), dim3(256), 0, s, g, nc, u->scan_excl, u->scan_tiles,
-                           u->coords[k + 1], u->off[k + 1], u->parent[k]);
+                           u->counts + k + 1, u->coords[k + 1], u->off[k + 1], u->parent[k]);
         if (int e = check_launch("pool_emit_k")) return e;
         hipLaunchKernelGGL(nmap_level_k, dim3((unsigned)((u->cap + 255) / 256)), dim3(256), 0, s, u->coords[k + 1],
                            u->off[k + 1], u->counts + k + 1, u->Hk[k + 1], u->Wk[k + 1], u->cap, u->nmap_t[k + 1],
@@ -1190,9 +1153,8 @@ pmg_unet* pmg_unet_create(const pmg_unet_config* cfg) {
         take((void**)&u->xd[k], (size_t)4 * cap * c.channels[k]);
     }
     take((void**)&u->xb, (size_t)4 * cap * CL);
-    take((void**)&u->scan_cnt, 4 * maxcols);
     take((void**)&u->scan_excl, 4 * maxcols);
-    take((void**)&u->scan_tiles, 4 * (maxcols / kScanTile + 2));
+    take((void**)&u->scan_tiles, 4 * (maxcols / 256 + 2));
     const size_t elt = c.precision == PMG_PREC_FP16 ? 2 : 1;
     take((void**)&u->q1, elt * cap * u->Cmax);
     take((void**)&u->q2, elt * cap * u->Cmax);
