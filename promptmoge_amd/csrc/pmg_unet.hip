@@ -21,7 +21,8 @@
 //   blocks at levels >= 1  generic-map MFMA conv with the device row count (launch_conv_i8_dev: the weight-staged
 //                          spconv_g2_k / spconv_g2r_k at C = 64 / 128 / 256, spconv_k otherwise) + a row
 //                          LayerNorm kernel
-//   PoolDown               children's fp32 mean (row order, / count) quantised in one kernel, then an int8 GEMM
+//   PoolDown               one kernel: children's fp32 mean (row order, / count) quantised, int8 GEMM, and the next
+//                          block's LayerNorm codes (fp16: mean-pool kernel, GEMM, row LayerNorm kernel)
 //   encoder conditioning   per token: quantise-transpose of the planar feature, int8 GEMM (+ the planar bias map),
 //                          gathered per voxel by its column in the concat-quantise of fuse_proj.0's input
 //   fuse_proj              int8 GEMM + SiLU + requantise, int8 GEMM
@@ -529,6 +530,162 @@ __global__ __launch_bounds__(256) void gemm_i8_k(GemmArgs g) {
     }
 }
 
+// PoolDown as one kernel (int8): the children's mean of each coarse voxel (pool_quant_k's arithmetic), quantised,
+// times the pool linear (gemm_i8_k's EPI_BIAS arithmetic) -> the coarse fp32 row, and, when the level has a block,
+// that block's LayerNorm -> SiLU -> int8 codes (rows_ln_k's arithmetic). One wave per 16 coarse voxels holds all Cn
+// = 16 NB output channels, so the pooled codes are formed once per voxel and the row is whole for the LayerNorm;
+// the accumulators go from the MFMA layout (lane (r, g): rows 4g + i, column r) to the row layout of the
+// LayerNorm (lane (r, g): row r, channels 16j + 4g + i) through the wave's LDS tile.
+struct PoolLinArgs {
+    const float* x;         // fine level [cap][Ck] fp32
+    int Ck, Cn;
+    PoolGeom g;
+    const int4* coords_c;   // coarse voxels
+    const int64_t* count;   // coarse voxel count (device)
+    float pool_mult;        // the pool linear's input quantisation
+    const int8_t* w;        // [Cn][Ck]
+    float a_scale;
+    const float* w_scale;   // [Cn]
+    const float* bias;      // [Cn] or NULL
+    float* y_out;           // coarse [cap][Cn] fp32
+    const float* gamma;     // next block's LayerNorm, or NULL (no codes)
+    const float* beta;
+    float ln_mult;
+    int8_t* codes;          // coarse [cap][Cn]
+};
+
+template <int NB>
+__global__ __launch_bounds__(256) void pool_linear_ln_k(PoolLinArgs a) {
+    constexpr int CN = 16 * NB;
+    constexpr int LDW = CN + 4;  // LDS tile row stride (floats)
+    __shared__ float tile[4][16 * LDW];
+    const int64_t rows = *a.count;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int r = lane & 15, gq = lane >> 4;
+    const int nchunk = a.Ck >> 4;  // 16-channel chunks of a fine row
+    const int rowb = a.Ck;         // bytes per weight row
+    float* tl = tile[wv];
+    for (int64_t mb = blockIdx.x; mb * 64 < rows; mb += gridDim.x) {
+        const int64_t m0 = (mb * 4 + wv) * 16;
+        if (m0 >= rows) break;
+        const int64_t o = m0 + r;
+        const bool row_ok = o < rows;
+        // the children of coarse voxel o: runs of z / 2 == oc.w in its four child columns, in row order; lane
+        // group gq walks child column gq, and every lane of the row then reads the four runs
+        int32_t clo[4], chi[4];
+        {
+            const int4 oc = a.coords_c[row_ok ? o : 0];
+            int32_t p = 0, e = 0;
+            const int i = 2 * oc.y + (gq >> 1), j = 2 * oc.z + (gq & 1);
+            if (row_ok && i < a.g.Hf && j < a.g.Wf) {
+                int32_t lo, hi;
+                col_range(a.g.off, ((int64_t)oc.x * a.g.Hf + i) * a.g.Wf + j, lo, hi);
+                p = lo;
+                while (p < hi && (a.g.coords[p].w >> 1) < oc.w) ++p;
+                e = p;
+                while (e < hi && (a.g.coords[e].w >> 1) == oc.w) ++e;
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                clo[q] = __shfl(p, r + 16 * q, 64);
+                chi[q] = __shfl(e, r + 16 * q, 64);
+            }
+        }
+        const float cnt = (float)((chi[0] - clo[0]) + (chi[1] - clo[1]) + (chi[2] - clo[2]) + (chi[3] - clo[3]));
+        v4i acc[NB];
+#pragma unroll
+        for (int j = 0; j < NB; ++j) acc[j] = v4i{0, 0, 0, 0};
+        for (int q0 = 0; q0 < nchunk; q0 += 4) {
+            const int ch = q0 + gq;  // this lane group's 16-channel chunk
+            const bool on = ch < nchunk;
+            const int qc = on ? ch : nchunk - 1;
+            v4i bv[NB];
+#pragma unroll
+            for (int j = 0; j < NB; ++j) bv[j] = *(const v4i*)(a.w + (int64_t)(16 * j + r) * rowb + qc * 16);
+            // pooled mean of the chunk's 16 channels: fp32 sums from 0 in child row order, / count, quantised
+            v4i av = v4i{0, 0, 0, 0};
+            if (on && row_ok) {
+                float h[16];
+#pragma unroll
+                for (int e = 0; e < 16; ++e) h[e] = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    for (int32_t p = clo[q]; p < chi[q]; ++p) {
+                        const float* src = a.x + (int64_t)p * a.Ck + 16 * ch;
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) {
+                            const float4 f = *(const float4*)(src + 4 * v);
+                            h[4 * v + 0] = h[4 * v + 0] + f.x;
+                            h[4 * v + 1] = h[4 * v + 1] + f.y;
+                            h[4 * v + 2] = h[4 * v + 2] + f.z;
+                            h[4 * v + 3] = h[4 * v + 3] + f.w;
+                        }
+                    }
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const float m4[4] = {h[4 * v] / cnt, h[4 * v + 1] / cnt, h[4 * v + 2] / cnt, h[4 * v + 3] / cnt};
+                    av[v] = (int)pack_codes4(m4, a.pool_mult);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < NB; ++j)
+                acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, on ? bv[j] : v4i{0, 0, 0, 0}, acc[j], 0, 0, 0);
+        }
+        // y = (acc * a_scale) * w_scale[n] + bias[n] (gemm_i8_k's EPI_BIAS), through LDS into the row layout
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const int n = 16 * j + r;
+            const float ws = a.w_scale[n], bs = a.bias ? a.bias[n] : 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float y = (float)acc[j][i] * a.a_scale;
+                y = y * ws;
+                if (a.bias) y = y + bs;
+                tl[(4 * gq + i) * LDW + n] = y;
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's tile writes are in LDS
+        __builtin_amdgcn_wave_barrier();
+        float y[NB][4];
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const float4 v = *(const float4*)(tl + r * LDW + 16 * j + 4 * gq);
+            y[j][0] = v.x;
+            y[j][1] = v.y;
+            y[j][2] = v.z;
+            y[j][3] = v.w;
+            if (row_ok) *(float4*)(a.y_out + o * CN + 16 * j + 4 * gq) = v;
+        }
+        __builtin_amdgcn_wave_barrier();  // every lane has read the tile before the next trip writes it
+        if (!a.gamma) continue;
+        ln_silu_quad<NB, false>(y, a.gamma, a.beta, 1e-6f, gq);
+        uint32_t pk[NB];
+        silu_codes_packed<NB>(y, a.ln_mult, pk);
+        if (row_ok) {
+#pragma unroll
+            for (int j = 0; j < NB; ++j) *(uint32_t*)(a.codes + o * CN + 16 * j + 4 * gq) = pk[j];
+        }
+    }
+}
+
+static int launch_pool_linear_ln(const PoolLinArgs& a, int64_t cap, hipStream_t s) {
+    if (cap == 0) return PMG_OK;
+    PMG_REQUIRE(a.Ck % 16 == 0 && a.Ck > 0, "pool linear input width must be a multiple of 16");
+    const dim3 grid(row_grid(cap * 4));  // 64 coarse rows (256 threads) per block, grid-stride
+    switch (a.Cn) {
+        case 16: hipLaunchKernelGGL(pool_linear_ln_k<1>, grid, dim3(256), 0, s, a); break;
+        case 32: hipLaunchKernelGGL(pool_linear_ln_k<2>, grid, dim3(256), 0, s, a); break;
+        case 48: hipLaunchKernelGGL(pool_linear_ln_k<3>, grid, dim3(256), 0, s, a); break;
+        case 64: hipLaunchKernelGGL(pool_linear_ln_k<4>, grid, dim3(256), 0, s, a); break;
+        case 96: hipLaunchKernelGGL(pool_linear_ln_k<6>, grid, dim3(256), 0, s, a); break;
+        case 128: hipLaunchKernelGGL(pool_linear_ln_k<8>, grid, dim3(256), 0, s, a); break;
+        case 192: hipLaunchKernelGGL(pool_linear_ln_k<12>, grid, dim3(256), 0, s, a); break;
+        case 256: hipLaunchKernelGGL(pool_linear_ln_k<16>, grid, dim3(256), 0, s, a); break;
+        default: return fail(PMG_E_INVALID, "unsupported level width " + std::to_string(a.Cn));
+    }
+    return check_launch("pool_linear_ln_k");
+}
+
 static int launch_gemm(const GemmArgs& g, int epi, bool f16, hipStream_t s) {
     PMG_REQUIRE(g.K % 16 == 0 && g.N % 16 == 0 && g.K > 0 && g.N > 0, "GEMM sizes must be multiples of 16");
     if (g.rows_cap == 0) return PMG_OK;
@@ -911,18 +1068,25 @@ static int enqueue_unet(pmg_unet* u, const float* feats, const int32_t* coords, 
         if (k + 1 == L) break;
         const int Ck = c.channels[k], Cn = c.channels[k + 1];
         PoolGeom g{u->coords[k], u->off[k], c.B, u->Hk[k], u->Wk[k], u->Hk[k + 1], u->Wk[k + 1]};
-        if (f16)
-            hipLaunchKernelGGL(pool_quant_k<_Float16>, dim3(row_grid(cap * (Ck / 4))), dim3(256), 0, s, u->xd[k], Ck,
-                               g, u->coords[k + 1], u->counts + k + 1, 1.0f, (_Float16*)u->codes);
-        else
-            hipLaunchKernelGGL(pool_quant_k<int8_t>, dim3(row_grid(cap * (Ck / 4))), dim3(256), 0, s, u->xd[k], Ck,
-                               g, u->coords[k + 1], u->counts + k + 1, u->pool[k].q_mult, (int8_t*)u->codes);
+        const pmg_block_weights* nb = !u->down[k + 1].empty() ? &u->down[k + 1][0] : nullptr;
+        if (!f16) {  // pool mean + linear + the next block's LayerNorm codes in one kernel
+            const pmg_linear_weights& lw = u->pool[k];
+            PoolLinArgs pa{u->xd[k], Ck, Cn, g, u->coords[k + 1], u->counts + k + 1, lw.q_mult,
+                           (const int8_t*)lw.w, lw.a_scale, lw.w_scale, lw.bias, u->xd[k + 1],
+                           nb ? nb->ln_gamma : nullptr, nb ? nb->ln_beta : nullptr, nb ? nb->q1_mult : 1.0f,
+                           (int8_t*)u->q1};
+            if (int e = launch_pool_linear_ln(pa, cap, s)) return e;
+            continue;
+        }
+        // fp16 (the teacher): mean pool to fp16 codes, the fp16 GEMM, then the next block's LayerNorm
+        hipLaunchKernelGGL(pool_quant_k<_Float16>, dim3(row_grid(cap * (Ck / 4))), dim3(256), 0, s, u->xd[k], Ck, g,
+                           u->coords[k + 1], u->counts + k + 1, 1.0f, (_Float16*)u->codes);
         if (int e = check_launch("pool_quant_k")) return e;
         if (int e = linear(u, u->codes, u->counts + k + 1, cap, Ck, u->pool[k], Cn, PMG_EPI_BIAS, 0.0f, u->xd[k + 1],
                            nullptr, s))
             return e;
-        if (!u->down[k + 1].empty())
-            if (int e = ln_codes(u, k + 1, u->xd[k + 1], u->down[k + 1][0], s)) return e;
+        if (nb)
+            if (int e = ln_codes(u, k + 1, u->xd[k + 1], *nb, s)) return e;
     }
 
     // encoder conditioning and fuse_proj at the deepest level (sparse_unet.py:233-240)
