@@ -26,7 +26,8 @@
 //   encoder conditioning   per token: quantise-transpose of the planar feature, int8 GEMM (+ the planar bias map),
 //                          gathered per voxel by its column in the concat-quantise of fuse_proj.0's input
 //   fuse_proj              int8 GEMM + SiLU + requantise, int8 GEMM
-//   NearestUp              quantise, int8 GEMM at the coarse level, then parent gather + skip + next LayerNorm
+//   NearestUp              one kernel per fine voxel (int8): parent row's codes, int8 GEMM, + skip, next LayerNorm
+//                          (fp16: quantise, GEMM at the coarse level, then parent gather + skip + LayerNorm)
 //   out_proj               in the epilogue of the last level-0 conv
 #include <climits>
 #include <cstring>
@@ -686,6 +687,128 @@ static int launch_pool_linear_ln(const PoolLinArgs& a, int64_t cap, hipStream_t 
     return check_launch("pool_linear_ln_k");
 }
 
+// NearestUp as one kernel (int8): for each fine voxel i, the codes of its parent's coarse row (quant_rows_k's
+// arithmetic) times the up linear (gemm_i8_k's EPI_BIAS), plus the skip row (rows_ln_k's UP gather: lin[parent] +
+// skip), written as the fine fp32 row, then the next block's LayerNorm -> SiLU -> int8 codes when the level has a
+// block. The linear runs per fine voxel instead of once per coarse voxel (a parent has 1.7-4 children on Model A):
+// the MFMA work is small, and the coarse linear's fp32 rows are neither written nor read back.
+struct UpLinArgs {
+    const float* cur;       // coarse level [cap][Cs] fp32
+    int Cs, Ct;
+    const int32_t* parent;  // fine voxel -> coarse row
+    const int64_t* count;   // fine voxel count (device)
+    float in_mult;          // the up linear's input quantisation
+    const int8_t* w;        // [Ct][Cs]
+    float a_scale;
+    const float* w_scale;   // [Ct]
+    const float* bias;      // [Ct] or NULL
+    const float* skip;      // fine [cap][Ct] fp32 (the encoder side's row)
+    float* y_out;           // fine [cap][Ct] fp32
+    const float* gamma;     // next block's LayerNorm, or NULL (no codes)
+    const float* beta;
+    float ln_mult;
+    int8_t* codes;          // fine [cap][Ct]
+};
+
+template <int NB>
+__global__ __launch_bounds__(256) void up_linear_ln_k(UpLinArgs a) {
+    constexpr int CT = 16 * NB;
+    constexpr int LDW = CT + 4;  // LDS tile row stride (floats)
+    __shared__ float tile[4][16 * LDW];
+    const int64_t rows = *a.count;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int r = lane & 15, gq = lane >> 4;
+    const int nchunk = a.Cs >> 4;  // 16-channel chunks of a coarse row
+    const int rowb = a.Cs;         // bytes per weight row
+    float* tl = tile[wv];
+    for (int64_t mb = blockIdx.x; mb * 64 < rows; mb += gridDim.x) {
+        const int64_t m0 = (mb * 4 + wv) * 16;
+        if (m0 >= rows) break;
+        const int64_t i = m0 + r;
+        const bool row_ok = i < rows;
+        const int64_t par = row_ok ? (int64_t)a.parent[i] : 0;
+        v4i acc[NB];
+#pragma unroll
+        for (int j = 0; j < NB; ++j) acc[j] = v4i{0, 0, 0, 0};
+        for (int q0 = 0; q0 < nchunk; q0 += 4) {
+            const int ch = q0 + gq;  // this lane group's 16-channel chunk
+            const bool on = ch < nchunk;
+            const int qc = on ? ch : nchunk - 1;
+            v4i bv[NB];
+#pragma unroll
+            for (int j = 0; j < NB; ++j) bv[j] = *(const v4i*)(a.w + (int64_t)(16 * j + r) * rowb + qc * 16);
+            const float* src = a.cur + par * a.Cs + 16 * qc;
+            float4 f[4];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) f[v] = *(const float4*)(src + 4 * v);
+            v4i av;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const float h[4] = {f[v].x, f[v].y, f[v].z, f[v].w};
+                av[v] = (int)pack_codes4(h, a.in_mult);
+            }
+            if (!(on && row_ok)) av = v4i{0, 0, 0, 0};
+#pragma unroll
+            for (int j = 0; j < NB; ++j)
+                acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, on ? bv[j] : v4i{0, 0, 0, 0}, acc[j], 0, 0, 0);
+        }
+        // lin = (acc * a_scale) * w_scale[n] + bias[n] (gemm_i8_k's EPI_BIAS), through LDS into the row layout
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const int n = 16 * j + r;
+            const float ws = a.w_scale[n], bs = a.bias ? a.bias[n] : 0.0f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                float y = (float)acc[j][q] * a.a_scale;
+                y = y * ws;
+                if (a.bias) y = y + bs;
+                tl[(4 * gq + q) * LDW + n] = y;
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's tile writes are in LDS
+        __builtin_amdgcn_wave_barrier();
+        const int64_t io = row_ok ? i : 0;
+        float y[NB][4];
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const float4 v = *(const float4*)(tl + r * LDW + 16 * j + 4 * gq);
+            const float4 k = *(const float4*)(a.skip + io * CT + 16 * j + 4 * gq);
+            y[j][0] = v.x + k.x;
+            y[j][1] = v.y + k.y;
+            y[j][2] = v.z + k.z;
+            y[j][3] = v.w + k.w;
+            if (row_ok) *(float4*)(a.y_out + i * CT + 16 * j + 4 * gq) = make_float4(y[j][0], y[j][1], y[j][2], y[j][3]);
+        }
+        __builtin_amdgcn_wave_barrier();  // every lane has read the tile before the next trip writes it
+        if (!a.gamma) continue;
+        ln_silu_quad<NB, false>(y, a.gamma, a.beta, 1e-6f, gq);
+        uint32_t pk[NB];
+        silu_codes_packed<NB>(y, a.ln_mult, pk);
+        if (row_ok) {
+#pragma unroll
+            for (int j = 0; j < NB; ++j) *(uint32_t*)(a.codes + i * CT + 16 * j + 4 * gq) = pk[j];
+        }
+    }
+}
+
+static int launch_up_linear_ln(const UpLinArgs& a, int64_t cap, hipStream_t s) {
+    if (cap == 0) return PMG_OK;
+    PMG_REQUIRE(a.Cs % 16 == 0 && a.Cs > 0, "up linear input width must be a multiple of 16");
+    const dim3 grid(row_grid(cap * 4));  // 64 fine rows (256 threads) per block, grid-stride
+    switch (a.Ct) {
+        case 16: hipLaunchKernelGGL(up_linear_ln_k<1>, grid, dim3(256), 0, s, a); break;
+        case 32: hipLaunchKernelGGL(up_linear_ln_k<2>, grid, dim3(256), 0, s, a); break;
+        case 48: hipLaunchKernelGGL(up_linear_ln_k<3>, grid, dim3(256), 0, s, a); break;
+        case 64: hipLaunchKernelGGL(up_linear_ln_k<4>, grid, dim3(256), 0, s, a); break;
+        case 96: hipLaunchKernelGGL(up_linear_ln_k<6>, grid, dim3(256), 0, s, a); break;
+        case 128: hipLaunchKernelGGL(up_linear_ln_k<8>, grid, dim3(256), 0, s, a); break;
+        case 192: hipLaunchKernelGGL(up_linear_ln_k<12>, grid, dim3(256), 0, s, a); break;
+        case 256: hipLaunchKernelGGL(up_linear_ln_k<16>, grid, dim3(256), 0, s, a); break;
+        default: return fail(PMG_E_INVALID, "unsupported level width " + std::to_string(a.Ct));
+    }
+    return check_launch("up_linear_ln_k");
+}
+
 static int launch_gemm(const GemmArgs& g, int epi, bool f16, hipStream_t s) {
     PMG_REQUIRE(g.K % 16 == 0 && g.N % 16 == 0 && g.K > 0 && g.N > 0, "GEMM sizes must be multiples of 16");
     if (g.rows_cap == 0) return PMG_OK;
@@ -1130,21 +1253,25 @@ static int enqueue_unet(pmg_unet* u, const float* feats, const int32_t* coords, 
     for (int i = 0; i + 1 < L; ++i) {
         const int t = L - 2 - i;
         const int Cs = c.channels[t + 1], Ct = c.channels[t];
-        if (f16)
+        const pmg_block_weights* fb = !u->dec[i].empty() ? &u->dec[i][0] : nullptr;
+        if (!f16) {  // parent codes + linear + skip + the next block's LayerNorm codes in one kernel, per fine voxel
+            const pmg_linear_weights& lw = u->up[i];
+            UpLinArgs ua{cur, Cs, Ct, u->parent[t], u->counts + t, lw.q_mult, (const int8_t*)lw.w, lw.a_scale,
+                         lw.w_scale, lw.bias, u->xd[t], u->xu[t], fb ? fb->ln_gamma : nullptr,
+                         fb ? fb->ln_beta : nullptr, fb ? fb->q1_mult : 1.0f, (int8_t*)u->q1};
+            if (int e = launch_up_linear_ln(ua, cap, s)) return e;
+        } else {  // fp16 (the teacher): quantise, the fp16 GEMM at the coarse level, then the gather + LayerNorm
             hipLaunchKernelGGL(quant_rows_k<_Float16>, dim3(row_grid(cap * Cs / 4)), dim3(256), 0, s, cur, Cs,
                                u->counts + t + 1, 1.0f, (_Float16*)u->codes);
-        else
-            hipLaunchKernelGGL(quant_rows_k<int8_t>, dim3(row_grid(cap * Cs / 4)), dim3(256), 0, s, cur, Cs,
-                               u->counts + t + 1, u->up[i].q_mult, (int8_t*)u->codes);
-        if (int e = check_launch("quant_rows_k")) return e;
-        if (int e = linear(u, u->codes, u->counts + t + 1, cap, Cs, u->up[i], Ct, PMG_EPI_BIAS, 0.0f, u->lin,
-                           nullptr, s))
-            return e;
-        const pmg_block_weights* fb = !u->dec[i].empty() ? &u->dec[i][0] : nullptr;
-        if (int e = launch_rows_ln(true, Ct, u->lin, u->parent[t], u->xd[t], u->counts + t, cap,
-                                   fb ? fb->ln_gamma : nullptr, fb ? fb->ln_beta : nullptr, fb ? fb->q1_mult : 1.0f,
-                                   u->xu[t], u->q1, f16, s))
-            return e;
+            if (int e = check_launch("quant_rows_k")) return e;
+            if (int e = linear(u, u->codes, u->counts + t + 1, cap, Cs, u->up[i], Ct, PMG_EPI_BIAS, 0.0f, u->lin,
+                               nullptr, s))
+                return e;
+            if (int e = launch_rows_ln(true, Ct, u->lin, u->parent[t], u->xd[t], u->counts + t, cap,
+                                       fb ? fb->ln_gamma : nullptr, fb ? fb->ln_beta : nullptr,
+                                       fb ? fb->q1_mult : 1.0f, u->xu[t], u->q1, f16, s))
+                return e;
+        }
         if (int e = enqueue_stage(u, t, u->dec[i], u->xu[t], t == 0 ? &rout : nullptr, s)) return e;
         cur = u->xu[t];
     }
