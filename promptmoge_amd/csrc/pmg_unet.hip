@@ -809,11 +809,11 @@ static int launch_up_linear_ln(const UpLinArgs& a, int64_t cap, hipStream_t s) {
     return check_launch("up_linear_ln_k");
 }
 
-static int launch_gemm(const GemmArgs& g, int epi, bool f16, hipStream_t s) {
+static int launch_gemm(const GemmArgs& g, int epi, bool f16, hipStream_t s, bool narrow = false) {
     PMG_REQUIRE(g.K % 16 == 0 && g.N % 16 == 0 && g.K > 0 && g.N > 0, "GEMM sizes must be multiples of 16");
     if (g.rows_cap == 0) return PMG_OK;
     const int b = g.N / 16;
-    const int nb = b % 4 == 0 ? 4 : (b % 2 == 0 ? 2 : 1);
+    const int nb = narrow ? 1 : (b % 4 == 0 ? 4 : (b % 2 == 0 ? 2 : 1));
     const unsigned gy = (unsigned)(g.N / (16 * nb));
     int64_t gx = (g.rows_cap + 63) / 64;
     const int64_t gx_max = kRowBlocksMax / gy > 0 ? kRowBlocksMax / gy : 1;  // device-sized rows: grid-stride
@@ -1089,10 +1089,10 @@ static int ln_codes(pmg_unet* u, int k, const float* x, const pmg_block_weights&
 
 static int linear(pmg_unet* u, const void* a, const int64_t* rows_dev, int64_t rows_cap, int K,
                   const pmg_linear_weights& lw, int N, int epi, float out_mult, void* out, const float* planar,
-                  hipStream_t s) {
+                  hipStream_t s, bool narrow = false) {
     GemmArgs g{a, lw.w, rows_cap, rows_dev, K, N, lw.a_scale, lw.w_scale, lw.bias, out_mult, out, planar,
                (int64_t)u->R * u->Cc};
-    return launch_gemm(g, epi, u->cfg.precision == PMG_PREC_FP16, s);
+    return launch_gemm(g, epi, u->cfg.precision == PMG_PREC_FP16, s, narrow);
 }
 
 // The level structure (levels 1 .. L-1) from the level-0 coordinates.
@@ -1224,8 +1224,11 @@ static int enqueue_unet(pmg_unet* u, const float* feats, const int32_t* coords, 
             hipLaunchKernelGGL(enc_quant_k<int8_t>, grid, dim3(256), 0, s, enc_feat, c.enc_channels,
                                (int64_t)u->R * u->Cc, u->enc.q_mult, (int8_t*)u->enc_codes);
         if (int e = check_launch("enc_quant_k")) return e;
+        // the encoder tokens and the deepest level are a few thousand rows with long K: one 16-column block per
+        // wave gives the GEMM four times the waves (Model A: encoder_fuse 20 -> 13 us, fuse_proj 30 -> 28 us)
+        const bool narrow_top = top >= 2;
         if (int e = linear(u, u->enc_codes, nullptr, u->T, c.enc_channels, u->enc, CL, PMG_EPI_BIAS, 0.0f,
-                           u->enc_tok, enc_bias, s))
+                           u->enc_tok, enc_bias, s, true))
             return e;
         if (f16)
             hipLaunchKernelGGL(concat_quant_k<_Float16>, dim3(row_grid(cap * (CL / 2))), dim3(256), 0, s,
@@ -1237,10 +1240,10 @@ static int enqueue_unet(pmg_unet* u, const float* feats, const int32_t* coords, 
                                u->fuse0.q_mult, (int8_t*)u->codes);
         if (int e = check_launch("concat_quant_k")) return e;
         if (int e = linear(u, u->codes, u->counts + top, cap, 2 * CL, u->fuse0, CL, PMG_EPI_Q, u->fuse2.q_mult,
-                           u->codes2, nullptr, s))
+                           u->codes2, nullptr, s, narrow_top))
             return e;
         if (int e = linear(u, u->codes2, u->counts + top, cap, CL, u->fuse2, CL, PMG_EPI_BIAS, 0.0f, u->xb, nullptr,
-                           s))
+                           s, narrow_top))
             return e;
     }
     // bottleneck (sparse_unet.py:244-247)
