@@ -954,11 +954,13 @@ static int launch_g2_dev(const ConvArgs& a, int epilogue, hipStream_t s) {
     if constexpr (C == 64) {
         static_assert(NB == 4, "C = 64 keeps all 64 output channels");
         static_assert(RS == 2, "the resident-weight kernel has no tap split");
+        // gathers three taps ahead (a 4-slot ring): on the U-Net's level 1 (183k voxels) 2.5 us faster per conv
+        // than one tap ahead
         switch (epilogue) {
-            case PMG_EPI_ACC: hipLaunchKernelGGL((spconv_g2r_k<C, PMG_EPI_ACC, T, PF>), grid, dim3(kG2Threads), 0, s, a); break;
-            case PMG_EPI_Q: hipLaunchKernelGGL((spconv_g2r_k<C, PMG_EPI_Q, T, PF>), grid, dim3(kG2Threads), 0, s, a); break;
-            case PMG_EPI_R: hipLaunchKernelGGL((spconv_g2r_k<C, PMG_EPI_R, T, PF>), grid, dim3(kG2Threads), 0, s, a); break;
-            default: hipLaunchKernelGGL((spconv_g2r_k<C, PMG_EPI_BIAS, T, PF>), grid, dim3(kG2Threads), 0, s, a); break;
+            case PMG_EPI_ACC: hipLaunchKernelGGL((spconv_g2r_k<C, PMG_EPI_ACC, T, PF, 4>), grid, dim3(kG2Threads), 0, s, a); break;
+            case PMG_EPI_Q: hipLaunchKernelGGL((spconv_g2r_k<C, PMG_EPI_Q, T, PF, 4>), grid, dim3(kG2Threads), 0, s, a); break;
+            case PMG_EPI_R: hipLaunchKernelGGL((spconv_g2r_k<C, PMG_EPI_R, T, PF, 4>), grid, dim3(kG2Threads), 0, s, a); break;
+            default: hipLaunchKernelGGL((spconv_g2r_k<C, PMG_EPI_BIAS, T, PF, 4>), grid, dim3(kG2Threads), 0, s, a); break;
         }
         return check_launch("spconv_g2r_k");
     } else {
