@@ -20,6 +20,14 @@ namespace pmg {
 // (kVoxBlocks per batch item), so that few blocks meet at the per-batch min/max atomics: one block per 256 pixels
 // serialised 2400 same-address atomics at 480 x 640 (30 us).
 constexpr int kVoxBlocks = 64;
+// The per-batch-item key range before voxelize_k's atomics: zmin = INT_MAX, zmax = INT_MIN (one launch for both).
+__global__ __launch_bounds__(256) void minmax_init_k(int32_t* zmin, int32_t* zmax, int B) {
+    const int b = blockIdx.x * 256 + threadIdx.x;
+    if (b < B) {
+        zmin[b] = INT_MAX;
+        zmax[b] = INT_MIN;
+    }
+}
 __global__ __launch_bounds__(256) void voxelize_k(const float* __restrict__ logz, int64_t stride, int HW,
                                                   float res, int32_t* __restrict__ zq, int32_t* zmin,
                                                   int32_t* zmax) {
@@ -492,8 +500,8 @@ int pmg_voxelize(const float* logz, int64_t stride, int B, int H, int W, float r
     PMG_REQUIRE((int64_t)H * W <= INT_MAX && (int64_t)B * H * W <= INT_MAX, "map too large");
     PMG_REQUIRE(B <= 65535, "batch too large");
     hipStream_t s = (hipStream_t)stream;
-    fill_u32(zmin, 0x7fffffffu, B, s);
-    fill_u32(zmax, 0x80000000u, B, s);
+    hipLaunchKernelGGL(minmax_init_k, dim3((unsigned)((B + 255) / 256)), dim3(256), 0, s, zmin, zmax, B);
+    if (int e = check_launch("minmax_init_k")) return e;
     const int HW = H * W;
     const int nb = (HW + 255) / 256;
     dim3 grid(nb < kVoxBlocks ? nb : kVoxBlocks, B);
