@@ -100,17 +100,50 @@ __device__ inline void child_ranges(const PoolGeom& g, int64_t C, int32_t (&lo)[
     }
 }
 
-// The smallest z / 2 at the heads of the four lists (INT_MAX when all are exhausted). z >= 0, so z >> 1 = floor.
-__device__ inline int merge_min(const int4* coords, const int32_t (&h)[4], const int32_t (&e)[4]) {
-    int mn = INT_MAX;
+// The four child columns' lists merged by z / 2 (z >= 0, so z >> 1 = floor): zh[q] caches z / 2 at the head of list
+// q (INT_MAX once it is exhausted), so a step reads only the heads it advances, all four loads issued together.
+struct ChildMerge {
+    int32_t h[4], e[4];
+    int zh[4];
+    __device__ inline int head_z(const int4* coords, int q) const {
+        return h[q] < e[q] ? coords[h[q]].w >> 1 : INT_MAX;
+    }
+    __device__ inline void init(const PoolGeom& g, int64_t C) {
+        child_ranges(g, C, h, e);
+        int z[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-        if (h[q] < e[q]) {
-            const int z = coords[h[q]].w >> 1;
-            mn = z < mn ? z : mn;
+        for (int q = 0; q < 4; ++q) z[q] = g.coords[h[q] < e[q] ? h[q] : 0].w >> 1;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) zh[q] = h[q] < e[q] ? z[q] : INT_MAX;
+    }
+    __device__ inline int min_z() const {
+        int mn = zh[0];
+#pragma unroll
+        for (int q = 1; q < 4; ++q) mn = zh[q] < mn ? zh[q] : mn;
+        return mn;
+    }
+    // Consumes every head equal to mn (the voxels of one coarse voxel), calling take(row) in list order.
+    template <class Take>
+    __device__ inline void consume(const int4* coords, int mn, Take take) {
+        for (;;) {
+            bool adv = false;
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                if (zh[q] == mn) {
+                    take(h[q]);
+                    ++h[q];
+                    adv = true;
+                }
+            if (!adv) break;
+            int z[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) z[q] = coords[h[q] < e[q] ? h[q] : 0].w >> 1;
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                if (zh[q] == mn) zh[q] = h[q] < e[q] ? z[q] : INT_MAX;
         }
-    return mn;
-}
+    }
+};
 
 // One thread per coarse column: its voxel count (the distinct z / 2 of its child columns), and the exclusive scan
 // of the counts within the block's 256 columns (excl) with the block's total (tile_sum).
@@ -120,14 +153,12 @@ __global__ __launch_bounds__(256) void pool_count_k(PoolGeom g, int64_t ncols, i
     const int64_t C = (int64_t)blockIdx.x * 256 + threadIdx.x;
     int n = 0;
     if (C < ncols) {
-        int32_t h[4], e[4];
-        child_ranges(g, C, h, e);
+        ChildMerge cm;
+        cm.init(g, C);
         for (;;) {
-            const int mn = merge_min(g.coords, h, e);
+            const int mn = cm.min_z();
             if (mn == INT_MAX) break;
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-                while (h[q] < e[q] && (g.coords[h[q]].w >> 1) == mn) ++h[q];
+            cm.consume(g.coords, mn, [](int32_t) {});
             ++n;
         }
     }
@@ -169,16 +200,14 @@ __global__ __launch_bounds__(256) void pool_emit_k(PoolGeom g, int64_t ncols, co
     const int b = (int)(C / per);
     const int rem = (int)(C - (int64_t)b * per);
     const int I = rem / g.Wc, J = rem - (rem / g.Wc) * g.Wc;
-    int32_t h[4], e[4];
-    child_ranges(g, C, h, e);
+    ChildMerge cm;
+    cm.init(g, C);
     int32_t o = base;
     for (;;) {
-        const int mn = merge_min(g.coords, h, e);
+        const int mn = cm.min_z();
         if (mn == INT_MAX) break;
         coords_c[o] = make_int4(b, I, J, mn);
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            while (h[q] < e[q] && (g.coords[h[q]].w >> 1) == mn) parent[h[q]++] = o;
+        cm.consume(g.coords, mn, [&](int32_t row) { parent[row] = o; });
         ++o;
     }
 }
@@ -194,28 +223,46 @@ __global__ __launch_bounds__(256) void nmap_level_k(const int4* __restrict__ coo
     uint32_t rmask = 0;
     if (o < M) {
         const int4 c = coords[o];
+        // the 9 neighbouring columns' voxel ranges, all loaded before any is walked
+        int32_t p[9], hi[9];
 #pragma unroll
-        for (int di = -1; di <= 1; ++di)
+        for (int k = 0; k < 9; ++k) {
+            const int i = c.y + k / 3 - 1, j = c.z + k % 3 - 1;
+            const bool in = i >= 0 && i < H && j >= 0 && j < W;
+            const int64_t col = in ? ((int64_t)c.x * H + i) * W + j : 0;
+            p[k] = in ? off[col] : 0;
+            hi[k] = in ? off[col + 1] : 0;
+        }
+        // walk the columns in lock step, one voxel of each per trip (its z loaded for all 9 before any is
+        // compared); a column stops at its end or above z + 1
+        int32_t f[27];
 #pragma unroll
-            for (int dj = -1; dj <= 1; ++dj) {
-                int32_t f[3] = {-1, -1, -1};
-                const int i = c.y + di, j = c.z + dj;
-                if (i >= 0 && i < H && j >= 0 && j < W) {
-                    const int64_t col = ((int64_t)c.x * H + i) * W + j;
-                    const int32_t lo = off[col], hi = off[col + 1];
-                    for (int32_t p = lo; p < hi; ++p) {
-                        const int z = coords[p].w;
-                        if (z > c.w + 1) break;
-                        if (z >= c.w - 1) f[z - (c.w - 1)] = p;
-                    }
-                }
+        for (int v = 0; v < 27; ++v) f[v] = -1;
+        for (;;) {
+            int zc[9];
 #pragma unroll
-                for (int dz = 0; dz < 3; ++dz) {
-                    const int v = (di + 1) * 9 + (dj + 1) * 3 + dz;
-                    nmap_t[(int64_t)v * cap + o] = f[dz];
-                    rmask |= (f[dz] >= 0 ? 1u : 0u) << v;
+            for (int k = 0; k < 9; ++k) zc[k] = coords[p[k] < hi[k] ? p[k] : 0].w;
+            bool any = false;
+#pragma unroll
+            for (int k = 0; k < 9; ++k) {
+                if (p[k] < hi[k] && zc[k] <= c.w + 1) {
+                    const int dz = zc[k] - (c.w - 1);
+#pragma unroll
+                    for (int d = 0; d < 3; ++d)
+                        if (dz == d) f[3 * k + d] = p[k];
+                    ++p[k];
+                    any = true;
+                } else {
+                    p[k] = hi[k];
                 }
             }
+            if (!any) break;
+        }
+#pragma unroll
+        for (int v = 0; v < 27; ++v) {
+            nmap_t[(int64_t)v * cap + o] = f[v];
+            rmask |= (f[v] >= 0 ? 1u : 0u) << v;
+        }
     }
 #pragma unroll
     for (int sh = 1; sh < 16; sh <<= 1) rmask |= __shfl_xor(rmask, sh, 16);
