@@ -172,13 +172,15 @@ __global__ __launch_bounds__(256) void pool_count_k(PoolGeom g, int64_t ncols, i
     if (threadIdx.x == 255) tile_sum[blockIdx.x] = before + (int32_t)incl;
 }
 
-// Writes the coarse voxels of column C (coordinates and the column's CSR start) and the parent of every child. The
-// block's first row is the sum of the tile totals of the blocks before it (pool_count_k's tiling: 256 columns per
-// block); the last block also writes the level's voxel count and the end of its column CSR.
+// Writes the coarse voxels of column C (coordinates and the column's CSR start), the parent of every child and, per
+// coarse voxel, its children: for child column q, the first child's row | (the number of children, 0 - 2) << 30
+// (a column holds at most the two voxels z = 2 Z, 2 Z + 1 of coarse voxel Z). The block's first row is the sum of
+// the tile totals of the blocks before it (pool_count_k's tiling: 256 columns per block); the last block also
+// writes the level's voxel count and the end of its column CSR.
 __global__ __launch_bounds__(256) void pool_emit_k(PoolGeom g, int64_t ncols, const int32_t* __restrict__ excl,
                                                    const int32_t* __restrict__ tile_sum, int64_t* __restrict__ count,
                                                    int4* __restrict__ coords_c, int32_t* __restrict__ off_c,
-                                                   int32_t* __restrict__ parent) {
+                                                   int32_t* __restrict__ parent, int4* __restrict__ child) {
     __shared__ int32_t wsum[4];
     int32_t t = 0;
     for (int64_t q = threadIdx.x; q < (int64_t)blockIdx.x; q += 256) t += tile_sum[q];
@@ -207,7 +209,10 @@ __global__ __launch_bounds__(256) void pool_emit_k(PoolGeom g, int64_t ncols, co
         const int mn = cm.min_z();
         if (mn == INT_MAX) break;
         coords_c[o] = make_int4(b, I, J, mn);
+        const int32_t h0 = cm.h[0], h1 = cm.h[1], h2 = cm.h[2], h3 = cm.h[3];
         cm.consume(g.coords, mn, [&](int32_t row) { parent[row] = o; });
+        child[o] = make_int4(h0 | ((cm.h[0] - h0) << 30), h1 | ((cm.h[1] - h1) << 30), h2 | ((cm.h[2] - h2) << 30),
+                             h3 | ((cm.h[3] - h3) << 30));
         ++o;
     }
 }
@@ -589,6 +594,7 @@ struct PoolLinArgs {
     int Ck, Cn;
     PoolGeom g;
     const int4* coords_c;   // coarse voxels
+    const int4* child;      // per coarse voxel: first child row | children << 30 per child column (pool_emit_k)
     const int64_t* count;   // coarse voxel count (device)
     float pool_mult;        // the pool linear's input quantisation
     const int8_t* w;        // [Cn][Ck]
@@ -856,6 +862,236 @@ static int launch_up_linear_ln(const UpLinArgs& a, int64_t cap, hipStream_t s) {
     return check_launch("up_linear_ln_k");
 }
 
+// PoolDown and NearestUp (int8) with the output channels split over the block's four waves, for level widths of 64,
+// 128, 192 and 256 (Cn = 16 NB, NB % 4 == 0). A block takes RG groups of 16 rows at a time:
+//   1. the linear's input codes -- the pooled children's mean (PoolDown: the children read from the coarse voxel's
+//      child record, all of them requested at once, summed from 0 in child row order) or the parent's row (NearestUp),
+//      quantised -- of each (row group, 64-channel trip) pair, formed by one wave and kept in LDS as the MFMA's A
+//      operand (lane (r, g): row r, 16 codes of chunk 4 trip + g);
+//   2. wave w multiplies them by its quarter of the weight rows (its B operands, loaded once per block), the
+//      result (gemm_i8_k's EPI_BIAS arithmetic) goes to an LDS tile of whole rows;
+//   3. each wave takes a quarter of the rows in the row layout of the LayerNorm (lane (r, g): row r, channels
+//      16 j + 4 g + i; the quad-order sums of ln_silu_quad): (the skip row added,) the fp32 row written, then the
+//      next block's LayerNorm -> SiLU -> int8 codes.
+// The same arithmetic as pool_linear_ln_k / up_linear_ln_k, operation for operation. At the coarse levels (a few
+// thousand rows) a block of one row group puts four waves on 16 rows where those kernels had one wave reading every
+// weight row and walking the children one dependent load at a time.
+template <bool UP, int NB, int RG, int KT>
+struct RowLin4 {
+    static constexpr int CN = 16 * NB, NBW = NB / 4, LDW = CN + 4, R = 16 * RG;
+};
+
+// Step 2 and 3's shared part: acc -> fp32 (a_scale, w_scale, bias) into the tile.
+template <int NB, int RG, int LDW>
+__device__ inline void lin4_tile(float* tile, const v4i (&acc)[RG][NB / 4], float a_scale, const float* w_scale,
+                                 const float* bias, int wv, int r, int gq) {
+#pragma unroll
+    for (int j = 0; j < NB / 4; ++j) {
+        const int n = 16 * ((NB / 4) * wv + j) + r;
+        const float ws = w_scale[n], bs = bias ? bias[n] : 0.0f;
+#pragma unroll
+        for (int rg = 0; rg < RG; ++rg)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float y = (float)acc[rg][j][i] * a_scale;
+                y = y * ws;
+                if (bias) y = y + bs;
+                tile[(16 * rg + 4 * gq + i) * LDW + n] = y;
+            }
+    }
+}
+
+template <bool UP, int NB, int RG, int KT, class Args>
+__global__ __launch_bounds__(256) void rowlin4_k(Args a) {
+    typedef RowLin4<UP, NB, RG, KT> G;
+    constexpr int CN = G::CN, NBW = G::NBW, LDW = G::LDW, R = G::R;
+    __shared__ float tile[R * LDW];
+    __shared__ v4i s_a[RG][KT][64];
+    const int64_t rows = *a.count;
+    if ((int64_t)blockIdx.x * R >= rows) return;  // before the weight loads: most of the grid has no rows
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int r = lane & 15, gq = lane >> 4;
+    int Kin;
+    if constexpr (UP) Kin = a.Cs;
+    else Kin = a.Ck;
+    const int nchunk = Kin >> 4;  // 16-channel chunks of an input row
+    // this wave's B operands: W[16 (NBW wv + j) + r][chunk 4 t + g], every trip
+    v4i bw[KT][NBW];
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+        const int ch = 4 * t + gq;
+#pragma unroll
+        for (int j = 0; j < NBW; ++j)
+            bw[t][j] = ch < nchunk ? *(const v4i*)(a.w + (int64_t)(16 * (NBW * wv + j) + r) * Kin + 16 * ch)
+                                   : v4i{0, 0, 0, 0};
+    }
+    // step 3's rows: wave w takes rows [w R/4, (w + 1) R/4); lanes with r >= R/4 repeat a row and store nothing
+    constexpr int RW = R / 4;
+    const int lr = wv * RW + (r % RW);
+    const bool lact = r < RW;
+    for (int64_t mb = blockIdx.x; mb * R < rows; mb += gridDim.x) {
+        const int64_t m0 = mb * R;
+        // ---- 1. input codes of (row group, trip) tasks
+        for (int task = wv; task < RG * KT; task += 4) {
+            const int rg = RG == 1 ? 0 : task % RG, t = RG == 1 ? task : task / RG;
+            const int64_t o = m0 + 16 * rg + r;
+            const bool row_ok = o < rows;
+            const int ch = 4 * t + gq;
+            const bool on = row_ok && ch < nchunk;
+            v4i av = v4i{0, 0, 0, 0};
+            if constexpr (UP) {
+                const int64_t par = row_ok ? (int64_t)a.parent[o] : 0;
+                const float* src = a.cur + par * a.Cs + 16 * (ch < nchunk ? ch : nchunk - 1);
+                float4 f[4];
+#pragma unroll
+                for (int v = 0; v < 4; ++v) f[v] = *(const float4*)(src + 4 * v);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const float h[4] = {f[v].x, f[v].y, f[v].z, f[v].w};
+                    av[v] = (int)pack_codes4(h, a.in_mult);
+                }
+                if (!on) av = v4i{0, 0, 0, 0};
+            } else {
+                const int4 ci = a.child[row_ok ? o : 0];
+                const int32_t cr[4] = {ci.x, ci.y, ci.z, ci.w};
+                int head[4], nc[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    head[q] = cr[q] & 0x3fffffff;
+                    nc[q] = (int)((uint32_t)cr[q] >> 30);
+                }
+                if (on) {
+                    // the children's 16 channels, two child columns' worth requested at a time, added in child
+                    // row order
+                    float h[16];
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) h[e] = 0.0f;
+#pragma unroll
+                    for (int qp = 0; qp < 4; qp += 2) {
+                        float4 f[2][2][4];
+#pragma unroll
+                        for (int q = 0; q < 2; ++q)
+#pragma unroll
+                            for (int i = 0; i < 2; ++i) {
+                                const int cq = qp + q;
+                                const float* src = a.x + (int64_t)(i < nc[cq] ? head[cq] + i : 0) * a.Ck + 16 * ch;
+#pragma unroll
+                                for (int v = 0; v < 4; ++v) f[q][i][v] = *(const float4*)(src + 4 * v);
+                            }
+#pragma unroll
+                        for (int q = 0; q < 2; ++q)
+#pragma unroll
+                            for (int i = 0; i < 2; ++i)
+                                if (i < nc[qp + q]) {
+#pragma unroll
+                                    for (int v = 0; v < 4; ++v) {
+                                        h[4 * v + 0] = h[4 * v + 0] + f[q][i][v].x;
+                                        h[4 * v + 1] = h[4 * v + 1] + f[q][i][v].y;
+                                        h[4 * v + 2] = h[4 * v + 2] + f[q][i][v].z;
+                                        h[4 * v + 3] = h[4 * v + 3] + f[q][i][v].w;
+                                    }
+                                }
+                    }
+                    const float cnt = (float)(nc[0] + nc[1] + nc[2] + nc[3]);
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const float m4[4] = {h[4 * v] / cnt, h[4 * v + 1] / cnt, h[4 * v + 2] / cnt,
+                                             h[4 * v + 3] / cnt};
+                        av[v] = (int)pack_codes4(m4, a.pool_mult);
+                    }
+                }
+            }
+            s_a[rg][t][lane] = av;
+        }
+        const int64_t o3 = m0 + lr;
+        const bool ok3 = lact && o3 < rows;
+        __syncthreads();
+        // ---- 2. this wave's quarter of the output channels
+        v4i acc[RG][NBW];
+#pragma unroll
+        for (int rg = 0; rg < RG; ++rg)
+#pragma unroll
+            for (int j = 0; j < NBW; ++j) acc[rg][j] = v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int t = 0; t < KT; ++t)
+#pragma unroll
+            for (int rg = 0; rg < RG; ++rg) {
+                const v4i av = s_a[rg][t][lane];
+#pragma unroll
+                for (int j = 0; j < NBW; ++j)
+                    acc[rg][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bw[t][j], acc[rg][j], 0, 0, 0);
+            }
+        lin4_tile<NB, RG, LDW>(tile, acc, a.a_scale, a.w_scale, a.bias, wv, r, gq);
+        __syncthreads();
+        // ---- 3. whole rows: (skip,) the fp32 row, LayerNorm codes
+        float y[NB][4];
+        float4 sk[UP ? NB : 1];
+        if constexpr (UP) {  // the skip rows (NearestUp)
+            const int64_t io = o3 < rows ? o3 : 0;
+#pragma unroll
+            for (int j = 0; j < NB; ++j) sk[j] = *(const float4*)(a.skip + io * CN + 16 * j + 4 * gq);
+        }
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const float4 v = *(const float4*)(tile + lr * LDW + 16 * j + 4 * gq);
+            if constexpr (UP) {
+                y[j][0] = v.x + sk[j].x;
+                y[j][1] = v.y + sk[j].y;
+                y[j][2] = v.z + sk[j].z;
+                y[j][3] = v.w + sk[j].w;
+            } else {
+                y[j][0] = v.x;
+                y[j][1] = v.y;
+                y[j][2] = v.z;
+                y[j][3] = v.w;
+            }
+            if (ok3) *(float4*)(a.y_out + o3 * CN + 16 * j + 4 * gq) = make_float4(y[j][0], y[j][1], y[j][2], y[j][3]);
+        }
+        if (a.gamma) {
+            ln_silu_quad<NB, false>(y, a.gamma, a.beta, 1e-6f, gq);
+            uint32_t pk[NB];
+            silu_codes_packed<NB>(y, a.ln_mult, pk);
+            if (ok3) {
+#pragma unroll
+                for (int j = 0; j < NB; ++j) *(uint32_t*)(a.codes + o3 * CN + 16 * j + 4 * gq) = pk[j];
+            }
+        }
+        __syncthreads();  // the tile and the input codes are rewritten by the next trip
+    }
+}
+
+// Row groups per block of rowlin4_k on level k: one (16-row blocks) when the level is expected to hold at most 4096
+// rows -- a surface keeps about 2 cap / 4^k voxels on level k -- so that its few rows still spread over the CUs (at
+// 16 NB = 256 channels the LayerNorm's registers leave one block per CU); else four (64-row blocks: the weight
+// operands of a block are reused over four row tiles and every lane of the LayerNorm phase holds a row). Measured on
+// the A-shape U-Net (levels 1-4: 183582, 48758, 11016, 2567 rows): PoolDown into level 4 20 us with one row group,
+// 29 us with four; every other PoolDown / NearestUp faster with four.
+static bool rowlin4_rg4(int64_t cap, int k) { return (2 * cap >> (2 * k)) > 4096; }
+
+// Launch of rowlin4_k when it takes the widths (Cout a multiple of 64 up to 256, Cin up to 256); returns -1 when it
+// does not (the caller launches the one-wave-per-16-rows kernel). rg4: four row groups per block (levels with many
+// rows), else one.
+template <bool UP, class Args>
+static int launch_rowlin4(const Args& a, int Cin, int Cout, bool rg4, int64_t cap, hipStream_t s) {
+    if (Cout % 64 != 0 || Cout > 256 || Cin % 16 != 0 || Cin > 256) return -1;
+    const int KT = (Cin / 16 + 3) / 4, NB = Cout / 16;
+    const int R = rg4 ? 64 : 16;
+    int64_t blocks = (cap + R - 1) / R;
+    if (blocks > kRowBlocksMax) blocks = kRowBlocksMax;
+    const dim3 grid((unsigned)blocks);
+#define PMG_RL4(NBV, RGV, KTV) \
+    if (NB == NBV && (rg4 ? 4 : 1) == RGV && KT == KTV) { \
+        hipLaunchKernelGGL((rowlin4_k<UP, NBV, RGV, KTV, Args>), grid, dim3(256), 0, s, a); \
+        return check_launch(UP ? "rowlin4_k (up)" : "rowlin4_k (pool)"); \
+    }
+#define PMG_RL4_KT(NBV, RGV) PMG_RL4(NBV, RGV, 1) PMG_RL4(NBV, RGV, 2) PMG_RL4(NBV, RGV, 3) PMG_RL4(NBV, RGV, 4)
+    PMG_RL4_KT(4, 1) PMG_RL4_KT(4, 4) PMG_RL4_KT(8, 1) PMG_RL4_KT(8, 4)
+    PMG_RL4_KT(12, 1) PMG_RL4_KT(12, 4) PMG_RL4_KT(16, 1) PMG_RL4_KT(16, 4)
+#undef PMG_RL4_KT
+#undef PMG_RL4
+    return -1;
+}
+
 static int launch_gemm(const GemmArgs& g, int epi, bool f16, hipStream_t s, bool narrow = false) {
     PMG_REQUIRE(g.K % 16 == 0 && g.N % 16 == 0 && g.K > 0 && g.N > 0, "GEMM sizes must be multiples of 16");
     if (g.rows_cap == 0) return PMG_OK;
@@ -963,6 +1199,7 @@ struct pmg_unet {
     int4* coords[kMaxLevels] = {};      // [cap] (level 0: the caller's or coords0)
     int32_t* off[kMaxLevels] = {};      // column CSR [ncols + 1] (level 0: NULL)
     int32_t* parent[kMaxLevels] = {};   // level k -> k + 1 [cap]
+    int4* child[kMaxLevels] = {};       // level k + 1 -> its children on level k [cap] (pool_emit_k)
     int32_t* nmap_t[kMaxLevels] = {};   // [27][cap] (levels >= 1)
     uint32_t* tmask[kMaxLevels] = {};   // [cap / 16 + 1]
     float* xd[kMaxLevels] = {};         // down-stage stream = skip [cap][C_k]
@@ -1151,7 +1388,7 @@ static int enqueue_structure(pmg_unet* u, hipStream_t s) {
         hipLaunchKernelGGL(pool_count_k, dim3(gb), dim3(256), 0, s, g, nc, u->scan_excl, u->scan_tiles);
         if (int e = check_launch("pool_count_k")) return e;
         hipLaunchKernelGGL(pool_emit_k, dim3(gb), dim3(256), 0, s, g, nc, u->scan_excl, u->scan_tiles,
-                           u->counts + k + 1, u->coords[k + 1], u->off[k + 1], u->parent[k]);
+                           u->counts + k + 1, u->coords[k + 1], u->off[k + 1], u->parent[k], u->child[k]);
         if (int e = check_launch("pool_emit_k")) return e;
         hipLaunchKernelGGL(nmap_level_k, dim3((unsigned)((u->cap + 255) / 256)), dim3(256), 0, s, u->coords[k + 1],
                            u->off[k + 1], u->counts + k + 1, u->Hk[k + 1], u->Wk[k + 1], u->cap, u->nmap_t[k + 1],
@@ -1241,11 +1478,16 @@ static int enqueue_unet(pmg_unet* u, const float* feats, const int32_t* coords, 
         const pmg_block_weights* nb = !u->down[k + 1].empty() ? &u->down[k + 1][0] : nullptr;
         if (!f16) {  // pool mean + linear + the next block's LayerNorm codes in one kernel
             const pmg_linear_weights& lw = u->pool[k];
-            PoolLinArgs pa{u->xd[k], Ck, Cn, g, u->coords[k + 1], u->counts + k + 1, lw.q_mult,
+            PoolLinArgs pa{u->xd[k], Ck, Cn, g, u->coords[k + 1], u->child[k], u->counts + k + 1, lw.q_mult,
                            (const int8_t*)lw.w, lw.a_scale, lw.w_scale, lw.bias, u->xd[k + 1],
                            nb ? nb->ln_gamma : nullptr, nb ? nb->ln_beta : nullptr, nb ? nb->q1_mult : 1.0f,
                            (int8_t*)u->q1};
-            if (int e = launch_pool_linear_ln(pa, cap, s)) return e;
+            const int rc = launch_rowlin4<false>(pa, Ck, Cn, rowlin4_rg4(cap, k + 1), cap, s);
+            if (rc == -1) {
+                if (int e = launch_pool_linear_ln(pa, cap, s)) return e;
+            } else if (rc) {
+                return rc;
+            }
             continue;
         }
         // fp16 (the teacher): mean pool to fp16 codes, the fp16 GEMM, then the next block's LayerNorm
@@ -1309,7 +1551,12 @@ static int enqueue_unet(pmg_unet* u, const float* feats, const int32_t* coords, 
             UpLinArgs ua{cur, Cs, Ct, u->parent[t], u->counts + t, lw.q_mult, (const int8_t*)lw.w, lw.a_scale,
                          lw.w_scale, lw.bias, u->xd[t], u->xu[t], fb ? fb->ln_gamma : nullptr,
                          fb ? fb->ln_beta : nullptr, fb ? fb->q1_mult : 1.0f, (int8_t*)u->q1};
-            if (int e = launch_up_linear_ln(ua, cap, s)) return e;
+            const int rc = launch_rowlin4<true>(ua, Cs, Ct, rowlin4_rg4(cap, t), cap, s);
+            if (rc == -1) {
+                if (int e = launch_up_linear_ln(ua, cap, s)) return e;
+            } else if (rc) {
+                return rc;
+            }
         } else {  // fp16 (the teacher): quantise, the fp16 GEMM at the coarse level, then the gather + LayerNorm
             hipLaunchKernelGGL(quant_rows_k<_Float16>, dim3(row_grid(cap * Cs / 4)), dim3(256), 0, s, cur, Cs,
                                u->counts + t + 1, 1.0f, (_Float16*)u->codes);
@@ -1489,6 +1736,7 @@ pmg_unet* pmg_unet_create(const pmg_unet_config* cfg) {
         }
         if (k + 1 < L) {
             take((void**)&u->parent[k], 4 * cap);
+            take((void**)&u->child[k], 16 * cap);
             take((void**)&u->xu[k], (size_t)4 * cap * c.channels[k]);
         }
         take((void**)&u->xd[k], (size_t)4 * cap * c.channels[k]);
