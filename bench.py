@@ -280,10 +280,20 @@ def microbench(stream):
         ntu, tmu, nru, rmu = ops.nmap_hash(cd, shape, rows=True, row_mask=True)
         torch.cuda.synchronize()
         hash_ms = graph_ms(lambda: ops.nmap_hash(cd, shape, row_mask=True), 5, stream)
+        # the same map from the (b, x, y) columns' row runs: the set is in _linearise order (as voxelisation and
+        # pool caches leave it); the order is checked on the device inside the timed call, and its status read after
+        sws = ops.sorted_workspace(shape, dev)
+        nts = ops.nmap_sorted(cd, shape, row_mask=True, workspace=sws)[0]
+        torch.cuda.synchronize()
+        sorted_ms = graph_ms(lambda: ops.nmap_sorted(cd, shape, row_mask=True, workspace=sws), 5, stream)
+        if ops.sorted_status(sws) != 0 or not torch.equal(nts, ntu):
+            raise RuntimeError("microbench: the sorted map differs from the hash map")
         pu = int((ntu >= 0).sum().item())
         M = coords.shape[0]
         micro = {"voxels": int(M), "pairs": pu, "mean_active_taps": round(pu / M, 3), "hash_map_ms": round(hash_ms, 4),
-                 "hash_map_gbs": round((16 * M + 108 * M) / (hash_ms * 1e-3) / 1e9, 1)}
+                 "hash_map_gbs": round((16 * M + 108 * M) / (hash_ms * 1e-3) / 1e9, 1),
+                 "sorted_map_ms": round(sorted_ms, 4),
+                 "sorted_map_gbs": round((16 * M + 108 * M) / (sorted_ms * 1e-3) / 1e9, 1)}
         g = torch.Generator(device="cpu").manual_seed(5)
         for Cm in (64, 128):
             # the map's processing order for this width (rows sorted by tap mask within windows of ORDER_WINDOW[Cm]

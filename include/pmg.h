@@ -90,6 +90,19 @@ int pmg_nmap_hash(const int32_t* coords, int64_t M, const int64_t* sparse_shape_
                   int32_t* nmap_rows, uint32_t* tile_mask, uint32_t* row_mask, void* workspace,
                   size_t workspace_bytes, void* stream);
 
+/* pmg_nmap_sorted -- pmg_nmap_hash for coordinates in strictly increasing _linearise order (_core.py:89-94): the
+ * order of _SortedIndex's sorted keys (_core.py:105-124, which sorts them itself) and of the voxel sets that
+ * voxelisation and pool caches produce. Same outputs as pmg_nmap_hash, found through a dense table of the (b, x, y)
+ * columns' row runs instead of a hash. The precondition is checked on the device: a row outside sparse_shape or
+ * not after its predecessor sets bit 0 of the status word (the first 4 bytes of the workspace), and the outputs
+ * are then not valid. Workspace: pmg_sorted_workspace_bytes(sparse_shape) bytes (0: more than 2^31 columns),
+ * 16-byte aligned; its status word must be zero before the first call and is never cleared by a call (sticky);
+ * the rest may hold anything. Calls that share a workspace must not overlap. M < 2^31 - 1. */
+size_t pmg_sorted_workspace_bytes(const int64_t* sparse_shape_host);
+int pmg_nmap_sorted(const int32_t* coords, int64_t M, const int64_t* sparse_shape_host, int32_t* nmap_t,
+                    int32_t* nmap_rows, uint32_t* tile_mask, uint32_t* row_mask, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
 /* pmg_row_order -- a processing order for pmg_spconv_i8_ordered (no counterpart in the reference; it changes no
  * result): within each window of `window` consecutive rows (0: one window), the rows sorted, stably, by their
  * 27-bit tap mask (row_mask [M], bit v = tap v present, as pmg_nmap_hash writes it), so that the tiles and chunks

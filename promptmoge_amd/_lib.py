@@ -99,6 +99,8 @@ SIGNATURES = {
     "pmg_nmap_column": (i32, [vp, vp, i32, i32, i32, vp, vp, vp, vp, vp]),
     "pmg_hash_workspace_bytes": (sz, [i64]),
     "pmg_nmap_hash": (i32, [vp, i64, vp, vp, vp, vp, vp, vp, sz, vp]),
+    "pmg_sorted_workspace_bytes": (sz, [vp]),
+    "pmg_nmap_sorted": (i32, [vp, i64, vp, vp, vp, vp, vp, vp, sz, vp]),
     "pmg_pool_cache_workspace_bytes": (sz, [i64]),
     "pmg_pool_cache": (i32, [vp, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]),
     "pmg_sparse_pool": (i32, [vp, i64, i32, vp, vp, i64, i32, vp, vp]),

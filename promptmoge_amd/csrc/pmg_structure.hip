@@ -384,6 +384,141 @@ __global__ __launch_bounds__(256) void brick_query_k(const int4* __restrict__ co
 }
 
 // ------------------------------------------------------------------------------------------------------------
+// Generic map for coordinates in increasing _linearise order (_core.py:89-94): the order of _SortedIndex's sorted
+// keys (_core.py:105-124), and the order voxelisation and pool caches produce. The voxels of a (b, x, y) column are
+// then one contiguous run in increasing z, so a dense table over the B * X * Y columns holds each run's [start, end)
+// and a neighbour is found in its column's run: no hashing, no atomics, no probing. The table is never cleared:
+// sorted_heads_k rewrites the entry of every column this set holds, and an entry is trusted only if it names a row
+// range of this set whose first row lies in that column, which no stale entry of an absent column can.
+
+__device__ inline uint64_t lin_key_u(const int4& c, const Shape4& S) {
+    return (((uint64_t)(uint32_t)c.x * (uint64_t)S.s1 + (uint32_t)c.y) * (uint64_t)S.s2 + (uint32_t)c.z) *
+               (uint64_t)S.s3 + (uint32_t)c.w;
+}
+
+// Each row checks that it lies inside the shape and follows the previous row in _linearise order (else the status
+// word gets bit 0: the map is then not valid); the first and last rows of a column's run write its table entry.
+// Columns are numbered (b X + x) Y + y < 2^31.
+__global__ __launch_bounds__(256) void sorted_heads_k(const int4* __restrict__ coords, int64_t M, Shape4 S,
+                                                      int2* __restrict__ cols, uint32_t* __restrict__ status) {
+    const int64_t m = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (m >= M) return;
+    const int4 c = coords[m];
+    const int4 pv = coords[m > 0 ? m - 1 : 0];
+    const int4 nx = coords[m + 1 < M ? m + 1 : m];
+    const bool inside = in_shape(c.x, c.y, c.z, c.w, S);
+    const bool bad = !inside || (m > 0 && !(lin_key_u(pv, S) < lin_key_u(c, S)));
+    if (bad) {
+        __hip_atomic_fetch_or(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    const bool first = m == 0 || pv.x != c.x || pv.y != c.y || pv.z != c.z;
+    const bool last = m + 1 == M || nx.x != c.x || nx.y != c.y || nx.z != c.z;
+    int32_t* e = (int32_t*)&cols[((uint32_t)c.x * (uint32_t)S.s1 + (uint32_t)c.y) * (uint32_t)S.s2 + (uint32_t)c.z];
+    if (first) e[0] = (int32_t)m;
+    if (last) e[1] = (int32_t)(m + 1);
+}
+
+// Query (_SortedIndex.lookup semantics, _core.py:114-124): the 9 neighbouring columns' entries are loaded together
+// and validated by their first rows; in each run the lower bound of z - 1 (the first row itself, or a binary search
+// in lock step over the columns that start lower, bounded by the row z - 1 would have without gaps), then the rows
+// holding z - 1, z, z + 1 among the next three, each placed by its z. Same outputs as brick_query_k.
+__global__ __launch_bounds__(256) void sorted_query_k(const int4* __restrict__ coords, int64_t M, Shape4 S,
+                                                      const int2* __restrict__ cols, int32_t* __restrict__ nmap_t,
+                                                      int32_t* __restrict__ nmap_rows, uint32_t* tile_mask,
+                                                      uint32_t* __restrict__ row_mask) {
+    const int64_t m = xcd_chunk(blockIdx.x, gridDim.x) * 256 + threadIdx.x;
+    uint32_t rmask = 0;
+    if (m < M) {
+        const int4 c = coords[m];
+        const int zlo = c.w - 1;
+        const int X = (int)S.s1, Y = (int)S.s2;
+        const uint32_t cb = (uint32_t)c.x * (uint32_t)X;
+        int2 r[9];
+        bool in[9];
+#pragma unroll
+        for (int k = 0; k < 9; ++k) {
+            const int x = c.y + k / 3 - 1, y = c.z + k % 3 - 1;
+            in[k] = x >= 0 && x < X && y >= 0 && y < Y;
+            r[k] = cols[in[k] ? (cb + (uint32_t)x) * (uint32_t)Y + (uint32_t)y : 0u];  // the 9 loads together
+        }
+        int4 h[9];
+#pragma unroll
+        for (int k = 0; k < 9; ++k) {
+            in[k] = in[k] && r[k].x >= 0 && r[k].x < r[k].y && (int64_t)r[k].y <= M;
+            h[k] = coords[in[k] ? r[k].x : 0];
+        }
+        // lo: the first row of the run with z >= z - 1 (searched over [lo, hi) when the run starts lower)
+        int32_t lo[9], hi[9];
+        bool srch = false, below[9];
+#pragma unroll
+        for (int k = 0; k < 9; ++k) {
+            const int x = c.y + k / 3 - 1, y = c.z + k % 3 - 1;
+            in[k] = in[k] && h[k].x == c.x && h[k].y == x && h[k].z == y;
+            // z rises by at least 1 per row, so the row start + (z - 1 - z_first) + 1 already lies above z - 1
+            below[k] = in[k] && h[k].w < zlo;
+            const bool below = below[k];
+            const int64_t cap = (int64_t)r[k].x + ((int64_t)zlo - h[k].w) + 1;
+            lo[k] = below ? r[k].x + 1 : r[k].x;
+            hi[k] = below ? (int32_t)(cap < r[k].y ? cap : r[k].y) : r[k].x;
+            srch = srch || hi[k] > lo[k];
+        }
+        while (srch) {  // every search range halves per trip
+            int zm[9];
+#pragma unroll
+            for (int k = 0; k < 9; ++k) zm[k] = coords[hi[k] > lo[k] ? lo[k] + (hi[k] - lo[k]) / 2 : 0].w;
+            srch = false;
+#pragma unroll
+            for (int k = 0; k < 9; ++k) {
+                if (hi[k] > lo[k]) {
+                    const int32_t mid = lo[k] + (hi[k] - lo[k]) / 2;
+                    if (zm[k] < zlo) lo[k] = mid + 1;
+                    else hi[k] = mid;
+                    srch = srch || hi[k] > lo[k];
+                }
+            }
+        }
+        // rows lo, lo + 1, lo + 2 hold the run's z values from z - 1 up, in order: each is placed by its z. Where
+        // no search ran, row lo is the first row (its z is known) and row lo + j lies at or above z_first + j, so
+        // only rows that can still hold z + 1 or below are read.
+        int hit[27];
+#pragma unroll
+        for (int v = 0; v < 27; ++v) hit[v] = -1;
+#pragma unroll
+        for (int k = 0; k < 9; ++k) {
+            const int jmax = below[k] ? 2 : c.w + 1 - h[k].w;
+            int zf[3];
+#pragma unroll
+            for (int j = 0; j < 3; ++j) {
+                zf[j] = j == 0 && !below[k] ? h[k].w : INT_MIN;
+                if (in[k] && j <= jmax && lo[k] + j < r[k].y && (j > 0 || below[k])) zf[j] = coords[lo[k] + j].w;
+            }
+#pragma unroll
+            for (int j = 0; j < 3; ++j) {
+                const int dz = zf[j] - zlo;
+                const bool ok = in[k] && j <= jmax && lo[k] + j < r[k].y;
+#pragma unroll
+                for (int d = 0; d < 3; ++d)
+                    if (ok && dz == d) hit[3 * k + d] = lo[k] + j;
+            }
+        }
+#pragma unroll
+        for (int v = 0; v < 27; ++v) rmask |= (hit[v] >= 0 ? 1u : 0u) << v;
+        if (nmap_t) {
+            int32_t* o = nmap_t + m;
+#pragma unroll
+            for (int v = 0; v < 27; ++v) o[(int64_t)v * M] = hit[v];
+        }
+        if (nmap_rows) {
+#pragma unroll
+            for (int v = 0; v < 27; ++v) nmap_rows[m * 27 + v] = hit[v];
+        }
+        if (row_mask) row_mask[m] = rmask;
+    }
+    store_tile_mask(rmask, m, M, tile_mask);
+}
+
+// ------------------------------------------------------------------------------------------------------------
 // Row-major (M, 27) -> tap-major [27][M] plus tile masks.
 __global__ __launch_bounds__(256) void nmap_from_rows_k(const int32_t* __restrict__ rows, int64_t M,
                                                         int32_t* __restrict__ nmap_t, uint32_t* tile_mask) {
@@ -577,6 +712,39 @@ int pmg_nmap_hash(const int32_t* coords, int64_t M, const int64_t* shape, int32_
     hipLaunchKernelGGL(brick_query_k, g, dim3(256), 0, s, (const int4*)coords, M, T, nmap_t, nmap_rows, tile_mask,
                        row_mask);
     return check_launch("brick_query_k");
+}
+
+size_t pmg_sorted_workspace_bytes(const int64_t* shape) {
+    if (!shape) return 0;
+    for (int d = 0; d < 3; ++d)
+        if (shape[d] <= 0) return 0;
+    const double cols = (double)shape[0] * (double)shape[1] * (double)shape[2];
+    if (cols > (double)((int64_t)1 << 31)) return 0;
+    return 256 + (size_t)cols * sizeof(int2);
+}
+
+int pmg_nmap_sorted(const int32_t* coords, int64_t M, const int64_t* shape, int32_t* nmap_t, int32_t* nmap_rows,
+                    uint32_t* tile_mask, uint32_t* row_mask, void* workspace, size_t workspace_bytes, void* stream) {
+    PMG_REQUIRE(coords && shape, "null argument");
+    PMG_REQUIRE(M >= 0 && M < ((int64_t)1 << 31) - 1, "bad voxel count");
+    PMG_REQUIRE(aligned16(coords), "coords must be 16-byte aligned");
+    for (int d = 0; d < 4; ++d) PMG_REQUIRE(shape[d] > 0 && shape[d] <= INT_MAX, "bad sparse shape");
+    const double span = (double)shape[0] * (double)shape[1] * (double)shape[2] * (double)shape[3];
+    PMG_REQUIRE(span < 1.8e19, "sparse shape too large for 64-bit keys");
+    const size_t need = pmg_sorted_workspace_bytes(shape);
+    PMG_REQUIRE(need > 0, "more than 2^31 (b, x, y) columns");
+    PMG_REQUIRE(workspace && workspace_bytes >= need && aligned16(workspace), "workspace too small");
+    if (M == 0) return PMG_OK;
+    hipStream_t s = (hipStream_t)stream;
+    const Shape4 S{shape[0], shape[1], shape[2], shape[3]};
+    uint32_t* status = (uint32_t*)workspace;
+    int2* cols = (int2*)((char*)workspace + 256);
+    const dim3 g((unsigned)((M + 255) / 256));
+    hipLaunchKernelGGL(sorted_heads_k, g, dim3(256), 0, s, (const int4*)coords, M, S, cols, status);
+    if (int e = check_launch("sorted_heads_k")) return e;
+    hipLaunchKernelGGL(sorted_query_k, g, dim3(256), 0, s, (const int4*)coords, M, S, (const int2*)cols, nmap_t,
+                       nmap_rows, tile_mask, row_mask);
+    return check_launch("sorted_query_k");
 }
 
 int pmg_nmap_from_rows(const int32_t* nmap_rows, int64_t M, int32_t* nmap_t, uint32_t* tile_mask, void* stream) {

@@ -113,6 +113,46 @@ def nmap_hash(coords: torch.Tensor, sparse_shape: Sequence[int], *, taps: bool =
     return (nt, tm, nr, rm) if row_mask else (nt, tm, nr)
 
 
+def sorted_workspace(sparse_shape: Sequence[int], device) -> torch.Tensor:
+    """A workspace for nmap_sorted: its status word zeroed, the rest uninitialised (reusable by later calls)."""
+    shape = (C.c_int64 * 4)(*[int(s) for s in sparse_shape[:4]])
+    nbytes = lib().pmg_sorted_workspace_bytes(shape)
+    if nbytes == 0:
+        raise ValueError("nmap_sorted: more than 2^31 (b, x, y) columns")
+    ws = torch.empty((nbytes,), dtype=torch.uint8, device=device)
+    ws[:256].zero_()
+    return ws
+
+
+def sorted_status(ws: torch.Tensor) -> int:
+    """The status word of an nmap_sorted workspace (reads it back): 0 while every call saw sorted coordinates."""
+    return int(ws[:4].view(torch.int32).item())
+
+
+def nmap_sorted(coords: torch.Tensor, sparse_shape: Sequence[int], *, taps: bool = True, rows: bool = False,
+                row_mask: bool = False, workspace: Optional[torch.Tensor] = None):
+    """nmap_hash for coords in strictly increasing _linearise order (the order _SortedIndex sorts into): the same
+    outputs, from the (b, x, y) columns' row runs. The order is checked on the device; `workspace` (sorted_workspace)
+    carries the sticky status word, read with sorted_status -- without one, a fresh workspace is checked here (one
+    synchronisation) and a violation raises."""
+    coords = _dev(coords, "coords", torch.int32)
+    if coords.ndim != 2 or coords.shape[1] != 4:
+        raise ValueError("coords must be (M, 4)")
+    M = coords.shape[0]
+    dev = coords.device
+    own = workspace is None
+    ws = sorted_workspace(sparse_shape, dev) if own else workspace
+    nt = torch.empty((27, M), dtype=torch.int32, device=dev) if taps else None
+    nr = torch.empty((M, 27), dtype=torch.int32, device=dev) if rows else None
+    tm = torch.empty(((M + 15) // 16,), dtype=torch.int32, device=dev)
+    rm = torch.empty((M,), dtype=torch.int32, device=dev) if row_mask else None
+    shape = (C.c_int64 * 4)(*[int(s) for s in sparse_shape[:4]])
+    call("pmg_nmap_sorted", _p(coords), M, shape, _p(nt), _p(nr), _p(tm), _p(rm), _p(ws), ws.numel(), _stream())
+    if own and sorted_status(ws) != 0:
+        raise ValueError("nmap_sorted: coords are not in increasing _linearise order (or lie outside sparse_shape)")
+    return (nt, tm, nr, rm) if row_mask else (nt, tm, nr)
+
+
 ROW_ORDER_WINDOW = 1 << 18
 
 

@@ -66,6 +66,15 @@ def test_invalid_shapes_rejected_on_host(libpmg):
     big = (C.c_int64 * 4)(1 << 20, 1 << 20, 1 << 20, 1 << 20)
     assert libpmg.pmg_nmap_hash(C.c_void_p(16), 5, big, None, None, None, None, dummy, 1 << 30,
                                 None) == _lib.PMG_E_INVALID
+    # sorted map: workspace too small, unaligned workspace, more than 2^31 columns
+    sh = (C.c_int64 * 4)(1, 64, 64, 64)
+    assert libpmg.pmg_nmap_sorted(C.c_void_p(16), 5, sh, None, None, None, None, C.c_void_p(256), 64,
+                                  None) == _lib.PMG_E_INVALID
+    assert libpmg.pmg_nmap_sorted(C.c_void_p(16), 5, sh, None, None, None, None, C.c_void_p(260), 1 << 20,
+                                  None) == _lib.PMG_E_INVALID
+    wide = (C.c_int64 * 4)(4, 1 << 16, 1 << 16, 8)
+    assert libpmg.pmg_nmap_sorted(C.c_void_p(16), 5, wide, None, None, None, None, C.c_void_p(256), 1 << 40,
+                                  None) == _lib.PMG_E_INVALID
     # ordered conv: only Ci = Co = 64 / 128
     assert libpmg.pmg_spconv_i8_ordered(dummy, dummy, dummy, dummy, 10, 32, 32, dummy, 0, 1.0, dummy, None, 1.0,
                                         None, dummy, None) == _lib.PMG_E_INVALID
@@ -79,6 +88,9 @@ def test_refiner_create_rejects_bad_config(libpmg):
 
 def test_workspace_sizes(libpmg):
     assert libpmg.pmg_hash_workspace_bytes(1_000_000) >= 4 * 1_000_000 * 12
+    # sorted map: a status line plus a (start, end) run per (b, x, y) column; 0 beyond 2^31 columns
+    assert libpmg.pmg_sorted_workspace_bytes((C.c_int64 * 4)(2, 1024, 1024, 1024)) == 256 + 8 * 2 * 1024 * 1024
+    assert libpmg.pmg_sorted_workspace_bytes((C.c_int64 * 4)(4, 1 << 16, 1 << 16, 8)) == 0
     assert libpmg.pmg_fit_workspace_bytes(307_200, 10) >= 10 * 3 * 2048 * 4
     assert libpmg.pmg_kmap_workspace_bytes(1000) >= 27 * 4 * 4
 

@@ -92,6 +92,9 @@ def test_microbench_set_map_and_conv(gpu, C):
     nmap = ost.nmap_sorted(coords, shape)
     assert np.array_equal(nt.cpu().numpy().T, nmap)
     assert np.array_equal(tm.cpu().numpy().view(np.uint32), ost.tile_masks(nmap))
+    # the set is in _linearise order: the column-run map is the same map
+    st, stm, snr, srm = ops.nmap_sorted(torch.from_numpy(coords).to(gpu), shape, rows=True, row_mask=True)
+    assert torch.equal(st, nt) and torch.equal(stm, tm) and torch.equal(snr, nr) and torch.equal(srm, rm)
     rng = np.random.default_rng(C)
     x = rng.integers(-127, 128, size=(M, C)).astype(np.int8)
     w = rng.integers(-127, 128, size=(C, 3, 3, 3, C)).astype(np.int8)

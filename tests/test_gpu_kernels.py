@@ -186,6 +186,61 @@ def test_hash_map_surface_voxels(gpu):
     assert 6 <= occ <= 16, occ  # surface-like occupancy
 
 
+def _lin_sorted(coords, shape):
+    """coords in increasing _linearise order (_core.py:89-94)."""
+    key = np.zeros(coords.shape[0], np.int64)
+    for d in range(4):
+        key = key * shape[d] + coords[:, d]
+    return coords[np.argsort(key, kind="stable")]
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_sorted_map_generic(gpu, seed):
+    """nmap_sorted on a sorted set equals the oracle's sorted map (rows, taps, tile and row masks), with voxels on
+    every face of a shape and two batch items."""
+    announce(f"sorted map generic seed={seed}")
+    rng = np.random.default_rng(seed)
+    shape = (2, 40, 50, 60)
+    allc = np.stack(np.meshgrid(*[np.arange(s) for s in shape], indexing="ij"), -1).reshape(-1, 4)
+    coords = _lin_sorted(allc[rng.random(allc.shape[0]) < 0.15].astype(np.int32), shape)
+    ref = ost.nmap_sorted(coords, shape)
+    nt, tm, nr, rm = ops.nmap_sorted(_t(coords, gpu), shape, taps=True, rows=True, row_mask=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(nr.cpu().numpy(), ref)
+    assert np.array_equal(nt.cpu().numpy(), ref.T)
+    assert np.array_equal(tm.cpu().numpy().view(np.uint32), ost.tile_masks(ref))
+    bits = ((ref >= 0).astype(np.uint64) << np.arange(27, dtype=np.uint64)).sum(1).astype(np.uint32)
+    assert np.array_equal(rm.cpu().numpy().view(np.uint32), bits)
+
+
+def test_sorted_map_long_columns_stale_table_and_order_check(gpu):
+    """Columns of up to 200 voxels (the binary search of the run), a workspace reused by a second, different set
+    (its table entries from the first set must not be trusted), and an unsorted set, which the device check
+    reports through the sticky status word."""
+    announce("sorted map long columns, stale table, order check")
+    rng = np.random.default_rng(7)
+    shape = (1, 24, 20, 200)
+    ws = ops.sorted_workspace(shape, gpu)
+    sets = []
+    for dens in (0.9, 0.3):
+        allc = np.stack(np.meshgrid(*[np.arange(s) for s in shape], indexing="ij"), -1).reshape(-1, 4)
+        keep = rng.random(allc.shape[0]) < dens * (allc[:, 1] % 3 != 1)  # some columns empty, others dense
+        sets.append(_lin_sorted(allc[keep].astype(np.int32), shape))
+    for coords in sets:
+        ref = ost.nmap_sorted(coords, shape)
+        nt, tm, nr = ops.nmap_sorted(_t(coords, gpu), shape, rows=True, workspace=ws)
+        torch.cuda.synchronize()
+        assert np.array_equal(nr.cpu().numpy(), ref)
+        assert np.array_equal(tm.cpu().numpy().view(np.uint32), ost.tile_masks(ref))
+    assert ops.sorted_status(ws) == 0
+    bad = sets[1].copy()
+    bad[[10, 11]] = bad[[11, 10]]
+    ops.nmap_sorted(_t(bad, gpu), shape, workspace=ws)
+    assert ops.sorted_status(ws) == 1
+    with pytest.raises(ValueError, match="increasing"):
+        ops.nmap_sorted(_t(bad, gpu), shape)
+
+
 def test_kmap_and_rows(gpu):
     announce("kmap compact + nmap_from_rows")
     cfg, sc = _scene("B")
