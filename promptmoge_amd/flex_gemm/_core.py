@@ -171,8 +171,10 @@ def build_submanifold_cache(coords: Tensor, sparse_shape: Sequence[int], kernel_
                             dilation: Optional[Sequence[int]] = None,
                             backend: Literal["auto", "column", "sorted", "hash"] = "auto") -> NeighborCache:
     """Neighbour map of `coords` with itself (_core.py:307-336). backend "auto" uses the GPU column stencil when the
-    coords are one voxel per pixel column in raster order (level 0) and the GPU hash otherwise; "sorted" is
-    accepted as a name for the generic map (the hash gives the same map as the reference's sorted backend)."""
+    coords are one voxel per pixel column in raster order (level 0); otherwise (and for "sorted") the column-run
+    map when the coords are in increasing _linearise order (checked on the device, read in one host
+    synchronisation, as the column test is), else the GPU hash ("hash": always). All give the reference's sorted
+    backend's map."""
     D = len(kernel_size)
     batch_dims = coords.shape[1] - D
     dilation = tuple(dilation) if dilation is not None else (1,) * D
@@ -191,8 +193,15 @@ def build_submanifold_cache(coords: Tensor, sparse_shape: Sequence[int], kernel_
         nmap_t, tile_mask, _, _ = _ops.nmap_column(zq)
         used = "column"
     else:
-        nmap_t, tile_mask, _ = _ops.nmap_hash(c32, [int(s) for s in sparse_shape[:4]])
+        shape4 = [int(s) for s in sparse_shape[:4]]
         used = "hash"
+        if backend in ("auto", "sorted") and _ops.sorted_workspace_fits(shape4):
+            ws = _ops.sorted_workspace(shape4, c32.device)
+            nmap_t, tile_mask, _ = _ops.nmap_sorted(c32, shape4, workspace=ws)
+            if _ops.sorted_status(ws) == 0:
+                used = "sorted"
+        if used == "hash":
+            nmap_t, tile_mask, _ = _ops.nmap_hash(c32, shape4)
     return NeighborCache(coords, coords, nmap_t=nmap_t, tile_mask=tile_mask, num_kernels=27,
                          kernel_size=tuple(kernel_size), dilation=dilation, input_sparse_shape=sparse_shape,
                          output_sparse_shape=sparse_shape, symmetric=True, build_backend=used)

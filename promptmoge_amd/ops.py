@@ -124,6 +124,12 @@ def sorted_workspace(sparse_shape: Sequence[int], device) -> torch.Tensor:
     return ws
 
 
+def sorted_workspace_fits(sparse_shape: Sequence[int]) -> bool:
+    """Whether nmap_sorted takes this sparse shape (at most 2^31 (b, x, y) columns)."""
+    shape = (C.c_int64 * 4)(*[int(s) for s in sparse_shape[:4]])
+    return lib().pmg_sorted_workspace_bytes(shape) > 0
+
+
 def sorted_status(ws: torch.Tensor) -> int:
     """The status word of an nmap_sorted workspace (reads it back): 0 while every call saw sorted coordinates."""
     return int(ws[:4].view(torch.int32).item())

@@ -115,6 +115,21 @@ def test_cache_generic_uses_hash(gpu):
 
 
 @pytest.mark.gpu
+def test_cache_sorted_set_uses_column_runs(gpu):
+    """A set in _linearise order takes the column-run map (the same map); backend "hash" forces the hash."""
+    announce("flex_gemm cache sorted set")
+    coords = spec.make_voxels(20_000, 64, seed=6).astype(np.int32)  # lexicographically sorted
+    shape = (1, 64, 64, 64)
+    ref = ost.nmap_sorted(coords, shape)
+    cache = fg.ops.build_submanifold_cache(torch.from_numpy(coords).to(gpu), shape, (3, 3, 3))
+    assert cache.build_backend == "sorted"
+    assert np.array_equal(cache.nmap.cpu().numpy(), ref)
+    forced = fg.ops.build_submanifold_cache(torch.from_numpy(coords).to(gpu), shape, (3, 3, 3), backend="hash")
+    assert forced.build_backend == "hash"
+    assert np.array_equal(forced.nmap.cpu().numpy(), ref)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("dtype,ci,co", [(torch.float32, 32, 48), (torch.float32, 6, 10), (torch.float16, 64, 64),
                                          (torch.bfloat16, 16, 32), (torch.float32, 64, 64), (torch.float16, 32, 32),
                                          (torch.float16, 128, 128), (torch.bfloat16, 64, 64)])
