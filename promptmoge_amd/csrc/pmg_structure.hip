@@ -450,14 +450,13 @@ __global__ __launch_bounds__(256) void sorted_query_k(const int4* __restrict__ c
         }
         // lo: the first row of the run with z >= z - 1 (searched over [lo, hi) when the run starts lower)
         int32_t lo[9], hi[9];
-        bool srch = false, below[9];
+        bool srch = false;
 #pragma unroll
         for (int k = 0; k < 9; ++k) {
             const int x = c.y + k / 3 - 1, y = c.z + k % 3 - 1;
             in[k] = in[k] && h[k].x == c.x && h[k].y == x && h[k].z == y;
             // z rises by at least 1 per row, so the row start + (z - 1 - z_first) + 1 already lies above z - 1
-            below[k] = in[k] && h[k].w < zlo;
-            const bool below = below[k];
+            const bool below = in[k] && h[k].w < zlo;
             const int64_t cap = (int64_t)r[k].x + ((int64_t)zlo - h[k].w) + 1;
             lo[k] = below ? r[k].x + 1 : r[k].x;
             hi[k] = below ? (int32_t)(cap < r[k].y ? cap : r[k].y) : r[k].x;
@@ -478,25 +477,19 @@ __global__ __launch_bounds__(256) void sorted_query_k(const int4* __restrict__ c
                 }
             }
         }
-        // rows lo, lo + 1, lo + 2 hold the run's z values from z - 1 up, in order: each is placed by its z. Where
-        // no search ran, row lo is the first row (its z is known) and row lo + j lies at or above z_first + j, so
-        // only rows that can still hold z + 1 or below are read.
+        // rows lo, lo + 1, lo + 2 hold the run's z values from z - 1 up, in order: each is placed by its z
         int hit[27];
 #pragma unroll
         for (int v = 0; v < 27; ++v) hit[v] = -1;
 #pragma unroll
         for (int k = 0; k < 9; ++k) {
-            const int jmax = below[k] ? 2 : c.w + 1 - h[k].w;
             int zf[3];
 #pragma unroll
-            for (int j = 0; j < 3; ++j) {
-                zf[j] = j == 0 && !below[k] ? h[k].w : INT_MIN;
-                if (in[k] && j <= jmax && lo[k] + j < r[k].y && (j > 0 || below[k])) zf[j] = coords[lo[k] + j].w;
-            }
+            for (int j = 0; j < 3; ++j) zf[j] = coords[in[k] && lo[k] + j < r[k].y ? lo[k] + j : 0].w;
 #pragma unroll
             for (int j = 0; j < 3; ++j) {
                 const int dz = zf[j] - zlo;
-                const bool ok = in[k] && j <= jmax && lo[k] + j < r[k].y;
+                const bool ok = in[k] && lo[k] + j < r[k].y;
 #pragma unroll
                 for (int d = 0; d < 3; ++d)
                     if (ok && dz == d) hit[3 * k + d] = lo[k] + j;

@@ -1238,6 +1238,12 @@ struct pmg_unet {
     std::vector<pmg_linear_weights> pool, up;
     pmg_linear_weights enc{}, fuse0{}, fuse2{};
 
+    // the level structure is built on a side stream beside the level-0 layers (a parallel branch of the captured
+    // graph): fork after the level-0 coordinates, join before each level's first use
+    hipStream_t side = nullptr;
+    hipEvent_t ev_fork = nullptr;
+    hipEvent_t ev_level[kMaxLevels] = {};
+
     GraphCache graphs;
 };
 
@@ -1379,8 +1385,9 @@ static int linear(pmg_unet* u, const void* a, const int64_t* rows_dev, int64_t r
     return launch_gemm(g, epi, u->cfg.precision == PMG_PREC_FP16, s, narrow);
 }
 
-// The level structure (levels 1 .. L-1) from the level-0 coordinates.
-static int enqueue_structure(pmg_unet* u, hipStream_t s) {
+// The level structure (levels 1 .. L-1) from the level-0 coordinates; with `done`, level k + 1's event is recorded
+// after its kernels.
+static int enqueue_structure(pmg_unet* u, hipStream_t s, hipEvent_t* done = nullptr) {
     for (int k = 0; k + 1 < u->L; ++k) {
         PoolGeom g{u->coords[k], u->off[k], u->cfg.B, u->Hk[k], u->Wk[k], u->Hk[k + 1], u->Wk[k + 1]};
         const int64_t nc = u->ncols[k + 1];
@@ -1394,6 +1401,7 @@ static int enqueue_structure(pmg_unet* u, hipStream_t s) {
                            u->off[k + 1], u->counts + k + 1, u->Hk[k + 1], u->Wk[k + 1], u->cap, u->nmap_t[k + 1],
                            u->tmask[k + 1]);
         if (int e = check_launch("nmap_level_k")) return e;
+        if (done) PMG_CHECK_HIP(hipEventRecord(done[k + 1], s));
     }
     return PMG_OK;
 }
@@ -1466,13 +1474,17 @@ static int enqueue_unet(pmg_unet* u, const float* feats, const int32_t* coords, 
     in.zkeys = zkeys;
     in.zkey_stride = 4;
     const bool f16 = c.precision == PMG_PREC_FP16;
+    // the level structure on the side stream, concurrent with the input stage and the level-0 blocks
+    PMG_CHECK_HIP(hipEventRecord(u->ev_fork, s));
+    PMG_CHECK_HIP(hipStreamWaitEvent(u->side, u->ev_fork, 0));
+    if (int e = enqueue_structure(u, u->side, u->ev_level)) return e;
     if (int e = launch_input_stage(in, f16, s)) return e;
-    if (int e = enqueue_structure(u, s)) return e;
 
     // down stages and PoolDown (sparse_unet.py:223-231; flex_sparse_blocks.py:85-90)
     for (int k = 0; k < L; ++k) {
         if (int e = enqueue_stage(u, k, u->down[k], u->xd[k], nullptr, s)) return e;
         if (k + 1 == L) break;
+        PMG_CHECK_HIP(hipStreamWaitEvent(s, u->ev_level[k + 1], 0));  // level k + 1's structure is built
         const int Ck = c.channels[k], Cn = c.channels[k + 1];
         PoolGeom g{u->coords[k], u->off[k], c.B, u->Hk[k], u->Wk[k], u->Hk[k + 1], u->Wk[k + 1]};
         const pmg_block_weights* nb = !u->down[k + 1].empty() ? &u->down[k + 1][0] : nullptr;
@@ -1780,12 +1792,25 @@ pmg_unet* pmg_unet_create(const pmg_unet_config* cfg) {
         delete u;
         return nullptr;
     }
+    bool ok = hipStreamCreateWithFlags(&u->side, hipStreamNonBlocking) == hipSuccess &&
+              hipEventCreateWithFlags(&u->ev_fork, hipEventDisableTiming) == hipSuccess;
+    for (int k = 1; k < L && ok; ++k) ok = hipEventCreateWithFlags(&u->ev_level[k], hipEventDisableTiming) == hipSuccess;
+    if (!ok) {
+        set_error("pmg_unet_create: creating the structure stream or its events failed");
+        pmg_unet_destroy(u);
+        return nullptr;
+    }
     return u;
 }
 
 void pmg_unet_destroy(pmg_unet* u) {
     if (!u) return;
     u->graphs.clear();
+    if (u->side) (void)hipStreamSynchronize(u->side);
+    for (int k = 0; k < kMaxLevels; ++k)
+        if (u->ev_level[k]) (void)hipEventDestroy(u->ev_level[k]);
+    if (u->ev_fork) (void)hipEventDestroy(u->ev_fork);
+    if (u->side) (void)hipStreamDestroy(u->side);
     if (u->step_arena) (void)hipFree(u->step_arena);
     if (u->arena) (void)hipFree(u->arena);
     delete u;
