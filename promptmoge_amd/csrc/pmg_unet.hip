@@ -1243,6 +1243,7 @@ struct pmg_unet {
     hipStream_t side = nullptr;
     hipEvent_t ev_fork = nullptr;
     hipEvent_t ev_level[kMaxLevels] = {};
+    hipEvent_t ev_enc = nullptr;  // the encoder tokens (also made on the side stream)
 
     GraphCache graphs;
 };
@@ -1478,6 +1479,26 @@ static int enqueue_unet(pmg_unet* u, const float* feats, const int32_t* coords, 
     PMG_CHECK_HIP(hipEventRecord(u->ev_fork, s));
     PMG_CHECK_HIP(hipStreamWaitEvent(u->side, u->ev_fork, 0));
     if (int e = enqueue_structure(u, u->side, u->ev_level)) return e;
+    // then, on the same side stream, the encoder conditioning's tokens: the encoder feature quantised and
+    // transposed, times encoder_fuse (+ the planar bias map) per token (sparse_unet.py:160-174, 227-232)
+    {
+        const int CL = c.channels[L - 1];
+        const dim3 grid((unsigned)(((int64_t)u->R * u->Cc + 63) / 64), (unsigned)((c.enc_channels + 63) / 64),
+                        (unsigned)c.B);
+        if (f16)
+            hipLaunchKernelGGL(enc_quant_k<_Float16>, grid, dim3(256), 0, u->side, enc_feat, c.enc_channels,
+                               (int64_t)u->R * u->Cc, 1.0f, (_Float16*)u->enc_codes);
+        else
+            hipLaunchKernelGGL(enc_quant_k<int8_t>, grid, dim3(256), 0, u->side, enc_feat, c.enc_channels,
+                               (int64_t)u->R * u->Cc, u->enc.q_mult, (int8_t*)u->enc_codes);
+        if (int e = check_launch("enc_quant_k")) return e;
+        // the encoder tokens and the deepest level are a few thousand rows with long K: one 16-column block per
+        // wave gives the GEMM four times the waves (Model A: encoder_fuse 20 -> 13 us, fuse_proj 30 -> 28 us)
+        if (int e = linear(u, u->enc_codes, nullptr, u->T, c.enc_channels, u->enc, CL, PMG_EPI_BIAS, 0.0f,
+                           u->enc_tok, enc_bias, u->side, true))
+            return e;
+        PMG_CHECK_HIP(hipEventRecord(u->ev_enc, u->side));
+    }
     if (int e = launch_input_stage(in, f16, s)) return e;
 
     // down stages and PoolDown (sparse_unet.py:223-231; flex_sparse_blocks.py:85-90)
@@ -1516,21 +1537,9 @@ static int enqueue_unet(pmg_unet* u, const float* feats, const int32_t* coords, 
     // encoder conditioning and fuse_proj at the deepest level (sparse_unet.py:233-240)
     const int top = L - 1, CL = c.channels[top];
     {
-        const dim3 grid((unsigned)(((int64_t)u->R * u->Cc + 63) / 64), (unsigned)((c.enc_channels + 63) / 64),
-                        (unsigned)c.B);
-        if (f16)
-            hipLaunchKernelGGL(enc_quant_k<_Float16>, grid, dim3(256), 0, s, enc_feat, c.enc_channels,
-                               (int64_t)u->R * u->Cc, 1.0f, (_Float16*)u->enc_codes);
-        else
-            hipLaunchKernelGGL(enc_quant_k<int8_t>, grid, dim3(256), 0, s, enc_feat, c.enc_channels,
-                               (int64_t)u->R * u->Cc, u->enc.q_mult, (int8_t*)u->enc_codes);
-        if (int e = check_launch("enc_quant_k")) return e;
-        // the encoder tokens and the deepest level are a few thousand rows with long K: one 16-column block per
-        // wave gives the GEMM four times the waves (Model A: encoder_fuse 20 -> 13 us, fuse_proj 30 -> 28 us)
+        // the encoder tokens (enc_tok) were made on the side stream
+        PMG_CHECK_HIP(hipStreamWaitEvent(s, u->ev_enc, 0));
         const bool narrow_top = top >= 2;
-        if (int e = linear(u, u->enc_codes, nullptr, u->T, c.enc_channels, u->enc, CL, PMG_EPI_BIAS, 0.0f,
-                           u->enc_tok, enc_bias, s, true))
-            return e;
         if (f16)
             hipLaunchKernelGGL(concat_quant_k<_Float16>, dim3(row_grid(cap * (CL / 2))), dim3(256), 0, s,
                                u->xd[top], u->enc_tok, u->coords[top], u->counts + top, CL, u->R, u->Cc, 1.0f,
@@ -1793,7 +1802,8 @@ pmg_unet* pmg_unet_create(const pmg_unet_config* cfg) {
         return nullptr;
     }
     bool ok = hipStreamCreateWithFlags(&u->side, hipStreamNonBlocking) == hipSuccess &&
-              hipEventCreateWithFlags(&u->ev_fork, hipEventDisableTiming) == hipSuccess;
+              hipEventCreateWithFlags(&u->ev_fork, hipEventDisableTiming) == hipSuccess &&
+              hipEventCreateWithFlags(&u->ev_enc, hipEventDisableTiming) == hipSuccess;
     for (int k = 1; k < L && ok; ++k) ok = hipEventCreateWithFlags(&u->ev_level[k], hipEventDisableTiming) == hipSuccess;
     if (!ok) {
         set_error("pmg_unet_create: creating the structure stream or its events failed");
@@ -1810,6 +1820,7 @@ void pmg_unet_destroy(pmg_unet* u) {
     for (int k = 0; k < kMaxLevels; ++k)
         if (u->ev_level[k]) (void)hipEventDestroy(u->ev_level[k]);
     if (u->ev_fork) (void)hipEventDestroy(u->ev_fork);
+    if (u->ev_enc) (void)hipEventDestroy(u->ev_enc);
     if (u->side) (void)hipStreamDestroy(u->side);
     if (u->step_arena) (void)hipFree(u->step_arena);
     if (u->arena) (void)hipFree(u->arena);
