@@ -65,6 +65,7 @@ struct pmg_refiner {
     int32_t* zmin = nullptr;
     int32_t* zmax = nullptr;
     float* x = nullptr;
+    float* rg = nullptr;  // [M][2] prompt features of the step, for the first block's recomputed skip
     void* q1 = nullptr;
     void* q2 = nullptr;
     float* st_scratch = nullptr;
@@ -78,11 +79,20 @@ struct pmg_refiner {
 
 static size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
+// Whether the first block's conv2 recomputes the input stage's h from the level-0 inputs instead of reading it
+// (the int8 neighbour-pixel-major kernel, C <= 64, with a next block: its LayerNorm epilogue): the input stage then
+// stores no h, and the first residual epilogue reads 20 bytes per row instead of 4 C.
+static bool recompute_x0(const pmg_refiner* r) {
+    return r->cfg.precision != PMG_PREC_FP16 && r->cfg.C <= 64 && r->blocks.size() >= 2;
+}
+
 // Residual blocks: conv1 (bias, SiLU, requantise) then conv2 (bias, skip, and either the next block's
 // LayerNorm/SiLU/quantise or, after the last block, out_proj and either the log-depth update of the point map or
-// the module's (M, 1) output). Expects x and q1 from the input stage.
+// the module's (M, 1) output). Expects q1 and either x from the input stage or, with x0_feats (recompute_x0), the
+// level-0 features (and prompt features x0_rg, or NULL) from which the first block's skip is formed.
 static int enqueue_blocks(pmg_refiner* r, const float* points, float* points_out, float* delta_out, hipStream_t s,
-                          const float* gate_lidar = nullptr, const float* gate_conf = nullptr) {
+                          const float* gate_lidar, const float* gate_conf, const float* x0_feats,
+                          const float* x0_rg) {
     const pmg_refiner_config& c = r->cfg;
     const int prec = c.precision == PMG_PREC_FP16 ? PMG_PREC_FP16 : PMG_PREC_INT8;
     const int64_t M = r->M;
@@ -115,6 +125,14 @@ static int enqueue_blocks(pmg_refiner* r, const float* points, float* points_out
         a2.bias = bk.b2;
         a2.skip = r->x;
         a2.out = r->x;
+        if (k == 0 && x0_feats) {
+            a2.x0_feats = x0_feats;
+            a2.x0_rg = x0_rg;
+            a2.x0_in_w = r->w.in_w;
+            a2.x0_in_b = r->w.in_b;
+            a2.x0_pr_w = r->w.pr_w;
+            a2.x0_pr_b = r->w.pr_b;
+        }
         if (k + 1 < nbk) {
             const pmg_block_weights& bn = r->blocks[k + 1];
             a2.ln_gamma = bn.ln_gamma;
@@ -207,8 +225,15 @@ static int enqueue_step(pmg_refiner* r, const float* points, float* points_out, 
     in.conf = conf;
     in.st = st;
     in.use_prompt = c.use_prompt;
+    const bool x0 = recompute_x0(r);
+    if (x0) {
+        in.x_out = nullptr;
+        in.rg_out = c.use_prompt ? r->rg : nullptr;
+    }
     if (int e = launch_input_stage(in, f16, s)) return e;
-    if (int e = enqueue_blocks(r, points, points_out, nullptr, s, lidar, conf)) return e;
+    if (int e = enqueue_blocks(r, points, points_out, nullptr, s, lidar, conf, x0 ? points : nullptr,
+                               x0 && c.use_prompt ? r->rg : nullptr))
+        return e;
 
     if (c.anchor > 0.0f) {
         // v3.py:570-573: _lidar_in_affine_frame on the refined logz (the prompt fit's inputs), then the pull
@@ -270,8 +295,11 @@ static int enqueue_forward(pmg_refiner* r, const float* feats, const int32_t* co
     in.use_prompt = prompt_feats != nullptr;
     in.zkeys = coords ? coords + 3 : nullptr;
     in.zkey_stride = 4;
+    const bool x0 = recompute_x0(r);
+    if (x0) in.x_out = nullptr;
     if (int e = launch_input_stage(in, r->cfg.precision == PMG_PREC_FP16, s)) return e;
-    return enqueue_blocks(r, nullptr, nullptr, delta_out, s);
+    return enqueue_blocks(r, nullptr, nullptr, delta_out, s, nullptr, nullptr, x0 ? feats : nullptr,
+                          x0 ? prompt_feats : nullptr);
 }
 
 extern "C" {
@@ -321,6 +349,7 @@ pmg_refiner* pmg_refiner_create(const pmg_refiner_config* cfg) {
     };
     const size_t o_zq = take(M * 4), o_zmin = take(c.B * 4), o_zmax = take(c.B * 4);
     const size_t o_x = take(M * c.C * 4), o_q1 = take(M * c.C * elt), o_q2 = take(M * c.C * elt);
+    const size_t o_rg = take(M * 2 * 4);
     const size_t o_st = take(6 * c.B * 4), o_f0 = take(r->fit_ws_bytes[0]), o_f1 = take(r->fit_ws_bytes[1]);
     r->arena_bytes = off;
     if (hipMalloc(&r->arena, r->arena_bytes) != hipSuccess) {
@@ -339,6 +368,7 @@ pmg_refiner* pmg_refiner_create(const pmg_refiner_config* cfg) {
     r->zmin = (int32_t*)(a + o_zmin);
     r->zmax = (int32_t*)(a + o_zmax);
     r->x = (float*)(a + o_x);
+    r->rg = (float*)(a + o_rg);
     r->q1 = a + o_q1;
     r->q2 = a + o_q2;
     r->st_scratch = (float*)(a + o_st);

@@ -139,6 +139,22 @@ __device__ inline float lidar_uncertainty(float d, float c) {
     return valid ? 1.0f - c * (1.0f - ru) : 1.0f;
 }
 
+// One channel of the level-0 residual stream h = input_proj(x/z, y/z, logz) (+ prompt_proj(residual, gate))
+// (sparse_unet.py:189-192), in the one operation order every kernel that forms it uses, so a kernel that recomputes
+// h instead of reading it gets the same bits. w: the channel's input_proj row (3), b its bias; pw, pb: prompt_proj's.
+__device__ inline float x0_channel(float w0, float w1, float w2, float b, float f0, float f1, float f2, bool prompt,
+                                   float pw0, float pw1, float pb, float res, float gate) {
+    float t = b + w0 * f0;
+    t = t + w1 * f1;
+    t = t + w2 * f2;
+    if (prompt) {
+        float pp = pb + pw0 * res;
+        pp = pp + pw1 * gate;
+        t = t + pp;
+    }
+    return t;
+}
+
 // Row layout shared by the fused epilogues and the row kernels: a wave covers 16 rows; lane l holds row l % 16
 // and, of its C channels, n = 16j + 4g + i with g = l / 16 (j < C/16, i < 4). Row reductions run in the "quad"
 // order: each lane sums its channels (j outer, i inner) from 0, then the four lane groups combine as

@@ -102,6 +102,55 @@ __device__ inline void load_skip(const ColConvArgs& a, int m, int M, int g, v4f 
     for (int j = 0; j < C / 16; ++j) sk[j] = *(const v4f*)(a.skip + mo * C + 16 * j + 4 * g);
 }
 
+// The 4-float vector pointer of the address space of a float pointer type (global or LDS constants).
+template <class P>
+struct P4Of {
+    typedef const v4f* type;
+};
+template <>
+struct P4Of<const __attribute__((address_space(3))) float*> {
+    typedef const __attribute__((address_space(3))) v4f* type;
+};
+template <class P>
+using P4 = typename P4Of<P>::type;
+
+// The first block's skip recomputed from the level-0 inputs (ColConvArgs::x0_feats): the row's (x/z, y/z, logz,
+// residual, gate) are loaded first (x0_load, issued early like load_skip), then the lane's channels of h are formed
+// from the staged input_proj / prompt_proj constants (x0_skip; the layout of ColConvArgs: in_w [C][3], in_b [C],
+// pr_w [C][2], pr_b [C] at offsets 0, 3C, 4C, 6C).
+__device__ inline void x0_load(const ColConvArgs& a, int m, int M, float (&in)[5]) {
+    const int64_t mo = m < M ? m : 0;
+    in[0] = a.x0_feats[mo * 3 + 0];
+    in[1] = a.x0_feats[mo * 3 + 1];
+    in[2] = a.x0_feats[mo * 3 + 2];
+    if (a.x0_rg) {
+        const float2 rg = *(const float2*)(a.x0_rg + mo * 2);
+        in[3] = rg.x;
+        in[4] = rg.y;
+    } else {
+        in[3] = in[4] = 0.0f;
+    }
+}
+
+template <int C, class P>
+__device__ inline void x0_skip(P c, bool prompt, const float (&in)[5], int g, v4f (&sk)[C / 16]) {
+#pragma unroll
+    for (int j = 0; j < C / 16; ++j) {
+        const int n0 = 16 * j + 4 * g;
+        const v4f w0 = *(P4<P>)(c + 3 * n0), w1 = *(P4<P>)(c + 3 * n0 + 4), w2 = *(P4<P>)(c + 3 * n0 + 8);
+        const v4f b = *(P4<P>)(c + 3 * C + n0);
+        const v4f p0 = *(P4<P>)(c + 4 * C + 2 * n0), p1 = *(P4<P>)(c + 4 * C + 2 * n0 + 4);
+        const v4f pb = *(P4<P>)(c + 6 * C + n0);
+        const float wi[12] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3], w2[0], w2[1], w2[2], w2[3]};
+        const float pw[8] = {p0[0], p0[1], p0[2], p0[3], p1[0], p1[1], p1[2], p1[3]};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            sk[j][i] = x0_channel(wi[3 * i], wi[3 * i + 1], wi[3 * i + 2], b[i], in[0], in[1], in[2], prompt,
+                                  pw[2 * i], pw[2 * i + 1], pb[i], in[3], in[4]);
+        if constexpr (C / 16 >= 4) __builtin_amdgcn_sched_barrier(0);  // one block's constants live at a time
+    }
+}
+
 template <typename T, int C, int EPI, class P = const float*>
 __device__ inline void col_epilogue(const ColConvArgs& a, const typename ColAcc<T>::type (&acc)[C / 16], int m,
                                     int M, int g, const EpiConst<P>& k, const v4f (&sk)[C / 16]) {
@@ -819,10 +868,11 @@ struct ColvGeom {
     static constexpr int NCHUNK = 3 * kWin * NCH;
     static constexpr int PF = (NCHUNK + kGroupThreads - 1) / kGroupThreads;  // window chunks per thread
     static constexpr int PFZ = (ZWORDS + kGroupThreads - 1) / kGroupThreads;  // window keys per thread
-    static constexpr int LDS = WBYTES + 2 * XBYTES + 2 * ZWORDS * 4 + 5 * C * 4;
+    static constexpr int LDS = WBYTES + 2 * XBYTES + 2 * ZWORDS * 4 + 5 * C * 4 + 7 * C * 4;  // (+ x0 constants)
 };
 
-template <int C, int EPI, int TT, int WG>
+// X0: the residual epilogue's skip is the first block's h, recomputed per row (x0_load / x0_skip) instead of read.
+template <int C, int EPI, int TT, int WG, bool X0>
 __global__ __launch_bounds__(128 * WG, 1) void spconv_colv_k(ColConvArgs a) {
     typedef ColvGeom<C, TT, WG> G;
     constexpr int kRows = G::kRows, kSeg = G::kSeg, kWin = G::kWin, GT = G::kGroupThreads;
@@ -834,6 +884,7 @@ __global__ __launch_bounds__(128 * WG, 1) void spconv_colv_k(ColConvArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t s_x[2][G::XBYTES];
     __shared__ int s_z[2][G::ZWORDS];
     __shared__ float s_k[5][C];  // w_scale, bias, ln gamma, ln beta, out_w
+    __shared__ __attribute__((aligned(16))) float s_x0[X0 ? 7 * C : 4];  // in_w [C][3], in_b, pr_w [C][2], pr_b
     __shared__ __attribute__((aligned(16))) v4i s_zx;  // the operand of a neighbour that is not the step's tap
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -866,6 +917,15 @@ __global__ __launch_bounds__(128 * WG, 1) void spconv_colv_k(ColConvArgs a) {
         const int q = e / C, n = e - (e / C) * C;
         const float* src = q == 0 ? a.w_scale : q == 1 ? a.bias : q == 2 ? a.ln_gamma : q == 3 ? a.ln_beta : a.out_w;
         s_k[q][n] = src ? src[n] : 0.0f;
+    }
+    if constexpr (X0) {
+        const bool pr = a.x0_rg != nullptr;
+        for (int e = tid; e < 7 * C; e += G::kThreads)
+            s_x0[e] = e < 3 * C ? a.x0_in_w[e]
+                      : e < 4 * C ? a.x0_in_b[e - 3 * C]
+                      : !pr       ? 0.0f
+                      : e < 6 * C ? a.x0_pr_w[e - 4 * C]
+                                  : a.x0_pr_b[e - 6 * C];
     }
     typedef const __attribute__((address_space(3))) float* kptr;
     const EpiConst<kptr> kc{(kptr)s_k[0], (kptr)s_k[1], (kptr)s_k[2], (kptr)s_k[3], (kptr)s_k[4], a.bias != nullptr};
@@ -959,7 +1019,8 @@ __global__ __launch_bounds__(128 * WG, 1) void spconv_colv_k(ColConvArgs a) {
     constexpr bool kRes = EPI == PMG_EPI_R || EPI == PMG_EPI_RLN || EPI == PMG_EPI_ROUT;
     constexpr bool kSkipEarly = TT * NB <= 8;  // else the residual inputs would not fit in registers beside the MFMAs
     v4i acc[TT][NB];
-    v4f sk[TT][NB];  // residual inputs of the segment in flight
+    v4f sk[TT][NB];      // residual inputs of the segment in flight
+    float x0in[TT][5];   // (X0) the rows' level-0 inputs, from which the epilogue forms sk
     // Half periods: group 0 runs M0 E0 M1 E1 ..., group 1 runs - M0 E0 M1 E1 ... (Mk: loads of window k+1 and of
     // segment k's residual inputs issued, then the matrix work of segment k; Ek: window k+1 written to LDS, then
     // the epilogue of segment k; -: idle). The global loads thus have a whole half period to arrive. Both groups
@@ -971,8 +1032,14 @@ __global__ __launch_bounds__(128 * WG, 1) void spconv_colv_k(ColConvArgs a) {
         } else if ((hp & 1) == 0) {
             if (kk < nk) {
                 const int s0 = (first + kk * stride) * kSeg;
+                // (X0: the rows' inputs are requested before the next window, so that forming the skip after the
+                // matrix work waits for them only)
+                if constexpr (kRes && kSkipEarly && X0) {
+#pragma unroll
+                    for (int t = 0; t < TT; ++t) x0_load(a, s0 + kRows * wq + 16 * t + r, M, x0in[t]);
+                }
                 if (kk + 1 < nk) fetch(first + (kk + 1) * stride);
-                if constexpr (kRes && kSkipEarly) {
+                if constexpr (kRes && kSkipEarly && !X0) {
 #pragma unroll
                     for (int t = 0; t < TT; ++t) load_skip<C>(a, s0 + kRows * wq + 16 * t + r, M, g, sk[t]);
                 }
@@ -1043,17 +1110,30 @@ __global__ __launch_bounds__(128 * WG, 1) void spconv_colv_k(ColConvArgs a) {
                                 __builtin_amdgcn_mfma_i32_16x16x64_i8(Wt[st % 3][j], XM[st % 3][t], acc[t][j], 0, 0, 0);
                     __builtin_amdgcn_sched_barrier(0);
                 }
+                // (X0) the skip is formed here, after the matrix work is issued: the epilogue half, which sets the
+                // period of the residual epilogues, keeps only the work it had with a loaded skip
+                if constexpr (kRes && kSkipEarly && X0) {
+#pragma unroll
+                    for (int t = 0; t < TT; ++t) x0_skip<C, kptr>((kptr)s_x0, a.x0_rg != nullptr, x0in[t], g, sk[t]);
+                }
             }
         } else if (kk < nk) {
             const int s0 = (first + kk * stride) * kSeg;
             if constexpr (kRes && !kSkipEarly) {
 #pragma unroll
-                for (int t = 0; t < TT; ++t) load_skip<C>(a, s0 + kRows * wq + 16 * t + r, M, g, sk[t]);
+                for (int t = 0; t < TT; ++t) {
+                    if constexpr (X0)
+                        x0_load(a, s0 + kRows * wq + 16 * t + r, M, x0in[t]);
+                    else
+                        load_skip<C>(a, s0 + kRows * wq + 16 * t + r, M, g, sk[t]);
+                }
             }
             if (kk + 1 < nk) commit();  // this group's matrix work on its window ended at the last barrier
 #pragma unroll
-            for (int t = 0; t < TT; ++t)
+            for (int t = 0; t < TT; ++t) {
+                if constexpr (kRes && !kSkipEarly && X0) x0_skip<C, kptr>((kptr)s_x0, a.x0_rg != nullptr, x0in[t], g, sk[t]);
                 col_epilogue<int8_t, C, EPI, kptr>(a, acc[t], s0 + kRows * wq + 16 * t + r, M, g, kc, sk[t]);
+            }
         }
         __syncthreads();
     }
@@ -1072,7 +1152,13 @@ static int launch_colv_tt(const ColConvArgs& a, hipStream_t s) {
     const int64_t nseg = (a.M + G::kSeg - 1) / G::kSeg;
     const int64_t cus = num_cus();
     const unsigned grid = (unsigned)((nseg + 1) / 2 < cus ? (nseg + 1) / 2 : cus);
-    hipLaunchKernelGGL((spconv_colv_k<C, EPI, TT, WG>), dim3(grid), dim3(G::kThreads), 0, s, a);
+    if constexpr (EPI == PMG_EPI_RLN) {
+        if (a.x0_feats) {
+            hipLaunchKernelGGL((spconv_colv_k<C, EPI, TT, WG, true>), dim3(grid), dim3(G::kThreads), 0, s, a);
+            return check_launch("spconv_colv_k");
+        }
+    }
+    hipLaunchKernelGGL((spconv_colv_k<C, EPI, TT, WG, false>), dim3(grid), dim3(G::kThreads), 0, s, a);
     return check_launch("spconv_colv_k");
 }
 
@@ -1108,6 +1194,8 @@ static int launch_colv2(const ColConvArgs& a, int epi, hipStream_t s) {
 }
 
 int launch_conv_col(int precision, const ColConvArgs& a, int C, int epi, hipStream_t s) {
+    if (a.x0_feats && !(precision == PMG_PREC_INT8 && C <= 64 && epi == PMG_EPI_RLN))
+        return fail(PMG_E_INVALID, "pmg_spconv_col: a recomputed first-block skip needs int8, C <= 64 and RLN");
     if (precision == PMG_PREC_INT8) {
         switch (C) {
             case 16: return launch_colv2<16>(a, epi, s);

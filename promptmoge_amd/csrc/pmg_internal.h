@@ -33,6 +33,7 @@ struct InputStage {
     const float* prompt_in;  // [M][2] given prompt features, or NULL (computed from the LiDAR when use_prompt)
     const int32_t* zkeys;    // given z keys (coords[:, 3]) with element stride zkey_stride, or NULL
     int64_t zkey_stride;
+    float* rg_out;  // [M][2] prompt features (residual, gate) written for a conv that recomputes h, or NULL
 };
 int launch_input_stage(const InputStage& in, bool f16, hipStream_t s);
 
@@ -109,6 +110,15 @@ struct ColConvArgs {
     const float* gate_conf;
     int gate_dh, gate_dw;
     float gate_floor, gate_scale;
+    // Residual epilogues of the first block: with x0_feats set, the skip is not read from `skip` but recomputed per
+    // row as the input stage's h = input_proj(x0_feats[m]) (+ prompt_proj(x0_rg[m]) when x0_rg is set), so h is never
+    // stored (x0_feats [M][3]; x0_rg [M][2]; x0_in_w [C][3], x0_in_b, x0_pr_w [C][2], x0_pr_b).
+    const float* x0_feats;
+    const float* x0_rg;
+    const float* x0_in_w;
+    const float* x0_in_b;
+    const float* x0_pr_w;
+    const float* x0_pr_b;
 };
 int launch_conv_col(int precision, const ColConvArgs& a, int C, int epi, hipStream_t s);
 

@@ -56,7 +56,8 @@ __global__ __launch_bounds__(256) void ln_silu_k(const float* __restrict__ x, in
 // Fused input stage of one refiner step (single level):
 //   prompt residual and gate          MoGeModel._lidar_in_affine_frame, v3.py:373-383, and v3.py:552-555
 //   h = input_proj(x/z, y/z, logz) (+ prompt_proj(residual, gate))   sparse_unet.py:189-192
-//   x_out = h (the residual stream), then the first block's LayerNorm/SiLU and quantise (or fp16).
+//   x_out = h (the residual stream; or NULL when the first block's conv recomputes h: rg_out then keeps the prompt
+//   features for it), then the first block's LayerNorm/SiLU and quantise (or fp16).
 // Nearest resizing of the LiDAR map uses F.interpolate's index rule src = min(floor(dst * (in/out)), in-1).
 struct InputArgs {
     const float* points;  // [M][3]
@@ -81,6 +82,7 @@ struct InputArgs {
     const float* prompt_in;  // [M][2] given prompt features (residual, gate), or NULL: computed from the LiDAR
     const int32_t* zkeys;    // given voxel z keys (coords[:, 3], element stride zkey_stride), or NULL
     int64_t zkey_stride;
+    float* rg_out;  // [M][2] the prompt features (residual, gate) of each row, or NULL
 };
 
 __device__ inline void prompt_feats(const InputArgs& a, int b, int i, int j, float logz, float& res, float& gate) {
@@ -158,19 +160,12 @@ __global__ __launch_bounds__(256) void input_stage_k(InputArgs a) {
         const float4 pb = *(const float4*)(c_prb + n0);
         const float bb[4] = {bi.x, bi.y, bi.z, bi.w}, pbb[4] = {pb.x, pb.y, pb.z, pb.w};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float t = bb[i] + wi[3 * i] * f0;
-            t = t + wi[3 * i + 1] * f1;
-            t = t + wi[3 * i + 2] * f2;
-            if (prompt) {
-                float pp = pbb[i] + pw[2 * i] * res;
-                pp = pp + pw[2 * i + 1] * gate;
-                t = t + pp;
-            }
-            y[j][i] = t;
-        }
+        for (int i = 0; i < 4; ++i)
+            y[j][i] = x0_channel(wi[3 * i], wi[3 * i + 1], wi[3 * i + 2], bb[i], f0, f1, f2, prompt, pw[2 * i],
+                                 pw[2 * i + 1], pbb[i], res, gate);
     }
-    if (ok) {
+    if (ok && g == 0 && a.rg_out) *(float2*)(a.rg_out + mo * 2) = make_float2(res, gate);
+    if (ok && a.x_out) {
 #pragma unroll
         for (int j = 0; j < NB; ++j)
             *(float4*)(a.x_out + mo * C + 16 * j + 4 * g) = make_float4(y[j][0], y[j][1], y[j][2], y[j][3]);
@@ -220,7 +215,7 @@ int launch_ln_silu(const float* x, int64_t M, int C, const float* gamma, const f
 int launch_input_stage(const InputStage& in, bool f16, hipStream_t s) {
     InputArgs a{in.points, in.B, in.H, in.W, in.lidar, in.conf, in.dh, in.dw, in.st, in.use_prompt, in.soft_gate,
                 in.in_w, in.in_b, in.pr_w, in.pr_b, in.x_out, in.gamma, in.beta, in.eps, in.out_mult, in.q_out,
-                in.resolution, in.zq_out, in.prompt_in, in.zkeys, in.zkey_stride};
+                in.resolution, in.zq_out, in.prompt_in, in.zkeys, in.zkey_stride, in.rg_out};
     const int64_t M = (int64_t)in.B * in.H * in.W;
     const dim3 g((unsigned)((M + 63) / 64));
     if (f16) {
