@@ -98,89 +98,119 @@ __device__ inline void prompt_feats(const InputArgs& a, int b, int i, int j, flo
     res = (lda - logz) * gate;
 }
 
-// One wave per 16 rows, lane (r, g) holds channels 16j + 4g + i of row r. The per-channel constants (input_proj,
-// prompt_proj, LayerNorm) are staged in LDS once per block; the prompt features of a row are computed by its
-// lane-group-0 lane and passed to the row's other lanes.
+// One row per lane: the lane forms all C channels of its row in registers, so the row's own work (voxel key, LiDAR
+// lookup and prompt features, the LayerNorm statistics) is done once per row rather than once per lane group, and
+// the codes of a row are stored as 16-byte vectors. The per-channel constants are the same for every lane (scalar
+// loads). The LayerNorm sums keep the quad order of the row layout of the epilogues -- partial sums s_g over
+// channels 16j + 4g + i (j outer, i inner), then ((s0 + s1) + (s2 + s3)) -- so the codes are those of that layout.
 template <int C, bool F16>
 __global__ __launch_bounds__(256) void input_stage_k(InputArgs a) {
-    constexpr int NB = C / 16;
-    __shared__ __attribute__((aligned(16))) float s_c[10 * C];  // in_w [C][3], in_b, pr_w [C][2], pr_b, gamma, beta
-    for (int e = threadIdx.x; e < 10 * C; e += 256) {
+    constexpr int NB = C / 16, NQ = C / 4;
+    // in_w [C][3], in_b, pr_w [C][2], pr_b, gamma, beta: read by every lane at the same address (LDS broadcast)
+    __shared__ __attribute__((aligned(16))) float s_c[9 * C];
+    for (int e = threadIdx.x; e < 9 * C; e += 256) {
         float v;
         if (e < 3 * C) v = a.in_w[e];
         else if (e < 4 * C) v = a.in_b[e - 3 * C];
         else if (e < 6 * C) v = a.use_prompt ? a.pr_w[e - 4 * C] : 0.0f;
         else if (e < 7 * C) v = a.use_prompt ? a.pr_b[e - 6 * C] : 0.0f;
         else if (e < 8 * C) v = a.gamma[e - 7 * C];
-        else if (e < 9 * C) v = a.beta[e - 8 * C];
-        else v = 0.0f;
+        else v = a.beta[e - 8 * C];
         s_c[e] = v;
     }
-    const float* c_inw = s_c;
-    const float* c_inb = s_c + 3 * C;
-    const float* c_prw = s_c + 4 * C;
-    const float* c_prb = s_c + 6 * C;
-    const float* c_gam = s_c + 7 * C;
-    const float* c_bet = s_c + 8 * C;
+    typedef const __attribute__((address_space(3))) v4f* c4;
+    const c4 c_inw = (c4)s_c, c_inb = (c4)(s_c + 3 * C), c_prw = (c4)(s_c + 4 * C), c_prb = (c4)(s_c + 6 * C);
+    const c4 c_gam = (c4)(s_c + 7 * C), c_bet = (c4)(s_c + 8 * C);
     const int64_t M = (int64_t)a.B * a.H * a.W;
-    const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
-    const int64_t m = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 16 + r;
-    const bool ok = m < M;
-    const int64_t mo = ok ? m : 0;
-    const float f0 = a.points[mo * 3 + 0], f1 = a.points[mo * 3 + 1], f2 = a.points[mo * 3 + 2];
-    if (ok && g == 0 && a.zq_out)
-        a.zq_out[mo] = a.zkeys ? a.zkeys[mo * a.zkey_stride] : (int32_t)rne(f2 * a.resolution);
+    const int64_t m0 = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const bool ok = m0 < M;
+    const int64_t m = ok ? m0 : M - 1;
+    const float f0 = a.points[m * 3 + 0], f1 = a.points[m * 3 + 1], f2 = a.points[m * 3 + 2];
+    if (ok && a.zq_out) a.zq_out[m] = a.zkeys ? a.zkeys[m * a.zkey_stride] : (int32_t)rne(f2 * a.resolution);
     float res = 0.0f, gate = 0.0f;
     if (a.prompt_in) {  // Sparse3DUNet.forward's prompt_feats (sparse_unet.py:191-193)
-        res = a.prompt_in[mo * 2];
-        gate = a.prompt_in[mo * 2 + 1];
+        res = a.prompt_in[m * 2];
+        gate = a.prompt_in[m * 2 + 1];
     } else if (a.use_prompt) {
-        if (g == 0) {
-            const int64_t HW = (int64_t)a.H * a.W;
-            const int b = (int)(mo / HW);
-            const int p = (int)(mo - b * HW);
-            const int i = p / a.W, j = p - (p / a.W) * a.W;
-            prompt_feats(a, b, i, j, f2, res, gate);
-        }
-        res = __shfl(res, r, 64);  // lane r (group 0) holds row r's values
-        gate = __shfl(gate, r, 64);
+        const int64_t HW = (int64_t)a.H * a.W;
+        const int b = (int)(m / HW);
+        const int p = (int)(m - b * HW);
+        const int i = p / a.W, j = p - (p / a.W) * a.W;
+        prompt_feats(a, b, i, j, f2, res, gate);
     }
+    if (ok && a.rg_out) *(float2*)(a.rg_out + m * 2) = make_float2(res, gate);
     __syncthreads();  // constants staged
     const bool prompt = a.use_prompt;
-    float y[NB][4];
+    // (one quad of channels between scheduling barriers: the constants of one quad are live at a time)
+    float y[NQ][4];
 #pragma unroll
-    for (int j = 0; j < NB; ++j) {
-        const int n0 = 16 * j + 4 * g;
-        const float4 w0 = *(const float4*)(c_inw + 3 * n0), w1 = *(const float4*)(c_inw + 3 * n0 + 4);
-        const float4 w2 = *(const float4*)(c_inw + 3 * n0 + 8);
-        const float wi[12] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w, w2.x, w2.y, w2.z, w2.w};
-        const float4 bi = *(const float4*)(c_inb + n0);
-        const float4 p0 = *(const float4*)(c_prw + 2 * n0), p1 = *(const float4*)(c_prw + 2 * n0 + 4);
-        const float pw[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-        const float4 pb = *(const float4*)(c_prb + n0);
-        const float bb[4] = {bi.x, bi.y, bi.z, bi.w}, pbb[4] = {pb.x, pb.y, pb.z, pb.w};
+    for (int q = 0; q < NQ; ++q) {
+        const v4f w0 = c_inw[3 * q], w1 = c_inw[3 * q + 1], w2 = c_inw[3 * q + 2], b = c_inb[q];
+        const v4f p0 = c_prw[2 * q], p1 = c_prw[2 * q + 1], pb = c_prb[q];
+        const float wi[12] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3], w2[0], w2[1], w2[2], w2[3]};
+        const float pw[8] = {p0[0], p0[1], p0[2], p0[3], p1[0], p1[1], p1[2], p1[3]};
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            y[j][i] = x0_channel(wi[3 * i], wi[3 * i + 1], wi[3 * i + 2], bb[i], f0, f1, f2, prompt, pw[2 * i],
-                                 pw[2 * i + 1], pbb[i], res, gate);
+            y[q][i] = x0_channel(wi[3 * i], wi[3 * i + 1], wi[3 * i + 2], b[i], f0, f1, f2, prompt, pw[2 * i],
+                                 pw[2 * i + 1], pb[i], res, gate);
+        __builtin_amdgcn_sched_barrier(0);
     }
-    if (ok && g == 0 && a.rg_out) *(float2*)(a.rg_out + mo * 2) = make_float2(res, gate);
     if (ok && a.x_out) {
 #pragma unroll
-        for (int j = 0; j < NB; ++j)
-            *(float4*)(a.x_out + mo * C + 16 * j + 4 * g) = make_float4(y[j][0], y[j][1], y[j][2], y[j][3]);
+        for (int q = 0; q < NQ; ++q)
+            *(float4*)(a.x_out + m * C + 4 * q) = make_float4(y[q][0], y[q][1], y[q][2], y[q][3]);
     }
-    typedef const __attribute__((address_space(3))) float* kptr;
-    ln_silu_quad<NB, F16, kptr>(y, (kptr)c_gam, (kptr)c_bet, a.eps, g);
-    if (!ok) return;
-    if constexpr (F16) {
+    // LayerNorm (two-pass) + affine, in the quad order
+    float sg[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int j = 0; j < NB; ++j) store_half4(y[j], (_Float16*)a.q_out + mo * C + 16 * j + 4 * g);
-    } else {
-        uint32_t pk[NB];
-        silu_codes_packed<NB>(y, a.out_mult, pk);
+    for (int j = 0; j < NB; ++j)
 #pragma unroll
-        for (int j = 0; j < NB; ++j) *(uint32_t*)((int8_t*)a.q_out + mo * C + 16 * j + 4 * g) = pk[j];
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sg[g] = sg[g] + y[4 * j + g][i];
+    const float mean = ((sg[0] + sg[1]) + (sg[2] + sg[3])) / (float)C;
+    float vg[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float d = y[4 * j + g][i] - mean;
+                vg[g] = vg[g] + d * d;
+            }
+    const float var = ((vg[0] + vg[1]) + (vg[2] + vg[3])) / (float)C;
+    const float rstd = 1.0f / __builtin_sqrtf(var + a.eps);
+    // per 16 channels: normalise, then the fp16 SiLU or the int8 codes, one 16-byte store (fp16: two)
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+        float t[4][4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const v4f gm = c_gam[4 * j + q], bt = c_bet[4 * j + q];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float v = (y[4 * j + q][i] - mean) * rstd;
+                v = v * gm[i];
+                v = v + bt[i];
+                t[q][i] = F16 ? silu_fast(v) : v;
+            }
+        }
+        if constexpr (F16) {
+            typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                h8 hv;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) hv[i] = (_Float16)t[2 * h + i / 4][i % 4];
+                if (ok) *(h8*)((_Float16*)a.q_out + m * C + 16 * j + 8 * h) = hv;
+            }
+        } else {
+            uint32_t pk[4];
+            silu_codes_packed<4>(t, a.out_mult, pk);
+            if (ok) *(v4i*)((int8_t*)a.q_out + m * C + 16 * j) = v4i{(int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3]};
+        }
+        __builtin_amdgcn_sched_barrier(0);
     }
 }
 
@@ -217,7 +247,7 @@ int launch_input_stage(const InputStage& in, bool f16, hipStream_t s) {
                 in.in_w, in.in_b, in.pr_w, in.pr_b, in.x_out, in.gamma, in.beta, in.eps, in.out_mult, in.q_out,
                 in.resolution, in.zq_out, in.prompt_in, in.zkeys, in.zkey_stride, in.rg_out};
     const int64_t M = (int64_t)in.B * in.H * in.W;
-    const dim3 g((unsigned)((M + 63) / 64));
+    const dim3 g((unsigned)((M + 255) / 256));
     if (f16) {
         PMG_C_SWITCH(in.C, hipLaunchKernelGGL((input_stage_k<CC, true>), g, dim3(256), 0, s, a));
     } else {
