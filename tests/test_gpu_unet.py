@@ -131,6 +131,31 @@ def test_unet_keys_from_depth_and_graph_replay(gpu):
     assert np.abs(a.cpu().numpy() - d.cpu().numpy()).max() > 1e-4
 
 
+def test_unet_reused_inputs_read_in_place(gpu):
+    """Inputs passed again (the same tensors as the previous call) are read in place by their own captured graph:
+    the result equals the staged call's, and a change written into those tensors in place is seen by the next
+    replay (the graph reads the buffers at replay time)."""
+    announce("unet reused input tensors read in place")
+    w, levels, pts, coords, enc, bias, pf, (B, H, W, Z) = _setup("small3")
+    M = B * H * W
+    mod = UNetRefiner(w)
+    shape = torch.Size([B, H, W, Z, 3])
+    tf, tc, te, tb, tp = (_t(a, gpu) for a in (pts.reshape(M, 3), coords, enc, bias, pf))
+    first = mod(tf, tc, shape, te, prompt_feats=tp, encoder_bias_map=tb)  # staged
+    again = [mod(tf, tc, shape, te, prompt_feats=tp, encoder_bias_map=tb) for _ in range(3)]  # in place
+    te.mul_(0.5)
+    tp[:, 0] += 0.01
+    changed = mod(tf, tc, shape, te, prompt_feats=tp, encoder_bias_map=tb)
+    staged = mod(tf.clone(), tc, shape, te.clone(), prompt_feats=tp.clone(), encoder_bias_map=tb)
+    torch.cuda.synchronize()
+    for o in again:
+        assert np.array_equal(first.cpu().numpy(), o.cpu().numpy())
+    assert np.array_equal(changed.cpu().numpy(), staged.cpu().numpy())
+    ref = ou.forward(pts.reshape(M, 3), levels, w, te.cpu().numpy(), tp.cpu().numpy(), bias, mode="int8")
+    assert np.array_equal(changed.cpu().numpy()[:, 0], ref)
+    assert np.abs(changed.cpu().numpy() - first.cpu().numpy()).max() > 1e-4
+
+
 def test_unet_from_refiner_bin(gpu, tmp_path):
     """A refiner exported in the Metal engine's format (refiner.bin / refiner.json) and loaded back: the GPU module
     built from the file equals the oracle on the loaded (stored int8) weights, with the file's uv_bias as the bias
