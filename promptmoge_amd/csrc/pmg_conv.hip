@@ -314,9 +314,11 @@ __device__ inline void store_tile_codes(const ConvArgs& a, const v4i (&acc)[T][N
 // Host-sized generic-map launches deal groups of kXcdGroup consecutive chunks round-robin over the 8 XCDs (block b
 // runs on XCD b % 8): neighbouring chunks (rows that share neighbours) stay on one XCD's L2, and the work evens out
 // where it varies along the row order (rows sorted by tap mask; measured at C = 128 on the 1M-voxel surface set:
-// 0.369 ms with one contiguous band per XCD, 0.324 ms dealt in groups of 16). Device-sized launches (a few chunks)
-// keep one contiguous band per XCD.
+// 0.369 ms with one contiguous band per XCD, 0.324 ms dealt in groups of 16). Launches with fewer than 8 groups of
+// chunks (every device-sized launch of a coarse level, small host-sized sets) keep one contiguous band per XCD:
+// groups would put all of the work on the first XCDs (21 chunks: 16 on XCD 0, 5 on XCD 1, the other six idle).
 constexpr int kXcdGroup = 16;
+__host__ __device__ inline int xcd_group(int64_t nunits) { return nunits >= 8 * kXcdGroup ? kXcdGroup : 0; }
 
 constexpr int kBufWord3 = 0x00020000;  // buffer descriptor word 3 for raw (untyped) loads on gfx9
 constexpr int kG2Threads = 512;       // 8 waves: two per SIMD, 256 registers each
@@ -425,7 +427,7 @@ __global__ __launch_bounds__(kG2Threads, 1) void spconv_g2_k(ConvArgs a) {
         for (int kk = 0; kk < WPP; ++kk) dst[(wv + kG2Waves * (part * WPP + kk)) * 64 + lane] = st[kk];
     };
 
-    constexpr int gi = kDev ? 0 : kXcdGroup;
+    const int gi = kDev ? 0 : xcd_group(nunit);
     for (int kq = bi;; kq += nbx) {
         const int un = gi ? ((kq / gi) * nx + x) * gi + kq % gi : c0 + kq;
         if (un >= (gi ? nunit : c1)) break;
@@ -708,7 +710,7 @@ __global__ __launch_bounds__(64 * NWV, 1) void spconv_g2r_k(ConvArgs a) {
     const int x = b % nx, bi = b / nx, nbx = (G - x + nx - 1) / nx;
     const int c0 = (int)((int64_t)nchunk * x / nx), c1 = (int)((int64_t)nchunk * (x + 1) / nx);
     // each wave takes the block's chunks independently: wave wv of chunk ch owns rows [16 T wv, 16 T (wv + 1))
-    const int gi = a.m_dev ? 0 : kXcdGroup;
+    const int gi = a.m_dev ? 0 : xcd_group(nchunk);
     for (int kq = bi;; kq += nbx) {
         const int ch = gi ? ((kq / gi) * nx + x) * gi + kq % gi : c0 + kq;
         if (ch >= (gi ? nchunk : c1)) break;
