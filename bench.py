@@ -182,6 +182,10 @@ def setup(cfg_name):
         step = RefinerStep(w, 1, cfg.H, cfg.W, precision=cfg.precision, fit_iters=cfg.fit_iters)
         step(env["P"], env["L"], env["Cf"], out=env["Pout"])
         step.check()
+        if cfg.precision != "int8":  # the single-kernel timings below are int8 (config A); fits only
+            torch.cuda.synchronize()
+            env["step"] = step
+            return env
         zq, _, _ = ops.voxelize(P[..., 2:], 256.0, stride=3, shape=(1, cfg.H, cfg.W))
         x = step.buffer("x").clone()
         b0, b1 = step.weights.blocks[0], step.weights.blocks[-1]
@@ -339,8 +343,8 @@ def microbench(stream):
 def fit_trace(args):
     """The metric fit's own per-round record: block 0 of fit_k writes, into the workspace header, the wall clock
     (100 MHz) at the launch, after the first solve and after every trim round, with the round's selection path
-    (0 bracket, 1 bracket missed -> radix, 2 radix, 3 radix + third pass), its candidate count, and the number of
-    rounds run (the loop stops at a fixed point). Prints one line per round for the prompt fit and the final fit of
+    (bracket, window pass, radix passes, and the fallbacks between them), its histogram passes, its candidate count
+    and threshold, and the number of rounds run (the loop stops at a fixed point). Prints one line per round for the prompt fit and the final fit of
     the configuration, on its input point map and on the map one refiner step made (the last of 20 runs each). A
     library built with PMG_FIT_PHASE_TRACE=1 (python -m promptmoge_amd.build) also records the phases of each
     round, which are printed after it."""
@@ -352,7 +356,8 @@ def fit_trace(args):
     env = setup(args.config)
     cfg = env["cfg"]
     P, L, Cf, Pr = env["P"], env["L"], env["Cf"], env["Pout"]
-    names = {0: "bracket", 1: "bracket missed -> radix", 2: "radix", 3: "radix + third pass"}
+    names = {0: "bracket", 2: "radix", 4: "window", 5: "bracket missed -> window", 6: "window missed -> radix",
+             7: "bracket, window missed -> radix"}
     with torch.cuda.stream(env["stream"]):
         # on the input point map, and on the map one refiner step made (what the final fit and the prompt fits of
         # later steps see)
@@ -372,8 +377,13 @@ def fit_trace(args):
             for it in range(int(tr[130])):
                 t = int(tr[2 * it + 1])
                 dt = ((t - prev) & 0xffffffff) / 100.0
-                line = (f"round {it:2d} {dt:8.2f}  path {names.get(int(tr[2 * it]) & 15, '?'):24s} "
-                        f"candidates {int(tr[2 * it]) >> 4}")
+                thr = int(tr[768 + it])
+                move = f"{thr - int(tr[768 + it - 1]):+10d}" if it else " " * 10
+                code = int(tr[2 * it])
+                pname = names.get(code & 7, "?") + (" + one-value threshold" if code & 8 else "")
+                line = (f"round {it:2d} {dt:8.2f}  path {pname:32s} passes {(code >> 4) & 15}  "
+                        f"candidates {code >> 8:5d}  threshold {np.uint32(thr).view(np.float32):.6e} "
+                        f"(move {move} ulps)")
                 mk = [int(v) for v in tr[256 + it * 8: 256 + it * 8 + 7]]
                 if it < 32 and any(mk):  # phase marks: a library built with PMG_FIT_PHASE_TRACE=1
                     d = [((mk[k + 1] - mk[k]) & 0xffffffff) / 100.0 for k in range(6)]
@@ -662,7 +672,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="A", choices=["A", "B", "H"])
+    ap.add_argument("--config", default="A", choices=["A", "B", "H", "T"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-micro", action="store_true", help="skip the 1M-voxel conv microbench")
     ap.add_argument("--no-others", action="store_true", help="skip the K-step T and H frame timings")
@@ -689,6 +699,8 @@ def main() -> int:
     sys.path.insert(0, ROOT)
     if args.kernels_only:
         return kernels_only(args)
+    if args.config == "T" and not args.fit_trace:
+        ap.error("--config T serves --fit-trace only; the T frame is timed by --other T")
     if args.fit_trace:
         return fit_trace(args)
     if args.micro_only:

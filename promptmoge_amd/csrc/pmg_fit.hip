@@ -12,17 +12,21 @@
 // (n*sxx - sx^2 cancels badly in fp32) in a fixed order, and every block reduces the published per-block partials
 // itself, so all blocks hold bit-identical (s, t) and take identical branches.
 //
-// The threshold is the exact k-th smallest residual; non-negative fp32 values order like their bit patterns. A trim
-// round costs ONE barrier when the threshold stays inside a bracket [lo, hi] predicted from the previous rounds
-// (+-(2 |last move| + 1024) ulps, capped so that about 1024 candidates are expected at the density seen last time):
-// each block publishes how many of its residuals fall below lo, its fp64 sums over those (they are in the new weight
-// set whatever the exact threshold), and its residuals inside the bracket ("candidates", with z and target). After
-// the barrier every block loads all candidates into LDS, selects the exact k-th among them (each thread ranks one
-// candidate when there are at most 256, else an LDS radix select), and adds the candidates at or below it to the
-// sums -- the next (s, t) without a second barrier. Rounds 0 and 1 (no measured move yet), and any round whose k-th
-// leaves its bracket, first run two global radix passes over the top 22 bits (LDS histogram per block, merged by
-// atomics) that narrow the bracket to one 1024-value bin; if even that bin holds more than kCandCap candidates, a
-// third pass finds the threshold and the sums take one more barrier.
+// The threshold is the exact k-th smallest residual; non-negative fp32 values order like their bit patterns ("keys").
+// A trim round costs ONE barrier when the threshold stays inside a bracket [lo, hi] predicted from the previous
+// rounds (along the last move's direction half of it, against it a quarter, plus a margin of ~32 expected
+// candidates): each block publishes how many of its residuals fall below lo, its fp64 sums over those (they are in
+// the new weight set whatever the exact threshold), and its residuals inside the bracket ("candidates", with z and
+// target). After the barrier every block loads all candidates into LDS, selects the exact k-th among them (each
+// thread ranks one candidate when there are at most 96, else an LDS radix select), and adds the candidates at or
+// below it to the sums -- the next (s, t) without a second barrier. When the predicted bracket would hold more than
+// ~1500 candidates (large moves), a histogram pass over a window of twice its range goes first (2048 bins of a
+// power-of-two width, LDS histogram per block, merged by atomics), and the stage runs on the bin that holds the
+// k-th; a bracket that misses is followed by such a window on the side that holds the k-th. Rounds 0 and 1 (no
+// measured move yet), and a window that misses, run radix passes over the whole key range (bins of 2^21 keys, then
+// 2^10 within the first bin, then single keys, each only while the bin holds more than 2048 keys); when one key
+// value holds the k-th and more than kCandCap elements, it is the threshold and the sums take one more barrier.
+// The stage checks that its bracket holds the k-th, so a prediction can cost time but never change a result.
 //
 // Fixed point: once a round reproduces the previous round's (s, t) bit for bit, every later round would repeat
 // it exactly, so the loop stops there with the bit-identical result (on the synthetic scenes after 3 rounds).
@@ -48,7 +52,11 @@ constexpr int kFitEPTMax = 32;                         // elements per thread, i
 constexpr int kFitPerBlockMax = kFitThreads * kFitEPTMax;  // 8192
 constexpr int kFitMaxBlocks = kFitThreads;             // N <= 2^21
 constexpr int kFitBins = 2048;
+constexpr int kFitHistWords = kFitBins + 64;           // one global histogram: the bins, then 16 below-window counts
+constexpr int kFitHistSlots = 6;                       // histogram passes a round can take (window 3 + radix 3)
 constexpr int kCandCap = 32768;                        // candidates every block holds in LDS (128 KiB)
+constexpr unsigned kStageMax = 2048;                   // a pass bin with more elements is split by another pass
+constexpr double kBracketMax = 1536.0;                 // expected candidates above which a window pass goes first
 constexpr uint32_t kInvalid = 0xffffffffu;             // residual key of a padding slot: above every residual
 constexpr int kFitTraceRounds = 64;
 constexpr size_t kFitHeader = 4096;                    // barrier, error flag, trace, completion count
@@ -66,7 +74,7 @@ struct FitWs {
     unsigned* err_seen;   // launches whose bounded wait expired since the owner last cleared it (sticky)
     uint64_t* partials;   // [2][kFitMaxBlocks][5] fp64 bit patterns
     unsigned* counts;     // [2][kFitMaxBlocks][2]: below, candidates
-    unsigned* hist;       // [iters][3][kFitBins]
+    unsigned* hist;       // [iters][kFitHistSlots][kFitHistWords]
     uint32_t* c_key;      // [2][nb][elements per block]: residual bits | mask << 31
     float* c_z;           // [2][nb][elements per block]
     float* c_t;           // [2][nb][elements per block]
@@ -204,18 +212,23 @@ struct FitShared {
     long long kk;
     int ok;
     unsigned bin, below;
+    unsigned bincnt, hbelow;  // elements in the found bin; this block's keys below a pass window
+    int found;                // find_bin found the rank in the histogram
     unsigned total_below, total_cand;
     uint32_t blo_last, bhi_last;  // bracket of the last stage
     int last;                     // this block is the launch's last one to finish
 };
 
-// Finds, in a 2048-bin histogram, the bin holding the rank-th element (1-based); sets sh.bin and sh.below (the
-// count in the bins before it). The histogram is read through `load`.
-template <class Load>
-__device__ inline void find_bin(FitShared& sh, unsigned rank, Load load) {
-    constexpr int per = kFitBins / kFitThreads;  // 4 consecutive bins per thread
+// Finds, in a 2048-bin histogram whose bins follow `base` smaller elements, the bin holding the rank-th element
+// (1-based); sets sh.bin, sh.below (the count before it, base included), sh.bincnt (the bin's count) and sh.found
+// (0 when the rank-th element lies below the bins or above them). The bins are read through `load` and base
+// through `load_base`, all in one round trip.
+template <class Load, class LoadBase>
+__device__ inline void find_bin(FitShared& sh, unsigned rank, Load load, LoadBase load_base) {
+    constexpr int per = kFitBins / kFitThreads;  // 8 consecutive bins per thread
     unsigned cnt[per];
     unsigned local = 0;
+    const unsigned base = load_base();
 #pragma unroll
     for (int e = 0; e < per; ++e) {
         cnt[e] = load(threadIdx.x * per + e);
@@ -224,9 +237,11 @@ __device__ inline void find_bin(FitShared& sh, unsigned rank, Load load) {
     if (threadIdx.x == 0) {
         sh.bin = 0;
         sh.below = 0;
+        sh.bincnt = 0;
+        sh.found = 0;
     }
     unsigned total;
-    const unsigned excl = block_excl_scan(local, sh.tmp, total);
+    const unsigned excl = block_excl_scan(local, sh.tmp, total) + base;
     if (excl < rank && rank <= excl + local) {
         unsigned cum = excl;
 #pragma unroll
@@ -234,6 +249,8 @@ __device__ inline void find_bin(FitShared& sh, unsigned rank, Load load) {
             if (cum + cnt[e] >= rank) {
                 sh.bin = (unsigned)(threadIdx.x * per + e);
                 sh.below = cum;
+                sh.bincnt = cnt[e];
+                sh.found = 1;
                 break;
             }
             cum += cnt[e];
@@ -257,7 +274,7 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
     if (b == 0 && tid == 0) ws.trace[2 * kFitTraceRounds + 1] = (uint32_t)wall_clock64();  // launch start
     // clear this launch's global histograms; the first barrier orders this before any use
     {
-        const int64_t words = (int64_t)(a.iters > 0 ? a.iters : 1) * 3 * kFitBins;
+        const int64_t words = (int64_t)(a.iters > 0 ? a.iters : 1) * kFitHistSlots * kFitHistWords;
         for (int64_t q = (int64_t)b * kFitThreads + tid; q < words; q += (int64_t)nb * kFitThreads) ws.hist[q] = 0u;
     }
 
@@ -433,9 +450,18 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
     }
 
     if (b == 0 && tid == 0) ws.trace[2 * kFitTraceRounds] = (uint32_t)wall_clock64();  // initial solve done
+    if (tid == 0) {  // the last stage's record, read by the next round's plan before any stage has run
+        sh.total_cand = 0;
+        sh.blo_last = 0;
+        sh.bhi_last = 0;
+    }
+    __syncthreads();
     uint32_t thr = 0, thr_prev = 0;
-    bool have_bracket = false, have_prev = false, have_prev2 = false;
-    uint32_t lo = 0, hi = 0;
+    bool have_prev = false;
+    // the next round's plan (see its computation at the end of a round): mode, bracket, window
+    int plan_mode = 2, plan_wsh = 0;
+    uint32_t lo = 0, hi = 0, plan_wlo = 0;
+    float dens = 0.0f;  // candidates per key near the threshold, from the last stage with enough of them
 
     // A fit that falls back to (1, 0) never changes (s, t): its trim rounds cannot affect the result.
     int rounds = 0;  // trim rounds run (the loop stops early at a fixed point)
@@ -581,8 +607,9 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
             FIT_MARK(4);
             uint32_t prefix = 0, pmask = 0;
             int top = 0;
-            if (total <= (unsigned)kFitThreads) {
-                // few candidates: each thread ranks its own against all of them (LDS broadcast reads)
+            if (total <= 96u) {
+                // few candidates: each thread ranks its own against all of them (LDS broadcast reads; beyond ~100
+                // candidates the radix select below is faster)
                 if (tid == 0) sh.bin = 0;
                 __syncthreads();
                 if ((unsigned)tid < total) {
@@ -627,7 +654,7 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
                     if ((key & pmask) == prefix) atomicAdd(&sh.hist[(key >> shb) & dmask], 1u);
                 }
                 __syncthreads();
-                find_bin(sh, rank, [&](int q) { return sh.hist[q]; });
+                find_bin(sh, rank, [&](int q) { return sh.hist[q]; }, [] { return 0u; });
                 prefix |= sh.bin << shb;
                 pmask |= dmask << shb;
                 rank -= sh.below;
@@ -680,42 +707,125 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
             FIT_MARK(6);
         };
 
-        // One call site per phase keeps the unrolled element loops from being duplicated.
-        int path = have_bracket && have_prev2 ? 0 : 2;  // 0 bracket, 1 bracket missed then radix, 2 radix, 3 radix + third pass
-        bool use_bracket = have_bracket && have_prev2;
-        uint32_t blo = lo, bhi = hi, prefix = 0;
-        unsigned rank = kk;
+        // Histogram pass over a window of keys: bin q counts the keys in [wlo + q 2^wsh, wlo + (q+1) 2^wsh), q < 2048,
+        // and one more counter the keys below wlo; blocks merge their LDS histograms into this round's global slot
+        // `hslot` by atomics, and after one barrier every block finds the bin holding the kk-th key. Returns false
+        // when that key lies outside the window; else pbin_lo / pbin_cnt give the bin's first key and its count.
+        // One call site serves the radix passes and the predicted windows (the unrolled element loop exists once).
+        int hslot = 0;
+        uint32_t pbin_lo = 0;
+        unsigned pbin_cnt = 0, pbin_below = 0;
+        // `below` is the count of keys below wlo when the caller knows it (the radix range starts at 0, and a pass
+        // that splits a bin follows the keys before that bin), else kNoBelow: the pass counts them, into 16 words
+        // (block b adds to word b % 16) so that the 75-94 blocks' atomics do not all queue on one address.
+        constexpr unsigned kNoBelow = 0xffffffffu;
+        auto hist_pass = [&](uint32_t wlo, int wsh, unsigned below) -> bool {
+            asm volatile("" : "+v"(mbits), "+v"(vbits));
+            for (int q = tid; q < kFitBins; q += kFitThreads) sh.hist[q] = 0;
+            if (tid == 0) sh.hbelow = 0;
+            __syncthreads();
+            unsigned nbelow = 0;
+#pragma unroll
+            for (int j = 0; j < kFitEPT; ++j) {  // one branch per element (around its LDS atomic)
+                const uint32_t k = rb[j];
+                const bool v = (vbits >> j) & 1u;
+                const uint32_t q = (k - wlo) >> wsh;
+                nbelow += (v && k < wlo) ? 1u : 0u;
+                if (v && k >= wlo && q < (uint32_t)kFitBins) atomicAdd(&sh.hist[q], 1u);
+            }
+            const bool count_below = below == kNoBelow;
+            if (count_below) {
+                nbelow = wave_incl_scan_u32(nbelow);
+                if ((tid & 63) == 63 && nbelow) atomicAdd(&sh.hbelow, nbelow);
+            }
+            __syncthreads();
+            unsigned* gh = ws.hist + ((int64_t)it * kFitHistSlots + hslot) * kFitHistWords;
+            hslot = hslot + 1 < kFitHistSlots ? hslot + 1 : hslot;  // at most 6 passes a round (never reached)
+            for (int q = tid; q < kFitBins; q += kFitThreads)
+                if (sh.hist[q]) atomicAdd(&gh[q], sh.hist[q]);
+            if (count_below && tid == 0 && sh.hbelow) atomicAdd(&gh[kFitBins + (b & 15)], sh.hbelow);
+            fit_barrier(ws, nb, ++sync_seq, a.spin_limit);
+            find_bin(
+                sh, kk, [&](int q) { return __hip_atomic_load(&gh[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); },
+                [&] {
+                    if (!count_below) return below;
+                    unsigned v = 0;
+#pragma unroll
+                    for (int q = 0; q < 16; ++q)
+                        v += __hip_atomic_load(&gh[kFitBins + q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    return v;
+                });
+            if (!sh.found) return false;  // below or above the window (read from LDS: the block branches as one)
+            pbin_lo = wlo + (sh.bin << wsh);
+            pbin_cnt = sh.bincnt;
+            pbin_below = sh.below;
+            return true;
+        };
+
+        // The round's selection. mode 0: one bracket stage on the predicted bracket [lo, hi]; 1: a histogram pass on
+        // the predicted window, then a stage on its bin; 2: radix passes over the whole key range (bits 31..21, then
+        // 20..10 of the first bin, then single values, each only while the bin holds more than kStageMax keys),
+        // then a stage on the bin. A bracket stage that misses the k-th is followed by a window on the side that
+        // holds it; a window that misses it, by the radix passes. Trace codes: 0 bracket, 2 radix, 4 window,
+        // 5 bracket missed -> window, 6 window missed -> radix, 7 bracket and window missed -> radix; +8 when one
+        // value holds the k-th and more than kCandCap keys (its sums take a barrier of their own).
+        int mode = plan_mode;
+        int path = mode == 0 ? 0 : (mode == 1 ? 4 : 2);
+        int passes = 0;
+        uint32_t blo = lo, bhi = hi, wlo = plan_wlo;
+        int wsh = plan_wsh;
 #pragma nounroll
         for (;;) {
-            if (!use_bracket) {
-                // ---- global radix passes over bits 31..21 and 20..10
-                uint32_t pmask = 0;
-                prefix = 0;
-                rank = kk;
-#pragma nounroll
-                for (int pass = 0; pass < 2; ++pass) {
-                    const int shb = pass == 0 ? 21 : 10;
-                    asm volatile("" : "+v"(mbits), "+v"(vbits));
-                    for (int q = tid; q < kFitBins; q += kFitThreads) sh.hist[q] = 0;
-                    __syncthreads();
-#pragma unroll
-                    for (int j = 0; j < kFitEPT; ++j)
-                        if (((vbits >> j) & 1u) && (rb[j] & pmask) == prefix)
-                            atomicAdd(&sh.hist[(rb[j] >> shb) & (kFitBins - 1)], 1u);
-                    __syncthreads();
-                    unsigned* gh = ws.hist + ((int64_t)it * 3 + pass) * kFitBins;
-                    for (int q = tid; q < kFitBins; q += kFitThreads)
-                        if (sh.hist[q]) atomicAdd(&gh[q], sh.hist[q]);
-                    fit_barrier(ws, nb, ++sync_seq, a.spin_limit);
-                    find_bin(sh, rank, [&](int q) {
-                        return __hip_atomic_load(&gh[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    });
-                    prefix |= sh.bin << shb;
-                    pmask |= (uint32_t)(kFitBins - 1) << shb;
-                    rank -= sh.below;
+            if (mode != 0) {
+                if (mode == 2) {
+                    wlo = 0;
+                    wsh = 21;
                 }
-                blo = prefix;
-                bhi = prefix | 1023u;
+                bool hit;
+                unsigned below = mode == 2 ? 0u : kNoBelow;
+#pragma nounroll
+                for (;;) {
+                    hit = hist_pass(wlo, wsh, below);
+                    ++passes;
+                    if (!hit || pbin_cnt <= kStageMax || wsh == 0) break;
+                    wlo = pbin_lo;  // split the bin: 2048 sub-bins of 2^(wsh - 11) keys
+                    wsh = wsh > 11 ? wsh - 11 : 0;
+                    below = pbin_below;
+                }
+                if (!hit) {
+                    if (mode == 2) break;  // the whole range holds every key: only after an expired wait
+                    mode = 2;
+                    path = path == 5 ? 7 : 6;
+                    continue;
+                }
+                blo = pbin_lo;
+                const uint64_t e = (uint64_t)pbin_lo + ((1ull << wsh) - 1u);
+                bhi = e > 0xffffffffull ? 0xffffffffu : (uint32_t)e;
+                if (pbin_cnt > (unsigned)kCandCap) {
+                    // one value (wsh == 0) holds the k-th and more keys than LDS holds: it is the threshold; the
+                    // sums over the keys at or below it take one more barrier
+                    path |= 8;
+                    thr = blo;
+                    double v[5] = {0.0, 0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+                    for (int j = 0; j < kFitEPT; ++j) {
+                        if (((mbits >> j) & 1u) && rb[j] <= thr) {
+                            const double zd = zr[j], td = tr[j];
+                            v[0] += 1.0;
+                            v[1] += zd;
+                            v[2] += td;
+                            v[3] += zd * zd;
+                            v[4] += zd * td;
+                        }
+                    }
+                    publish(v, 0u, 0u);
+                    fit_barrier(ws, nb, ++sync_seq, a.spin_limit);
+                    double g[5];
+                    gather_partials(g);
+                    ++stage;
+                    solve(g, false);
+                    break;
+                }
             }
             stage_bracket(blo, bhi);
             const unsigned tbl = sh.total_below, tcd = sh.total_cand;
@@ -724,77 +834,78 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
                 break;
             }
             ++stage;
-            if (use_bracket) {  // the k-th left the bracket: narrow it with the radix passes
-                use_bracket = false;
-                path = 1;
-                continue;
+            if (mode != 0) break;  // a pass bin the stage does not confirm: only after an expired wait
+            // the bracket missed: a window of 2^plan_wsh-key bins on the side that holds the k-th (or, when the
+            // bracket held it among more candidates than LDS holds, a window over the bracket itself)
+            mode = 1;
+            path = 5;
+            wsh = plan_wsh;
+            const uint64_t span = (uint64_t)kFitBins << wsh;
+            if (kk <= tbl) {
+                wlo = (uint64_t)blo > span ? blo - (uint32_t)span : 0u;
+            } else if (kk <= tbl + tcd) {
+                wlo = blo;
+                wsh = 0;
+                while (((uint64_t)kFitBins << wsh) < (uint64_t)bhi - blo + 1u && wsh < 21) ++wsh;
+            } else if (bhi == 0xffffffffu) {
+                mode = 2;
+            } else {
+                wlo = bhi + 1u;
             }
-            // ---- one 1024-value bin holds more candidates than fit in LDS: a third global pass (bits 9..0) gives
-            // the threshold, and the sums take one more barrier
-            path = 3;
-            asm volatile("" : "+v"(mbits), "+v"(vbits));
-            for (int q = tid; q < kFitBins; q += kFitThreads) sh.hist[q] = 0;
-            __syncthreads();
-#pragma unroll
-            for (int j = 0; j < kFitEPT; ++j)
-                if (((vbits >> j) & 1u) && (rb[j] & ~1023u) == prefix) atomicAdd(&sh.hist[rb[j] & 1023u], 1u);
-            __syncthreads();
-            unsigned* gh = ws.hist + ((int64_t)it * 3 + 2) * kFitBins;
-            for (int q = tid; q < 1024; q += kFitThreads)
-                if (sh.hist[q]) atomicAdd(&gh[q], sh.hist[q]);
-            fit_barrier(ws, nb, ++sync_seq, a.spin_limit);
-            find_bin(sh, rank, [&](int q) {
-                return __hip_atomic_load(&gh[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            });
-            thr = prefix | sh.bin;
-            double v[5] = {0.0, 0.0, 0.0, 0.0, 0.0};
-#pragma unroll
-            for (int j = 0; j < kFitEPT; ++j) {
-                if (((mbits >> j) & 1u) && rb[j] <= thr) {
-                    const double zd = zr[j], td = tr[j];
-                    v[0] += 1.0;
-                    v[1] += zd;
-                    v[2] += td;
-                    v[3] += zd * zd;
-                    v[4] += zd * td;
-                }
-            }
-            publish(v, 0u, 0u);
-            fit_barrier(ws, nb, ++sync_seq, a.spin_limit);
-            double g[5];
-            gather_partials(g);
-            ++stage;
-            solve(g, false);
-            break;
         }
 
         if (b == 0 && tid == 0 && it < kFitTraceRounds) {
-            ws.trace[2 * it] = (uint32_t)path | (sh.total_cand << 4);
+            ws.trace[2 * it] = (uint32_t)path | ((uint32_t)(passes < 15 ? passes : 15) << 4) | (sh.total_cand << 8);
             ws.trace[768 + it] = thr;
             ws.trace[2 * it + 1] = (uint32_t)wall_clock64();
         }
-        // ---- next round's bracket: around thr, as wide as twice the last move (in ulps) plus a margin
-        // ... but no wider than what holds about 1024 candidates at the density the last stage saw around its
-        // threshold (candidates per ulp of its bracket), and never wider than 2^18 ulps (3 %). (Measured on the
-        // A, B and H scenes against 2048, 512 and 256 candidates: 1024 is 2-6 us faster per fit than 2048, while
-        // 512 and 256 miss the first bracket of the refined A map and fall back to the radix passes.)
-        uint64_t D = have_prev ? 2ull * (thr > thr_prev ? thr - thr_prev : thr_prev - thr) + 1024u : (1ull << 18);
-        {
-            const double dens = (double)sh.total_cand / (double)((uint64_t)sh.bhi_last - sh.blo_last + 1);
-            const double dmax = dens > 0.0 ? 512.0 / dens : (double)(1u << 18);
-            uint64_t cap = dmax < 2048.0 ? 2048u : (dmax > (double)(1u << 18) ? (1ull << 18) : (uint64_t)dmax);
-            if (D > cap) D = cap;
-        }
-        lo = (uint64_t)thr > D ? thr - (uint32_t)D : 0u;
-        hi = (uint64_t)thr + D > 0x7fffffffull ? 0x7fffffffu : thr + (uint32_t)D;
-        have_bracket = true;
-        thr_prev = thr;
-        have_prev2 = have_prev;  // the first bracket waits for one measured move: round 1 usually jumps far
-        have_prev = true;
         // Fixed point: when a round reproduces the previous (s, t) bit for bit, the next round sees the same
         // residuals, hence the same k-th value, weights and sums, so every remaining round -- and the final
         // solve -- returns exactly these (s, t). Stopping here gives the bit-identical result.
-        if (same) break;
+        // ---- the next round's plan. The threshold's move from round to round (in keys, which order like the
+        // values) shrinks by 2-5x per round on the refined maps, keeps its sign while it is large, and jitters by
+        // ~10^3 keys near the fixed point. The bracket reaches a quarter of the last move against it and half a move
+        // along it, plus a margin of at least 2048 keys and ~32 expected candidates; when that bracket would hold
+        // more than kBracketMax candidates at the density the stages saw (candidates per key, kept from the last
+        // stage with at least 64), a window pass over twice that range goes first, its bins sized for 2048 over the
+        // range. A move of more than an octave is the first trim dropping the outliers of an exact point map: the
+        // next round usually repeats the threshold, so the bracket is ~1024 expected candidates around it. After
+        // round 0 (no move seen yet) the radix passes run again: the first trim moves the threshold by up to ten
+        // octaves on an exact point map, farther than a window covers cheaply.
+        if (same) break;  // the fixed point below: no next round to plan
+        // (heuristics only, in fp32 with the hardware reciprocal: the plan never changes a result)
+        if (sh.total_cand >= 64u || dens <= 0.0f)
+            dens = (float)sh.total_cand * __builtin_amdgcn_rcpf((float)(sh.bhi_last - sh.blo_last) + 1.0f);
+        plan_mode = 2;
+        if (have_prev) {
+            // keys are below 2^31 (non-negative floats, NaN included), so every range here fits 32 bits
+            const bool up = thr >= thr_prev;
+            const uint32_t am = up ? thr - thr_prev : thr_prev - thr;
+            const float rdens = dens > 0.0f ? __builtin_amdgcn_rcpf(dens) : 0.0f;
+            auto keys_for = [&](float cands) {  // keys that hold about `cands` candidates, in [2048, 2^18]
+                const float k = dens > 0.0f ? cands * rdens : 2048.0f;
+                return (uint32_t)(k < 2048.0f ? 2048.0f : (k > 262144.0f ? 262144.0f : k));
+            };
+            const bool jump = am > (1u << 23);  // a jump of over an octave predicts no move
+            uint32_t along = am / 2 + keys_for(32.0f), against = am / 4 + keys_for(32.0f);
+            if (jump) along = against = keys_for(512.0f);
+            const float expect = dens * ((float)(along + against) + 1.0f);
+            const uint32_t dn = up ? against : along, dp = up ? along : against;
+            if (expect <= kBracketMax || jump) {
+                plan_mode = 0;
+                lo = thr > dn ? thr - dn : 0u;
+                hi = thr + dp < thr ? 0xffffffffu : thr + dp;
+            } else {
+                plan_mode = 1;
+            }
+            // window bins: the smallest power of two that spans twice the bracket's range in 2048 bins
+            const uint32_t span = 2 * (along + against);
+            const int lg = 32 - __builtin_clz(span - 1u);  // ceil(log2(span)), span >= 2^13
+            plan_wsh = lg > 11 ? (lg - 11 < 21 ? lg - 11 : 21) : 0;
+            plan_wlo = thr > 2 * dn ? thr - 2 * dn : 0u;
+        }
+        thr_prev = thr;
+        have_prev = true;
     }
 
     if (b == 0 && tid == 0) {
@@ -851,7 +962,7 @@ static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 size_t fit_workspace_bytes(int64_t N, int iters) {
     const int64_t n = N > 0 ? N : 1;
     const size_t nb = (size_t)fit_blocks(n);
-    const size_t hist = (size_t)(iters > 0 ? iters : 1) * 3 * kFitBins * sizeof(unsigned);
+    const size_t hist = (size_t)(iters > 0 ? iters : 1) * kFitHistSlots * kFitHistWords * sizeof(unsigned);
     const size_t cand = 2 * nb * (size_t)kFitThreads * fit_ept(n) * sizeof(uint32_t);
     return kFitHeader + align256(kFitMaxBlocks * 64) + align256(2 * kFitMaxBlocks * 5 * sizeof(uint64_t)) +
            align256(2 * kFitMaxBlocks * 2 * sizeof(unsigned)) +
@@ -900,7 +1011,7 @@ int launch_fit(const FitLaunch& f, hipStream_t s) {
     ws.counts = (unsigned*)p;
     p += align256(2 * kFitMaxBlocks * 2 * sizeof(unsigned));
     ws.hist = (unsigned*)p;
-    p += align256((size_t)(f.iters > 0 ? f.iters : 1) * 3 * kFitBins * sizeof(unsigned));
+    p += align256((size_t)(f.iters > 0 ? f.iters : 1) * kFitHistSlots * kFitHistWords * sizeof(unsigned));
     const size_t cand = align256(2 * (size_t)nb * kFitThreads * ept * sizeof(uint32_t));
     ws.c_key = (uint32_t*)p;
     ws.c_z = (float*)(p + cand);
