@@ -22,10 +22,11 @@
 // below it to the sums -- the next (s, t) without a second barrier. When the predicted bracket would hold more than
 // ~1500 candidates (large moves), a histogram pass over a window of twice its range goes first (2048 bins of a
 // power-of-two width, LDS histogram per block, merged by atomics), and the stage runs on the bin that holds the
-// k-th; a bracket that misses is followed by such a window on the side that holds the k-th. Rounds 0 and 1 (no
-// measured move yet), and a window that misses, run radix passes over the whole key range (bins of 2^21 keys, then
-// 2^10 within the first bin, then single keys, each only while the bin holds more than 2048 keys); when one key
-// value holds the k-th and more than kCandCap elements, it is the threshold and the sums take one more barrier.
+// k-th; a bracket that misses is followed by such a window on the side that holds the k-th, and round 1 takes a
+// window over 16 octaves around round 0's threshold. Round 0 (no threshold yet), and a window that misses, run
+// radix passes over the whole key range (bins of 2^21 keys, then 2^10 within the first bin, then single keys, each
+// only while the bin holds more than 2048 keys); when one key value holds the k-th and more than kCandCap
+// elements, it is the threshold and the sums take one more barrier.
 // The stage checks that its bracket holds the k-th, so a prediction can cost time but never change a result.
 //
 // Fixed point: once a round reproduces the previous round's (s, t) bit for bit, every later round would repeat
@@ -869,15 +870,20 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
         // more than kBracketMax candidates at the density the stages saw (candidates per key, kept from the last
         // stage with at least 64), a window pass over twice that range goes first, its bins sized for 2048 over the
         // range. A move of more than an octave is the first trim dropping the outliers of an exact point map: the
-        // next round usually repeats the threshold, so the bracket is ~1024 expected candidates around it. After
-        // round 0 (no move seen yet) the radix passes run again: the first trim moves the threshold by up to ten
-        // octaves on an exact point map, farther than a window covers cheaply.
+        // next round usually repeats the threshold, so the bracket is ~256 expected candidates around it.
         if (same) break;  // the fixed point below: no next round to plan
         // (heuristics only, in fp32 with the hardware reciprocal: the plan never changes a result)
         if (sh.total_cand >= 64u || dens <= 0.0f)
             dens = (float)sh.total_cand * __builtin_amdgcn_rcpf((float)(sh.bhi_last - sh.blo_last) + 1.0f);
         plan_mode = 2;
-        if (have_prev) {
+        if (!have_prev) {
+            // after round 0: the first trim drops the outliers' pull, and the threshold falls by up to ~11 octaves
+            // (exact point maps) or moves by under one (noisy ones); a window from 14 octaves below to 2 above it
+            // in 2048 bins of 2^16 keys (1/128 octave) holds it
+            plan_mode = 1;
+            plan_wsh = 16;
+            plan_wlo = thr > (14u << 23) ? thr - (14u << 23) : 0u;
+        } else {
             // keys are below 2^31 (non-negative floats, NaN included), so every range here fits 32 bits
             const bool up = thr >= thr_prev;
             const uint32_t am = up ? thr - thr_prev : thr_prev - thr;
@@ -888,7 +894,7 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
             };
             const bool jump = am > (1u << 23);  // a jump of over an octave predicts no move
             uint32_t along = am / 2 + keys_for(32.0f), against = am / 4 + keys_for(32.0f);
-            if (jump) along = against = keys_for(512.0f);
+            if (jump) along = against = keys_for(128.0f);
             const float expect = dens * ((float)(along + against) + 1.0f);
             const uint32_t dn = up ? against : along, dp = up ? along : against;
             if (expect <= kBracketMax || jump) {
