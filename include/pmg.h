@@ -277,6 +277,12 @@ int pmg_fit_scale_shift_static(const float* z, const float* target, const uint8_
  * enqueued after the call (0 restores the default, about 0.1 s). Returns the previous value. A tiny limit makes
  * waits expire with every kernel still running to its end, so tests can exercise the error path. */
 unsigned pmg_debug_fit_spin_limit(unsigned polls);
+/* Test hook (no counterpart in the reference): makes the metric fit's round plans wrong on purpose, for the fits
+ * enqueued after the call, so that tests reach the selection's fallbacks -- 1: each predicted bracket moved just
+ * above its range (a window on the side that holds the k-th follows its miss); 2: each plan a window above every
+ * finite residual (the radix passes follow its miss); 3: windows of 2^21-key bins (split passes); 0 (or any other
+ * value) restores the normal plan. Results do not depend on the plan. Returns the previous mode. */
+unsigned pmg_debug_fit_plan(unsigned mode);
 int pmg_fit_scale_shift(const float* z, const float* target, const uint8_t* mask, int B, int64_t N, int iters,
                         float trim, int min_points, float* st, int32_t* info, void* workspace,
                         size_t workspace_bytes, void* stream);

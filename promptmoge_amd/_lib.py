@@ -120,6 +120,7 @@ SIGNATURES = {
     "pmg_ln_silu_f16": (i32, [vp, i64, i32, vp, vp, f32, vp, vp]),
     "pmg_fit_workspace_bytes": (sz, [i64, i32]),
     "pmg_debug_fit_spin_limit": (C.c_uint, [C.c_uint]),
+    "pmg_debug_fit_plan": (C.c_uint, [C.c_uint]),
     "pmg_fit_scale_shift_static": (i32, [vp, vp, vp, i32, i64, i32, f32, i32, vp, vp, vp]),
     "pmg_fit_scale_shift": (i32, [vp, vp, vp, i32, i64, i32, f32, i32, vp, vp, vp, sz, vp]),
     "pmg_fit_prompt": (i32, [vp, i64, vp, vp, i32, i32, i32, i32, i32, i32, f32, i32, vp, vp, vp, sz, vp]),

@@ -99,6 +99,7 @@ struct FitArgs {
     float* st;
     int32_t* info;
     unsigned spin_limit;  // polls of one barrier wait before it gives up
+    int plan_debug;       // test hook: 0, or a deliberately wrong round plan (see pmg_debug_fit_plan)
     FitWs ws;
 };
 
@@ -910,6 +911,22 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
             plan_wsh = lg > 11 ? (lg - 11 < 21 ? lg - 11 : 21) : 0;
             plan_wlo = thr > 2 * dn ? thr - 2 * dn : 0u;
         }
+        // Test hook: plans that are wrong on purpose, to exercise the fallbacks (the results must not change).
+        // 1: a bracket just above its predicted range (the k-th usually lies below: a window on that side follows);
+        // 2: every plan a window above +inf (it misses: the radix passes follow); 3: windows of 2^21-key bins from
+        // 2^24 keys below the threshold (split passes with a counted below-window part).
+        if (a.plan_debug == 1 && plan_mode == 0) {
+            const uint32_t w = hi - lo;
+            lo = hi < 0xffffffffu ? hi + 1u : hi;
+            hi = lo + w < lo ? 0xffffffffu : lo + w;
+        } else if (a.plan_debug == 2) {
+            plan_mode = 1;
+            plan_wlo = 0x7f800001u;
+            plan_wsh = 0;
+        } else if (a.plan_debug == 3 && plan_mode == 1) {
+            plan_wlo = thr > (1u << 24) ? thr - (1u << 24) : 0u;
+            plan_wsh = 21;
+        }
         thr_prev = thr;
         have_prev = true;
     }
@@ -978,6 +995,8 @@ size_t fit_workspace_bytes(int64_t N, int iters) {
 // Polls of one barrier wait before it expires (~0.1 s at the default); lowered only by the test hook
 // pmg_debug_fit_spin_limit, so that tests can make waits expire with every kernel still exiting normally.
 static unsigned g_fit_spin_limit = 1u << 23;
+// Wrong-on-purpose round plans for tests (pmg_debug_fit_plan); 0 in normal use.
+static int g_fit_plan_debug = 0;
 
 int launch_fit(const FitLaunch& f, hipStream_t s) {
     PMG_REQUIRE(f.N > 0 && f.N <= (int64_t)kFitMaxBlocks * kFitPerBlockMax, "N must be in [1, 2^21]");
@@ -1025,7 +1044,7 @@ int launch_fit(const FitLaunch& f, hipStream_t s) {
     for (int b = 0; b < f.B; ++b) {
         FitArgs a{f.mode, f.z, f.tg, f.mask, f.logz, f.stride, f.lidar, f.conf, f.H, f.W, f.dh, f.dw,
                   f.N, f.iters, (float)(1.0 - (double)f.trim), f.min_points, b, f.st, f.info,
-                  g_fit_spin_limit, ws};
+                  g_fit_spin_limit, g_fit_plan_debug, ws};
         if (ept == 16)
             hipLaunchKernelGGL(fit_k<16>, dim3(nb), dim3(kFitThreads), 0, s, a);
         else
@@ -1196,6 +1215,12 @@ int pmg_fit_scale_shift_static(const float* z, const float* target, const uint8_
 unsigned pmg_debug_fit_spin_limit(unsigned polls) {
     const unsigned prev = g_fit_spin_limit;
     g_fit_spin_limit = polls ? polls : (1u << 23);
+    return prev;
+}
+
+unsigned pmg_debug_fit_plan(unsigned mode) {
+    const unsigned prev = (unsigned)g_fit_plan_debug;
+    g_fit_plan_debug = mode <= 3 ? (int)mode : 0;
     return prev;
 }
 

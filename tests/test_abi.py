@@ -175,6 +175,13 @@ def test_refiner_create_rejects_maps_beyond_the_fit(libpmg):
     assert b"final_fit" in libpmg.pmg_last_error()
 
 
+def test_fit_plan_hook_round_trips(libpmg):
+    prev = libpmg.pmg_debug_fit_plan(2)
+    assert prev == 0
+    assert libpmg.pmg_debug_fit_plan(9) == 2  # out of range: the normal plan
+    assert libpmg.pmg_debug_fit_plan(0) == 0
+
+
 def test_fit_spin_limit_hook_round_trips(libpmg):
     prev = libpmg.pmg_debug_fit_spin_limit(7)
     assert prev == 1 << 23

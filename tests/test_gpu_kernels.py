@@ -584,6 +584,65 @@ def test_fit_expired_wait_is_reported_and_does_not_leak(gpu, libpmg):
     assert np.array_equal(s2, s0) and np.array_equal(t2, t0)
 
 
+def _fit_trace(ws: "torch.Tensor"):
+    """Block 0's round record in the fit workspace: per round the selection path code (low 3 bits: 0 bracket, 2 radix,
+    4 window, 5 bracket missed -> window, 6 window missed -> radix, 7 both missed -> radix; bit 3: one-value
+    threshold) and the histogram passes; the number of rounds run."""
+    tr = ws[128:128 + 4096].cpu().numpy().view(np.uint32)
+    rounds = int(tr[130])
+    return [(int(tr[2 * i]) & 15, (int(tr[2 * i]) >> 4) & 15) for i in range(rounds)]
+
+
+def test_fit_plan_fallbacks_do_not_change_results(gpu, libpmg):
+    """The selection's plan only decides how fast the exact k-th is found. With plans made wrong on purpose
+    (pmg_debug_fit_plan: brackets moved off their range, windows that miss, coarse windows that need split passes)
+    every fallback path runs, and (s, t) and the last threshold stay bit-identical to the normal plan's, on data
+    whose threshold moves for all 10 rounds (noisy line with outliers) and on an exact line with outliers (the
+    threshold collapses by many octaves after the first trim)."""
+    announce("fit plan fallbacks (debug plans 1-3 against the normal plan)")
+    rng = np.random.default_rng(11)
+    N = 300_000
+    z = rng.uniform(0.5, 6, size=(2, N)).astype(np.float32)
+    t = np.empty_like(z)
+    t[0] = 0.7 * z[0] + 0.3 + rng.normal(0, 0.03, size=N)
+    t[0] = np.where(rng.random(N) < 0.15, t[0] * rng.uniform(0.3, 3, size=N), t[0])
+    t[1] = 1.3 * z[1] + 0.05
+    t[1] = np.where(rng.random(N) < 0.1, t[1] * rng.uniform(0.5, 2, size=N), t[1])
+    t = t.astype(np.float32)
+    m = rng.random((2, N)) < 0.8
+    runs = {}
+    try:
+        for mode in (0, 1, 2, 3):
+            libpmg.pmg_debug_fit_plan(mode)
+            paths = []
+            res = []
+            for b in range(2):  # one item per call, so that the workspace holds that item's trace
+                zb = _t(z[b:b + 1], gpu)
+                s_, t_, info = ops.fit_scale_shift(zb, _t(t[b:b + 1], gpu), _t(m[b:b + 1], gpu), iters=10,
+                                                   return_info=True)
+                torch.cuda.synchronize()
+                ws = ops._fit_workspace(0, zb.device)  # the workspace this stream's calls use
+                paths.append(_fit_trace(ws))
+                info = info.cpu().numpy()
+                assert info[0, 4] == 0
+                res.append((float(s_[0]), float(t_[0]), int(info[0, 3])))
+            runs[mode] = (res, paths)
+    finally:
+        libpmg.pmg_debug_fit_plan(0)
+    so, to, _ = ofit.fit_f64(z, t, m, iters=10, return_info=True)
+    for b in range(2):
+        _close_st(runs[0][0][b][0], runs[0][0][b][1], so[b], to[b])
+    for mode in (1, 2, 3):
+        assert runs[mode][0] == runs[0][0], (mode, runs[mode][0], runs[0][0])
+    codes = {mode: {c for p in runs[mode][1] for c, _ in p} for mode in runs}
+    assert 0 in codes[0] and 4 in codes[0], codes[0]  # the normal plan takes brackets and windows here
+    assert 5 in codes[1], codes[1]                    # a missed bracket, then a window on the k-th's side
+    assert codes[2] <= {2, 6, 7}, codes[2]            # no plan ever holds the k-th: radix after every miss
+    assert 6 in codes[2], codes[2]
+    split = [n for p in runs[3][1] for c, n in p if c == 4]
+    assert split and max(split) >= 2, runs[3][1]      # coarse windows need split passes
+
+
 @pytest.mark.parametrize("name", ["B", "A", "H"])
 def test_fit_prompt_scene(gpu, name):
     announce(f"fit prompt scene={name}")
