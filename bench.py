@@ -356,8 +356,8 @@ def fit_trace(args):
     env = setup(args.config)
     cfg = env["cfg"]
     P, L, Cf, Pr = env["P"], env["L"], env["Cf"], env["Pout"]
-    names = {0: "bracket", 2: "radix", 4: "window", 5: "bracket missed -> window", 6: "window missed -> radix",
-             7: "bracket, window missed -> radix"}
+    names = {0: "bracket", 1: "bracket missed -> radix", 2: "radix", 4: "window", 5: "bracket missed -> window",
+             6: "window missed -> radix", 7: "bracket, window missed -> radix"}
     with torch.cuda.stream(env["stream"]):
         # on the input point map, and on the map one refiner step made (what the final fit and the prompt fits of
         # later steps see)

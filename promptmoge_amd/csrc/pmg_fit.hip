@@ -768,8 +768,9 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
         // the predicted window, then a stage on its bin; 2: radix passes over the whole key range (bits 31..21, then
         // 20..10 of the first bin, then single values, each only while the bin holds more than kStageMax keys),
         // then a stage on the bin. A bracket stage that misses the k-th is followed by a window on the side that
-        // holds it; a window that misses it, by the radix passes. Trace codes: 0 bracket, 2 radix, 4 window,
-        // 5 bracket missed -> window, 6 window missed -> radix, 7 bracket and window missed -> radix; +8 when one
+        // holds it; a window that misses it, by the radix passes. Trace codes: 0 bracket, 1 bracket missed -> radix
+        // (no key above it), 2 radix, 4 window, 5 bracket missed -> window, 6 window missed -> radix, 7 bracket and
+        // window missed -> radix; +8 when one
         // value holds the k-th and more than kCandCap keys (its sums take a barrier of their own).
         int mode = plan_mode;
         int path = mode == 0 ? 0 : (mode == 1 ? 4 : 2);
@@ -851,6 +852,7 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
                 while (((uint64_t)kFitBins << wsh) < (uint64_t)bhi - blo + 1u && wsh < 21) ++wsh;
             } else if (bhi == 0xffffffffu) {
                 mode = 2;
+                path = 1;
             } else {
                 wlo = bhi + 1u;
             }

@@ -585,9 +585,9 @@ def test_fit_expired_wait_is_reported_and_does_not_leak(gpu, libpmg):
 
 
 def _fit_trace(ws: "torch.Tensor"):
-    """Block 0's round record in the fit workspace: per round the selection path code (low 3 bits: 0 bracket, 2 radix,
-    4 window, 5 bracket missed -> window, 6 window missed -> radix, 7 both missed -> radix; bit 3: one-value
-    threshold) and the histogram passes; the number of rounds run."""
+    """Block 0's round record in the fit workspace: per round the selection path code (low 3 bits: 0 bracket,
+    1 bracket missed -> radix, 2 radix, 4 window, 5 bracket missed -> window, 6 window missed -> radix, 7 both
+    missed -> radix; bit 3: one-value threshold) and the histogram passes; the number of rounds run."""
     tr = ws[128:128 + 4096].cpu().numpy().view(np.uint32)
     rounds = int(tr[130])
     return [(int(tr[2 * i]) & 15, (int(tr[2 * i]) >> 4) & 15) for i in range(rounds)]
@@ -637,7 +637,7 @@ def test_fit_plan_fallbacks_do_not_change_results(gpu, libpmg):
     codes = {mode: {c for p in runs[mode][1] for c, _ in p} for mode in runs}
     assert 0 in codes[0] and 4 in codes[0], codes[0]  # the normal plan takes brackets and windows here
     assert 5 in codes[1], codes[1]                    # a missed bracket, then a window on the k-th's side
-    assert codes[2] <= {2, 6, 7}, codes[2]            # no plan ever holds the k-th: radix after every miss
+    assert codes[2] <= {1, 2, 6, 7}, codes[2]         # no plan ever holds the k-th: radix after every miss
     assert 6 in codes[2], codes[2]
     split = [n for p in runs[3][1] for c, n in p if c == 4]
     assert split and max(split) >= 2, runs[3][1]      # coarse windows need split passes
