@@ -74,7 +74,6 @@ struct FitWs {
     unsigned* done;       // blocks of the current launch that have finished (the last one resets it to 0)
     unsigned* err_seen;   // launches whose bounded wait expired since the owner last cleared it (sticky)
     uint64_t* partials;   // [2][kFitMaxBlocks][5] fp64 bit patterns
-    unsigned* counts;     // [2][kFitMaxBlocks][2]: below, candidates
     unsigned* hist;       // [iters][kFitHistSlots][kFitHistWords]
     uint32_t* c_key;      // [2][nb][elements per block]: residual bits | mask << 31
     float* c_z;           // [2][nb][elements per block]
@@ -104,22 +103,34 @@ struct FitArgs {
 };
 
 // Device-wide barrier for a fully resident grid, by per-block flags: block b's thread 0 publishes (release, agent
-// scope) the barrier's sequence number in its own flag line; thread t < nb waits (bounded) until block t's flag has
-// reached it, then acquires. Global writes before it are visible after it. Flag values only grow within a launch
-// and across launches (the epoch in bar[2]), so a block that is already one barrier ahead still satisfies a late
-// waiter; every data buffer exchanged across a barrier is double-buffered, so that block cannot overwrite what the
-// late waiter is about to read. Half the cost of a central arrival counter (no serialised read-modify-write, and
-// every waiter polls one line in parallel with the others).
-__device__ inline void fit_barrier(const FitWs& ws, unsigned nb, unsigned want, unsigned spin_limit) {
+// scope) the barrier's sequence number, with a 32-bit payload, in its own flag line; thread t < nb waits (bounded)
+// until block t's flag has reached it, then acquires, and returns block t's payload (0 in other threads). Global
+// writes before it are visible after it. Flag values only grow within a launch and across launches (the epoch in
+// bar[2]), so a block that is already one barrier ahead still satisfies a late waiter; the flag of an even barrier
+// and that of an odd one are separate 64-bit words of the line (sequence number low, payload high, one atomic
+// store), and every data buffer exchanged across a barrier is double-buffered, so that block cannot overwrite what
+// the late waiter is about to read (a block cannot get two barriers ahead). Half the cost of a central arrival
+// counter (no serialised read-modify-write, and every waiter polls one line in parallel with the others); the
+// payload carries a stage's candidate counts, which saves the read of them after the barrier.
+__device__ inline unsigned fit_barrier(const FitWs& ws, unsigned nb, unsigned want, unsigned spin_limit,
+                                       unsigned payload = 0u) {
     __syncthreads();
+    uint64_t* const f64 = (uint64_t*)ws.flags;  // 8 words per block's 64-byte line: [0] even barriers, [1] odd
     if (threadIdx.x == 0) {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        __hip_atomic_store(&ws.flags[blockIdx.x * 16], want, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&f64[blockIdx.x * 8 + (want & 1u)], ((uint64_t)payload << 32) | want, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
     }
+    unsigned got = 0;
     if (threadIdx.x < nb && __hip_atomic_load(ws.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) {
         unsigned spins = 0;
-        while ((int)(__hip_atomic_load(&ws.flags[threadIdx.x * 16], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) -
-                     want) < 0) {
+        for (;;) {
+            const uint64_t v =
+                __hip_atomic_load(&f64[threadIdx.x * 8 + (want & 1u)], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if ((int)((unsigned)v - want) >= 0) {
+                got = (unsigned)(v >> 32);
+                break;
+            }
             __builtin_amdgcn_s_sleep(1);
             if (++spins > spin_limit) {
                 __hip_atomic_store(ws.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -129,6 +140,7 @@ __device__ inline void fit_barrier(const FitWs& ws, unsigned nb, unsigned want, 
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     }
     __syncthreads();
+    return got;
 }
 
 // Fixed-order block reduction of 5 doubles (DPP wave scans, then waves in order); result in every thread.
@@ -341,16 +353,13 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
     }
 
     int stage = 0;  // publish buffers alternate between consecutive publishes
-    // Publishes this block's fp64 sums (and, for a bracket stage, counts) into buffer `stage & 1`.
-    auto publish = [&](double (&v)[5], unsigned below, unsigned ncand) {
+    // Publishes this block's fp64 sums into buffer `stage & 1` (a bracket stage's counts ride on its barrier).
+    auto publish = [&](double (&v)[5]) {
         block_sum5(v, sh.red);
         if (tid == 0) {
             uint64_t* p = ws.partials + ((size_t)(stage & 1) * kFitMaxBlocks + b) * 5;
 #pragma unroll
             for (int k = 0; k < 5; ++k) p[k] = __builtin_bit_cast(uint64_t, v[k]);
-            unsigned* c = ws.counts + ((size_t)(stage & 1) * kFitMaxBlocks + b) * 2;
-            c[0] = below;
-            c[1] = ncand;
         }
     };
     // Sum of all blocks' published partials of buffer `stage & 1`, in block order, in every thread.
@@ -441,7 +450,7 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
             }
         }
         FIT_MARK0(0);
-        publish(v, 0u, 0u);
+        publish(v);
         FIT_MARK0(1);
         fit_barrier(ws, nb, ++sync_seq, a.spin_limit);
         FIT_MARK0(2);
@@ -526,17 +535,17 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
                     ++slot;
                 }
             }
-            publish(v, packed_total >> 16, ncb);
+            publish(v);
             FIT_MARK(1);
-            fit_barrier(ws, nb, ++sync_seq, a.spin_limit);
+            // the block's counts (below in the high half, candidates in the low half) ride on the barrier's flag
+            const unsigned counts = fit_barrier(ws, nb, ++sync_seq, a.spin_limit, packed_total);
             FIT_MARK(2);
-            load_partials();
+            load_partials();  // needed only by the sums after the selection: in flight with the candidate loads
             // totals and region offsets, in block order
             unsigned cb = 0, cc = 0;
             if (tid < nb) {
-                const unsigned* c = ws.counts + ((size_t)(stage & 1) * kFitMaxBlocks + tid) * 2;
-                cb = __hip_atomic_load(&c[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                cc = __hip_atomic_load(&c[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                cb = counts >> 16;
+                cc = counts & 0xffffu;
                 // a block publishes at most its own element count; the clamp only matters after an expired wait,
                 // when the counts may be another launch's, and keeps every candidate read inside this launch's
                 // regions
@@ -821,7 +830,7 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
                             v[4] += zd * td;
                         }
                     }
-                    publish(v, 0u, 0u);
+                    publish(v);
                     fit_barrier(ws, nb, ++sync_seq, a.spin_limit);
                     double g[5];
                     gather_partials(g);
@@ -990,7 +999,6 @@ size_t fit_workspace_bytes(int64_t N, int iters) {
     const size_t hist = (size_t)(iters > 0 ? iters : 1) * kFitHistSlots * kFitHistWords * sizeof(unsigned);
     const size_t cand = 2 * nb * (size_t)kFitThreads * fit_ept(n) * sizeof(uint32_t);
     return kFitHeader + align256(kFitMaxBlocks * 64) + align256(2 * kFitMaxBlocks * 5 * sizeof(uint64_t)) +
-           align256(2 * kFitMaxBlocks * 2 * sizeof(unsigned)) +
            align256(hist) + 3 * align256(cand);
 }
 
@@ -1035,8 +1043,6 @@ int launch_fit(const FitLaunch& f, hipStream_t s) {
     p += align256(kFitMaxBlocks * 64);
     ws.partials = (uint64_t*)p;
     p += align256(2 * kFitMaxBlocks * 5 * sizeof(uint64_t));
-    ws.counts = (unsigned*)p;
-    p += align256(2 * kFitMaxBlocks * 2 * sizeof(unsigned));
     ws.hist = (unsigned*)p;
     p += align256((size_t)(f.iters > 0 ? f.iters : 1) * kFitHistSlots * kFitHistWords * sizeof(unsigned));
     const size_t cand = align256(2 * (size_t)nb * kFitThreads * ept * sizeof(uint32_t));
