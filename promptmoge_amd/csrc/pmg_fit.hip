@@ -1148,7 +1148,7 @@ int launch_final_fit(const FinalFit& f, hipStream_t s) {
 
 // ------------------------------------------------------------------------------------------------------------
 // Allocation-free fit: the workspace is a file-scope device array, one copy per GPU, instead of caller memory.
-// 14 MiB holds the workspace of N <= 2^19 elements per batch item at iters <= 16 (13.0 MB). Host code never uses
+// 14 MiB holds the workspace of N <= 2^19 elements per batch item at iters <= 16 (13.4 MB). Host code never uses
 // the array's name as an address: at a device's first call its address is looked up with hipGetSymbolAddress
 // (the device current), kept per device, and only that pointer reaches kernels.
 constexpr size_t kStaticFitBytes = (size_t)14 << 20;
