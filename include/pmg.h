@@ -281,7 +281,7 @@ unsigned pmg_debug_fit_spin_limit(unsigned polls);
  * enqueued after the call, so that tests reach the selection's fallbacks -- 1: each predicted bracket moved just
  * above its range (a window on the side that holds the k-th follows its miss); 2: each plan a window above every
  * finite residual (the radix passes follow its miss); 3: windows of 2^21-key bins (split passes); 0 (or any other
- * value) restores the normal plan. Results do not depend on the plan. Returns the previous mode. */
+ * value) restores the normal plan. Results do not depend on the plan. Returns the previous mode. ABI version 5. */
 unsigned pmg_debug_fit_plan(unsigned mode);
 int pmg_fit_scale_shift(const float* z, const float* target, const uint8_t* mask, int B, int64_t N, int iters,
                         float trim, int min_points, float* st, int32_t* info, void* workspace,

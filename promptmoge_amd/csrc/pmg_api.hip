@@ -306,7 +306,7 @@ extern "C" {
 
 const char* pmg_last_error(void) { return g_last_error.c_str(); }
 
-int pmg_version(void) { return 4; }
+int pmg_version(void) { return 5; }
 
 pmg_refiner* pmg_refiner_create(const pmg_refiner_config* cfg) {
     if (!cfg) {

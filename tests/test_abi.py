@@ -37,7 +37,7 @@ def test_every_declared_symbol_is_exported_and_bound(libpmg):
 
 
 def test_version_and_error_string(libpmg):
-    assert libpmg.pmg_version() == 4
+    assert libpmg.pmg_version() == 5
     rc = libpmg.pmg_voxelize(None, 1, 1, 1, 1, 256.0, None, None, None, None)
     assert rc == _lib.PMG_E_INVALID
     assert b"null" in libpmg.pmg_last_error()
