@@ -1,8 +1,8 @@
 """The reference's CPU path for one int8 refiner step, in torch on the host: the CPU baseline that bench.py times.
 
 TEST / BASELINE INFRASTRUCTURE ONLY (bench.py's cpu_baseline leg and tests/). A restatement of the _fallback path
-op for op with torch's CPU kernels, as BASELINE.md's plan asks (the reference's own Python does not travel to the GPU
-box):
+op for op with torch's CPU kernels, so that the baseline is the reference's algorithm on the host's cores (the
+reference's own Python does not travel to the GPU box):
 
   prompt fit      fit_scale_shift (moge/model/modules/prompt_stem.py:211-240): masked sums, torch.kthvalue per batch
                   item, iters + 1 solves
