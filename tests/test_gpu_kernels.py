@@ -643,6 +643,51 @@ def test_fit_plan_fallbacks_do_not_change_results(gpu, libpmg):
     assert split and max(split) >= 2, runs[3][1]      # coarse windows need split passes
 
 
+def _random_fit_case(rng):
+    """A seeded fit problem of varied shape: size, line, noise, outlier rate and spread, mask density, targets near
+    the 1e-3 clamp, ties (rounded targets), iteration count."""
+    N = int(rng.choice([3_000, 40_000, 150_000, 300_000, 700_000]))
+    s0, t0 = rng.uniform(0.2, 3.0), rng.uniform(-0.5, 0.5)
+    z = rng.uniform(0.05, 8.0, size=N).astype(np.float32)
+    t = s0 * z + t0 + rng.normal(0, rng.choice([0.0, 1e-4, 1e-2, 0.1]), size=N)
+    out = rng.random(N) < rng.choice([0.0, 0.05, 0.15, 0.3])
+    t = np.where(out, t * rng.uniform(0.2, 5.0, size=N), t)
+    if rng.random() < 0.3:
+        t = np.where(rng.random(N) < 0.05, rng.uniform(0, 2e-3, size=N), t)  # targets at the 1e-3 clamp
+    if rng.random() < 0.3:
+        t = np.round(t, 2)  # ties among residuals
+    m = rng.random(N) < rng.choice([0.3, 0.8, 1.0])
+    iters = int(rng.choice([1, 4, 10]))
+    return z[None], t.astype(np.float32)[None], m[None], iters
+
+
+def test_fit_random_cases_and_forced_plans(gpu, libpmg):
+    """Seeded random fit problems (sizes 3k-700k, both element layouts of the kernel): (s, t) against the fp64
+    oracle within 1e-5 and the threshold bit-equal when (s, t) are; and under each wrong-on-purpose plan
+    (pmg_debug_fit_plan 1-3) the normal plan's (s, t) and threshold bit for bit."""
+    rng = np.random.default_rng(2026)
+    for case in range(12):
+        z, t, m, iters = _random_fit_case(rng)
+        announce(f"fit random case {case}: N={z.shape[1]} iters={iters}")
+        so, to, info_o = ofit.fit_f64(z, t, m, iters=iters, return_info=True)
+        res = {}
+        try:
+            for mode in (0, 1, 2, 3):
+                libpmg.pmg_debug_fit_plan(mode)
+                s_, t_, info = ops.fit_scale_shift(_t(z, gpu), _t(t, gpu), _t(m, gpu), iters=iters, return_info=True)
+                info = info.cpu().numpy()
+                assert info[0, 4] == 0
+                res[mode] = (float(s_[0]), float(t_[0]), int(info[0, 3]))
+        finally:
+            libpmg.pmg_debug_fit_plan(0)
+        s0_, t0_, thr0 = res[0]
+        _close_st(s0_, t0_, so[0], to[0])
+        if np.float32(s0_) == np.float32(so[0]) and np.float32(t0_) == np.float32(to[0]):
+            assert thr0 == np.float32(info_o[0]["thr"]).view(np.int32), case
+        for mode in (1, 2, 3):
+            assert res[mode] == res[0], (case, mode, res[mode], res[0])
+
+
 @pytest.mark.parametrize("name", ["B", "A", "H"])
 def test_fit_prompt_scene(gpu, name):
     announce(f"fit prompt scene={name}")
