@@ -5,8 +5,8 @@
 //       r = |s*z + t - target| / max(target, 1e-3) on mask, +inf elsewhere
 //       thr = kthvalue(r, min(k, N));  w = mask & (r <= thr)
 //
-// Design. One persistent kernel per batch item with few, fat blocks (256 threads x 32 elements = 8192 elements each,
-// or x 16 up to 2^19 elements; held in registers for the whole fit, so HBM is read once): a device-wide barrier costs more the more blocks
+// Design. One persistent kernel per batch item with few, fat blocks (256 threads x 16, 24 or 32 elements by the
+// size, held in registers for the whole fit, so HBM is read once): a device-wide barrier costs more the more blocks
 // arrive, and a trim round is latency-bound, not bandwidth-bound. Phases are separated by a device-wide barrier of
 // per-block flags (fit_barrier). Sums are accumulated in fp64
 // (n*sxx - sx^2 cancels badly in fp32) in a fixed order, and every block reduces the published per-block partials
@@ -984,8 +984,12 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
 }
 
 // Elements per thread: 16 up to 2^19 elements (twice the blocks: faster loads and per-block passes, while the
-// device-wide barrier still costs little), else 32.
-static int fit_ept(int64_t N) { return N <= (int64_t(1) << 19) ? 16 : 32; }
+// device-wide barrier still costs little), 24 up to 1.5 M (config H's 762,048: 124 blocks; measured against 20 and
+// 28 per thread, 149 / 109 blocks, and the 32 used before: the fits on H's input / refined map took 85 / 210 us
+// against 96 / 239, 86 / 212 and 91 / 220), else 32.
+static int fit_ept(int64_t N) {
+    return N <= (int64_t(1) << 19) ? 16 : N <= (int64_t)kFitThreads * 24 * kFitMaxBlocks ? 24 : 32;
+}
 static int fit_blocks(int64_t N) {
     const int64_t per = (int64_t)kFitThreads * fit_ept(N);
     return (int)((N + per - 1) / per);
@@ -1017,12 +1021,14 @@ int launch_fit(const FitLaunch& f, hipStream_t s) {
     PMG_REQUIRE(aligned16(f.workspace), "workspace must be 16-byte aligned");
     const int nb = fit_blocks(f.N);
     const int ept = fit_ept(f.N);
-    static int max_resident[2] = {-1, -1};
-    int& mr = max_resident[ept == 16 ? 0 : 1];
+    static int max_resident[3] = {-1, -1, -1};
+    int& mr = max_resident[ept == 16 ? 0 : ept == 24 ? 1 : 2];
     if (mr < 0) {
         int per_cu = 0;
         if (ept == 16)
             PMG_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fit_k<16>, kFitThreads, 0));
+        else if (ept == 24)
+            PMG_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fit_k<24>, kFitThreads, 0));
         else
             PMG_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fit_k<32>, kFitThreads, 0));
         mr = per_cu * num_cus();
@@ -1055,6 +1061,8 @@ int launch_fit(const FitLaunch& f, hipStream_t s) {
                   g_fit_spin_limit, g_fit_plan_debug, ws};
         if (ept == 16)
             hipLaunchKernelGGL(fit_k<16>, dim3(nb), dim3(kFitThreads), 0, s, a);
+        else if (ept == 24)
+            hipLaunchKernelGGL(fit_k<24>, dim3(nb), dim3(kFitThreads), 0, s, a);
         else
             hipLaunchKernelGGL(fit_k<32>, dim3(nb), dim3(kFitThreads), 0, s, a);
         if (int e = check_launch("fit_k")) return e;
