@@ -81,7 +81,7 @@ struct FitWs {
 };
 
 struct FitArgs {
-    int mode;  // 0: (z, target, mask) arrays; 1: prompt map (logz, LiDAR, conf)
+    int mode;  // 0: (z, target, mask) arrays; 1: prompt map (logz, LiDAR, conf); 2: final fit, LiDAR at the map's size
     const float* z;
     const float* tg;
     const uint8_t* mask;
@@ -316,6 +316,28 @@ __global__ __launch_bounds__(kFitThreads) void fit_k(FitArgs a) {
             }
 #pragma unroll
             for (int j = 0; j < kFitEPT; ++j) mbits |= ((vbits >> j) & (mk[j] != 0 ? 1u : 0u)) << j;
+        } else if (a.mode == 2) {
+            // the final fit on a LiDAR map of the depth map's own size (v3.py:768-775): every area window is one
+            // pixel, so the pooled depth is exp(logz) itself (0 + z and z / 1 / 1 are exact) and the mask is
+            // conf >= 2 & lidar > 0 & z > 0 (& mask_binary), as final_inputs_k forms them for larger windows
+            const int64_t o0 = (int64_t)a.b * a.N;
+            float lc[kFitEPT];
+            uint8_t mb[kFitEPT];
+#pragma unroll
+            for (int j = 0; j < kFitEPT; ++j) {
+                int64_t i = (int64_t)i0 + j * kFitThreads;
+                i = i < last ? i : last;
+                zr[j] = a.logz[(o0 + i) * a.stride];
+                tr[j] = a.lidar[o0 + i];
+                lc[j] = a.conf[o0 + i];
+                mb[j] = a.mask ? a.mask[o0 + i] : (uint8_t)1;
+            }
+#pragma unroll
+            for (int j = 0; j < kFitEPT; ++j) {
+                zr[j] = exp_f32(zr[j]);
+                const bool m = ((vbits >> j) & 1u) && lc[j] >= 2.0f && tr[j] > 0.0f && zr[j] > 0.0f && mb[j] != 0;
+                mbits |= (m ? 1u : 0u) << j;
+            }
         } else {
             // v3.py:373-378: z = exp(logz); nearest LiDAR sample (F.interpolate's index rule); mask = valid & c >= 0.999
             const uint32_t W = (uint32_t)a.W;
@@ -1132,6 +1154,31 @@ int launch_final_fit(const FinalFit& f, hipStream_t s) {
     const int64_t N = (int64_t)f.dh * f.dw;
     const int64_t n_out = (int64_t)f.B * N;
     const size_t fit_bytes = align256(fit_workspace_bytes(N, f.iters));
+    if (f.dh == f.H && f.dw == f.W) {
+        // one-pixel area windows: the fit reads exp(logz), the LiDAR, conf and mask_binary itself (no
+        // final_inputs_k launch; the same values)
+        FitLaunch g{};
+        g.mode = 2;
+        g.logz = f.logz;
+        g.stride = f.stride;
+        g.lidar = f.lidar;
+        g.conf = f.conf;
+        g.mask = f.mask_binary;
+        g.H = f.H;
+        g.W = f.W;
+        g.dh = f.dh;
+        g.dw = f.dw;
+        g.B = f.B;
+        g.N = N;
+        g.iters = f.iters;
+        g.trim = f.trim;
+        g.min_points = f.min_points;
+        g.st = f.st;
+        g.info = f.info;
+        g.workspace = f.workspace;
+        g.workspace_bytes = fit_bytes;
+        return launch_fit(g, s);
+    }
     float* z_lr = (float*)((uint8_t*)f.workspace + fit_bytes);
     uint8_t* m_lr = (uint8_t*)f.workspace + fit_bytes + align256((size_t)n_out * sizeof(float));
     hipLaunchKernelGGL(final_inputs_k, dim3((unsigned)((n_out + 255) / 256)), dim3(256), 0, s, f.logz, f.stride,

@@ -707,6 +707,7 @@ def _lowres(sc, dh, dw):
 
 
 @pytest.mark.parametrize("name,dh,dw,with_mask", [("A", 192, 256, False), ("A", 192, 256, True), ("B", 240, 320, False),
+                                                   ("B", 240, 320, True), ("A", 480, 640, True),
                                                    ("H", 189, 252, False)])
 def test_fit_final_scene(gpu, name, dh, dw, with_mask):
     """The final metric fit (v3.py:768-778) at LiDAR resolution: area-pooled depth and the LiDAR mask."""
